@@ -1,0 +1,755 @@
+// Fused mHC backward (the VJP of mhc_mlx/metal.py:2787-2857 / the MLX
+// autograd of reference.py:148-184), for layer-wide or per-token parameters.
+//
+// With g = dout, a = activated H_pre, p = activated H_post, w = rms weight:
+//   y   = sum_i a_i x_i                 inv = 1/sqrt(mean_c y^2 + eps)
+//   dyn = sum_i p_i g_i                 d_r = sum_c dyn * y * w
+//   dy  = dyn*inv*w - (inv^3/C)*d_r*y
+//   dx_j  = sum_i M_ij g_i + a_j dy
+//   dM_ij = sum g_i x_j   dA_j = sum dy x_j   dP_i = sum g_i y inv w
+//   dw_c  = sum_t dyn * y * inv
+//
+// Stage 1 (fused_bwd_kernel): persistent workgroups, one token at a time.
+// Each thread owns one chunk of V channels x n streams of x and g in
+// registers; one block reduction per token yields inv and d_r; then dx is
+// written and the parameter-gradient contributions are accumulated.  Each
+// workgroup finally writes one row of partial sums (dw over its tokens and,
+// for layer-wide parameters, dM/dA/dP).  Per-token parameter gradients are
+// reduced across the workgroup per token and written directly.
+// Stage 2 (reduce kernels): fixed-order sum of the partial rows — the
+// result is bitwise reproducible for a given device and shape.
+#include "mhc_device.hpp"
+#include "mhc_generic.hpp"
+#include "mhc_host.hpp"
+#include "mhc_plan.hpp"
+#include "mhc_reduce.hpp"
+
+namespace mhc {
+
+struct BwdArgs {
+  const void* x;
+  const void* g;
+  void* dx;
+  const float* M;
+  const float* hpre;
+  const float* hpost;
+  const float* w;
+  float* part;
+  float* dM_tok;
+  float* dpre_tok;
+  float* dpost_tok;
+  int64_t T;
+  int64_t M_ts;
+  int64_t h_ts;
+  int n;
+  int C;
+  int Cp;
+  int P;
+  int nchunks;
+  int reload;
+  int h_mode;
+  int vec;
+  int rblk;  // butterfly blocks per cross-wave staging round
+  float eps;
+};
+
+constexpr int kBwdStageBudget = 48 * 1024;
+constexpr int kReduceSplit = 64;
+
+template <int NMAX>
+MHC_DEV void bwd_stage_params(float* buf, const BwdArgs& A, int64_t t) {
+  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
+  const int n = A.n;
+  const float* M = A.M + t * A.M_ts;
+  const float* hp = A.hpre + t * A.h_ts;
+  const float* hq = A.hpost + t * A.h_ts;
+  for (int idx = threadIdx.x; idx < NPAR; idx += blockDim.x) {
+    float v = 0.0f;
+    if (idx < NMAX * NMAX) {
+      const int i = idx / NMAX, j = idx % NMAX;
+      if (i < n && j < n) v = M[i * n + j];
+    } else if (idx < NMAX * NMAX + NMAX) {
+      const int i = idx - NMAX * NMAX;
+      if (i < n) v = A.h_mode == MHC_H_RAW ? sigmoidf_(hp[i]) : hp[i];
+    } else {
+      const int i = idx - NMAX * NMAX - NMAX;
+      if (i < n) v = A.h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(hq[i]) : hq[i];
+    }
+    buf[idx] = v;
+  }
+}
+
+MHC_DEV float bwd_uniform(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// Parameters either in uniform registers (small layer-wide n) or in LDS.
+template <int NMAX, bool LDS>
+struct ParView {
+  const float* par;
+  float Ms[LDS ? 1 : NMAX * NMAX];
+  float as[LDS ? 1 : NMAX];
+  float ps[LDS ? 1 : NMAX];
+  MHC_DEV float a(int i) const {
+    if constexpr (LDS) return par[NMAX * NMAX + i]; else return as[i];
+  }
+  MHC_DEV float p(int i) const {
+    if constexpr (LDS) return par[NMAX * NMAX + NMAX + i]; else return ps[i];
+  }
+  MHC_DEV float m(int i, int j) const {
+    if constexpr (LDS) return par[i * NMAX + j]; else return Ms[i * NMAX + j];
+  }
+};
+
+// Flattened per-token parameter-gradient index k (NMAX-padded):
+//   [0, NMAX^2)            dM[k / NMAX][k % NMAX]
+//   [NMAX^2, NMAX^2+NMAX)  dA[k - NMAX^2]
+//   [NMAX^2+NMAX, KP)      dP[k - NMAX^2 - NMAX]
+template <int NMAX, typename XT, typename GT, typename DT, bool PAR_LDS, bool REG_ACC, int NBLK>
+MHC_DEV void bwd_chunk_phase_b(const ParView<NMAX, PAR_LDS>& pv, const Vec<XT, BwdCfg<NMAX>::V> (&xr)[NMAX],
+                               const Vec<GT, BwdCfg<NMAX>::V> (&gr)[NMAX],
+                               const float (&y)[BwdCfg<NMAX>::V], const float (&dyn)[BwdCfg<NMAX>::V],
+                               const float (&wv)[BwdCfg<NMAX>::V], float (&dwv)[BwdCfg<NMAX>::V],
+                               float inv, float kf, int n, DT* dxt, int C, int c0, int valid, bool vec,
+                               float (&accM)[REG_ACC ? NMAX * NMAX : 1], float (&accA)[REG_ACC ? NMAX : 1],
+                               float (&accP)[REG_ACC ? NMAX : 1], float (&accL)[NBLK], int lane) {
+  constexpr int V = BwdCfg<NMAX>::V;
+  constexpr int KP = NMAX * NMAX + 2 * NMAX;
+  float dy[V], yn[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const float yi = y[v] * inv;
+    dy[v] = dyn[v] * inv * wv[v] - kf * y[v];
+    yn[v] = yi * wv[v];
+    dwv[v] = fmaf(dyn[v], yi, dwv[v]);
+  }
+  // dx_j = sum_i M_ij g_i + a_j dy
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) {
+    if (j < n) {
+      float o[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) acc = fmaf(pv.m(i, j), gr[i].get(v), acc);
+        o[v] = fmaf(pv.a(j), dy[v], acc);
+      }
+      DT* dst = dxt + (int64_t)j * C + c0;
+      if (vec && valid == V) store_vec<DT, V>(dst, o);
+      else store_partial<DT, V>(dst, o, valid);
+    }
+  }
+  if constexpr (REG_ACC) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float xv[NMAX], gv[NMAX];
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        xv[i] = xr[i].get(v);
+        gv[i] = gr[i].get(v);
+      }
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) accM[i * NMAX + j] = fmaf(gv[i], xv[j], accM[i * NMAX + j]);
+        accA[i] = fmaf(dy[v], xv[i], accA[i]);
+        accP[i] = fmaf(gv[i], yn[v], accP[i]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b) {
+      float pvv[64];
+#pragma unroll
+      for (int kk = 0; kk < 64; ++kk) {
+        const int k = 64 * b + kk;
+        float s = 0.0f;
+        if (k < NMAX * NMAX) {
+          const int i = k / NMAX, j = k % NMAX;
+#pragma unroll
+          for (int v = 0; v < V; ++v) s = fmaf(gr[i].get(v), xr[j].get(v), s);
+        } else if (k < NMAX * NMAX + NMAX) {
+          const int j = k - NMAX * NMAX;
+#pragma unroll
+          for (int v = 0; v < V; ++v) s = fmaf(dy[v], xr[j].get(v), s);
+        } else if (k < KP) {
+          const int i = k - NMAX * NMAX - NMAX;
+#pragma unroll
+          for (int v = 0; v < V; ++v) s = fmaf(gr[i].get(v), yn[v], s);
+        }
+        pvv[kk] = s;
+      }
+      wave_reduce_scatter<1>(pvv, lane);
+      accL[b] += pvv[0];
+    }
+  }
+}
+
+template <int NMAX, typename XT, typename GT, typename DT, bool PT>
+__global__ __launch_bounds__(1024) void fused_bwd_kernel(BwdArgs A) {
+  constexpr int V = BwdCfg<NMAX>::V;
+  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
+  constexpr bool PAR_LDS = PT || NMAX > 8;
+  constexpr bool REG_ACC = !PT && NMAX <= 8;
+  constexpr int KP = NMAX * NMAX + 2 * NMAX;
+  constexpr int NBLK = (KP + 63) / 64;
+  extern __shared__ float bwd_smem[];
+  __shared__ float s_red[2][2][16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int n = A.n;
+  const int C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  const XT* __restrict__ X = (const XT*)A.x;
+  const GT* __restrict__ Gr = (const GT*)A.g;
+  DT* __restrict__ DX = (DT*)A.dx;
+  const float* __restrict__ Wt = A.w;
+  float* s_par = bwd_smem;
+  float* s_stage = bwd_smem + (PAR_LDS ? (PT ? 3 : 1) * NPAR : 0);
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  const int R = A.rblk;
+
+  ParView<NMAX, PAR_LDS> pv;
+  pv.par = s_par;
+  if constexpr (!PAR_LDS) {
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      float av = 0.0f, pq = 0.0f;
+      if (i < n) {
+        av = A.hpre[i];
+        pq = A.hpost[i];
+        if (A.h_mode == MHC_H_RAW) {
+          av = sigmoidf_(av);
+          pq = 2.0f * sigmoidf_(pq);
+        }
+      }
+      pv.as[i] = bwd_uniform(av);
+      pv.ps[i] = bwd_uniform(pq);
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) pv.Ms[i * NMAX + j] = (i < n && j < n) ? A.M[i * n + j] : 0.0f;
+    }
+  } else {
+    if (PT) {
+      if ((int64_t)blockIdx.x < A.T) bwd_stage_params<NMAX>(s_par, A, blockIdx.x);
+    } else {
+      bwd_stage_params<NMAX>(s_par, A, 0);
+    }
+  }
+
+  // owned chunk (register path) and dw accumulators
+  const int q0 = tid;
+  const int c00 = q0 * V;
+  const bool act0 = !A.reload && q0 < A.nchunks;
+  const int valid0 = act0 ? min(V, C - c00) : 0;
+  float wv[V], dwv[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    wv[v] = (act0 && c00 + v < C) ? Wt[c00 + v] : 0.0f;
+    dwv[v] = 0.0f;
+  }
+  if (A.reload) {
+    for (int c = tid; c < A.Cp; c += blockDim.x) prow[c] = 0.0f;
+  }
+  float accM[REG_ACC ? NMAX * NMAX : 1], accA[REG_ACC ? NMAX : 1], accP[REG_ACC ? NMAX : 1];
+  float accL[NBLK];
+#pragma unroll
+  for (int k = 0; k < (REG_ACC ? NMAX * NMAX : 1); ++k) accM[k] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < (REG_ACC ? NMAX : 1); ++k) {
+    accA[k] = 0.0f;
+    accP[k] = 0.0f;
+  }
+#pragma unroll
+  for (int b = 0; b < NBLK; ++b) accL[b] = 0.0f;
+  __syncthreads();
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    if constexpr (PT) {
+      pv.par = s_par + (it % 3) * NPAR;
+      const int64_t tn = t + gridDim.x;
+      if (tn < A.T) bwd_stage_params<NMAX>(s_par + ((it + 1) % 3) * NPAR, A, tn);
+#pragma unroll
+      for (int b = 0; b < NBLK; ++b) accL[b] = 0.0f;
+    }
+    const XT* xt = X + t * nC;
+    const GT* gt = Gr + t * nC;
+    DT* dxt = DX + t * nC;
+
+    // ---- phase A: y, dyn and the two per-token reductions
+    float ss = 0.0f, sr = 0.0f;
+    Vec<XT, V> xr[NMAX];
+    Vec<GT, V> gr[NMAX];
+    float y[V], dyn[V];
+    if (!A.reload) {
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        if (act0 && i < n) {
+          if (A.vec && valid0 == V) {
+            xr[i].load(xt + (int64_t)i * C + c00);
+            gr[i].load(gt + (int64_t)i * C + c00);
+          } else {
+            xr[i].load_partial(xt + (int64_t)i * C + c00, valid0);
+            gr[i].load_partial(gt + (int64_t)i * C + c00, valid0);
+          }
+        } else {
+          xr[i].zero();
+          gr[i].zero();
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        float ya = 0.0f, da = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          ya = fmaf(pv.a(i), xr[i].get(v), ya);
+          da = fmaf(pv.p(i), gr[i].get(v), da);
+        }
+        y[v] = ya;
+        dyn[v] = da;
+        ss = fmaf(ya, ya, ss);
+        sr = fmaf(da * ya, wv[v], sr);
+      }
+    } else {
+      for (int q = tid; q < A.nchunks; q += blockDim.x) {
+        const int c0 = q * V;
+        const int valid = min(V, C - c0);
+        float ya[V], da[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) ya[v] = da[v] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          if (i < n) {
+            Vec<XT, V> xv;
+            Vec<GT, V> gv;
+            if (A.vec && valid == V) {
+              xv.load(xt + (int64_t)i * C + c0);
+              gv.load(gt + (int64_t)i * C + c0);
+            } else {
+              xv.load_partial(xt + (int64_t)i * C + c0, valid);
+              gv.load_partial(gt + (int64_t)i * C + c0, valid);
+            }
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              ya[v] = fmaf(pv.a(i), xv.get(v), ya[v]);
+              da[v] = fmaf(pv.p(i), gv.get(v), da[v]);
+            }
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float wc = c0 + v < C ? Wt[c0 + v] : 0.0f;
+          ss = fmaf(ya[v], ya[v], ss);
+          sr = fmaf(da[v] * ya[v], wc, sr);
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    __syncthreads();
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+
+    // ---- phase B: dx, dw, parameter-gradient contributions
+    if (!A.reload) {
+      if (act0 || !REG_ACC) {
+        bwd_chunk_phase_b<NMAX, XT, GT, DT, PAR_LDS, REG_ACC, NBLK>(
+            pv, xr, gr, y, dyn, wv, dwv, inv, kf, act0 ? n : 0, dxt, C, c00, valid0, A.vec != 0,
+            accM, accA, accP, accL, lane);
+      }
+    } else {
+      // all lanes of a wave iterate together so the butterflies stay converged
+      const int nq = (int)ceil_div(A.nchunks, blockDim.x) * blockDim.x;
+      for (int q = tid; q < nq; q += blockDim.x) {
+        const bool act = q < A.nchunks;
+        const int c0 = q * V;
+        const int valid = act ? min(V, C - c0) : 0;
+        Vec<XT, V> xq[NMAX];
+        Vec<GT, V> gq[NMAX];
+        float yq[V], dq[V], wq[V], dwq[V];
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          if (act && i < n) {
+            if (A.vec && valid == V) {
+              xq[i].load(xt + (int64_t)i * C + c0);
+              gq[i].load(gt + (int64_t)i * C + c0);
+            } else {
+              xq[i].load_partial(xt + (int64_t)i * C + c0, valid);
+              gq[i].load_partial(gt + (int64_t)i * C + c0, valid);
+            }
+          } else {
+            xq[i].zero();
+            gq[i].zero();
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          float ya = 0.0f, da = 0.0f;
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) {
+            ya = fmaf(pv.a(i), xq[i].get(v), ya);
+            da = fmaf(pv.p(i), gq[i].get(v), da);
+          }
+          yq[v] = ya;
+          dq[v] = da;
+          wq[v] = (act && c0 + v < C) ? Wt[c0 + v] : 0.0f;
+          dwq[v] = 0.0f;
+        }
+        bwd_chunk_phase_b<NMAX, XT, GT, DT, PAR_LDS, REG_ACC, NBLK>(
+            pv, xq, gq, yq, dq, wq, dwq, inv, kf, act ? n : 0, dxt, C, c0, valid, A.vec != 0, accM,
+            accA, accP, accL, lane);
+        if (act) {
+#pragma unroll
+          for (int v = 0; v < V; ++v)
+            if (v < valid) prow[c0 + v] += dwq[v];
+        }
+      }
+    }
+
+    // ---- per-token parameter gradients: cross-wave sum and write
+    if constexpr (PT) {
+      const float* par = pv.par;
+      for (int b0 = 0; b0 < NBLK; b0 += R) {
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b)
+          if (b >= b0 && b < b0 + R) s_stage[((wave * R) + (b - b0)) * 64 + lane] = accL[b];
+        __syncthreads();
+        const int cnt = min(R, NBLK - b0) * 64;
+        for (int idx = tid; idx < cnt; idx += blockDim.x) {
+          float s = 0.0f;
+          for (int w = 0; w < nwaves; ++w) s += s_stage[((w * R) + (idx >> 6)) * 64 + (idx & 63)];
+          const int k = b0 * 64 + idx;
+          if (k < NMAX * NMAX) {
+            const int i = k / NMAX, j = k % NMAX;
+            if (i < n && j < n) A.dM_tok[t * n * n + i * n + j] = s;
+          } else if (k < NMAX * NMAX + NMAX) {
+            const int j = k - NMAX * NMAX;
+            if (j < n) {
+              const float av = par[NMAX * NMAX + j];
+              A.dpre_tok[t * n + j] = A.h_mode == MHC_H_RAW ? s * av * (1.0f - av) : s;
+            }
+          } else if (k < KP) {
+            const int i = k - NMAX * NMAX - NMAX;
+            if (i < n) {
+              const float pq = par[NMAX * NMAX + NMAX + i];
+              A.dpost_tok[t * n + i] = A.h_mode == MHC_H_RAW ? s * pq * (1.0f - 0.5f * pq) : s;
+            }
+          }
+        }
+        if (b0 + R < NBLK) __syncthreads();
+      }
+    }
+  }
+
+  // ---- this workgroup's partial row
+  if (!A.reload && act0) {
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (v < valid0) prow[c00 + v] = dwv[v];
+  }
+  if (tid == 0)
+    for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
+  if constexpr (!PT) {
+    if constexpr (REG_ACC) {
+#pragma unroll
+      for (int b = 0; b < NBLK; ++b) {
+        float pvv[64];
+#pragma unroll
+        for (int kk = 0; kk < 64; ++kk) {
+          const int k = 64 * b + kk;
+          pvv[kk] = k < NMAX * NMAX ? accM[k < NMAX * NMAX ? k : 0]
+                  : k < NMAX * NMAX + NMAX ? accA[(k - NMAX * NMAX) % NMAX]
+                  : k < KP ? accP[(k - NMAX * NMAX - NMAX) % NMAX] : 0.0f;
+        }
+        wave_reduce_scatter<1>(pvv, lane);
+        accL[b] = pvv[0];
+      }
+    }
+    __syncthreads();
+    for (int b0 = 0; b0 < NBLK; b0 += R) {
+#pragma unroll
+      for (int b = 0; b < NBLK; ++b)
+        if (b >= b0 && b < b0 + R) s_stage[((wave * R) + (b - b0)) * 64 + lane] = accL[b];
+      __syncthreads();
+      const int cnt = min(R, NBLK - b0) * 64;
+      for (int idx = tid; idx < cnt; idx += blockDim.x) {
+        float s = 0.0f;
+        for (int w = 0; w < nwaves; ++w) s += s_stage[((w * R) + (idx >> 6)) * 64 + (idx & 63)];
+        const int k = b0 * 64 + idx;
+        if (k < NMAX * NMAX) {
+          const int i = k / NMAX, j = k % NMAX;
+          if (i < n && j < n) prow[A.Cp + i * n + j] = s;
+        } else if (k < NMAX * NMAX + NMAX) {
+          const int j = k - NMAX * NMAX;
+          if (j < n) prow[A.Cp + n * n + j] = s;
+        } else if (k < KP) {
+          const int i = k - NMAX * NMAX - NMAX;
+          if (i < n) prow[A.Cp + n * n + n + i] = s;
+        }
+      }
+      __syncthreads();
+    }
+    if (tid == 0)
+      for (int c = A.Cp + n * n + 2 * n; c < A.P; ++c) prow[c] = 0.0f;
+  }
+}
+
+// Stage 2b: final column sums and the activation chain.
+__global__ __launch_bounds__(256) void reduce_final_kernel(
+    const float* __restrict__ part2, int S, int P, int n, int C, int Cp, int per_token,
+    const float* __restrict__ hpre, const float* __restrict__ hpost, int h_mode,
+    float* __restrict__ dM, float* __restrict__ dpre, float* __restrict__ dpost,
+    float* __restrict__ dw) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= P) return;
+  float s = 0.0f;
+  for (int k = 0; k < S; ++k) s += part2[(int64_t)k * P + c];
+  if (c < C) {
+    dw[c] = s;
+    return;
+  }
+  if (per_token || c < Cp) return;
+  const int k = c - Cp;
+  if (k < n * n) {
+    dM[k] = s;
+  } else if (k < n * n + n) {
+    const int j = k - n * n;
+    if (h_mode == MHC_H_RAW) {
+      const float a = sigmoidf_(hpre[j]);
+      s = s * a * (1.0f - a);
+    }
+    dpre[j] = s;
+  } else if (k < n * n + 2 * n) {
+    const int i = k - n * n - n;
+    if (h_mode == MHC_H_RAW) {
+      const float sg = sigmoidf_(hpost[i]);
+      s = s * 2.0f * sg * (1.0f - sg);
+    }
+    dpost[i] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct BwdLayout {
+  int Cp;
+  int P;
+  int64_t gmax;
+  size_t scratch_off;  // generic path: 2*C floats per workgroup after the partial rows
+  size_t bytes;
+};
+
+BwdLayout bwd_layout(int64_t T, int n, int C, int per_token) {
+  BwdLayout L{};
+  L.Cp = round_up(C, 4);
+  L.P = per_token ? L.Cp : L.Cp + round_up(n * n + 2 * n, 4);
+  L.gmax = std::max<int64_t>(1, std::min<int64_t>(T, (int64_t)device_cu_count() * 8));
+  L.scratch_off = (size_t)(L.gmax + kReduceSplit) * (size_t)L.P * sizeof(float);
+  L.bytes = L.scratch_off;
+  if (nmax_for(n) == 0) L.bytes += (size_t)L.gmax * 2 * (size_t)C * sizeof(float);
+  return L;
+}
+
+template <int NMAX, typename XT, typename GT, bool PT>
+int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  constexpr int V = BwdCfg<NMAX>::V;
+  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
+  constexpr int KP = NMAX * NMAX + 2 * NMAX;
+  constexpr int NBLK = (KP + 63) / 64;
+  A.nchunks = (int)ceil_div(A.C, V);
+  static const int tpb_pref = env_int("MHC_BWD_TPB", 0);
+  const ThreadPlan tp = plan_threads(A.nchunks, 1, tpb_pref);
+  A.reload = tp.reload;
+  const int nwaves = tp.tpb / 64;
+  const bool par_lds = PT || NMAX > 8;
+  const size_t par_bytes = par_lds ? (size_t)(PT ? 3 : 1) * NPAR * sizeof(float) : 0;
+  int rblk = (int)((kBwdStageBudget - (int)par_bytes) / (nwaves * 64 * (int)sizeof(float)));
+  rblk = std::max(1, std::min(rblk, NBLK));
+  A.rblk = rblk;
+  const size_t smem = par_bytes + (size_t)nwaves * rblk * 64 * sizeof(float);
+  const void* kfn = (const void*)fused_bwd_kernel<NMAX, XT, GT, XT, PT>;
+  const int occ = occupancy_blocks(kfn, tp.tpb, smem);
+  if (occ <= 0)
+    return set_error(MHC_ERR_INVALID_ARG, "fused_bwd: no occupancy for %d threads (n=%d C=%d)",
+                     tp.tpb, A.n, A.C);
+  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+  A.Cp = L.Cp;
+  A.P = L.P;
+  hipLaunchKernelGGL((fused_bwd_kernel<NMAX, XT, GT, XT, PT>), dim3((unsigned)blocks), dim3(tp.tpb),
+                     smem, stream, A);
+  MHC_CHECK_LAUNCH("fused_bwd_kernel");
+  *num_partials = blocks;
+  return MHC_OK;
+}
+
+template <typename XT, typename GT, bool PT>
+int bwd_dispatch_n(const BwdArgs& A, const BwdLayout& L, int64_t* np, hipStream_t s) {
+  switch (nmax_for(A.n)) {
+    case 4: return launch_bwd<4, XT, GT, PT>(A, L, np, s);
+    case 8: return launch_bwd<8, XT, GT, PT>(A, L, np, s);
+    default: return launch_bwd<16, XT, GT, PT>(A, L, np, s);
+  }
+}
+
+template <bool PT>
+int bwd_dispatch_types(const BwdArgs& A, const BwdLayout& L, int xd, int gd, int64_t* np,
+                       hipStream_t s) {
+  if (xd == MHC_DTYPE_F32 && gd == MHC_DTYPE_F32) return bwd_dispatch_n<float, float, PT>(A, L, np, s);
+  if (xd == MHC_DTYPE_BF16 && gd == MHC_DTYPE_BF16) return bwd_dispatch_n<__bf16, __bf16, PT>(A, L, np, s);
+  if (xd == MHC_DTYPE_BF16 && gd == MHC_DTYPE_F32) return bwd_dispatch_n<__bf16, float, PT>(A, L, np, s);
+  if (xd == MHC_DTYPE_F16 && gd == MHC_DTYPE_F16) return bwd_dispatch_n<_Float16, _Float16, PT>(A, L, np, s);
+  if (xd == MHC_DTYPE_F16 && gd == MHC_DTYPE_F32) return bwd_dispatch_n<_Float16, float, PT>(A, L, np, s);
+  return set_error(MHC_ERR_INVALID_ARG,
+                   "fused_bwd: unsupported (x_dtype=%d, dout_dtype=%d); dout must be fp32 or x's dtype",
+                   xd, gd);
+}
+
+}  // namespace
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" size_t mhc_fused_bwd_workspace_bytes(int64_t T, int n, int C, int per_token) {
+  if (T <= 0 || n < 1 || n > MHC_MAX_N || C < 1) return 0;
+  return bwd_layout(T, n, C, per_token).bytes;
+}
+
+extern "C" int mhc_fused_bwd_partials(const void* x, int x_dtype, const void* dout, int dout_dtype,
+                                      const float* M, int64_t M_token_stride, const float* h_pre,
+                                      const float* h_post, int64_t h_token_stride, int h_mode,
+                                      const float* rms_weight, void* dx, int dx_dtype,
+                                      float* dM_tok, float* dh_pre_tok, float* dh_post_tok,
+                                      void* workspace, size_t workspace_bytes, int64_t T, int n,
+                                      int C, float eps, int64_t* num_partials, void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(num_partials != nullptr, "num_partials must not be NULL");
+  *num_partials = 0;
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1, "C=%d must be positive", C);
+  MHC_CHECK_ARG(T >= 0, "T=%lld must be >= 0", (long long)T);
+  MHC_CHECK_ARG(h_mode == MHC_H_ACTIVATED || h_mode == MHC_H_RAW, "h_mode=%d must be ACTIVATED or RAW",
+                h_mode);
+  MHC_CHECK_ARG(M_token_stride == 0 || M_token_stride == (int64_t)n * n,
+                "M_token_stride must be 0 or n*n");
+  MHC_CHECK_ARG(h_token_stride == 0 || h_token_stride == n, "h_token_stride must be 0 or n");
+  MHC_CHECK_ARG((M_token_stride == 0) == (h_token_stride == 0),
+                "M and h must both be per-token or both layer-wide");
+  MHC_CHECK_ARG(dx_dtype == x_dtype, "dx_dtype (%d) must equal x_dtype (%d)", dx_dtype, x_dtype);
+  if (T == 0) return MHC_OK;
+  const int per_token = M_token_stride != 0;
+  MHC_CHECK_ARG(x && dout && M && h_pre && h_post && rms_weight && dx, "null pointer argument");
+  MHC_CHECK_ARG(!per_token || (dM_tok && dh_pre_tok && dh_post_tok),
+                "per-token mode needs dM_tok, dh_pre_tok and dh_post_tok");
+  const BwdLayout L = bwd_layout(T, n, C, per_token);
+  MHC_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.bytes,
+                "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes,
+                L.bytes);
+  MHC_CHECK_ARG(aligned(workspace, 16), "workspace must be 16-byte aligned");
+  const int xb = dtype_bytes(x_dtype), gb = dtype_bytes(dout_dtype);
+  MHC_CHECK_ARG(xb > 0 && gb > 0, "unknown dtype code");
+  BwdArgs A{};
+  A.x = x; A.g = dout; A.dx = dx; A.M = M; A.hpre = h_pre; A.hpost = h_post; A.w = rms_weight;
+  A.part = (float*)workspace; A.dM_tok = dM_tok; A.dpre_tok = dh_pre_tok; A.dpost_tok = dh_post_tok;
+  A.T = T; A.M_ts = M_token_stride; A.h_ts = h_token_stride; A.n = n; A.C = C; A.h_mode = h_mode;
+  A.eps = eps;
+  MHC_CHECK_ARG(dout_dtype == MHC_DTYPE_F32 || dout_dtype == x_dtype,
+                "dout_dtype (%d) must be fp32 or x_dtype (%d)", dout_dtype, x_dtype);
+  if (nmax_for(n) == 0) {
+    GenArgs G{};
+    G.x = x; G.g = dout; G.out = dx; G.M = M; G.hpre = h_pre; G.hpost = h_post; G.w = rms_weight;
+    G.part = (float*)workspace;
+    G.scratch = (float*)((char*)workspace + L.scratch_off);
+    G.dM_tok = dM_tok; G.dpre_tok = dh_pre_tok; G.dpost_tok = dh_post_tok;
+    G.T = T; G.M_ts = M_token_stride; G.h_ts = h_token_stride; G.n = n; G.C = C; G.Cp = L.Cp;
+    G.P = L.P; G.h_mode = h_mode; G.eps = eps;
+    return gen_fused_bwd(G, x_dtype, dout_dtype, (hipStream_t)stream, num_partials);
+  }
+  const int V = bwd_vec_width(nmax_for(n));
+  const int ax = std::min(16, V * xb), ag = std::min(16, V * gb);
+  A.vec = (C % V == 0) && aligned(x, ax) && aligned(dx, ax) && aligned(dout, ag) &&
+          ((int64_t)C * xb) % ax == 0 && ((int64_t)C * gb) % ag == 0 ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  return per_token ? bwd_dispatch_types<true>(A, L, x_dtype, dout_dtype, num_partials, s)
+                   : bwd_dispatch_types<false>(A, L, x_dtype, dout_dtype, num_partials, s);
+}
+
+extern "C" int mhc_reduce_param_grads(const void* workspace, size_t workspace_bytes,
+                                      int64_t num_partials, int n, int C, int per_token,
+                                      const float* h_pre, const float* h_post, int h_mode,
+                                      float* dM, float* dh_pre, float* dh_post,
+                                      float* d_rms_weight, void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1, "C=%d must be positive", C);
+  MHC_CHECK_ARG(d_rms_weight != nullptr, "d_rms_weight must not be NULL");
+  MHC_CHECK_ARG(per_token || (dM && dh_pre && dh_post), "dM, dh_pre and dh_post must not be NULL");
+  MHC_CHECK_ARG(per_token || h_mode != MHC_H_RAW || (h_pre && h_post),
+                "raw-logit mode needs h_pre and h_post");
+  MHC_CHECK_ARG(num_partials >= 0, "num_partials must be >= 0");
+  hipStream_t s = (hipStream_t)stream;
+  if (num_partials == 0) {
+    MHC_CHECK_HIP(hipMemsetAsync(d_rms_weight, 0, sizeof(float) * C, s));
+    if (!per_token) {
+      MHC_CHECK_HIP(hipMemsetAsync(dM, 0, sizeof(float) * n * n, s));
+      MHC_CHECK_HIP(hipMemsetAsync(dh_pre, 0, sizeof(float) * n, s));
+      MHC_CHECK_HIP(hipMemsetAsync(dh_post, 0, sizeof(float) * n, s));
+    }
+    return MHC_OK;
+  }
+  const int Cp = round_up(C, 4);
+  const int P = per_token ? Cp : Cp + round_up(n * n + 2 * n, 4);
+  const size_t need = (size_t)(num_partials + kReduceSplit) * (size_t)P * sizeof(float);
+  MHC_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
+  const float* part = (const float*)workspace;
+  float* part2 = (float*)workspace + (size_t)num_partials * P;
+  const int S = (int)std::min<int64_t>(kReduceSplit, num_partials);
+  const int rows = (int)ceil_div(num_partials, S);
+  const int S_used = (int)ceil_div(num_partials, rows);
+  dim3 g1((unsigned)ceil_div(P / 4, 256), (unsigned)S_used);
+  hipLaunchKernelGGL(reduce_rows_kernel, g1, dim3(256), 0, s, part, part2, num_partials, P, rows);
+  MHC_CHECK_LAUNCH("reduce_rows_kernel");
+  hipLaunchKernelGGL(reduce_final_kernel, dim3((unsigned)ceil_div(P, 256)), dim3(256), 0, s, part2,
+                     S_used, P, n, C, Cp, per_token, h_pre, h_post, h_mode, dM, dh_pre, dh_post,
+                     d_rms_weight);
+  MHC_CHECK_LAUNCH("reduce_final_kernel");
+  return MHC_OK;
+}
+
+extern "C" int mhc_fused_bwd(const void* x, int x_dtype, const void* dout, int dout_dtype,
+                             const float* M, int64_t M_token_stride, const float* h_pre,
+                             const float* h_post, int64_t h_token_stride, int h_mode,
+                             const float* rms_weight, void* dx, int dx_dtype, float* dM,
+                             float* dh_pre, float* dh_post, float* d_rms_weight, void* workspace,
+                             size_t workspace_bytes, int64_t T, int n, int C, float eps,
+                             void* stream) {
+  const int per_token = M_token_stride != 0;
+  int64_t np = 0;
+  int rc = mhc_fused_bwd_partials(x, x_dtype, dout, dout_dtype, M, M_token_stride, h_pre, h_post,
+                                  h_token_stride, h_mode, rms_weight, dx, dx_dtype,
+                                  per_token ? dM : nullptr, per_token ? dh_pre : nullptr,
+                                  per_token ? dh_post : nullptr, workspace, workspace_bytes, T, n,
+                                  C, eps, &np, stream);
+  if (rc != MHC_OK) return rc;
+  return mhc_reduce_param_grads(workspace, workspace_bytes, np, n, C, per_token, h_pre, h_post,
+                                h_mode, per_token ? nullptr : dM, per_token ? nullptr : dh_pre,
+                                per_token ? nullptr : dh_post, d_rms_weight, stream);
+}

@@ -1,0 +1,379 @@
+// Fused mHC forward: stream aggregate + RMSNorm + n x n stream mix + H_post
+// residual add in one pass over x (mhc_mlx/reference.py:148-184).
+//
+// One workgroup processes one token at a time (persistent grid, grid-stride
+// over tokens).  The token's n x C tile is split into channel chunks of V
+// consecutive channels; thread `tid` owns chunks tid, tid + TPB, ... and
+// keeps every stream of its chunks in registers (packed 16-bit when x is
+// bf16/fp16) from the load until the store, so x is read from HBM exactly
+// once.  Per token:
+//   phase A  load chunk, y = sum_i a_i x_i, accumulate y^2
+//   reduce   wave butterfly + one LDS slot per wave + one barrier
+//   phase B  out_i = sum_j M_ij x_j + p_i * (y * inv) * w, store
+// When the tile does not fit in registers (very large n*C) the kernel runs a
+// second pass over x instead ("reload").
+#include "mhc_device.hpp"
+#include "mhc_generic.hpp"
+#include "mhc_host.hpp"
+#include "mhc_plan.hpp"
+
+namespace mhc {
+
+struct FwdArgs {
+  const void* x;
+  void* out;
+  float* inv_rms;
+  const float* M;
+  const float* hpre;
+  const float* hpost;
+  const float* w;
+  int64_t T;
+  int64_t M_ts;
+  int64_t h_ts;
+  int n;
+  int C;
+  int nchunks;
+  int ch;
+  int h_mode;
+  int vec;
+  int reload;
+  float eps;
+};
+
+// Stage (M padded to NMAX x NMAX, a, p) for token t into `buf`.
+template <int NMAX>
+MHC_DEV void fwd_stage_params(float* buf, const FwdArgs& A, int64_t t) {
+  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
+  const int n = A.n;
+  const float* M = A.M + t * A.M_ts;
+  const float* hp = A.hpre + t * A.h_ts;
+  const float* hq = A.hpost + t * A.h_ts;
+  for (int idx = threadIdx.x; idx < NPAR; idx += blockDim.x) {
+    float v = 0.0f;
+    if (idx < NMAX * NMAX) {
+      const int i = idx / NMAX, j = idx % NMAX;
+      if (i < n && j < n) v = M[i * n + j];
+    } else if (idx < NMAX * NMAX + NMAX) {
+      const int i = idx - NMAX * NMAX;
+      if (i < n) v = A.h_mode == MHC_H_RAW ? sigmoidf_(hp[i]) : hp[i];
+    } else {
+      const int i = idx - NMAX * NMAX - NMAX;
+      if (i < n) v = A.h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(hq[i]) : hq[i];
+    }
+    buf[idx] = v;
+  }
+}
+
+MHC_DEV float uniform_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+template <int NMAX, typename XT, typename OT, bool PT>
+__global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
+  constexpr int V = FwdCfg<NMAX>::V;
+  constexpr int CH = FwdCfg<NMAX>::CH;
+  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
+  // Parameters live in registers (uniform) for small static n, else in LDS.
+  constexpr bool PAR_LDS = PT || NMAX > 8;
+  extern __shared__ float fwd_smem[];
+  __shared__ float s_red[2][16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int n = A.n;
+  const int C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  const XT* __restrict__ X = (const XT*)A.x;
+  OT* __restrict__ O = (OT*)A.out;
+  const float* __restrict__ Wt = A.w;
+
+  // static parameters in uniform registers
+  float Ms[PAR_LDS ? 1 : NMAX * NMAX], as[PAR_LDS ? 1 : NMAX], ps[PAR_LDS ? 1 : NMAX];
+  if constexpr (!PAR_LDS) {
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      float av = 0.0f, pv = 0.0f;
+      if (i < n) {
+        av = A.hpre[i];
+        pv = A.hpost[i];
+        if (A.h_mode == MHC_H_RAW) {
+          av = sigmoidf_(av);
+          pv = 2.0f * sigmoidf_(pv);
+        }
+      }
+      as[i] = uniform_f(av);
+      ps[i] = uniform_f(pv);
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = (i < n && j < n) ? A.M[i * n + j] : 0.0f;
+    }
+  } else {
+    if (PT) {
+      if ((int64_t)blockIdx.x < A.T) fwd_stage_params<NMAX>(fwd_smem, A, blockIdx.x);
+    } else {
+      fwd_stage_params<NMAX>(fwd_smem, A, 0);
+    }
+    __syncthreads();
+  }
+
+  // rms weight of the owned chunks (register-resident path)
+  float wv[CH][V];
+  if (!A.reload) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int q = tid + j * blockDim.x;
+      const int c0 = q * V;
+      const bool act = (j < A.ch) && (q < A.nchunks);
+#pragma unroll
+      for (int v = 0; v < V; ++v) wv[j][v] = (act && c0 + v < C) ? Wt[c0 + v] : 0.0f;
+    }
+  }
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const float* par = fwd_smem + (PT ? (it % 3) * NPAR : 0);
+    if constexpr (PT) {
+      const int64_t tn = t + gridDim.x;
+      if (tn < A.T) fwd_stage_params<NMAX>(fwd_smem + ((it + 1) % 3) * NPAR, A, tn);
+    }
+    auto a_at = [&](int i) -> float {
+      if constexpr (PAR_LDS) return par[NMAX * NMAX + i]; else return as[i];
+    };
+    auto p_at = [&](int i) -> float {
+      if constexpr (PAR_LDS) return par[NMAX * NMAX + NMAX + i]; else return ps[i];
+    };
+    auto m_at = [&](int i, int j) -> float {
+      if constexpr (PAR_LDS) return par[i * NMAX + j]; else return Ms[i * NMAX + j];
+    };
+    const XT* xt = X + t * nC;
+    OT* ot = O + t * nC;
+
+    if (!A.reload) {
+      Vec<XT, V> xr[CH][NMAX];
+      float y[CH][V];
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int q = tid + j * blockDim.x;
+        const bool act = (j < A.ch) && (q < A.nchunks);
+        const int c0 = q * V;
+        const int valid = act ? min(V, C - c0) : 0;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          if (act && i < n) {
+            if (A.vec && valid == V) xr[j][i].load(xt + (int64_t)i * C + c0);
+            else xr[j][i].load_partial(xt + (int64_t)i * C + c0, valid);
+          } else {
+            xr[j][i].zero();
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) acc = fmaf(a_at(i), xr[j][i].get(v), acc);
+          y[j][v] = acc;
+          ss = fmaf(acc, acc, ss);
+        }
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) s_red[it & 1][wave] = ss;
+      __syncthreads();
+      float tot = 0.0f;
+      for (int w = 0; w < nwaves; ++w) tot += s_red[it & 1][w];
+      const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
+      if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int q = tid + j * blockDim.x;
+        const bool act = (j < A.ch) && (q < A.nchunks);
+        if (!act) continue;
+        const int c0 = q * V;
+        const int valid = min(V, C - c0);
+        float yn[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) yn[v] = (y[j][v] * inv) * wv[j][v];
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          if (i < n) {
+            float o[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              float acc = 0.0f;
+#pragma unroll
+              for (int k = 0; k < NMAX; ++k) acc = fmaf(m_at(i, k), xr[j][k].get(v), acc);
+              o[v] = fmaf(yn[v], p_at(i), acc);
+            }
+            OT* dst = ot + (int64_t)i * C + c0;
+            if (A.vec && valid == V) store_vec<OT, V>(dst, o);
+            else store_partial<OT, V>(dst, o, valid);
+          }
+        }
+      }
+    } else {
+      // two passes over x (tile larger than the register budget)
+      float ss = 0.0f;
+      for (int q = tid; q < A.nchunks; q += blockDim.x) {
+        const int c0 = q * V;
+        const int valid = min(V, C - c0);
+        float y[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) y[v] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          if (i < n) {
+            Vec<XT, V> xv;
+            if (A.vec && valid == V) xv.load(xt + (int64_t)i * C + c0);
+            else xv.load_partial(xt + (int64_t)i * C + c0, valid);
+#pragma unroll
+            for (int v = 0; v < V; ++v) y[v] = fmaf(a_at(i), xv.get(v), y[v]);
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) ss = fmaf(y[v], y[v], ss);
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) s_red[it & 1][wave] = ss;
+      __syncthreads();
+      float tot = 0.0f;
+      for (int w = 0; w < nwaves; ++w) tot += s_red[it & 1][w];
+      const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
+      if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
+      for (int q = tid; q < A.nchunks; q += blockDim.x) {
+        const int c0 = q * V;
+        const int valid = min(V, C - c0);
+        Vec<XT, V> xr[NMAX];
+        float yn[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) yn[v] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          if (i < n) {
+            if (A.vec && valid == V) xr[i].load(xt + (int64_t)i * C + c0);
+            else xr[i].load_partial(xt + (int64_t)i * C + c0, valid);
+          } else {
+            xr[i].zero();
+          }
+#pragma unroll
+          for (int v = 0; v < V; ++v) yn[v] = fmaf(a_at(i), xr[i].get(v), yn[v]);
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) yn[v] = (yn[v] * inv) * (c0 + v < C ? Wt[c0 + v] : 0.0f);
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          if (i < n) {
+            float o[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              float acc = 0.0f;
+#pragma unroll
+              for (int k = 0; k < NMAX; ++k) acc = fmaf(m_at(i, k), xr[k].get(v), acc);
+              o[v] = fmaf(yn[v], p_at(i), acc);
+            }
+            OT* dst = ot + (int64_t)i * C + c0;
+            if (A.vec && valid == V) store_vec<OT, V>(dst, o);
+            else store_partial<OT, V>(dst, o, valid);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+namespace {
+
+template <int NMAX, typename XT, typename OT, bool PT>
+int launch_fwd(FwdArgs A, hipStream_t stream) {
+  constexpr int V = FwdCfg<NMAX>::V;
+  constexpr int CH = FwdCfg<NMAX>::CH;
+  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
+  A.nchunks = (int)ceil_div(A.C, V);
+  const ThreadPlan tp = plan_threads(A.nchunks, CH, env_int("MHC_FWD_TPB", 0));
+  A.ch = tp.ch;
+  A.reload = tp.reload;
+  const bool par_lds = PT || NMAX > 8;
+  const size_t smem = par_lds ? (size_t)(PT ? 3 : 1) * NPAR * sizeof(float) : 0;
+  const void* kfn = (const void*)fused_fwd_kernel<NMAX, XT, OT, PT>;
+  const int occ = occupancy_blocks(kfn, tp.tpb, smem);
+  if (occ <= 0)
+    return set_error(MHC_ERR_INVALID_ARG, "fused_fwd: no occupancy for %d threads (n=%d C=%d)",
+                     tp.tpb, A.n, A.C);
+  int64_t blocks = std::min<int64_t>(A.T, (int64_t)device_cu_count() * occ);
+  blocks = std::max<int64_t>(blocks, 1);
+  hipLaunchKernelGGL((fused_fwd_kernel<NMAX, XT, OT, PT>), dim3((unsigned)blocks), dim3(tp.tpb),
+                     smem, stream, A);
+  MHC_CHECK_LAUNCH("fused_fwd_kernel");
+  return MHC_OK;
+}
+
+template <typename XT, typename OT, bool PT>
+int dispatch_n(const FwdArgs& A, hipStream_t s) {
+  switch (nmax_for(A.n)) {
+    case 4: return launch_fwd<4, XT, OT, PT>(A, s);
+    case 8: return launch_fwd<8, XT, OT, PT>(A, s);
+    default: return launch_fwd<16, XT, OT, PT>(A, s);
+  }
+}
+
+template <bool PT>
+int dispatch_types(const FwdArgs& A, int xd, int od, hipStream_t s) {
+  if (xd == MHC_DTYPE_F32 && od == MHC_DTYPE_F32) return dispatch_n<float, float, PT>(A, s);
+  if (xd == MHC_DTYPE_BF16 && od == MHC_DTYPE_F32) return dispatch_n<__bf16, float, PT>(A, s);
+  if (xd == MHC_DTYPE_BF16 && od == MHC_DTYPE_BF16) return dispatch_n<__bf16, __bf16, PT>(A, s);
+  if (xd == MHC_DTYPE_F16 && od == MHC_DTYPE_F32) return dispatch_n<_Float16, float, PT>(A, s);
+  if (xd == MHC_DTYPE_F16 && od == MHC_DTYPE_F16) return dispatch_n<_Float16, _Float16, PT>(A, s);
+  return set_error(MHC_ERR_INVALID_ARG,
+                   "fused_fwd: unsupported (x_dtype=%d, out_dtype=%d); out must be fp32 or x's dtype",
+                   xd, od);
+}
+
+}  // namespace
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" int mhc_fused_fwd(const void* x, int x_dtype, const float* M, int64_t M_token_stride,
+                             const float* h_pre, const float* h_post, int64_t h_token_stride,
+                             int h_mode, const float* rms_weight, void* out, int out_dtype,
+                             float* inv_rms, int64_t T, int n, int C, float eps, void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1, "C=%d must be positive", C);
+  MHC_CHECK_ARG(T >= 0, "T=%lld must be >= 0", (long long)T);
+  MHC_CHECK_ARG(h_mode == MHC_H_ACTIVATED || h_mode == MHC_H_RAW, "h_mode=%d must be ACTIVATED or RAW",
+                h_mode);
+  MHC_CHECK_ARG(M_token_stride == 0 || M_token_stride == (int64_t)n * n,
+                "M_token_stride must be 0 or n*n");
+  MHC_CHECK_ARG(h_token_stride == 0 || h_token_stride == n, "h_token_stride must be 0 or n");
+  MHC_CHECK_ARG((M_token_stride == 0) == (h_token_stride == 0),
+                "M and h must both be per-token or both layer-wide");
+  if (T == 0) return MHC_OK;
+  MHC_CHECK_ARG(x && M && h_pre && h_post && rms_weight && out, "null pointer argument");
+  FwdArgs A{};
+  A.x = x; A.out = out; A.inv_rms = inv_rms; A.M = M; A.hpre = h_pre; A.hpost = h_post;
+  A.w = rms_weight; A.T = T; A.M_ts = M_token_stride; A.h_ts = h_token_stride; A.n = n; A.C = C;
+  A.h_mode = h_mode; A.eps = eps;
+  const int xb = dtype_bytes(x_dtype), ob = dtype_bytes(out_dtype);
+  MHC_CHECK_ARG(xb > 0 && ob > 0, "unknown dtype code");
+  MHC_CHECK_ARG(out_dtype == MHC_DTYPE_F32 || out_dtype == x_dtype,
+                "out_dtype (%d) must be fp32 or x_dtype (%d)", out_dtype, x_dtype);
+  if (nmax_for(n) == 0) {
+    GenArgs G{};
+    G.x = x; G.out = out; G.M = M; G.hpre = h_pre; G.hpost = h_post; G.w = rms_weight;
+    G.inv_rms = inv_rms; G.T = T; G.M_ts = M_token_stride; G.h_ts = h_token_stride; G.n = n;
+    G.C = C; G.h_mode = h_mode; G.eps = eps;
+    return gen_fused_fwd(G, x_dtype, out_dtype, (hipStream_t)stream);
+  }
+  const int V = fwd_vec_width(nmax_for(n));
+  const int align_x = std::min(16, V * xb), align_o = std::min(16, V * ob);
+  A.vec = (C % V == 0) && aligned(x, align_x) && aligned(out, align_o) &&
+          ((int64_t)C * xb) % align_x == 0 && ((int64_t)C * ob) % align_o == 0 ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  return M_token_stride ? dispatch_types<true>(A, x_dtype, out_dtype, s)
+                        : dispatch_types<false>(A, x_dtype, out_dtype, s);
+}

@@ -1,0 +1,80 @@
+// Launch planning shared by the fused kernels: per-n tile shapes, thread
+// counts, occupancy (cached) and tuning overrides.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include <algorithm>
+
+#include "mhc_host.hpp"
+
+namespace mhc {
+
+// Forward tile: V consecutive channels per chunk, up to CH chunks per thread
+// held in registers.  NMAX is n rounded up to {4, 8, 16, 32, 64}.
+template <int NMAX>
+struct FwdCfg {
+  static constexpr int V = NMAX <= 8 ? 8 : 64 / NMAX;
+  static constexpr int CH = NMAX <= 4 ? 2 : 1;
+};
+
+// Backward tile: x and dout of one chunk per thread.
+template <int NMAX>
+struct BwdCfg {
+  static constexpr int V = NMAX <= 4 ? 8 : (NMAX == 8 ? 4 : (NMAX == 16 ? 2 : 1));
+};
+
+// Register-tiled kernels exist for NMAX in {4, 8, 16}; 0 selects the
+// runtime-n kernels of generic.hip (16 < n <= 64).
+inline int nmax_for(int n) { return n <= 4 ? 4 : (n <= 8 ? 8 : (n <= 16 ? 16 : 0)); }
+inline int fwd_vec_width(int nmax) { return nmax <= 8 ? 8 : 64 / nmax; }
+inline int bwd_vec_width(int nmax) { return nmax <= 4 ? 8 : (nmax == 8 ? 4 : (nmax == 16 ? 2 : 1)); }
+
+inline int dtype_bytes(int code) {
+  switch (code) {
+    case MHC_DTYPE_F32: return 4;
+    case MHC_DTYPE_BF16: return 2;
+    case MHC_DTYPE_F16: return 2;
+    default: return 0;
+  }
+}
+
+struct ThreadPlan {
+  int tpb;     // threads per block
+  int ch;      // chunks per thread held in registers
+  int reload;  // 1: tile does not fit, two passes over the inputs
+};
+
+// Smallest block (multiple of 64, <= 1024) holding nchunks with at most
+// `chmax` chunks per thread; `tpb_pref` > 0 forces the block size.
+inline ThreadPlan plan_threads(int nchunks, int chmax, int tpb_pref) {
+  ThreadPlan p{};
+  if (tpb_pref > 0) {
+    p.tpb = std::min(1024, std::max(64, round_up(tpb_pref, 64)));
+    p.ch = (int)ceil_div(nchunks, p.tpb);
+    p.reload = p.ch > chmax ? 1 : 0;
+    if (p.reload) p.ch = 0;
+    return p;
+  }
+  int tpb = round_up((int)ceil_div(nchunks, chmax), 64);
+  if (tpb <= 1024) {
+    p.tpb = std::max(64, tpb);
+    p.ch = (int)ceil_div(nchunks, p.tpb);
+    p.reload = 0;
+  } else {
+    p.tpb = 1024;
+    p.ch = 0;
+    p.reload = 1;
+  }
+  return p;
+}
+
+// Resident blocks per CU for a kernel at a block size (cached).
+int occupancy_blocks(const void* kernel, int tpb, size_t smem);
+
+// Integer tuning override from the environment (0 when unset).
+int env_int(const char* name, int dflt);
+
+}  // namespace mhc

@@ -1,0 +1,708 @@
+// MHCRewire kernels (mhc_mlx/layer.py:302-337, 469-492):
+//   pre-scale     x_pre[t,i,c] = a_i x[t,i,c]
+//   post-combine  out[t,i,c] = p_i (y[t,i,c] + sum_j M_ij a_j x[t,j,c])
+// and their VJPs.  With h_mode == MHC_H_NONE (a = p = 1) the post-combine is
+// stream_mix_add (metal.py:954-1014: out = M x + y_dist).
+//
+// Work item = (token, chunk of V channels x n streams); items are processed
+// grid-stride by a persistent grid.  The VJPs accumulate the per-stream sums
+// (S_ij = sum g_i x_j, Yd_i = sum g_i y_i, Sa_i = sum g_i x_i) per thread,
+// reduce them over the workgroup at the end into one partial row per
+// workgroup and finish with the fixed-order row reduction.
+#include "mhc_device.hpp"
+#include "mhc_generic.hpp"
+#include "mhc_host.hpp"
+#include "mhc_plan.hpp"
+#include "mhc_reduce.hpp"
+
+namespace mhc {
+
+namespace {
+
+constexpr int kMixThreads = 256;
+constexpr int kMixSplit = 64;
+
+template <int NMAX>
+struct MixCfg {
+  static constexpr int V = NMAX <= 8 ? 8 : 64 / NMAX;
+};
+
+struct MixArgs {
+  const void* x;
+  const void* y;
+  const void* g;
+  void* out;   // fwd: out; bwd: dx
+  void* dy;    // bwd only (may be null)
+  const void* acc;  // stream_scale bwd: optional dx accumulator
+  const float* M;
+  const float* hpre;
+  const float* hpost;
+  float* part;
+  int64_t T;
+  int n;
+  int C;
+  int nchunks;
+  int h_mode;
+  int vec;
+  int P;
+};
+
+// Mf (NMAX x NMAX, Mf_ij = p_i M_ij a_j), a, p into LDS.
+template <int NMAX>
+MHC_DEV void mix_stage(float* buf, const MixArgs& A) {
+  const int n = A.n;
+  for (int idx = threadIdx.x; idx < NMAX * NMAX + 2 * NMAX; idx += blockDim.x) {
+    float v = 0.0f;
+    auto act_a = [&](int i) {
+      if (A.h_mode == MHC_H_NONE) return 1.0f;
+      return A.h_mode == MHC_H_RAW ? sigmoidf_(A.hpre[i]) : A.hpre[i];
+    };
+    auto act_p = [&](int i) {
+      if (A.h_mode == MHC_H_NONE) return 1.0f;
+      return A.h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(A.hpost[i]) : A.hpost[i];
+    };
+    if (idx < NMAX * NMAX) {
+      const int i = idx / NMAX, j = idx % NMAX;
+      if (i < n && j < n && A.M) v = act_p(i) * A.M[i * n + j] * act_a(j);
+    } else if (idx < NMAX * NMAX + NMAX) {
+      const int i = idx - NMAX * NMAX;
+      if (i < n) v = act_a(i);
+    } else {
+      const int i = idx - NMAX * NMAX - NMAX;
+      if (i < n) v = act_p(i);
+    }
+    buf[idx] = v;
+  }
+}
+
+template <typename T, int V>
+MHC_DEV void load_chunk(Vec<T, V>& r, const T* p, bool vec, int valid) {
+  if (vec && valid == V) r.load(p);
+  else r.load_partial(p, valid);
+}
+
+template <typename T, int V>
+MHC_DEV void store_chunk(T* p, const float (&v)[V], bool vec, int valid) {
+  if (vec && valid == V) store_vec<T, V>(p, v);
+  else store_partial<T, V>(p, v, valid);
+}
+
+template <int NMAX, typename XT, typename YT, typename OT>
+__global__ __launch_bounds__(kMixThreads) void mix_add_fwd_kernel(MixArgs A) {
+  constexpr int V = MixCfg<NMAX>::V;
+  __shared__ float s_par[NMAX * NMAX + 2 * NMAX];
+  mix_stage<NMAX>(s_par, A);
+  __syncthreads();
+  const int n = A.n, C = A.C;
+  const int64_t items = A.T * A.nchunks;
+  const XT* X = (const XT*)A.x;
+  const YT* Y = (const YT*)A.y;
+  OT* O = (OT*)A.out;
+  for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < items;
+       item += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = item / A.nchunks;
+    const int q = (int)(item - t * A.nchunks);
+    const int c0 = q * V;
+    const int valid = min(V, C - c0);
+    const int64_t base = t * n * C + c0;
+    Vec<XT, V> xr[NMAX];
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) {
+      if (j < n) load_chunk<XT, V>(xr[j], X + base + (int64_t)j * C, A.vec, valid);
+      else xr[j].zero();
+    }
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      if (i < n) {
+        Vec<YT, V> yr;
+        if (Y) load_chunk<YT, V>(yr, Y + base + (int64_t)i * C, A.vec, valid);
+        else yr.zero();
+        const float p = s_par[NMAX * NMAX + NMAX + i];
+        float o[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int j = 0; j < NMAX; ++j) acc = fmaf(s_par[i * NMAX + j], xr[j].get(v), acc);
+          o[v] = fmaf(p, yr.get(v), acc);
+        }
+        store_chunk<OT, V>(O + base + (int64_t)i * C, o, A.vec, valid);
+      }
+    }
+  }
+}
+
+// VJP of the post-combine.  Per-thread sums: S_ij (NMAX^2) then Yd_i (NMAX).
+template <int NMAX, typename XT, typename YT, typename GT>
+__global__ __launch_bounds__(kMixThreads) void mix_add_bwd_kernel(MixArgs A) {
+  constexpr int V = MixCfg<NMAX>::V;
+  constexpr int K = NMAX * NMAX + NMAX;
+  constexpr int NBLK = (K + 63) / 64;
+  constexpr bool REG = NMAX <= 8;
+  __shared__ float s_par[NMAX * NMAX + 2 * NMAX];
+  __shared__ float s_stage[(kMixThreads / 64) * 64];
+  mix_stage<NMAX>(s_par, A);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int n = A.n, C = A.C;
+  const int64_t items = A.T * A.nchunks;
+  const XT* X = (const XT*)A.x;
+  const YT* Y = (const YT*)A.y;
+  const GT* Gd = (const GT*)A.g;
+  XT* DX = (XT*)A.out;
+  YT* DY = (YT*)A.dy;
+  // REG: full per-thread sums; else one lane-owned butterfly result per block
+  float acc[REG ? 64 * NBLK : 1];
+  float accL[NBLK];
+#pragma unroll
+  for (int k = 0; k < (REG ? 64 * NBLK : 1); ++k) acc[k] = 0.0f;
+#pragma unroll
+  for (int b = 0; b < NBLK; ++b) accL[b] = 0.0f;
+  const int64_t nitems_pad = ceil_div(items, (int64_t)gridDim.x * blockDim.x) * gridDim.x * blockDim.x;
+  for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < nitems_pad;
+       item += (int64_t)gridDim.x * blockDim.x) {
+    const bool act = item < items;
+    const int64_t t = act ? item / A.nchunks : 0;
+    const int q = act ? (int)(item - t * A.nchunks) : 0;
+    const int c0 = q * V;
+    const int valid = act ? min(V, C - c0) : 0;
+    const int64_t base = t * n * C + c0;
+    Vec<XT, V> xr[NMAX];
+    Vec<GT, V> gr[NMAX];
+    Vec<YT, V> yr[NMAX];
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) {
+      if (act && j < n) {
+        load_chunk<XT, V>(xr[j], X + base + (int64_t)j * C, A.vec, valid);
+        load_chunk<GT, V>(gr[j], Gd + base + (int64_t)j * C, A.vec, valid);
+        if (Y) load_chunk<YT, V>(yr[j], Y + base + (int64_t)j * C, A.vec, valid);
+        else yr[j].zero();
+      } else {
+        xr[j].zero();
+        gr[j].zero();
+        yr[j].zero();
+      }
+    }
+    if (act) {
+      // dx_j = sum_i Mf_ij g_i
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) {
+        if (j < n) {
+          float o[V];
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NMAX; ++i) s = fmaf(s_par[i * NMAX + j], gr[i].get(v), s);
+            o[v] = s;
+          }
+          store_chunk<XT, V>(DX + base + (int64_t)j * C, o, A.vec, valid);
+        }
+      }
+      // dy_i = p_i g_i
+      if (DY) {
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          if (i < n) {
+            const float p = s_par[NMAX * NMAX + NMAX + i];
+            float o[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) o[v] = p * gr[i].get(v);
+            store_chunk<YT, V>(DY + base + (int64_t)i * C, o, A.vec, valid);
+          }
+        }
+      }
+    }
+    if constexpr (REG) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          const float gv = gr[i].get(v);
+#pragma unroll
+          for (int j = 0; j < NMAX; ++j) acc[i * NMAX + j] = fmaf(gv, xr[j].get(v), acc[i * NMAX + j]);
+          acc[NMAX * NMAX + i] = fmaf(gv, yr[i].get(v), acc[NMAX * NMAX + i]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < NBLK; ++b) {
+        float pv[64];
+#pragma unroll
+        for (int kk = 0; kk < 64; ++kk) {
+          const int k = 64 * b + kk;
+          float s = 0.0f;
+          if (k < NMAX * NMAX) {
+            const int i = k / NMAX, j = k % NMAX;
+#pragma unroll
+            for (int v = 0; v < V; ++v) s = fmaf(gr[i].get(v), xr[j].get(v), s);
+          } else if (k < K) {
+            const int i = k - NMAX * NMAX;
+#pragma unroll
+            for (int v = 0; v < V; ++v) s = fmaf(gr[i].get(v), yr[i].get(v), s);
+          }
+          pv[kk] = s;
+        }
+        wave_reduce_scatter<1>(pv, lane);
+        accL[b] += pv[0];
+      }
+    }
+  }
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  // reduce the sums into this workgroup's row (n-indexed: S then Yd)
+  {
+    const int wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b) {
+      float v;
+      if constexpr (REG) {
+        float pv[64];
+#pragma unroll
+        for (int kk = 0; kk < 64; ++kk) pv[kk] = acc[(64 * b + kk) % (REG ? 64 * NBLK : 1)];
+        wave_reduce_scatter<1>(pv, lane);
+        v = pv[0];
+      } else {
+        v = accL[b];
+      }
+      __syncthreads();
+      s_stage[wave * 64 + lane] = v;
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        float s = 0.0f;
+        for (int w = 0; w < nwaves; ++w) s += s_stage[w * 64 + threadIdx.x];
+        const int k = 64 * b + threadIdx.x;
+        if (k < NMAX * NMAX) {
+          const int i = k / NMAX, j = k % NMAX;
+          if (i < n && j < n) prow[i * n + j] = s;
+        } else if (k < K) {
+          const int i = k - NMAX * NMAX;
+          if (i < n) prow[n * n + i] = s;
+        }
+      }
+    }
+    if (threadIdx.x == 0)
+      for (int c = n * n + n; c < A.P; ++c) prow[c] = 0.0f;
+  }
+}
+
+// Final: sum S partial rows, then dM / dh_pre / dh_post (one block).
+__global__ __launch_bounds__(256) void mix_final_kernel(const float* __restrict__ part2, int S,
+                                                        int P, int n, int h_mode,
+                                                        const float* __restrict__ M,
+                                                        const float* __restrict__ hpre,
+                                                        const float* __restrict__ hpost,
+                                                        float* __restrict__ dM,
+                                                        float* __restrict__ dpre,
+                                                        float* __restrict__ dpost) {
+  extern __shared__ float s_sum[];  // [n*n + n]: S then Yd
+  const int K = n * n + n;
+  for (int c = threadIdx.x; c < K; c += blockDim.x) {
+    float s = 0.0f;
+    for (int k = 0; k < S; ++k) s += part2[(int64_t)k * P + c];
+    s_sum[c] = s;
+  }
+  __syncthreads();
+  auto a_of = [&](int j) {
+    if (h_mode == MHC_H_NONE) return 1.0f;
+    return h_mode == MHC_H_RAW ? sigmoidf_(hpre[j]) : hpre[j];
+  };
+  auto p_of = [&](int i) {
+    if (h_mode == MHC_H_NONE) return 1.0f;
+    return h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(hpost[i]) : hpost[i];
+  };
+  for (int k = threadIdx.x; k < n * n; k += blockDim.x) {
+    const int i = k / n, j = k % n;
+    dM[k] = h_mode == MHC_H_NONE ? s_sum[k] : p_of(i) * s_sum[k] * a_of(j);
+  }
+  if (h_mode == MHC_H_NONE) return;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) s = fmaf(p_of(i) * M[i * n + j], s_sum[i * n + j], s);
+    if (h_mode == MHC_H_RAW) {
+      const float a = sigmoidf_(hpre[j]);
+      s *= a * (1.0f - a);
+    }
+    dpre[j] = s;
+  }
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    float s = 0.0f;
+    for (int j = 0; j < n; ++j) s = fmaf(M[i * n + j] * a_of(j), s_sum[i * n + j], s);
+    s += s_sum[n * n + i];
+    if (h_mode == MHC_H_RAW) {
+      const float sg = sigmoidf_(hpost[i]);
+      s *= 2.0f * sg * (1.0f - sg);
+    }
+    dpost[i] = s;
+  }
+}
+
+// pre-scale forward: out_i = a_i x_i.  grid.y = stream i; x dimension over
+// (token, chunk of 8 channels).
+template <typename XT, typename OT>
+__global__ __launch_bounds__(kMixThreads) void scale_fwd_kernel(MixArgs A) {
+  constexpr int V = 8;
+  const int i = blockIdx.y;
+  const float hv = A.hpre[i];
+  const float a = A.h_mode == MHC_H_RAW ? sigmoidf_(hv) : hv;
+  const int n = A.n, C = A.C;
+  const int64_t items = A.T * A.nchunks;
+  const XT* X = (const XT*)A.x;
+  OT* O = (OT*)A.out;
+  for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < items;
+       item += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = item / A.nchunks;
+    const int q = (int)(item - t * A.nchunks);
+    const int c0 = q * V;
+    const int valid = min(V, C - c0);
+    const int64_t off = (t * n + i) * C + c0;
+    Vec<XT, V> xr;
+    load_chunk<XT, V>(xr, X + off, A.vec, valid);
+    float o[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) o[v] = a * xr.get(v);
+    store_chunk<OT, V>(O + off, o, A.vec, valid);
+  }
+}
+
+// pre-scale VJP: dx_i = a_i g_i (+ acc), Sa_i = sum g_i x_i.  grid.y = stream
+// i; block (bx, i) writes column i of partial row bx.
+template <typename XT, typename GT>
+__global__ __launch_bounds__(kMixThreads) void scale_bwd_kernel(MixArgs A) {
+  constexpr int V = 8;
+  __shared__ float s_stage[kMixThreads / 64];
+  const int i = blockIdx.y;
+  const float hv = A.hpre[i];
+  const float a = A.h_mode == MHC_H_RAW ? sigmoidf_(hv) : hv;
+  const int n = A.n, C = A.C;
+  const int64_t items = A.T * A.nchunks;
+  const XT* X = (const XT*)A.x;
+  const GT* Gd = (const GT*)A.g;
+  const XT* ACC = (const XT*)A.acc;
+  XT* DX = (XT*)A.out;
+  float acc = 0.0f;
+  for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < items;
+       item += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = item / A.nchunks;
+    const int q = (int)(item - t * A.nchunks);
+    const int c0 = q * V;
+    const int valid = min(V, C - c0);
+    const int64_t off = (t * n + i) * C + c0;
+    Vec<XT, V> xr;
+    Vec<GT, V> gr;
+    load_chunk<XT, V>(xr, X + off, A.vec, valid);
+    load_chunk<GT, V>(gr, Gd + off, A.vec, valid);
+    float o[V];
+    if (ACC) {
+      Vec<XT, V> ar;
+      load_chunk<XT, V>(ar, ACC + off, A.vec, valid);
+#pragma unroll
+      for (int v = 0; v < V; ++v) o[v] = fmaf(a, gr.get(v), ar.get(v));
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v) o[v] = a * gr.get(v);
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc = fmaf(gr.get(v), xr.get(v), acc);
+    store_chunk<XT, V>(DX + off, o, A.vec, valid);
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) s_stage[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) s += s_stage[w];
+    prow[i] = s;
+    if (i == 0)
+      for (int c = n; c < A.P; ++c) prow[c] = 0.0f;
+  }
+}
+
+__global__ __launch_bounds__(64) void scale_final_kernel(const float* __restrict__ part2, int S,
+                                                         int P, int n, int h_mode,
+                                                         const float* __restrict__ hpre,
+                                                         float* __restrict__ dpre) {
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    float s = 0.0f;
+    for (int k = 0; k < S; ++k) s += part2[(int64_t)k * P + j];
+    if (h_mode == MHC_H_RAW) {
+      const float a = sigmoidf_(hpre[j]);
+      s *= a * (1.0f - a);
+    }
+    dpre[j] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host helpers
+// ---------------------------------------------------------------------------
+
+int mix_vec_width(int nmax) { return nmax == 0 ? 1 : (nmax <= 8 ? 8 : 64 / nmax); }
+
+int64_t mix_grid(int64_t work, int cus) {
+  int64_t g = ceil_div(work, kMixThreads);
+  g = std::min<int64_t>(g, (int64_t)cus * 8);
+  return std::max<int64_t>(g, 1);
+}
+
+bool io_vec_ok(int C, int V, std::initializer_list<std::pair<const void*, int>> ptrs) {
+  if (C % V != 0) return false;
+  for (auto& pr : ptrs) {
+    if (pr.first == nullptr) continue;
+    const int al = std::min(16, V * pr.second);
+    if (!aligned(pr.first, al) || ((int64_t)C * pr.second) % al != 0) return false;
+  }
+  return true;
+}
+
+template <typename F>
+int by_nmax(int n, F&& f) {
+  switch (nmax_for(n)) {
+    case 4: return f(std::integral_constant<int, 4>{});
+    case 8: return f(std::integral_constant<int, 8>{});
+    default: return f(std::integral_constant<int, 16>{});
+  }
+}
+
+// second / third dtype: fp32 or the same as the first
+template <typename T1, typename F>
+int by_pair(int code2, F&& f) {
+  if (code2 == MHC_DTYPE_F32) return f((float*)nullptr);
+  if ((code2 == MHC_DTYPE_BF16 && std::is_same<T1, __bf16>::value) ||
+      (code2 == MHC_DTYPE_F16 && std::is_same<T1, _Float16>::value))
+    return f((T1*)nullptr);
+  return set_error(MHC_ERR_INVALID_ARG, "unsupported dtype combination (dtype %d with %s)", code2,
+                   std::is_same<T1, float>::value ? "fp32" : "a 16-bit first operand");
+}
+
+template <typename F>
+int by_dtype(int code, F&& f) {
+  switch (code) {
+    case MHC_DTYPE_F32: return f((float*)nullptr);
+    case MHC_DTYPE_BF16: return f((__bf16*)nullptr);
+    case MHC_DTYPE_F16: return f((_Float16*)nullptr);
+    default: return set_error(MHC_ERR_INVALID_ARG, "unknown dtype code %d", code);
+  }
+}
+
+int mix_rows(int n) { return round_up(n * n + n, 4); }
+
+}  // namespace
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" int mhc_stream_mix_add_fwd(const void* x, int x_dtype, const void* y, int y_dtype,
+                                      const float* M, const float* h_pre, const float* h_post,
+                                      int h_mode, void* out, int out_dtype, int64_t T, int n, int C,
+                                      void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1 && T >= 0, "invalid T=%lld / C=%d", (long long)T, C);
+  MHC_CHECK_ARG(h_mode == MHC_H_NONE || h_mode == MHC_H_ACTIVATED || h_mode == MHC_H_RAW,
+                "invalid h_mode %d", h_mode);
+  if (T == 0) return MHC_OK;
+  MHC_CHECK_ARG(x && M && out, "null pointer argument");
+  MHC_CHECK_ARG(h_mode == MHC_H_NONE || (h_pre && h_post), "h_pre/h_post required");
+  MHC_CHECK_ARG(dtype_bytes(x_dtype) && dtype_bytes(out_dtype) && (!y || dtype_bytes(y_dtype)),
+                "unknown dtype code");
+  MixArgs A{};
+  A.x = x; A.y = y; A.out = out; A.M = M; A.hpre = h_pre; A.hpost = h_post; A.T = T; A.n = n;
+  A.C = C; A.h_mode = h_mode;
+  const int V = mix_vec_width(nmax_for(n));
+  A.nchunks = (int)ceil_div(C, V);
+  A.vec = io_vec_ok(C, V, {{x, dtype_bytes(x_dtype)}, {y, y ? dtype_bytes(y_dtype) : 4},
+                           {out, dtype_bytes(out_dtype)}});
+  const int64_t blocks = mix_grid(T * A.nchunks, device_cu_count());
+  hipStream_t s = (hipStream_t)stream;
+  const int ydt = y ? y_dtype : x_dtype;
+  if (nmax_for(n) == 0) {
+    GenArgs G{};
+    G.x = x; G.y = y; G.out = out; G.M = M; G.hpre = h_pre; G.hpost = h_post; G.T = T; G.n = n;
+    G.C = C; G.h_mode = h_mode;
+    return gen_mix_fwd(G, x_dtype, ydt, out_dtype, s);
+  }
+  return by_nmax(n, [&](auto nm) {
+    constexpr int NM = decltype(nm)::value;
+    return by_dtype(x_dtype, [&](auto* xp) {
+      using XT = std::remove_pointer_t<decltype(xp)>;
+      return by_pair<XT>(ydt, [&](auto* yp) {
+        using YT = std::remove_pointer_t<decltype(yp)>;
+        return by_pair<XT>(out_dtype, [&](auto* op) {
+          using OT = std::remove_pointer_t<decltype(op)>;
+          hipLaunchKernelGGL((mix_add_fwd_kernel<NM, XT, YT, OT>), dim3((unsigned)blocks),
+                             dim3(kMixThreads), 0, s, A);
+          MHC_CHECK_LAUNCH("mix_add_fwd_kernel");
+          return MHC_OK;
+        });
+      });
+    });
+  });
+}
+
+extern "C" size_t mhc_stream_mix_add_bwd_workspace_bytes(int64_t T, int n, int C) {
+  if (T <= 0 || n < 1 || n > MHC_MAX_N || C < 1) return 0;
+  const int V = mix_vec_width(nmax_for(n));
+  const int64_t G = mix_grid(T * ceil_div(C, V), device_cu_count());
+  return (size_t)(G + kMixSplit) * (size_t)mix_rows(n) * sizeof(float);
+}
+
+extern "C" int mhc_stream_mix_add_bwd(const void* x, int x_dtype, const void* y, int y_dtype,
+                                      const void* dout, int dout_dtype, const float* M,
+                                      const float* h_pre, const float* h_post, int h_mode,
+                                      void* dx, int dx_dtype, void* dy, int dy_dtype, float* dM,
+                                      float* dh_pre, float* dh_post, void* workspace,
+                                      size_t workspace_bytes, int64_t T, int n, int C,
+                                      void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1 && T >= 1, "invalid T=%lld / C=%d", (long long)T, C);
+  MHC_CHECK_ARG(h_mode == MHC_H_NONE || h_mode == MHC_H_ACTIVATED || h_mode == MHC_H_RAW,
+                "invalid h_mode %d", h_mode);
+  MHC_CHECK_ARG(x && dout && M && dx && dM, "null pointer argument");
+  MHC_CHECK_ARG(h_mode == MHC_H_NONE || (h_pre && h_post && dh_pre && dh_post),
+                "h_pre/h_post and their gradients are required");
+  MHC_CHECK_ARG(dx_dtype == x_dtype, "dx_dtype must equal x_dtype");
+  MHC_CHECK_ARG(!dy || !y || dy_dtype == y_dtype, "dy_dtype must equal y_dtype");
+  MHC_CHECK_ARG(dtype_bytes(x_dtype) && dtype_bytes(dout_dtype), "unknown dtype code");
+  const int V = mix_vec_width(nmax_for(n));
+  const int nch = (int)ceil_div(C, V);
+  const int64_t G = mix_grid(T * nch, device_cu_count());
+  const int P = mix_rows(n);
+  const size_t need = (size_t)(G + kMixSplit) * P * sizeof(float);
+  MHC_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
+                "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
+  MixArgs A{};
+  A.x = x; A.y = y; A.g = dout; A.out = dx; A.dy = dy; A.M = M; A.hpre = h_pre; A.hpost = h_post;
+  A.part = (float*)workspace; A.T = T; A.n = n; A.C = C; A.nchunks = nch; A.h_mode = h_mode; A.P = P;
+  const int ydt = y ? y_dtype : (dy ? dy_dtype : x_dtype);
+  A.vec = io_vec_ok(C, V, {{x, dtype_bytes(x_dtype)}, {y, dtype_bytes(ydt)},
+                           {dout, dtype_bytes(dout_dtype)}, {dy, dtype_bytes(ydt)}});
+  hipStream_t s = (hipStream_t)stream;
+  int rc;
+  if (nmax_for(n) == 0) {
+    GenArgs Gg{};
+    Gg.x = x; Gg.y = y; Gg.g = dout; Gg.out = dx; Gg.dy = dy; Gg.M = M; Gg.hpre = h_pre;
+    Gg.hpost = h_post; Gg.part = (float*)workspace; Gg.T = T; Gg.n = n; Gg.C = C; Gg.P = P;
+    Gg.h_mode = h_mode;
+    rc = gen_mix_bwd(Gg, x_dtype, ydt, dout_dtype, s, G);
+  } else rc = by_nmax(n, [&](auto nm) {
+    constexpr int NM = decltype(nm)::value;
+    return by_dtype(x_dtype, [&](auto* xp) {
+      using XT = std::remove_pointer_t<decltype(xp)>;
+      return by_pair<XT>(ydt, [&](auto* yp) {
+        using YT = std::remove_pointer_t<decltype(yp)>;
+        return by_pair<XT>(dout_dtype, [&](auto* gp) {
+          using GT = std::remove_pointer_t<decltype(gp)>;
+          hipLaunchKernelGGL((mix_add_bwd_kernel<NM, XT, YT, GT>), dim3((unsigned)G),
+                             dim3(kMixThreads), 0, s, A);
+          MHC_CHECK_LAUNCH("mix_add_bwd_kernel");
+          return MHC_OK;
+        });
+      });
+    });
+  });
+  if (rc != MHC_OK) return rc;
+  float* part2 = (float*)workspace + (size_t)G * P;
+  const int S = (int)std::min<int64_t>(kMixSplit, G);
+  const int rows = (int)ceil_div(G, S);
+  const int S_used = (int)ceil_div(G, rows);
+  hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)ceil_div(P / 4, 256), (unsigned)S_used),
+                     dim3(256), 0, s, (const float*)workspace, part2, G, P, rows);
+  MHC_CHECK_LAUNCH("reduce_rows_kernel");
+  hipLaunchKernelGGL(mix_final_kernel, dim3(1), dim3(256), (size_t)(n * n + n) * sizeof(float), s,
+                     part2, S_used, P, n, h_mode, M, h_pre, h_post, dM, dh_pre, dh_post);
+  MHC_CHECK_LAUNCH("mix_final_kernel");
+  return MHC_OK;
+}
+
+extern "C" int mhc_stream_scale_fwd(const void* x, int x_dtype, const float* h_pre, int h_mode,
+                                    void* out, int out_dtype, int64_t T, int n, int C,
+                                    void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1 && T >= 0, "invalid T=%lld / C=%d", (long long)T, C);
+  MHC_CHECK_ARG(h_mode == MHC_H_ACTIVATED || h_mode == MHC_H_RAW, "invalid h_mode %d", h_mode);
+  if (T == 0) return MHC_OK;
+  MHC_CHECK_ARG(x && h_pre && out, "null pointer argument");
+  MHC_CHECK_ARG(dtype_bytes(x_dtype) && dtype_bytes(out_dtype), "unknown dtype code");
+  MixArgs A{};
+  A.x = x; A.out = out; A.hpre = h_pre; A.T = T; A.n = n; A.C = C; A.h_mode = h_mode;
+  A.nchunks = (int)ceil_div(C, 8);
+  A.vec = io_vec_ok(C, 8, {{x, dtype_bytes(x_dtype)}, {out, dtype_bytes(out_dtype)}});
+  const int64_t bx = std::max<int64_t>(
+      1, std::min<int64_t>(ceil_div(T * A.nchunks, kMixThreads), (int64_t)device_cu_count() * 8 / n + 1));
+  hipStream_t s = (hipStream_t)stream;
+  return by_dtype(x_dtype, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    return by_pair<XT>(out_dtype, [&](auto* op) {
+      using OT = std::remove_pointer_t<decltype(op)>;
+      hipLaunchKernelGGL((scale_fwd_kernel<XT, OT>), dim3((unsigned)bx, (unsigned)n), dim3(kMixThreads),
+                         0, s, A);
+      MHC_CHECK_LAUNCH("scale_fwd_kernel");
+      return MHC_OK;
+    });
+  });
+}
+
+namespace {
+int64_t scale_bwd_grid(int64_t T, int n, int C) {
+  const int64_t nch = ceil_div(C, 8);
+  return std::max<int64_t>(
+      1, std::min<int64_t>(ceil_div(T * nch, kMixThreads), (int64_t)device_cu_count() * 8 / n + 1));
+}
+}  // namespace
+
+extern "C" size_t mhc_stream_scale_bwd_workspace_bytes(int64_t T, int n, int C) {
+  if (T <= 0 || n < 1 || n > MHC_MAX_N || C < 1) return 0;
+  const int64_t G = scale_bwd_grid(T, n, C);
+  return (size_t)(G + kMixSplit) * (size_t)round_up(n, 4) * sizeof(float);
+}
+
+extern "C" int mhc_stream_scale_bwd(const void* x, int x_dtype, const void* dout, int dout_dtype,
+                                    const float* h_pre, int h_mode, const void* dx_accum, void* dx,
+                                    int dx_dtype, float* dh_pre, void* workspace,
+                                    size_t workspace_bytes, int64_t T, int n, int C,
+                                    void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1 && T >= 1, "invalid T=%lld / C=%d", (long long)T, C);
+  MHC_CHECK_ARG(h_mode == MHC_H_ACTIVATED || h_mode == MHC_H_RAW, "invalid h_mode %d", h_mode);
+  MHC_CHECK_ARG(x && dout && h_pre && dx && dh_pre, "null pointer argument");
+  MHC_CHECK_ARG(dx_dtype == x_dtype, "dx_dtype must equal x_dtype");
+  MHC_CHECK_ARG(dtype_bytes(x_dtype) && dtype_bytes(dout_dtype), "unknown dtype code");
+  const int64_t G = scale_bwd_grid(T, n, C);
+  const int P = round_up(n, 4);
+  const size_t need = (size_t)(G + kMixSplit) * P * sizeof(float);
+  MHC_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
+                "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
+  MixArgs A{};
+  A.x = x; A.g = dout; A.acc = dx_accum; A.out = dx; A.hpre = h_pre;
+  A.part = (float*)workspace; A.T = T; A.n = n; A.C = C; A.nchunks = (int)ceil_div(C, 8);
+  A.h_mode = h_mode; A.P = P;
+  A.vec = io_vec_ok(C, 8, {{x, dtype_bytes(x_dtype)}, {dout, dtype_bytes(dout_dtype)},
+                           {dx_accum, dtype_bytes(x_dtype)}, {dx, dtype_bytes(x_dtype)}});
+  hipStream_t s = (hipStream_t)stream;
+  int rc = by_dtype(x_dtype, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    return by_pair<XT>(dout_dtype, [&](auto* gp) {
+      using GT = std::remove_pointer_t<decltype(gp)>;
+      hipLaunchKernelGGL((scale_bwd_kernel<XT, GT>), dim3((unsigned)G, (unsigned)n), dim3(kMixThreads),
+                         0, s, A);
+      MHC_CHECK_LAUNCH("scale_bwd_kernel");
+      return MHC_OK;
+    });
+  });
+  if (rc != MHC_OK) return rc;
+  float* part2 = (float*)workspace + (size_t)G * P;
+  const int S = (int)std::min<int64_t>(kMixSplit, G);
+  const int rows = (int)ceil_div(G, S);
+  const int S_used = (int)ceil_div(G, rows);
+  hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)ceil_div(P / 4, 256), (unsigned)S_used),
+                     dim3(256), 0, s, (const float*)workspace, part2, G, P, rows);
+  MHC_CHECK_LAUNCH("reduce_rows_kernel");
+  hipLaunchKernelGGL(scale_final_kernel, dim3(1), dim3(64), 0, s, part2, S_used, P, n, h_mode, h_pre,
+                     dh_pre);
+  MHC_CHECK_LAUNCH("scale_final_kernel");
+  return MHC_OK;
+}

@@ -1,0 +1,114 @@
+"""ctypes binding of libmhc_hip.so (declared in include/mhc_hip.h).
+
+The library is loaded once, from this package directory.  There is no
+fallback: if the library is missing or fails to load, every accelerated op
+raises RuntimeError naming the path and the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmhc_hip.so"
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+DTYPE_F16 = 2
+
+H_NONE = 0
+H_ACTIVATED = 1
+H_RAW = 2
+
+MAX_N = 64
+
+_VP = ctypes.c_void_p
+_I32 = ctypes.c_int
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+_SZ = ctypes.c_size_t
+_PI64 = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (argtypes, restype); must list exactly the functions of mhc_hip.h
+SIGNATURES = {
+    "mhc_abi_version": ([], _I32),
+    "mhc_last_error": ([], ctypes.c_char_p),
+    "mhc_sinkhorn_fwd": ([_VP, _VP, _I64, _I32, _I32, _F32, _VP], _I32),
+    "mhc_sinkhorn_bwd_workspace_bytes": ([_I64, _I32, _I32], _SZ),
+    "mhc_sinkhorn_bwd": ([_VP, _VP, _VP, _I64, _I32, _I32, _F32, _VP, _SZ, _VP], _I32),
+    "mhc_fused_fwd": ([_VP, _I32, _VP, _I64, _VP, _VP, _I64, _I32, _VP, _VP, _I32, _VP, _I64, _I32,
+                       _I32, _F32, _VP], _I32),
+    "mhc_fused_bwd_workspace_bytes": ([_I64, _I32, _I32, _I32], _SZ),
+    "mhc_fused_bwd_partials": ([_VP, _I32, _VP, _I32, _VP, _I64, _VP, _VP, _I64, _I32, _VP, _VP, _I32,
+                                _VP, _VP, _VP, _VP, _SZ, _I64, _I32, _I32, _F32, _PI64, _VP], _I32),
+    "mhc_reduce_param_grads": ([_VP, _SZ, _I64, _I32, _I32, _I32, _VP, _VP, _I32, _VP, _VP, _VP, _VP,
+                                _VP], _I32),
+    "mhc_fused_bwd": ([_VP, _I32, _VP, _I32, _VP, _I64, _VP, _VP, _I64, _I32, _VP, _VP, _I32, _VP, _VP,
+                       _VP, _VP, _VP, _SZ, _I64, _I32, _I32, _F32, _VP], _I32),
+    "mhc_stream_mix_add_fwd": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP, _I32, _VP, _I32, _I64, _I32, _I32,
+                                _VP], _I32),
+    "mhc_stream_mix_add_bwd_workspace_bytes": ([_I64, _I32, _I32], _SZ),
+    "mhc_stream_mix_add_bwd": ([_VP, _I32, _VP, _I32, _VP, _I32, _VP, _VP, _VP, _I32, _VP, _I32, _VP,
+                                _I32, _VP, _VP, _VP, _VP, _SZ, _I64, _I32, _I32, _VP], _I32),
+    "mhc_stream_scale_fwd": ([_VP, _I32, _VP, _I32, _VP, _I32, _I64, _I32, _I32, _VP], _I32),
+    "mhc_stream_scale_bwd_workspace_bytes": ([_I64, _I32, _I32], _SZ),
+    "mhc_stream_scale_bwd": ([_VP, _I32, _VP, _I32, _VP, _I32, _VP, _VP, _I32, _VP, _VP, _SZ, _I64,
+                              _I32, _I32, _VP], _I32),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class MHCError(RuntimeError):
+    """A HIP runtime failure reported by libmhc_hip (positive hipError_t)."""
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Load libmhc_hip.so (once) and bind every signature; raise RuntimeError if absent."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise RuntimeError(
+                f"libmhc_hip.so not found at {p}; build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)"
+            )
+        lib = ctypes.CDLL(str(p))
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        if lib.mhc_abi_version() != 1:
+            raise RuntimeError(f"{p}: unexpected ABI version {lib.mhc_abi_version()}")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load().mhc_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Translate a library status into ValueError (bad argument) / MHCError (HIP)."""
+    if rc == 0:
+        return
+    msg = last_error()
+    if rc < 0:
+        raise ValueError(f"{what}: {msg}")
+    raise MHCError(f"{what}: HIP error {rc}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))

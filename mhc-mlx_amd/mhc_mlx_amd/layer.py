@@ -1,0 +1,303 @@
+"""MHCLayer / MHCRewire: torch modules with the reference's constructor and
+call contract (mhc_mlx/layer.py:58-492), backed by libmhc_hip on MI355X.
+
+Forward semantics (layer.py:1-12):
+  H_pre_act = sigmoid(H_pre_raw), H_post_act = 2 sigmoid(H_post_raw)
+  M = sinkhorn_knopp(exp(H_res_raw))
+  out = stream_mix(x, M) + H_post_act * rms_norm(sum_i H_pre_act[i] x[:, i], w)
+
+Paths:
+* accelerated (default, ``use_metal=True``): one autograd Function per call
+  (Sinkhorn + fused kernel forward; fused backward + reduction + Sinkhorn
+  VJP), all in libmhc_hip.  GPU tensors are required; errors raise.
+* reference (``use_metal=False`` or ``MHC_MLX_DISABLE_METAL=1`` /
+  ``MHC_HIP_DISABLE=1``): the torch restatement in reference.py, as the
+  reference layer does (layer.py:122-126, 423-431).
+
+The reference's dispatch-policy knobs are accepted with the same validation
+and the same predicates (``_should_avoid_fused`` etc.).  On MI355X every
+branch they select is served by the HIP kernels: the reference used them to
+route around slow Metal shapes, which this library does not have.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from . import reference as ref
+
+__all__ = ["MHCLayer", "MHCRewire"]
+
+
+def _disabled_by_env() -> bool:
+    return os.getenv("MHC_MLX_DISABLE_METAL", "0") == "1" or os.getenv("MHC_HIP_DISABLE", "0") == "1"
+
+
+class MHCLayer(nn.Module):
+    def __init__(
+        self,
+        n: int,
+        C: int,
+        sinkhorn_iters: int = 20,
+        eps: float = 1e-5,
+        use_metal: bool = True,
+        threads_per_group: int | None = 256,
+        identity_init: bool = True,
+        auto_dispatch: bool = True,
+        compile_reference: bool | None = None,
+        dispatch_policy: str = "auto",
+        hybrid_latency: bool = False,
+        hybrid_min_C: int = 8192,
+        latency_avoid_fused_n32_max_C: int = 2048,
+        latency_avoid_fused_B1_min_n: int = 16,
+        throughput_allow_fused_n32_min_B: int = 8,
+        throughput_allow_fused_n32_min_C: int = 4096,
+        throughput_allow_fused_n32_small_C: int = 512,
+        fused_backward: bool = False,
+        mix_kernel: str = "auto",
+        *,
+        use_hip: bool | None = None,
+        device=None,
+    ):
+        super().__init__()
+        # layer.py:83-102
+        if n <= 0:
+            raise ValueError("n must be positive")
+        if C <= 0:
+            raise ValueError("C must be positive")
+        if dispatch_policy not in {"auto", "throughput", "latency"}:
+            raise ValueError("dispatch_policy must be one of: auto, throughput, latency")
+        if hybrid_min_C <= 0:
+            raise ValueError("hybrid_min_C must be positive")
+        if latency_avoid_fused_n32_max_C <= 0:
+            raise ValueError("latency_avoid_fused_n32_max_C must be positive")
+        if latency_avoid_fused_B1_min_n <= 0:
+            raise ValueError("latency_avoid_fused_B1_min_n must be positive")
+        if throughput_allow_fused_n32_min_B <= 0:
+            raise ValueError("throughput_allow_fused_n32_min_B must be positive")
+        if throughput_allow_fused_n32_min_C <= 0:
+            raise ValueError("throughput_allow_fused_n32_min_C must be positive")
+        if throughput_allow_fused_n32_small_C < 0:
+            raise ValueError("throughput_allow_fused_n32_small_C must be >= 0")
+        if mix_kernel not in {"auto", "1d", "2d"}:
+            raise ValueError("mix_kernel must be one of: auto, 1d, 2d")
+
+        self.n = int(n)
+        self.C = int(C)
+        self.sinkhorn_iters = int(sinkhorn_iters)
+        self.eps = float(eps)
+        self.auto_dispatch = bool(auto_dispatch)
+        self.dispatch_policy = str(dispatch_policy)
+        self.hybrid_latency = bool(hybrid_latency)
+        self.hybrid_min_C = int(hybrid_min_C)
+        self.latency_avoid_fused_n32_max_C = int(latency_avoid_fused_n32_max_C)
+        self.latency_avoid_fused_B1_min_n = int(latency_avoid_fused_B1_min_n)
+        self.throughput_allow_fused_n32_min_B = int(throughput_allow_fused_n32_min_B)
+        self.throughput_allow_fused_n32_min_C = int(throughput_allow_fused_n32_min_C)
+        self.throughput_allow_fused_n32_small_C = int(throughput_allow_fused_n32_small_C)
+        self.fused_backward = bool(fused_backward)
+        self.mix_kernel = str(mix_kernel)
+        accel = bool(use_metal) if use_hip is None else bool(use_hip)
+        # layer.py:121-126 (Metal availability is HIP availability here)
+        self.metal_available = True
+        self.use_metal = False if _disabled_by_env() else accel
+        self.threads_per_group = None if threads_per_group is None else int(threads_per_group)
+        self.identity_init = bool(identity_init)
+        if compile_reference is None:
+            self.compile_reference = self.use_metal and self.auto_dispatch
+        else:
+            self.compile_reference = bool(compile_reference)
+
+        # layer.py:139-153: identity-friendly init
+        kw = dict(dtype=torch.float32, device=device)
+        if self.identity_init:
+            off = 12.0
+            self.H_pre_raw = nn.Parameter(torch.full((self.n,), -off, **kw))
+            self.H_post_raw = nn.Parameter(torch.full((self.n,), -off, **kw))
+            self.H_res_raw = nn.Parameter(torch.full((self.n, self.n), -off, **kw) + torch.eye(self.n, **kw) * off)
+        else:
+            self.H_pre_raw = nn.Parameter(torch.zeros((self.n,), **kw))
+            self.H_post_raw = nn.Parameter(torch.zeros((self.n,), **kw))
+            self.H_res_raw = nn.Parameter(torch.zeros((self.n, self.n), **kw))
+        self.rms_weight = nn.Parameter(torch.ones((self.C,), **kw))
+
+    @property
+    def use_hip(self) -> bool:
+        return self.use_metal
+
+    # ---- policy predicates (layer.py:175-244), kept with identical results
+    def _should_use_metal(self, B: int, n: int, C: int) -> bool:
+        if _disabled_by_env():
+            return False
+        if not self.use_metal:
+            return False
+        if n > 64:
+            return False
+        return True
+
+    def _latency_policy_enabled(self) -> bool:
+        return self.dispatch_policy == "latency"
+
+    def _throughput_policy_enabled(self) -> bool:
+        return self.dispatch_policy == "throughput"
+
+    def _should_avoid_fused_latency(self, B: int, n: int, C: int) -> bool:
+        if n == 32 and C <= self.latency_avoid_fused_n32_max_C:
+            return True
+        if B == 1 and n >= self.latency_avoid_fused_B1_min_n:
+            return True
+        return False
+
+    def _should_avoid_fused_throughput(self, B: int, n: int, C: int) -> bool:
+        if n != 32:
+            return False
+        if B < self.throughput_allow_fused_n32_min_B:
+            return True
+        allow_small = self.throughput_allow_fused_n32_small_C > 0 and C == self.throughput_allow_fused_n32_small_C
+        allow_large = C >= self.throughput_allow_fused_n32_min_C
+        return not (allow_small or allow_large)
+
+    def _should_avoid_fused(self, B: int, n: int, C: int) -> bool:
+        if not self.use_metal or not self.auto_dispatch:
+            return False
+        lat, thr = self._latency_policy_enabled(), self._throughput_policy_enabled()
+        if not (lat or thr):
+            return False
+        if lat and self._should_avoid_fused_latency(B, n, C):
+            return True
+        if thr and self._should_avoid_fused_throughput(B, n, C):
+            return True
+        return False
+
+    def _should_use_hybrid(self, B: int, n: int, C: int) -> bool:
+        if not self.use_metal or not self.auto_dispatch or not self.hybrid_latency:
+            return False
+        if not self._latency_policy_enabled():
+            return False
+        return n == 32 and B == 1 and C >= self.hybrid_min_C
+
+    def _should_use_reference_fallback(self, B: int, n: int, C: int) -> bool:
+        if not self.use_metal or not self.auto_dispatch:
+            return False
+        if not self._should_avoid_fused(B, n, C):
+            return False
+        return not self._should_use_hybrid(B, n, C)
+
+    def _should_use_fused_backward(self, B: int, n: int, C: int) -> bool:
+        return bool(self.fused_backward)
+
+    # ---- API
+    def mixing_matrix(self) -> torch.Tensor:
+        """Current mixing matrix M = sinkhorn(exp(H_res_raw)) (layer.py:155-173)."""
+        if self.use_metal and self.H_res_raw.is_cuda and not _disabled_by_env():
+            return ops.sinkhorn_knopp_hip_autograd(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps,
+                                                   threads_per_group=self.threads_per_group)
+        return ref.mixing_matrix_from_logits(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps)
+
+    def _reference_forward(self, x, H_pre_raw, H_post_raw, H_res_raw, rms_weight):
+        return ref.mhc_forward_reference(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight,
+                                         sinkhorn_iters=self.sinkhorn_iters, eps=self.eps)
+
+    def post_combine(self, x_reshaped: torch.Tensor, y_inner_reshaped: torch.Tensor) -> torch.Tensor:
+        """H_post * (y_inner + (M diag(H_pre)) x) on [B, n, C] views (layer.py:302-337); fp32 out."""
+        if self.use_metal and not _disabled_by_env():
+            return ops.post_combine(x_reshaped, y_inner_reshaped, self.H_pre_raw, self.H_post_raw, self.H_res_raw,
+                                    sinkhorn_iters=self.sinkhorn_iters, eps=self.eps)
+        H_pre_act, H_post_act = ref.activate_pre_post(self.H_pre_raw, self.H_post_raw)
+        M = ref.mixing_matrix_from_logits(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps)
+        M_final = M * H_pre_act.reshape(1, -1)
+        x_mixed = torch.einsum("ij,...jd->...id", M_final, x_reshaped.to(M_final.dtype))
+        return (y_inner_reshaped.to(x_mixed.dtype) + x_mixed) * H_post_act.reshape(1, self.n, 1)
+
+    def _check(self, x: torch.Tensor):
+        if x.ndim != 3:
+            raise ValueError(f"x_expanded must be [B, n, C], got shape {tuple(x.shape)}")
+        B, n, C = (int(s) for s in x.shape)
+        if n != self.n:
+            raise ValueError(f"x_expanded n={n} does not match layer n={self.n}")
+        if C != self.C:
+            raise ValueError(f"x_expanded C={C} does not match layer C={self.C}")
+        return B, n, C
+
+    @staticmethod
+    def _kernel_out_dtype(x: torch.Tensor, return_dtype):
+        # layer.py:361-364: emit a half type directly only when it matches x
+        if return_dtype is not None and return_dtype == x.dtype and return_dtype in (torch.float16, torch.bfloat16):
+            return return_dtype
+        return None
+
+    def forward(self, x_expanded: torch.Tensor, *, return_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """Run the mHC layer on x_expanded [B, n, C] (layer.py:339-435)."""
+        B, n, C = self._check(x_expanded)
+        if self._should_use_metal(B, n, C):
+            out = ops.mhc_layer_forward(x_expanded, self.H_pre_raw, self.H_post_raw, self.H_res_raw, self.rms_weight,
+                                        sinkhorn_iters=self.sinkhorn_iters, eps=self.eps,
+                                        output_dtype=self._kernel_out_dtype(x_expanded, return_dtype))
+        else:
+            out = self._reference_forward(x_expanded, self.H_pre_raw, self.H_post_raw, self.H_res_raw,
+                                          self.rms_weight)
+        if return_dtype is not None and out.dtype != return_dtype:
+            out = out.to(return_dtype)
+        return out
+
+    def forward_dynamic(self, x_expanded: torch.Tensor, H_pre_raw: torch.Tensor, H_post_raw: torch.Tensor,
+                        H_res_raw: torch.Tensor, *, return_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """Per-token mappings (extension): H_pre_raw, H_post_raw [B, n]; H_res_raw [B, n, n] logits.
+
+        Uses this layer's rms_weight, sinkhorn_iters and eps.
+        """
+        B, n, C = self._check(x_expanded)
+        if tuple(H_pre_raw.shape) != (B, n) or tuple(H_post_raw.shape) != (B, n):
+            raise ValueError(f"H_pre_raw / H_post_raw must be [B, n]=[{B}, {n}]")
+        if tuple(H_res_raw.shape) != (B, n, n):
+            raise ValueError(f"H_res_raw must be [B, n, n]=[{B}, {n}, {n}], got {tuple(H_res_raw.shape)}")
+        if self._should_use_metal(B, n, C):
+            out = ops.mhc_layer_forward_dynamic(x_expanded, H_pre_raw, H_post_raw, H_res_raw, self.rms_weight,
+                                                sinkhorn_iters=self.sinkhorn_iters, eps=self.eps,
+                                                output_dtype=self._kernel_out_dtype(x_expanded, return_dtype))
+        else:
+            out = self._reference_forward(x_expanded, H_pre_raw, H_post_raw, H_res_raw, self.rms_weight)
+        if return_dtype is not None and out.dtype != return_dtype:
+            out = out.to(return_dtype)
+        return out
+
+
+class MHCRewire(nn.Module):
+    """Wrap any dims -> dims module with mHC residual mixing (layer.py:438-492).
+
+    out = H_post * (inner(H_pre * x) + (M diag(H_pre)) x), with x [..., dims]
+    viewed as n streams of C = dims // n channels.
+    """
+
+    def __init__(self, inner: nn.Module, dims: int, n: int = 32, **mhc_kwargs):
+        super().__init__()
+        self.inner = inner
+        self.n = n
+        self.dims = dims
+        if dims % n != 0:
+            raise ValueError(f"dims {dims} must be divisible by n={n}")
+        self.mhc = MHCLayer(n=n, C=dims // n, **mhc_kwargs)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        dims = x.shape[-1]
+        if dims % self.n != 0:
+            raise ValueError(f"input dims {dims} must be divisible by n={self.n}")
+        C = dims // self.n
+        x3 = x.reshape(-1, self.n, C)
+        hip = self.mhc.use_metal and not _disabled_by_env()
+        if hip:
+            x_pre = ops.stream_scale(x3, self.mhc.H_pre_raw)
+        else:
+            H_pre_act, _ = ref.activate_pre_post(self.mhc.H_pre_raw, self.mhc.H_post_raw)
+            x_pre = x3 * H_pre_act.reshape(1, self.n, 1).to(x3.dtype)
+        y_inner = self.inner(x_pre.reshape(x.shape))
+        if tuple(y_inner.shape) != tuple(x.shape):
+            raise ValueError(
+                f"inner module must preserve the shape: got {tuple(y_inner.shape)} for input {tuple(x.shape)}"
+            )
+        out = self.mhc.post_combine(x3, y_inner.reshape(-1, self.n, C))
+        return out.reshape(x.shape)

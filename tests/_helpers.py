@@ -1,0 +1,56 @@
+"""Shared test helpers: seeded inputs, dtype rounding, error metrics."""
+
+import numpy as np
+import torch
+
+from oracle import mhc_oracle as O
+
+TORCH_DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.default_rng(seed)
+
+
+def to_dtype_np(a: np.ndarray, dt: str) -> np.ndarray:
+    """Round float data to dt's grid (returned as float32 values)."""
+    a = np.asarray(a, dtype=np.float32)
+    if dt == "bf16":
+        return O.bf16_round(a)
+    if dt == "f16":
+        return O.f16_round(a)
+    return a
+
+
+def dev_tensor(a: np.ndarray, dt: str = "f32", device: str = "cuda") -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device).to(TORCH_DT[dt])
+
+
+def np_of(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def rel_err(got, ref) -> float:
+    """max |got - ref| / max(max |ref|, tiny)  (the reference tests' relative metric)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = max(float(np.abs(ref).max()) if ref.size else 0.0, 1e-30)
+    return float(np.abs(got - ref).max()) / den if ref.size else 0.0
+
+
+def max_abs(got, ref) -> float:
+    return float(np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64)).max())
+
+
+# tolerance per output dtype (reference tests: fp32 1e-5, fp16 5e-3, bf16 2e-2)
+TOL = {"f32": 1e-5, "f16": 5e-3, "bf16": 2e-2}
+
+
+def params(g: np.random.Generator, n: int, C: int, per_token_B: int | None = None):
+    """Seeded raw parameters: N(0,1) logits, rms weight 1 + 0.02 N(0,1)."""
+    shp = (n,) if per_token_B is None else (per_token_B, n)
+    hpre = g.standard_normal(shp).astype(np.float32)
+    hpost = g.standard_normal(shp).astype(np.float32)
+    hres = g.standard_normal(shp + (n,)).astype(np.float32)
+    w = (1.0 + 0.02 * g.standard_normal(C)).astype(np.float32)
+    return hpre, hpost, hres, w

@@ -1,0 +1,156 @@
+"""GPU tests of the MHCLayer module contract (reference layer.py / tests).
+
+Mirrors test_layer_forward_matches_reference (test_correctness.py:223-251),
+test_latency_fallback_corner (:254-291), test_backward_matches_reference
+(:294-344, here with every gradient compared), test_reference_fallback
+(:346-360), test_determinism.py and test_concurrency.py.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mhc_oracle as O
+from tests._helpers import dev_tensor, np_of, params, rel_err, rng, to_dtype_np
+
+from mhc_mlx_amd import MHCLayer, _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _set(layer, hpre, hpost, hres, w):
+    with torch.no_grad():
+        layer.H_pre_raw.copy_(torch.from_numpy(hpre))
+        layer.H_post_raw.copy_(torch.from_numpy(hpost))
+        layer.H_res_raw.copy_(torch.from_numpy(hres))
+        layer.rms_weight.copy_(torch.from_numpy(w))
+
+
+@pytest.mark.parametrize("B,n,C", [(1, 4, 64), (2, 8, 128), (2, 16, 256), (1, 32, 256)])
+def test_layer_forward_matches_reference(B, n, C):
+    g = rng(100 + n)
+    x = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    hpre, hpost, hres, _ = params(g, n, C)
+    w = np.ones(C, np.float32)
+    hip = MHCLayer(n=n, C=C, auto_dispatch=False).cuda()
+    refl = MHCLayer(n=n, C=C, use_metal=False).cuda()
+    for l in (hip, refl):
+        _set(l, hpre, hpost, hres, w)
+    xt = dev_tensor(x, "bf16")
+    y_hip, y_ref = np_of(hip(xt)), np_of(refl(xt))
+    oracle = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=1e-5)
+    for y in (y_hip, y_ref):
+        assert np.abs(y - oracle).max() < 1e-4 and rel_err(y, oracle) < 1e-4
+    assert hip(xt).dtype == torch.float32
+
+
+def test_latency_policy_corner_uses_hip():
+    B, n, C = 1, 32, 1024
+    g = rng(7)
+    x = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    hpre, hpost, hres, w = params(g, n, C)
+    auto = MHCLayer(n=n, C=C, dispatch_policy="latency", hybrid_latency=True).cuda()
+    _set(auto, hpre, hpost, hres, w)
+    assert auto._should_use_reference_fallback(B, n, C)
+    out = np_of(auto(dev_tensor(x, "bf16")))
+    oracle = O.mhc_forward_reference(x, hpre, hpost, hres, w)
+    assert rel_err(out, oracle) < 1e-4
+
+
+@pytest.mark.parametrize("ret", [None, torch.bfloat16, torch.float16, torch.float32])
+def test_return_dtype_semantics(ret):
+    n, C = 4, 256
+    layer = MHCLayer(n=n, C=C, identity_init=False).cuda()
+    x = torch.randn(3, n, C, device="cuda", dtype=torch.bfloat16)
+    out = layer(x, return_dtype=ret)
+    assert out.dtype == (torch.float32 if ret is None else ret)
+
+
+def test_layer_backward_matches_oracle_all_grads():
+    """Reference test_backward_matches_reference (B=1, n=4, C=16, 5 iterations), all grads."""
+    B, n, C = 1, 4, 16
+    g = rng(9)
+    x = g.standard_normal((B, n, C)).astype(np.float32)
+    dout = g.standard_normal((B, n, C)).astype(np.float32)
+    hpre, hpost, hres, w = params(g, n, C)
+    layer = MHCLayer(n=n, C=C, sinkhorn_iters=5).cuda()
+    _set(layer, hpre, hpost, hres, w)
+    xt = dev_tensor(x).requires_grad_(True)
+    out = layer(xt)
+    ref_out = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=5)
+    assert abs(float(out.sum()) - ref_out.sum()) < 1e-4  # the reference test's loss check
+    out.backward(dev_tensor(dout))
+    ref = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=5)
+    gots = [np_of(xt.grad), np_of(layer.H_pre_raw.grad), np_of(layer.H_post_raw.grad),
+            np_of(layer.H_res_raw.grad), np_of(layer.rms_weight.grad)]
+    for got, r in zip(gots, ref):
+        assert rel_err(got, r) < 1e-4
+
+
+def test_sum_loss_gives_zero_h_res_gradient():
+    """loss = sum(out): dM = 1 c^T has constant columns, so dH_res vanishes."""
+    layer = MHCLayer(n=4, C=16, identity_init=False).cuda()
+    with torch.no_grad():
+        layer.H_res_raw.normal_()
+    x = torch.randn(3, 4, 16, device="cuda")
+    layer(x).sum().backward()
+    assert layer.H_res_raw.grad.abs().max().item() < 1e-5
+
+
+def test_env_disable_forces_reference(monkeypatch):
+    monkeypatch.setenv("MHC_MLX_DISABLE_METAL", "1")
+    layer = MHCLayer(n=4, C=16).cuda()
+    assert layer._should_use_metal(1, 4, 16) is False
+    y = layer(torch.randn(1, 4, 16, device="cuda"))
+    assert y.shape == (1, 4, 16)
+
+
+def test_hip_path_is_the_one_that_runs(monkeypatch):
+    """The accelerated layer must call the library (no silent torch path)."""
+    calls = []
+    orig = _lib.call
+
+    def spy(name, *args):
+        calls.append(name)
+        return orig(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    layer = MHCLayer(n=4, C=128).cuda()
+    x = torch.randn(2, 4, 128, device="cuda", requires_grad=True)
+    layer(x).sum().backward()
+    for k in ("mhc_sinkhorn_fwd", "mhc_fused_fwd", "mhc_fused_bwd_partials", "mhc_reduce_param_grads",
+              "mhc_sinkhorn_bwd"):
+        assert k in calls
+
+
+def test_determinism_and_state_dict():
+    torch.manual_seed(42)
+    a = MHCLayer(n=16, C=64, identity_init=False).cuda()
+    b = MHCLayer(n=16, C=64, identity_init=False).cuda()
+    b.load_state_dict(a.state_dict())
+    assert list(a.state_dict().keys()) == ["H_pre_raw", "H_post_raw", "H_res_raw", "rms_weight"]
+    x = torch.randn(1, 16, 64, device="cuda")
+    assert torch.equal(a(x), b(x))
+
+
+def test_mixing_matrix_doubly_stochastic_and_bomb():
+    layer = MHCLayer(n=32, C=64).cuda()
+    with torch.no_grad():
+        layer.H_res_raw.fill_(100.0)
+    M = layer.mixing_matrix()
+    assert torch.isfinite(M).all()
+    assert (M.sum(1) - 1).abs().max().item() <= 1e-3 and (M.sum(0) - 1).abs().max().item() <= 1e-3
+
+
+def test_forward_dynamic_api():
+    B, n, C = 4, 16, 64
+    g = rng(3)
+    x = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=B)
+    layer = MHCLayer(n=n, C=C).cuda()
+    with torch.no_grad():
+        layer.rms_weight.copy_(torch.from_numpy(w))
+    out = layer.forward_dynamic(dev_tensor(x, "bf16"), dev_tensor(hpre), dev_tensor(hpost), dev_tensor(hres),
+                                return_dtype=torch.bfloat16)
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w)
+    assert out.dtype == torch.bfloat16 and rel_err(np_of(out), ref) < 2e-2

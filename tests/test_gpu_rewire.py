@@ -1,0 +1,137 @@
+"""GPU parity: MHCRewire kernels (post-combine, pre-scale, stream_mix_add).
+
+Mirrors tests/test_rewire.py and tests/test_folding.py of the reference,
+plus gradient comparisons with the float64 oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mhc_oracle as O
+from tests._helpers import dev_tensor, np_of, params, rel_err, rng, to_dtype_np
+
+from mhc_mlx_amd import MHCRewire, ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("B,n,C", [(3, 4, 64), (2, 16, 16), (2, 32, 16), (4, 3, 10), (2, 8, 1024)])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_post_combine_matches_oracle(B, n, C, xdt):
+    g = rng(40 + B + n + C)
+    x = to_dtype_np(g.standard_normal((B, n, C)), xdt)
+    y = to_dtype_np(g.standard_normal((B, n, C)), xdt)
+    dout = g.standard_normal((B, n, C)).astype(np.float32)
+    hpre, hpost, hres, _ = params(g, n, C)
+    xt = dev_tensor(x, xdt).requires_grad_(True)
+    yt = dev_tensor(y, xdt).requires_grad_(True)
+    ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres)]
+    out = ops.post_combine(xt, yt, *ps, sinkhorn_iters=20, eps=1e-5)
+    assert out.dtype == torch.float32
+    ref = O.post_combine(x, y, hpre, hpost, hres, 20, 1e-5)
+    assert rel_err(np_of(out), ref) < 1e-5
+    out.backward(dev_tensor(dout))
+    refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    gots = [np_of(xt.grad), np_of(yt.grad)] + [np_of(t.grad) for t in ps]
+    for name, got, r in zip(["dx", "dy", "dH_pre", "dH_post", "dH_res"], gots, refs):
+        tol = (1e-5 if xdt == "f32" else 2e-2) if name in ("dx", "dy") else 1e-4
+        assert rel_err(got, r) < tol, (name, B, n, C, xdt, rel_err(got, r))
+
+
+@pytest.mark.parametrize("n,C", [(4, 64), (16, 16), (32, 8), (3, 9)])
+def test_stream_mix_add_matches_reference_semantics(n, C):
+    """stream_mix_add_metal: out = M x + y_dist (fp32); VJP dx = M^T g, dM = sum g x^T, dy = g."""
+    B = 3
+    g = rng(60 + n)
+    x = g.standard_normal((B, n, C)).astype(np.float32)
+    yd = g.standard_normal((B, n, C)).astype(np.float32)
+    M = g.random((n, n)).astype(np.float32)
+    dout = g.standard_normal((B, n, C)).astype(np.float32)
+    xt, Mt, yt = (dev_tensor(v).requires_grad_(True) for v in (x, M, yd))
+    out = ops.stream_mix_add_hip_autograd(xt, Mt, yt)
+    assert rel_err(np_of(out), np.einsum("ij,bjc->bic", M, x) + yd) < 1e-5
+    out.backward(dev_tensor(dout))
+    assert rel_err(np_of(xt.grad), np.einsum("ij,bic->bjc", M, dout)) < 1e-5
+    assert rel_err(np_of(Mt.grad), np.einsum("bic,bjc->ij", dout, x)) < 1e-5
+    assert rel_err(np_of(yt.grad), dout) == 0.0
+
+
+@pytest.mark.parametrize("n,C", [(4, 64), (16, 16), (64, 8), (5, 11)])
+def test_stream_scale_matches_oracle(n, C):
+    B = 4
+    g = rng(70 + n)
+    x = g.standard_normal((B, n, C)).astype(np.float32)
+    hpre = g.standard_normal(n).astype(np.float32)
+    dout = g.standard_normal((B, n, C)).astype(np.float32)
+    xt, ht = dev_tensor(x).requires_grad_(True), dev_tensor(hpre).requires_grad_(True)
+    out = ops.stream_scale(xt, ht)
+    a = O.sigmoid(hpre)
+    assert rel_err(np_of(out), x * a[None, :, None]) < 1e-6
+    out.backward(dev_tensor(dout))
+    assert rel_err(np_of(xt.grad), dout * a[None, :, None]) < 1e-6
+    ref_dh = np.einsum("bic,bic->i", dout, x) * a * (1 - a)
+    assert rel_err(np_of(ht.grad), ref_dh) < 1e-5
+
+
+@pytest.mark.parametrize("dims,n,T", [(64, 4, 3), (256, 16, 2), (512, 32, 2), (4096, 4, 16)])
+def test_rewire_linear_matches_oracle(dims, n, T):
+    g = rng(dims + n)
+    torch.manual_seed(dims)
+    lin = torch.nn.Linear(dims, dims, bias=False).cuda()
+    with torch.no_grad():
+        lin.weight.copy_(torch.from_numpy((0.02 * g.standard_normal((dims, dims))).astype(np.float32)))
+    model = MHCRewire(lin, dims=dims, n=n).cuda()
+    hpre, hpost, hres, _ = params(g, n, dims // n)
+    with torch.no_grad():
+        model.mhc.H_pre_raw.copy_(torch.from_numpy(hpre))
+        model.mhc.H_post_raw.copy_(torch.from_numpy(hpost))
+        model.mhc.H_res_raw.copy_(torch.from_numpy(hres))
+    x = g.standard_normal((T, dims)).astype(np.float32)
+    dout = g.standard_normal((T, dims)).astype(np.float32)
+    xt = dev_tensor(x).requires_grad_(True)
+    out = model(xt)
+    W = lin.weight.detach().cpu().numpy()
+    ref_out, _ = O.rewire_linear_forward(x, W, hpre, hpost, hres)
+    # the inner GEMM runs in torch (TF32 off by default on ROCm fp32 GEMMs)
+    assert rel_err(np_of(out), ref_out) < 1e-4
+    out.backward(dev_tensor(dout))
+    dx, dW, dpre, dpost, dres = O.rewire_linear_backward(x, W, hpre, hpost, hres, dout)
+    assert rel_err(np_of(xt.grad), dx) < 1e-4
+    assert rel_err(np_of(lin.weight.grad), dW) < 1e-4
+    assert rel_err(np_of(model.mhc.H_pre_raw.grad), dpre) < 1e-4
+    assert rel_err(np_of(model.mhc.H_post_raw.grad), dpost) < 1e-4
+    assert rel_err(np_of(model.mhc.H_res_raw.grad), dres) < 1e-4
+
+
+def test_rewire_folded_equals_explicit():
+    """Reference test_weight_folding_correctness: same params, same output (<1e-5)."""
+    dims, n = 256, 16
+    torch.manual_seed(42)
+    lin = torch.nn.Linear(dims, dims).cuda()
+
+    class NoFold(torch.nn.Module):
+        def __init__(self, l):
+            super().__init__()
+            self.l = l
+
+        def forward(self, x):
+            return self.l(x)
+
+    a = MHCRewire(lin, dims=dims, n=n).cuda()
+    b = MHCRewire(NoFold(lin), dims=dims, n=n).cuda()
+    b.mhc.load_state_dict(a.mhc.state_dict())
+    x = torch.randn(1, dims, device="cuda")
+    assert (a(x) - b(x)).abs().max().item() < 1e-5
+
+
+def test_rewire_shapes_and_errors():
+    dims, n = 512, 16
+    model = MHCRewire(torch.nn.Linear(dims, dims), dims=dims, n=n).cuda()
+    y = model(torch.randn(2, dims, device="cuda"))
+    assert y.shape == (2, dims) and model.mhc.n == n and model.mhc.C == dims // n
+    bad = MHCRewire(torch.nn.Linear(dims, 256), dims=dims, n=32).cuda()
+    with pytest.raises(ValueError):
+        bad(torch.randn(1, dims, device="cuda"))
+    blk = MHCRewire(torch.nn.Sequential(torch.nn.RMSNorm(1024), torch.nn.Linear(1024, 1024)), dims=1024, n=32).cuda()
+    assert blk(torch.randn(1, 16, 1024, device="cuda")).shape == (1, 16, 1024)

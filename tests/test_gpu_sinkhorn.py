@@ -1,0 +1,159 @@
+"""GPU parity: batched Sinkhorn-Knopp forward and VJP vs the oracle.
+
+Mirrors the reference's tests/test_correctness.py:33-49 (n=4/20 iters tol
+1e-5; n=16/10 iters tol 1e-4 there, 1e-5 here), tests/test_stability.py
+(logits all 100.0, n=32) and tests/test_stress.py:17-31 (eps 1e-3 / 1e-6),
+plus eps-mask cases and the doubly-stochastic residual criterion.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mhc_oracle as O
+from tests._helpers import dev_tensor, np_of, rng
+
+from mhc_mlx_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _fwd(H: np.ndarray, iters: int, eps: float) -> np.ndarray:
+    return np_of(ops.sinkhorn_knopp_hip(dev_tensor(H), iters=iters, eps=eps))
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8, 12, 16, 24, 32, 64])
+@pytest.mark.parametrize("iters", [0, 1, 5, 20])
+def test_sinkhorn_fwd_matches_oracle(n, iters):
+    g = rng(1000 + n * 7 + iters)
+    batch = 5
+    H = g.standard_normal((batch, n, n)).astype(np.float32)
+    got = _fwd(H, iters, 1e-5)
+    ref = O.mixing_matrix_from_logits(H, iters=iters, eps=1e-5)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() < 1e-5, (n, iters, np.abs(got - ref).max())
+
+
+@pytest.mark.parametrize("n,iters,tol", [(4, 20, 1e-5), (16, 10, 1e-5)])
+def test_sinkhorn_single_matrix_reference_tolerances(n, iters, tol):
+    H = rng(0).standard_normal((n, n)).astype(np.float32)
+    got = _fwd(H, iters, 1e-5)
+    ref = O.mixing_matrix_from_logits(H, iters=iters, eps=1e-5)
+    assert got.shape == (n, n)
+    assert np.abs(got - ref).max() < tol
+
+
+@pytest.mark.parametrize("eps", [1e-3, 1e-6])
+def test_sinkhorn_eps_extremes(eps):
+    H = rng(123).standard_normal((8, 8)).astype(np.float32)
+    got = _fwd(H, 20, eps)
+    ref = O.mixing_matrix_from_logits(H, iters=20, eps=eps)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() < 1e-5
+
+
+def test_sinkhorn_bomb_logits_n32():
+    H = np.full((32, 32), 100.0, dtype=np.float32)
+    got = _fwd(H, 20, 1e-5)
+    assert np.isfinite(got).all()
+    assert np.abs(got.sum(1) - 1).max() <= 1e-3 and np.abs(got.sum(0) - 1).max() <= 1e-3
+    assert np.abs(got - 1.0 / 32).max() < 1e-6
+
+
+def test_sinkhorn_identity_init():
+    n = 8
+    H = (np.full((n, n), -12.0) + np.eye(n) * 12.0).astype(np.float32)
+    got = _fwd(H, 20, 1e-5)
+    assert np.abs(got - np.eye(n)).max() < 1e-4
+
+
+def test_sinkhorn_masked_columns_and_rows():
+    # column 2 is ~e^-40 after the row-max shift: its sum falls below eps and
+    # the reference zeroes it; row 3 then carries (almost) nothing.
+    n = 6
+    g = rng(7)
+    H = g.standard_normal((3, n, n)).astype(np.float32)
+    H[:, :, 2] = -40.0
+    H[1, 3, :] = -45.0
+    H[1, 3, 2] = 0.0
+    for eps in (1e-5, 1e-3):
+        got = _fwd(H, 20, eps)
+        ref = O.mixing_matrix_from_logits(H.astype(np.float64), iters=20, eps=eps)
+        assert np.abs(got - ref).max() < 1e-5
+
+
+@pytest.mark.parametrize("n,batch", [(4, 16384), (16, 1024)])
+def test_sinkhorn_ds_residual(n, batch):
+    """Row/column-sum residual: <= max(1e-5, oracle(fp32) residual + 1e-6)."""
+    H = rng(5 + n).standard_normal((batch, n, n)).astype(np.float32)
+    got = _fwd(H, 20, 1e-6)
+    ref32 = O.mixing_matrix_from_logits(H, iters=20, eps=1e-6, dtype=np.float32)
+    assert O.ds_residual(got) <= max(1e-5, O.ds_residual(ref32) + 1e-6)
+    # column sums are exactly normalised by the last step
+    assert np.abs(got.sum(-2) - 1).max() < 1e-5
+
+
+# ------------------------------------------------------------------ VJP
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 7, 8, 16, 24, 32, 64])
+@pytest.mark.parametrize("iters", [1, 5, 20])
+def test_sinkhorn_vjp_matches_oracle(n, iters):
+    g = rng(3000 + n * 3 + iters)
+    batch = 3
+    H = g.standard_normal((batch, n, n)).astype(np.float32)
+    dM = g.standard_normal((batch, n, n)).astype(np.float32)
+    Ht = dev_tensor(H).requires_grad_(True)
+    M = ops.sinkhorn_knopp_hip_autograd(Ht, iters=iters, eps=1e-5)
+    M.backward(dev_tensor(dM))
+    got = np_of(Ht.grad)
+    ref = O.sinkhorn_knopp_vjp(H, dM, iters=iters, eps=1e-5)
+    scale = max(np.abs(ref).max(), 1e-3)
+    assert np.abs(got - ref).max() / scale < 1e-4, (n, iters, np.abs(got - ref).max(), scale)
+    # row sums of dH vanish (row-shift invariance)
+    assert np.abs(got.sum(-1)).max() < 1e-4 * max(1.0, np.abs(dM).max())
+
+
+def test_sinkhorn_vjp_masked_columns():
+    n = 6
+    g = rng(11)
+    H = g.standard_normal((2, n, n)).astype(np.float32)
+    H[:, :, 4] = -40.0
+    dM = g.standard_normal((2, n, n)).astype(np.float32)
+    Ht = dev_tensor(H).requires_grad_(True)
+    ops.sinkhorn_knopp_hip_autograd(Ht, iters=20, eps=1e-5).backward(dev_tensor(dM))
+    ref = O.sinkhorn_knopp_vjp(H.astype(np.float64), dM, iters=20, eps=1e-5)
+    got = np_of(Ht.grad)
+    assert np.abs(got - ref).max() < 1e-4 * max(1.0, np.abs(ref).max())
+
+
+def test_sinkhorn_vjp_long_iterations_use_workspace():
+    # 4 * iters * 64 floats per wave exceeds the LDS budget: global state path
+    n, iters = 64, 80
+    g = rng(21)
+    H = g.standard_normal((2, n, n)).astype(np.float32)
+    dM = g.standard_normal((2, n, n)).astype(np.float32)
+    from mhc_mlx_amd import _lib
+    assert _lib.query("mhc_sinkhorn_bwd_workspace_bytes", 2, n, iters) > 0
+    Ht = dev_tensor(H).requires_grad_(True)
+    ops.sinkhorn_knopp_hip_autograd(Ht, iters=iters, eps=1e-5).backward(dev_tensor(dM))
+    ref = O.sinkhorn_knopp_vjp(H, dM, iters=iters, eps=1e-5)
+    got = np_of(Ht.grad)
+    assert np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-3) < 1e-4
+
+
+def test_sinkhorn_vjp_constant_column_cotangent_is_zero():
+    # dM = 1 c^T: column sums of M are fixed to 1, so the gradient vanishes
+    n = 5
+    H = rng(2).standard_normal((n, n)).astype(np.float32)
+    c = rng(3).standard_normal(n).astype(np.float32)
+    dM = np.ones((n, 1), np.float32) * c[None, :]
+    Ht = dev_tensor(H).requires_grad_(True)
+    ops.sinkhorn_knopp_hip_autograd(Ht, iters=20, eps=1e-5).backward(dev_tensor(dM))
+    assert np.abs(np_of(Ht.grad)).max() < 1e-5
+
+
+def test_sinkhorn_rejects_bad_shapes():
+    with pytest.raises(ValueError, match="square"):
+        ops.sinkhorn_knopp_hip(torch.zeros(3, 4, device="cuda"))
+    with pytest.raises(ValueError, match="MAX_N_ALLOWED"):
+        ops.sinkhorn_knopp_hip(torch.zeros(65, 65, device="cuda"))
