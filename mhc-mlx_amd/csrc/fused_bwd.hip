@@ -18,6 +18,8 @@
 // reduced across the workgroup per token and written directly.
 // Stage 2 (reduce kernels): fixed-order sum of the partial rows — the
 // result is bitwise reproducible for a given device and shape.
+#include <type_traits>
+
 #include "mhc_device.hpp"
 #include "mhc_generic.hpp"
 #include "mhc_host.hpp"
@@ -507,6 +509,264 @@ __global__ __launch_bounds__(1024) void fused_bwd_kernel(BwdArgs A) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Layer-wide parameters, n <= 8: the headline shape (n = 4).
+//
+// Thread `tid` owns CHK chunks of V channels (chunk q = tid + k * blockDim.x)
+// for every token the workgroup visits, so its slice of dw and the n^2 + 2n
+// parameter-gradient sums stay in registers for the whole kernel.  x and g
+// are held packed (two 16-bit elements per VGPR) across the RMS barrier and
+// unpacked again after it; the fp32 copies of phase A are not kept live.
+// With 16-bit x and g, dM_ij = sum g_i x_j runs on v_dot2 over the packed
+// words (two channels per instruction, exact bf16/fp16 products, fp32 sum).
+// ---------------------------------------------------------------------------
+
+template <typename XT, typename GT>
+struct LwCfg {
+  static constexpr int kElem = ElemTraits<XT>::kBytes > ElemTraits<GT>::kBytes ? ElemTraits<XT>::kBytes
+                                                                                : ElemTraits<GT>::kBytes;
+};
+
+template <int NMAX, typename XT, typename GT>
+constexpr int lw_vec() {
+  return (NMAX <= 4 ? 16 : 8) / LwCfg<XT, GT>::kElem;
+}
+
+template <typename T>
+MHC_DEV float dot2_acc(uint32_t g, uint32_t x, float acc);
+template <>
+MHC_DEV float dot2_acc<__bf16>(uint32_t g, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, g), __builtin_bit_cast(bf16x2, x), acc,
+                                         false);
+}
+template <>
+MHC_DEV float dot2_acc<_Float16>(uint32_t g, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, g), __builtin_bit_cast(f16x2, x), acc, false);
+}
+
+// Opaque to the optimiser: forces values derived from `w` to be recomputed.
+MHC_DEV void reg_fence(uint32_t& w) { asm volatile("" : "+v"(w)); }
+
+// FULL: n == NMAX, 16-byte aligned rows and every owned chunk complete, so
+// the token loop has no per-stream or per-chunk conditions.
+template <int NMAX, typename XT, typename GT, int CHK, bool FULL>
+__global__ __attribute__((amdgpu_flat_work_group_size(64, 1024), amdgpu_waves_per_eu(4)))
+void fused_bwd_lw_kernel(BwdArgs A) {
+  constexpr int V = lw_vec<NMAX, XT, GT>();
+  constexpr int K = NMAX * NMAX + 2 * NMAX;
+  constexpr bool DOT = std::is_same<XT, GT>::value && ElemTraits<XT>::kBytes == 2;
+  __shared__ float s_red[2][2][16];
+  __shared__ float s_acc[16][K];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int n = FULL ? NMAX : A.n;
+  const int C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  const XT* __restrict__ X = (const XT*)A.x;
+  const GT* __restrict__ Gr = (const GT*)A.g;
+  XT* __restrict__ DX = (XT*)A.dx;
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+
+  float Ms[NMAX * NMAX], as[NMAX], ps[NMAX];
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i) {
+    float av = 0.0f, pq = 0.0f;
+    if (i < n) {
+      av = A.hpre[i];
+      pq = A.hpost[i];
+      if (A.h_mode == MHC_H_RAW) {
+        av = sigmoidf_(av);
+        pq = 2.0f * sigmoidf_(pq);
+      }
+    }
+    as[i] = bwd_uniform(av);
+    ps[i] = bwd_uniform(pq);
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = bwd_uniform((i < n && j < n) ? A.M[i * n + j] : 0.0f);
+  }
+
+  int c0[CHK], valid[CHK];
+  float wv[CHK][V], dwv[CHK][V];
+#pragma unroll
+  for (int k = 0; k < CHK; ++k) {
+    const int q = tid + k * blockDim.x;
+    c0[k] = q * V;
+    valid[k] = FULL ? V : (q < A.nchunks ? min(V, C - c0[k]) : 0);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      wv[k][v] = v < valid[k] ? A.w[c0[k] + v] : 0.0f;
+      dwv[k][v] = 0.0f;
+    }
+  }
+  float accM[NMAX * NMAX], accA[NMAX], accP[NMAX];
+#pragma unroll
+  for (int k = 0; k < NMAX * NMAX; ++k) accM[k] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NMAX; ++k) accA[k] = accP[k] = 0.0f;
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const XT* xt = X + t * nC;
+    const GT* gt = Gr + t * nC;
+    XT* dxt = DX + t * nC;
+    Vec<XT, V> xr[CHK][NMAX];
+    Vec<GT, V> gr[CHK][NMAX];
+#pragma unroll
+    for (int k = 0; k < CHK; ++k) {
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        if (FULL || (i < n && valid[k] == V && A.vec)) {
+          xr[k][i].load(xt + (int64_t)i * C + c0[k]);
+          gr[k][i].load(gt + (int64_t)i * C + c0[k]);
+        } else if (i < n && valid[k] > 0) {
+          xr[k][i].load_partial(xt + (int64_t)i * C + c0[k], valid[k]);
+          gr[k][i].load_partial(gt + (int64_t)i * C + c0[k], valid[k]);
+        } else {
+          xr[k][i].zero();
+          gr[k][i].zero();
+        }
+      }
+    }
+    // ---- phase A: y, dyn and the per-token sums  sum y^2, sum dyn*y*w
+    float y[CHK][V], dyn[CHK][V];
+    float ss = 0.0f, sr = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CHK; ++k) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        float ya = 0.0f, da = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          ya = fmaf(as[i], xr[k][i].get(v), ya);
+          da = fmaf(ps[i], gr[k][i].get(v), da);
+        }
+        y[k][v] = ya;
+        dyn[k][v] = da;
+        ss = fmaf(ya, ya, ss);
+        sr = fmaf(da * ya, wv[k][v], sr);
+      }
+    }
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    __syncthreads();
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+
+    // ---- phase B: dx, dw and the parameter-gradient sums, two channels
+    // at a time so dx is packed as it is produced (only the packed dx words
+    // of one chunk are live, never n*V fp32 values).
+#pragma unroll
+    for (int k = 0; k < CHK; ++k) {
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+#pragma unroll
+        for (int w = 0; w < Vec<XT, V>::kWords; ++w) reg_fence(xr[k][i].w[w]);
+#pragma unroll
+        for (int w = 0; w < Vec<GT, V>::kWords; ++w) reg_fence(gr[k][i].w[w]);
+      }
+      float dxo[NMAX][V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float yi = y[k][v] * inv;
+        const float dy = dyn[k][v] * inv * wv[k][v] - kf * y[k][v];
+        const float yn = yi * wv[k][v];
+        dwv[k][v] = fmaf(dyn[k][v], yi, dwv[k][v]);
+        float gs[NMAX], xs[NMAX];
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          gs[i] = gr[k][i].get(v);
+          xs[i] = xr[k][i].get(v);
+        }
+        // dx_j = sum_i M_ij g_i + a_j dy
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+          float acc = as[j] * dy;
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) acc = fmaf(Ms[i * NMAX + j], gs[i], acc);
+          dxo[j][v] = acc;
+        }
+        // dA_j += dy x_j,  dP_i += g_i yn  (and dM without dot2)
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          accA[i] = fmaf(dy, xs[i], accA[i]);
+          accP[i] = fmaf(gs[i], yn, accP[i]);
+        }
+        if constexpr (!DOT) {
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) {
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) accM[i * NMAX + j] = fmaf(gs[i], xs[j], accM[i * NMAX + j]);
+          }
+        } else if (v & 1) {
+          const int w = v >> 1;
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) {
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j)
+              accM[i * NMAX + j] = dot2_acc<XT>(gr[k][i].w[w], xr[k][j].w[w], accM[i * NMAX + j]);
+          }
+        }
+      }
+      if (FULL || valid[k] > 0) {
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+          if (FULL || j < n) {
+            XT* dst = dxt + (int64_t)j * C + c0[k];
+            if (FULL || (A.vec && valid[k] == V)) store_vec<XT, V>(dst, dxo[j]);
+            else store_partial<XT, V>(dst, dxo[j], valid[k]);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- this workgroup's partial row: dw slice, then wave and block sums
+#pragma unroll
+  for (int k = 0; k < CHK; ++k) {
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (v < valid[k]) prow[c0[k] + v] = dwv[k][v];
+  }
+  if (tid == 0)
+    for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float v = k < NMAX * NMAX ? accM[k] : (k < NMAX * NMAX + NMAX ? accA[k - NMAX * NMAX]
+                                                                        : accP[k - NMAX * NMAX - NMAX]);
+    const float s = wave_sum(v);
+    if (lane == 0) s_acc[wave][k] = s;
+  }
+  __syncthreads();
+  for (int k = tid; k < K; k += blockDim.x) {
+    float s = 0.0f;
+    for (int w = 0; w < nwaves; ++w) s += s_acc[w][k];
+    int dst = -1;
+    if (k < NMAX * NMAX) {
+      const int i = k / NMAX, j = k % NMAX;
+      if (i < n && j < n) dst = i * n + j;
+    } else if (k < NMAX * NMAX + NMAX) {
+      if (k - NMAX * NMAX < n) dst = n * n + (k - NMAX * NMAX);
+    } else {
+      if (k - NMAX * NMAX - NMAX < n) dst = n * n + n + (k - NMAX * NMAX - NMAX);
+    }
+    if (dst >= 0) prow[A.Cp + dst] = s;
+  }
+  if (tid == 0)
+    for (int c = A.Cp + n * n + 2 * n; c < A.P; ++c) prow[c] = 0.0f;
+}
+
 // Stage 2b: final column sums and the activation chain.
 __global__ __launch_bounds__(256) void reduce_final_kernel(
     const float* __restrict__ part2, int S, int P, int n, int C, int Cp, int per_token,
@@ -567,8 +827,58 @@ BwdLayout bwd_layout(int64_t T, int n, int C, int per_token) {
   return L;
 }
 
+// Layer-wide n <= 8: chunks per thread (1 or 2) from MHC_BWD_CHK, default 1.
+// Returns 1 when the shape is not covered (C too large for the register
+// tile), so the caller falls back to fused_bwd_kernel.
+template <int NMAX, typename XT, typename GT, int CHK>
+int launch_bwd_lw_chk(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  constexpr int V = lw_vec<NMAX, XT, GT>();
+  A.nchunks = (int)ceil_div(A.C, V);
+  const int tpb = std::max(64, round_up((int)ceil_div(A.nchunks, CHK), 64));
+  if (tpb > 1024) return 1;
+  const bool full = A.n == NMAX && A.vec && A.C % V == 0 && A.nchunks == tpb * CHK;
+  const void* kfn = full ? (const void*)fused_bwd_lw_kernel<NMAX, XT, GT, CHK, true>
+                         : (const void*)fused_bwd_lw_kernel<NMAX, XT, GT, CHK, false>;
+  const int occ = occupancy_blocks(kfn, tpb, 0);
+  if (occ <= 0)
+    return set_error(MHC_ERR_INVALID_ARG, "fused_bwd: no occupancy for %d threads (n=%d C=%d)", tpb, A.n,
+                     A.C);
+  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
+  const int grid_pref = env_int("MHC_BWD_GRID", 0);
+  if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+  A.Cp = L.Cp;
+  A.P = L.P;
+  if (full)
+    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, CHK, true>), dim3((unsigned)blocks), dim3(tpb), 0,
+                       stream, A);
+  else
+    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, CHK, false>), dim3((unsigned)blocks), dim3(tpb), 0,
+                       stream, A);
+  MHC_CHECK_LAUNCH("fused_bwd_lw_kernel");
+  *num_partials = blocks;
+  return MHC_OK;
+}
+
+template <int NMAX, typename XT, typename GT>
+int launch_bwd_lw(const BwdArgs& A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  static const int chk = env_int("MHC_BWD_CHK", 1);
+  if (chk == 2) {
+    const int rc = launch_bwd_lw_chk<NMAX, XT, GT, 2>(A, L, num_partials, stream);
+    if (rc != 1) return rc;
+  }
+  return launch_bwd_lw_chk<NMAX, XT, GT, 1>(A, L, num_partials, stream);
+}
+
 template <int NMAX, typename XT, typename GT, bool PT>
 int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  if constexpr (!PT && NMAX <= 8) {
+    static const int legacy = env_int("MHC_BWD_LEGACY", 0);
+    if (!legacy) {
+      const int rc = launch_bwd_lw<NMAX, XT, GT>(A, L, num_partials, stream);
+      if (rc != 1) return rc;
+    }
+  }
   constexpr int V = BwdCfg<NMAX>::V;
   constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
   constexpr int KP = NMAX * NMAX + 2 * NMAX;
