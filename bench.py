@@ -101,13 +101,33 @@ def _cpu_baseline(n, C, budget_s=12.0, chunk=64):
 
 
 def _traffic():
-    p = ROOT / "profiles" / "fused_bwd_cfg2_traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            return None
+    """HBM bytes per fused-backward launch from the committed rocprofv3 --pmc summary (None if absent)."""
+    p = ROOT / "profiles" / "cfg2_fused_bwd_traffic.md"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
     return None
+
+
+def _copy_probe(mib: int, reps: int = 5) -> int:
+    """Plain copy of a known size (read mib MiB, write mib MiB per launch).
+
+    Run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, its counters give the
+    factor that turns those counters into bytes for this device.
+    """
+    import torch
+
+    nbytes = mib << 20
+    src = torch.ones(nbytes // 4, device="cuda:0", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes, "launches": reps,
+                      "kernel": "torch.mul(src, 1.0, out=dst) fp32"}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -118,7 +138,11 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-latency", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain fp32 copy of this many MiB (counter calibration)")
     args = ap.parse_args()
+    if args.copy_probe_mib > 0:
+        return _copy_probe(args.copy_probe_mib)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU per box; the mHC path shards by token "
