@@ -132,6 +132,51 @@ int mhc_fused_bwd(const void* x, int x_dtype, const void* dout, int dout_dtype, 
                   void* stream);
 
 /* --------------------------------------------------------------------- */
+/* Whole layer from raw parameters (MHCLayer.__call__ and its VJP)         */
+/* --------------------------------------------------------------------- */
+
+/* Forward of MHCLayer (layer.py:383-407 with the reference.py:164-184
+ * math): M_out = sinkhorn_knopp(exp(h_res_raw)) then the fused forward with
+ * a = sigmoid(h_pre_raw), p = 2*sigmoid(h_post_raw).  Layer-wide parameters
+ * ([n], [n], [n,n]; M_out [n,n]) or, with per_token != 0, per-token ones
+ * ([T,n], [T,n], [T,n,n]; M_out [T,n,n]).  M_out is kept for mhc_layer_bwd.
+ * Replaces sinkhorn_knopp_metal_autograd + activate_pre_post +
+ * mhc_forward_fused_metal_autograd as called from layer.py:387-407. */
+int mhc_layer_fwd(const void* x, int x_dtype, const float* h_pre_raw, const float* h_post_raw,
+                  const float* h_res_raw, const float* rms_weight, void* out, int out_dtype,
+                  float* M_out, int64_t T, int n, int C, int per_token, int iters, float eps,
+                  void* stream);
+
+size_t mhc_layer_bwd_workspace_bytes(int64_t T, int n, int C, int per_token, int iters);
+
+/* VJP of mhc_layer_fwd for cotangent dout: dx (x's dtype) and the gradients
+ * w.r.t. the raw parameters (same shapes as the parameters) and rms_weight
+ * [C].  M is the M_out of the forward.  Layer-wide: one partial-sums pass
+ * over x and dout, then one launch that reduces the partial rows in a fixed
+ * order, applies the sigmoid chain and runs the Sinkhorn VJP through all
+ * `iters` iterations.  Per token: the same, plus a batched Sinkhorn VJP.
+ * Replaces the MLX autograd chain through _mhc_fused_autograd_fn._f_vjp
+ * (metal.py:2787-2857), activate_pre_post (reference.py:51-55) and the
+ * Sinkhorn VJP (metal.py:2724-2739). */
+int mhc_layer_bwd(const void* x, int x_dtype, const void* dout, int dout_dtype,
+                  const float* h_pre_raw, const float* h_post_raw, const float* h_res_raw,
+                  const float* M, const float* rms_weight, void* dx, float* d_h_pre_raw,
+                  float* d_h_post_raw, float* d_h_res_raw, float* d_rms_weight, void* workspace,
+                  size_t workspace_bytes, int64_t T, int n, int C, int per_token, int iters,
+                  float eps, void* stream);
+
+/* Second stage of mhc_layer_bwd on its own: after mhc_fused_bwd_partials
+ * (h_mode MHC_H_RAW, the first mhc_fused_bwd_workspace_bytes() bytes of this
+ * workspace, per-token dM / dh written into d_h_res_raw / d_h_pre_raw /
+ * d_h_post_raw), reduce the `num_partials` rows and run the Sinkhorn VJP.
+ * Lets a caller time the partial-sums kernel separately. */
+int mhc_layer_bwd_reduce(void* workspace, size_t workspace_bytes, int64_t num_partials,
+                         const float* h_pre_raw, const float* h_post_raw, const float* h_res_raw,
+                         float* d_h_pre_raw, float* d_h_post_raw, float* d_h_res_raw,
+                         float* d_rms_weight, int64_t T, int n, int C, int per_token, int iters,
+                         float eps, void* stream);
+
+/* --------------------------------------------------------------------- */
 /* Stream mix + add (MHCRewire post-combine)                              */
 /* --------------------------------------------------------------------- */
 

@@ -25,6 +25,7 @@
 #include "mhc_host.hpp"
 #include "mhc_plan.hpp"
 #include "mhc_reduce.hpp"
+#include "mhc_sinkhorn.hpp"
 
 namespace mhc {
 
@@ -767,38 +768,132 @@ void fused_bwd_lw_kernel(BwdArgs A) {
     for (int c = A.Cp + n * n + 2 * n; c < A.P; ++c) prow[c] = 0.0f;
 }
 
-// Stage 2b: final column sums and the activation chain.
-__global__ __launch_bounds__(256) void reduce_final_kernel(
-    const float* __restrict__ part2, int S, int P, int n, int C, int Cp, int per_token,
-    const float* __restrict__ hpre, const float* __restrict__ hpost, int h_mode,
-    float* __restrict__ dM, float* __restrict__ dpre, float* __restrict__ dpost,
-    float* __restrict__ dw) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= P) return;
-  float s = 0.0f;
-  for (int k = 0; k < S; ++k) s += part2[(int64_t)k * P + c];
-  if (c < C) {
-    dw[c] = s;
-    return;
+// ---------------------------------------------------------------------------
+// Stage 2: fixed-order column sums of the G partial rows, two launches.
+//
+// reduce_rows_kernel (mhc_reduce.hpp) folds the G rows into S <= kReduceSplit
+// rows (part2); param_finish_kernel adds those S rows, writes the final sums
+// with the activation chain and, for layer-wide n <= SKNP, runs the Sinkhorn
+// VJP dH_res = VJP(H_res, dM) on wavefront 0 of the workgroup that owns the
+// parameter columns.  The kernel boundary between the two launches makes
+// every XCD's rows visible without device-scope fences, and the association
+// of every sum is fixed, so results are bitwise reproducible.
+//
+// param_finish_kernel: a workgroup owns kFinCols float4 columns and splits
+// the S rows over kFinPhases row phases (rows k = phase mod kFinPhases),
+// combined in phase order through LDS.  The dw columns [0, Cp) and the
+// parameter columns [Cp, P) are cut into workgroups separately, so the
+// n^2 + 2n parameter sums of n <= 8 sit in one workgroup.
+// ---------------------------------------------------------------------------
+
+constexpr int kFinCols = 64;
+constexpr int kFinPhases = 4;
+constexpr int kFinThreads = kFinCols * kFinPhases;
+
+struct RedArgs {
+  const float* part2;
+  int S;
+  int P;
+  int Cp;
+  int C;
+  int n;
+  int nd;  // workgroups over the dw columns
+  int per_token;
+  int h_mode;
+  const float* hpre;
+  const float* hpost;
+  float* dM;
+  float* dpre;
+  float* dpost;
+  float* dw;
+  const float* hres;  // SKNP > 0: H_res logits [n, n]
+  float* dhres;
+  int iters;
+  float eps;
+};
+
+template <int SKNP>
+__global__ __launch_bounds__(kFinThreads) void param_finish_kernel(RedArgs R) {
+  extern __shared__ float fin_smem[];  // SKNP > 0: dM [n*n], then the VJP state
+  __shared__ float4 s_part[kFinPhases][kFinCols];
+  const int tid = threadIdx.x;
+  const int col4 = tid % kFinCols;
+  const int phase = tid / kFinCols;
+  const int wg = blockIdx.x;
+  int base, end;
+  if (wg < R.nd) {
+    base = wg * 4 * kFinCols;
+    end = min(R.Cp, base + 4 * kFinCols);
+  } else {
+    base = R.Cp + (wg - R.nd) * 4 * kFinCols;
+    end = min(R.P, base + 4 * kFinCols);
   }
-  if (per_token || c < Cp) return;
-  const int k = c - Cp;
-  if (k < n * n) {
-    dM[k] = s;
-  } else if (k < n * n + n) {
-    const int j = k - n * n;
-    if (h_mode == MHC_H_RAW) {
-      const float a = sigmoidf_(hpre[j]);
-      s = s * a * (1.0f - a);
+  const int c = base + 4 * col4;
+  const bool act = c < end;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (act) {
+    const float* src = R.part2 + c;
+    float4 a0 = v, a1 = v;
+    int k = phase;
+    for (; k + kFinPhases < R.S; k += 2 * kFinPhases) {
+      const float4 u0 = *reinterpret_cast<const float4*>(src + (int64_t)k * R.P);
+      const float4 u1 = *reinterpret_cast<const float4*>(src + (int64_t)(k + kFinPhases) * R.P);
+      a0 = make_float4(a0.x + u0.x, a0.y + u0.y, a0.z + u0.z, a0.w + u0.w);
+      a1 = make_float4(a1.x + u1.x, a1.y + u1.y, a1.z + u1.z, a1.w + u1.w);
     }
-    dpre[j] = s;
-  } else if (k < n * n + 2 * n) {
-    const int i = k - n * n - n;
-    if (h_mode == MHC_H_RAW) {
-      const float sg = sigmoidf_(hpost[i]);
-      s = s * 2.0f * sg * (1.0f - sg);
+    if (k < R.S) {
+      const float4 u0 = *reinterpret_cast<const float4*>(src + (int64_t)k * R.P);
+      a0 = make_float4(a0.x + u0.x, a0.y + u0.y, a0.z + u0.z, a0.w + u0.w);
     }
-    dpost[i] = s;
+    v = make_float4(a0.x + a1.x, a0.y + a1.y, a0.z + a1.z, a0.w + a1.w);
+  }
+  s_part[phase][col4] = v;
+  __syncthreads();
+  const int n = R.n, nn = n * n;
+  float* s_dM = fin_smem;
+  if (phase == 0 && act) {
+#pragma unroll
+    for (int ph = 1; ph < kFinPhases; ++ph) {
+      const float4 u = s_part[ph][col4];
+      v = make_float4(v.x + u.x, v.y + u.y, v.z + u.z, v.w + u.w);
+    }
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int col = c + e;
+      float s = vv[e];
+      if (col < R.C) {
+        R.dw[col] = s;
+      } else if (!R.per_token && col >= R.Cp) {
+        const int k = col - R.Cp;
+        if (k < nn) {
+          if (R.dM != nullptr) R.dM[k] = s;
+          if constexpr (SKNP > 0) s_dM[k] = s;
+        } else if (k < nn + n) {
+          const int j = k - nn;
+          if (R.h_mode == MHC_H_RAW) {
+            const float a = sigmoidf_(R.hpre[j]);
+            s = s * a * (1.0f - a);
+          }
+          R.dpre[j] = s;
+        } else if (k < nn + 2 * n) {
+          const int i = k - nn - n;
+          if (R.h_mode == MHC_H_RAW) {
+            const float sg = sigmoidf_(R.hpost[i]);
+            s = s * 2.0f * sg * (1.0f - sg);
+          }
+          R.dpost[i] = s;
+        }
+      }
+    }
+  }
+  if constexpr (SKNP > 0) {
+    if (wg == R.nd) {
+      __syncthreads();  // s_dM complete
+      if (tid < 64)
+        sk_bwd_group<SKNP>(R.hres, s_dM, R.dhres, tid < SkLayout<SKNP>::G, n, R.iters, R.eps,
+                           fin_smem + round_up(nn, 4), tid);
+    }
   }
 }
 
@@ -812,10 +907,11 @@ struct BwdLayout {
   int Cp;
   int P;
   int64_t gmax;
-  size_t scratch_off;  // generic path: 2*C floats per workgroup after the partial rows
+  size_t scratch_off;  // generic path: 2*C floats per workgroup after part2
   size_t bytes;
 };
 
+// Workspace: [part: one row per workgroup][part2: kReduceSplit rows][scratch]
 BwdLayout bwd_layout(int64_t T, int n, int C, int per_token) {
   BwdLayout L{};
   L.Cp = round_up(C, 4);
@@ -827,47 +923,38 @@ BwdLayout bwd_layout(int64_t T, int n, int C, int per_token) {
   return L;
 }
 
-// Layer-wide n <= 8: chunks per thread (1 or 2) from MHC_BWD_CHK, default 1.
-// Returns 1 when the shape is not covered (C too large for the register
-// tile), so the caller falls back to fused_bwd_kernel.
-template <int NMAX, typename XT, typename GT, int CHK>
-int launch_bwd_lw_chk(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+void set_rows(BwdArgs& A, const BwdLayout& L) {
+  A.Cp = L.Cp;
+  A.P = L.P;
+}
+
+// Layer-wide n <= 8 (fused_bwd_lw_kernel).  Returns 1 when the shape is not
+// covered (C too large for one chunk per thread), so the caller falls back
+// to fused_bwd_kernel.
+template <int NMAX, typename XT, typename GT>
+int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
   constexpr int V = lw_vec<NMAX, XT, GT>();
   A.nchunks = (int)ceil_div(A.C, V);
-  const int tpb = std::max(64, round_up((int)ceil_div(A.nchunks, CHK), 64));
+  const int tpb = std::max(64, round_up(A.nchunks, 64));
   if (tpb > 1024) return 1;
-  const bool full = A.n == NMAX && A.vec && A.C % V == 0 && A.nchunks == tpb * CHK;
-  const void* kfn = full ? (const void*)fused_bwd_lw_kernel<NMAX, XT, GT, CHK, true>
-                         : (const void*)fused_bwd_lw_kernel<NMAX, XT, GT, CHK, false>;
-  const int occ = occupancy_blocks(kfn, tpb, 0);
-  if (occ <= 0)
-    return set_error(MHC_ERR_INVALID_ARG, "fused_bwd: no occupancy for %d threads (n=%d C=%d)", tpb, A.n,
-                     A.C);
-  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
+  const bool full = A.n == NMAX && A.vec && A.C % V == 0 && A.nchunks == tpb;
+  // Grid: the workspace's full row budget (8 workgroups per CU) streams
+  // faster than one resident wave of workgroups (562 vs 576 us at config 2);
+  // MHC_BWD_GRID overrides the count.
+  int64_t blocks = L.gmax;
   const int grid_pref = env_int("MHC_BWD_GRID", 0);
   if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
-  A.Cp = L.Cp;
-  A.P = L.P;
+  set_rows(A, L);
   if (full)
-    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, CHK, true>), dim3((unsigned)blocks), dim3(tpb), 0,
+    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, true>), dim3((unsigned)blocks), dim3(tpb), 0,
                        stream, A);
   else
-    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, CHK, false>), dim3((unsigned)blocks), dim3(tpb), 0,
+    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, false>), dim3((unsigned)blocks), dim3(tpb), 0,
                        stream, A);
   MHC_CHECK_LAUNCH("fused_bwd_lw_kernel");
   *num_partials = blocks;
   return MHC_OK;
-}
-
-template <int NMAX, typename XT, typename GT>
-int launch_bwd_lw(const BwdArgs& A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
-  static const int chk = env_int("MHC_BWD_CHK", 1);
-  if (chk == 2) {
-    const int rc = launch_bwd_lw_chk<NMAX, XT, GT, 2>(A, L, num_partials, stream);
-    if (rc != 1) return rc;
-  }
-  return launch_bwd_lw_chk<NMAX, XT, GT, 1>(A, L, num_partials, stream);
 }
 
 template <int NMAX, typename XT, typename GT, bool PT>
@@ -901,8 +988,7 @@ int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t
                      tp.tpb, A.n, A.C);
   int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
-  A.Cp = L.Cp;
-  A.P = L.P;
+  set_rows(A, L);
   hipLaunchKernelGGL((fused_bwd_kernel<NMAX, XT, GT, XT, PT>), dim3((unsigned)blocks), dim3(tp.tpb),
                      smem, stream, A);
   MHC_CHECK_LAUNCH("fused_bwd_kernel");
@@ -1001,6 +1087,65 @@ extern "C" int mhc_fused_bwd_partials(const void* x, int x_dtype, const void* do
                    : bwd_dispatch_types<false>(A, L, x_dtype, dout_dtype, num_partials, s);
 }
 
+namespace mhc {
+namespace {
+
+// Reduce `G` partial rows: reduce_rows_kernel then param_finish_kernel.
+// With hres != NULL the Sinkhorn VJP of the reduced dM runs in the second
+// launch; returns 1 when that fusion is not possible (per-token parameters,
+// n > 8, or VJP state beyond the LDS budget).
+int launch_param_reduce(const void* workspace, size_t workspace_bytes, int64_t G, int n, int C, int per_token,
+                        const float* h_pre, const float* h_post, int h_mode, float* dM, float* dh_pre,
+                        float* dh_post, float* dw, const float* hres, float* dhres, int iters, float eps,
+                        hipStream_t s) {
+  RedArgs R{};
+  R.Cp = round_up(C, 4);
+  R.P = per_token ? R.Cp : R.Cp + round_up(n * n + 2 * n, 4);
+  R.nd = (int)ceil_div(R.Cp, 4 * kFinCols);
+  const int nwg = R.nd + (int)ceil_div(R.P - R.Cp, 4 * kFinCols);
+  int sknp = 0;
+  size_t smem = 0;
+  if (hres != nullptr) {
+    if (per_token || n > 8) return 1;
+    sknp = next_pow2(n);
+    smem = ((size_t)round_up(n * n, 4) + (size_t)sk_state_floats(sknp, iters)) * sizeof(float);
+    if (smem > 48 * 1024) return 1;
+  }
+  if (G > 0) {
+    const size_t need = (size_t)(G + kReduceSplit) * (size_t)R.P * sizeof(float);
+    MHC_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                  "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
+    MHC_CHECK_ARG(aligned(workspace, 16), "workspace must be 16-byte aligned");
+    const int S0 = (int)std::min<int64_t>(kReduceSplit, G);
+    const int rows = (int)ceil_div(G, S0);
+    R.S = (int)ceil_div(G, rows);
+    float* part2 = (float*)workspace + G * (int64_t)R.P;
+    hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)ceil_div(R.P / 4, 256), (unsigned)R.S), dim3(256), 0,
+                       s, (const float*)workspace, part2, G, R.P, rows);
+    MHC_CHECK_LAUNCH("reduce_rows_kernel");
+    R.part2 = part2;
+  } else {
+    R.S = 0;  // no rows: every sum is zero
+    R.part2 = nullptr;
+  }
+  R.C = C; R.n = n; R.per_token = per_token; R.h_mode = h_mode;
+  R.hpre = h_pre; R.hpost = h_post; R.dM = dM; R.dpre = dh_pre; R.dpost = dh_post; R.dw = dw;
+  R.hres = hres; R.dhres = dhres; R.iters = iters; R.eps = eps;
+  const dim3 grid((unsigned)nwg);
+  switch (sknp) {
+    case 0: hipLaunchKernelGGL((param_finish_kernel<0>), grid, dim3(kFinThreads), 0, s, R); break;
+    case 1: hipLaunchKernelGGL((param_finish_kernel<1>), grid, dim3(kFinThreads), smem, s, R); break;
+    case 2: hipLaunchKernelGGL((param_finish_kernel<2>), grid, dim3(kFinThreads), smem, s, R); break;
+    case 4: hipLaunchKernelGGL((param_finish_kernel<4>), grid, dim3(kFinThreads), smem, s, R); break;
+    default: hipLaunchKernelGGL((param_finish_kernel<8>), grid, dim3(kFinThreads), smem, s, R); break;
+  }
+  MHC_CHECK_LAUNCH("param_finish_kernel");
+  return MHC_OK;
+}
+
+}  // namespace
+}  // namespace mhc
+
 extern "C" int mhc_reduce_param_grads(const void* workspace, size_t workspace_bytes,
                                       int64_t num_partials, int n, int C, int per_token,
                                       const float* h_pre, const float* h_post, int h_mode,
@@ -1014,34 +1159,9 @@ extern "C" int mhc_reduce_param_grads(const void* workspace, size_t workspace_by
   MHC_CHECK_ARG(per_token || h_mode != MHC_H_RAW || (h_pre && h_post),
                 "raw-logit mode needs h_pre and h_post");
   MHC_CHECK_ARG(num_partials >= 0, "num_partials must be >= 0");
-  hipStream_t s = (hipStream_t)stream;
-  if (num_partials == 0) {
-    MHC_CHECK_HIP(hipMemsetAsync(d_rms_weight, 0, sizeof(float) * C, s));
-    if (!per_token) {
-      MHC_CHECK_HIP(hipMemsetAsync(dM, 0, sizeof(float) * n * n, s));
-      MHC_CHECK_HIP(hipMemsetAsync(dh_pre, 0, sizeof(float) * n, s));
-      MHC_CHECK_HIP(hipMemsetAsync(dh_post, 0, sizeof(float) * n, s));
-    }
-    return MHC_OK;
-  }
-  const int Cp = round_up(C, 4);
-  const int P = per_token ? Cp : Cp + round_up(n * n + 2 * n, 4);
-  const size_t need = (size_t)(num_partials + kReduceSplit) * (size_t)P * sizeof(float);
-  MHC_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
-                "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
-  const float* part = (const float*)workspace;
-  float* part2 = (float*)workspace + (size_t)num_partials * P;
-  const int S = (int)std::min<int64_t>(kReduceSplit, num_partials);
-  const int rows = (int)ceil_div(num_partials, S);
-  const int S_used = (int)ceil_div(num_partials, rows);
-  dim3 g1((unsigned)ceil_div(P / 4, 256), (unsigned)S_used);
-  hipLaunchKernelGGL(reduce_rows_kernel, g1, dim3(256), 0, s, part, part2, num_partials, P, rows);
-  MHC_CHECK_LAUNCH("reduce_rows_kernel");
-  hipLaunchKernelGGL(reduce_final_kernel, dim3((unsigned)ceil_div(P, 256)), dim3(256), 0, s, part2,
-                     S_used, P, n, C, Cp, per_token, h_pre, h_post, h_mode, dM, dh_pre, dh_post,
-                     d_rms_weight);
-  MHC_CHECK_LAUNCH("reduce_final_kernel");
-  return MHC_OK;
+  return launch_param_reduce(workspace, workspace_bytes, num_partials, n, C, per_token, h_pre, h_post, h_mode,
+                             dM, dh_pre, dh_post, d_rms_weight, nullptr, nullptr, 0, 0.0f,
+                             (hipStream_t)stream);
 }
 
 extern "C" int mhc_fused_bwd(const void* x, int x_dtype, const void* dout, int dout_dtype,
@@ -1062,4 +1182,109 @@ extern "C" int mhc_fused_bwd(const void* x, int x_dtype, const void* dout, int d
   return mhc_reduce_param_grads(workspace, workspace_bytes, np, n, C, per_token, h_pre, h_post,
                                 h_mode, per_token ? nullptr : dM, per_token ? nullptr : dh_pre,
                                 per_token ? nullptr : dh_post, d_rms_weight, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Layer-level backward (raw parameters in, raw-parameter gradients out)
+// ---------------------------------------------------------------------------
+
+namespace mhc {
+namespace {
+
+struct LayerBwdLayout {
+  size_t bwd_bytes;  // mhc_fused_bwd_workspace_bytes
+  size_t dM_off;     // layer-wide: reduced dM [n, n]
+  size_t sk_off;     // Sinkhorn VJP workspace
+  size_t bytes;
+};
+
+LayerBwdLayout layer_bwd_layout(int64_t T, int n, int C, int per_token, int iters) {
+  LayerBwdLayout L{};
+  L.bwd_bytes = bwd_layout(T, n, C, per_token).bytes;
+  L.dM_off = (L.bwd_bytes + 255) / 256 * 256;
+  L.sk_off = L.dM_off + (size_t)round_up(n * n, 64) * sizeof(float);
+  L.bytes = L.sk_off + mhc_sinkhorn_bwd_workspace_bytes(per_token ? T : 1, n, iters);
+  return L;
+}
+
+}  // namespace
+}  // namespace mhc
+
+extern "C" size_t mhc_layer_bwd_workspace_bytes(int64_t T, int n, int C, int per_token, int iters) {
+  if (T <= 0 || n < 1 || n > MHC_MAX_N || C < 1 || iters < 0) return 0;
+  return layer_bwd_layout(T, n, C, per_token, iters).bytes;
+}
+
+extern "C" int mhc_layer_bwd_reduce(void* workspace, size_t workspace_bytes, int64_t num_partials,
+                                    const float* h_pre_raw, const float* h_post_raw, const float* h_res_raw,
+                                    float* d_h_pre_raw, float* d_h_post_raw, float* d_h_res_raw,
+                                    float* d_rms_weight, int64_t T, int n, int C, int per_token, int iters,
+                                    float eps, void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1, "C=%d must be positive", C);
+  MHC_CHECK_ARG(T >= 0 && num_partials >= 0, "T and num_partials must be >= 0");
+  MHC_CHECK_ARG(iters >= 0, "iters=%d must be >= 0", iters);
+  MHC_CHECK_ARG(h_pre_raw && h_post_raw && h_res_raw, "null parameter pointer");
+  MHC_CHECK_ARG(d_h_pre_raw && d_h_post_raw && d_h_res_raw && d_rms_weight, "null gradient pointer");
+  MHC_CHECK_ARG(num_partials == 0 || T > 0, "num_partials must be 0 when T == 0");
+  hipStream_t s = (hipStream_t)stream;
+  if (per_token && T == 0) return MHC_OK;
+  const LayerBwdLayout L = layer_bwd_layout(std::max<int64_t>(T, 1), n, C, per_token, iters);
+  MHC_CHECK_ARG(T == 0 || (workspace != nullptr && workspace_bytes >= L.bytes),
+                "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, L.bytes);
+  char* ws = (char*)workspace;
+  int rc;
+  if (per_token) {
+    // d_h_res_raw holds dM per token (written by the partials pass); the
+    // Sinkhorn VJP runs in place.
+    rc = launch_param_reduce(ws, L.bwd_bytes, num_partials, n, C, 1, nullptr, nullptr, MHC_H_RAW, nullptr,
+                             nullptr, nullptr, d_rms_weight, nullptr, nullptr, 0, 0.0f, s);
+    if (rc != MHC_OK) return rc;
+    const size_t skb = mhc_sinkhorn_bwd_workspace_bytes(T, n, iters);
+    return mhc_sinkhorn_bwd(h_res_raw, d_h_res_raw, d_h_res_raw, T, n, iters, eps, skb ? ws + L.sk_off : nullptr,
+                            skb, stream);
+  }
+  float* dM = T > 0 ? reinterpret_cast<float*>(ws + L.dM_off) : nullptr;
+  rc = launch_param_reduce(ws, L.bwd_bytes, num_partials, n, C, 0, h_pre_raw, h_post_raw, MHC_H_RAW, dM,
+                           d_h_pre_raw, d_h_post_raw, d_rms_weight, h_res_raw, d_h_res_raw, iters, eps, s);
+  if (rc != 1) return rc;
+  // VJP state too large for one workgroup's LDS (or n > 16): separate launch
+  MHC_CHECK_ARG(T > 0, "T=0 with n=%d needs a workspace for the Sinkhorn VJP", n);
+  rc = launch_param_reduce(ws, L.bwd_bytes, num_partials, n, C, 0, h_pre_raw, h_post_raw, MHC_H_RAW, dM,
+                           d_h_pre_raw, d_h_post_raw, d_rms_weight, nullptr, nullptr, 0, 0.0f, s);
+  if (rc != MHC_OK) return rc;
+  const size_t skb = mhc_sinkhorn_bwd_workspace_bytes(1, n, iters);
+  return mhc_sinkhorn_bwd(h_res_raw, dM, d_h_res_raw, 1, n, iters, eps, skb ? ws + L.sk_off : nullptr, skb,
+                          stream);
+}
+
+extern "C" int mhc_layer_bwd(const void* x, int x_dtype, const void* dout, int dout_dtype,
+                             const float* h_pre_raw, const float* h_post_raw, const float* h_res_raw,
+                             const float* M, const float* rms_weight, void* dx, float* d_h_pre_raw,
+                             float* d_h_post_raw, float* d_h_res_raw, float* d_rms_weight, void* workspace,
+                             size_t workspace_bytes, int64_t T, int n, int C, int per_token, int iters,
+                             float eps, void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n >= 1 && n <= MHC_MAX_N, "n=%d must be in [1, %d]", n, MHC_MAX_N);
+  MHC_CHECK_ARG(C >= 1, "C=%d must be positive", C);
+  MHC_CHECK_ARG(T >= 0, "T=%lld must be >= 0", (long long)T);
+  MHC_CHECK_ARG(iters >= 0, "iters=%d must be >= 0", iters);
+  MHC_CHECK_ARG(M != nullptr && rms_weight != nullptr, "null parameter pointer");
+  MHC_CHECK_ARG(h_pre_raw && h_post_raw && h_res_raw, "null parameter pointer");
+  MHC_CHECK_ARG(d_h_pre_raw && d_h_post_raw && d_h_res_raw && d_rms_weight, "null gradient pointer");
+  int64_t np = 0;
+  if (T > 0) {
+    const LayerBwdLayout L = layer_bwd_layout(T, n, C, per_token, iters);
+    MHC_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.bytes,
+                  "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, L.bytes);
+    const int rc = mhc_fused_bwd_partials(
+        x, x_dtype, dout, dout_dtype, M, per_token ? (int64_t)n * n : 0, h_pre_raw, h_post_raw,
+        per_token ? n : 0, MHC_H_RAW, rms_weight, dx, x_dtype, per_token ? d_h_res_raw : nullptr,
+        per_token ? d_h_pre_raw : nullptr, per_token ? d_h_post_raw : nullptr, workspace, L.bwd_bytes, T, n, C,
+        eps, &np, stream);
+    if (rc != MHC_OK) return rc;
+  }
+  return mhc_layer_bwd_reduce(workspace, workspace_bytes, np, h_pre_raw, h_post_raw, h_res_raw, d_h_pre_raw,
+                              d_h_post_raw, d_h_res_raw, d_rms_weight, T, n, C, per_token, iters, eps, stream);
 }

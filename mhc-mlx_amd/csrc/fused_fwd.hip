@@ -282,16 +282,136 @@ __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// Layer-wide parameters, n == NMAX <= 8, full tiles (the headline shapes).
+//
+// One workgroup per token: TPB threads own CH chunks of V channels each and
+// exactly cover the token (C == TPB * CH * V), 16-byte aligned rows.  No
+// per-stream, per-chunk or per-channel conditions remain; M, a and p are
+// wave-uniform scalars.  The grid-stride loop only matters for T > kMaxGrid.
+// ---------------------------------------------------------------------------
+
+template <int NMAX, typename XT, typename OT, int CH>
+__global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
+  constexpr int V = FwdCfg<NMAX>::V;
+  __shared__ float s_red[2][16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int C = A.C;
+  const int64_t nC = (int64_t)NMAX * C;
+
+  float Ms[NMAX * NMAX], as[NMAX], ps[NMAX];
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i) {
+    float av = A.hpre[i], pv = A.hpost[i];
+    if (A.h_mode == MHC_H_RAW) {
+      av = sigmoidf_(av);
+      pv = 2.0f * sigmoidf_(pv);
+    }
+    as[i] = uniform_f(av);
+    ps[i] = uniform_f(pv);
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = uniform_f(A.M[i * NMAX + j]);
+  }
+  int c0[CH];
+  float wv[CH][V];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    c0[k] = (tid + k * (int)blockDim.x) * V;
+#pragma unroll
+    for (int v = 0; v < V; ++v) wv[k][v] = A.w[c0[k] + v];
+  }
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const XT* xt = (const XT*)A.x + t * nC;
+    OT* ot = (OT*)A.out + t * nC;
+    Vec<XT, V> xr[CH][NMAX];
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) xr[k][i].load(xt + i * C + c0[k]);
+    float y[CH][V];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) acc = fmaf(as[i], xr[k][i].get(v), acc);
+        y[k][v] = acc;
+        ss = fmaf(acc, acc, ss);
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) s_red[it & 1][wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < nwaves; ++w) tot += s_red[it & 1][w];
+    const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
+    if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      float yn[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) yn[v] = (y[k][v] * inv) * wv[k][v];
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        float o[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int j = 0; j < NMAX; ++j) acc = fmaf(Ms[i * NMAX + j], xr[k][j].get(v), acc);
+          o[v] = fmaf(yn[v], ps[i], acc);
+        }
+        store_vec<OT, V>(ot + i * C + c0[k], o);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
 namespace {
+
+// Full-tile kernel for layer-wide n == NMAX <= 8.  Returns 1 when the shape
+// is not covered (the caller then uses fused_fwd_kernel).
+template <int NMAX, typename XT, typename OT>
+int launch_fwd_full(FwdArgs A, hipStream_t stream) {
+  constexpr int V = FwdCfg<NMAX>::V;
+  if (A.n != NMAX || !A.vec || A.C % V != 0) return 1;
+  const int nchunks = A.C / V;
+  // Two chunks per thread stream best at large T; with fewer tokens than
+  // CUs (latency regime) each token is spread over twice the lanes.
+  int ch = (A.T < device_cu_count() || NMAX > 4) ? 1 : 2;
+  if (nchunks % (64 * ch) != 0) ch = 1;
+  if (nchunks % 64 != 0 || nchunks / ch > 1024) return 1;
+  const int tpb = nchunks / ch;
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, kMaxGrid));
+  if (ch == 2)
+    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 2>), dim3((unsigned)blocks), dim3(tpb), 0,
+                       stream, A);
+  else
+    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1>), dim3((unsigned)blocks), dim3(tpb), 0,
+                       stream, A);
+  MHC_CHECK_LAUNCH("fused_fwd_full_kernel");
+  return MHC_OK;
+}
 
 template <int NMAX, typename XT, typename OT, bool PT>
 int launch_fwd(FwdArgs A, hipStream_t stream) {
   constexpr int V = FwdCfg<NMAX>::V;
   constexpr int CH = FwdCfg<NMAX>::CH;
   constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
+  if constexpr (!PT && NMAX <= 8) {
+    const int rc = launch_fwd_full<NMAX, XT, OT>(A, stream);
+    if (rc != 1) return rc;
+  }
   A.nchunks = (int)ceil_div(A.C, V);
   const ThreadPlan tp = plan_threads(A.nchunks, CH, env_int("MHC_FWD_TPB", 0));
   A.ch = tp.ch;
@@ -303,8 +423,10 @@ int launch_fwd(FwdArgs A, hipStream_t stream) {
   if (occ <= 0)
     return set_error(MHC_ERR_INVALID_ARG, "fused_fwd: no occupancy for %d threads (n=%d C=%d)",
                      tp.tpb, A.n, A.C);
-  int64_t blocks = std::min<int64_t>(A.T, (int64_t)device_cu_count() * occ);
-  blocks = std::max<int64_t>(blocks, 1);
+  // Persistent grid (per-token parameters are staged one token ahead).
+  const int grid_per_cu = env_int("MHC_FWD_GRID", 0);
+  int64_t blocks = (int64_t)device_cu_count() * (grid_per_cu > 0 ? grid_per_cu : occ);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, blocks));
   hipLaunchKernelGGL((fused_fwd_kernel<NMAX, XT, OT, PT>), dim3((unsigned)blocks), dim3(tp.tpb),
                      smem, stream, A);
   MHC_CHECK_LAUNCH("fused_fwd_kernel");
@@ -376,4 +498,20 @@ extern "C" int mhc_fused_fwd(const void* x, int x_dtype, const float* M, int64_t
   hipStream_t s = (hipStream_t)stream;
   return M_token_stride ? dispatch_types<true>(A, x_dtype, out_dtype, s)
                         : dispatch_types<false>(A, x_dtype, out_dtype, s);
+}
+
+extern "C" int mhc_layer_fwd(const void* x, int x_dtype, const float* h_pre_raw, const float* h_post_raw,
+                             const float* h_res_raw, const float* rms_weight, void* out, int out_dtype,
+                             float* M_out, int64_t T, int n, int C, int per_token, int iters, float eps,
+                             void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(T >= 0, "T=%lld must be >= 0", (long long)T);
+  MHC_CHECK_ARG(M_out != nullptr && h_res_raw != nullptr, "null pointer argument");
+  const int64_t batch = per_token ? T : 1;
+  if (batch > 0) {
+    const int rc = mhc_sinkhorn_fwd(h_res_raw, M_out, batch, n, iters, eps, stream);
+    if (rc != MHC_OK) return rc;
+  }
+  return mhc_fused_fwd(x, x_dtype, M_out, per_token ? (int64_t)n * n : 0, h_pre_raw, h_post_raw,
+                       per_token ? n : 0, MHC_H_RAW, rms_weight, out, out_dtype, nullptr, T, n, C, eps, stream);
 }

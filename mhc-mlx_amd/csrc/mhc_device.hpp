@@ -18,6 +18,8 @@ constexpr int kWave = 64;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Element type codes shared with the C ABI (include/mhc_hip.h).
 enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
@@ -90,20 +92,21 @@ struct Vec {
     }
   }
 
-  // Vector load of V elements; p must be aligned to min(16, kBytes).
+  // Vector load of V elements; p must be aligned to min(16, kBytes).  The
+  // activations are streamed once, so the loads carry the non-temporal hint.
   MHC_DEV void load(const T* p) {
     const char* b = reinterpret_cast<const char*>(p);
     if constexpr (kBytes % 16 == 0) {
 #pragma unroll
       for (int k = 0; k < kBytes / 16; ++k) {
-        uint4 u = reinterpret_cast<const uint4*>(b)[k];
+        const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(b) + k);
         w[4 * k + 0] = u.x; w[4 * k + 1] = u.y; w[4 * k + 2] = u.z; w[4 * k + 3] = u.w;
       }
     } else if constexpr (kBytes == 8) {
-      uint2 u = *reinterpret_cast<const uint2*>(b);
+      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(b));
       w[0] = u.x; w[1] = u.y;
     } else if constexpr (kBytes == 4) {
-      w[0] = *reinterpret_cast<const uint32_t*>(b);
+      w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(b));
     } else {
       static_assert(kBytes == 2, "unsupported vector width");
       w[0] = (uint32_t)(*reinterpret_cast<const uint16_t*>(b));
@@ -126,20 +129,33 @@ struct Vec {
   }
 };
 
-// Store V fp32 values as T; p aligned to min(16, V*sizeof(T)).
+// Non-temporal stores of whole 4 / 8 / 16-byte words.
+MHC_DEV void st_nt(uint32_t* p, uint32_t a) { __builtin_nontemporal_store(a, p); }
+MHC_DEV void st_nt(uint32_t* p, uint32_t a, uint32_t b) {
+  const u32x2 v = {a, b};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
+}
+MHC_DEV void st_nt(uint32_t* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const u32x4 v = {a, b, c, d};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+// Store V fp32 values as T; p aligned to min(16, V*sizeof(T)).  Streamed
+// outputs, so the stores carry the non-temporal hint.
 template <typename T, int V>
 MHC_DEV void store_vec(T* p, const float (&v)[V]) {
   constexpr int kBytes = V * ElemTraits<T>::kBytes;
-  char* b = reinterpret_cast<char*>(p);
+  uint32_t* b = reinterpret_cast<uint32_t*>(p);
   if constexpr (ElemTraits<T>::kBytes == 4) {
     if constexpr (kBytes % 16 == 0) {
 #pragma unroll
       for (int k = 0; k < V / 4; ++k)
-        reinterpret_cast<float4*>(b)[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        st_nt(b + 4 * k, __builtin_bit_cast(uint32_t, v[4 * k]), __builtin_bit_cast(uint32_t, v[4 * k + 1]),
+              __builtin_bit_cast(uint32_t, v[4 * k + 2]), __builtin_bit_cast(uint32_t, v[4 * k + 3]));
     } else if constexpr (kBytes == 8) {
-      *reinterpret_cast<float2*>(b) = make_float2(v[0], v[1]);
+      st_nt(b, __builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]));
     } else {
-      *reinterpret_cast<float*>(b) = v[0];
+      st_nt(b, __builtin_bit_cast(uint32_t, v[0]));
     }
   } else {
     if constexpr (V == 1) {
@@ -150,12 +166,11 @@ MHC_DEV void store_vec(T* p, const float (&v)[V]) {
       for (int k = 0; k < V / 2; ++k) wd[k] = pack2<T>(v[2 * k], v[2 * k + 1]);
       if constexpr (kBytes % 16 == 0) {
 #pragma unroll
-        for (int k = 0; k < kBytes / 16; ++k)
-          reinterpret_cast<uint4*>(b)[k] = make_uint4(wd[4 * k], wd[4 * k + 1], wd[4 * k + 2], wd[4 * k + 3]);
+        for (int k = 0; k < kBytes / 16; ++k) st_nt(b + 4 * k, wd[4 * k], wd[4 * k + 1], wd[4 * k + 2], wd[4 * k + 3]);
       } else if constexpr (kBytes == 8) {
-        *reinterpret_cast<uint2*>(b) = make_uint2(wd[0], wd[1]);
+        st_nt(b, wd[0], wd[1]);
       } else {
-        *reinterpret_cast<uint32_t*>(b) = wd[0];
+        st_nt(b, wd[0]);
       }
     }
   }
@@ -169,32 +184,71 @@ MHC_DEV void store_partial(T* p, const float (&v)[V], int valid) {
 }
 
 // --------------------------------------------------------------------------
-// wave64 reductions (butterflies: every lane ends with a bitwise-identical
-// result because each pairwise add is commutative-symmetric)
+// wave64 reductions
+//
+// Steps inside a 16-lane DPP row use DPP lane permutes (no LDS traffic):
+// quad_perm for lane^1 and lane^2, row_half_mirror (lane^7 within 8) and
+// row_mirror (lane^15 within 16) once the lower bits are already reduced,
+// row_ror:8 (== lane^8) and row_ror:4 (== lane^4 once bit 3 is reduced).
+// Steps across rows (lane^16, lane^32) use ds_bpermute.  Every step adds
+// the same pair of values on both partner lanes, so all lanes of a group end
+// with bitwise-identical results.
 // --------------------------------------------------------------------------
 
 MHC_DEV float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
 
-// all-reduce (sum) across aligned groups of `Lanes` lanes, Lanes a power of 2
-template <int Lanes>
-MHC_DEV float group_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < Lanes; m <<= 1) v += shfl_xor(v, m);
+template <int CTRL>
+MHC_DEV float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                               false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane ^ 7 within 8
+constexpr int kDppMirror = 0x140;     // lane ^ 15 within 16
+constexpr int kDppRor4 = 0x124;       // row_ror:4
+constexpr int kDppRor8 = 0x128;       // row_ror:8
+
+struct SumOp {
+  MHC_DEV float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+  MHC_DEV float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// all-reduce across aligned groups of `Lanes` lanes, Lanes a power of 2
+template <int Lanes, typename Op>
+MHC_DEV float group_reduce(float v, Op op) {
+  if constexpr (Lanes >= 2) v = op(v, dpp_mov<kDppXor1>(v));
+  if constexpr (Lanes >= 4) v = op(v, dpp_mov<kDppXor2>(v));
+  if constexpr (Lanes >= 8) v = op(v, dpp_mov<kDppHalfMirror>(v));
+  if constexpr (Lanes >= 16) v = op(v, dpp_mov<kDppMirror>(v));
+  if constexpr (Lanes >= 32) v = op(v, shfl_xor(v, 16));
+  if constexpr (Lanes >= 64) v = op(v, shfl_xor(v, 32));
   return v;
 }
 
 template <int Lanes>
-MHC_DEV float group_max(float v) {
-#pragma unroll
-  for (int m = 1; m < Lanes; m <<= 1) v = fmaxf(v, shfl_xor(v, m));
-  return v;
-}
+MHC_DEV float group_sum(float v) { return group_reduce<Lanes>(v, SumOp{}); }
 
-// all-reduce across lanes {l, l^Stride, l^2Stride, ...} up to Span lanes
+template <int Lanes>
+MHC_DEV float group_max(float v) { return group_reduce<Lanes>(v, MaxOp{}); }
+
+// all-reduce (sum) across lanes {l, l^Stride, l^2Stride, ...} up to Span lanes
 template <int Stride, int Span>
 MHC_DEV float strided_sum(float v) {
-#pragma unroll
-  for (int m = Stride; m < Span; m <<= 1) v += shfl_xor(v, m);
+  if constexpr (Stride <= 1 && Span >= 2) v += dpp_mov<kDppXor1>(v);
+  if constexpr (Stride <= 2 && Span >= 4) v += dpp_mov<kDppXor2>(v);
+  if constexpr (Stride <= 4 && Span >= 16) {
+    v += dpp_mov<kDppRor8>(v);  // lane ^ 8
+    v += dpp_mov<kDppRor4>(v);  // lane ^ 4 (bit 3 already reduced)
+  } else if constexpr (Stride == 8 && Span >= 16) {
+    v += dpp_mov<kDppRor8>(v);
+  } else if constexpr (Stride <= 4 && Span == 8) {
+    v += shfl_xor(v, 4);
+  }
+  if constexpr (Stride <= 16 && Span >= 32) v += shfl_xor(v, 16);
+  if constexpr (Stride <= 32 && Span >= 64) v += shfl_xor(v, 32);
   return v;
 }
 

@@ -77,4 +77,8 @@ int occupancy_blocks(const void* kernel, int tpb, size_t smem);
 // Integer tuning override from the environment (0 when unset).
 int env_int(const char* name, int dflt);
 
+// Upper bound on a one-dimensional grid; larger token counts are covered by
+// the kernels' grid-stride loops.
+constexpr int64_t kMaxGrid = 1 << 24;
+
 }  // namespace mhc

@@ -1,0 +1,221 @@
+// Sinkhorn-Knopp projection and its VJP for the matrices of one wavefront
+// (device functions shared by the batched kernels and the fused reduction).
+//
+// Semantics follow mhc_mlx/reference.py:20-48, 58-69:
+//   K = exp(H - rowmax(H));  repeat `iters` times:
+//     row step:    s_i = sum_j P_ij;  P_ij *= (s_i > eps ? 1/s_i : 1)
+//     column step: s_j = sum_i P_ij;  P_ij *= (s_j > eps ? 1/s_j : 0)
+//
+// Lane layout for an NP x NP matrix (NP = n rounded up to a power of two,
+// padding entries are exact zeros and never change a sum):
+//   E   elements per lane (NP*NP/64, at least 1),
+//   LR  lanes per row (a row is LR consecutive lanes, E columns each),
+//   G   lanes per matrix (NP*LR), MPW = 64/G matrices per wavefront.
+// Row sums reduce over LR adjacent lanes, column sums over lanes LR apart;
+// all `iters` rounds stay in registers.
+//
+// The VJP recomputes the forward and records, per iteration, the row and
+// column sums and the cumulative row/column scale vectors R_k, C_k
+// (4 * iters * W floats per wavefront).  The pre-step matrices are rebuilt
+// as R K C, which stays exact for masked (zeroed) columns, unlike dividing
+// the scaled matrix by its scale.
+#pragma once
+
+#include "mhc_device.hpp"
+
+namespace mhc {
+
+template <int NP>
+struct SkLayout {
+  static constexpr int E = NP * NP >= 64 ? NP * NP / 64 : 1;
+  static constexpr int LR = NP / E;
+  static constexpr int G = NP * LR;
+  static constexpr int MPW = 64 / G;
+  static constexpr int W = MPW * NP;  // row (or column) slots per wavefront
+};
+
+// Floats of VJP state per wavefront.
+__host__ __device__ inline int64_t sk_state_floats(int np, int iters) {
+  const int e = np * np >= 64 ? np * np / 64 : 1;
+  const int lr = np / e;
+  const int g = np * lr;
+  return (int64_t)4 * (iters > 0 ? iters : 1) * (64 / g) * np;
+}
+
+// Forward for the matrix of this lane's group: H / out point at that
+// matrix ([n, n] row-major); mvalid false for groups past the batch.
+template <int NP>
+MHC_DEV void sk_fwd_group(const float* __restrict__ H, float* __restrict__ out, bool mvalid, int n,
+                          int iters, float eps, int lane) {
+  using L = SkLayout<NP>;
+  const int lm = lane % L::G;
+  const int r = lm / L::LR;
+  const int c0 = (lm % L::LR) * L::E;
+  const bool rvalid = mvalid && r < n;
+  const float* Hr = H + (int64_t)r * n;
+  float P[L::E];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < L::E; ++e) {
+    const bool v = rvalid && (c0 + e) < n;
+    P[e] = v ? Hr[c0 + e] : -INFINITY;
+    mx = fmaxf(mx, P[e]);
+  }
+  mx = group_max<L::LR>(mx);
+#pragma unroll
+  for (int e = 0; e < L::E; ++e) {
+    const bool v = rvalid && (c0 + e) < n;
+    P[e] = v ? expf(P[e] - mx) : 0.0f;
+  }
+  for (int it = 0; it < iters; ++it) {
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) s += P[e];
+    s = group_sum<L::LR>(s);
+    const float rsc = (rvalid && s > eps) ? 1.0f / s : 1.0f;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) P[e] *= rsc;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) {
+      const float cs = strided_sum<L::LR, L::G>(P[e]);
+      const bool cv = mvalid && (c0 + e) < n;
+      const float csc = (cv && cs > eps) ? 1.0f / cs : 0.0f;
+      P[e] *= csc;
+    }
+  }
+  if (rvalid) {
+    float* O = out + (int64_t)r * n;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e)
+      if ((c0 + e) < n) O[c0 + e] = P[e];
+  }
+}
+
+// VJP for the matrix of this lane's group: dlogits = d/dH <dM, SK(H)>.
+// st: this wavefront's state, layout [4][iters][W] (row sums, cumulative row
+// scale R_k, column sums, cumulative column scale C_k).
+template <int NP>
+MHC_DEV void sk_bwd_group(const float* __restrict__ H, const float* __restrict__ dM,
+                          float* __restrict__ dlogits, bool mvalid, int n, int iters, float eps,
+                          float* st, int lane) {
+  using L = SkLayout<NP>;
+  const int lm = lane % L::G;
+  const int msub = lane / L::G;
+  const int r = lm / L::LR;
+  const int c0 = (lm % L::LR) * L::E;
+  const bool rvalid = mvalid && r < n;
+  float* st_rs = st;
+  float* st_R = st + (int64_t)iters * L::W;
+  float* st_cs = st + (int64_t)2 * iters * L::W;
+  float* st_C = st + (int64_t)3 * iters * L::W;
+  const int rslot = msub * NP + r;
+  const int cslot = msub * NP + c0;
+
+  const float* Hrow = H + (int64_t)r * n;
+  float Hr[L::E], K[L::E], P[L::E];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < L::E; ++e) {
+    const bool v = rvalid && (c0 + e) < n;
+    Hr[e] = v ? Hrow[c0 + e] : -INFINITY;
+    mx = fmaxf(mx, Hr[e]);
+  }
+  mx = group_max<L::LR>(mx);
+#pragma unroll
+  for (int e = 0; e < L::E; ++e) {
+    const bool v = rvalid && (c0 + e) < n;
+    K[e] = v ? expf(Hr[e] - mx) : 0.0f;
+    P[e] = K[e];
+  }
+  // forward recompute, recording sums and cumulative scales
+  float Rc = 1.0f;
+  float Cc[L::E];
+#pragma unroll
+  for (int e = 0; e < L::E; ++e) Cc[e] = 1.0f;
+  for (int it = 0; it < iters; ++it) {
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) s += P[e];
+    s = group_sum<L::LR>(s);
+    const float rsc = (rvalid && s > eps) ? 1.0f / s : 1.0f;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) P[e] *= rsc;
+    Rc *= rsc;
+    st_rs[(int64_t)it * L::W + rslot] = s;
+    st_R[(int64_t)it * L::W + rslot] = Rc;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) {
+      const float cs = strided_sum<L::LR, L::G>(P[e]);
+      const bool cv = mvalid && (c0 + e) < n;
+      const float csc = (cv && cs > eps) ? 1.0f / cs : 0.0f;
+      P[e] *= csc;
+      Cc[e] *= csc;
+      st_cs[(int64_t)it * L::W + cslot + e] = cs;
+      st_C[(int64_t)it * L::W + cslot + e] = Cc[e];
+    }
+  }
+  // reverse sweep
+  float Gd[L::E];
+  {
+    const float* D = dM + (int64_t)r * n;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) {
+      const bool v = rvalid && (c0 + e) < n;
+      Gd[e] = v ? D[c0 + e] : 0.0f;
+    }
+  }
+  for (int it = iters - 1; it >= 0; --it) {
+    const float Rk = st_R[(int64_t)it * L::W + rslot];
+    const float Rp = it > 0 ? st_R[(int64_t)(it - 1) * L::W + rslot] : 1.0f;
+    float Cp[L::E];
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) Cp[e] = it > 0 ? st_C[(int64_t)(it - 1) * L::W + cslot + e] : 1.0f;
+    // column step: input R_k K C_{k-1}
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) {
+      const float pin = Rk * K[e] * Cp[e];
+      const float dot = strided_sum<L::LR, L::G>(Gd[e] * pin);
+      const float cs = st_cs[(int64_t)it * L::W + cslot + e];
+      const bool cv = mvalid && (c0 + e) < n;
+      if (cv && cs > eps) {
+        const float sc = 1.0f / cs;
+        Gd[e] = sc * Gd[e] - sc * sc * dot;
+      } else {
+        Gd[e] = 0.0f;
+      }
+    }
+    // row step: input R_{k-1} K C_{k-1}
+    float prod = 0.0f;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e) prod += Gd[e] * (Rp * K[e] * Cp[e]);
+    const float dot = group_sum<L::LR>(prod);
+    const float rs = st_rs[(int64_t)it * L::W + rslot];
+    if (rvalid && rs > eps) {
+      const float sc = 1.0f / rs;
+#pragma unroll
+      for (int e = 0; e < L::E; ++e) Gd[e] = sc * Gd[e] - sc * sc * dot;
+    }
+  }
+  // through exp and the row-max shift (gradient of the max split evenly
+  // among tied maxima; it is zero in exact arithmetic)
+  float cnt = 0.0f, tot = 0.0f;
+  float dsh[L::E];
+#pragma unroll
+  for (int e = 0; e < L::E; ++e) {
+    const bool v = rvalid && (c0 + e) < n;
+    dsh[e] = v ? Gd[e] * K[e] : 0.0f;
+    tot += dsh[e];
+    cnt += (v && Hr[e] == mx) ? 1.0f : 0.0f;
+  }
+  tot = group_sum<L::LR>(tot);
+  cnt = group_sum<L::LR>(cnt);
+  if (rvalid) {
+    float* O = dlogits + (int64_t)r * n;
+    const float corr = cnt > 0.0f ? tot / cnt : 0.0f;
+#pragma unroll
+    for (int e = 0; e < L::E; ++e)
+      if ((c0 + e) < n) O[c0 + e] = dsh[e] - (Hr[e] == mx ? corr : 0.0f);
+  }
+}
+
+}  // namespace mhc

@@ -26,7 +26,7 @@ import ctypes
 
 import torch
 
-from . import _lib
+from . import _lib, profiling
 from .profiling import timed
 
 __all__ = [
@@ -332,21 +332,80 @@ def mhc_forward_fused_hip_autograd(x, M, H_pre, H_post, rms_weight, eps: float =
 # layer-level fused functions (raw logits)
 # --------------------------------------------------------------------------
 
+def _layer_fwd(x, hpre, hpost, hres, w, iters, eps, out_dtype, per_token):
+    """mhc_layer_fwd: Sinkhorn projection + fused forward from raw parameters. Returns (out, M)."""
+    B, n, C = (int(s) for s in x.shape)
+    xc = x.detach().contiguous()
+    hp, hq, hr, wc = _f32(hpre), _f32(hpost), _f32(hres), _f32(w)
+    M = torch.empty_like(hr)
+    out = torch.empty((B, n, C), dtype=out_dtype, device=x.device)
+    s = _stream(xc)
+    if profiling._active is None:
+        _lib.call("mhc_layer_fwd", _p(xc), _code(xc.dtype), _p(hp), _p(hq), _p(hr), _p(wc), _p(out),
+                  _code(out_dtype), _p(M), B, n, C, int(per_token), int(iters), float(eps), s)
+        return out, M
+    # under a kernel timer: the same two kernels, launched by separate calls
+    with timed("sinkhorn_fwd"):
+        _lib.call("mhc_sinkhorn_fwd", _p(hr), _p(M), B if per_token else 1, n, int(iters), float(eps), s)
+    with timed("fused_fwd"):
+        _lib.call("mhc_fused_fwd", _p(xc), _code(xc.dtype), _p(M), n * n if per_token else 0, _p(hp), _p(hq),
+                  n if per_token else 0, _lib.H_RAW, _p(wc), _p(out), _code(out_dtype), None, B, n, C,
+                  float(eps), s)
+    return out, M
+
+
+def _layer_bwd(x, g, hpre, hpost, hres, M, w, iters, eps, per_token):
+    """mhc_layer_bwd: (dx, dH_pre_raw, dH_post_raw, dH_res_raw, d_rms_weight)."""
+    B, n, C = (int(s) for s in x.shape)
+    dev = x.device
+    xc = x.detach().contiguous()
+    gdt = g.dtype if g.dtype in (torch.float32, xc.dtype) else torch.float32
+    gc = g.detach().to(gdt).contiguous()
+    hp, hq, hr, Mc, wc = _f32(hpre), _f32(hpost), _f32(hres), _f32(M), _f32(w)
+    dx = torch.empty_like(xc)
+    dpre = torch.empty_like(hp)
+    dpost = torch.empty_like(hq)
+    dres = torch.empty_like(hr)
+    dw = torch.empty((C,), dtype=torch.float32, device=dev)
+    nb = _lib.query("mhc_layer_bwd_workspace_bytes", B, n, C, int(per_token), int(iters))
+    ws = _ws(nb, dev)
+    s = _stream(xc)
+    if profiling._active is None:
+        _lib.call("mhc_layer_bwd", _p(xc), _code(xc.dtype), _p(gc), _code(gc.dtype), _p(hp), _p(hq), _p(hr),
+                  _p(Mc), _p(wc), _p(dx), _p(dpre), _p(dpost), _p(dres), _p(dw), _p(ws), nb, B, n, C,
+                  int(per_token), int(iters), float(eps), s)
+        return dx, dpre, dpost, dres, dw
+    # under a kernel timer: partial sums and the reduction as separate calls
+    np_ = ctypes.c_int64(0)
+    if B > 0:
+        nbp = _lib.query("mhc_fused_bwd_workspace_bytes", B, n, C, int(per_token))
+        with timed("fused_bwd"):
+            _lib.call("mhc_fused_bwd_partials", _p(xc), _code(xc.dtype), _p(gc), _code(gc.dtype), _p(Mc),
+                      n * n if per_token else 0, _p(hp), _p(hq), n if per_token else 0, _lib.H_RAW, _p(wc),
+                      _p(dx), _code(xc.dtype), _p(dres) if per_token else None,
+                      _p(dpre) if per_token else None, _p(dpost) if per_token else None, _p(ws), nbp, B, n, C,
+                      float(eps), ctypes.byref(np_), s)
+    with timed("layer_bwd_reduce"):
+        _lib.call("mhc_layer_bwd_reduce", _p(ws), nb, np_.value, _p(hp), _p(hq), _p(hr), _p(dpre), _p(dpost),
+                  _p(dres), _p(dw), B, n, C, int(per_token), int(iters), float(eps), s)
+    return dx, dpre, dpost, dres, dw
+
+
 class MHCLayerFn(torch.autograd.Function):
     """Whole MHCLayer forward/backward from raw parameters (layer.py:383-407).
 
-    Forward: Sinkhorn projection, then the fused kernel with the sigmoid
-    activations applied inside.  Backward: fused dx + partials, the
-    fixed-order reduction with the activation chain, then the Sinkhorn VJP.
-    Parameters are layer-wide ([n], [n], [n, n]) or per token ([B, n],
-    [B, n], [B, n, n]).
+    Forward: one library call (Sinkhorn projection, then the fused kernel
+    with the sigmoid activations applied inside).  Backward: one library call
+    (fused dx + partial sums, then a single launch that reduces the partial
+    rows in a fixed order, applies the activation chain and runs the Sinkhorn
+    VJP).  Parameters are layer-wide ([n], [n], [n, n]) or per token
+    ([B, n], [B, n], [B, n, n]).
     """
 
     @staticmethod
     def forward(ctx, x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype):
         per_token = H_res_raw.ndim == 3
-        M = _sinkhorn_fwd(H_res_raw, iters, eps)
-        out = _fused_fwd(x, M, H_pre_raw, H_post_raw, rms_weight, eps, out_dtype, _lib.H_RAW, per_token)
+        out, M = _layer_fwd(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype, per_token)
         ctx.save_for_backward(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, M)
         ctx.iters, ctx.eps, ctx.per_token = iters, eps, per_token
         return out
@@ -354,9 +413,8 @@ class MHCLayerFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         x, hpre, hpost, hres, w, M = ctx.saved_tensors
-        dx, dM, dpre, dpost, dw = _fused_bwd(x, dout, M, hpre, hpost, w, ctx.eps, _lib.H_RAW,
-                                             ctx.per_token)
-        dres = _sinkhorn_bwd(hres, dM, ctx.iters, ctx.eps)
+        dx, dpre, dpost, dres, dw = _layer_bwd(x, dout, hpre, hpost, hres, M, w, ctx.iters, ctx.eps,
+                                               ctx.per_token)
         return (dx, dpre.to(hpre.dtype), dpost.to(hpost.dtype), dres.to(hres.dtype), dw.to(w.dtype),
                 None, None, None)
 

@@ -1,0 +1,103 @@
+"""The C ABI: include/mhc_hip.h <-> libmhc_hip.so <-> the ctypes table (CPU only).
+
+Loading the library and calling its pure-host entry points (version, error
+text, argument validation) needs no GPU; nothing here launches a kernel.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mhc_mlx_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mhc_hip.h"
+
+
+def _declarations():
+    """{name: parameter count} of every function declared in the header."""
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(mhc_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libmhc_hip.so not built")
+    return _lib.load()
+
+
+def test_header_declares_the_ctypes_table():
+    decl = _declarations()
+    assert set(decl) == set(_lib.SIGNATURES), set(decl) ^ set(_lib.SIGNATURES)
+    for name, (args, _res) in _lib.SIGNATURES.items():
+        assert len(args) == decl[name], name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declarations():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_error_text(lib):
+    assert lib.mhc_abi_version() == 1
+    assert isinstance(lib.mhc_last_error(), bytes)
+
+
+@pytest.mark.parametrize("n,C,T", [(0, 16, 1), (65, 16, 1), (4, 0, 1), (4, 16, -1)])
+def test_fused_fwd_rejects_bad_shapes_on_the_host(lib, n, C, T):
+    rc = lib.mhc_fused_fwd(None, 1, None, 0, None, None, 0, _lib.H_RAW, None, None, 1, None, T, n, C,
+                           ctypes.c_float(1e-6), None)
+    assert rc == -1
+    assert lib.mhc_last_error()
+
+
+def test_fused_fwd_rejects_mixed_parameter_modes(lib):
+    rc = lib.mhc_fused_fwd(None, 1, None, 16, None, None, 0, _lib.H_RAW, None, None, 1, None, 8, 4, 16,
+                           ctypes.c_float(1e-6), None)
+    assert rc == -1
+    assert b"per-token" in lib.mhc_last_error()
+
+
+def test_fused_fwd_rejects_bad_output_dtype(lib):
+    dummy = ctypes.c_void_p(16)
+    rc = lib.mhc_fused_fwd(dummy, 1, dummy, 0, dummy, dummy, 0, _lib.H_RAW, dummy, dummy, 2, None, 8, 4, 16,
+                           ctypes.c_float(1e-6), None)
+    assert rc == -1
+    assert b"out_dtype" in lib.mhc_last_error()
+
+
+def test_zero_tokens_is_a_no_op(lib):
+    rc = lib.mhc_fused_fwd(None, 1, None, 0, None, None, 0, _lib.H_RAW, None, None, 1, None, 0, 4, 16,
+                           ctypes.c_float(1e-6), None)
+    assert rc == 0
+
+
+def test_sinkhorn_rejects_bad_arguments(lib):
+    assert lib.mhc_sinkhorn_fwd(None, None, 1, 0, 20, ctypes.c_float(1e-5), None) == -1
+    assert lib.mhc_sinkhorn_fwd(None, None, 1, 4, -1, ctypes.c_float(1e-5), None) == -1
+    assert lib.mhc_sinkhorn_fwd(None, None, 0, 4, 20, ctypes.c_float(1e-5), None) == 0
+    assert lib.mhc_sinkhorn_fwd(None, None, 2, 4, 20, ctypes.c_float(1e-5), None) == -1
+
+
+def test_layer_bwd_rejects_null_gradients(lib):
+    dummy = ctypes.c_void_p(16)
+    rc = lib.mhc_layer_bwd(dummy, 1, dummy, 1, dummy, dummy, dummy, dummy, dummy, dummy, None, None, None, None,
+                           None, 0, 8, 4, 16, 0, 20, ctypes.c_float(1e-6), None)
+    assert rc == -1
+    assert b"gradient" in lib.mhc_last_error()
+
+
+def test_check_maps_status_to_exceptions(lib):
+    _lib.check(0, "ok")
+    lib.mhc_sinkhorn_fwd(None, None, 1, 0, 20, ctypes.c_float(1e-5), None)
+    with pytest.raises(ValueError):
+        _lib.check(-1, "mhc_sinkhorn_fwd")
+    with pytest.raises(_lib.MHCError):
+        _lib.check(1, "x")

@@ -118,9 +118,41 @@ def test_hip_path_is_the_one_that_runs(monkeypatch):
     layer = MHCLayer(n=4, C=128).cuda()
     x = torch.randn(2, 4, 128, device="cuda", requires_grad=True)
     layer(x).sum().backward()
-    for k in ("mhc_sinkhorn_fwd", "mhc_fused_fwd", "mhc_fused_bwd_partials", "mhc_reduce_param_grads",
-              "mhc_sinkhorn_bwd"):
+    assert "mhc_layer_fwd" in calls and "mhc_layer_bwd" in calls
+
+
+def test_timed_path_uses_the_same_kernels(monkeypatch):
+    """Under kernel_timer the layer splits its calls per kernel; results are bitwise equal."""
+    from mhc_mlx_amd import kernel_timer
+
+    torch.manual_seed(3)
+    layer = MHCLayer(n=4, C=512, identity_init=False).cuda()
+    x = torch.randn(33, 4, 512, device="cuda", dtype=torch.bfloat16)
+    g = torch.randn_like(x)
+
+    def run():
+        xx = x.clone().requires_grad_(True)
+        out = layer(xx, return_dtype=torch.bfloat16)
+        grads = torch.autograd.grad(out, [xx] + list(layer.parameters()), g)
+        return [out] + list(grads)
+
+    plain = run()
+    calls = []
+    orig = _lib.call
+
+    def spy(name, *args):
+        calls.append(name)
+        return orig(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    with kernel_timer() as kt:
+        timed = run()
+        stats = kt.stats()
+    for k in ("mhc_sinkhorn_fwd", "mhc_fused_fwd", "mhc_fused_bwd_partials", "mhc_layer_bwd_reduce"):
         assert k in calls
+    assert {"sinkhorn_fwd", "fused_fwd", "fused_bwd", "layer_bwd_reduce"} <= set(stats)
+    for a, b in zip(plain, timed):
+        assert torch.equal(a, b)
 
 
 def test_determinism_and_state_dict():
