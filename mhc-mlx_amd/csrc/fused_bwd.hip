@@ -890,9 +890,14 @@ __global__ __launch_bounds__(kFinThreads) void param_finish_kernel(RedArgs R) {
   if constexpr (SKNP > 0) {
     if (wg == R.nd) {
       __syncthreads();  // s_dM complete
-      if (tid < 64)
-        sk_bwd_group<SKNP>(R.hres, s_dM, R.dhres, tid < SkLayout<SKNP>::G, n, R.iters, R.eps,
-                           fin_smem + round_up(nn, 4), tid);
+      if (tid < 64) {
+        if (R.iters <= kSkRegIters)
+          sk_bwd_group_reg<SKNP, kSkRegIters>(R.hres, s_dM, R.dhres, tid < SkLayout<SKNP>::G, n, R.iters, R.eps,
+                                              tid);
+        else
+          sk_bwd_group<SKNP>(R.hres, s_dM, R.dhres, tid < SkLayout<SKNP>::G, n, R.iters, R.eps,
+                             fin_smem + round_up(nn, 4), tid);
+      }
     }
   }
 }
@@ -946,12 +951,11 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
   if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
   set_rows(A, L);
+  const dim3 g((unsigned)blocks), b(tpb);
   if (full)
-    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, true>), dim3((unsigned)blocks), dim3(tpb), 0,
-                       stream, A);
+    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, true>), g, b, 0, stream, A);
   else
-    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, false>), dim3((unsigned)blocks), dim3(tpb), 0,
-                       stream, A);
+    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, false>), g, b, 0, stream, A);
   MHC_CHECK_LAUNCH("fused_bwd_lw_kernel");
   *num_partials = blocks;
   return MHC_OK;

@@ -393,12 +393,11 @@ int launch_fwd_full(FwdArgs A, hipStream_t stream) {
   if (nchunks % 64 != 0 || nchunks / ch > 1024) return 1;
   const int tpb = nchunks / ch;
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, kMaxGrid));
+  const dim3 g((unsigned)blocks), b(tpb);
   if (ch == 2)
-    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 2>), dim3((unsigned)blocks), dim3(tpb), 0,
-                       stream, A);
+    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 2>), g, b, 0, stream, A);
   else
-    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1>), dim3((unsigned)blocks), dim3(tpb), 0,
-                       stream, A);
+    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1>), g, b, 0, stream, A);
   MHC_CHECK_LAUNCH("fused_fwd_full_kernel");
   return MHC_OK;
 }

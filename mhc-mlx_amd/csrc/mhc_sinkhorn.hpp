@@ -25,6 +25,14 @@
 
 namespace mhc {
 
+// Row / column scale 1/s: the hardware reciprocal (v_rcp_f32, within 1 ulp;
+// s > eps > 0 is never denormal).  The reference divides by s; the results
+// agree to a few ulp, far inside the fp32 tolerance.
+MHC_DEV float sk_rcp(float s) { return __builtin_amdgcn_rcpf(s); }
+
+// Iteration counts up to this keep the VJP state in registers (n <= 8).
+constexpr int kSkRegIters = 32;
+
 template <int NP>
 struct SkLayout {
   static constexpr int E = NP * NP >= 64 ? NP * NP / 64 : 1;
@@ -72,14 +80,14 @@ MHC_DEV void sk_fwd_group(const float* __restrict__ H, float* __restrict__ out, 
 #pragma unroll
     for (int e = 0; e < L::E; ++e) s += P[e];
     s = group_sum<L::LR>(s);
-    const float rsc = (rvalid && s > eps) ? 1.0f / s : 1.0f;
+    const float rsc = (rvalid && s > eps) ? sk_rcp(s) : 1.0f;
 #pragma unroll
     for (int e = 0; e < L::E; ++e) P[e] *= rsc;
 #pragma unroll
     for (int e = 0; e < L::E; ++e) {
       const float cs = strided_sum<L::LR, L::G>(P[e]);
       const bool cv = mvalid && (c0 + e) < n;
-      const float csc = (cv && cs > eps) ? 1.0f / cs : 0.0f;
+      const float csc = (cv && cs > eps) ? sk_rcp(cs) : 0.0f;
       P[e] *= csc;
     }
   }
@@ -137,7 +145,7 @@ MHC_DEV void sk_bwd_group(const float* __restrict__ H, const float* __restrict__
 #pragma unroll
     for (int e = 0; e < L::E; ++e) s += P[e];
     s = group_sum<L::LR>(s);
-    const float rsc = (rvalid && s > eps) ? 1.0f / s : 1.0f;
+    const float rsc = (rvalid && s > eps) ? sk_rcp(s) : 1.0f;
 #pragma unroll
     for (int e = 0; e < L::E; ++e) P[e] *= rsc;
     Rc *= rsc;
@@ -147,7 +155,7 @@ MHC_DEV void sk_bwd_group(const float* __restrict__ H, const float* __restrict__
     for (int e = 0; e < L::E; ++e) {
       const float cs = strided_sum<L::LR, L::G>(P[e]);
       const bool cv = mvalid && (c0 + e) < n;
-      const float csc = (cv && cs > eps) ? 1.0f / cs : 0.0f;
+      const float csc = (cv && cs > eps) ? sk_rcp(cs) : 0.0f;
       P[e] *= csc;
       Cc[e] *= csc;
       st_cs[(int64_t)it * L::W + cslot + e] = cs;
@@ -178,7 +186,7 @@ MHC_DEV void sk_bwd_group(const float* __restrict__ H, const float* __restrict__
       const float cs = st_cs[(int64_t)it * L::W + cslot + e];
       const bool cv = mvalid && (c0 + e) < n;
       if (cv && cs > eps) {
-        const float sc = 1.0f / cs;
+        const float sc = sk_rcp(cs);
         Gd[e] = sc * Gd[e] - sc * sc * dot;
       } else {
         Gd[e] = 0.0f;
@@ -191,7 +199,7 @@ MHC_DEV void sk_bwd_group(const float* __restrict__ H, const float* __restrict__
     const float dot = group_sum<L::LR>(prod);
     const float rs = st_rs[(int64_t)it * L::W + rslot];
     if (rvalid && rs > eps) {
-      const float sc = 1.0f / rs;
+      const float sc = sk_rcp(rs);
 #pragma unroll
       for (int e = 0; e < L::E; ++e) Gd[e] = sc * Gd[e] - sc * sc * dot;
     }
@@ -215,6 +223,72 @@ MHC_DEV void sk_bwd_group(const float* __restrict__ H, const float* __restrict__
 #pragma unroll
     for (int e = 0; e < L::E; ++e)
       if ((c0 + e) < n) O[c0 + e] = dsh[e] - (Hr[e] == mx ? corr : 0.0f);
+  }
+}
+
+// sk_bwd_group with the per-iteration state in registers: one element per
+// lane (NP <= 8) and iters <= ITMAX, loops fully unrolled and predicated on
+// the uniform iteration count.  Same arithmetic, same results.
+template <int NP, int ITMAX>
+MHC_DEV void sk_bwd_group_reg(const float* __restrict__ H, const float* __restrict__ dM,
+                              float* __restrict__ dlogits, bool mvalid, int n, int iters, float eps, int lane) {
+  using L = SkLayout<NP>;
+  static_assert(L::E == 1, "register state holds one element per lane");
+  const int lm = lane % L::G;
+  const int r = lm / L::LR;
+  const int c0 = lm % L::LR;
+  const bool rvalid = mvalid && r < n;
+  const bool v = rvalid && c0 < n;
+  const bool cv = mvalid && c0 < n;
+  const float Hr = v ? H[(int64_t)r * n + c0] : -INFINITY;
+  const float mx = group_max<L::LR>(Hr);
+  const float K = v ? expf(Hr - mx) : 0.0f;
+  float rs_[ITMAX], R_[ITMAX], cs_[ITMAX], C_[ITMAX];
+  float P = K, Rc = 1.0f, Cc = 1.0f;
+#pragma unroll
+  for (int it = 0; it < ITMAX; ++it) {
+    if (it < iters) {
+      const float s = group_sum<L::LR>(P);
+      const float rsc = (rvalid && s > eps) ? sk_rcp(s) : 1.0f;
+      P *= rsc;
+      Rc *= rsc;
+      rs_[it] = s;
+      R_[it] = Rc;
+      const float cs = strided_sum<L::LR, L::G>(P);
+      const float csc = (cv && cs > eps) ? sk_rcp(cs) : 0.0f;
+      P *= csc;
+      Cc *= csc;
+      cs_[it] = cs;
+      C_[it] = Cc;
+    }
+  }
+  float Gd = v ? dM[(int64_t)r * n + c0] : 0.0f;
+#pragma unroll
+  for (int it = ITMAX - 1; it >= 0; --it) {
+    if (it < iters) {
+      const float Rk = R_[it];
+      const float Rp = it > 0 ? R_[it > 0 ? it - 1 : 0] : 1.0f;
+      const float Cp = it > 0 ? C_[it > 0 ? it - 1 : 0] : 1.0f;
+      const float dotc = strided_sum<L::LR, L::G>(Gd * (Rk * K * Cp));
+      if (cv && cs_[it] > eps) {
+        const float sc = sk_rcp(cs_[it]);
+        Gd = sc * Gd - sc * sc * dotc;
+      } else {
+        Gd = 0.0f;
+      }
+      const float dotr = group_sum<L::LR>(Gd * (Rp * K * Cp));
+      if (rvalid && rs_[it] > eps) {
+        const float sc = sk_rcp(rs_[it]);
+        Gd = sc * Gd - sc * sc * dotr;
+      }
+    }
+  }
+  const float dsh = v ? Gd * K : 0.0f;
+  const float tot = group_sum<L::LR>(dsh);
+  const float cnt = group_sum<L::LR>((v && Hr == mx) ? 1.0f : 0.0f);
+  if (v) {
+    const float corr = cnt > 0.0f ? tot / cnt : 0.0f;
+    dlogits[(int64_t)r * n + c0] = dsh - (Hr == mx ? corr : 0.0f);
   }
 }
 

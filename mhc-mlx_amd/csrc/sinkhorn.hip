@@ -55,6 +55,13 @@ __global__ __launch_bounds__(kSkThreads) void sinkhorn_bwd_kernel(
     const int64_t mat = grp * L::MPW + msub;
     const bool mvalid = mat < batch;
     const int64_t m = mvalid ? mat : 0;
+    if constexpr (SkLayout<NP>::E == 1) {
+      if (iters <= kSkRegIters) {
+        sk_bwd_group_reg<NP, kSkRegIters>(logits + m * nn, dM + m * nn, dlogits + m * nn, mvalid, n, iters, eps,
+                                          lane);
+        continue;
+      }
+    }
     sk_bwd_group<NP>(logits + m * nn, dM + m * nn, dlogits + m * nn, mvalid, n, iters, eps, st, lane);
   }
 }

@@ -1,0 +1,276 @@
+"""GPU parity at the benchmark configurations and on every kernel path they use.
+
+* Config 0 (x [1,4,512] fp32) and config 1 (x [32,4,2048] bf16) are small
+  enough for the float64 oracle at full size.
+* Shapes that reach the full-tile kernels (two chunks per thread, T >= CU
+  count) and the multi-row parameter reduction (more than 64 partial rows),
+  at sizes the oracle finishes in about a second.
+* Config 2 (32768 x 4 x 4096 bf16, fwd+bwd) and config 3 (16384 x 16 x 1024
+  bf16, per-token parameters) at full size, through properties that do not
+  need the oracle to see every token: tokens are independent, so out / dx
+  (and the per-token parameter gradients) of a random sample of tokens must
+  match the oracle run on those tokens alone; the layer-wide parameter
+  gradients are sums over tokens and are compared with a float64 torch
+  reference of the same sums computed on the GPU in chunks, then chained
+  through the oracle's sigmoid and Sinkhorn VJP; the mixing matrices must be
+  doubly stochastic to the oracle's own residual; a second run must be
+  bitwise identical.
+* Config 4 (MHCRewire(Linear(4096, 4096)), n=4, 8192 tokens) against the
+  explicit fp32 formulation of layer.py:332-337 with the same bf16 GEMM.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mhc_oracle as O
+from tests._helpers import dev_tensor, np_of, params, rel_err, rng, to_dtype_np
+
+from mhc_mlx_amd import MHCLayer, MHCRewire, ops
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+def _layer_from(hpre, hpost, hres, w, n, C):
+    layer = MHCLayer(n=n, C=C, sinkhorn_iters=20, eps=EPS).cuda()
+    with torch.no_grad():
+        layer.H_pre_raw.copy_(torch.from_numpy(hpre))
+        layer.H_post_raw.copy_(torch.from_numpy(hpost))
+        layer.H_res_raw.copy_(torch.from_numpy(hres))
+        layer.rms_weight.copy_(torch.from_numpy(w))
+    return layer
+
+
+def _fwd_bwd(layer, x, dout):
+    xt = x.clone().requires_grad_(True)
+    out = layer(xt, return_dtype=x.dtype)
+    grads = torch.autograd.grad(out, [xt] + list(layer.parameters()), dout)
+    return out, grads
+
+
+# --------------------------------------------------------------- configs 0 and 1
+
+
+def test_config0_forward_fp32():
+    """x [1,4,512] fp32 N(0,1), seed 0, eps 1e-6."""
+    g = rng(0)
+    x = g.standard_normal((1, 4, 512)).astype(np.float32)
+    hpre, hpost, hres, w = params(g, 4, 512)
+    layer = _layer_from(hpre, hpost, hres, w, 4, 512)
+    out = layer(dev_tensor(x))
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    assert out.dtype == torch.float32
+    assert rel_err(np_of(out), ref) < 1e-5
+
+
+def test_config1_forward_bf16():
+    """x [32,4,2048] bf16 with bf16 output (latency regime)."""
+    g = rng(1)
+    x = to_dtype_np(g.standard_normal((32, 4, 2048)), "bf16")
+    hpre, hpost, hres, w = params(g, 4, 2048)
+    layer = _layer_from(hpre, hpost, hres, w, 4, 2048)
+    out = layer(dev_tensor(x, "bf16"), return_dtype=torch.bfloat16)
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    got = np_of(out)
+    assert rel_err(got, ref) < 2e-2
+    assert (np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6).all()
+
+
+# ----------------------------------------------------- full-tile kernel paths
+
+
+@pytest.mark.parametrize("T,n,C,dt", [(300, 4, 1024, "bf16"), (300, 4, 1024, "f32"), (300, 8, 512, "bf16"),
+                                      (600, 4, 1024, "bf16"), (40, 4, 2048, "f16")])
+def test_full_tile_paths_fwd_bwd(T, n, C, dt):
+    """T >= CU count (two chunks per thread), C a multiple of the tile, > 64 partial rows."""
+    g = rng(T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C)
+    layer = _layer_from(hpre, hpost, hres, w, n, C)
+    xt = dev_tensor(x, dt)
+    out, grads = _fwd_bwd(layer, xt, dev_tensor(dout, dt))
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    tol = {"f32": 1e-5, "bf16": 2e-2, "f16": 5e-3}[dt]
+    assert rel_err(np_of(out), ref) < tol
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    for name, got, r in zip(["dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], grads, refs):
+        t = tol if name == "dx" else 1e-4
+        assert rel_err(np_of(got), r) < t, (name, rel_err(np_of(got), r))
+
+
+# -------------------------------------------------------- full-size helpers
+
+
+def _param_grads_f64(x, g, a, p, M, w, chunk=2048):
+    """Layer-wide sums of the VJP in float64 on the GPU (same equations as the oracle)."""
+    T, n, C = x.shape
+    a, p, w = a.double(), p.double(), w.double()
+    dM = torch.zeros(n, n, dtype=torch.float64, device=x.device)
+    dA = torch.zeros(n, dtype=torch.float64, device=x.device)
+    dP = torch.zeros(n, dtype=torch.float64, device=x.device)
+    dw = torch.zeros(C, dtype=torch.float64, device=x.device)
+    for s in range(0, T, chunk):
+        xf = x[s:s + chunk].double()
+        gf = g[s:s + chunk].double()
+        y = (xf * a[None, :, None]).sum(1)
+        inv = torch.rsqrt((y * y).mean(-1) + EPS)
+        dyn = (gf * p[None, :, None]).sum(1)
+        d_r = (dyn * y * w).sum(-1)
+        dy = dyn * inv[:, None] * w - ((inv ** 3) / C * d_r)[:, None] * y
+        for i in range(n):
+            for j in range(n):
+                dM[i, j] += (gf[:, i] * xf[:, j]).sum()
+        dA += (dy[:, None, :] * xf).sum((0, 2))
+        dP += (gf * (y * inv[:, None] * w)[:, None, :]).sum((0, 2))
+        dw += (dyn * y * inv[:, None]).sum(0)
+    return dM.cpu().numpy(), dA.cpu().numpy(), dP.cpu().numpy(), dw.cpu().numpy()
+
+
+def _sample(T, k, seed):
+    return np.sort(np.random.default_rng(seed).choice(T, size=k, replace=False))
+
+
+# --------------------------------------------------------------- config 2
+
+
+def test_config2_full_size_fwd_bwd():
+    """32768 tokens x 4 streams x 4096 channels, bf16, all gradients."""
+    T, n, C = 32768, 4, 4096
+    g = rng(2)
+    hpre, hpost, hres, w = params(g, n, C)
+    layer = _layer_from(hpre, hpost, hres, w, n, C)
+    gen = torch.Generator("cuda").manual_seed(2)
+    x = torch.randn(T, n, C, device="cuda", dtype=torch.bfloat16, generator=gen)
+    dout = torch.randn(T, n, C, device="cuda", dtype=torch.bfloat16, generator=gen)
+    out, grads = _fwd_bwd(layer, x, dout)
+    dx, d_pre, d_post, d_res, d_w = grads
+
+    # token-local outputs on a sample of tokens vs the oracle on those tokens
+    idx = _sample(T, 48, 20)
+    xs, gs = np_of(x[idx]).astype(np.float32), np_of(dout[idx]).astype(np.float32)
+    ref = O.mhc_forward_reference(xs, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    assert rel_err(np_of(out[idx]), ref) < 2e-2
+    rdx = O.mhc_backward_reference(xs, hpre, hpost, hres, w, gs, sinkhorn_iters=20, eps=EPS)[0]
+    assert rel_err(np_of(dx[idx]), rdx) < 2e-2
+
+    # layer-wide sums vs float64 on the GPU, chained through the oracle
+    a, p = O.activate_pre_post(hpre, hpost)
+    M = O.mixing_matrix_from_logits(hres, iters=20, eps=EPS)
+    dM, dA, dP, dw = _param_grads_f64(x, dout, torch.from_numpy(a).cuda(), torch.from_numpy(p).cuda(),
+                                      torch.from_numpy(M).cuda(), torch.from_numpy(w).cuda())
+    s_pre, s_post = O.sigmoid(hpre), O.sigmoid(hpost)
+    assert rel_err(np_of(d_pre), dA * s_pre * (1 - s_pre)) < 1e-4
+    assert rel_err(np_of(d_post), dP * 2 * s_post * (1 - s_post)) < 1e-4
+    assert rel_err(np_of(d_w), dw) < 1e-4
+    assert rel_err(np_of(d_res), O.sinkhorn_knopp_vjp(hres, dM, iters=20, eps=EPS)) < 1e-4
+
+    # the mixing matrix and a bitwise rerun
+    Mg = np_of(layer.mixing_matrix())
+    assert rel_err(Mg, M) < 1e-5
+    assert O.ds_residual(Mg) <= max(1e-5, O.ds_residual(M) + 1e-6)
+    out2, grads2 = _fwd_bwd(layer, x, dout)
+    assert torch.equal(out, out2)
+    for u, v in zip(grads, grads2):
+        assert torch.equal(u, v)
+
+
+# --------------------------------------------------------------- config 3
+
+
+def test_config3_full_size_dynamic_fwd_bwd():
+    """16384 tokens x 16 streams x 1024 channels, bf16, per-token H (batched Sinkhorn over 16384 matrices)."""
+    T, n, C = 16384, 16, 1024
+    g = rng(3)
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T)
+    layer = MHCLayer(n=n, C=C, sinkhorn_iters=20, eps=EPS).cuda()
+    with torch.no_grad():
+        layer.rms_weight.copy_(torch.from_numpy(w))
+    gen = torch.Generator("cuda").manual_seed(3)
+    x = torch.randn(T, n, C, device="cuda", dtype=torch.bfloat16, generator=gen)
+    dout = torch.randn(T, n, C, device="cuda", dtype=torch.bfloat16, generator=gen)
+    ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres)]
+    xt = x.clone().requires_grad_(True)
+    out = layer.forward_dynamic(xt, *ps, return_dtype=torch.bfloat16)
+    grads = torch.autograd.grad(out, [xt] + ps + [layer.rms_weight], dout)
+    dx, d_pre, d_post, d_res, d_w = grads
+
+    # everything but d_w is token-local: sample tokens vs the oracle
+    idx = _sample(T, 32, 30)
+    xs, gs = np_of(x[idx]).astype(np.float32), np_of(dout[idx]).astype(np.float32)
+    hp, hq, hr = hpre[idx], hpost[idx], hres[idx]
+    ref = O.mhc_forward_reference(xs, hp, hq, hr, w, sinkhorn_iters=20, eps=EPS)
+    assert rel_err(np_of(out[idx]), ref) < 2e-2
+    refs = O.mhc_backward_reference(xs, hp, hq, hr, w, gs, sinkhorn_iters=20, eps=EPS)
+    assert rel_err(np_of(dx[idx]), refs[0]) < 2e-2
+    assert rel_err(np_of(d_pre[idx]), refs[1]) < 1e-4
+    assert rel_err(np_of(d_post[idx]), refs[2]) < 1e-4
+    assert rel_err(np_of(d_res[idx]), refs[3]) < 1e-4
+
+    # d_w sums every token: float64 reference on the GPU with per-token a, p
+    a, p = O.activate_pre_post(hpre, hpost)
+    at, pt = torch.from_numpy(a).cuda(), torch.from_numpy(p).cuda()
+    wt = torch.from_numpy(w).cuda().double()
+    dw = torch.zeros(C, dtype=torch.float64, device="cuda")
+    for s in range(0, T, 2048):
+        xf, gf = x[s:s + 2048].double(), dout[s:s + 2048].double()
+        y = (xf * at[s:s + 2048, :, None]).sum(1)
+        inv = torch.rsqrt((y * y).mean(-1) + EPS)
+        dyn = (gf * pt[s:s + 2048, :, None]).sum(1)
+        dw += (dyn * y * inv[:, None]).sum(0)
+    assert rel_err(np_of(d_w), dw.cpu().numpy()) < 1e-4
+
+    # all 16384 mixing matrices: doubly stochastic to the oracle's residual
+    Mg = ops.sinkhorn_knopp_hip(dev_tensor(hres), iters=20, eps=EPS)
+    Mo = O.mixing_matrix_from_logits(hres[idx], iters=20, eps=EPS)
+    assert rel_err(np_of(Mg[idx]), Mo) < 1e-5
+    Mh = np_of(Mg)
+    res = max(np.abs(Mh.sum(-1) - 1).max(), np.abs(Mh.sum(-2) - 1).max())
+    Mall = O.mixing_matrix_from_logits(hres, iters=20, eps=EPS)
+    res_o = max(np.abs(Mall.sum(-1) - 1).max(), np.abs(Mall.sum(-2) - 1).max())
+    assert res <= max(1e-5, res_o + 1e-6), (res, res_o)
+
+
+# --------------------------------------------------------------- config 4
+
+
+def test_config4_rewire_linear_full_size():
+    """MHCRewire(Linear(4096, 4096, bias=False), dims=4096, n=4): C = 1024 per the API (layer.py:464-467)."""
+    T, dims, n = 8192, 4096, 4
+    torch.manual_seed(4)
+    inner = torch.nn.Linear(dims, dims, bias=False).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        inner.weight.normal_(0.0, 0.02)
+    m = MHCRewire(inner, dims=dims, n=n, eps=EPS, identity_init=False).cuda()
+    with torch.no_grad():
+        for prm in (m.mhc.H_pre_raw, m.mhc.H_post_raw, m.mhc.H_res_raw):
+            prm.normal_()
+    x = torch.randn(T, dims, device="cuda", dtype=torch.bfloat16).requires_grad_(True)
+    g = torch.randn(T, dims, device="cuda", dtype=torch.float32)
+    out = m(x)
+    gx, gw, gpre, gpost, gres = torch.autograd.grad(
+        out, [x, inner.weight, m.mhc.H_pre_raw, m.mhc.H_post_raw, m.mhc.H_res_raw], g)
+
+    # explicit fp32 formulation with the same bf16 GEMM
+    xr = x.detach().clone().requires_grad_(True)
+    hp = m.mhc.H_pre_raw.detach().clone().requires_grad_(True)
+    hq = m.mhc.H_post_raw.detach().clone().requires_grad_(True)
+    hr = m.mhc.H_res_raw.detach().clone()
+    a = torch.sigmoid(hp)
+    p = 2 * torch.sigmoid(hq)
+    x3 = xr.float().reshape(T, n, dims // n)
+    x_pre = (x3 * a[None, :, None]).to(torch.bfloat16).reshape(T, dims)
+    y = torch.nn.functional.linear(x_pre, inner.weight).float().reshape(T, n, dims // n)
+    M = torch.from_numpy(O.mixing_matrix_from_logits(hr.cpu().numpy(), iters=20, eps=EPS)).float().cuda()
+    Mf = M * a[None, :]
+    mixed = (Mf[None, :, :, None] * x3[:, None, :, :]).sum(2)
+    ref = ((y + mixed) * p[None, :, None]).reshape(T, dims)
+    assert out.dtype == torch.float32
+    assert rel_err(np_of(out), np_of(ref)) < 1e-2
+    rgx, rpre, rpost = torch.autograd.grad(ref, [xr, hp, hq], g)
+    assert rel_err(np_of(gx), np_of(rgx)) < 2e-2
+    assert rel_err(np_of(gpre), np_of(rpre)) < 1e-2
+    assert rel_err(np_of(gpost), np_of(rpost)) < 1e-2
+    assert torch.isfinite(gw).all() and torch.isfinite(gres).all()
