@@ -1,16 +1,22 @@
-"""Benchmark: fused mHC forward + backward on one MI355X.
+"""Benchmark of the fused mHC layer on one MI355X (BASELINE.json metric).
 
-Workload: MHCLayer(n=4, C=4096) on 32768 tokens (B=8 x T=4096 flattened),
-bf16 activations with bf16 output (return_dtype=bf16) and a bf16 upstream
+Headline (config 2): MHCLayer(n=4, C=4096) on 32768 tokens (B=8 x T=4096
+flattened), bf16 activations, bf16 output (return_dtype=bf16), bf16 upstream
 gradient; one step = forward + backward with gradients for x, H_pre_raw,
-H_post_raw, H_res_raw (through 20 Sinkhorn iterations) and rms_weight.
+H_post_raw, H_res_raw (through all 20 Sinkhorn iterations) and rms_weight.
 Synthetic seeded data; random parameters drawn as in the BASELINE recipe.
 
-Prints one JSON line (rank 0): tokens/s over the timed steps, the HBM
-roofline of the dominant kernel (fused backward) from HIP events recorded
-around its launches during the timed steps, the forward latency at B=32 and
-B=1, and the CPU baseline (the numpy oracle, fp32, one thread, on a bounded
-token sample of the same workload).
+Timed regions (all on the stream the library launches on):
+  1. K eager steps, no instrumentation          -> value, ms_per_step
+  2. K steps with per-kernel HIP events          -> roofline of the dominant
+     kernel (the backward partial-sums pass) and of the forward kernel
+Extras: forward latency at B=32, C=2048 (config 1) and B=1, C=4096 (eager
+calls); config 3 (per-token H, n=16) fwd+bwd; config 4
+(MHCRewire around Linear(4096, 4096)) with mHC kernel time reported apart
+from the GEMM.  cpu_baseline: the numpy oracle in fp32 on one core over a
+bounded token sample of config 2.
+
+Prints one JSON line.
 """
 
 from __future__ import annotations
@@ -30,22 +36,24 @@ for _p in (ROOT, ROOT / "mhc-mlx_amd"):
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "mHC fwd+bwd tokens/s & % HBM peak (n=4,C=4096,bf16); B=1 fwd latency µs"
+EPS = 1e-6
 
 
-def _params(g, n, C):
+def _params(g, n, C, per_token=None):
     import numpy as np
 
-    return (g.standard_normal(n).astype(np.float32), g.standard_normal(n).astype(np.float32),
-            g.standard_normal((n, n)).astype(np.float32), (1 + 0.02 * g.standard_normal(C)).astype(np.float32))
+    shp = (n,) if per_token is None else (per_token, n)
+    return (g.standard_normal(shp).astype(np.float32), g.standard_normal(shp).astype(np.float32),
+            g.standard_normal(shp + (n,)).astype(np.float32), (1 + 0.02 * g.standard_normal(C)).astype(np.float32))
 
 
-def _layer(n, C, dev, g, eps):
+def _layer(n, C, dev, g):
     import torch
 
     from mhc_mlx_amd import MHCLayer
 
     hpre, hpost, hres, w = _params(g, n, C)
-    layer = MHCLayer(n=n, C=C, sinkhorn_iters=20, eps=eps).to(dev)
+    layer = MHCLayer(n=n, C=C, sinkhorn_iters=20, eps=EPS).to(dev)
     with torch.no_grad():
         layer.H_pre_raw.copy_(torch.from_numpy(hpre))
         layer.H_post_raw.copy_(torch.from_numpy(hpost))
@@ -54,30 +62,123 @@ def _layer(n, C, dev, g, eps):
     return layer
 
 
-def _fwd_latency_us(n, C, B, dev, reps=200):
-    import numpy as np
+def _time_loop(fn, steps):
+    """Mean ms per call of `fn` over `steps` calls, bracketed by synchronize + events."""
     import torch
 
-    g = np.random.default_rng(1)
-    layer = _layer(n, C, dev, g, 1e-6)
-    x = torch.randn(B, n, C, device=dev, dtype=torch.bfloat16)
-    with torch.no_grad():
-        for _ in range(20):
-            layer(x, return_dtype=torch.bfloat16)
-        torch.cuda.synchronize()
-        ts = []
-        for _ in range(reps):
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            layer(x, return_dtype=torch.bfloat16)
-            e.record()
-            e.synchronize()
-            ts.append(s.elapsed_time(e) * 1e3)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def _median_us(fn, reps):
+    import torch
+
+    ts = []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        ts.append(s.elapsed_time(e) * 1e3)
     return statistics.median(ts)
 
 
+def _fwd_latency(n, C, B, dev, reps=200):
+    """Forward latency (µs, median of eager calls, each bracketed by events)."""
+    import numpy as np
+    import torch
+
+    layer = _layer(n, C, dev, np.random.default_rng(1))
+    x = torch.randn(B, n, C, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        fwd = lambda: layer(x, return_dtype=torch.bfloat16)  # noqa: E731
+        for _ in range(20):
+            fwd()
+        eager = _median_us(fwd, reps)
+    return {"eager_us": round(eager, 2), "kernel_launches": 2}
+
+
+def _config3(dev, steps, warmup):
+    """Per-token mappings: 16384 tokens, n=16, C=1024, bf16, fwd+bwd."""
+    import numpy as np
+    import torch
+
+    from mhc_mlx_amd import MHCLayer, kernel_timer
+
+    T, n, C = 16384, 16, 1024
+    hpre, hpost, hres, w = _params(np.random.default_rng(3), n, C, per_token=T)
+    layer = MHCLayer(n=n, C=C, sinkhorn_iters=20, eps=EPS).to(dev)
+    with torch.no_grad():
+        layer.rms_weight.copy_(torch.from_numpy(w))
+    gen = torch.Generator(dev).manual_seed(3)
+    x = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen).requires_grad_(True)
+    dout = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen)
+    ps = [torch.from_numpy(v).to(dev).requires_grad_(True) for v in (hpre, hpost, hres)]
+
+    def step():
+        out = layer.forward_dynamic(x, *ps, return_dtype=torch.bfloat16)
+        return torch.autograd.grad(out, [x] + ps + [layer.rms_weight], dout)
+
+    for _ in range(warmup):
+        step()
+    ms = _time_loop(step, steps)
+    with kernel_timer() as kt:
+        _time_loop(step, steps)
+        st = kt.stats()
+    e = T * n * C * 2
+    fwd_bytes = 2 * e + T * (n * n + 2 * n) * 4
+    bwd_bytes = 3 * e + T * (n * n + 2 * n) * 4 * 2
+    kern = {k: round(v["mean_ms"] * 1e3, 1) for k, v in st.items()}
+    return {"workload": "config 3: per-token H, 16384 tokens, n=16, C=1024, bf16, fwd+bwd",
+            "tokens_per_s": T / (ms / 1e3), "ms_per_step": ms,
+            "step_hbm_frac": (fwd_bytes + bwd_bytes) / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+            "kernels_us": kern,
+            "fused_bwd_hbm_frac": bwd_bytes / (st["fused_bwd"]["mean_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS,
+            "fused_fwd_hbm_frac": fwd_bytes / (st["fused_fwd"]["mean_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS}
+
+
+def _config4(dev, steps, warmup):
+    """MHCRewire(Linear(4096, 4096, bias=False)), n=4 (C = 1024 per the API), 8192 tokens, bf16, fwd+bwd."""
+    import torch
+
+    from mhc_mlx_amd import MHCRewire, kernel_timer
+
+    T, dims, n = 8192, 4096, 4
+    torch.manual_seed(4)
+    inner = torch.nn.Linear(dims, dims, bias=False).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        inner.weight.normal_(0.0, 0.02)
+    m = MHCRewire(inner, dims=dims, n=n, eps=EPS, identity_init=False).to(dev)
+    x = torch.randn(T, dims, device=dev, dtype=torch.bfloat16).requires_grad_(True)
+    g = torch.randn(T, dims, device=dev, dtype=torch.float32)
+    prm = [x, inner.weight, m.mhc.H_pre_raw, m.mhc.H_post_raw, m.mhc.H_res_raw]
+
+    def step():
+        return torch.autograd.grad(m(x), prm, g)
+
+    for _ in range(warmup):
+        step()
+    ms = _time_loop(step, steps)
+    with kernel_timer() as kt:
+        ms_t = _time_loop(step, steps)
+        st = kt.stats()
+    mhc_ms = sum(v["mean_ms"] for v in st.values())
+    return {"workload": "config 4: MHCRewire(Linear(4096,4096)), n=4, C=1024, 8192 tokens, bf16, fwd+bwd",
+            "ms_per_step": ms, "tokens_per_s": T / (ms / 1e3),
+            "mhc_kernels_us": {k: round(v["mean_ms"] * 1e3, 1) for k, v in st.items()},
+            "mhc_kernels_ms_per_step": mhc_ms,
+            "gemm_and_other_ms_per_step": ms_t - mhc_ms}
+
+
 def _cpu_baseline(n, C, budget_s=12.0, chunk=64):
-    """Oracle (numpy fp32 restatement of reference.py + its VJP) on token chunks."""
+    """Oracle (numpy fp32 restatement of reference.py + its VJP) on token chunks, one core."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
@@ -91,8 +192,8 @@ def _cpu_baseline(n, C, budget_s=12.0, chunk=64):
     t0 = time.perf_counter()
     with threadpool_limits(limits=1):
         while time.perf_counter() - t0 < budget_s:
-            O.mhc_forward_reference(x, hpre, hpost, hres, w, 20, 1e-6, dtype=np.float32)
-            O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, 20, 1e-6, dtype=np.float32)
+            O.mhc_forward_reference(x, hpre, hpost, hres, w, 20, EPS, dtype=np.float32)
+            O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, 20, EPS, dtype=np.float32)
             done += chunk
     dt = time.perf_counter() - t0
     return {"value": done / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
@@ -101,7 +202,7 @@ def _cpu_baseline(n, C, budget_s=12.0, chunk=64):
 
 
 def _traffic():
-    """HBM bytes per fused-backward launch from the committed rocprofv3 --pmc summary (None if absent)."""
+    """HBM bytes per backward partial-sums launch from the committed rocprofv3 --pmc summary."""
     p = ROOT / "profiles" / "cfg2_fused_bwd_traffic.md"
     if not p.exists():
         return None
@@ -138,6 +239,7 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-latency", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 3 and 4")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain fp32 copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -157,8 +259,7 @@ def main() -> int:
     _lib.load()
     dev = torch.device("cuda:0")
     T, n, C = args.tokens, 4, 4096
-    g = np.random.default_rng(0)
-    layer = _layer(n, C, dev, g, 1e-6)
+    layer = _layer(n, C, dev, np.random.default_rng(0))
     x = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=torch.Generator(dev).manual_seed(0))
     dout = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=torch.Generator(dev).manual_seed(1))
     x.requires_grad_(True)
@@ -170,27 +271,20 @@ def main() -> int:
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
+    # 1. the timed steps (eager, uninstrumented)
+    ms_step = _time_loop(step, args.steps)
+    tokens_per_s = T / (ms_step / 1e3)
+    # 2. the same steps with per-kernel HIP events on the launch stream
     with kernel_timer() as kt:
-        t_start = torch.cuda.Event(enable_timing=True)
-        t_end = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t_start.record()
-        for _ in range(args.steps):
-            step()
-        t_end.record()
-        torch.cuda.synchronize()
+        _time_loop(step, args.steps)
         stats = kt.stats()
-    ms_total = t_start.elapsed_time(t_end)
-    ms_step = ms_total / args.steps
-    tokens_per_s = T * args.steps / (ms_total / 1e3)
 
     elems = T * n * C
     bytes_fwd = 2 * elems * 2          # read x, write out (bf16)
     bytes_bwd = 3 * elems * 2          # read x, read dout, write dx (bf16)
     bwd_ms = stats["fused_bwd"]["mean_ms"]
-    achieved = bytes_bwd / (bwd_ms / 1e3) / 1e9
     fwd_ms = stats["fused_fwd"]["mean_ms"]
+    achieved = bytes_bwd / (bwd_ms / 1e3) / 1e9
 
     result = {
         "metric": METRIC,
@@ -205,20 +299,26 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "mHC fwd+bwd, config 2", "tokens": T, "n": n, "C": C,
-                   "io_dtype": "bf16", "sinkhorn_iters": 20, "eps": 1e-6, "parallelism": "none (1 GPU)"},
+        "config": {"workload": "config 2: MHCLayer fwd+bwd, 32768 tokens (B=8 x T=4096), n=4, C=4096, bf16 I/O",
+                   "tokens": T, "n": n, "C": C, "sinkhorn_iters": 20, "eps": EPS, "parallelism": "none (1 GPU)"},
         "step_hbm_frac": (bytes_fwd + bytes_bwd) / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic(),
-                     "kernel": "fused_bwd_kernel", "algorithmic_bytes_per_launch": bytes_bwd},
-        "kernels_ms": {k: round(v["mean_ms"], 4) for k, v in stats.items()},
+                     "kernel": "fused_bwd_lw_kernel (backward partial-sums pass)",
+                     "algorithmic_bytes_per_launch": bytes_bwd},
+        "kernels_us": {k: round(v["mean_ms"] * 1e3, 1) for k, v in stats.items()},
         "fused_fwd_hbm_frac": bytes_fwd / (fwd_ms / 1e3) / 1e9 / HBM_PEAK_GBS,
     }
     del x, dout
     torch.cuda.empty_cache()
     if not args.no_latency:
-        result["fwd_latency_us_B32_C2048"] = _fwd_latency_us(4, 2048, 32, dev)
-        result["fwd_latency_us_B1_C4096"] = _fwd_latency_us(4, 4096, 1, dev)
+        result["fwd_latency"] = {"config1_B32_C2048": _fwd_latency(4, 2048, 32, dev),
+                                 "B1_C4096": _fwd_latency(4, 4096, 1, dev)}
+    if not args.no_extra:
+        result["config3"] = _config3(dev, 10, 3)
+        torch.cuda.empty_cache()
+        result["config4"] = _config4(dev, 10, 3)
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(n, C)
     print(json.dumps(result), flush=True)
