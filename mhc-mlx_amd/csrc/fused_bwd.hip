@@ -769,6 +769,225 @@ void fused_bwd_lw_kernel(BwdArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// Per-token parameters, n == 16, 16-bit x and dout, C <= 1024 (config 3).
+//
+// Per token the parameter gradients are n^2 + 2n = 288 sums over C
+// channels; the n x n block dM = G X^T is a GEMM with K = C and runs on
+// MFMA (v_mfma_f32_16x16x16 bf16/fp16: exact 16-bit products, fp32
+// accumulation).  Thread `tid` owns channels [4 tid, 4 tid + 4) of every
+// stream (8-byte coalesced loads).  Each wave copies its 256-channel slice of
+// x and g into LDS rows (one row per stream, padded by 16 bytes) and
+// accumulates dM over that slice with 16 MFMA steps; the four slices are
+// added in wave order after a second barrier.  dx, dy and the dw
+// accumulation stay on the VALU with M read as LDS broadcasts; dA and dP are
+// reduce-scattered across each wave.  Parameters of the next token are
+// staged in a three-slot LDS ring while the current one is processed.
+// ---------------------------------------------------------------------------
+
+template <typename T>
+MHC_DEV f32x4 mfma16(uint2 a, uint2 b, f32x4 c);
+template <>
+MHC_DEV f32x4 mfma16<__bf16>(uint2 a, uint2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                   0, 0, 0);
+}
+template <>
+MHC_DEV f32x4 mfma16<_Float16>(uint2 a, uint2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
+                                               0, 0);
+}
+
+constexpr int kPt16Row = 256 + 8;  // 16-bit elements per LDS row: 256 channels + 16-byte pad
+constexpr int kPt16K = 16 * 16 + 2 * 16;
+
+template <typename XT>
+MHC_DEV void pt16_stage(float* buf, const BwdArgs& A, int64_t t) {
+  // buf: M^T [16][16] (buf[j*16 + i] = M[i][j]), a [16], p [16]
+  const float* M = A.M + t * 256;
+  for (int k = threadIdx.x; k < kPt16K; k += blockDim.x) {
+    if (k < 256) {
+      buf[(k & 15) * 16 + (k >> 4)] = M[k];
+    } else if (k < 272) {
+      const float h = A.hpre[t * 16 + (k - 256)];
+      buf[k] = A.h_mode == MHC_H_RAW ? sigmoidf_(h) : h;
+    } else {
+      const float h = A.hpost[t * 16 + (k - 272)];
+      buf[k] = A.h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(h) : h;
+    }
+  }
+}
+
+template <typename XT>
+__global__ __launch_bounds__(256) void fused_bwd_pt16_kernel(BwdArgs A) {
+  constexpr int N = 16, V = 4;
+  __shared__ uint16_t s_x[4][N][kPt16Row];
+  __shared__ uint16_t s_g[4][N][kPt16Row];
+  __shared__ float s_par[3][kPt16K];
+  // written after the first barrier of a token and read before the first
+  // barrier of the next one: one buffer suffices
+  __shared__ float s_part[4][256];
+  __shared__ float s_rows[4][4][32];
+  __shared__ float s_red[2][2][4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int C = A.C;
+  const int c0 = tid * V;
+  const int64_t nC = (int64_t)N * C;
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+
+  float wv[V], dwv[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    wv[v] = A.w[c0 + v];
+    dwv[v] = 0.0f;
+  }
+  if ((int64_t)blockIdx.x < A.T) pt16_stage<XT>(s_par[0], A, blockIdx.x);
+  __syncthreads();
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const float* par = s_par[it % 3];
+    const int64_t tn = t + gridDim.x;
+    if (tn < A.T) pt16_stage<XT>(s_par[(it + 1) % 3], A, tn);
+    const uint2* xt = reinterpret_cast<const uint2*>((const XT*)A.x + t * nC + c0);
+    const uint2* gt = reinterpret_cast<const uint2*>((const XT*)A.g + t * nC + c0);
+    uint2 xr[N], gr[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(xt + (int64_t)i * (C / V)));
+      const u32x2 q = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(gt + (int64_t)i * (C / V)));
+      xr[i] = make_uint2(u.x, u.y);
+      gr[i] = make_uint2(q.x, q.y);
+    }
+    // this wave's slice of x and g, row = stream, for the MFMA below
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      *reinterpret_cast<uint2*>(&s_x[wave][i][lane * V]) = xr[i];
+      *reinterpret_cast<uint2*>(&s_g[wave][i][lane * V]) = gr[i];
+    }
+    // y, dyn and the two per-token sums
+    float y[V], dyn[V];
+    float ss = 0.0f, sr = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float ya = 0.0f, da = 0.0f;
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const uint32_t wx = (v & 2) ? xr[i].y : xr[i].x;
+        const uint32_t wg = (v & 2) ? gr[i].y : gr[i].x;
+        ya = fmaf(par[256 + i], (v & 1) ? hi16<XT>(wx) : lo16<XT>(wx), ya);
+        da = fmaf(par[272 + i], (v & 1) ? hi16<XT>(wg) : lo16<XT>(wg), da);
+      }
+      y[v] = ya;
+      dyn[v] = da;
+      ss = fmaf(ya, ya, ss);
+      sr = fmaf(da * ya, wv[v], sr);
+    }
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    __syncthreads();
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+    float dy[V], yn[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const float yi = y[v] * inv;
+      dy[v] = dyn[v] * inv * wv[v] - kf * y[v];
+      yn[v] = yi * wv[v];
+      dwv[v] = fmaf(dyn[v], yi, dwv[v]);
+    }
+    // dx_j = sum_i M_ij g_i + a_j dy  (M^T rows are LDS broadcasts)
+    XT* dxt = (XT*)A.dx + t * nC + c0;
+#pragma unroll 4
+    for (int j = 0; j < N; ++j) {
+      const float aj = par[256 + j];
+      float o[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) o[v] = aj * dy[v];
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const float m = par[j * 16 + i];
+        o[0] = fmaf(m, lo16<XT>(gr[i].x), o[0]);
+        o[1] = fmaf(m, hi16<XT>(gr[i].x), o[1]);
+        o[2] = fmaf(m, lo16<XT>(gr[i].y), o[2]);
+        o[3] = fmaf(m, hi16<XT>(gr[i].y), o[3]);
+      }
+      st_nt(reinterpret_cast<uint32_t*>(dxt + (int64_t)j * C), pack2<XT>(o[0], o[1]), pack2<XT>(o[2], o[3]));
+    }
+    // dA_j = sum dy x_j, dP_i = sum g_i yn: lane partials summed across each
+    // 16-lane row (DPP), then one value per lane goes to LDS; the four rows
+    // and four waves are added after the barrier
+    {
+      float oa = 0.0f, op = 0.0f;
+      const int r = lane & 15;
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        float sa = 0.0f, sp = 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const uint32_t wx = (v & 2) ? xr[i].y : xr[i].x;
+          const uint32_t wg = (v & 2) ? gr[i].y : gr[i].x;
+          sa = fmaf(dy[v], (v & 1) ? hi16<XT>(wx) : lo16<XT>(wx), sa);
+          sp = fmaf((v & 1) ? hi16<XT>(wg) : lo16<XT>(wg), yn[v], sp);
+        }
+        sa = group_sum<16>(sa);
+        sp = group_sum<16>(sp);
+        oa = r == i ? sa : oa;
+        op = r == i ? sp : op;
+      }
+      s_rows[wave][lane >> 4][r] = oa;
+      s_rows[wave][lane >> 4][16 + r] = op;
+    }
+    // dM over this wave's 256 channels on MFMA: A = G (rows i), B = X^T
+    {
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      const int r = lane & 15;
+      const int kq = 4 * (lane >> 4);
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) {
+        const uint2 a = *reinterpret_cast<const uint2*>(&s_g[wave][r][ks * 16 + kq]);
+        const uint2 b = *reinterpret_cast<const uint2*>(&s_x[wave][r][ks * 16 + kq]);
+        acc = mfma16<XT>(a, b, acc);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) s_part[wave][(kq + v) * 16 + r] = acc[v];
+    }
+    __syncthreads();
+    for (int k = tid; k < kPt16K; k += blockDim.x) {
+      float s = 0.0f;
+      if (k < 256) {
+        for (int w = 0; w < nwaves; ++w) s += s_part[w][k];
+      } else {
+        for (int w = 0; w < nwaves; ++w)
+          s += (s_rows[w][0][k - 256] + s_rows[w][1][k - 256]) + (s_rows[w][2][k - 256] + s_rows[w][3][k - 256]);
+      }
+      if (k < 256) {
+        A.dM_tok[t * 256 + k] = s;
+      } else if (k < 272) {
+        const float av = par[k];
+        A.dpre_tok[t * 16 + (k - 256)] = A.h_mode == MHC_H_RAW ? s * av * (1.0f - av) : s;
+      } else {
+        const float pq = par[k];
+        A.dpost_tok[t * 16 + (k - 272)] = A.h_mode == MHC_H_RAW ? s * pq * (1.0f - 0.5f * pq) : s;
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) prow[c0 + v] = dwv[v];
+}
+
+// ---------------------------------------------------------------------------
 // Stage 2: fixed-order column sums of the G partial rows, two launches.
 //
 // reduce_rows_kernel (mhc_reduce.hpp) folds the G rows into S <= kReduceSplit
@@ -961,8 +1180,31 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
   return MHC_OK;
 }
 
+// Per-token n == 16 with 16-bit x == dout and C a multiple of 256 up to 1024
+// (fused_bwd_pt16_kernel).  Returns 1 when the shape is not covered.
+template <typename XT>
+int launch_bwd_pt16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  if (A.n != 16 || A.C % 256 != 0 || A.C > 1024) return 1;
+  if (!aligned(A.x, 8) || !aligned(A.g, 8) || !aligned(A.dx, 8)) return 1;
+  const int tpb = A.C / 4;
+  const void* kfn = (const void*)fused_bwd_pt16_kernel<XT>;
+  const int occ = occupancy_blocks(kfn, tpb, 0);
+  if (occ <= 0) return 1;
+  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+  set_rows(A, L);
+  hipLaunchKernelGGL((fused_bwd_pt16_kernel<XT>), dim3((unsigned)blocks), dim3(tpb), 0, stream, A);
+  MHC_CHECK_LAUNCH("fused_bwd_pt16_kernel");
+  *num_partials = blocks;
+  return MHC_OK;
+}
+
 template <int NMAX, typename XT, typename GT, bool PT>
 int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  if constexpr (PT && NMAX == 16 && std::is_same<XT, GT>::value && ElemTraits<XT>::kBytes == 2) {
+    const int rc = launch_bwd_pt16<XT>(A, L, num_partials, stream);
+    if (rc != 1) return rc;
+  }
   if constexpr (!PT && NMAX <= 8) {
     static const int legacy = env_int("MHC_BWD_LEGACY", 0);
     if (!legacy) {

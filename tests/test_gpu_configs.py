@@ -274,3 +274,24 @@ def test_config4_rewire_linear_full_size():
     assert rel_err(np_of(gpre), np_of(rpre)) < 1e-2
     assert rel_err(np_of(gpost), np_of(rpost)) < 1e-2
     assert torch.isfinite(gw).all() and torch.isfinite(gres).all()
+
+
+@pytest.mark.parametrize("T,C,dt", [(300, 1024, "bf16"), (40, 256, "bf16"), (70, 512, "f16"), (3, 1024, "bf16")])
+def test_per_token_n16_mfma_path(T, C, dt):
+    """Per-token n=16 with C a multiple of 256 (the MFMA parameter-gradient kernel), all gradients."""
+    n = 16
+    g = rng(7000 + T + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T)
+    ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+    xt = dev_tensor(x, dt).requires_grad_(True)
+    out = ops.mhc_layer_forward_dynamic(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+    tol = {"bf16": 2e-2, "f16": 5e-3}[dt]
+    assert rel_err(np_of(out), O.mhc_forward_reference(x, hpre, hpost, hres, w, 20, EPS)) < tol
+    out.backward(dev_tensor(dout, dt))
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    gots = [xt.grad] + [p.grad for p in ps]
+    for name, got, r in zip(["dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], gots, refs):
+        t = tol if name == "dx" else 1e-4
+        assert rel_err(np_of(got), r) < t, (name, rel_err(np_of(got), r))
