@@ -290,7 +290,7 @@ __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
 // wave-uniform scalars.  The grid-stride loop only matters for T > kMaxGrid.
 // ---------------------------------------------------------------------------
 
-template <int NMAX, typename XT, typename OT, int CH>
+template <int NMAX, typename XT, typename OT, int CH, bool RAW>
 __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
   constexpr int V = FwdCfg<NMAX>::V;
   __shared__ float s_red[2][16];
@@ -300,31 +300,13 @@ __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
   const int nwaves = blockDim.x >> 6;
   const int C = A.C;
   const int64_t nC = (int64_t)NMAX * C;
-
-  float Ms[NMAX * NMAX], as[NMAX], ps[NMAX];
-#pragma unroll
-  for (int i = 0; i < NMAX; ++i) {
-    float av = A.hpre[i], pv = A.hpost[i];
-    if (A.h_mode == MHC_H_RAW) {
-      av = sigmoidf_(av);
-      pv = 2.0f * sigmoidf_(pv);
-    }
-    as[i] = uniform_f(av);
-    ps[i] = uniform_f(pv);
-#pragma unroll
-    for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = uniform_f(A.M[i * NMAX + j]);
-  }
   int c0[CH];
-  float wv[CH][V];
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    c0[k] = (tid + k * (int)blockDim.x) * V;
-#pragma unroll
-    for (int v = 0; v < V; ++v) wv[k][v] = A.w[c0[k] + v];
-  }
+  for (int k = 0; k < CH; ++k) c0[k] = (tid + k * (int)blockDim.x) * V;
 
   int it = 0;
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    // the token's loads go out first; parameters and w are read while they fly
     const XT* xt = (const XT*)A.x + t * nC;
     OT* ot = (OT*)A.out + t * nC;
     Vec<XT, V> xr[CH][NMAX];
@@ -332,6 +314,25 @@ __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
     for (int k = 0; k < CH; ++k)
 #pragma unroll
       for (int i = 0; i < NMAX; ++i) xr[k][i].load(xt + i * C + c0[k]);
+    float Ms[NMAX * NMAX], as[NMAX], ps[NMAX];
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      float av = A.hpre[i], pv = A.hpost[i];
+      if constexpr (RAW) {
+        av = sigmoidf_(av);
+        pv = 2.0f * sigmoidf_(pv);
+      }
+      as[i] = uniform_f(av);
+      ps[i] = uniform_f(pv);
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = uniform_f(A.M[i * NMAX + j]);
+    }
+    float wv[CH][V];
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+#pragma unroll
+      for (int v = 0; v < V; ++v) wv[k][v] = A.w[c0[k] + v];
+
     float y[CH][V];
     float ss = 0.0f;
 #pragma unroll
@@ -394,10 +395,14 @@ int launch_fwd_full(FwdArgs A, hipStream_t stream) {
   const int tpb = nchunks / ch;
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, kMaxGrid));
   const dim3 g((unsigned)blocks), b(tpb);
-  if (ch == 2)
-    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 2>), g, b, 0, stream, A);
-  else
-    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1>), g, b, 0, stream, A);
+  const bool raw = A.h_mode == MHC_H_RAW;
+  if (ch == 2) {
+    if (raw) hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 2, true>), g, b, 0, stream, A);
+    else hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 2, false>), g, b, 0, stream, A);
+  } else {
+    if (raw) hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1, true>), g, b, 0, stream, A);
+    else hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1, false>), g, b, 0, stream, A);
+  }
   MHC_CHECK_LAUNCH("fused_fwd_full_kernel");
   return MHC_OK;
 }
