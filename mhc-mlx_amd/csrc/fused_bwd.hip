@@ -656,7 +656,7 @@ void fused_bwd_lw_kernel(BwdArgs A) {
       s_red[it & 1][0][wave] = ss;
       s_red[it & 1][1][wave] = sr;
     }
-    __syncthreads();
+    lds_barrier();
     float tss = 0.0f, tsr = 0.0f;
     for (int w = 0; w < nwaves; ++w) {
       tss += s_red[it & 1][0][w];

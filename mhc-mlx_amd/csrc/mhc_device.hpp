@@ -276,6 +276,26 @@ MHC_DEV void wave_reduce_scatter(float (&v)[64 * R], int lane) {
 }
 
 // --------------------------------------------------------------------------
+// synchronisation
+// --------------------------------------------------------------------------
+
+// s_waitcnt immediate for lgkmcnt(0) alone (gfx9 encoding: vmcnt[3:0] |
+// expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]; vmcnt and expcnt left
+// at their maximum).
+constexpr int kWaitLgkm0 = 0xC07F;
+
+// Workgroup barrier for data exchanged through LDS only.  __syncthreads()
+// is a workgroup-scope release/acquire fence and waits for every
+// outstanding global access as well (for instance the previous token's
+// output stores); here only LDS traffic has to be complete.
+MHC_DEV void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// --------------------------------------------------------------------------
 // math
 // --------------------------------------------------------------------------
 
