@@ -13,7 +13,7 @@ Timed regions (all on the stream the library launches on):
 Extras: forward latency at B=32, C=2048 (config 1) and B=1, C=4096 (eager
 calls); config 3 (per-token H, n=16) fwd+bwd; config 4
 (MHCRewire around Linear(4096, 4096)) with mHC kernel time reported apart
-from the GEMM.  cpu_baseline: the numpy oracle in fp32 on one core over a
+from the GEMM; residual_add_agg at config 2's shape.  cpu_baseline: the numpy oracle in fp32 on one core over a
 bounded token sample of config 2.
 
 Prints one JSON line.
@@ -177,6 +177,30 @@ def _config4(dev, steps, warmup):
             "gemm_and_other_ms_per_step": ms_t - mhc_ms}
 
 
+def _residual(dev, steps, warmup):
+    """residual_add_agg (utils.py:4-24) at config 2's shape: x, res [32768, 4, 4096] bf16 -> out bf16, y_agg fp32."""
+    import torch
+
+    from mhc_mlx_amd import kernel_timer, ops
+
+    T, n, C = 32768, 4, 4096
+    gen = torch.Generator(dev).manual_seed(5)
+    x = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen)
+    res = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen)
+    h = torch.rand(n, device=dev, generator=gen)
+    fwd = lambda: ops.residual_add_agg_hip(x, res, h, output_dtype=torch.bfloat16)  # noqa: E731
+    with torch.no_grad():
+        for _ in range(warmup):
+            fwd()
+        with kernel_timer() as kt:
+            _time_loop(fwd, steps)
+            st = kt.stats()["residual_add_agg"]
+    nbytes = 3 * T * n * C * 2 + T * C * 4
+    return {"workload": "residual_add_agg, 32768 tokens, n=4, C=4096, bf16 in/out, y_agg fp32",
+            "us_per_call": st["mean_ms"] * 1e3, "algorithmic_bytes": nbytes,
+            "hbm_frac": nbytes / (st["mean_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS}
+
+
 def _cpu_baseline(n, C, budget_s=12.0, chunk=64):
     """Oracle (numpy fp32 restatement of reference.py + its VJP) on token chunks, one core."""
     import numpy as np
@@ -318,6 +342,8 @@ def main() -> int:
         result["config3"] = _config3(dev, 10, 3)
         torch.cuda.empty_cache()
         result["config4"] = _config4(dev, 10, 3)
+        torch.cuda.empty_cache()
+        result["residual_add_agg"] = _residual(dev, 10, 3)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(n, C)

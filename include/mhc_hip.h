@@ -218,6 +218,34 @@ int mhc_stream_scale_bwd(const void* x, int x_dtype, const void* dout, int dout_
                          int dx_dtype, float* dh_pre, void* workspace, size_t workspace_bytes,
                          int64_t T, int n, int C, void* stream);
 
+/* --------------------------------------------------------------------- */
+/* Residual add + stream aggregate                                         */
+/* --------------------------------------------------------------------- */
+
+/* out[t,i,c] = x[t,i,c] + res[t,i,c];  y_agg[t,c] = sum_i a_i (x + res)[t,i,c]
+ * with the sum taken in fp32 before out is rounded to out_dtype.
+ * x and res share `dtype`; y_agg is [T, C] fp32.  h_mode MHC_H_ACTIVATED
+ * (a = h_pre, as the reference passes it) or MHC_H_RAW (a = sigmoid(h_pre)).
+ * Replaces residual_add_agg_metal (metal.py:1673-1731; kernel
+ * residual_add_agg.metal:39-66) behind residual_add_agg (utils.py:4-24). */
+int mhc_residual_add_agg_fwd(const void* x, const void* res, int dtype, const float* h_pre,
+                             int h_mode, void* out, int out_dtype, float* y_agg, int64_t T, int n,
+                             int C, void* stream);
+
+size_t mhc_residual_add_agg_bwd_workspace_bytes(int64_t T, int n, int C);
+
+/* VJP of mhc_residual_add_agg_fwd for cotangents dout ([T,n,C], fp32 or
+ * `dtype`; NULL = 0) and dy_agg ([T,C] fp32; NULL = 0):
+ *   dx = dres = dout_i + a_i dy_agg     (each written if not NULL, in `dtype`)
+ *   dh_pre_i = sum_{t,c} dy_agg (x + res)_i  (chained through the sigmoid for
+ *   MHC_H_RAW; skipped if dh_pre is NULL, which needs no workspace).
+ * The reference kernel has no VJP (an mx.fast.metal_kernel without a
+ * custom_function); this is the gradient of the math it computes. */
+int mhc_residual_add_agg_bwd(const void* x, const void* res, int dtype, const void* dout,
+                             int dout_dtype, const float* dy_agg, const float* h_pre, int h_mode,
+                             void* dx, void* dres, float* dh_pre, void* workspace,
+                             size_t workspace_bytes, int64_t T, int n, int C, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,6 +12,7 @@ from .ops import (
     mhc_layer_forward,
     mhc_layer_forward_dynamic,
     post_combine,
+    residual_add_agg_hip,
     sinkhorn_knopp_hip,
     sinkhorn_knopp_hip_autograd,
     stream_mix_add_hip,
@@ -19,6 +20,7 @@ from .ops import (
     stream_scale,
 )
 from .profiling import kernel_timer
+from .utils import residual_add_agg
 
 __version__ = "0.1.0"
 
@@ -33,6 +35,8 @@ __all__ = [
     "mhc_layer_forward",
     "mhc_layer_forward_dynamic",
     "post_combine",
+    "residual_add_agg",
+    "residual_add_agg_hip",
     "sinkhorn_knopp_hip",
     "sinkhorn_knopp_hip_autograd",
     "stream_mix_add_hip",

@@ -62,6 +62,10 @@ SIGNATURES = {
     "mhc_stream_scale_bwd_workspace_bytes": ([_I64, _I32, _I32], _SZ),
     "mhc_stream_scale_bwd": ([_VP, _I32, _VP, _I32, _VP, _I32, _VP, _VP, _I32, _VP, _VP, _SZ, _I64,
                               _I32, _I32, _VP], _I32),
+    "mhc_residual_add_agg_fwd": ([_VP, _VP, _I32, _VP, _I32, _VP, _I32, _VP, _I64, _I32, _I32, _VP], _I32),
+    "mhc_residual_add_agg_bwd_workspace_bytes": ([_I64, _I32, _I32], _SZ),
+    "mhc_residual_add_agg_bwd": ([_VP, _VP, _I32, _VP, _I32, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _SZ, _I64,
+                                  _I32, _I32, _VP], _I32),
 }
 
 _lock = threading.Lock()

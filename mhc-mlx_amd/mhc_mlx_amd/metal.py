@@ -7,6 +7,7 @@ each one is the corresponding ``mhc_mlx_amd.ops`` function.
 from .ops import (  # noqa: F401
     mhc_forward_fused_hip as mhc_forward_fused_metal,
     mhc_forward_fused_hip_autograd as mhc_forward_fused_metal_autograd,
+    residual_add_agg_hip as residual_add_agg_metal,
     sinkhorn_knopp_hip as sinkhorn_knopp_metal,
     sinkhorn_knopp_hip_autograd as sinkhorn_knopp_metal_autograd,
     stream_mix_add_hip as stream_mix_add_metal,
@@ -17,6 +18,7 @@ from .ops import (  # noqa: F401
 __all__ = [
     "mhc_forward_fused_metal",
     "mhc_forward_fused_metal_autograd",
+    "residual_add_agg_metal",
     "sinkhorn_knopp_metal",
     "sinkhorn_knopp_metal_autograd",
     "stream_mix_add_metal",

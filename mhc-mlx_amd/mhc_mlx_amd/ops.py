@@ -16,6 +16,9 @@ projection and its VJP inside the library): ``mhc_layer_forward``,
 ``mhc_layer_forward_dynamic`` (per-token parameters), ``post_combine`` and
 ``stream_scale`` (MHCRewire, layer.py:302-337, 469-492).
 
+Block helper: ``residual_add_agg_hip`` (metal.py:1673-1731, utils.py:4-24),
+differentiable here although the reference's kernel is not.
+
 All work is enqueued on torch's current stream of the input's device.  Every
 op requires GPU tensors and the built library; there is no silent fallback.
 """
@@ -40,6 +43,7 @@ __all__ = [
     "mhc_layer_forward_dynamic",
     "post_combine",
     "stream_scale",
+    "residual_add_agg_hip",
     "suggest_threads_per_group",
 ]
 
@@ -619,3 +623,95 @@ def stream_scale(x, H_pre_raw):
     _validate_n(int(x.shape[1]))
     _require_gpu(x, H_pre_raw)
     return StreamScaleFn.apply(x, H_pre_raw)
+
+
+# --------------------------------------------------------------------------
+# residual add + aggregate (utils.py:4-24, metal.py:1673-1731)
+# --------------------------------------------------------------------------
+
+def _res_inputs(x, res):
+    """Both inputs in one dtype: a mixed pair is promoted to fp32 (exact for bf16 / fp16), as the
+    reference upcasts bf16 operands to fp32 before its kernel (metal.py:856-859, 1718-1719)."""
+    xc, rc = x.detach(), res.detach()
+    if xc.dtype != rc.dtype:
+        xc, rc = xc.to(torch.float32), rc.to(torch.float32)
+    _code(xc.dtype)
+    return xc.contiguous(), rc.contiguous()
+
+
+class ResidualAddAggFn(torch.autograd.Function):
+    """(out, y_agg) = (x + res, sum_i H_pre[i] (x + res)[:, i]); H_pre is used as given.
+
+    Backward (an extension; the reference kernel is not differentiable):
+    dx = dres = dout + H_pre[i] dy_agg, dH_pre[i] = sum dy_agg (x + res)[:, i].
+    """
+
+    @staticmethod
+    def forward(ctx, x, res, H_pre, out_dtype):
+        B, n, C = (int(s) for s in x.shape)
+        xc, rc = _res_inputs(x, res)
+        hp = _f32(H_pre)
+        out = torch.empty((B, n, C), dtype=out_dtype, device=x.device)
+        y_agg = torch.empty((B, C), dtype=torch.float32, device=x.device)
+        with timed("residual_add_agg"):
+            _lib.call("mhc_residual_add_agg_fwd", _p(xc), _p(rc), _code(xc.dtype), _p(hp), _lib.H_ACTIVATED,
+                      _p(out), _code(out_dtype), _p(y_agg), B, n, C, _stream(xc))
+        ctx.save_for_backward(x, res, H_pre)
+        ctx.set_materialize_grads(False)
+        return out, y_agg
+
+    @staticmethod
+    def backward(ctx, dout, dy):
+        x, res, hpre = ctx.saved_tensors
+        B, n, C = (int(s) for s in x.shape)
+        xc, rc = _res_inputs(x, res)
+        hp = _f32(hpre)
+        want_h = ctx.needs_input_grad[2]
+        gc = None
+        if dout is not None:
+            gdt = dout.dtype if dout.dtype in (torch.float32, xc.dtype) else torch.float32
+            gc = dout.detach().to(gdt).contiguous()
+        dyc = None if dy is None else dy.detach().to(torch.float32).contiguous()
+        dx = torch.empty_like(xc) if ctx.needs_input_grad[0] else None
+        dres = torch.empty_like(xc) if ctx.needs_input_grad[1] else None
+        dpre = torch.empty((n,), dtype=torch.float32, device=xc.device) if want_h else None
+        nb = _lib.query("mhc_residual_add_agg_bwd_workspace_bytes", B, n, C) if want_h else 0
+        ws = _ws(nb, xc.device)
+        with timed("residual_add_agg_bwd"):
+            _lib.call("mhc_residual_add_agg_bwd", _p(xc), _p(rc), _code(xc.dtype), _p(gc),
+                      _code(gc.dtype) if gc is not None else _code(xc.dtype), _p(dyc), _p(hp), _lib.H_ACTIVATED,
+                      _p(dx), _p(dres), _p(dpre), _p(ws), nb, B, n, C, _stream(xc))
+        if dx is not None and dx.dtype != x.dtype:
+            dx = dx.to(x.dtype)
+        if dres is not None and dres.dtype != res.dtype:
+            dres = dres.to(res.dtype)
+        return dx, dres, (dpre.to(hpre.dtype) if dpre is not None else None), None
+
+
+def residual_add_agg_hip(x, res, H_pre, threads_per_group=None, output_dtype=None, verbose: bool = False):
+    """Fused residual add + aggregate (metal.py:1673-1731), differentiable.
+
+    Returns (out [B, n, C], y_agg [B, C] fp32) with out = x + res and
+    y_agg = sum_i H_pre[i] * out[:, i].  ``out`` is fp32 unless
+    ``output_dtype`` names float16 / bfloat16 (any input dtype, as the
+    reference allows).  ``threads_per_group`` is validated as the reference
+    does; launch shapes are chosen by the library.
+    """
+    if x.ndim != 3:
+        raise ValueError(f"x must be [B, n, C], got shape {tuple(x.shape)}")
+    if tuple(res.shape) != tuple(x.shape):
+        raise ValueError(f"res must match x shape, got {tuple(res.shape)} vs {tuple(x.shape)}")
+    B, n, C = (int(s) for s in x.shape)
+    _validate_n(n)
+    if threads_per_group is not None and threads_per_group <= 0:
+        raise ValueError("threads_per_group must be positive")
+    if H_pre.ndim != 1 or int(H_pre.shape[0]) != n:
+        raise ValueError(f"H_pre must be [n]=[{n}], got shape {tuple(H_pre.shape)}")
+    if output_dtype is None:
+        out_dtype = torch.float32
+    elif output_dtype in (torch.float32, torch.float16, torch.bfloat16):
+        out_dtype = output_dtype
+    else:
+        raise ValueError(f"unsupported output_dtype: {output_dtype}")
+    _require_gpu(x, res, H_pre)
+    return ResidualAddAggFn.apply(x, res, H_pre, out_dtype)

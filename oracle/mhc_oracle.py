@@ -32,6 +32,10 @@ Pinning (each function's independent checks live in ``tests/test_oracle_*.py``):
 * ``post_combine`` (+ backward): explicit (non-folded) formulation, the
   weight-folding equivalence of ``tests/test_folding.py:6-39`` and
   torch.autograd.
+* ``residual_add_agg`` (+ backward): pure-Python loops on tiny shapes,
+  res = 0 reduces y_agg to ``stream_aggregate``, symmetry in (x, res), a
+  one-hot H_pre selects one stream; torch.autograd (float64) and central
+  finite differences for the backward.
 
 No function here is "parity unpinned".  The reference itself cannot be
 imported in this container (it needs MLX, which is absent), so bitwise MLX
@@ -64,6 +68,8 @@ __all__ = [
     "ds_residual",
     "rewire_linear_forward",
     "rewire_linear_backward",
+    "residual_add_agg",
+    "residual_add_agg_backward",
 ]
 
 
@@ -428,3 +434,35 @@ def rewire_linear_backward(x, W, H_pre_raw, H_post_raw, H_res_raw, dout, sinkhor
     s_pre = sigmoid(H_pre_raw, dtype)
     dpre = dpre + np.einsum("bjc,bjc->j", dx_pre3, x3) * s_pre * (1.0 - s_pre)
     return dx3.reshape(T, dims), dW, dpre, dpost, dres
+
+
+# --------------------------------------------------------------------------
+# residual add + aggregate
+# --------------------------------------------------------------------------
+
+def residual_add_agg(x, res, H_pre, dtype=np.float64):
+    """utils.py:4-24 / residual_add_agg.metal:39-66: (out, y_agg).
+
+    out[b, i, c] = x + res; y_agg[b, c] = sum_i H_pre[i] * out[b, i, c], with
+    y_agg taken from the sum before out is rounded to its output dtype
+    (the kernel aggregates the fp32 ``val``, residual_add_agg.metal:55-62).
+    H_pre is used as given (no activation).
+    """
+    val = np.asarray(x, dtype=dtype) + np.asarray(res, dtype=dtype)
+    w = np.asarray(H_pre, dtype=dtype)
+    y_agg = (val * w[None, :, None]).sum(axis=1)
+    return val, y_agg
+
+
+def residual_add_agg_backward(x, res, H_pre, dout=None, dy_agg=None, dtype=np.float64):
+    """VJP of residual_add_agg: (dx, dres, dH_pre); dout / dy_agg of None count as zero."""
+    val = np.asarray(x, dtype=dtype) + np.asarray(res, dtype=dtype)
+    w = np.asarray(H_pre, dtype=dtype)
+    d = np.zeros_like(val) if dout is None else np.asarray(dout, dtype=dtype).copy()
+    if dy_agg is None:
+        dH = np.zeros(val.shape[1], dtype=dtype)
+    else:
+        dy = np.asarray(dy_agg, dtype=dtype)
+        d = d + w[None, :, None] * dy[:, None, :]
+        dH = np.einsum("bc,bic->i", dy, val)
+    return d, d.copy(), dH

@@ -11,8 +11,8 @@ this environment (it needs MLX), so two kinds of fixtures are kept:
 * regression vectors from the float64 oracle (oracle/mhc_oracle.py, pinned
   by tests/test_oracle_*.py) for the BASELINE config-0 recipe, the
   deterministic arange recipe of tests/test_correctness.py:147-156 of the
-  reference, a small backward with every gradient, and a mini config 3
-  (per-token parameters).
+  reference, a small backward with every gradient, a mini config 3
+  (per-token parameters) and a small residual_add_agg with its gradients.
 
 Inputs are seeded numpy draws; every file is a plain .npz (no pickles).
 """
@@ -112,12 +112,27 @@ def cfg3_mini():
                 dres=dres, dw=dw, iters=20, eps=1e-6)
 
 
+def residual_mini():
+    """residual_add_agg (utils.py:4-24): bf16-representable inputs, odd C, every gradient."""
+    g = np.random.default_rng(7)
+    B, n, C = 3, 4, 129
+    x = O.bf16_round(g.standard_normal((B, n, C)).astype(np.float32))
+    res = O.bf16_round(g.standard_normal((B, n, C)).astype(np.float32))
+    h = O.sigmoid(g.standard_normal(n)).astype(np.float32)
+    dout = g.standard_normal((B, n, C)).astype(np.float32)
+    dy = g.standard_normal((B, C)).astype(np.float32)
+    out, y_agg = O.residual_add_agg(x, res, h)
+    dx, dres, dh = O.residual_add_agg_backward(x, res, h, dout, dy)
+    return dict(x=x, res=res, h=h, dout=dout, dy=dy, out=out, y_agg=y_agg, dx=dx, dres=dres, dh=dh)
+
+
 FIXTURES = {
     "sinkhorn_closed_forms.npz": closed_forms,
     "cfg0_fwd.npz": cfg0,
     "arange_kat.npz": arange_kat,
     "bwd_small.npz": bwd_small,
     "cfg3_mini.npz": cfg3_mini,
+    "residual_mini.npz": residual_mini,
 }
 
 

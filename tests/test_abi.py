@@ -101,3 +101,12 @@ def test_check_maps_status_to_exceptions(lib):
         _lib.check(-1, "mhc_sinkhorn_fwd")
     with pytest.raises(_lib.MHCError):
         _lib.check(1, "x")
+
+
+def test_residual_add_agg_rejects_bad_arguments_on_the_host(lib):
+    assert lib.mhc_residual_add_agg_fwd(None, None, 1, None, _lib.H_ACTIVATED, None, 0, None, 4, 0, 8, None) == -1
+    assert lib.mhc_residual_add_agg_fwd(None, None, 1, None, 7, None, 0, None, 4, 4, 8, None) == -1
+    assert lib.mhc_residual_add_agg_fwd(None, None, 1, None, _lib.H_ACTIVATED, None, 0, None, 4, 4, 8, None) == -1
+    assert b"null pointer" in lib.mhc_last_error()
+    assert lib.mhc_residual_add_agg_bwd(None, None, 9, None, 0, None, None, _lib.H_ACTIVATED, None, None, None,
+                                        None, 0, 4, 4, 8, None) == -1

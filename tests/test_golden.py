@@ -53,3 +53,11 @@ def test_oracle_reproduces_backward_fixtures(name):
                                      sinkhorn_iters=it, eps=eps)
     for k, g in zip(["dx", "dpre", "dpost", "dres", "dw"], grads):
         assert np.allclose(g, z[k], rtol=1e-10, atol=1e-14), k
+
+
+def test_oracle_reproduces_residual_fixture():
+    z = load("residual_mini.npz")
+    out, y = O.residual_add_agg(z["x"], z["res"], z["h"])
+    assert np.allclose(out, z["out"], rtol=1e-12, atol=0) and np.allclose(y, z["y_agg"], rtol=1e-12, atol=1e-15)
+    for k, g in zip(["dx", "dres", "dh"], O.residual_add_agg_backward(z["x"], z["res"], z["h"], z["dout"], z["dy"])):
+        assert np.allclose(g, z[k], rtol=1e-12, atol=1e-14), k

@@ -4,6 +4,7 @@ from pathlib import Path
 
 import numpy as np
 import pytest
+import torch
 
 from tests._helpers import dev_tensor, np_of, rel_err
 
@@ -65,3 +66,18 @@ def test_backward_fixtures(name, per_token):
     assert rel_err(np_of(out), z["out"]) < 1e-5
     for k, g in zip(["dx", "dpre", "dpost", "dres", "dw"], grads):
         assert rel_err(np_of(g), z[k]) < (1e-5 if k == "dx" else 1e-4), (k, rel_err(np_of(g), z[k]))
+
+
+@pytest.mark.parametrize("dt,tol", [("f32", 1e-5), ("bf16", 1e-5)])
+def test_residual_fixture(dt, tol):
+    """The fixture's inputs are bf16-representable: both dtypes see the same values."""
+    z = load("residual_mini.npz")
+    xt = dev_tensor(z["x"], dt).requires_grad_(True)
+    rt = dev_tensor(z["res"], dt).requires_grad_(True)
+    ht = dev_tensor(z["h"]).requires_grad_(True)
+    out, y = ops.residual_add_agg_hip(xt, rt, ht)
+    assert rel_err(np_of(out), z["out"]) < tol and rel_err(np_of(y), z["y_agg"]) < tol
+    torch.autograd.backward([out, y], [dev_tensor(z["dout"]), dev_tensor(z["dy"])])
+    assert rel_err(np_of(ht.grad), z["dh"]) < 1e-5
+    gtol = 1e-5 if dt == "f32" else 2e-2
+    assert rel_err(np_of(xt.grad), z["dx"]) < gtol and rel_err(np_of(rt.grad), z["dres"]) < gtol
