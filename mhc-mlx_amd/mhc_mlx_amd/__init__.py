@@ -5,6 +5,7 @@ runs in libmhc_hip.so (hand-written HIP kernels, C ABI in include/mhc_hip.h).
 """
 
 from .layer import MHCLayer, MHCRewire
+from .patching import AutoPatcher
 from . import ops, reference
 from .ops import (
     mhc_forward_fused_hip,
@@ -25,6 +26,7 @@ from .utils import residual_add_agg
 __version__ = "0.1.0"
 
 __all__ = [
+    "AutoPatcher",
     "MHCLayer",
     "MHCRewire",
     "ops",

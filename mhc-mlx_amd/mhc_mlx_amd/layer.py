@@ -202,16 +202,26 @@ class MHCLayer(nn.Module):
         return ref.mhc_forward_reference(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight,
                                          sinkhorn_iters=self.sinkhorn_iters, eps=self.eps)
 
-    def post_combine(self, x_reshaped: torch.Tensor, y_inner_reshaped: torch.Tensor) -> torch.Tensor:
-        """H_post * (y_inner + (M diag(H_pre)) x) on [B, n, C] views (layer.py:302-337); fp32 out."""
+    def post_combine(self, x_reshaped: torch.Tensor, y_inner_reshaped: torch.Tensor, *,
+                     return_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """H_post * (y_inner + (M diag(H_pre)) x) on [B, n, C] views (layer.py:302-337).
+
+        fp32 out as in the reference; ``return_dtype`` (extension) casts it, and a half type equal to
+        x's dtype is written by the kernel directly.
+        """
         if self.use_metal and not _disabled_by_env():
-            return ops.post_combine(x_reshaped, y_inner_reshaped, self.H_pre_raw, self.H_post_raw, self.H_res_raw,
-                                    sinkhorn_iters=self.sinkhorn_iters, eps=self.eps)
-        H_pre_act, H_post_act = ref.activate_pre_post(self.H_pre_raw, self.H_post_raw)
-        M = ref.mixing_matrix_from_logits(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps)
-        M_final = M * H_pre_act.reshape(1, -1)
-        x_mixed = torch.einsum("ij,...jd->...id", M_final, x_reshaped.to(M_final.dtype))
-        return (y_inner_reshaped.to(x_mixed.dtype) + x_mixed) * H_post_act.reshape(1, self.n, 1)
+            kdt = self._kernel_out_dtype(x_reshaped, return_dtype)
+            out = ops.post_combine(x_reshaped, y_inner_reshaped, self.H_pre_raw, self.H_post_raw, self.H_res_raw,
+                                   sinkhorn_iters=self.sinkhorn_iters, eps=self.eps, output_dtype=kdt)
+        else:
+            H_pre_act, H_post_act = ref.activate_pre_post(self.H_pre_raw, self.H_post_raw)
+            M = ref.mixing_matrix_from_logits(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps)
+            M_final = M * H_pre_act.reshape(1, -1)
+            x_mixed = torch.einsum("ij,...jd->...id", M_final, x_reshaped.to(M_final.dtype))
+            out = (y_inner_reshaped.to(x_mixed.dtype) + x_mixed) * H_post_act.reshape(1, self.n, 1)
+        if return_dtype is not None and out.dtype != return_dtype:
+            out = out.to(return_dtype)
+        return out
 
     def _check(self, x: torch.Tensor):
         if x.ndim != 3:
@@ -270,14 +280,18 @@ class MHCRewire(nn.Module):
     """Wrap any dims -> dims module with mHC residual mixing (layer.py:438-492).
 
     out = H_post * (inner(H_pre * x) + (M diag(H_pre)) x), with x [..., dims]
-    viewed as n streams of C = dims // n channels.
+    viewed as n streams of C = dims // n channels.  The output is fp32 as in
+    the reference; ``return_dtype`` (extension, e.g. torch.bfloat16 for a
+    half-precision model) selects another output dtype.
     """
 
-    def __init__(self, inner: nn.Module, dims: int, n: int = 32, **mhc_kwargs):
+    def __init__(self, inner: nn.Module, dims: int, n: int = 32, *, return_dtype: torch.dtype | None = None,
+                 **mhc_kwargs):
         super().__init__()
         self.inner = inner
         self.n = n
         self.dims = dims
+        self.return_dtype = return_dtype
         if dims % n != 0:
             raise ValueError(f"dims {dims} must be divisible by n={n}")
         self.mhc = MHCLayer(n=n, C=dims // n, **mhc_kwargs)
@@ -299,5 +313,5 @@ class MHCRewire(nn.Module):
             raise ValueError(
                 f"inner module must preserve the shape: got {tuple(y_inner.shape)} for input {tuple(x.shape)}"
             )
-        out = self.mhc.post_combine(x3, y_inner.reshape(-1, self.n, C))
+        out = self.mhc.post_combine(x3, y_inner.reshape(-1, self.n, C), return_dtype=self.return_dtype)
         return out.reshape(x.shape)
