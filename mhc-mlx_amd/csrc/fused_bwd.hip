@@ -784,19 +784,6 @@ void fused_bwd_lw_kernel(BwdArgs A) {
 // staged in a three-slot LDS ring while the current one is processed.
 // ---------------------------------------------------------------------------
 
-template <typename T>
-MHC_DEV f32x4 mfma16(uint2 a, uint2 b, f32x4 c);
-template <>
-MHC_DEV f32x4 mfma16<__bf16>(uint2 a, uint2 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
-                                                   0, 0, 0);
-}
-template <>
-MHC_DEV f32x4 mfma16<_Float16>(uint2 a, uint2 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
-                                               0, 0);
-}
-
 constexpr int kPt16Row = 256 + 8;  // 16-bit elements per LDS row: 256 channels + 16-byte pad
 constexpr int kPt16K = 16 * 16 + 2 * 16;
 

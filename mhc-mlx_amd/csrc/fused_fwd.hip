@@ -12,6 +12,8 @@
 //   phase B  out_i = sum_j M_ij x_j + p_i * (y * inv) * w, store
 // When the tile does not fit in registers (very large n*C) the kernel runs a
 // second pass over x instead ("reload").
+#include <type_traits>
+
 #include "mhc_device.hpp"
 #include "mhc_generic.hpp"
 #include "mhc_host.hpp"
@@ -375,10 +377,176 @@ __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// n == 16, 16-bit x, C a multiple of 128: the stream mix and the aggregate on
+// MFMA (config 3 and any 16-stream layer).
+//
+// At n = 16 the mix is 256 FMAs per channel, more VALU issue time than the
+// token's HBM time, so it moves to the matrix cores: per 16 channels
+//   out[0..16) = M X,   y = a^T X     (X = 16 streams x 16 channels)
+// as v_mfma_f32_16x16x16 with M and a (fp32) each split into three 16-bit
+// terms (split3): the products are those of fp32 M and a with the 16-bit
+// x, accumulated in fp32.  For y the A operand repeats a in every row, so
+// every lane receives y of its column.
+//
+// Layout: a wave handles slabs of 128 channels; lane (q = lane >> 4,
+// r = lane & 15) loads streams 4q .. 4q+3 of channels [8r, 8r + 8) of the
+// slab (four 16-byte loads).  For MFMA number v (0..7) the B operand of the
+// lane is stream 4q .. 4q+3 of channel 8r + v, and the result D holds out of
+// streams 4q .. 4q+3 at that channel: after the eight MFMAs the lane owns
+// out for exactly the elements it loaded, stored as 16-byte rows.  One token
+// per workgroup of S / SPW waves (S = C / 128 slabs, SPW slabs per wave).
+// ---------------------------------------------------------------------------
+
+template <typename XT>
+MHC_DEV uint32_t pack_lo16(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
+template <typename XT>
+MHC_DEV uint32_t pack_hi16(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xFFFF0000u); }
+
+template <typename XT, typename OT, int SPW, bool PT, bool RAW>
+__global__ __launch_bounds__(SPW == 2 ? 512 : 1024) void fused_fwd_mfma16_kernel(FwdArgs A) {
+  constexpr int N = 16;
+  __shared__ float s_red[2][16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int C = A.C;
+  const int64_t nC = (int64_t)N * C;
+  int cb[SPW];
+#pragma unroll
+  for (int s = 0; s < SPW; ++s) cb[s] = (wave * SPW + s) * 128 + 8 * r;
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const XT* xt = (const XT*)A.x + t * nC;
+    OT* ot = (OT*)A.out + t * nC;
+    Vec<XT, 8> xr[SPW][4];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xr[s][k].load(xt + (int64_t)(4 * q + k) * C + cb[s]);
+
+    // parameters of this token: M row r, columns 4q..4q+3; a and p of streams 4q..4q+3
+    const float4 m4 = *reinterpret_cast<const float4*>(A.M + (PT ? t * 256 : 0) + r * 16 + 4 * q);
+    const float4 h4 = *reinterpret_cast<const float4*>(A.hpre + (PT ? t * 16 : 0) + 4 * q);
+    const float4 g4 = *reinterpret_cast<const float4*>(A.hpost + (PT ? t * 16 : 0) + 4 * q);
+    float av[4] = {h4.x, h4.y, h4.z, h4.w}, pv[4] = {g4.x, g4.y, g4.z, g4.w};
+    if constexpr (RAW) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        av[k] = sigmoidf_(av[k]);
+        pv[k] = 2.0f * sigmoidf_(pv[k]);
+      }
+    }
+    uint2 am[3], aa[3];
+    {
+      const float mv[4] = {m4.x, m4.y, m4.z, m4.w};
+      uint32_t hm[4][3], ha[4][3];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        split3<XT>(mv[k], hm[k]);
+        split3<XT>(av[k], ha[k]);
+      }
+#pragma unroll
+      for (int e = 0; e < 3; ++e) {
+        am[e] = make_uint2(hm[0][e] | (hm[1][e] << 16), hm[2][e] | (hm[3][e] << 16));
+        aa[e] = make_uint2(ha[0][e] | (ha[1][e] << 16), ha[2][e] | (ha[3][e] << 16));
+      }
+    }
+
+    f32x4 dmix[SPW][8];
+    float y[SPW][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int wd = v >> 1;
+        uint2 b;
+        if (v & 1) {
+          b.x = pack_hi16<XT>(xr[s][0].w[wd], xr[s][1].w[wd]);
+          b.y = pack_hi16<XT>(xr[s][2].w[wd], xr[s][3].w[wd]);
+        } else {
+          b.x = pack_lo16<XT>(xr[s][0].w[wd], xr[s][1].w[wd]);
+          b.y = pack_lo16<XT>(xr[s][2].w[wd], xr[s][3].w[wd]);
+        }
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 accy = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 2; e >= 0; --e) {
+          acc = mfma16<XT>(am[e], b, acc);
+          accy = mfma16<XT>(aa[e], b, accy);
+        }
+        dmix[s][v] = acc;
+        y[s][v] = accy[0];
+        ss = fmaf(accy[0], accy[0], ss);
+      }
+    }
+    // the four lanes of a column hold the same y: count it once
+    ss = q == 0 ? ss : 0.0f;
+    ss = wave_sum(ss);
+    if (lane == 0) s_red[it & 1][wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < nwaves; ++w) tot += s_red[it & 1][w];
+    const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
+    if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      const float4 w0 = *reinterpret_cast<const float4*>(A.w + cb[s]);
+      const float4 w1 = *reinterpret_cast<const float4*>(A.w + cb[s] + 4);
+      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      float yn[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) yn[v] = (y[s][v] * inv) * wv[v];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float o[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) o[v] = fmaf(yn[v], pv[k], dmix[s][v][k]);
+        store_vec<OT, 8>(ot + (int64_t)(4 * q + k) * C + cb[s], o);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
 namespace {
+
+// MFMA kernel for n == 16 with 16-bit x.  Returns 1 when the shape is not
+// covered (the caller then uses fused_fwd_kernel).
+template <typename XT, typename OT, bool PT>
+int launch_fwd_mfma16(FwdArgs A, hipStream_t stream) {
+  if constexpr (std::is_same<XT, float>::value) {
+    return 1;
+  } else {
+    if (A.n != 16 || !A.vec || A.C % 128 != 0) return 1;
+    if (!aligned(A.M, 16) || !aligned(A.hpre, 16) || !aligned(A.hpost, 16) || !aligned(A.w, 16)) return 1;
+    if (env_int("MHC_FWD_MFMA", 1) == 0) return 1;
+    const int S = A.C / 128;
+    int spw = env_int("MHC_FWD_SPW", S % 2 == 0 && S >= 8 ? 2 : 1);
+    if (spw != 1 && spw != 2) spw = 1;
+    if (S % spw != 0) spw = 1;
+    const int waves = S / spw;
+    if (waves > (spw == 2 ? 8 : 16)) return 1;
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, kMaxGrid));
+    const dim3 g((unsigned)blocks), b(waves * 64);
+    const bool raw = A.h_mode == MHC_H_RAW;
+    if (spw == 2) {
+      if (raw) hipLaunchKernelGGL((fused_fwd_mfma16_kernel<XT, OT, 2, PT, true>), g, b, 0, stream, A);
+      else hipLaunchKernelGGL((fused_fwd_mfma16_kernel<XT, OT, 2, PT, false>), g, b, 0, stream, A);
+    } else {
+      if (raw) hipLaunchKernelGGL((fused_fwd_mfma16_kernel<XT, OT, 1, PT, true>), g, b, 0, stream, A);
+      else hipLaunchKernelGGL((fused_fwd_mfma16_kernel<XT, OT, 1, PT, false>), g, b, 0, stream, A);
+    }
+    MHC_CHECK_LAUNCH("fused_fwd_mfma16_kernel");
+    return MHC_OK;
+  }
+}
 
 // Full-tile kernel for layer-wide n == NMAX <= 8.  Returns 1 when the shape
 // is not covered (the caller then uses fused_fwd_kernel).
@@ -414,6 +582,10 @@ int launch_fwd(FwdArgs A, hipStream_t stream) {
   constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
   if constexpr (!PT && NMAX <= 8) {
     const int rc = launch_fwd_full<NMAX, XT, OT>(A, stream);
+    if (rc != 1) return rc;
+  }
+  if constexpr (NMAX == 16) {
+    const int rc = launch_fwd_mfma16<XT, OT, PT>(A, stream);
     if (rc != 1) return rc;
   }
   A.nchunks = (int)ceil_div(A.C, V);

@@ -296,6 +296,50 @@ MHC_DEV void lds_barrier() {
 }
 
 // --------------------------------------------------------------------------
+// MFMA (v_mfma_f32_16x16x16 bf16 / fp16: exact 16-bit products, fp32
+// accumulation).  Operand layout for lane l (r = l & 15, q = l >> 4):
+//   A: row r, k = 4q .. 4q+3        B: column r, k = 4q .. 4q+3
+//   D: rows 4q .. 4q+3 of column r (acc[0..3])
+// Each uint2 operand holds four 16-bit elements, k ascending from the low
+// half of .x.
+// --------------------------------------------------------------------------
+
+template <typename T>
+MHC_DEV f32x4 mfma16(uint2 a, uint2 b, f32x4 c);
+template <>
+MHC_DEV f32x4 mfma16<__bf16>(uint2 a, uint2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                   0, 0, 0);
+}
+template <>
+MHC_DEV f32x4 mfma16<_Float16>(uint2 a, uint2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
+                                               0, 0);
+}
+
+// 16-bit bit pattern of v rounded to T (RNE) and back.
+template <typename T> MHC_DEV uint32_t bits16(float v);
+template <> MHC_DEV uint32_t bits16<__bf16>(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+template <> MHC_DEV uint32_t bits16<_Float16>(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+template <typename T> MHC_DEV float from16(uint32_t b) { return lo16<T>(b); }
+
+// fp32 v as three 16-bit terms h[0] + h[1] + h[2] (each the RNE rounding of
+// the remainder left by the previous ones).  For bf16 the sum is exactly v
+// (3 x 8 significant bits cover fp32's 24; bf16 shares fp32's exponent
+// range); for fp16 the remainder after three terms is below 2^-33 |v| (plus
+// fp16's 2^-24 underflow step), far inside fp32 rounding of a 16-term dot
+// product.  An MFMA over the three terms against 16-bit data therefore forms
+// the fp32 product of v with that data.
+template <typename T>
+MHC_DEV void split3(float v, uint32_t (&h)[3]) {
+  h[0] = bits16<T>(v);
+  const float r1 = v - from16<T>(h[0]);
+  h[1] = bits16<T>(r1);
+  const float r2 = r1 - from16<T>(h[1]);
+  h[2] = bits16<T>(r2);
+}
+
+// --------------------------------------------------------------------------
 // math
 // --------------------------------------------------------------------------
 

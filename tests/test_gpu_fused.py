@@ -23,6 +23,8 @@ pytestmark = pytest.mark.gpu
 FWD_SHAPES = [
     (2, 4, 128), (2, 4, 129), (1, 4, 512), (3, 3, 64), (2, 1, 40), (2, 2, 24), (2, 8, 128),
     (2, 5, 72), (2, 16, 64), (2, 16, 256), (1, 32, 256), (2, 24, 40), (1, 64, 64), (2, 4, 20000),
+    # n = 16 with C a multiple of 128: the MFMA forward (one or two 128-channel slabs per wave)
+    (3, 16, 128), (2, 16, 384), (2, 16, 1024), (1, 16, 2048),
 ]
 
 
@@ -138,8 +140,9 @@ def test_layer_backward_raw_matches_oracle(B, n, C, xdt):
         assert rel_err(got, r) < tol, (name, B, n, C, xdt, rel_err(got, r))
 
 
-@pytest.mark.parametrize("B,n,C", [(6, 4, 96), (5, 16, 64), (4, 8, 33), (3, 24, 40), (3, 3, 16)])
-@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+@pytest.mark.parametrize("B,n,C", [(6, 4, 96), (5, 16, 64), (4, 8, 33), (3, 24, 40), (3, 3, 16), (4, 16, 256),
+                                   (3, 16, 1024)])
+@pytest.mark.parametrize("xdt", ["f32", "bf16", "f16"])
 def test_dynamic_per_token_matches_oracle(B, n, C, xdt):
     """Per-token H_pre/H_post [B, n] and H_res [B, n, n] (forward and all gradients)."""
     x, dout, hpre, hpost, hres, w = _bwd_case(B, n, C, xdt, xdt, 1300 + B + n + C, per_token=True)
