@@ -975,6 +975,327 @@ __global__ __launch_bounds__(256) void fused_bwd_pt16_kernel(BwdArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// n == 16, 16-bit x == dout, C a multiple of 128: every 16 x 16 contraction
+// on MFMA (per-token parameters, config 3; layer-wide n == 16 uses the
+// generic kernel).
+//
+// Lane layout as in the MFMA forward (fused_fwd.hip): wave w owns SPW
+// 128-channel slabs; per slab, lane (q = lane >> 4, r = lane & 15) loads
+// streams 4q .. 4q+3 of channels [8r, 8r + 8) of x and of g (16-byte loads).
+// Two slabs per wave halve the per-wave work that does not scale with the
+// channels (parameter activations and splits, the per-token sums).  Per channel v of that range
+// the B operands are streams 4q .. 4q+3 of channel 8r + v, and
+//   y   = a^T X,  dyn = p^T G                  (before the RMS barrier)
+//   dx  = M^T G + a dy                          (after it; a dy is the C input)
+// with M, a, p split into three 16-bit terms (split3), so the products are
+// those of the fp32 parameters with the 16-bit data.  dM = G X^T has K = C:
+// each wave stages its slab of x and g in LDS as rows of one stream and
+// accumulates dM over its channels with 8 MFMAs; the waves' parts are added
+// in wave order.  After the RMS barrier the lane reads its x and g back from
+// that slab instead of keeping them in registers across the barrier.  Both
+// per-token barriers order LDS data only (lds_barrier): a full
+// __syncthreads() would also wait for the token's dx stores.  dA and dP are lane partials summed across each
+// 16-lane row (DPP) and across waves in order; dw stays in registers across
+// the tokens of the (persistent) workgroup and ends in its partial row.
+// ---------------------------------------------------------------------------
+
+constexpr int kMf16Row = 128 + 8;  // LDS row (16-bit elements): 68 dwords, 4 mod 64 banks
+constexpr int kMf16MaxWaves = 8;
+
+template <typename XT, int SPW, bool RAW>
+__global__ __launch_bounds__(SPW == 2 ? 256 : 512) __attribute__((amdgpu_waves_per_eu(2)))
+void fused_bwd_mfma16_kernel(BwdArgs A) {
+  constexpr int N = 16;
+  constexpr int SLAB = 2 * N * kMf16Row;  // 16-bit elements of one staged slab (x rows, then g rows)
+  extern __shared__ uint16_t mf_lds[];
+  constexpr int MW = SPW == 2 ? 4 : kMf16MaxWaves;  // waves per workgroup at most
+  __shared__ float s_red[2][2][MW];
+  __shared__ float s_dm[MW][256];
+  __shared__ float s_ap[MW][32];
+  __shared__ float s_act[2][32];  // activated a, p of the token (parity-buffered)
+  __shared__ __align__(16) float s_w[1024];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int C = A.C;
+  const int64_t nC = (int64_t)N * C;
+  uint16_t* slab_lds = mf_lds + (size_t)wave * SPW * SLAB;
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  int cb[SPW];
+#pragma unroll
+  for (int s = 0; s < SPW; ++s) cb[s] = (wave * SPW + s) * 128 + 8 * r;
+
+  float dwv[SPW][8];
+#pragma unroll
+  for (int s = 0; s < SPW; ++s)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) dwv[s][v] = 0.0f;
+  // rms weight of the workgroup's channels, staged once
+  for (int c = tid; c < C; c += blockDim.x) s_w[c] = A.w[c];
+
+  // the token's parameters are loaded one token ahead (registers): a, p of
+  // streams 4q..4q+3 and column r of M, rows 4q..4q+3
+  float4 nh = make_float4(0.f, 0.f, 0.f, 0.f), ng = nh, nm = nh;
+  if ((int64_t)blockIdx.x < A.T) {
+    const int64_t t0 = blockIdx.x;
+    nh = *reinterpret_cast<const float4*>(A.hpre + t0 * 16 + 4 * q);
+    ng = *reinterpret_cast<const float4*>(A.hpost + t0 * 16 + 4 * q);
+    const float* M0 = A.M + t0 * 256 + (4 * q) * 16 + r;
+    nm = make_float4(M0[0], M0[16], M0[32], M0[48]);
+  }
+  __syncthreads();
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const XT* xt = (const XT*)A.x + t * nC;
+    const XT* gt = (const XT*)A.g + t * nC;
+    const float4 h4 = nh, g4 = ng, m4 = nm;
+    float y[SPW][8], dyn[SPW][8];
+    float ss = 0.0f, sr = 0.0f;
+    f32x4 dm = {0.0f, 0.0f, 0.0f, 0.0f};
+    float av[4];
+    {
+      Vec<XT, 8> xr[SPW][4], gr[SPW][4];
+#pragma unroll
+      for (int s = 0; s < SPW; ++s)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          xr[s][k].load(xt + (int64_t)(4 * q + k) * C + cb[s]);
+          gr[s][k].load(gt + (int64_t)(4 * q + k) * C + cb[s]);
+        }
+      {
+        const int64_t tn = t + gridDim.x;
+        if (tn < A.T) {
+          nh = *reinterpret_cast<const float4*>(A.hpre + tn * 16 + 4 * q);
+          ng = *reinterpret_cast<const float4*>(A.hpost + tn * 16 + 4 * q);
+          const float* Mn = A.M + tn * 256 + (4 * q) * 16 + r;
+          nm = make_float4(Mn[0], Mn[16], Mn[32], Mn[48]);
+        }
+      }
+      float pv[4];
+      av[0] = h4.x; av[1] = h4.y; av[2] = h4.z; av[3] = h4.w;
+      pv[0] = g4.x; pv[1] = g4.y; pv[2] = g4.z; pv[3] = g4.w;
+      if constexpr (RAW) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          av[k] = sigmoid_fast(av[k]);
+          pv[k] = 2.0f * sigmoid_fast(pv[k]);
+        }
+      }
+      if (wave == 0 && r == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          s_act[it & 1][4 * q + k] = av[k];
+          s_act[it & 1][16 + 4 * q + k] = pv[k];
+        }
+      }
+      uint2 aa[3], ap[3];
+      {
+        uint32_t ha[4][3], hp[4][3];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          split3<XT>(av[k], ha[k]);
+          split3<XT>(pv[k], hp[k]);
+        }
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {
+          aa[e] = make_uint2(ha[0][e] | (ha[1][e] << 16), ha[2][e] | (ha[3][e] << 16));
+          ap[e] = make_uint2(hp[0][e] | (hp[1][e] << 16), hp[2][e] | (hp[3][e] << 16));
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < SPW; ++s) {
+        uint16_t* sx = slab_lds + s * SLAB;
+        uint16_t* sg = sx + N * kMf16Row;
+        const float4 w0 = *reinterpret_cast<const float4*>(&s_w[cb[s]]);
+        const float4 w1 = *reinterpret_cast<const float4*>(&s_w[cb[s] + 4]);
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        // stage the slab (one LDS row per stream): dM below, dx / dA / dP after the barrier
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          *reinterpret_cast<uint4*>(&sx[(4 * q + k) * kMf16Row + 8 * r]) =
+              make_uint4(xr[s][k].w[0], xr[s][k].w[1], xr[s][k].w[2], xr[s][k].w[3]);
+          *reinterpret_cast<uint4*>(&sg[(4 * q + k) * kMf16Row + 8 * r]) =
+              make_uint4(gr[s][k].w[0], gr[s][k].w[1], gr[s][k].w[2], gr[s][k].w[3]);
+        }
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const int wd = v >> 1;
+          uint2 bx, bg;
+          if (v & 1) {
+            bx = make_uint2(pack_hi16<XT>(xr[s][0].w[wd], xr[s][1].w[wd]), pack_hi16<XT>(xr[s][2].w[wd], xr[s][3].w[wd]));
+            bg = make_uint2(pack_hi16<XT>(gr[s][0].w[wd], gr[s][1].w[wd]), pack_hi16<XT>(gr[s][2].w[wd], gr[s][3].w[wd]));
+          } else {
+            bx = make_uint2(pack_lo16<XT>(xr[s][0].w[wd], xr[s][1].w[wd]), pack_lo16<XT>(xr[s][2].w[wd], xr[s][3].w[wd]));
+            bg = make_uint2(pack_lo16<XT>(gr[s][0].w[wd], gr[s][1].w[wd]), pack_lo16<XT>(gr[s][2].w[wd], gr[s][3].w[wd]));
+          }
+          f32x4 accy = {0.0f, 0.0f, 0.0f, 0.0f}, accd = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int e = 2; e >= 0; --e) {
+            accy = mfma16<XT>(aa[e], bx, accy);
+            accd = mfma16<XT>(ap[e], bg, accd);
+          }
+          y[s][v] = accy[0];
+          dyn[s][v] = accd[0];
+          ss = fmaf(accy[0], accy[0], ss);
+          sr = fmaf(accd[0] * accy[0], wv[v], sr);
+        }
+        // dM over the slab: A = G rows (stream i), B = X^T, K = 16 channels per step
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const uint2 a = *reinterpret_cast<const uint2*>(&sg[r * kMf16Row + 16 * kk + 4 * q]);
+          const uint2 b = *reinterpret_cast<const uint2*>(&sx[r * kMf16Row + 16 * kk + 4 * q]);
+          dm = mfma16<XT>(a, b, dm);
+        }
+      }
+    }
+    // the four lanes of a column hold the same y and dyn: count them once
+    ss = q == 0 ? ss : 0.0f;
+    sr = q == 0 ? sr : 0.0f;
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    lds_barrier();
+    // s_dm / s_ap are written after this barrier and read after the next one:
+    // a wave can only write them again once every wave has passed this
+    // barrier of the following token, i.e. finished reading them.
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s_dm[wave][(4 * q + k) * 16 + r] = dm[k];
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+
+    // column r of M (rows 4q..4q+3) as the A operand of M^T
+    uint2 amt[3];
+    {
+      const float mv[4] = {m4.x, m4.y, m4.z, m4.w};
+      uint32_t hm[4][3];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) split3<XT>(mv[k], hm[k]);
+#pragma unroll
+      for (int e = 0; e < 3; ++e) amt[e] = make_uint2(hm[0][e] | (hm[1][e] << 16), hm[2][e] | (hm[3][e] << 16));
+    }
+    float dA[4] = {0.0f, 0.0f, 0.0f, 0.0f}, dP[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    XT* dxt = (XT*)A.dx + t * nC;
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      const uint16_t* sx = slab_lds + s * SLAB;
+      const uint16_t* sg = sx + N * kMf16Row;
+      const float4 w0 = *reinterpret_cast<const float4*>(&s_w[cb[s]]);
+      const float4 w1 = *reinterpret_cast<const float4*>(&s_w[cb[s] + 4]);
+      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      // dy, yn (and the dw contribution) per channel
+      float dyv[8], ynv[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const float yi = y[s][v] * inv;
+        dyv[v] = dyn[s][v] * inv * wv[v] - kf * y[s][v];
+        ynv[v] = yi * wv[v];
+        dwv[s][v] = fmaf(dyn[s][v], yi, dwv[s][v]);
+      }
+      {
+        // dx = M^T g + a dy on MFMA (a dy enters as the accumulator), and dP, from g
+        Vec<XT, 8> gr[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint4 ug = *reinterpret_cast<const uint4*>(&sg[(4 * q + k) * kMf16Row + 8 * r]);
+          gr[k].w[0] = ug.x; gr[k].w[1] = ug.y; gr[k].w[2] = ug.z; gr[k].w[3] = ug.w;
+        }
+        uint32_t ow[4][4];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const int wd = v >> 1;
+          uint2 bg;
+          if (v & 1)
+            bg = make_uint2(pack_hi16<XT>(gr[0].w[wd], gr[1].w[wd]), pack_hi16<XT>(gr[2].w[wd], gr[3].w[wd]));
+          else
+            bg = make_uint2(pack_lo16<XT>(gr[0].w[wd], gr[1].w[wd]), pack_lo16<XT>(gr[2].w[wd], gr[3].w[wd]));
+          f32x4 acc = {av[0] * dyv[v], av[1] * dyv[v], av[2] * dyv[v], av[3] * dyv[v]};
+#pragma unroll
+          for (int e = 2; e >= 0; --e) acc = mfma16<XT>(amt[e], bg, acc);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (v & 1) ow[k][wd] |= bits16<XT>(acc[k]) << 16;
+            else ow[k][wd] = bits16<XT>(acc[k]);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          st_nt(reinterpret_cast<uint32_t*>(dxt + (int64_t)(4 * q + k) * C + cb[s]), ow[k][0], ow[k][1], ow[k][2],
+                ow[k][3]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int v = 0; v < 8; ++v) dP[k] = fmaf(gr[k].get(v), ynv[v], dP[k]);
+      }
+      // dA from x, one stream row at a time
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        Vec<XT, 8> xv;
+        const uint4 ux = *reinterpret_cast<const uint4*>(&sx[(4 * q + k) * kMf16Row + 8 * r]);
+        xv.w[0] = ux.x; xv.w[1] = ux.y; xv.w[2] = ux.z; xv.w[3] = ux.w;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) dA[k] = fmaf(dyv[v], xv.get(v), dA[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      dA[k] = group_sum<16>(dA[k]);
+      dP[k] = group_sum<16>(dP[k]);
+    }
+    if (r == 0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        s_ap[wave][4 * q + k] = dA[k];
+        s_ap[wave][16 + 4 * q + k] = dP[k];
+      }
+    }
+    lds_barrier();
+    for (int k = tid; k < 256 + 32; k += blockDim.x) {
+      float sum = 0.0f;
+      if (k < 256) {
+        for (int w = 0; w < nwaves; ++w) sum += s_dm[w][k];
+        A.dM_tok[t * 256 + k] = sum;
+      } else if (k < 272) {
+        for (int w = 0; w < nwaves; ++w) sum += s_ap[w][k - 256];
+        const int j = k - 256;
+        if constexpr (RAW) {
+          const float ajv = s_act[it & 1][j];
+          sum *= ajv * (1.0f - ajv);
+        }
+        A.dpre_tok[t * 16 + j] = sum;
+      } else {
+        for (int w = 0; w < nwaves; ++w) sum += s_ap[w][k - 256];
+        const int i = k - 272;
+        if constexpr (RAW) {
+          const float piv = s_act[it & 1][16 + i];
+          sum *= piv * (1.0f - 0.5f * piv);
+        }
+        A.dpost_tok[t * 16 + i] = sum;
+      }
+    }
+  }
+  if (q == 0) {
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      *reinterpret_cast<float4*>(prow + cb[s]) = make_float4(dwv[s][0], dwv[s][1], dwv[s][2], dwv[s][3]);
+      *reinterpret_cast<float4*>(prow + cb[s] + 4) = make_float4(dwv[s][4], dwv[s][5], dwv[s][6], dwv[s][7]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Stage 2: fixed-order column sums of the G partial rows, two launches.
 //
 // reduce_rows_kernel (mhc_reduce.hpp) folds the G rows into S <= kReduceSplit
@@ -1169,6 +1490,49 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
 
 // Per-token n == 16 with 16-bit x == dout and C a multiple of 256 up to 1024
 // (fused_bwd_pt16_kernel).  Returns 1 when the shape is not covered.
+// Per-token n == 16 on MFMA (fused_bwd_mfma16_kernel): 16-bit x == dout, C a
+// multiple of 128 up to 1024 (two 128-channel slabs per wave when C / 128 is
+// even, else one), 16-byte aligned operands.  Returns 1 when the shape is not
+// covered.
+template <typename XT>
+int launch_bwd_mfma16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  if (A.n != 16 || A.C % 128 != 0 || A.C > 1024) return 1;
+  if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.dx, 16) || !aligned(A.M, 16) ||
+      !aligned(A.hpre, 16) || !aligned(A.hpost, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
+    return 1;
+  if (env_int("MHC_BWD_MFMA", 1) == 0) return 1;
+  const int S = A.C / 128;
+  int spw = env_int("MHC_BWD_SPW", S % 2 == 0 ? 2 : 1);
+  if (spw != 1 && spw != 2) spw = 1;
+  if (S % spw != 0) spw = 1;
+  const int waves = S / spw;
+  if (waves > (spw == 2 ? 4 : kMf16MaxWaves)) return 1;
+  const size_t smem = (size_t)waves * spw * 2 * 16 * kMf16Row * sizeof(uint16_t);
+  const bool raw = A.h_mode == MHC_H_RAW;
+  const void* kfn = spw == 2 ? (raw ? (const void*)fused_bwd_mfma16_kernel<XT, 2, true>
+                                    : (const void*)fused_bwd_mfma16_kernel<XT, 2, false>)
+                             : (raw ? (const void*)fused_bwd_mfma16_kernel<XT, 1, true>
+                                    : (const void*)fused_bwd_mfma16_kernel<XT, 1, false>);
+  const int occ = occupancy_blocks(kfn, waves * 64, smem);
+  if (occ <= 0) return 1;
+  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
+  const int grid_pref = env_int("MHC_BWD_GRID", 0);
+  if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+  set_rows(A, L);
+  const dim3 g((unsigned)blocks), b(waves * 64);
+  if (spw == 2) {
+    if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 2, true>), g, b, smem, stream, A);
+    else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 2, false>), g, b, smem, stream, A);
+  } else {
+    if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 1, true>), g, b, smem, stream, A);
+    else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 1, false>), g, b, smem, stream, A);
+  }
+  MHC_CHECK_LAUNCH("fused_bwd_mfma16_kernel");
+  *num_partials = blocks;
+  return MHC_OK;
+}
+
 template <typename XT>
 int launch_bwd_pt16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
   if (A.n != 16 || A.C % 256 != 0 || A.C > 1024) return 1;
@@ -1189,7 +1553,9 @@ int launch_bwd_pt16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStr
 template <int NMAX, typename XT, typename GT, bool PT>
 int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
   if constexpr (PT && NMAX == 16 && std::is_same<XT, GT>::value && ElemTraits<XT>::kBytes == 2) {
-    const int rc = launch_bwd_pt16<XT>(A, L, num_partials, stream);
+    int rc = launch_bwd_mfma16<XT>(A, L, num_partials, stream);
+    if (rc != 1) return rc;
+    rc = launch_bwd_pt16<XT>(A, L, num_partials, stream);
     if (rc != 1) return rc;
   }
   if constexpr (!PT && NMAX <= 8) {

@@ -397,11 +397,6 @@ __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
 // per workgroup of S / SPW waves (S = C / 128 slabs, SPW slabs per wave).
 // ---------------------------------------------------------------------------
 
-template <typename XT>
-MHC_DEV uint32_t pack_lo16(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
-template <typename XT>
-MHC_DEV uint32_t pack_hi16(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xFFFF0000u); }
-
 template <typename XT, typename OT, int SPW, bool PT, bool RAW>
 __global__ __launch_bounds__(SPW == 2 ? 512 : 1024) void fused_fwd_mfma16_kernel(FwdArgs A) {
   constexpr int N = 16;
@@ -455,6 +450,13 @@ __global__ __launch_bounds__(SPW == 2 ? 512 : 1024) void fused_fwd_mfma16_kernel
       }
     }
 
+    // rms weight of the lane's channels, in flight with the tile
+    float4 wq[SPW][2];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      wq[s][0] = *reinterpret_cast<const float4*>(A.w + cb[s]);
+      wq[s][1] = *reinterpret_cast<const float4*>(A.w + cb[s] + 4);
+    }
     f32x4 dmix[SPW][8];
     float y[SPW][8];
     float ss = 0.0f;
@@ -494,8 +496,7 @@ __global__ __launch_bounds__(SPW == 2 ? 512 : 1024) void fused_fwd_mfma16_kernel
     if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
-      const float4 w0 = *reinterpret_cast<const float4*>(A.w + cb[s]);
-      const float4 w1 = *reinterpret_cast<const float4*>(A.w + cb[s] + 4);
+      const float4 w0 = wq[s][0], w1 = wq[s][1];
       const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
       float yn[8];
 #pragma unroll

@@ -339,11 +339,27 @@ MHC_DEV void split3(float v, uint32_t (&h)[3]) {
   h[2] = bits16<T>(r2);
 }
 
+// Two packed words of 16-bit elements -> one word of their low (high)
+// halves, a's in the low half: element v of four streams becomes an MFMA
+// operand without leaving registers.
+template <typename XT>
+MHC_DEV uint32_t pack_lo16(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
+template <typename XT>
+MHC_DEV uint32_t pack_hi16(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xFFFF0000u); }
+
 // --------------------------------------------------------------------------
 // math
 // --------------------------------------------------------------------------
 
 // reference.py:53-54 activations
 MHC_DEV float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// The same from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32, each
+// within 1 ulp; the exponent is rounded once after scaling by log2 e):
+// relative error within a few 1e-7 over |z| <= 30 and exact limits 0 / 1
+// beyond.  For kernels that evaluate activations per token and lane.
+MHC_DEV float sigmoid_fast(float z) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
+}
 
 }  // namespace mhc

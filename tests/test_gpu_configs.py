@@ -276,9 +276,11 @@ def test_config4_rewire_linear_full_size():
     assert torch.isfinite(gw).all() and torch.isfinite(gres).all()
 
 
-@pytest.mark.parametrize("T,C,dt", [(300, 1024, "bf16"), (40, 256, "bf16"), (70, 512, "f16"), (3, 1024, "bf16")])
+@pytest.mark.parametrize("T,C,dt", [(300, 1024, "bf16"), (40, 256, "bf16"), (70, 512, "f16"), (3, 1024, "bf16"),
+                                   (50, 384, "bf16"), (20, 128, "f16"), (9, 768, "bf16"), (1500, 256, "bf16")])
 def test_per_token_n16_mfma_path(T, C, dt):
-    """Per-token n=16 with C a multiple of 256 (the MFMA parameter-gradient kernel), all gradients."""
+    """Per-token n=16 with C a multiple of 128 (the MFMA kernels: one or two 128-channel slabs per wave;
+    T = 1500 exceeds the persistent backward grid, so workgroups walk several tokens), all gradients."""
     n = 16
     g = rng(7000 + T + C)
     x = to_dtype_np(g.standard_normal((T, n, C)), dt)
@@ -295,3 +297,61 @@ def test_per_token_n16_mfma_path(T, C, dt):
     for name, got, r in zip(["dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], gots, refs):
         t = tol if name == "dx" else 1e-4
         assert rel_err(np_of(got), r) < t, (name, rel_err(np_of(got), r))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_per_token_n16_activated_c_abi(dt):
+    """mhc_fused_bwd through the C ABI with per-token M and activated H (h_mode ACTIVATED): the
+    op-level VJP contract (gradients w.r.t. M and the activated H, metal.py:2857) on the MFMA kernel."""
+    import ctypes
+
+    from mhc_mlx_amd import _lib
+
+    T, n, C = 600, 16, 512
+    g = rng(7100)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    a = O.sigmoid(g.standard_normal((T, n))).astype(np.float32)
+    p = (2 * O.sigmoid(g.standard_normal((T, n)))).astype(np.float32)
+    M = O.mixing_matrix_from_logits(g.standard_normal((T, n, n)), 20, EPS).astype(np.float32)
+    w = (1 + 0.02 * g.standard_normal(C)).astype(np.float32)
+    xt, gt = dev_tensor(x, dt), dev_tensor(dout, dt)
+    Mt, at, pt, wt = (dev_tensor(v) for v in (M, a, p, w))
+    dx = torch.empty_like(xt)
+    dM = torch.empty((T, n, n), device="cuda")
+    da = torch.empty((T, n), device="cuda")
+    dp = torch.empty((T, n), device="cuda")
+    dw = torch.empty((C,), device="cuda")
+    nb = _lib.query("mhc_fused_bwd_workspace_bytes", T, n, C, 1)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    code = {"bf16": _lib.DTYPE_BF16, "f16": _lib.DTYPE_F16}[dt]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    _lib.call("mhc_fused_bwd", P(xt), code, P(gt), code, P(Mt), n * n, P(at), P(pt), n, _lib.H_ACTIVATED, P(wt),
+              P(dx), code, P(dM), P(da), P(dp), P(dw), P(ws), nb, T, n, C, ctypes.c_float(EPS),
+              ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    rdx, rdM, rda, rdp, rdw = O.mhc_fused_backward(x, M, a, p, w, dout, eps=EPS)
+    tol = {"bf16": 2e-2, "f16": 5e-3}[dt]
+    assert rel_err(np_of(dx), rdx) < tol
+    for name, got, r in (("dM", dM, rdM), ("dH_pre", da, rda), ("dH_post", dp, rdp), ("d_w", dw, rdw)):
+        assert rel_err(np_of(got), r) < 1e-4, (name, rel_err(np_of(got), r))
+
+
+def test_per_token_n16_valu_fallback(monkeypatch):
+    """The VALU kernels that serve n = 16 when the MFMA kernels decline (here forced off through
+    their environment switches, read at every launch) give the same parity."""
+    monkeypatch.setenv("MHC_FWD_MFMA", "0")
+    monkeypatch.setenv("MHC_BWD_MFMA", "0")
+    T, n, C, dt = 40, 16, 512, "bf16"
+    g = rng(7200)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T)
+    ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+    xt = dev_tensor(x, dt).requires_grad_(True)
+    out = ops.mhc_layer_forward_dynamic(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+    assert rel_err(np_of(out), O.mhc_forward_reference(x, hpre, hpost, hres, w, 20, EPS)) < 2e-2
+    out.backward(dev_tensor(dout, dt))
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    gots = [xt.grad] + [p.grad for p in ps]
+    for name, got, r in zip(["dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], gots, refs):
+        assert rel_err(np_of(got), r) < (2e-2 if name == "dx" else 1e-4), name
