@@ -3,6 +3,7 @@
 // mhc_mlx/reference.py:20-48, 58-69 that they follow).
 #include "mhc_device.hpp"
 #include "mhc_host.hpp"
+#include "mhc_plan.hpp"
 #include "mhc_sinkhorn.hpp"
 
 namespace mhc {
@@ -67,10 +68,321 @@ __global__ __launch_bounds__(kSkThreads) void sinkhorn_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// n == 16, batched (per-token mappings, config 3): four lanes per matrix.
+//
+// With CPL columns per lane (4 by default), lane (g = lane / LPM,
+// p = lane % LPM), LPM = 16 / CPL, holds columns CPL*p .. CPL*p + CPL-1 of
+// all 16 rows of matrix g (64 / LPM matrices per wave, one float4 / float2
+// per row).  Column sums are in-lane (15 adds per column); row sums add the
+// lane's columns and finish across the LPM lanes of the matrix with DPP
+// permutes, so no iteration touches LDS.  With CPL = 4: ~200 VALU per
+// iteration and lane for the row step and ~140 for the column step, i.e.
+// ~21 per matrix, against ~75 plus 8 ds_bpermute per matrix for the
+// one-matrix-per-wave layout.
+//
+// exp(H - rowmax) uses the hardware exp2 after scaling by log2 e (relative
+// error ~|H - max| * 2^-24, far inside the fp32 tolerance).
+//
+// The VJP recomputes the forward and writes, per iteration, the cumulative
+// row / column scales R_k, C_k and the row / column sums to a workspace
+// (64 floats per matrix and iteration, [iters][R | rs | C | cs][16]); the
+// reverse sweep reads them back.  The workspace of a wave is private to it
+// and read shortly after being written, so it stays in the caches.
+// ---------------------------------------------------------------------------
+
+constexpr int kSk16Threads = 256;
+
+MHC_DEV float sk16_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
+// CPL columns per lane: LPM = 16 / CPL lanes per matrix, 64 / LPM matrices per wave.
+template <int CPL>
+struct Sk16 {
+  static constexpr int LPM = 16 / CPL;
+  static constexpr int MPW = 64 / LPM;
+  static constexpr int RPL = 16 / LPM;  // rows of the row vectors recorded per lane
+};
+
+template <int CPL>
+MHC_DEV void sk16_lds(const float* __restrict__ src, float (&v)[CPL]) {
+  if constexpr (CPL == 4) {
+    const float4 f = *reinterpret_cast<const float4*>(src);
+    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+  } else {
+    const float2 f = *reinterpret_cast<const float2*>(src);
+    v[0] = f.x; v[1] = f.y;
+  }
+}
+
+template <int CPL>
+MHC_DEV void sk16_st(float* __restrict__ dst, const float (&v)[CPL]) {
+  if constexpr (CPL == 4) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+  else *reinterpret_cast<float2*>(dst) = make_float2(v[0], v[1]);
+}
+
+// K = exp(H - rowmax) of the lane's CPL columns x 16 rows.
+template <int CPL>
+MHC_DEV void sk16_load_k(const float* __restrict__ Hm, bool mvalid, int p, float (&K)[16][CPL]) {
+  constexpr int LPM = Sk16<CPL>::LPM;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (mvalid) sk16_lds<CPL>(Hm + i * 16 + CPL * p, K[i]);
+    else {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) K[i][e] = -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float mx = K[i][0];
+#pragma unroll
+    for (int e = 1; e < CPL; ++e) mx = fmaxf(mx, K[i][e]);
+    mx = group_max<LPM>(mx);
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) K[i][e] = mvalid ? sk16_exp(K[i][e] - mx) : 0.0f;
+  }
+}
+
+// One row step and one column step on P, recording sums and scales through
+// the callbacks (inlined).
+template <int CPL, typename RowRec, typename ColRec>
+MHC_DEV void sk16_iter(float (&P)[16][CPL], float eps, RowRec&& row_rec, ColRec&& col_rec) {
+  constexpr int LPM = Sk16<CPL>::LPM;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float s = P[i][0];
+#pragma unroll
+    for (int e = 1; e < CPL; ++e) s += P[i][e];
+    s = group_sum<LPM>(s);
+    const float rsc = s > eps ? sk_rcp(s) : 1.0f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) P[i][e] *= rsc;
+    row_rec(i, s, rsc);
+  }
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    float cs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cs += P[i][e];
+    const float csc = cs > eps ? sk_rcp(cs) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) P[i][e] *= csc;
+    col_rec(e, cs, csc);
+  }
+}
+
+template <int CPL>
+MHC_DEV int64_t sk16_matrix(int& p) {
+  constexpr int LPM = Sk16<CPL>::LPM;
+  const int lane = threadIdx.x & 63;
+  p = lane % LPM;
+  return ((int64_t)blockIdx.x * (kSk16Threads / 64) + (threadIdx.x >> 6)) * Sk16<CPL>::MPW + lane / LPM;
+}
+
+template <int CPL>
+__global__ __launch_bounds__(kSk16Threads) void sinkhorn16_fwd_kernel(const float* __restrict__ logits,
+                                                                      float* __restrict__ out, int64_t batch,
+                                                                      int iters, float eps) {
+  int p;
+  const int64_t m = sk16_matrix<CPL>(p);
+  const bool mvalid = m < batch;
+  float P[16][CPL];
+  sk16_load_k<CPL>(logits + (mvalid ? m : 0) * 256, mvalid, p, P);
+  for (int it = 0; it < iters; ++it)
+    sk16_iter<CPL>(P, eps, [](int, float, float) {}, [](int, float, float) {});
+  if (mvalid) {
+    float* O = out + m * 256;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sk16_st<CPL>(O + i * 16 + CPL * p, P[i]);
+  }
+}
+
+// st: [batch][iters][4][16] floats (R_k, rs_k, C_k, cs_k).  dM may alias dlogits.
+template <int CPL>
+__global__ __launch_bounds__(kSk16Threads) void sinkhorn16_bwd_kernel(const float* __restrict__ logits,
+                                                                      const float* dM, float* dlogits,
+                                                                      int64_t batch, int iters, float eps,
+                                                                      float* __restrict__ st) {
+  constexpr int LPM = Sk16<CPL>::LPM;
+  constexpr int RPL = Sk16<CPL>::RPL;
+  int p;
+  const int64_t m = sk16_matrix<CPL>(p);
+  const bool mvalid = m < batch;
+  const int64_t mm = mvalid ? m : 0;
+  float K[16][CPL];
+  sk16_load_k<CPL>(logits + mm * 256, mvalid, p, K);
+  float* sm = st + mm * (int64_t)iters * 64;
+
+  // forward recompute, recording R_k, rs_k (rows RPL*p ..) and C_k, cs_k (columns CPL*p ..)
+  {
+    float P[16][CPL];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) P[i][e] = K[i][e];
+    float R[16], Cc[CPL];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) R[i] = 1.0f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) Cc[e] = 1.0f;
+    for (int it = 0; it < iters; ++it) {
+      float rs[16], cs[CPL];
+      sk16_iter<CPL>(P, eps,
+                     [&](int i, float s, float rsc) {
+                       rs[i] = s;
+                       R[i] *= rsc;
+                     },
+                     [&](int e, float s, float csc) {
+                       cs[e] = s;
+                       Cc[e] *= csc;
+                     });
+      if (mvalid) {
+        float* sk = sm + (int64_t)it * 64;
+        float r4[RPL], s4[RPL];
+#pragma unroll
+        for (int k = 0; k < RPL; ++k) {
+          float rv = R[k], sv = rs[k];
+#pragma unroll
+          for (int q = 1; q < LPM; ++q)
+            if (p == q) {
+              rv = R[RPL * q + k];
+              sv = rs[RPL * q + k];
+            }
+          r4[k] = rv;
+          s4[k] = sv;
+        }
+        sk16_st<RPL>(sk + RPL * p, r4);
+        sk16_st<RPL>(sk + 16 + RPL * p, s4);
+        sk16_st<CPL>(sk + 32 + CPL * p, Cc);
+        sk16_st<CPL>(sk + 48 + CPL * p, cs);
+      }
+    }
+  }
+  // the state written by the other lanes of the matrix is read below
+  __builtin_amdgcn_s_waitcnt(0);
+  __threadfence_block();
+
+  float G[16][CPL];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (mvalid) sk16_lds<CPL>(dM + mm * 256 + i * 16 + CPL * p, G[i]);
+    else {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) G[i][e] = 0.0f;
+    }
+  }
+  auto ld16 = [&](const float* src, float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 f = *reinterpret_cast<const float4*>(src + 4 * k);
+      v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+    }
+  };
+  // Reverse sweep: iteration `it` reads R_it, rs_it, cs_it (own columns),
+  // R_{it-1} and C_{it-1} (own columns).  Invalid matrices (past the batch)
+  // never read the workspace.  The eps masks are selects, not branches.
+  for (int it = iters - 1; it >= 0; --it) {
+    float Rk[16], rs[16], Rp[16], csv[CPL], Cp[CPL];
+    if (mvalid) {
+      const float* sk = sm + (int64_t)it * 64;
+      ld16(sk, Rk);
+      ld16(sk + 16, rs);
+      sk16_lds<CPL>(sk + 48 + CPL * p, csv);
+      if (it > 0) {
+        ld16(sk - 64, Rp);
+        sk16_lds<CPL>(sk - 64 + 32 + CPL * p, Cp);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) Rp[i] = 1.0f;
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) Cp[e] = 1.0f;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Rk[i] = rs[i] = Rp[i] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) csv[e] = 0.0f, Cp[e] = 1.0f;
+    }
+    // K C_{k-1}: both steps' inputs are R K C_{k-1}, R = R_k (column step) or R_{k-1} (row step)
+    float KC[16][CPL];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) KC[i][e] = K[i][e] * Cp[e];
+    // column step (masked column: zero gradient)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dot = fmaf(G[i][e] * KC[i][e], Rk[i], dot);
+      const bool on = csv[e] > eps;
+      const float sc = on ? sk_rcp(csv[e]) : 0.0f;
+      const float sc2 = sc * sc * dot;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) G[i][e] = fmaf(sc, G[i][e], -sc2);
+    }
+    // row step (masked row: gradient passes unchanged)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float prod = 0.0f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) prod = fmaf(G[i][e], KC[i][e], prod);
+      const float dot = group_sum<LPM>(prod * Rp[i]);
+      const bool on = rs[i] > eps;
+      const float sc = on ? sk_rcp(rs[i]) : 1.0f;
+      const float sc2 = on ? sc * sc * dot : 0.0f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) G[i][e] = fmaf(sc, G[i][e], -sc2);
+    }
+  }
+  // through exp and the row-max shift (the max's gradient split evenly among
+  // tied maxima; zero in exact arithmetic)
+  if (mvalid) {
+    float* O = dlogits + mm * 256;
+    const float* Hm = logits + mm * 256;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float hv[CPL];
+      sk16_lds<CPL>(Hm + i * 16 + CPL * p, hv);
+      float mx = hv[0];
+#pragma unroll
+      for (int e = 1; e < CPL; ++e) mx = fmaxf(mx, hv[e]);
+      mx = group_max<LPM>(mx);
+      float dsh[CPL], tot = 0.0f, cnt = 0.0f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        dsh[e] = G[i][e] * K[i][e];
+        tot += dsh[e];
+        cnt += hv[e] == mx ? 1.0f : 0.0f;
+      }
+      tot = group_sum<LPM>(tot);
+      cnt = group_sum<LPM>(cnt);
+      const float corr = cnt > 0.0f ? tot / cnt : 0.0f;
+      float o[CPL];
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) o[e] = dsh[e] - (hv[e] == mx ? corr : 0.0f);
+      sk16_st<CPL>(O + i * 16 + CPL * p, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
 namespace {
+
+// The n == 16 kernels need 16-byte aligned matrices; MHC_SK16=0 turns them off.
+bool use_sk16(int n, const void* a, const void* b, const void* c) {
+  if (n != 16 || env_int("MHC_SK16", 1) == 0) return false;
+  return aligned(a, 16) && aligned(b, 16) && (c == nullptr || aligned(c, 16));
+}
+
+// MHC_SK16_CPL (2 or 4) selects the columns per lane (tuning override).
+int sk16_cpl() { return env_int("MHC_SK16_CPL", 4) == 2 ? 2 : 4; }
+
+int64_t sk16_blocks(int64_t batch, int cpl) {
+  return ceil_div(batch, (int64_t)(cpl == 4 ? Sk16<4>::MPW : Sk16<2>::MPW) * (kSk16Threads / 64));
+}
 
 struct SkPlan {
   int np;
@@ -155,6 +467,14 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
   MHC_CHECK_ARG(logits != nullptr && M != nullptr, "null pointer argument");
   const int cus = device_cu_count();
   hipStream_t s = (hipStream_t)stream;
+  if (use_sk16(n, logits, M, nullptr)) {
+    const int cpl = sk16_cpl();
+    const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
+    if (cpl == 4) hipLaunchKernelGGL(sinkhorn16_fwd_kernel<4>, g, b, 0, s, logits, M, batch, iters, eps);
+    else hipLaunchKernelGGL(sinkhorn16_fwd_kernel<2>, g, b, 0, s, logits, M, batch, iters, eps);
+    MHC_CHECK_LAUNCH("sinkhorn16_fwd_kernel");
+    return MHC_OK;
+  }
   switch (next_pow2(n)) {
     case 1: launch_fwd<1>(logits, M, batch, n, iters, eps, s, cus); break;
     case 2: launch_fwd<2>(logits, M, batch, n, iters, eps, s, cus); break;
@@ -168,9 +488,18 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
   return MHC_OK;
 }
 
+namespace {
+// n == 16: 64 floats of recorded state per matrix and iteration.
+size_t sk16_state_bytes(int64_t batch, int iters) {
+  return (size_t)batch * (size_t)(iters > 0 ? iters : 1) * 64 * sizeof(float);
+}
+}  // namespace
+
 extern "C" size_t mhc_sinkhorn_bwd_workspace_bytes(int64_t batch, int n, int iters) {
   if (n < 1 || n > MHC_MAX_N || batch <= 0 || iters < 0) return 0;
-  return plan_bwd(batch, n, iters, device_cu_count()).ws_bytes;
+  const size_t gen = plan_bwd(batch, n, iters, device_cu_count()).ws_bytes;
+  if (n == 16) return std::max(gen, sk16_state_bytes(batch, iters) + 16);
+  return gen;
 }
 
 extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlogits,
@@ -182,12 +511,29 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
   MHC_CHECK_ARG(iters >= 0, "iters=%d must be >= 0", iters);
   if (batch == 0) return MHC_OK;
   MHC_CHECK_ARG(logits != nullptr && dM != nullptr && dlogits != nullptr, "null pointer argument");
+  hipStream_t s = (hipStream_t)stream;
+  if (use_sk16(n, logits, dM, dlogits) && workspace != nullptr) {
+    // the recorded state starts at the first 16-byte boundary of the workspace
+    const uintptr_t base = reinterpret_cast<uintptr_t>(workspace);
+    const size_t pad = (size_t)((16 - base % 16) % 16);
+    const size_t need = sk16_state_bytes(batch, iters);
+    if (workspace_bytes >= need + pad) {
+      float* st = reinterpret_cast<float*>(base + pad);
+      const int cpl = sk16_cpl();
+      const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
+      if (cpl == 4)
+        hipLaunchKernelGGL(sinkhorn16_bwd_kernel<4>, g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);
+      else
+        hipLaunchKernelGGL(sinkhorn16_bwd_kernel<2>, g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);
+      MHC_CHECK_LAUNCH("sinkhorn16_bwd_kernel");
+      return MHC_OK;
+    }
+  }
   const SkPlan p = plan_bwd(batch, n, iters, device_cu_count());
   MHC_CHECK_ARG(workspace_bytes >= p.ws_bytes && (p.ws_bytes == 0 || workspace != nullptr),
                 "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes,
                 p.ws_bytes);
   float* ws = (float*)workspace;
-  hipStream_t s = (hipStream_t)stream;
   switch (p.np) {
     case 1: launch_bwd<1>(p, logits, dM, dlogits, batch, n, iters, eps, ws, s); break;
     case 2: launch_bwd<2>(p, logits, dM, dlogits, batch, n, iters, eps, ws, s); break;

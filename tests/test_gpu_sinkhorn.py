@@ -157,3 +157,71 @@ def test_sinkhorn_rejects_bad_shapes():
         ops.sinkhorn_knopp_hip(torch.zeros(3, 4, device="cuda"))
     with pytest.raises(ValueError, match="MAX_N_ALLOWED"):
         ops.sinkhorn_knopp_hip(torch.zeros(65, 65, device="cuda"))
+
+
+# ------------------------------------------------ n = 16 batched kernels
+# (four lanes per matrix, 16 matrices per wave, VJP state in the workspace)
+
+@pytest.mark.parametrize("batch", [1, 15, 17, 64, 65, 1000])
+def test_sinkhorn16_batches_and_tails(batch):
+    """Batches that leave waves and workgroups partly empty."""
+    g = rng(4000 + batch)
+    H = (2.0 * g.standard_normal((batch, 16, 16))).astype(np.float32)
+    dM = g.standard_normal((batch, 16, 16)).astype(np.float32)
+    got = _fwd(H, 20, 1e-6)
+    ref = O.mixing_matrix_from_logits(H, iters=20, eps=1e-6)
+    assert np.abs(got - ref).max() < 1e-5
+    Ht = dev_tensor(H).requires_grad_(True)
+    ops.sinkhorn_knopp_hip_autograd(Ht, iters=20, eps=1e-6).backward(dev_tensor(dM))
+    rg = O.sinkhorn_knopp_vjp(H, dM, iters=20, eps=1e-6)
+    assert np.abs(np_of(Ht.grad) - rg).max() / max(np.abs(rg).max(), 1e-3) < 1e-4
+
+
+def test_sinkhorn16_masked_rows_and_columns():
+    """Eps masks (reference.py:37-46): a column below eps is zeroed, a masked row passes its
+    gradient through unchanged."""
+    g = rng(4100)
+    H = g.standard_normal((40, 16, 16)).astype(np.float32)
+    H[::3, :, 5] = -40.0                       # a masked column in every third matrix
+    H[1::3, 7, :] = -45.0                      # a row that is all tiny ...
+    H[1::3, 7, 0] = 0.0                        # ... except one entry (its max)
+    dM = g.standard_normal((40, 16, 16)).astype(np.float32)
+    for eps in (1e-5, 1e-3):
+        got = _fwd(H, 20, eps)
+        ref = O.mixing_matrix_from_logits(H.astype(np.float64), iters=20, eps=eps)
+        assert np.abs(got - ref).max() < 1e-5, eps
+        Ht = dev_tensor(H).requires_grad_(True)
+        ops.sinkhorn_knopp_hip_autograd(Ht, iters=20, eps=eps).backward(dev_tensor(dM))
+        rg = O.sinkhorn_knopp_vjp(H.astype(np.float64), dM, iters=20, eps=eps)
+        assert np.abs(np_of(Ht.grad) - rg).max() < 1e-4 * max(1.0, np.abs(rg).max()), eps
+
+
+def test_sinkhorn16_vjp_in_place_c_abi():
+    """mhc_sinkhorn_bwd with dM and dlogits the same buffer (as the per-token layer backward uses
+    it) and iters = 0 (the VJP of exp and the row-max shift alone)."""
+    import ctypes
+
+    from mhc_mlx_amd import _lib
+
+    g = rng(4200)
+    B = 200
+    H = g.standard_normal((B, 16, 16)).astype(np.float32)
+    dM = g.standard_normal((B, 16, 16)).astype(np.float32)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for iters in (0, 1, 20):
+        Ht, buf = dev_tensor(H), dev_tensor(dM)
+        nb = _lib.query("mhc_sinkhorn_bwd_workspace_bytes", B, 16, iters)
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+        _lib.call("mhc_sinkhorn_bwd", P(Ht), P(buf), P(buf), B, 16, iters, ctypes.c_float(1e-6), P(ws), nb, s)
+        rg = O.sinkhorn_knopp_vjp(H, dM, iters=iters, eps=1e-6)
+        assert np.abs(np_of(buf) - rg).max() / max(np.abs(rg).max(), 1e-3) < 1e-4, iters
+
+
+def test_sinkhorn16_identity_init_and_bomb():
+    n = 16
+    Hi = (np.full((n, n), -12.0) + np.eye(n) * 12.0).astype(np.float32)
+    assert np.abs(_fwd(np.stack([Hi] * 20), 20, 1e-5) - np.eye(n)).max() < 1e-4
+    Hb = np.full((20, n, n), 100.0, np.float32)
+    got = _fwd(Hb, 20, 1e-5)
+    assert np.isfinite(got).all() and np.abs(got - 1.0 / n).max() < 1e-6
