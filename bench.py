@@ -102,7 +102,10 @@ def _fwd_latency(n, C, B, dev, reps=200):
         for _ in range(20):
             fwd()
         eager = _median_us(fwd, reps)
-    return {"eager_us": round(eager, 2), "kernel_launches": 2}
+    # layer-wide n in {4, 8} with at most one token per CU: the Sinkhorn projection runs inside the
+    # forward kernel (one launch); otherwise Sinkhorn and the fused forward are two launches
+    one = n in (4, 8) and B <= torch.cuda.get_device_properties(dev).multi_processor_count
+    return {"eager_us": round(eager, 2), "kernel_launches": 1 if one else 2}
 
 
 def _config3(dev, steps, warmup):

@@ -18,6 +18,7 @@
 #include "mhc_generic.hpp"
 #include "mhc_host.hpp"
 #include "mhc_plan.hpp"
+#include "mhc_sinkhorn.hpp"
 
 namespace mhc {
 
@@ -40,6 +41,10 @@ struct FwdArgs {
   int vec;
   int reload;
   float eps;
+  // in-kernel Sinkhorn (layer-wide n <= 8, latency regime): logits, iterations, M written by block 0
+  const float* hres;
+  float* M_out;
+  int iters;
 };
 
 // Stage (M padded to NMAX x NMAX, a, p) for token t into `buf`.
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
 // wave-uniform scalars.  The grid-stride loop only matters for T > kMaxGrid.
 // ---------------------------------------------------------------------------
 
-template <int NMAX, typename XT, typename OT, int CH, bool RAW>
+template <int NMAX, typename XT, typename OT, int CH, bool RAW, bool SKF = false>
 __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
   constexpr int V = FwdCfg<NMAX>::V;
   __shared__ float s_red[2][16];
@@ -306,6 +311,10 @@ __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
 #pragma unroll
   for (int k = 0; k < CH; ++k) c0[k] = (tid + k * (int)blockDim.x) * V;
 
+  // SKF: the Sinkhorn projection of the layer-wide logits runs in every wave
+  // (after the first token's loads are issued); block 0 stores M for the backward.
+  float Mk[SKF ? NMAX * NMAX : 1];
+
   int it = 0;
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
     // the token's loads go out first; parameters and w are read while they fly
@@ -316,6 +325,13 @@ __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
     for (int k = 0; k < CH; ++k)
 #pragma unroll
       for (int i = 0; i < NMAX; ++i) xr[k][i].load(xt + i * C + c0[k]);
+    if constexpr (SKF) {
+      if (it == 0) {
+        float mine;
+        sk_fwd_wave<NMAX>(A.hres, A.iters, A.eps, lane, Mk, mine);
+        if (blockIdx.x == 0 && tid < NMAX * NMAX) A.M_out[tid] = mine;
+      }
+    }
     float Ms[NMAX * NMAX], as[NMAX], ps[NMAX];
 #pragma unroll
     for (int i = 0; i < NMAX; ++i) {
@@ -327,7 +343,10 @@ __global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
       as[i] = uniform_f(av);
       ps[i] = uniform_f(pv);
 #pragma unroll
-      for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = uniform_f(A.M[i * NMAX + j]);
+      for (int j = 0; j < NMAX; ++j) {
+        if constexpr (SKF) Ms[i * NMAX + j] = Mk[i * NMAX + j];
+        else Ms[i * NMAX + j] = uniform_f(A.M[i * NMAX + j]);
+      }
     }
     float wv[CH][V];
 #pragma unroll
@@ -677,6 +696,48 @@ extern "C" int mhc_fused_fwd(const void* x, int x_dtype, const float* M, int64_t
                         : dispatch_types<false>(A, x_dtype, out_dtype, s);
 }
 
+namespace mhc {
+namespace {
+
+// One launch for the layer-wide forward at n == NMAX <= 8 with few tokens
+// (at most one per CU): the Sinkhorn projection runs in the forward kernel
+// instead of a launch of its own.  Returns 1 when the shape is not covered.
+template <int NMAX, typename XT, typename OT>
+int launch_fwd_full_skf(FwdArgs A, hipStream_t stream) {
+  constexpr int V = FwdCfg<NMAX>::V;
+  if (A.n != NMAX || !A.vec || A.C % V != 0) return 1;
+  const int nchunks = A.C / V;
+  if (nchunks % 64 != 0 || nchunks > 1024) return 1;
+  hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1, true, true>), dim3((unsigned)A.T), dim3(nchunks), 0,
+                     stream, A);
+  MHC_CHECK_LAUNCH("fused_fwd_full_kernel");
+  return MHC_OK;
+}
+
+int layer_fwd_single_launch(const FwdArgs& A, int xd, int od, hipStream_t s) {
+  if (env_int("MHC_FWD_SKF", 1) == 0 || A.T < 1 || A.T > device_cu_count()) return 1;
+  if (xd == MHC_DTYPE_BF16 && od == MHC_DTYPE_BF16) {
+    if (A.n == 4) return launch_fwd_full_skf<4, __bf16, __bf16>(A, s);
+    if (A.n == 8) return launch_fwd_full_skf<8, __bf16, __bf16>(A, s);
+  } else if (xd == MHC_DTYPE_BF16 && od == MHC_DTYPE_F32) {
+    if (A.n == 4) return launch_fwd_full_skf<4, __bf16, float>(A, s);
+    if (A.n == 8) return launch_fwd_full_skf<8, __bf16, float>(A, s);
+  } else if (xd == MHC_DTYPE_F32 && od == MHC_DTYPE_F32) {
+    if (A.n == 4) return launch_fwd_full_skf<4, float, float>(A, s);
+    if (A.n == 8) return launch_fwd_full_skf<8, float, float>(A, s);
+  } else if (xd == MHC_DTYPE_F16 && od == MHC_DTYPE_F16) {
+    if (A.n == 4) return launch_fwd_full_skf<4, _Float16, _Float16>(A, s);
+    if (A.n == 8) return launch_fwd_full_skf<8, _Float16, _Float16>(A, s);
+  } else if (xd == MHC_DTYPE_F16 && od == MHC_DTYPE_F32) {
+    if (A.n == 4) return launch_fwd_full_skf<4, _Float16, float>(A, s);
+    if (A.n == 8) return launch_fwd_full_skf<8, _Float16, float>(A, s);
+  }
+  return 1;
+}
+
+}  // namespace
+}  // namespace mhc
+
 extern "C" int mhc_layer_fwd(const void* x, int x_dtype, const float* h_pre_raw, const float* h_post_raw,
                              const float* h_res_raw, const float* rms_weight, void* out, int out_dtype,
                              float* M_out, int64_t T, int n, int C, int per_token, int iters, float eps,
@@ -684,6 +745,19 @@ extern "C" int mhc_layer_fwd(const void* x, int x_dtype, const float* h_pre_raw,
   clear_error();
   MHC_CHECK_ARG(T >= 0, "T=%lld must be >= 0", (long long)T);
   MHC_CHECK_ARG(M_out != nullptr && h_res_raw != nullptr, "null pointer argument");
+  if (!per_token && (n == 4 || n == 8) && T >= 1 && iters >= 0 && x && h_pre_raw && h_post_raw && rms_weight &&
+      out && dtype_bytes(x_dtype) && dtype_bytes(out_dtype)) {
+    FwdArgs A{};
+    A.x = x; A.out = out; A.M = M_out; A.hpre = h_pre_raw; A.hpost = h_post_raw; A.w = rms_weight; A.T = T;
+    A.n = n; A.C = C; A.h_mode = MHC_H_RAW; A.eps = eps; A.hres = h_res_raw; A.M_out = M_out; A.iters = iters;
+    const int V = fwd_vec_width(nmax_for(n));
+    const int xb = dtype_bytes(x_dtype), ob = dtype_bytes(out_dtype);
+    const int align_x = std::min(16, V * xb), align_o = std::min(16, V * ob);
+    A.vec = (C >= 1 && C % V == 0) && aligned(x, align_x) && aligned(out, align_o) &&
+            ((int64_t)C * xb) % align_x == 0 && ((int64_t)C * ob) % align_o == 0 ? 1 : 0;
+    const int rc = layer_fwd_single_launch(A, x_dtype, out_dtype, (hipStream_t)stream);
+    if (rc != 1) return rc;
+  }
   const int64_t batch = per_token ? T : 1;
   if (batch > 0) {
     const int rc = mhc_sinkhorn_fwd(h_res_raw, M_out, batch, n, iters, eps, stream);

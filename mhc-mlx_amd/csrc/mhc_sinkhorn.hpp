@@ -99,6 +99,35 @@ MHC_DEV void sk_fwd_group(const float* __restrict__ H, float* __restrict__ out, 
   }
 }
 
+// The same projection of one n x n matrix, n == NP <= 8, computed by a whole
+// wave (its 64 / G lane groups all process the matrix) with the lane layout
+// and arithmetic of sk_fwd_group, so the results are bitwise those of the
+// batched kernel.  Returns the matrix as wave-uniform values M[i * NP + j]
+// and, in `mine`, the element of lanes < NP * NP (row lane / NP, column
+// lane % NP).
+template <int NP>
+MHC_DEV void sk_fwd_wave(const float* __restrict__ H, int iters, float eps, int lane, float (&M)[NP * NP],
+                         float& mine) {
+  using L = SkLayout<NP>;
+  static_assert(L::E == 1 && L::LR == NP, "one element per lane, one row per NP lanes");
+  const int lm = lane % L::G;
+  const int r = lm / L::LR;
+  const int c = lm % L::LR;
+  float P = H[r * NP + c];
+  const float mx = group_max<L::LR>(P);
+  P = expf(P - mx);
+  for (int it = 0; it < iters; ++it) {
+    const float s = group_sum<L::LR>(P);
+    P *= s > eps ? sk_rcp(s) : 1.0f;
+    const float cs = strided_sum<L::LR, L::G>(P);
+    P *= cs > eps ? sk_rcp(cs) : 0.0f;
+  }
+  mine = P;
+#pragma unroll
+  for (int k = 0; k < NP * NP; ++k)
+    M[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, P), k));
+}
+
 // VJP for the matrix of this lane's group: dlogits = d/dH <dM, SK(H)>.
 // st: this wavefront's state, layout [4][iters][W] (row sums, cumulative row
 // scale R_k, column sums, cumulative column scale C_k).

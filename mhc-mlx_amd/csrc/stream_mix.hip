@@ -439,10 +439,24 @@ __global__ __launch_bounds__(64) void scale_final_kernel(const float* __restrict
 
 int mix_vec_width(int nmax) { return nmax == 0 ? 1 : (nmax <= 8 ? 8 : 64 / nmax); }
 
-int64_t mix_grid(int64_t work, int cus) {
+// Grid of a grid-stride kernel over `work` items: at most `per_cu`
+// workgroups per CU (per_cu < 0: one item per thread, up to kMaxGrid).
+// `env` names a tuning override of per_cu.
+int64_t mix_grid(int64_t work, int cus, const char* env = "MHC_MIX_GRID", int per_cu = 8) {
+  per_cu = env_int(env, per_cu);
   int64_t g = ceil_div(work, kMixThreads);
-  g = std::min<int64_t>(g, (int64_t)cus * 8);
+  g = std::min<int64_t>(g, per_cu < 0 ? kMaxGrid : (int64_t)cus * std::max(per_cu, 1));
   return std::max<int64_t>(g, 1);
+}
+
+// Workgroups along x of the per-stream scale kernels (grid.y = n): at most
+// 8 per CU over all streams by default; `env` overrides the per-CU count
+// (< 0: one item per thread).
+int64_t scale_grid(int64_t T, int n, int C, const char* env) {
+  const int per_cu = env_int(env, 8);
+  const int64_t g = ceil_div(T * ceil_div(C, 8), kMixThreads);
+  const int64_t cap = per_cu < 0 ? kMaxGrid : (int64_t)device_cu_count() * std::max(per_cu, 1) / n + 1;
+  return std::max<int64_t>(1, std::min<int64_t>(g, cap));
 }
 
 bool io_vec_ok(int C, int V, std::initializer_list<std::pair<const void*, int>> ptrs) {
@@ -513,7 +527,7 @@ extern "C" int mhc_stream_mix_add_fwd(const void* x, int x_dtype, const void* y,
   A.nchunks = (int)ceil_div(C, V);
   A.vec = io_vec_ok(C, V, {{x, dtype_bytes(x_dtype)}, {y, y ? dtype_bytes(y_dtype) : 4},
                            {out, dtype_bytes(out_dtype)}});
-  const int64_t blocks = mix_grid(T * A.nchunks, device_cu_count());
+  const int64_t blocks = mix_grid(T * A.nchunks, device_cu_count(), "MHC_MIX_FWD_GRID", 8);
   hipStream_t s = (hipStream_t)stream;
   const int ydt = y ? y_dtype : x_dtype;
   if (nmax_for(n) == 0) {
@@ -543,7 +557,7 @@ extern "C" int mhc_stream_mix_add_fwd(const void* x, int x_dtype, const void* y,
 extern "C" size_t mhc_stream_mix_add_bwd_workspace_bytes(int64_t T, int n, int C) {
   if (T <= 0 || n < 1 || n > MHC_MAX_N || C < 1) return 0;
   const int V = mix_vec_width(nmax_for(n));
-  const int64_t G = mix_grid(T * ceil_div(C, V), device_cu_count());
+  const int64_t G = mix_grid(T * ceil_div(C, V), device_cu_count(), "MHC_MIX_BWD_GRID", 8);
   return (size_t)(G + kMixSplit) * (size_t)mix_rows(n) * sizeof(float);
 }
 
@@ -567,7 +581,7 @@ extern "C" int mhc_stream_mix_add_bwd(const void* x, int x_dtype, const void* y,
   MHC_CHECK_ARG(dtype_bytes(x_dtype) && dtype_bytes(dout_dtype), "unknown dtype code");
   const int V = mix_vec_width(nmax_for(n));
   const int nch = (int)ceil_div(C, V);
-  const int64_t G = mix_grid(T * nch, device_cu_count());
+  const int64_t G = mix_grid(T * nch, device_cu_count(), "MHC_MIX_BWD_GRID", 8);
   const int P = mix_rows(n);
   const size_t need = (size_t)(G + kMixSplit) * P * sizeof(float);
   MHC_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
@@ -630,8 +644,7 @@ extern "C" int mhc_stream_scale_fwd(const void* x, int x_dtype, const float* h_p
   A.x = x; A.out = out; A.hpre = h_pre; A.T = T; A.n = n; A.C = C; A.h_mode = h_mode;
   A.nchunks = (int)ceil_div(C, 8);
   A.vec = io_vec_ok(C, 8, {{x, dtype_bytes(x_dtype)}, {out, dtype_bytes(out_dtype)}});
-  const int64_t bx = std::max<int64_t>(
-      1, std::min<int64_t>(ceil_div(T * A.nchunks, kMixThreads), (int64_t)device_cu_count() * 8 / n + 1));
+  const int64_t bx = scale_grid(T, n, C, "MHC_SCALE_FWD_GRID");
   hipStream_t s = (hipStream_t)stream;
   return by_dtype(x_dtype, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
@@ -646,11 +659,7 @@ extern "C" int mhc_stream_scale_fwd(const void* x, int x_dtype, const float* h_p
 }
 
 namespace {
-int64_t scale_bwd_grid(int64_t T, int n, int C) {
-  const int64_t nch = ceil_div(C, 8);
-  return std::max<int64_t>(
-      1, std::min<int64_t>(ceil_div(T * nch, kMixThreads), (int64_t)device_cu_count() * 8 / n + 1));
-}
+int64_t scale_bwd_grid(int64_t T, int n, int C) { return scale_grid(T, n, C, "MHC_SCALE_BWD_GRID"); }
 }  // namespace
 
 extern "C" size_t mhc_stream_scale_bwd_workspace_bytes(int64_t T, int n, int C) {

@@ -65,11 +65,18 @@ def _code(dt: torch.dtype) -> int:
 
 
 def _p(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    """Device pointer of t as an int (ctypes converts it for the c_void_p argtypes), or None."""
+    return t.data_ptr() if t is not None else None
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def _stream(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """hipStream_t of torch's current stream on t's device (as an int)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
+    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _require_gpu(*ts) -> None:
@@ -82,7 +89,16 @@ def _require_gpu(*ts) -> None:
 
 
 def _f32(t: torch.Tensor) -> torch.Tensor:
+    """t as contiguous fp32 (t itself when it already is: only its pointer is passed on)."""
+    if t.dtype is torch.float32 and t.is_contiguous():
+        return t
     return t.detach().to(torch.float32).contiguous()
+
+
+def _needs_grad(*ts) -> bool:
+    if not torch.is_grad_enabled():
+        return False
+    return any(t is not None and t.requires_grad for t in ts)
 
 
 def _ws(nbytes: int, dev) -> torch.Tensor | None:
@@ -338,8 +354,8 @@ def mhc_forward_fused_hip_autograd(x, M, H_pre, H_post, rms_weight, eps: float =
 
 def _layer_fwd(x, hpre, hpost, hres, w, iters, eps, out_dtype, per_token):
     """mhc_layer_fwd: Sinkhorn projection + fused forward from raw parameters. Returns (out, M)."""
-    B, n, C = (int(s) for s in x.shape)
-    xc = x.detach().contiguous()
+    B, n, C = x.shape
+    xc = x if x.is_contiguous() else x.contiguous()
     hp, hq, hr, wc = _f32(hpre), _f32(hpost), _f32(hres), _f32(w)
     M = torch.empty_like(hr)
     out = torch.empty((B, n, C), dtype=out_dtype, device=x.device)
@@ -425,12 +441,19 @@ class MHCLayerFn(torch.autograd.Function):
 
 def mhc_layer_forward(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, sinkhorn_iters: int = 20,
                       eps: float = 1e-5, output_dtype=None):
-    """mhc_forward_reference (reference.py:164-184) on the HIP path, with autograd."""
+    """mhc_forward_reference (reference.py:164-184) on the HIP path, with autograd.
+
+    When no input needs a gradient (inference, torch.no_grad) the kernels are
+    called directly, without an autograd node.
+    """
     if H_res_raw.ndim != 2 or H_res_raw.shape[0] != H_res_raw.shape[1]:
         raise ValueError(f"H_res_raw must be square [n, n], got shape {tuple(H_res_raw.shape)}")
     _fused_shapes(x, H_res_raw, H_pre_raw, H_post_raw, rms_weight)
     out_dtype = _normalize_output_dtype(output_dtype, x.dtype)
     _require_gpu(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight)
+    if not _needs_grad(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight):
+        return _layer_fwd(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, int(sinkhorn_iters), float(eps),
+                          out_dtype, False)[0]
     return MHCLayerFn.apply(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, int(sinkhorn_iters),
                             float(eps), out_dtype)
 
