@@ -550,8 +550,14 @@ MHC_DEV void reg_fence(uint32_t& w) { asm volatile("" : "+v"(w)); }
 
 // FULL: n == NMAX, 16-byte aligned rows and every owned chunk complete, so
 // the token loop has no per-stream or per-chunk conditions.
+// Waves per SIMD the layer-wide backward's registers are capped at (a
+// build-time tuning knob).
+#ifndef MHC_BWD_WPE
+#define MHC_BWD_WPE 4
+#endif
+
 template <int NMAX, typename XT, typename GT, int CHK, bool FULL>
-__global__ __attribute__((amdgpu_flat_work_group_size(64, 1024), amdgpu_waves_per_eu(4)))
+__global__ __attribute__((amdgpu_flat_work_group_size(64, 1024), amdgpu_waves_per_eu(MHC_BWD_WPE)))
 void fused_bwd_lw_kernel(BwdArgs A) {
   constexpr int V = lw_vec<NMAX, XT, GT>();
   constexpr int K = NMAX * NMAX + 2 * NMAX;

@@ -297,8 +297,19 @@ __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
 // wave-uniform scalars.  The grid-stride loop only matters for T > kMaxGrid.
 // ---------------------------------------------------------------------------
 
+// MHC_FWD_WPE > 0 (a build-time tuning knob) caps the registers of the
+// full-tile forward at that many waves per SIMD.
+#ifndef MHC_FWD_WPE
+#define MHC_FWD_WPE 0
+#endif
+#if MHC_FWD_WPE > 0
+#define MHC_FWD_FULL_ATTR __attribute__((amdgpu_waves_per_eu(MHC_FWD_WPE)))
+#else
+#define MHC_FWD_FULL_ATTR
+#endif
+
 template <int NMAX, typename XT, typename OT, int CH, bool RAW, bool SKF = false>
-__global__ __launch_bounds__(1024) void fused_fwd_full_kernel(FwdArgs A) {
+__global__ __launch_bounds__(1024) MHC_FWD_FULL_ATTR void fused_fwd_full_kernel(FwdArgs A) {
   constexpr int V = FwdCfg<NMAX>::V;
   __shared__ float s_red[2][16];
   const int tid = threadIdx.x;

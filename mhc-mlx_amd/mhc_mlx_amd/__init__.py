@@ -4,10 +4,14 @@
 runs in libmhc_hip.so (hand-written HIP kernels, C ABI in include/mhc_hip.h).
 """
 
-from .layer import MHCLayer, MHCRewire
-from .patching import AutoPatcher
-from . import ops, reference
-from .ops import (
+from . import tuning
+
+tuning.load()  # the tuning files of the working directory and ~/.cache/mhc-mlx (metal.py:21-33)
+
+from .layer import MHCLayer, MHCRewire  # noqa: E402
+from .patching import AutoPatcher  # noqa: E402
+from . import ops, reference  # noqa: E402
+from .ops import (  # noqa: E402
     mhc_forward_fused_hip,
     mhc_forward_fused_hip_autograd,
     mhc_layer_forward,
@@ -20,8 +24,8 @@ from .ops import (
     stream_mix_add_hip_autograd,
     stream_scale,
 )
-from .profiling import kernel_timer
-from .utils import residual_add_agg
+from .profiling import kernel_timer  # noqa: E402
+from .utils import residual_add_agg  # noqa: E402
 
 __version__ = "0.1.0"
 

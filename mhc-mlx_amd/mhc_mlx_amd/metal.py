@@ -14,6 +14,7 @@ from .ops import (  # noqa: F401
     stream_mix_add_hip_autograd as stream_mix_add_metal_autograd,
     suggest_threads_per_group,
 )
+from .tuning import _get_tuned_tpg  # noqa: F401
 
 __all__ = [
     "mhc_forward_fused_metal",
@@ -24,4 +25,5 @@ __all__ = [
     "stream_mix_add_metal",
     "stream_mix_add_metal_autograd",
     "suggest_threads_per_group",
+    "_get_tuned_tpg",
 ]

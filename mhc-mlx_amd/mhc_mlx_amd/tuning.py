@@ -1,0 +1,122 @@
+"""Tuning file: launch-shape choices measured on the GPU in use.
+
+The reference keeps a JSON file of per-kernel threadgroup sizes, read at
+import from ``mhc_tuning.json`` (working directory) and
+``~/.cache/mhc-mlx/tuning.json`` and queried with ``_get_tuned_tpg``
+(mhc_mlx/metal.py:21-36); ``scripts/tune.py`` writes it (tune.py:50-103).
+
+Here the same files are read the same way.  libmhc_hip chooses its
+launch shapes itself and exposes its tunable choices as environment
+variables that it reads at every launch (``MHC_RES_GRID`` and so on, listed
+in ``KNOBS``).  A tuning entry of this library maps an op name to the
+values of its knobs::
+
+    {"residual_add_agg": {"MHC_RES_GRID": -1}, "sinkhorn_16": {"MHC_SK16_CPL": 4}}
+
+Keys starting with ``_`` hold metadata (device, timings).
+``load()`` (run at import) exports such values, unless the variable is
+already set in the environment, so an explicit setting always wins.  Integer
+entries written for the reference (Metal threadgroup sizes) are kept for
+``_get_tuned_tpg`` and otherwise ignored.  ``python -m mhc_mlx_amd.tune``
+measures the candidates and writes the file.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+
+__all__ = ["KNOBS", "CONFIG_PATHS", "load", "apply", "tuning_config", "_get_tuned_tpg"]
+
+CONFIG_PATHS = [
+    "mhc_tuning.json",
+    os.path.join(os.path.expanduser("~"), ".cache", "mhc-mlx", "tuning.json"),
+]
+
+# op name -> (environment variable, candidate values).  The library reads each
+# variable at every launch; the first candidate is its built-in default.
+KNOBS: dict[str, tuple[str, list[int]]] = {
+    # workgroups per CU of the residual add + aggregate grid (-1: one item per thread)
+    "residual_add_agg": ("MHC_RES_GRID", [-1, 4, 8, 16]),
+    # workgroups per CU of the stream mix + add (post-combine) kernels
+    "stream_mix_add": ("MHC_MIX_FWD_GRID", [8, 16, 32, -1]),
+    "stream_mix_add_bwd": ("MHC_MIX_BWD_GRID", [8, 4, 16]),
+    # workgroups per CU of the MHCRewire pre-scale kernels
+    "stream_scale": ("MHC_SCALE_FWD_GRID", [8, 16, 32, -1]),
+    "stream_scale_bwd": ("MHC_SCALE_BWD_GRID", [8, 4, 16]),
+    # 128-channel slabs per wave of the n = 16 MFMA kernels
+    "mhc_fused_n16": ("MHC_FWD_SPW", [2, 1]),
+    "mhc_fused_bwd_n16": ("MHC_BWD_SPW", [2, 1]),
+    # columns per lane of the batched n = 16 Sinkhorn kernels
+    "sinkhorn_16": ("MHC_SK16_CPL", [4, 2]),
+    # persistent workgroups of the layer-wide backward (0: the library's choice)
+    "mhc_fused_bwd": ("MHC_BWD_GRID", [0, 512, 1024]),
+}
+
+_ENV_NAMES = {env for env, _ in KNOBS.values()}
+_TUNING_CONFIG: dict = {}
+
+
+def tuning_config() -> dict:
+    """The merged contents of the tuning files read so far."""
+    return dict(_TUNING_CONFIG)
+
+
+def apply(config: dict, override: bool = False) -> dict:
+    """Export the knob values of `config` ({op: {ENV: value}}); returns what was set.
+
+    A variable already present in the environment is left alone unless
+    `override` is true.  Unknown names and non-integer values raise
+    ValueError before anything is exported, so a corrupt file cannot pass
+    silently or apply in part.
+    """
+    values = {}
+    for op, entry in config.items():
+        if op.startswith("_") or not isinstance(entry, dict):
+            continue  # metadata, or a reference-format threadgroup size
+        for env, value in entry.items():
+            if env not in _ENV_NAMES:
+                raise ValueError(f"tuning entry {op!r}: unknown knob {env!r}")
+            if isinstance(value, bool) or not isinstance(value, int):
+                raise ValueError(f"tuning entry {op!r}: {env} must be an integer, got {value!r}")
+            values[env] = value
+    # all entries are valid: export them
+    done = {}
+    for env, value in values.items():
+        if override or env not in os.environ:
+            os.environ[env] = str(value)
+            done[env] = value
+    return done
+
+
+def load(paths: list[str] | None = None) -> dict:
+    """Read the tuning files (later files update earlier ones, as metal.py:28-33) and apply them.
+
+    Unreadable files are skipped, as the reference does; invalid knob entries
+    are reported with a warning and not applied.
+    """
+    merged = {}
+    for path in paths if paths is not None else CONFIG_PATHS:
+        if not os.path.exists(path):
+            continue
+        try:
+            with open(path) as f:
+                data = json.load(f)
+        except (OSError, ValueError):
+            continue
+        if isinstance(data, dict):
+            merged.update(data)
+    _TUNING_CONFIG.update(merged)
+    try:
+        apply(merged)
+    except ValueError as e:
+        import warnings
+
+        warnings.warn(f"mhc_mlx_amd: tuning file not applied: {e}")
+    return merged
+
+
+def _get_tuned_tpg(kernel_name: str, default: int) -> int:
+    """metal.py:35-36: the tuned threadgroup size of a kernel, or `default`."""
+    v = _TUNING_CONFIG.get(kernel_name, default)
+    return v if isinstance(v, int) and not isinstance(v, bool) else default
