@@ -498,7 +498,7 @@ size_t sk16_state_bytes(int64_t batch, int iters) {
 extern "C" size_t mhc_sinkhorn_bwd_workspace_bytes(int64_t batch, int n, int iters) {
   if (n < 1 || n > MHC_MAX_N || batch <= 0 || iters < 0) return 0;
   const size_t gen = plan_bwd(batch, n, iters, device_cu_count()).ws_bytes;
-  if (n == 16) return std::max(gen, sk16_state_bytes(batch, iters) + 16);
+  if (n == 16) return std::max(gen, sk16_state_bytes(batch, iters) + 256);
   return gen;
 }
 
@@ -513,9 +513,11 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
   MHC_CHECK_ARG(logits != nullptr && dM != nullptr && dlogits != nullptr, "null pointer argument");
   hipStream_t s = (hipStream_t)stream;
   if (use_sk16(n, logits, dM, dlogits) && workspace != nullptr) {
-    // the recorded state starts at the first 16-byte boundary of the workspace
+    // The recorded state starts at the first 256-byte boundary of the workspace:
+    // each matrix's records (256 bytes per iteration) then fill whole cache
+    // lines, none shared with a matrix that another wave or CU processes.
     const uintptr_t base = reinterpret_cast<uintptr_t>(workspace);
-    const size_t pad = (size_t)((16 - base % 16) % 16);
+    const size_t pad = (size_t)((256 - base % 256) % 256);
     const size_t need = sk16_state_bytes(batch, iters);
     if (workspace_bytes >= need + pad) {
       float* st = reinterpret_cast<float*>(base + pad);
