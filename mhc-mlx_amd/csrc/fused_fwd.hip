@@ -586,9 +586,12 @@ int launch_fwd_full(FwdArgs A, hipStream_t stream) {
   constexpr int V = FwdCfg<NMAX>::V;
   if (A.n != NMAX || !A.vec || A.C % V != 0) return 1;
   const int nchunks = A.C / V;
-  // Two chunks per thread stream best at large T; with fewer tokens than
-  // CUs (latency regime) each token is spread over twice the lanes.
-  int ch = (A.T < device_cu_count() || NMAX > 4) ? 1 : 2;
+  // One chunk per thread: the token's loads are split over the most lanes
+  // (config 2, 512-thread workgroups at 74 VGPRs: 355 us per launch against
+  // 380 us with two chunks per thread); two only when C needs them.
+  int ch = nchunks <= 64 * 16 ? 1 : 2;
+  const int ch_pref = env_int("MHC_FWD_CH", 0);
+  if (ch_pref == 1 || ch_pref == 2) ch = ch_pref;
   if (nchunks % (64 * ch) != 0) ch = 1;
   if (nchunks % 64 != 0 || nchunks / ch > 1024) return 1;
   const int tpb = nchunks / ch;

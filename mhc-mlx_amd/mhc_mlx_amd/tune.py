@@ -81,6 +81,10 @@ def workloads(scale: float = 1.0, dev="cuda"):
         out = ops.mhc_layer_forward_dynamic(x16, *p16, w16, output_dtype=bf)
         torch.autograd.grad(out, [x16] + p16 + [w16], d16)
 
+    def layer_fwd():
+        with torch.no_grad():
+            ops.mhc_layer_forward(xl, *pl, output_dtype=bf)
+
     def layer_step():
         out = ops.mhc_layer_forward(xl, *pl, output_dtype=bf)
         torch.autograd.grad(out, [xl] + pl, xl.detach())
@@ -94,6 +98,7 @@ def workloads(scale: float = 1.0, dev="cuda"):
         "mhc_fused_n16": n16_fwd,
         "mhc_fused_bwd_n16": n16_step,
         "sinkhorn_16": n16_step,
+        "mhc_fused": layer_fwd,
         "mhc_fused_bwd": layer_step,
     }
 

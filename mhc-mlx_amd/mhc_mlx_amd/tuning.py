@@ -49,6 +49,8 @@ KNOBS: dict[str, tuple[str, list[int]]] = {
     "mhc_fused_bwd_n16": ("MHC_BWD_SPW", [2, 1]),
     # columns per lane of the batched n = 16 Sinkhorn kernels
     "sinkhorn_16": ("MHC_SK16_CPL", [4, 2]),
+    # 8-channel chunks per thread of the layer-wide n <= 8 forward (1 unless C needs 2)
+    "mhc_fused": ("MHC_FWD_CH", [1, 2]),
     # persistent workgroups of the layer-wide backward (0: the library's choice)
     "mhc_fused_bwd": ("MHC_BWD_GRID", [0, 512, 1024]),
 }

@@ -27,6 +27,15 @@ def test_every_knob_has_its_default_first_and_distinct_envs():
         assert cands and len(cands) == len(set(cands)) and all(isinstance(c, int) for c in cands)
 
 
+def test_every_knob_is_read_by_the_library():
+    import pathlib
+
+    csrc = pathlib.Path(__file__).resolve().parents[1] / "mhc-mlx_amd" / "csrc"
+    text = "".join(p.read_text() for p in csrc.glob("*.hip"))
+    for env in KNOB_ENVS:
+        assert f'"{env}"' in text, env
+
+
 def test_load_exports_knobs_and_later_files_win(tmp_path, clean_env):
     a, b = tmp_path / "a.json", tmp_path / "b.json"
     a.write_text(json.dumps({"residual_add_agg": {"MHC_RES_GRID": 8}, "sinkhorn_16": {"MHC_SK16_CPL": 2}}))
