@@ -1098,19 +1098,8 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
         }
       }
       uint2 aa[3], ap[3];
-      {
-        uint32_t ha[4][3], hp[4][3];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          split3<XT>(av[k], ha[k]);
-          split3<XT>(pv[k], hp[k]);
-        }
-#pragma unroll
-        for (int e = 0; e < 3; ++e) {
-          aa[e] = make_uint2(ha[0][e] | (ha[1][e] << 16), ha[2][e] | (ha[3][e] << 16));
-          ap[e] = make_uint2(hp[0][e] | (hp[1][e] << 16), hp[2][e] | (hp[3][e] << 16));
-        }
-      }
+      split3x4<XT>(av, aa);
+      split3x4<XT>(pv, ap);
 #pragma unroll
       for (int s = 0; s < SPW; ++s) {
         uint16_t* sx = slab_lds + s * SLAB;
@@ -1186,11 +1175,7 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
     uint2 amt[3];
     {
       const float mv[4] = {m4.x, m4.y, m4.z, m4.w};
-      uint32_t hm[4][3];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) split3<XT>(mv[k], hm[k]);
-#pragma unroll
-      for (int e = 0; e < 3; ++e) amt[e] = make_uint2(hm[0][e] | (hm[1][e] << 16), hm[2][e] | (hm[3][e] << 16));
+      split3x4<XT>(mv, amt);
     }
     float dA[4] = {0.0f, 0.0f, 0.0f, 0.0f}, dP[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     XT* dxt = (XT*)A.dx + t * nC;
@@ -1219,6 +1204,7 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
           gr[k].w[0] = ug.x; gr[k].w[1] = ug.y; gr[k].w[2] = ug.z; gr[k].w[3] = ug.w;
         }
         uint32_t ow[4][4];
+        f32x4 even;  // dx of the even channel, packed with the odd one (one cvt per pair)
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           const int wd = v >> 1;
@@ -1230,10 +1216,11 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
           f32x4 acc = {av[0] * dyv[v], av[1] * dyv[v], av[2] * dyv[v], av[3] * dyv[v]};
 #pragma unroll
           for (int e = 2; e >= 0; --e) acc = mfma16<XT>(amt[e], bg, acc);
+          if (v & 1) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            if (v & 1) ow[k][wd] |= bits16<XT>(acc[k]) << 16;
-            else ow[k][wd] = bits16<XT>(acc[k]);
+            for (int k = 0; k < 4; ++k) ow[k][wd] = pack2<XT>(even[k], acc[k]);
+          } else {
+            even = acc;
           }
         }
 #pragma unroll

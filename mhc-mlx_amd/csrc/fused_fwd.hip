@@ -467,17 +467,8 @@ __global__ __launch_bounds__(SPW == 2 ? 512 : 1024) void fused_fwd_mfma16_kernel
     uint2 am[3], aa[3];
     {
       const float mv[4] = {m4.x, m4.y, m4.z, m4.w};
-      uint32_t hm[4][3], ha[4][3];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        split3<XT>(mv[k], hm[k]);
-        split3<XT>(av[k], ha[k]);
-      }
-#pragma unroll
-      for (int e = 0; e < 3; ++e) {
-        am[e] = make_uint2(hm[0][e] | (hm[1][e] << 16), hm[2][e] | (hm[3][e] << 16));
-        aa[e] = make_uint2(ha[0][e] | (ha[1][e] << 16), ha[2][e] | (ha[3][e] << 16));
-      }
+      split3x4<XT>(mv, am);
+      split3x4<XT>(av, aa);
     }
 
     // rms weight of the lane's channels, in flight with the tile

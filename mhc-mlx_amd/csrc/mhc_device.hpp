@@ -339,6 +339,26 @@ MHC_DEV void split3(float v, uint32_t (&h)[3]) {
   h[2] = bits16<T>(r2);
 }
 
+// split3 of four values as the three packed MFMA operands (terms e of
+// v[0..3], v[0] in the low half of .x): the same terms as split3, two values
+// per conversion instruction.
+template <typename T>
+MHC_DEV void split3x4(const float (&v)[4], uint2 (&out)[3]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float a = v[2 * h], b = v[2 * h + 1];
+    uint32_t w[3];
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+      w[e] = pack2<T>(a, b);
+      a -= lo16<T>(w[e]);
+      b -= hi16<T>(w[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 3; ++e) (h == 0 ? out[e].x : out[e].y) = w[e];
+  }
+}
+
 // Two packed words of 16-bit elements -> one word of their low (high)
 // halves, a's in the low half: element v of four streams becomes an MFMA
 // operand without leaving registers.
