@@ -82,10 +82,6 @@ MHC_DEV void bwd_stage_params(float* buf, const BwdArgs& A, int64_t t) {
   }
 }
 
-MHC_DEV float bwd_uniform(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
-}
-
 // Parameters either in uniform registers (small layer-wide n) or in LDS.
 template <int NMAX, bool LDS>
 struct ParView {
@@ -230,8 +226,8 @@ __global__ __launch_bounds__(1024) void fused_bwd_kernel(BwdArgs A) {
           pq = 2.0f * sigmoidf_(pq);
         }
       }
-      pv.as[i] = bwd_uniform(av);
-      pv.ps[i] = bwd_uniform(pq);
+      pv.as[i] = uniform_f(av);
+      pv.ps[i] = uniform_f(pq);
 #pragma unroll
       for (int j = 0; j < NMAX; ++j) pv.Ms[i * NMAX + j] = (i < n && j < n) ? A.M[i * n + j] : 0.0f;
     }
@@ -589,10 +585,10 @@ void fused_bwd_lw_kernel(BwdArgs A) {
         pq = 2.0f * sigmoidf_(pq);
       }
     }
-    as[i] = bwd_uniform(av);
-    ps[i] = bwd_uniform(pq);
+    as[i] = uniform_f(av);
+    ps[i] = uniform_f(pq);
 #pragma unroll
-    for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = bwd_uniform((i < n && j < n) ? A.M[i * n + j] : 0.0f);
+    for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = uniform_f((i < n && j < n) ? A.M[i * n + j] : 0.0f);
   }
 
   int c0[CHK], valid[CHK];
@@ -1352,20 +1348,20 @@ __global__ __launch_bounds__(kFinThreads) void param_finish_kernel(RedArgs R) {
   const bool act = c < end;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (act) {
+    // rows phase, phase + 4, ...: S <= 64 rows are 16 loads per thread, all
+    // in flight together, added as four fixed chains
     const float* src = R.part2 + c;
-    float4 a0 = v, a1 = v;
-    int k = phase;
-    for (; k + kFinPhases < R.S; k += 2 * kFinPhases) {
-      const float4 u0 = *reinterpret_cast<const float4*>(src + (int64_t)k * R.P);
-      const float4 u1 = *reinterpret_cast<const float4*>(src + (int64_t)(k + kFinPhases) * R.P);
-      a0 = make_float4(a0.x + u0.x, a0.y + u0.y, a0.z + u0.z, a0.w + u0.w);
-      a1 = make_float4(a1.x + u1.x, a1.y + u1.y, a1.z + u1.z, a1.w + u1.w);
+    float4 u[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int k = phase + m * kFinPhases;
+      u[m] = k < R.S ? *reinterpret_cast<const float4*>(src + (int64_t)k * R.P) : v;
     }
-    if (k < R.S) {
-      const float4 u0 = *reinterpret_cast<const float4*>(src + (int64_t)k * R.P);
-      a0 = make_float4(a0.x + u0.x, a0.y + u0.y, a0.z + u0.z, a0.w + u0.w);
-    }
-    v = make_float4(a0.x + a1.x, a0.y + a1.y, a0.z + a1.z, a0.w + a1.w);
+    for (int k = phase + 16 * kFinPhases; k < R.S; k += kFinPhases)
+      u[0] = f4add(u[0], *reinterpret_cast<const float4*>(src + (int64_t)k * R.P));
+#pragma unroll
+    for (int m = 4; m < 16; ++m) u[m & 3] = f4add(u[m & 3], u[m]);
+    v = f4add(f4add(u[0], u[1]), f4add(u[2], u[3]));
   }
   s_part[phase][col4] = v;
   __syncthreads();

@@ -71,10 +71,6 @@ MHC_DEV void fwd_stage_params(float* buf, const FwdArgs& A, int64_t t) {
   }
 }
 
-MHC_DEV float uniform_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
-}
-
 template <int NMAX, typename XT, typename OT, bool PT>
 __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
   constexpr int V = FwdCfg<NMAX>::V;

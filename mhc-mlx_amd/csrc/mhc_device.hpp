@@ -96,13 +96,20 @@ struct Vec {
   }
 
   // Vector load of V elements; p must be aligned to min(16, kBytes).  The
-  // activations are streamed once, so the loads carry the non-temporal hint.
+  // activations are streamed once, so loads of up to 16 bytes per lane carry
+  // the non-temporal hint.  Wider ones (a lane's 32 bytes as two 16-byte
+  // loads, so each instruction reads every other 16 bytes of the wave's
+  // span) stay cached: with the hint that pattern streams at 48% of HBM peak
+  // on gfx950, without it at 72% (1 GiB copy, read and write).
   MHC_DEV void load(const T* p) {
     const char* b = reinterpret_cast<const char*>(p);
     if constexpr (kBytes % 16 == 0) {
 #pragma unroll
       for (int k = 0; k < kBytes / 16; ++k) {
-        const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(b) + k);
+        const u32x4* a = reinterpret_cast<const u32x4*>(b) + k;
+        u32x4 u;
+        if constexpr (kBytes == 16) u = __builtin_nontemporal_load(a);
+        else u = *a;
         w[4 * k + 0] = u.x; w[4 * k + 1] = u.y; w[4 * k + 2] = u.z; w[4 * k + 3] = u.w;
       }
     } else if constexpr (kBytes == 8) {
@@ -143,8 +150,20 @@ MHC_DEV void st_nt(uint32_t* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) 
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+// A 16-byte word: non-temporal when the lane's whole span is this word,
+// cached when it is part of a wider span (see Vec::load).
+template <bool NT>
+MHC_DEV void st16(uint32_t* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  if constexpr (NT) {
+    st_nt(p, a, b, c, d);
+  } else {
+    const u32x4 v = {a, b, c, d};
+    *reinterpret_cast<u32x4*>(p) = v;
+  }
+}
+
 // Store V fp32 values as T; p aligned to min(16, V*sizeof(T)).  Streamed
-// outputs, so the stores carry the non-temporal hint.
+// outputs, so stores of up to 16 bytes per lane carry the non-temporal hint.
 template <typename T, int V>
 MHC_DEV void store_vec(T* p, const float (&v)[V]) {
   constexpr int kBytes = V * ElemTraits<T>::kBytes;
@@ -153,8 +172,9 @@ MHC_DEV void store_vec(T* p, const float (&v)[V]) {
     if constexpr (kBytes % 16 == 0) {
 #pragma unroll
       for (int k = 0; k < V / 4; ++k)
-        st_nt(b + 4 * k, __builtin_bit_cast(uint32_t, v[4 * k]), __builtin_bit_cast(uint32_t, v[4 * k + 1]),
-              __builtin_bit_cast(uint32_t, v[4 * k + 2]), __builtin_bit_cast(uint32_t, v[4 * k + 3]));
+        st16<kBytes == 16>(b + 4 * k, __builtin_bit_cast(uint32_t, v[4 * k]),
+                           __builtin_bit_cast(uint32_t, v[4 * k + 1]), __builtin_bit_cast(uint32_t, v[4 * k + 2]),
+                           __builtin_bit_cast(uint32_t, v[4 * k + 3]));
     } else if constexpr (kBytes == 8) {
       st_nt(b, __builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]));
     } else {
@@ -169,7 +189,8 @@ MHC_DEV void store_vec(T* p, const float (&v)[V]) {
       for (int k = 0; k < V / 2; ++k) wd[k] = pack2<T>(v[2 * k], v[2 * k + 1]);
       if constexpr (kBytes % 16 == 0) {
 #pragma unroll
-        for (int k = 0; k < kBytes / 16; ++k) st_nt(b + 4 * k, wd[4 * k], wd[4 * k + 1], wd[4 * k + 2], wd[4 * k + 3]);
+        for (int k = 0; k < kBytes / 16; ++k)
+          st16<kBytes == 16>(b + 4 * k, wd[4 * k], wd[4 * k + 1], wd[4 * k + 2], wd[4 * k + 3]);
       } else if constexpr (kBytes == 8) {
         st_nt(b, wd[0], wd[1]);
       } else {
@@ -184,6 +205,20 @@ MHC_DEV void store_partial(T* p, const float (&v)[V], int valid) {
 #pragma unroll
   for (int k = 0; k < V; ++k)
     if (k < valid) store1<T>(p + k, v[k]);
+}
+
+// Compiler-only fence: no instruction written before it is scheduled after
+// it or the other way round (keeps a work item's loads issued together,
+// ahead of the first wait, instead of interleaved with their uses).
+MHC_DEV void issue_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// A value every lane of the wave holds equally, moved to a scalar register
+// (parameters read by all lanes: one SGPR instead of one VGPR per value).
+MHC_DEV float uniform_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
 // --------------------------------------------------------------------------

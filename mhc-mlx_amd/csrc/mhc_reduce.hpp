@@ -10,7 +10,7 @@ namespace mhc {
 
 // part2[s][c] = sum over rows [s*rows, min(G, (s+1)*rows)) of part[row][c],
 // four columns per thread; P is a multiple of 4 and rows are 16-byte aligned.
-// Eight rows are loaded per step (enough loads in flight to cover HBM
+// Sixteen rows are loaded per step (enough loads in flight to cover HBM
 // latency) into four accumulators combined as (a0 + a1) + (a2 + a3): the
 // association is fixed by (G, rows) alone.
 MHC_REDUCE_INLINE float4 f4add(float4 a, float4 b) {
@@ -28,12 +28,14 @@ static __global__ __launch_bounds__(256) void reduce_rows_kernel(const float* __
   const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
   float4 a0 = z, a1 = z, a2 = z, a3 = z;
   int64_t g = g0;
-  for (; g + 8 <= g1; g += 8) {
-    float4 r[8];
+  for (; g + 16 <= g1; g += 16) {
+    float4 r[16];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) r[k] = *reinterpret_cast<const float4*>(src + (g + k) * P);
-    a0 = f4add(a0, r[0]); a1 = f4add(a1, r[1]); a2 = f4add(a2, r[2]); a3 = f4add(a3, r[3]);
-    a0 = f4add(a0, r[4]); a1 = f4add(a1, r[5]); a2 = f4add(a2, r[6]); a3 = f4add(a3, r[7]);
+    for (int k = 0; k < 16; ++k) r[k] = *reinterpret_cast<const float4*>(src + (g + k) * P);
+#pragma unroll
+    for (int k = 0; k < 16; k += 4) {
+      a0 = f4add(a0, r[k]); a1 = f4add(a1, r[k + 1]); a2 = f4add(a2, r[k + 2]); a3 = f4add(a3, r[k + 3]);
+    }
   }
   for (; g < g1; ++g) a0 = f4add(a0, *reinterpret_cast<const float4*>(src + g * P));
   *reinterpret_cast<float4*>(part2 + (int64_t)blockIdx.y * P + c4 * 4) = f4add(f4add(a0, a1), f4add(a2, a3));

@@ -22,9 +22,17 @@ namespace {
 constexpr int kMixThreads = 256;
 constexpr int kMixSplit = 64;
 
-template <int NMAX>
+// Channels per work item: 16 bytes per lane of the widest tensor for n <= 8
+// (8 channels when every tensor is 16-bit, 4 when one is fp32), so each
+// lane's access of any tensor is one coalesced load or store of at most 16 bytes.
+constexpr int mix_v(int nmax, int max_elem_bytes) {
+  return nmax == 0 ? 1 : (nmax <= 8 ? 16 / max_elem_bytes : 64 / nmax);
+}
+
+template <int NMAX, typename... Ts>
 struct MixCfg {
-  static constexpr int V = NMAX <= 8 ? 8 : 64 / NMAX;
+  static constexpr int kMaxBytes = std::max({ElemTraits<Ts>::kBytes...});
+  static constexpr int V = mix_v(NMAX, kMaxBytes);
 };
 
 struct MixArgs {
@@ -87,17 +95,83 @@ MHC_DEV void store_chunk(T* p, const float (&v)[V], bool vec, int valid) {
   else store_partial<T, V>(p, v, valid);
 }
 
-template <int NMAX, typename XT, typename YT, typename OT>
+// (token, chunk) of a grid-stride walk over T x nchunks items, advanced by
+// the fixed stride without a 64-bit division per item.
+struct ItemWalk {
+  int64_t t, dt;
+  int q, dq, nch;
+  MHC_DEV ItemWalk(int64_t first, int64_t stride, int nchunks) : nch(nchunks) {
+    t = first / nchunks;
+    q = (int)(first - t * nchunks);
+    dt = stride / nchunks;
+    dq = (int)(stride - dt * nchunks);
+  }
+  MHC_DEV void next() {
+    t += dt;
+    q += dq;
+    if (q >= nch) {
+      q -= nch;
+      ++t;
+    }
+  }
+};
+
+// FULL: n == NMAX, every chunk whole and 16-byte aligned, y present (and for
+// the VJP dy too, n <= 8): the item loop has no per-item conditions, so all
+// of an item's loads are issued together.
+template <int NMAX, typename XT, typename YT, typename OT, bool FULL>
 __global__ __launch_bounds__(kMixThreads) void mix_add_fwd_kernel(MixArgs A) {
-  constexpr int V = MixCfg<NMAX>::V;
+  constexpr int V = MixCfg<NMAX, XT, YT, OT>::V;
   __shared__ float s_par[NMAX * NMAX + 2 * NMAX];
   mix_stage<NMAX>(s_par, A);
   __syncthreads();
+  // n <= 4: Mf and p in scalar registers for the whole grid-stride loop
+  constexpr bool UREG = NMAX <= 4;
+  float mf[UREG ? NMAX * NMAX : 1], ps[UREG ? NMAX : 1];
+  if constexpr (UREG) {
+#pragma unroll
+    for (int k = 0; k < NMAX * NMAX; ++k) mf[k] = uniform_f(s_par[k]);
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) ps[i] = uniform_f(s_par[NMAX * NMAX + NMAX + i]);
+  }
+  auto mf_at = [&](int k) -> float {
+    if constexpr (UREG) return mf[k]; else return s_par[k];
+  };
+  auto p_at = [&](int i) -> float {
+    if constexpr (UREG) return ps[i]; else return s_par[NMAX * NMAX + NMAX + i];
+  };
   const int n = A.n, C = A.C;
   const int64_t items = A.T * A.nchunks;
-  const XT* X = (const XT*)A.x;
-  const YT* Y = (const YT*)A.y;
-  OT* O = (OT*)A.out;
+  const XT* __restrict__ X = (const XT*)A.x;
+  const YT* __restrict__ Y = (const YT*)A.y;
+  OT* __restrict__ O = (OT*)A.out;
+  if constexpr (FULL) {
+    for (ItemWalk w((int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x, A.nchunks);
+         w.t < A.T; w.next()) {
+      const int64_t base = w.t * NMAX * C + w.q * V;
+      Vec<XT, V> xr[NMAX];
+      Vec<YT, V> yr[NMAX];
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) {
+        xr[j].load(X + base + (int64_t)j * C);
+        yr[j].load(Y + base + (int64_t)j * C);
+      }
+      issue_fence();
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        float o[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int j = 0; j < NMAX; ++j) acc = fmaf(mf_at(i * NMAX + j), xr[j].get(v), acc);
+          o[v] = fmaf(p_at(i), yr[i].get(v), acc);
+        }
+        store_vec<OT, V>(O + base + (int64_t)i * C, o);
+      }
+    }
+    return;
+  }
   for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < items;
        item += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = item / A.nchunks;
@@ -105,26 +179,27 @@ __global__ __launch_bounds__(kMixThreads) void mix_add_fwd_kernel(MixArgs A) {
     const int c0 = q * V;
     const int valid = min(V, C - c0);
     const int64_t base = t * n * C + c0;
+    // every load of the item goes out before the first store
     Vec<XT, V> xr[NMAX];
+    Vec<YT, V> yr[NMAX];
 #pragma unroll
     for (int j = 0; j < NMAX; ++j) {
       if (j < n) load_chunk<XT, V>(xr[j], X + base + (int64_t)j * C, A.vec, valid);
       else xr[j].zero();
+      if (j < n && Y) load_chunk<YT, V>(yr[j], Y + base + (int64_t)j * C, A.vec, valid);
+      else yr[j].zero();
     }
 #pragma unroll
     for (int i = 0; i < NMAX; ++i) {
       if (i < n) {
-        Vec<YT, V> yr;
-        if (Y) load_chunk<YT, V>(yr, Y + base + (int64_t)i * C, A.vec, valid);
-        else yr.zero();
-        const float p = s_par[NMAX * NMAX + NMAX + i];
+        const float p = p_at(i);
         float o[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           float acc = 0.0f;
 #pragma unroll
-          for (int j = 0; j < NMAX; ++j) acc = fmaf(s_par[i * NMAX + j], xr[j].get(v), acc);
-          o[v] = fmaf(p, yr.get(v), acc);
+          for (int j = 0; j < NMAX; ++j) acc = fmaf(mf_at(i * NMAX + j), xr[j].get(v), acc);
+          o[v] = fmaf(p, yr[i].get(v), acc);
         }
         store_chunk<OT, V>(O + base + (int64_t)i * C, o, A.vec, valid);
       }
@@ -133,9 +208,9 @@ __global__ __launch_bounds__(kMixThreads) void mix_add_fwd_kernel(MixArgs A) {
 }
 
 // VJP of the post-combine.  Per-thread sums: S_ij (NMAX^2) then Yd_i (NMAX).
-template <int NMAX, typename XT, typename YT, typename GT>
+template <int NMAX, typename XT, typename YT, typename GT, bool FULL>
 __global__ __launch_bounds__(kMixThreads) void mix_add_bwd_kernel(MixArgs A) {
-  constexpr int V = MixCfg<NMAX>::V;
+  constexpr int V = MixCfg<NMAX, XT, YT, GT>::V;
   constexpr int K = NMAX * NMAX + NMAX;
   constexpr int NBLK = (K + 63) / 64;
   constexpr bool REG = NMAX <= 8;
@@ -143,14 +218,28 @@ __global__ __launch_bounds__(kMixThreads) void mix_add_bwd_kernel(MixArgs A) {
   __shared__ float s_stage[(kMixThreads / 64) * 64];
   mix_stage<NMAX>(s_par, A);
   __syncthreads();
+  constexpr bool UREG = NMAX <= 4;
+  float mf[UREG ? NMAX * NMAX : 1], ps[UREG ? NMAX : 1];
+  if constexpr (UREG) {
+#pragma unroll
+    for (int k = 0; k < NMAX * NMAX; ++k) mf[k] = uniform_f(s_par[k]);
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) ps[i] = uniform_f(s_par[NMAX * NMAX + NMAX + i]);
+  }
+  auto mf_at = [&](int k) -> float {
+    if constexpr (UREG) return mf[k]; else return s_par[k];
+  };
+  auto p_at = [&](int i) -> float {
+    if constexpr (UREG) return ps[i]; else return s_par[NMAX * NMAX + NMAX + i];
+  };
   const int lane = threadIdx.x & 63;
   const int n = A.n, C = A.C;
   const int64_t items = A.T * A.nchunks;
-  const XT* X = (const XT*)A.x;
-  const YT* Y = (const YT*)A.y;
-  const GT* Gd = (const GT*)A.g;
-  XT* DX = (XT*)A.out;
-  YT* DY = (YT*)A.dy;
+  const XT* __restrict__ X = (const XT*)A.x;
+  const YT* __restrict__ Y = (const YT*)A.y;
+  const GT* __restrict__ Gd = (const GT*)A.g;
+  XT* __restrict__ DX = (XT*)A.out;
+  YT* __restrict__ DY = (YT*)A.dy;
   // REG: full per-thread sums; else one lane-owned butterfly result per block
   float acc[REG ? 64 * NBLK : 1];
   float accL[NBLK];
@@ -158,7 +247,55 @@ __global__ __launch_bounds__(kMixThreads) void mix_add_bwd_kernel(MixArgs A) {
   for (int k = 0; k < (REG ? 64 * NBLK : 1); ++k) acc[k] = 0.0f;
 #pragma unroll
   for (int b = 0; b < NBLK; ++b) accL[b] = 0.0f;
-  const int64_t nitems_pad = ceil_div(items, (int64_t)gridDim.x * blockDim.x) * gridDim.x * blockDim.x;
+  static_assert(!FULL || REG, "the unconditional item loop keeps per-thread sums");
+  if constexpr (FULL) {
+    for (ItemWalk w((int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x, A.nchunks);
+         w.t < A.T; w.next()) {
+      const int64_t base = w.t * NMAX * C + w.q * V;
+      Vec<XT, V> xr[NMAX];
+      Vec<GT, V> gr[NMAX];
+      Vec<YT, V> yr[NMAX];
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) {
+        xr[j].load(X + base + (int64_t)j * C);
+        gr[j].load(Gd + base + (int64_t)j * C);
+        yr[j].load(Y + base + (int64_t)j * C);
+      }
+      issue_fence();
+      // dx_j = sum_i Mf_ij g_i, dy_i = p_i g_i
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) {
+        float o[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          float sum = 0.0f;
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) sum = fmaf(mf_at(i * NMAX + j), gr[i].get(v), sum);
+          o[v] = sum;
+        }
+        store_vec<XT, V>(DX + base + (int64_t)j * C, o);
+      }
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        float o[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) o[v] = p_at(i) * gr[i].get(v);
+        store_vec<YT, V>(DY + base + (int64_t)i * C, o);
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          const float gv = gr[i].get(v);
+#pragma unroll
+          for (int j = 0; j < NMAX; ++j) acc[i * NMAX + j] = fmaf(gv, xr[j].get(v), acc[i * NMAX + j]);
+          acc[NMAX * NMAX + i] = fmaf(gv, yr[i].get(v), acc[NMAX * NMAX + i]);
+        }
+      }
+    }
+  }
+  const int64_t nitems_pad =
+      FULL ? 0 : ceil_div(items, (int64_t)gridDim.x * blockDim.x) * gridDim.x * blockDim.x;
   for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < nitems_pad;
        item += (int64_t)gridDim.x * blockDim.x) {
     const bool act = item < items;
@@ -193,7 +330,7 @@ __global__ __launch_bounds__(kMixThreads) void mix_add_bwd_kernel(MixArgs A) {
           for (int v = 0; v < V; ++v) {
             float s = 0.0f;
 #pragma unroll
-            for (int i = 0; i < NMAX; ++i) s = fmaf(s_par[i * NMAX + j], gr[i].get(v), s);
+            for (int i = 0; i < NMAX; ++i) s = fmaf(mf_at(i * NMAX + j), gr[i].get(v), s);
             o[v] = s;
           }
           store_chunk<XT, V>(DX + base + (int64_t)j * C, o, A.vec, valid);
@@ -204,7 +341,7 @@ __global__ __launch_bounds__(kMixThreads) void mix_add_bwd_kernel(MixArgs A) {
 #pragma unroll
         for (int i = 0; i < NMAX; ++i) {
           if (i < n) {
-            const float p = s_par[NMAX * NMAX + NMAX + i];
+            const float p = p_at(i);
             float o[V];
 #pragma unroll
             for (int v = 0; v < V; ++v) o[v] = p * gr[i].get(v);
@@ -285,6 +422,19 @@ __global__ __launch_bounds__(kMixThreads) void mix_add_bwd_kernel(MixArgs A) {
   }
 }
 
+// Sums over the S <= 64 rows of part2 (row stride P) of columns
+// c0 .. c0 + 3 (those below K): row `lane` per lane, the four columns' loads
+// in flight together, then a fixed-order wave butterfly; every lane returns
+// the four sums.
+static_assert(kMixSplit <= 64, "col_sums4 takes one partial row per lane");
+MHC_DEV void col_sums4(const float* __restrict__ part2, int S, int P, int c0, int K, int lane,
+                       float (&v)[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (lane < S && c0 + e < K) ? part2[(int64_t)lane * P + c0 + e] : 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = wave_sum(v[e]);
+}
+
 // Final: sum S partial rows, then dM / dh_pre / dh_post (one block).
 __global__ __launch_bounds__(256) void mix_final_kernel(const float* __restrict__ part2, int S,
                                                         int P, int n, int h_mode,
@@ -296,10 +446,12 @@ __global__ __launch_bounds__(256) void mix_final_kernel(const float* __restrict_
                                                         float* __restrict__ dpost) {
   extern __shared__ float s_sum[];  // [n*n + n]: S then Yd
   const int K = n * n + n;
-  for (int c = threadIdx.x; c < K; c += blockDim.x) {
-    float s = 0.0f;
-    for (int k = 0; k < S; ++k) s += part2[(int64_t)k * P + c];
-    s_sum[c] = s;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  for (int c0 = 4 * wave; c0 < K; c0 += 4 * nwaves) {
+    float v[4];
+    col_sums4(part2, S, P, c0, K, lane, v);
+    if (lane == 0)
+      for (int e = 0; e < 4 && c0 + e < K; ++e) s_sum[c0 + e] = v[e];
   }
   __syncthreads();
   auto a_of = [&](int j) {
@@ -422,14 +574,22 @@ __global__ __launch_bounds__(64) void scale_final_kernel(const float* __restrict
                                                          int P, int n, int h_mode,
                                                          const float* __restrict__ hpre,
                                                          float* __restrict__ dpre) {
-  for (int j = threadIdx.x; j < n; j += blockDim.x) {
-    float s = 0.0f;
-    for (int k = 0; k < S; ++k) s += part2[(int64_t)k * P + j];
-    if (h_mode == MHC_H_RAW) {
-      const float a = sigmoidf_(hpre[j]);
-      s *= a * (1.0f - a);
+  const int lane = threadIdx.x & 63;
+  for (int c0 = 0; c0 < n; c0 += 4) {
+    float v[4];
+    col_sums4(part2, S, P, c0, n, lane, v);
+    if (lane < 4 && c0 + lane < n) {
+      const int j = c0 + lane;
+      float s = v[0];
+#pragma unroll
+      for (int e = 1; e < 4; ++e)
+        if (lane == e) s = v[e];
+      if (h_mode == MHC_H_RAW) {
+        const float a = sigmoidf_(hpre[j]);
+        s *= a * (1.0f - a);
+      }
+      dpre[j] = s;
     }
-    dpre[j] = s;
   }
 }
 
@@ -437,7 +597,11 @@ __global__ __launch_bounds__(64) void scale_final_kernel(const float* __restrict
 // host helpers
 // ---------------------------------------------------------------------------
 
-int mix_vec_width(int nmax) { return nmax == 0 ? 1 : (nmax <= 8 ? 8 : 64 / nmax); }
+int mix_vec_width(int nmax, std::initializer_list<int> dtype_sizes) {
+  int eb = 2;
+  for (int b : dtype_sizes) eb = std::max(eb, b);
+  return mix_v(nmax, eb);
+}
 
 // Grid of a grid-stride kernel over `work` items: at most `per_cu`
 // workgroups per CU (per_cu < 0: one item per thread, up to kMaxGrid).
@@ -523,7 +687,8 @@ extern "C" int mhc_stream_mix_add_fwd(const void* x, int x_dtype, const void* y,
   MixArgs A{};
   A.x = x; A.y = y; A.out = out; A.M = M; A.hpre = h_pre; A.hpost = h_post; A.T = T; A.n = n;
   A.C = C; A.h_mode = h_mode;
-  const int V = mix_vec_width(nmax_for(n));
+  const int V = mix_vec_width(nmax_for(n), {dtype_bytes(x_dtype), y ? dtype_bytes(y_dtype) : 2,
+                                            dtype_bytes(out_dtype)});
   A.nchunks = (int)ceil_div(C, V);
   A.vec = io_vec_ok(C, V, {{x, dtype_bytes(x_dtype)}, {y, y ? dtype_bytes(y_dtype) : 4},
                            {out, dtype_bytes(out_dtype)}});
@@ -544,8 +709,12 @@ extern "C" int mhc_stream_mix_add_fwd(const void* x, int x_dtype, const void* y,
         using YT = std::remove_pointer_t<decltype(yp)>;
         return by_pair<XT>(out_dtype, [&](auto* op) {
           using OT = std::remove_pointer_t<decltype(op)>;
-          hipLaunchKernelGGL((mix_add_fwd_kernel<NM, XT, YT, OT>), dim3((unsigned)blocks),
-                             dim3(kMixThreads), 0, s, A);
+          if (n == NM && A.vec && y)
+            hipLaunchKernelGGL((mix_add_fwd_kernel<NM, XT, YT, OT, true>), dim3((unsigned)blocks),
+                               dim3(kMixThreads), 0, s, A);
+          else
+            hipLaunchKernelGGL((mix_add_fwd_kernel<NM, XT, YT, OT, false>), dim3((unsigned)blocks),
+                               dim3(kMixThreads), 0, s, A);
           MHC_CHECK_LAUNCH("mix_add_fwd_kernel");
           return MHC_OK;
         });
@@ -556,7 +725,8 @@ extern "C" int mhc_stream_mix_add_fwd(const void* x, int x_dtype, const void* y,
 
 extern "C" size_t mhc_stream_mix_add_bwd_workspace_bytes(int64_t T, int n, int C) {
   if (T <= 0 || n < 1 || n > MHC_MAX_N || C < 1) return 0;
-  const int V = mix_vec_width(nmax_for(n));
+  // the narrowest item (fp32 operands) gives the most items and so the largest grid
+  const int V = mix_vec_width(nmax_for(n), {4});
   const int64_t G = mix_grid(T * ceil_div(C, V), device_cu_count(), "MHC_MIX_BWD_GRID", 8);
   return (size_t)(G + kMixSplit) * (size_t)mix_rows(n) * sizeof(float);
 }
@@ -579,7 +749,9 @@ extern "C" int mhc_stream_mix_add_bwd(const void* x, int x_dtype, const void* y,
   MHC_CHECK_ARG(dx_dtype == x_dtype, "dx_dtype must equal x_dtype");
   MHC_CHECK_ARG(!dy || !y || dy_dtype == y_dtype, "dy_dtype must equal y_dtype");
   MHC_CHECK_ARG(dtype_bytes(x_dtype) && dtype_bytes(dout_dtype), "unknown dtype code");
-  const int V = mix_vec_width(nmax_for(n));
+  const int ydt = y ? y_dtype : (dy ? dy_dtype : x_dtype);
+  MHC_CHECK_ARG(dtype_bytes(ydt), "unknown dtype code");
+  const int V = mix_vec_width(nmax_for(n), {dtype_bytes(x_dtype), dtype_bytes(ydt), dtype_bytes(dout_dtype)});
   const int nch = (int)ceil_div(C, V);
   const int64_t G = mix_grid(T * nch, device_cu_count(), "MHC_MIX_BWD_GRID", 8);
   const int P = mix_rows(n);
@@ -589,7 +761,6 @@ extern "C" int mhc_stream_mix_add_bwd(const void* x, int x_dtype, const void* y,
   MixArgs A{};
   A.x = x; A.y = y; A.g = dout; A.out = dx; A.dy = dy; A.M = M; A.hpre = h_pre; A.hpost = h_post;
   A.part = (float*)workspace; A.T = T; A.n = n; A.C = C; A.nchunks = nch; A.h_mode = h_mode; A.P = P;
-  const int ydt = y ? y_dtype : (dy ? dy_dtype : x_dtype);
   A.vec = io_vec_ok(C, V, {{x, dtype_bytes(x_dtype)}, {y, dtype_bytes(ydt)},
                            {dout, dtype_bytes(dout_dtype)}, {dy, dtype_bytes(ydt)}});
   hipStream_t s = (hipStream_t)stream;
@@ -608,7 +779,15 @@ extern "C" int mhc_stream_mix_add_bwd(const void* x, int x_dtype, const void* y,
         using YT = std::remove_pointer_t<decltype(yp)>;
         return by_pair<XT>(dout_dtype, [&](auto* gp) {
           using GT = std::remove_pointer_t<decltype(gp)>;
-          hipLaunchKernelGGL((mix_add_bwd_kernel<NM, XT, YT, GT>), dim3((unsigned)G),
+          if constexpr (NM <= 8) {
+            if (n == NM && A.vec && y && dy) {
+              hipLaunchKernelGGL((mix_add_bwd_kernel<NM, XT, YT, GT, true>), dim3((unsigned)G),
+                                 dim3(kMixThreads), 0, s, A);
+              MHC_CHECK_LAUNCH("mix_add_bwd_kernel");
+              return MHC_OK;
+            }
+          }
+          hipLaunchKernelGGL((mix_add_bwd_kernel<NM, XT, YT, GT, false>), dim3((unsigned)G),
                              dim3(kMixThreads), 0, s, A);
           MHC_CHECK_LAUNCH("mix_add_bwd_kernel");
           return MHC_OK;
