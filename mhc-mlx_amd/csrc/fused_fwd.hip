@@ -304,9 +304,17 @@ __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
 #define MHC_FWD_FULL_ATTR
 #endif
 
+// Channels per chunk of the full-tile kernel: 16 bytes per lane of the wider
+// of x and out (8 channels for 16-bit I/O, 4 with an fp32 side), so every
+// load and store is one coalesced access of at most 16 bytes per lane.
+template <typename XT, typename OT>
+constexpr int full_vec() {
+  return 16 / (ElemTraits<XT>::kBytes > ElemTraits<OT>::kBytes ? ElemTraits<XT>::kBytes : ElemTraits<OT>::kBytes);
+}
+
 template <int NMAX, typename XT, typename OT, int CH, bool RAW, bool SKF = false>
 __global__ __launch_bounds__(1024) MHC_FWD_FULL_ATTR void fused_fwd_full_kernel(FwdArgs A) {
-  constexpr int V = FwdCfg<NMAX>::V;
+  constexpr int V = full_vec<XT, OT>();
   __shared__ float s_red[2][16];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -570,13 +578,15 @@ int launch_fwd_mfma16(FwdArgs A, hipStream_t stream) {
 // is not covered (the caller then uses fused_fwd_kernel).
 template <int NMAX, typename XT, typename OT>
 int launch_fwd_full(FwdArgs A, hipStream_t stream) {
-  constexpr int V = FwdCfg<NMAX>::V;
+  // A.vec (checked for 8-channel chunks) implies the alignment of narrower ones
+  constexpr int V = full_vec<XT, OT>();
   if (A.n != NMAX || !A.vec || A.C % V != 0) return 1;
   const int nchunks = A.C / V;
-  // One chunk per thread: the token's loads are split over the most lanes
-  // (config 2, 512-thread workgroups at 74 VGPRs: 355 us per launch against
-  // 380 us with two chunks per thread); two only when C needs them.
-  int ch = nchunks <= 64 * 16 ? 1 : 2;
+  // Workgroups of at most 512 threads, one chunk per thread where that fits:
+  // at 32768 tokens x 4 x 4096, bf16 -> bf16 (8-channel chunks) runs 355 us
+  // with one chunk per thread against 380 us with two; bf16 -> fp32
+  // (4-channel chunks) 566 us with two against 625 us with one (1024 threads).
+  int ch = nchunks <= 512 ? 1 : 2;
   const int ch_pref = env_int("MHC_FWD_CH", 0);
   if (ch_pref == 1 || ch_pref == 2) ch = ch_pref;
   if (nchunks % (64 * ch) != 0) ch = 1;
@@ -705,7 +715,7 @@ namespace {
 // instead of a launch of its own.  Returns 1 when the shape is not covered.
 template <int NMAX, typename XT, typename OT>
 int launch_fwd_full_skf(FwdArgs A, hipStream_t stream) {
-  constexpr int V = FwdCfg<NMAX>::V;
+  constexpr int V = full_vec<XT, OT>();
   if (A.n != NMAX || !A.vec || A.C % V != 0) return 1;
   const int nchunks = A.C / V;
   if (nchunks % 64 != 0 || nchunks > 1024) return 1;
