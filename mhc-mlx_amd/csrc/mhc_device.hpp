@@ -163,16 +163,20 @@ MHC_DEV void st16(uint32_t* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
 }
 
 // Store V fp32 values as T; p aligned to min(16, V*sizeof(T)).  Streamed
-// outputs, so stores of up to 16 bytes per lane carry the non-temporal hint.
-template <typename T, int V>
+// outputs, so stores of up to 16 bytes per lane carry the non-temporal hint;
+// wider ones too when NT_WIDE (a kernel where that output is a small share
+// of the traffic: residual_add_agg's fp32 y_agg runs 645 us with the hint,
+// 663 us without, at 32768 x 4 x 4096).
+template <typename T, int V, bool NT_WIDE = false>
 MHC_DEV void store_vec(T* p, const float (&v)[V]) {
   constexpr int kBytes = V * ElemTraits<T>::kBytes;
+  constexpr bool kNT = kBytes == 16 || NT_WIDE;
   uint32_t* b = reinterpret_cast<uint32_t*>(p);
   if constexpr (ElemTraits<T>::kBytes == 4) {
     if constexpr (kBytes % 16 == 0) {
 #pragma unroll
       for (int k = 0; k < V / 4; ++k)
-        st16<kBytes == 16>(b + 4 * k, __builtin_bit_cast(uint32_t, v[4 * k]),
+        st16<kNT>(b + 4 * k, __builtin_bit_cast(uint32_t, v[4 * k]),
                            __builtin_bit_cast(uint32_t, v[4 * k + 1]), __builtin_bit_cast(uint32_t, v[4 * k + 2]),
                            __builtin_bit_cast(uint32_t, v[4 * k + 3]));
     } else if constexpr (kBytes == 8) {
@@ -190,7 +194,7 @@ MHC_DEV void store_vec(T* p, const float (&v)[V]) {
       if constexpr (kBytes % 16 == 0) {
 #pragma unroll
         for (int k = 0; k < kBytes / 16; ++k)
-          st16<kBytes == 16>(b + 4 * k, wd[4 * k], wd[4 * k + 1], wd[4 * k + 2], wd[4 * k + 3]);
+          st16<kNT>(b + 4 * k, wd[4 * k], wd[4 * k + 1], wd[4 * k + 2], wd[4 * k + 3]);
       } else if constexpr (kBytes == 8) {
         st_nt(b, wd[0], wd[1]);
       } else {

@@ -58,7 +58,7 @@ MHC_DEV void load_c(Vec<T, kResV>& r, const T* p, bool vec, int valid) {
 
 template <typename T>
 MHC_DEV void store_c(T* p, const float (&v)[kResV], bool vec, int valid) {
-  if (vec && valid == kResV) store_vec<T, kResV>(p, v);
+  if (vec && valid == kResV) store_vec<T, kResV, true>(p, v);
   else store_partial<T, kResV>(p, v, valid);
 }
 
