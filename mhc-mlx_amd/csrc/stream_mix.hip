@@ -490,7 +490,11 @@ __global__ __launch_bounds__(256) void mix_final_kernel(const float* __restrict_
 
 // pre-scale forward: out_i = a_i x_i.  grid.y = stream i; x dimension over
 // (token, chunk of 8 channels).
-template <typename XT, typename OT>
+// FULL (every chunk whole and 16-byte aligned): kScaleU items per thread per
+// step, their loads issued together ahead of their stores.
+constexpr int kScaleU = 4;
+
+template <typename XT, typename OT, bool FULL>
 __global__ __launch_bounds__(kMixThreads) void scale_fwd_kernel(MixArgs A) {
   constexpr int V = 8;
   const int i = blockIdx.y;
@@ -498,8 +502,33 @@ __global__ __launch_bounds__(kMixThreads) void scale_fwd_kernel(MixArgs A) {
   const float a = A.h_mode == MHC_H_RAW ? sigmoidf_(hv) : hv;
   const int n = A.n, C = A.C;
   const int64_t items = A.T * A.nchunks;
-  const XT* X = (const XT*)A.x;
-  OT* O = (OT*)A.out;
+  const XT* __restrict__ X = (const XT*)A.x;
+  OT* __restrict__ O = (OT*)A.out;
+  if constexpr (FULL) {
+    ItemWalk w((int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x, A.nchunks);
+    while (w.t < A.T) {
+      int64_t off[kScaleU];
+      bool on[kScaleU];
+      Vec<XT, V> xr[kScaleU];
+#pragma unroll
+      for (int u = 0; u < kScaleU; ++u) {
+        on[u] = w.t < A.T;
+        off[u] = on[u] ? (w.t * n + i) * C + w.q * V : 0;
+        if (on[u]) xr[u].load(X + off[u]);
+        w.next();
+      }
+      issue_fence();
+#pragma unroll
+      for (int u = 0; u < kScaleU; ++u) {
+        if (!on[u]) continue;
+        float o[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) o[v] = a * xr[u].get(v);
+        store_vec<OT, V>(O + off[u], o);
+      }
+    }
+    return;
+  }
   for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < items;
        item += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = item / A.nchunks;
@@ -518,7 +547,7 @@ __global__ __launch_bounds__(kMixThreads) void scale_fwd_kernel(MixArgs A) {
 
 // pre-scale VJP: dx_i = a_i g_i (+ acc), Sa_i = sum g_i x_i.  grid.y = stream
 // i; block (bx, i) writes column i of partial row bx.
-template <typename XT, typename GT>
+template <typename XT, typename GT, bool FULL>
 __global__ __launch_bounds__(kMixThreads) void scale_bwd_kernel(MixArgs A) {
   constexpr int V = 8;
   __shared__ float s_stage[kMixThreads / 64];
@@ -527,12 +556,47 @@ __global__ __launch_bounds__(kMixThreads) void scale_bwd_kernel(MixArgs A) {
   const float a = A.h_mode == MHC_H_RAW ? sigmoidf_(hv) : hv;
   const int n = A.n, C = A.C;
   const int64_t items = A.T * A.nchunks;
-  const XT* X = (const XT*)A.x;
-  const GT* Gd = (const GT*)A.g;
-  const XT* ACC = (const XT*)A.acc;
-  XT* DX = (XT*)A.out;
+  const XT* __restrict__ X = (const XT*)A.x;
+  const GT* __restrict__ Gd = (const GT*)A.g;
+  const XT* __restrict__ ACC = (const XT*)A.acc;
+  XT* __restrict__ DX = (XT*)A.out;
   float acc = 0.0f;
-  for (int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < items;
+  if constexpr (FULL) {
+    // the dx accumulator (ACC) is absent on this path
+    ItemWalk w((int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x, A.nchunks);
+    while (w.t < A.T) {
+      int64_t off[kScaleU];
+      bool on[kScaleU];
+      Vec<XT, V> xr[kScaleU];
+      Vec<GT, V> gr[kScaleU];
+#pragma unroll
+      for (int u = 0; u < kScaleU; ++u) {
+        on[u] = w.t < A.T;
+        off[u] = on[u] ? (w.t * n + i) * C + w.q * V : 0;
+        if (on[u]) {
+          xr[u].load(X + off[u]);
+          gr[u].load(Gd + off[u]);
+        } else {
+          xr[u].zero();
+          gr[u].zero();
+        }
+        w.next();
+      }
+      issue_fence();
+#pragma unroll
+      for (int u = 0; u < kScaleU; ++u) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc = fmaf(gr[u].get(v), xr[u].get(v), acc);
+        if (!on[u]) continue;
+        float o[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) o[v] = a * gr[u].get(v);
+        store_vec<XT, V>(DX + off[u], o);
+      }
+    }
+  }
+  // general path (FULL: nothing left)
+  for (int64_t item = FULL ? items : (int64_t)blockIdx.x * blockDim.x + threadIdx.x; item < items;
        item += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = item / A.nchunks;
     const int q = (int)(item - t * A.nchunks);
@@ -829,8 +893,12 @@ extern "C" int mhc_stream_scale_fwd(const void* x, int x_dtype, const float* h_p
     using XT = std::remove_pointer_t<decltype(xp)>;
     return by_pair<XT>(out_dtype, [&](auto* op) {
       using OT = std::remove_pointer_t<decltype(op)>;
-      hipLaunchKernelGGL((scale_fwd_kernel<XT, OT>), dim3((unsigned)bx, (unsigned)n), dim3(kMixThreads),
-                         0, s, A);
+      if (A.vec)
+        hipLaunchKernelGGL((scale_fwd_kernel<XT, OT, true>), dim3((unsigned)bx, (unsigned)n),
+                           dim3(kMixThreads), 0, s, A);
+      else
+        hipLaunchKernelGGL((scale_fwd_kernel<XT, OT, false>), dim3((unsigned)bx, (unsigned)n),
+                           dim3(kMixThreads), 0, s, A);
       MHC_CHECK_LAUNCH("scale_fwd_kernel");
       return MHC_OK;
     });
@@ -875,8 +943,12 @@ extern "C" int mhc_stream_scale_bwd(const void* x, int x_dtype, const void* dout
     using XT = std::remove_pointer_t<decltype(xp)>;
     return by_pair<XT>(dout_dtype, [&](auto* gp) {
       using GT = std::remove_pointer_t<decltype(gp)>;
-      hipLaunchKernelGGL((scale_bwd_kernel<XT, GT>), dim3((unsigned)G, (unsigned)n), dim3(kMixThreads),
-                         0, s, A);
+      if (A.vec && !dx_accum)
+        hipLaunchKernelGGL((scale_bwd_kernel<XT, GT, true>), dim3((unsigned)G, (unsigned)n),
+                           dim3(kMixThreads), 0, s, A);
+      else
+        hipLaunchKernelGGL((scale_bwd_kernel<XT, GT, false>), dim3((unsigned)G, (unsigned)n),
+                           dim3(kMixThreads), 0, s, A);
       MHC_CHECK_LAUNCH("scale_bwd_kernel");
       return MHC_OK;
     });
