@@ -39,6 +39,62 @@ def test_post_combine_matches_oracle(B, n, C, xdt):
         assert rel_err(got, r) < tol, (name, B, n, C, xdt, rel_err(got, r))
 
 
+@pytest.mark.parametrize("gdt", ["bf16", "f32"])
+def test_post_combine_bf16_with_bf16_or_fp32_grad(gdt):
+    """bf16 x and y with a bf16 gradient (8-channel items) or an fp32 one (4-channel items)."""
+    B, n, C = 5, 4, 256
+    g = rng(47)
+    x = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    y = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    dout = to_dtype_np(g.standard_normal((B, n, C)), gdt)
+    hpre, hpost, hres, _ = params(g, n, C)
+    xt = dev_tensor(x, "bf16").requires_grad_(True)
+    yt = dev_tensor(y, "bf16").requires_grad_(True)
+    ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres)]
+    out = ops.post_combine(xt, yt, *ps, sinkhorn_iters=20, eps=1e-5)
+    out.backward(dev_tensor(dout, gdt))
+    refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    gots = [np_of(xt.grad), np_of(yt.grad)] + [np_of(t.grad) for t in ps]
+    for name, got, r in zip(["dx", "dy", "dH_pre", "dH_post", "dH_res"], gots, refs):
+        tol = 2e-2 if name in ("dx", "dy") else 1e-4
+        assert rel_err(got, r) < tol, (name, gdt, rel_err(got, r))
+
+
+@pytest.mark.parametrize("gdt", ["bf16", "f32"])
+def test_rewire_kernels_walk_several_items_per_thread(monkeypatch, gdt):
+    """One workgroup per CU: each thread walks many (token, chunk) items and, with three
+    chunks per token (C = 24), the chunk index wraps between the items of a thread."""
+    for env in ("MHC_MIX_FWD_GRID", "MHC_MIX_BWD_GRID", "MHC_SCALE_FWD_GRID", "MHC_SCALE_BWD_GRID"):
+        monkeypatch.setenv(env, "1")
+    B, n, C = 30000, 4, 24
+    g = rng(48)
+    x = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    y = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    dout = to_dtype_np(g.standard_normal((B, n, C)), gdt)
+    hpre, hpost, hres, _ = params(g, n, C)
+    xt = dev_tensor(x, "bf16").requires_grad_(True)
+    yt = dev_tensor(y, "bf16").requires_grad_(True)
+    ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres)]
+    out = ops.post_combine(xt, yt, *ps, sinkhorn_iters=20, eps=1e-5)
+    assert rel_err(np_of(out), O.post_combine(x, y, hpre, hpost, hres, 20, 1e-5)) < 1e-5
+    out.backward(dev_tensor(dout, gdt))
+    refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    gots = [np_of(xt.grad), np_of(yt.grad)] + [np_of(t.grad) for t in ps]
+    for name, got, r in zip(["dx", "dy", "dH_pre", "dH_post", "dH_res"], gots, refs):
+        tol = 2e-2 if name in ("dx", "dy") else 1e-4
+        assert rel_err(got, r) < tol, (name, gdt, rel_err(got, r))
+    # pre-scale on the same walk
+    ht = dev_tensor(hpre).requires_grad_(True)
+    xs = dev_tensor(x, "bf16").requires_grad_(True)
+    sc = ops.stream_scale(xs, ht)
+    a = O.sigmoid(hpre)
+    assert rel_err(np_of(sc), x * a[None, :, None]) < 1e-2
+    sc.backward(dev_tensor(dout, "bf16"))
+    d16 = to_dtype_np(dout, "bf16").astype(np.float64)
+    assert rel_err(np_of(xs.grad), d16 * a[None, :, None]) < 1e-2
+    assert rel_err(np_of(ht.grad), np.einsum("bic,bic->i", d16, x) * a * (1 - a)) < 1e-4
+
+
 @pytest.mark.parametrize("n,C", [(4, 64), (16, 16), (32, 8), (3, 9)])
 def test_stream_mix_add_matches_reference_semantics(n, C):
     """stream_mix_add_metal: out = M x + y_dist (fp32); VJP dx = M^T g, dM = sum g x^T, dy = g."""
