@@ -76,6 +76,29 @@ int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlogits, int64
                      int n, int iters, float eps, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* Recorded state: the forward keeps what the VJP would otherwise recompute
+ * (per iteration the cumulative row/column scales and the row/column sums,
+ * 256 bytes per matrix).  This splits _sinkhorn_autograd_fn's forward and
+ * VJP (metal.py:2712-2758) the way an autograd function saves tensors for
+ * backward; the results are those of mhc_sinkhorn_fwd / mhc_sinkhorn_bwd.
+ *
+ * Bytes of the state buffer for this shape; 0 when no recorded path exists
+ * (n != 16, or the n == 16 kernels are switched off with MHC_SK16=0): then
+ * use mhc_sinkhorn_fwd / mhc_sinkhorn_bwd. */
+size_t mhc_sinkhorn_state_bytes(int64_t batch, int n, int iters);
+
+/* mhc_sinkhorn_fwd that also writes the state to `state` (state_bytes >=
+ * mhc_sinkhorn_state_bytes; logits and M 16-byte aligned). */
+int mhc_sinkhorn_fwd_record(const float* logits, float* M, void* state, size_t state_bytes,
+                            int64_t batch, int n, int iters, float eps, void* stream);
+
+/* mhc_sinkhorn_bwd from the state mhc_sinkhorn_fwd_record wrote for the same
+ * logits, iters and eps (no forward recompute, no workspace).  dM may alias
+ * dlogits. */
+int mhc_sinkhorn_bwd_recorded(const float* logits, const float* dM, float* dlogits,
+                              const void* state, size_t state_bytes, int64_t batch, int n,
+                              int iters, float eps, void* stream);
+
 /* --------------------------------------------------------------------- */
 /* Fused mHC forward: aggregate + RMSNorm + stream mix + H_post add         */
 /* --------------------------------------------------------------------- */

@@ -178,17 +178,70 @@ MHC_DEV int64_t sk16_matrix(int& p) {
   return ((int64_t)blockIdx.x * (kSk16Threads / 64) + (threadIdx.x >> 6)) * Sk16<CPL>::MPW + lane / LPM;
 }
 
+// The forward iterations on P, recording per iteration k the cumulative row
+// scales R_k and row sums rs_k (rows RPL*p ..) and the cumulative column
+// scales C_k and column sums cs_k (columns CPL*p ..) at sm + 64 k (when
+// mvalid).  P ends as M, bitwise the same as without recording.
 template <int CPL>
+MHC_DEV void sk16_forward_record(float (&P)[16][CPL], int iters, float eps, int p, bool mvalid, float* sm) {
+  constexpr int LPM = Sk16<CPL>::LPM;
+  constexpr int RPL = Sk16<CPL>::RPL;
+  float R[16], Cc[CPL];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) R[i] = 1.0f;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) Cc[e] = 1.0f;
+  for (int it = 0; it < iters; ++it) {
+    float rs[16], cs[CPL];
+    sk16_iter<CPL>(P, eps,
+                   [&](int i, float sum, float rsc) {
+                     rs[i] = sum;
+                     R[i] *= rsc;
+                   },
+                   [&](int e, float sum, float csc) {
+                     cs[e] = sum;
+                     Cc[e] *= csc;
+                   });
+    if (mvalid) {
+      float* sk = sm + (int64_t)it * 64;
+      float r4[RPL], s4[RPL];
+#pragma unroll
+      for (int k = 0; k < RPL; ++k) {
+        float rv = R[k], sv = rs[k];
+#pragma unroll
+        for (int q = 1; q < LPM; ++q)
+          if (p == q) {
+            rv = R[RPL * q + k];
+            sv = rs[RPL * q + k];
+          }
+        r4[k] = rv;
+        s4[k] = sv;
+      }
+      sk16_st<RPL>(sk + RPL * p, r4);
+      sk16_st<RPL>(sk + 16 + RPL * p, s4);
+      sk16_st<CPL>(sk + 32 + CPL * p, Cc);
+      sk16_st<CPL>(sk + 48 + CPL * p, cs);
+    }
+  }
+}
+
+// REC: also record the VJP state ([batch][iters][4][16] floats at st) for
+// sinkhorn16_bwd_kernel<CPL', true>.
+template <int CPL, bool REC>
 __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_fwd_kernel(const float* __restrict__ logits,
                                                                       float* __restrict__ out, int64_t batch,
-                                                                      int iters, float eps) {
+                                                                      int iters, float eps, float* __restrict__ st) {
   int p;
   const int64_t m = sk16_matrix<CPL>(p);
   const bool mvalid = m < batch;
   float P[16][CPL];
   sk16_load_k<CPL>(logits + (mvalid ? m : 0) * 256, mvalid, p, P);
-  for (int it = 0; it < iters; ++it)
-    sk16_iter<CPL>(P, eps, [](int, float, float) {}, [](int, float, float) {});
+  if constexpr (REC) {
+    sk16_forward_record<CPL>(P, iters, eps, p, mvalid, st + (mvalid ? m : 0) * (int64_t)iters * 64);
+  } else {
+    for (int it = 0; it < iters; ++it)
+      sk16_iter<CPL>(P, eps, [](int, float, float) {}, [](int, float, float) {});
+  }
   if (mvalid) {
     float* O = out + m * 256;
 #pragma unroll
@@ -197,13 +250,14 @@ __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_fwd_kernel(const floa
 }
 
 // st: [batch][iters][4][16] floats (R_k, rs_k, C_k, cs_k).  dM may alias dlogits.
-template <int CPL>
+// RECORDED: st was written by sinkhorn16_fwd_kernel<CPL', true> for the same
+// logits; otherwise the forward is recomputed here and recorded first.
+template <int CPL, bool RECORDED>
 __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_bwd_kernel(const float* __restrict__ logits,
                                                                       const float* dM, float* dlogits,
                                                                       int64_t batch, int iters, float eps,
                                                                       float* __restrict__ st) {
   constexpr int LPM = Sk16<CPL>::LPM;
-  constexpr int RPL = Sk16<CPL>::RPL;
   int p;
   const int64_t m = sk16_matrix<CPL>(p);
   const bool mvalid = m < batch;
@@ -212,54 +266,17 @@ __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_bwd_kernel(const floa
   sk16_load_k<CPL>(logits + mm * 256, mvalid, p, K);
   float* sm = st + mm * (int64_t)iters * 64;
 
-  // forward recompute, recording R_k, rs_k (rows RPL*p ..) and C_k, cs_k (columns CPL*p ..)
-  {
+  if constexpr (!RECORDED) {
     float P[16][CPL];
 #pragma unroll
     for (int i = 0; i < 16; ++i)
 #pragma unroll
       for (int e = 0; e < CPL; ++e) P[i][e] = K[i][e];
-    float R[16], Cc[CPL];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) R[i] = 1.0f;
-#pragma unroll
-    for (int e = 0; e < CPL; ++e) Cc[e] = 1.0f;
-    for (int it = 0; it < iters; ++it) {
-      float rs[16], cs[CPL];
-      sk16_iter<CPL>(P, eps,
-                     [&](int i, float s, float rsc) {
-                       rs[i] = s;
-                       R[i] *= rsc;
-                     },
-                     [&](int e, float s, float csc) {
-                       cs[e] = s;
-                       Cc[e] *= csc;
-                     });
-      if (mvalid) {
-        float* sk = sm + (int64_t)it * 64;
-        float r4[RPL], s4[RPL];
-#pragma unroll
-        for (int k = 0; k < RPL; ++k) {
-          float rv = R[k], sv = rs[k];
-#pragma unroll
-          for (int q = 1; q < LPM; ++q)
-            if (p == q) {
-              rv = R[RPL * q + k];
-              sv = rs[RPL * q + k];
-            }
-          r4[k] = rv;
-          s4[k] = sv;
-        }
-        sk16_st<RPL>(sk + RPL * p, r4);
-        sk16_st<RPL>(sk + 16 + RPL * p, s4);
-        sk16_st<CPL>(sk + 32 + CPL * p, Cc);
-        sk16_st<CPL>(sk + 48 + CPL * p, cs);
-      }
-    }
+    sk16_forward_record<CPL>(P, iters, eps, p, mvalid, sm);
+    // the state written by the other lanes of the matrix is read below
+    __builtin_amdgcn_s_waitcnt(0);
+    __threadfence_block();
   }
-  // the state written by the other lanes of the matrix is read below
-  __builtin_amdgcn_s_waitcnt(0);
-  __threadfence_block();
 
   float G[16][CPL];
 #pragma unroll
@@ -470,8 +487,10 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
   if (use_sk16(n, logits, M, nullptr)) {
     const int cpl = sk16_cpl();
     const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
-    if (cpl == 4) hipLaunchKernelGGL(sinkhorn16_fwd_kernel<4>, g, b, 0, s, logits, M, batch, iters, eps);
-    else hipLaunchKernelGGL(sinkhorn16_fwd_kernel<2>, g, b, 0, s, logits, M, batch, iters, eps);
+    if (cpl == 4)
+      hipLaunchKernelGGL((sinkhorn16_fwd_kernel<4, false>), g, b, 0, s, logits, M, batch, iters, eps, nullptr);
+    else
+      hipLaunchKernelGGL((sinkhorn16_fwd_kernel<2, false>), g, b, 0, s, logits, M, batch, iters, eps, nullptr);
     MHC_CHECK_LAUNCH("sinkhorn16_fwd_kernel");
     return MHC_OK;
   }
@@ -524,9 +543,11 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
       const int cpl = sk16_cpl();
       const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
       if (cpl == 4)
-        hipLaunchKernelGGL(sinkhorn16_bwd_kernel<4>, g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);
+        hipLaunchKernelGGL((sinkhorn16_bwd_kernel<4, false>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps,
+                           st);
       else
-        hipLaunchKernelGGL(sinkhorn16_bwd_kernel<2>, g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);
+        hipLaunchKernelGGL((sinkhorn16_bwd_kernel<2, false>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps,
+                           st);
       MHC_CHECK_LAUNCH("sinkhorn16_bwd_kernel");
       return MHC_OK;
     }
@@ -546,5 +567,73 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
     default: launch_bwd<64>(p, logits, dM, dlogits, batch, n, iters, eps, ws, s); break;
   }
   MHC_CHECK_LAUNCH("sinkhorn_bwd_kernel");
+  return MHC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Recorded state: the forward keeps what the VJP would otherwise recompute.
+// ---------------------------------------------------------------------------
+
+namespace {
+// The state starts at the first 256-byte boundary of the caller's buffer
+// (the same offset for the forward that writes it and the VJP that reads it).
+float* sk16_state_ptr(const void* state, size_t state_bytes, int64_t batch, int iters) {
+  const uintptr_t base = reinterpret_cast<uintptr_t>(state);
+  const size_t pad = (size_t)((256 - base % 256) % 256);
+  if (state == nullptr || state_bytes < sk16_state_bytes(batch, iters) + pad) return nullptr;
+  return reinterpret_cast<float*>(base + pad);
+}
+}  // namespace
+
+extern "C" size_t mhc_sinkhorn_state_bytes(int64_t batch, int n, int iters) {
+  if (n != 16 || batch <= 0 || iters < 0 || env_int("MHC_SK16", 1) == 0) return 0;
+  return sk16_state_bytes(batch, iters) + 256;
+}
+
+extern "C" int mhc_sinkhorn_fwd_record(const float* logits, float* M, void* state, size_t state_bytes,
+                                       int64_t batch, int n, int iters, float eps, void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n == 16, "a recorded Sinkhorn state exists for n == 16 only (n=%d)", n);
+  MHC_CHECK_ARG(batch >= 0, "batch=%lld must be >= 0", (long long)batch);
+  MHC_CHECK_ARG(iters >= 0, "iters=%d must be >= 0", iters);
+  if (batch == 0) return MHC_OK;
+  MHC_CHECK_ARG(logits != nullptr && M != nullptr, "null pointer argument");
+  MHC_CHECK_ARG(aligned(logits, 16) && aligned(M, 16), "logits and M must be 16-byte aligned");
+  float* st = sk16_state_ptr(state, state_bytes, batch, iters);
+  MHC_CHECK_ARG(st != nullptr, "state of %zu bytes is smaller than the %zu bytes required", state_bytes,
+                sk16_state_bytes(batch, iters) + 256);
+  hipStream_t s = (hipStream_t)stream;
+  const int cpl = sk16_cpl();
+  const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
+  if (cpl == 4)
+    hipLaunchKernelGGL((sinkhorn16_fwd_kernel<4, true>), g, b, 0, s, logits, M, batch, iters, eps, st);
+  else
+    hipLaunchKernelGGL((sinkhorn16_fwd_kernel<2, true>), g, b, 0, s, logits, M, batch, iters, eps, st);
+  MHC_CHECK_LAUNCH("sinkhorn16_fwd_kernel");
+  return MHC_OK;
+}
+
+extern "C" int mhc_sinkhorn_bwd_recorded(const float* logits, const float* dM, float* dlogits, const void* state,
+                                         size_t state_bytes, int64_t batch, int n, int iters, float eps,
+                                         void* stream) {
+  clear_error();
+  MHC_CHECK_ARG(n == 16, "a recorded Sinkhorn state exists for n == 16 only (n=%d)", n);
+  MHC_CHECK_ARG(batch >= 0, "batch=%lld must be >= 0", (long long)batch);
+  MHC_CHECK_ARG(iters >= 0, "iters=%d must be >= 0", iters);
+  if (batch == 0) return MHC_OK;
+  MHC_CHECK_ARG(logits != nullptr && dM != nullptr && dlogits != nullptr, "null pointer argument");
+  MHC_CHECK_ARG(aligned(logits, 16) && aligned(dM, 16) && aligned(dlogits, 16),
+                "logits, dM and dlogits must be 16-byte aligned");
+  float* st = sk16_state_ptr(state, state_bytes, batch, iters);
+  MHC_CHECK_ARG(st != nullptr, "state of %zu bytes is smaller than the %zu bytes required", state_bytes,
+                sk16_state_bytes(batch, iters) + 256);
+  hipStream_t s = (hipStream_t)stream;
+  const int cpl = sk16_cpl();
+  const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
+  if (cpl == 4)
+    hipLaunchKernelGGL((sinkhorn16_bwd_kernel<4, true>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);
+  else
+    hipLaunchKernelGGL((sinkhorn16_bwd_kernel<2, true>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);
+  MHC_CHECK_LAUNCH("sinkhorn16_bwd_kernel");
   return MHC_OK;
 }

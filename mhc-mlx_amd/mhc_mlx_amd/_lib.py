@@ -37,6 +37,9 @@ SIGNATURES = {
     "mhc_sinkhorn_fwd": ([_VP, _VP, _I64, _I32, _I32, _F32, _VP], _I32),
     "mhc_sinkhorn_bwd_workspace_bytes": ([_I64, _I32, _I32], _SZ),
     "mhc_sinkhorn_bwd": ([_VP, _VP, _VP, _I64, _I32, _I32, _F32, _VP, _SZ, _VP], _I32),
+    "mhc_sinkhorn_state_bytes": ([_I64, _I32, _I32], _SZ),
+    "mhc_sinkhorn_fwd_record": ([_VP, _VP, _VP, _SZ, _I64, _I32, _I32, _F32, _VP], _I32),
+    "mhc_sinkhorn_bwd_recorded": ([_VP, _VP, _VP, _VP, _SZ, _I64, _I32, _I32, _F32, _VP], _I32),
     "mhc_fused_fwd": ([_VP, _I32, _VP, _I64, _VP, _VP, _I64, _I32, _VP, _VP, _I32, _VP, _I64, _I32,
                        _I32, _F32, _VP], _I32),
     "mhc_fused_bwd_workspace_bytes": ([_I64, _I32, _I32, _I32], _SZ),

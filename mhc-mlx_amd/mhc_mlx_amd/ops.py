@@ -26,6 +26,7 @@ op requires GPU tensors and the built library; there is no silent fallback.
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -411,6 +412,66 @@ def _layer_bwd(x, g, hpre, hpost, hres, M, w, iters, eps, per_token):
     return dx, dpre, dpost, dres, dw
 
 
+def _sk_state_bytes(B: int, n: int, iters: int) -> int:
+    """Bytes of the Sinkhorn state a per-token forward records for its backward.
+
+    0 when the library has no recorded path for n, or when MHC_SK16_RECORD=0
+    (then the VJP recomputes the forward iterations and needs no saved
+    state: 256 bytes per token and iteration less memory between forward and
+    backward).
+    """
+    if os.environ.get("MHC_SK16_RECORD", "1") == "0":
+        return 0
+    return int(_lib.query("mhc_sinkhorn_state_bytes", B, n, iters))
+
+
+def _layer_fwd_recorded(x, hpre, hpost, hres, w, iters, eps, out_dtype, state):
+    """Per-token forward that records the Sinkhorn VJP state in `state`. Returns (out, M)."""
+    B, n, C = x.shape
+    xc = x if x.is_contiguous() else x.contiguous()
+    hp, hq, hr, wc = _f32(hpre), _f32(hpost), _f32(hres), _f32(w)
+    M = torch.empty_like(hr)
+    out = torch.empty((B, n, C), dtype=out_dtype, device=x.device)
+    s = _stream(xc)
+    with timed("sinkhorn_fwd"):
+        _lib.call("mhc_sinkhorn_fwd_record", _p(hr), _p(M), _p(state), state.numel(), B, n, int(iters), float(eps),
+                  s)
+    with timed("fused_fwd"):
+        _lib.call("mhc_fused_fwd", _p(xc), _code(xc.dtype), _p(M), n * n, _p(hp), _p(hq), n, _lib.H_RAW, _p(wc),
+                  _p(out), _code(out_dtype), None, B, n, C, float(eps), s)
+    return out, M
+
+
+def _layer_bwd_recorded(x, g, hpre, hpost, hres, M, w, iters, eps, state):
+    """Per-token backward from a recorded Sinkhorn state: (dx, dH_pre_raw, dH_post_raw, dH_res_raw, d_w)."""
+    B, n, C = (int(s) for s in x.shape)
+    dev = x.device
+    xc = x.detach().contiguous()
+    gdt = g.dtype if g.dtype in (torch.float32, xc.dtype) else torch.float32
+    gc = g.detach().to(gdt).contiguous()
+    hp, hq, hr, Mc, wc = _f32(hpre), _f32(hpost), _f32(hres), _f32(M), _f32(w)
+    dx = torch.empty_like(xc)
+    dpre = torch.empty_like(hp)
+    dpost = torch.empty_like(hq)
+    dres = torch.empty_like(hr)
+    dw = torch.empty((C,), dtype=torch.float32, device=dev)
+    nb = _lib.query("mhc_fused_bwd_workspace_bytes", B, n, C, 1)
+    ws = _ws(nb, dev)
+    s = _stream(xc)
+    np_ = ctypes.c_int64(0)
+    with timed("fused_bwd"):
+        # per-token dM goes to dres, the activated-H chain is applied in the kernel
+        _lib.call("mhc_fused_bwd_partials", _p(xc), _code(xc.dtype), _p(gc), _code(gc.dtype), _p(Mc), n * n,
+                  _p(hp), _p(hq), n, _lib.H_RAW, _p(wc), _p(dx), _code(xc.dtype), _p(dres), _p(dpre), _p(dpost),
+                  _p(ws), nb, B, n, C, float(eps), ctypes.byref(np_), s)
+    with timed("layer_bwd_reduce"):
+        _lib.call("mhc_reduce_param_grads", _p(ws), nb, np_.value, n, C, 1, None, None, _lib.H_RAW, None, None,
+                  None, _p(dw), s)
+        _lib.call("mhc_sinkhorn_bwd_recorded", _p(hr), _p(dres), _p(dres), _p(state), state.numel(), B, n,
+                  int(iters), float(eps), s)
+    return dx, dpre, dpost, dres, dw
+
+
 class MHCLayerFn(torch.autograd.Function):
     """Whole MHCLayer forward/backward from raw parameters (layer.py:383-407).
 
@@ -419,22 +480,39 @@ class MHCLayerFn(torch.autograd.Function):
     (fused dx + partial sums, then a single launch that reduces the partial
     rows in a fixed order, applies the activation chain and runs the Sinkhorn
     VJP).  Parameters are layer-wide ([n], [n], [n, n]) or per token
-    ([B, n], [B, n], [B, n, n]).
+    ([B, n], [B, n], [B, n, n]).  Per token at n = 16, when a gradient is
+    needed, the Sinkhorn forward also records the VJP's state (saved for
+    backward like an activation, 256 bytes per token and iteration), so the
+    backward skips recomputing the forward iterations.
     """
 
     @staticmethod
     def forward(ctx, x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype):
         per_token = H_res_raw.ndim == 3
-        out, M = _layer_fwd(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype, per_token)
-        ctx.save_for_backward(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, M)
+        # per-token n = 16 with gradients: the Sinkhorn forward records the VJP state
+        state = None
+        if per_token and any(ctx.needs_input_grad[:5]) and x.shape[0] > 0:
+            nb = _sk_state_bytes(int(x.shape[0]), int(x.shape[1]), iters)
+            if nb > 0:
+                state = torch.empty(nb, dtype=torch.uint8, device=x.device)
+        if state is not None:
+            out, M = _layer_fwd_recorded(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype,
+                                         state)
+        else:
+            out, M = _layer_fwd(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype, per_token)
+        ctx.save_for_backward(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, M, state)
         ctx.iters, ctx.eps, ctx.per_token = iters, eps, per_token
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        x, hpre, hpost, hres, w, M = ctx.saved_tensors
-        dx, dpre, dpost, dres, dw = _layer_bwd(x, dout, hpre, hpost, hres, M, w, ctx.iters, ctx.eps,
-                                               ctx.per_token)
+        x, hpre, hpost, hres, w, M, state = ctx.saved_tensors
+        if state is not None:
+            dx, dpre, dpost, dres, dw = _layer_bwd_recorded(x, dout, hpre, hpost, hres, M, w, ctx.iters, ctx.eps,
+                                                            state)
+        else:
+            dx, dpre, dpost, dres, dw = _layer_bwd(x, dout, hpre, hpost, hres, M, w, ctx.iters, ctx.eps,
+                                                   ctx.per_token)
         return (dx, dpre.to(hpre.dtype), dpost.to(hpost.dtype), dres.to(hres.dtype), dw.to(w.dtype),
                 None, None, None)
 

@@ -110,3 +110,21 @@ def test_residual_add_agg_rejects_bad_arguments_on_the_host(lib):
     assert b"null pointer" in lib.mhc_last_error()
     assert lib.mhc_residual_add_agg_bwd(None, None, 9, None, 0, None, None, _lib.H_ACTIVATED, None, None, None,
                                         None, 0, 4, 4, 8, None) == -1
+
+
+def test_sinkhorn_state_is_for_n16_only_and_checked_on_the_host(lib, monkeypatch):
+    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 8 * 20 * 256 + 256
+    assert lib.mhc_sinkhorn_state_bytes(8, 4, 20) == 0
+    assert lib.mhc_sinkhorn_state_bytes(0, 16, 20) == 0
+    monkeypatch.setenv("MHC_SK16", "0")
+    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 0
+    monkeypatch.delenv("MHC_SK16")
+    fake = ctypes.c_void_p(4096)  # never dereferenced: every call below is rejected on the host
+    eps = ctypes.c_float(1e-6)
+    assert lib.mhc_sinkhorn_fwd_record(fake, fake, fake, 1 << 20, 8, 4, 20, eps, None) == -1
+    assert b"n == 16" in lib.mhc_last_error()
+    assert lib.mhc_sinkhorn_fwd_record(fake, fake, fake, 100, 8, 16, 20, eps, None) == -1
+    assert b"smaller" in lib.mhc_last_error()
+    assert lib.mhc_sinkhorn_bwd_recorded(fake, fake, fake, None, 1 << 20, 8, 16, 20, eps, None) == -1
+    assert lib.mhc_sinkhorn_bwd_recorded(fake, fake, fake, fake, 1 << 20, 8, 16, -1, eps, None) == -1
+    assert lib.mhc_sinkhorn_fwd_record(fake, fake, fake, 0, 0, 16, 20, eps, None) == 0  # empty batch

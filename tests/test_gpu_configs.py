@@ -336,6 +336,39 @@ def test_per_token_n16_activated_c_abi(dt):
         assert rel_err(np_of(got), r) < 1e-4, (name, rel_err(np_of(got), r))
 
 
+@pytest.mark.parametrize("T,C", [(300, 1024), (37, 256)])
+def test_per_token_n16_recorded_sinkhorn_state(monkeypatch, T, C):
+    """Per-token n = 16 with gradients records the Sinkhorn VJP state in the forward
+    (mhc_sinkhorn_fwd_record) and the backward uses it (mhc_sinkhorn_bwd_recorded); with
+    MHC_SK16_RECORD=0 the backward recomputes it.  Both give bitwise the same output and gradients."""
+    from mhc_mlx_amd import kernel_timer
+
+    n = 16
+    g = rng(7300 + T)
+    x = to_dtype_np(g.standard_normal((T, n, C)), "bf16")
+    dout = dev_tensor(to_dtype_np(g.standard_normal((T, n, C)), "bf16"), "bf16")
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T)
+    results = []
+    for rec in ("1", "0"):
+        monkeypatch.setenv("MHC_SK16_RECORD", rec)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        xt = dev_tensor(x, "bf16").requires_grad_(True)
+        out = ops.mhc_layer_forward_dynamic(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+        out.backward(dout)
+        results.append([out.detach(), xt.grad] + [p.grad for p in ps])
+    for name, a, b in zip(["out", "dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], *results):
+        assert torch.equal(a, b), name
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, np_of(dout), sinkhorn_iters=20, eps=EPS)
+    assert rel_err(np_of(results[0][4]), refs[3]) < 1e-4
+    # without gradients nothing is recorded: the forward is the plain one (and identical)
+    monkeypatch.setenv("MHC_SK16_RECORD", "1")
+    with torch.no_grad():
+        ps = [dev_tensor(v) for v in (hpre, hpost, hres, w)]
+        out_ng = ops.mhc_layer_forward_dynamic(dev_tensor(x, "bf16"), *ps, sinkhorn_iters=20, eps=EPS,
+                                               output_dtype=torch.bfloat16)
+    assert torch.equal(out_ng, results[0][0])
+
+
 def test_per_token_n16_valu_fallback(monkeypatch):
     """The VALU kernels that serve n = 16 when the MFMA kernels decline (here forced off through
     their environment switches, read at every launch) give the same parity."""

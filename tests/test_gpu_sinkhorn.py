@@ -218,6 +218,50 @@ def test_sinkhorn16_vjp_in_place_c_abi():
         assert np.abs(np_of(buf) - rg).max() / max(np.abs(rg).max(), 1e-3) < 1e-4, iters
 
 
+@pytest.mark.parametrize("B,iters,cpl_fwd,cpl_bwd", [(200, 20, "4", "4"), (33, 1, "4", "2"), (65, 0, "2", "4"),
+                                                   (1000, 20, "2", "2")])
+def test_sinkhorn16_recorded_state_matches_recompute(monkeypatch, B, iters, cpl_fwd, cpl_bwd):
+    """mhc_sinkhorn_fwd_record / mhc_sinkhorn_bwd_recorded give bitwise the results of
+    mhc_sinkhorn_fwd / mhc_sinkhorn_bwd (the same iterations, recorded in the forward instead of
+    recomputed in the VJP) when both use the same lanes per matrix.  With different widths the
+    recorded row sums were added in another order (last-bit differences), so that case is held to
+    the oracle's tolerance.  The state buffer is deliberately not 256-byte aligned; masked rows and
+    columns included."""
+    import ctypes
+
+    from mhc_mlx_amd import _lib
+
+    g = rng(4300 + B + iters)
+    H = (2.0 * g.standard_normal((B, 16, 16))).astype(np.float32)
+    H[::5, :, 3] = -40.0
+    dM = g.standard_normal((B, 16, 16)).astype(np.float32)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    eps = ctypes.c_float(1e-5)
+    Ht = dev_tensor(H)
+    monkeypatch.setenv("MHC_SK16_CPL", cpl_fwd)
+    M_plain = torch.empty_like(Ht)
+    _lib.call("mhc_sinkhorn_fwd", P(Ht), P(M_plain), B, 16, iters, eps, s)
+    nst = _lib.query("mhc_sinkhorn_state_bytes", B, 16, iters)
+    assert nst == B * max(iters, 1) * 256 + 256
+    st_buf = torch.empty(nst + 64, dtype=torch.uint8, device="cuda")
+    st = st_buf[48:]  # 48 bytes past the allocation's start
+    M_rec = torch.empty_like(Ht)
+    _lib.call("mhc_sinkhorn_fwd_record", P(Ht), P(M_rec), P(st), nst, B, 16, iters, eps, s)
+    assert torch.equal(M_rec, M_plain)
+    monkeypatch.setenv("MHC_SK16_CPL", cpl_bwd)
+    d_rec = dev_tensor(dM)
+    _lib.call("mhc_sinkhorn_bwd_recorded", P(Ht), P(d_rec), P(d_rec), P(st), nst, B, 16, iters, eps, s)
+    nb = _lib.query("mhc_sinkhorn_bwd_workspace_bytes", B, 16, iters)
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+    d_plain = dev_tensor(dM)
+    _lib.call("mhc_sinkhorn_bwd", P(Ht), P(d_plain), P(d_plain), B, 16, iters, eps, P(ws), nb, s)
+    if cpl_fwd == cpl_bwd:
+        assert torch.equal(d_rec, d_plain)
+    rg = O.sinkhorn_knopp_vjp(H.astype(np.float64), dM, iters=iters, eps=1e-5)
+    assert np.abs(np_of(d_rec) - rg).max() < 1e-4 * max(1.0, np.abs(rg).max())
+
+
 def test_sinkhorn16_identity_init_and_bomb():
     n = 16
     Hi = (np.full((n, n), -12.0) + np.eye(n) * 12.0).astype(np.float32)
