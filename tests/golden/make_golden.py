@@ -12,7 +12,8 @@ this environment (it needs MLX), so two kinds of fixtures are kept:
   by tests/test_oracle_*.py) for the BASELINE config-0 recipe, the
   deterministic arange recipe of tests/test_correctness.py:147-156 of the
   reference, a small backward with every gradient, a mini config 3
-  (per-token parameters) and a small residual_add_agg with its gradients.
+  (per-token parameters), a small residual_add_agg and a small MHCRewire
+  post-combine / pre-scale, each with its gradients.
 
 Inputs are seeded numpy draws; every file is a plain .npz (no pickles).
 """
@@ -126,6 +127,35 @@ def residual_mini():
     return dict(x=x, res=res, h=h, dout=dout, dy=dy, out=out, y_agg=y_agg, dx=dx, dres=dres, dh=dh)
 
 
+def rewire_mini():
+    """MHCRewire post-combine and pre-scale (layer.py:302-337, 476-480): bf16-representable x and
+    y_inner, every gradient of both."""
+    g = np.random.default_rng(8)
+    B, n, C = 3, 4, 72
+    x = O.bf16_round(g.standard_normal((B, n, C)).astype(np.float32))
+    y = O.bf16_round(g.standard_normal((B, n, C)).astype(np.float32))
+    hpre = g.standard_normal(n).astype(np.float32)
+    hpost = g.standard_normal(n).astype(np.float32)
+    hres = g.standard_normal((n, n)).astype(np.float32)
+    dout = g.standard_normal((B, n, C)).astype(np.float32)
+    dscale = g.standard_normal((B, n, C)).astype(np.float32)
+    out = O.post_combine(x, y, hpre, hpost, hres, 20, 1e-5)
+    dx, dy, dpre, dpost, dres = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    a = O.sigmoid(hpre.astype(np.float64))
+    xs = x * a[None, :, None]
+
+    def scale_vjp(d):
+        d = d.astype(np.float64)
+        return d * a[None, :, None], np.einsum("bic,bic->i", d, x.astype(np.float64)) * a * (1.0 - a)
+
+    # a bf16 output takes its cotangent in bf16: the expected gradients for that rounding too
+    dxs, dpre_s = scale_vjp(dscale)
+    dxs16, dpre_s16 = scale_vjp(O.bf16_round(dscale))
+    return dict(x=x, y=y, hpre=hpre, hpost=hpost, hres=hres, dout=dout, dscale=dscale, out=out, dx=dx, dy=dy,
+                dpre=dpre, dpost=dpost, dres=dres, x_scaled=xs, dx_scaled=dxs, dpre_scaled=dpre_s,
+                dx_scaled_bf16=dxs16, dpre_scaled_bf16=dpre_s16)
+
+
 FIXTURES = {
     "sinkhorn_closed_forms.npz": closed_forms,
     "cfg0_fwd.npz": cfg0,
@@ -133,6 +163,7 @@ FIXTURES = {
     "bwd_small.npz": bwd_small,
     "cfg3_mini.npz": cfg3_mini,
     "residual_mini.npz": residual_mini,
+    "rewire_mini.npz": rewire_mini,
 }
 
 

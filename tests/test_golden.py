@@ -61,3 +61,12 @@ def test_oracle_reproduces_residual_fixture():
     assert np.allclose(out, z["out"], rtol=1e-12, atol=0) and np.allclose(y, z["y_agg"], rtol=1e-12, atol=1e-15)
     for k, g in zip(["dx", "dres", "dh"], O.residual_add_agg_backward(z["x"], z["res"], z["h"], z["dout"], z["dy"])):
         assert np.allclose(g, z[k], rtol=1e-12, atol=1e-14), k
+
+
+def test_oracle_reproduces_rewire_fixture():
+    z = load("rewire_mini.npz")
+    out = O.post_combine(z["x"], z["y"], z["hpre"], z["hpost"], z["hres"], 20, 1e-5)
+    assert np.allclose(out, z["out"], rtol=1e-12, atol=1e-15)
+    grads = O.post_combine_backward(z["x"], z["y"], z["hpre"], z["hpost"], z["hres"], z["dout"], 20, 1e-5)
+    for k, g in zip(["dx", "dy", "dpre", "dpost", "dres"], grads):
+        assert np.allclose(g, z[k], rtol=1e-12, atol=1e-14), k

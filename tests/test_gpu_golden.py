@@ -81,3 +81,27 @@ def test_residual_fixture(dt, tol):
     assert rel_err(np_of(ht.grad), z["dh"]) < 1e-5
     gtol = 1e-5 if dt == "f32" else 2e-2
     assert rel_err(np_of(xt.grad), z["dx"]) < gtol and rel_err(np_of(rt.grad), z["dres"]) < gtol
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_rewire_fixture(dt):
+    """MHCRewire post-combine and pre-scale against rewire_mini.npz (bf16-representable x and
+    y_inner: both dtypes see the same values; fp32 cotangents)."""
+    z = load("rewire_mini.npz")
+    xt = dev_tensor(z["x"], dt).requires_grad_(True)
+    yt = dev_tensor(z["y"], dt).requires_grad_(True)
+    ps = [dev_tensor(z[k]).requires_grad_(True) for k in ("hpre", "hpost", "hres")]
+    out = ops.post_combine(xt, yt, *ps, sinkhorn_iters=20, eps=1e-5)
+    assert rel_err(np_of(out), z["out"]) < 1e-5
+    out.backward(dev_tensor(z["dout"]))
+    for name, got in zip(["dx", "dy", "dpre", "dpost", "dres"], [xt.grad, yt.grad] + [p.grad for p in ps]):
+        tol = (1e-5 if dt == "f32" else 2e-2) if name in ("dx", "dy") else 1e-4
+        assert rel_err(np_of(got), z[name]) < tol, (name, rel_err(np_of(got), z[name]))
+    xs = dev_tensor(z["x"], dt).requires_grad_(True)
+    hs = dev_tensor(z["hpre"]).requires_grad_(True)
+    sc = ops.stream_scale(xs, hs)
+    assert rel_err(np_of(sc), z["x_scaled"]) < (1e-6 if dt == "f32" else 1e-2)
+    sc.backward(dev_tensor(z["dscale"]))  # cast to the output's dtype by autograd
+    sfx = "" if dt == "f32" else "_bf16"
+    assert rel_err(np_of(xs.grad), z["dx_scaled" + sfx]) < (1e-6 if dt == "f32" else 1e-2)
+    assert rel_err(np_of(hs.grad), z["dpre_scaled" + sfx]) < 1e-5
