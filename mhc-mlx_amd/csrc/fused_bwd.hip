@@ -1355,7 +1355,9 @@ __global__ __launch_bounds__(kFinThreads) void param_finish_kernel(RedArgs R) {
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
       const int k = phase + m * kFinPhases;
-      u[m] = k < R.S ? *reinterpret_cast<const float4*>(src + (int64_t)k * R.P) : v;
+      // the zero is a value, not the variable v: a conditional between two
+      // lvalues becomes a select of addresses, which puts v in scratch
+      u[m] = k < R.S ? *reinterpret_cast<const float4*>(src + (int64_t)k * R.P) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     for (int k = phase + 16 * kFinPhases; k < R.S; k += kFinPhases)
       u[0] = f4add(u[0], *reinterpret_cast<const float4*>(src + (int64_t)k * R.P));

@@ -307,8 +307,12 @@ MHC_DEV void wave_reduce_scatter(float (&v)[64 * R], int lane) {
     const bool upper = (lane & m) != 0;
 #pragma unroll
     for (int k = 0; k < half; ++k) {
-      const float keep = upper ? v[k + half] : v[k];
-      const float send = upper ? v[k] : v[k + half];
+      // select values, not array elements: `upper ? v[a] : v[b]` is an
+      // lvalue, which the compiler may turn into a select of addresses and
+      // move v to scratch memory
+      const float lo = v[k], hi = v[k + half];
+      const float keep = upper ? hi : lo;
+      const float send = upper ? lo : hi;
       v[k] = keep + shfl_xor(send, m);
     }
   }
