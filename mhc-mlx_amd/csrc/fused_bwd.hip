@@ -1004,10 +1004,21 @@ __global__ __launch_bounds__(256) void fused_bwd_pt16_kernel(BwdArgs A) {
 constexpr int kMf16Row = 128 + 8;  // LDS row (16-bit elements): 68 dwords, 4 mod 64 banks
 constexpr int kMf16MaxWaves = 8;
 
-template <typename XT, int SPW, bool RAW>
+// LW: layer-wide parameters (one M, a, p for every token).  The token's dM,
+// dA and dP are then added into per-thread sums across the workgroup's
+// tokens and end in its partial row after the dw slice, unactivated (the
+// reduction applies the activation chain to the totals).
+template <typename XT, int SPW, bool RAW, bool LW>
 __global__ __launch_bounds__(SPW == 2 ? 256 : 512) __attribute__((amdgpu_waves_per_eu(2)))
 void fused_bwd_mfma16_kernel(BwdArgs A) {
   constexpr int N = 16;
+  constexpr int64_t PS = LW ? 0 : 16;   // parameter strides per token
+  constexpr int64_t MS = LW ? 0 : 256;
+  constexpr int KP = 256 + 32;          // dM, dA, dP of a token
+  constexpr int KPT = (KP + 63) / 64;   // k per thread at 64 threads
+  float lw_acc[KPT];                    // LW: sums of k = tid + e * blockDim.x
+#pragma unroll
+  for (int e = 0; e < KPT; ++e) lw_acc[e] = 0.0f;
   constexpr int SLAB = 2 * N * kMf16Row;  // 16-bit elements of one staged slab (x rows, then g rows)
   extern __shared__ uint16_t mf_lds[];
   constexpr int MW = SPW == 2 ? 4 : kMf16MaxWaves;  // waves per workgroup at most
@@ -1042,9 +1053,9 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
   float4 nh = make_float4(0.f, 0.f, 0.f, 0.f), ng = nh, nm = nh;
   if ((int64_t)blockIdx.x < A.T) {
     const int64_t t0 = blockIdx.x;
-    nh = *reinterpret_cast<const float4*>(A.hpre + t0 * 16 + 4 * q);
-    ng = *reinterpret_cast<const float4*>(A.hpost + t0 * 16 + 4 * q);
-    const float* M0 = A.M + t0 * 256 + (4 * q) * 16 + r;
+    nh = *reinterpret_cast<const float4*>(A.hpre + t0 * PS + 4 * q);
+    ng = *reinterpret_cast<const float4*>(A.hpost + t0 * PS + 4 * q);
+    const float* M0 = A.M + t0 * MS + (4 * q) * 16 + r;
     nm = make_float4(M0[0], M0[16], M0[32], M0[48]);
   }
   __syncthreads();
@@ -1070,9 +1081,9 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
       {
         const int64_t tn = t + gridDim.x;
         if (tn < A.T) {
-          nh = *reinterpret_cast<const float4*>(A.hpre + tn * 16 + 4 * q);
-          ng = *reinterpret_cast<const float4*>(A.hpost + tn * 16 + 4 * q);
-          const float* Mn = A.M + tn * 256 + (4 * q) * 16 + r;
+          nh = *reinterpret_cast<const float4*>(A.hpre + tn * PS + 4 * q);
+          ng = *reinterpret_cast<const float4*>(A.hpost + tn * PS + 4 * q);
+          const float* Mn = A.M + tn * MS + (4 * q) * 16 + r;
           nm = make_float4(Mn[0], Mn[16], Mn[32], Mn[48]);
         }
       }
@@ -1251,7 +1262,22 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
       }
     }
     lds_barrier();
-    for (int k = tid; k < 256 + 32; k += blockDim.x) {
+    if constexpr (LW) {
+#pragma unroll
+      for (int e = 0; e < KPT; ++e) {
+        const int k = tid + e * blockDim.x;
+        if (k < KP) {
+          float sum = 0.0f;
+          if (k < 256) {
+            for (int w = 0; w < nwaves; ++w) sum += s_dm[w][k];
+          } else {
+            for (int w = 0; w < nwaves; ++w) sum += s_ap[w][k - 256];
+          }
+          lw_acc[e] += sum;
+        }
+      }
+    } else
+    for (int k = tid; k < KP; k += blockDim.x) {
       float sum = 0.0f;
       if (k < 256) {
         for (int w = 0; w < nwaves; ++w) sum += s_dm[w][k];
@@ -1280,6 +1306,14 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
     for (int s = 0; s < SPW; ++s) {
       *reinterpret_cast<float4*>(prow + cb[s]) = make_float4(dwv[s][0], dwv[s][1], dwv[s][2], dwv[s][3]);
       *reinterpret_cast<float4*>(prow + cb[s] + 4) = make_float4(dwv[s][4], dwv[s][5], dwv[s][6], dwv[s][7]);
+    }
+  }
+  if constexpr (LW) {
+    // [Cp | dM 256 | dA 16 | dP 16]: P = Cp + KP, no padding columns
+#pragma unroll
+    for (int e = 0; e < KPT; ++e) {
+      const int k = tid + e * blockDim.x;
+      if (k < KP) prow[A.Cp + k] = lw_acc[e];
     }
   }
 }
@@ -1481,13 +1515,14 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
 
 // Per-token n == 16 with 16-bit x == dout and C a multiple of 256 up to 1024
 // (fused_bwd_pt16_kernel).  Returns 1 when the shape is not covered.
-// Per-token n == 16 on MFMA (fused_bwd_mfma16_kernel): 16-bit x == dout, C a
-// multiple of 128 up to 1024 (two 128-channel slabs per wave when C / 128 is
-// even, else one), 16-byte aligned operands.  Returns 1 when the shape is not
-// covered.
-template <typename XT>
+// n == 16 on MFMA (fused_bwd_mfma16_kernel), per-token or (LW) layer-wide
+// parameters: 16-bit x == dout, C a multiple of 128 up to 1024 (two
+// 128-channel slabs per wave when C / 128 is even, else one), 16-byte aligned
+// operands.  Returns 1 when the shape is not covered.
+template <typename XT, bool LW>
 int launch_bwd_mfma16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
   if (A.n != 16 || A.C % 128 != 0 || A.C > 1024) return 1;
+  if (LW && L.P != L.Cp + 256 + 32) return 1;
   if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.dx, 16) || !aligned(A.M, 16) ||
       !aligned(A.hpre, 16) || !aligned(A.hpost, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
     return 1;
@@ -1500,10 +1535,10 @@ int launch_bwd_mfma16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipS
   if (waves > (spw == 2 ? 4 : kMf16MaxWaves)) return 1;
   const size_t smem = (size_t)waves * spw * 2 * 16 * kMf16Row * sizeof(uint16_t);
   const bool raw = A.h_mode == MHC_H_RAW;
-  const void* kfn = spw == 2 ? (raw ? (const void*)fused_bwd_mfma16_kernel<XT, 2, true>
-                                    : (const void*)fused_bwd_mfma16_kernel<XT, 2, false>)
-                             : (raw ? (const void*)fused_bwd_mfma16_kernel<XT, 1, true>
-                                    : (const void*)fused_bwd_mfma16_kernel<XT, 1, false>);
+  const void* kfn = spw == 2 ? (raw ? (const void*)fused_bwd_mfma16_kernel<XT, 2, true, LW>
+                                    : (const void*)fused_bwd_mfma16_kernel<XT, 2, false, LW>)
+                             : (raw ? (const void*)fused_bwd_mfma16_kernel<XT, 1, true, LW>
+                                    : (const void*)fused_bwd_mfma16_kernel<XT, 1, false, LW>);
   const int occ = occupancy_blocks(kfn, waves * 64, smem);
   if (occ <= 0) return 1;
   int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
@@ -1513,11 +1548,11 @@ int launch_bwd_mfma16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipS
   set_rows(A, L);
   const dim3 g((unsigned)blocks), b(waves * 64);
   if (spw == 2) {
-    if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 2, true>), g, b, smem, stream, A);
-    else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 2, false>), g, b, smem, stream, A);
+    if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 2, true, LW>), g, b, smem, stream, A);
+    else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 2, false, LW>), g, b, smem, stream, A);
   } else {
-    if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 1, true>), g, b, smem, stream, A);
-    else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 1, false>), g, b, smem, stream, A);
+    if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 1, true, LW>), g, b, smem, stream, A);
+    else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 1, false, LW>), g, b, smem, stream, A);
   }
   MHC_CHECK_LAUNCH("fused_bwd_mfma16_kernel");
   *num_partials = blocks;
@@ -1543,8 +1578,12 @@ int launch_bwd_pt16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStr
 
 template <int NMAX, typename XT, typename GT, bool PT>
 int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  if constexpr (!PT && NMAX == 16 && std::is_same<XT, GT>::value && ElemTraits<XT>::kBytes == 2) {
+    const int rc = launch_bwd_mfma16<XT, true>(A, L, num_partials, stream);
+    if (rc != 1) return rc;
+  }
   if constexpr (PT && NMAX == 16 && std::is_same<XT, GT>::value && ElemTraits<XT>::kBytes == 2) {
-    int rc = launch_bwd_mfma16<XT>(A, L, num_partials, stream);
+    int rc = launch_bwd_mfma16<XT, false>(A, L, num_partials, stream);
     if (rc != 1) return rc;
     rc = launch_bwd_pt16<XT>(A, L, num_partials, stream);
     if (rc != 1) return rc;

@@ -91,7 +91,10 @@ def test_identity_mapping_n4():
 # ------------------------------------------------------------------ backward
 
 BWD_SHAPES = [(2, 4, 128), (3, 4, 129), (2, 3, 64), (2, 8, 96), (2, 16, 64), (2, 5, 40), (2, 24, 48),
-              (1, 32, 64), (2, 4, 20000)]
+              (1, 32, 64), (2, 4, 20000),
+              # n = 16, C a multiple of 128 up to 1024: the MFMA backward with layer-wide
+              # parameters for 16-bit x == dout (one or two slabs per wave, 64-512 threads)
+              (3, 16, 128), (5, 16, 256), (4, 16, 384), (3, 16, 512), (2, 16, 1024)]
 
 
 def _bwd_case(B, n, C, xdt, gdt, seed, per_token=False):
