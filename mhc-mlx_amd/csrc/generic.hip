@@ -44,17 +44,28 @@ MHC_DEV float gen_block_sum(float v, float* s_red) {
   return t;
 }
 
-template <typename XT, typename OT>
+// Forward.  A thread owns channels c = tid, tid + blockDim.x, ...; in the
+// second pass the n values of its channel sit in registers (NMAX = 32 or 64
+// slots, the unused ones zero) and the n x n mix runs from them against rows
+// of M broadcast from LDS as float4s (row stride NMAX, zero-padded), so x is
+// read once per pass instead of once per output stream.
+template <typename XT, typename OT, int NMAX>
 __global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(GenArgs A) {
   __shared__ float s_par[kGenMaxPar];
+  __shared__ __align__(16) float s_M[NMAX * NMAX];
   __shared__ float s_red[2][kGenThreads / 64];
   const int n = A.n, C = A.C, nn = n * n;
   const XT* X = (const XT*)A.x;
   OT* O = (OT*)A.out;
   int it = 0;
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
-    __syncthreads();  // previous token done with s_par
+    __syncthreads();  // previous token done with s_par / s_M
     gen_stage(s_par, A.M + t * A.M_ts, A.hpre + t * A.h_ts, A.hpost + t * A.h_ts, n, A.h_mode);
+    const float* Mt = A.M + t * A.M_ts;
+    for (int k = threadIdx.x; k < NMAX * NMAX; k += blockDim.x) {
+      const int i = k / NMAX, j = k % NMAX;
+      s_M[k] = (i < n && j < n) ? Mt[i * n + j] : 0.0f;
+    }
     __syncthreads();
     const XT* xt = X + t * n * C;
     OT* ot = O + t * n * C;
@@ -68,28 +79,54 @@ __global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(GenArgs A) {
     const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
     if (A.inv_rms && threadIdx.x == 0) A.inv_rms[t] = inv;
     for (int c = threadIdx.x; c < C; c += blockDim.x) {
+      float xv[NMAX];
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) xv[j] = j < n ? load1<XT>(xt + (int64_t)j * C + c) : 0.0f;
       float y = 0.0f;
-      for (int i = 0; i < n; ++i) y = fmaf(s_par[nn + i], load1<XT>(xt + (int64_t)i * C + c), y);
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) y = fmaf(j < n ? s_par[nn + j] : 0.0f, xv[j], y);
       const float yn = (y * inv) * A.w[c];
       for (int i = 0; i < n; ++i) {
+        const float4* Mi = reinterpret_cast<const float4*>(s_M + i * NMAX);
         float acc = 0.0f;
-        for (int j = 0; j < n; ++j) acc = fmaf(s_par[i * n + j], load1<XT>(xt + (int64_t)j * C + c), acc);
+#pragma unroll
+        for (int j4 = 0; j4 < NMAX / 4; ++j4) {
+          const float4 m = Mi[j4];
+          acc = fmaf(m.x, xv[4 * j4], acc);
+          acc = fmaf(m.y, xv[4 * j4 + 1], acc);
+          acc = fmaf(m.z, xv[4 * j4 + 2], acc);
+          acc = fmaf(m.w, xv[4 * j4 + 3], acc);
+        }
         store1<OT>(ot + (int64_t)i * C + c, fmaf(yn, s_par[nn + n + i], acc));
       }
     }
   }
 }
 
-// Backward.  Per token: dy/yn go to this workgroup's scratch rows so the
-// parameter-gradient loops (threads over (i, j) pairs, loops over channels)
-// can read them.  Layer-wide sums accumulate in LDS slots, each owned by one
-// thread; dw accumulates in the workgroup's partial row.
-template <typename XT, typename GT>
+// Backward.  Per token:
+//  pass 1: y = a.x and d = p.g per channel give sum y^2 and sum d y w;
+//  pass 2: the n values of g of a channel sit in registers (NMAX slots, the
+//          unused ones zero); dx_j = sum_i M_ij g_i + a_j dy runs against rows
+//          of M^T broadcast from LDS as float4s; dy and yn = y inv w go to
+//          this workgroup's scratch rows and dw to its partial row;
+//  pass 3: the parameter gradients are the sums over channels of an
+//          (n+1) x (n+1) outer product -- rows g_0..g_{n-1}, dy; columns
+//          x_0..x_{n-1}, yn: dM_ij = sum g_i x_j, dA_j = sum dy x_j,
+//          dP_i = sum g_i yn.  A wavefront takes one 4 x 4 block at a time,
+//          its lanes over consecutive channels (coalesced loads), and adds
+//          the wave sums into the block's entries: in LDS across tokens for
+//          layer-wide parameters, or straight to the per-token outputs.
+//          Each entry belongs to one wavefront, so the order is fixed.
+template <typename XT, typename GT, int NMAX>
 __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs A) {
+  constexpr int NE = NMAX + 1;  // extended rows / columns
   __shared__ float s_par[kGenMaxPar];
-  __shared__ float s_acc[kGenMaxPar];
+  __shared__ __align__(16) float s_MT[NMAX * NMAX];
+  __shared__ float s_acc[NE * NE];
   __shared__ float s_red[2][2][kGenThreads / 64];
-  const int n = A.n, C = A.C, nn = n * n, K = nn + 2 * n;
+  const int n = A.n, C = A.C, nn = n * n;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int nb = (n + 1 + 3) / 4;  // 4-wide blocks of the n + 1 rows (and columns)
   const XT* X = (const XT*)A.x;
   const GT* Gd = (const GT*)A.g;
   XT* DX = (XT*)A.out;
@@ -97,11 +134,16 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs A) {
   float* sdy = A.scratch + (int64_t)blockIdx.x * 2 * A.C;
   float* syn = sdy + A.C;
   for (int c = threadIdx.x; c < A.P; c += blockDim.x) prow[c] = 0.0f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) s_acc[k] = 0.0f;
+  for (int k = threadIdx.x; k < NE * NE; k += blockDim.x) s_acc[k] = 0.0f;
   int it = 0;
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
-    __syncthreads();
+    __syncthreads();  // previous token done with s_par / s_MT
     gen_stage(s_par, A.M + t * A.M_ts, A.hpre + t * A.h_ts, A.hpost + t * A.h_ts, n, A.h_mode);
+    const float* Mt = A.M + t * A.M_ts;
+    for (int k = threadIdx.x; k < NMAX * NMAX; k += blockDim.x) {
+      const int j = k / NMAX, i = k % NMAX;  // s_MT[j][i] = M_ij
+      s_MT[k] = (i < n && j < n) ? Mt[i * n + j] : 0.0f;
+    }
     __syncthreads();
     const XT* xt = X + t * n * C;
     const GT* gt = Gd + t * n * C;
@@ -121,11 +163,13 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs A) {
     const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
     const float kf = (inv * inv * inv / (float)C) * tsr;
     for (int c = threadIdx.x; c < C; c += blockDim.x) {
+      float gv[NMAX];
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) gv[i] = i < n ? load1<GT>(gt + (int64_t)i * C + c) : 0.0f;
       float y = 0.0f, d = 0.0f;
-      for (int i = 0; i < n; ++i) {
-        y = fmaf(s_par[nn + i], load1<XT>(xt + (int64_t)i * C + c), y);
-        d = fmaf(s_par[nn + n + i], load1<GT>(gt + (int64_t)i * C + c), d);
-      }
+      for (int i = 0; i < n; ++i) y = fmaf(s_par[nn + i], load1<XT>(xt + (int64_t)i * C + c), y);
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) d = fmaf(i < n ? s_par[nn + n + i] : 0.0f, gv[i], d);
       const float wc = A.w[c];
       const float yi = y * inv;
       const float dy = d * inv * wc - kf * y;
@@ -133,43 +177,68 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs A) {
       syn[c] = yi * wc;
       prow[c] = fmaf(d, yi, prow[c]);
       for (int j = 0; j < n; ++j) {
+        const float4* Mj = reinterpret_cast<const float4*>(s_MT + j * NMAX);
         float acc = 0.0f;
-        for (int i = 0; i < n; ++i) acc = fmaf(s_par[i * n + j], load1<GT>(gt + (int64_t)i * C + c), acc);
+#pragma unroll
+        for (int i4 = 0; i4 < NMAX / 4; ++i4) {
+          const float4 m = Mj[i4];
+          acc = fmaf(m.x, gv[4 * i4], acc);
+          acc = fmaf(m.y, gv[4 * i4 + 1], acc);
+          acc = fmaf(m.z, gv[4 * i4 + 2], acc);
+          acc = fmaf(m.w, gv[4 * i4 + 3], acc);
+        }
         store1<XT>(dxt + (int64_t)j * C + c, fmaf(s_par[nn + j], dy, acc));
       }
     }
     __syncthreads();  // sdy / syn visible to the workgroup
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-      float s = 0.0f;
-      if (k < nn) {
-        const int i = k / n, j = k % n;
-        for (int c = 0; c < C; ++c)
-          s = fmaf(load1<GT>(gt + (int64_t)i * C + c), load1<XT>(xt + (int64_t)j * C + c), s);
-      } else if (k < nn + n) {
-        const int j = k - nn;
-        for (int c = 0; c < C; ++c) s = fmaf(sdy[c], load1<XT>(xt + (int64_t)j * C + c), s);
-      } else {
-        const int i = k - nn - n;
-        for (int c = 0; c < C; ++c) s = fmaf(load1<GT>(gt + (int64_t)i * C + c), syn[c], s);
-      }
-      if (A.M_ts) {
-        if (k < nn) {
-          A.dM_tok[t * nn + k] = s;
-        } else if (k < nn + n) {
-          const float av = s_par[k];
-          A.dpre_tok[t * n + (k - nn)] = A.h_mode == MHC_H_RAW ? s * av * (1.0f - av) : s;
-        } else {
-          const float pq = s_par[k];
-          A.dpost_tok[t * n + (k - nn - n)] = A.h_mode == MHC_H_RAW ? s * pq * (1.0f - 0.5f * pq) : s;
+    for (int blk = wave; blk < nb * nb; blk += nwaves) {
+      const int r0 = (blk / nb) * 4, c0 = (blk % nb) * 4;
+      float acc[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+      for (int c = lane; c < C; c += 64) {
+        float rv[4], cv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int ri = r0 + e, cj = c0 + e;
+          rv[e] = ri < n ? load1<GT>(gt + (int64_t)ri * C + c) : (ri == n ? sdy[c] : 0.0f);
+          cv[e] = cj < n ? load1<XT>(xt + (int64_t)cj * C + c) : (cj == n ? syn[c] : 0.0f);
         }
-      } else {
-        s_acc[k] += s;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = fmaf(rv[e >> 2], cv[e & 3], acc[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = wave_sum(acc[e]);
+        const int i = r0 + (e >> 2), j = c0 + (e & 3);
+        if (lane != 0 || i > n || j > n || (i == n && j == n)) continue;
+        if (A.M_ts) {
+          if (i < n && j < n) {
+            A.dM_tok[t * nn + i * n + j] = v;
+          } else if (i == n) {  // dA_j
+            const float av = s_par[nn + j];
+            A.dpre_tok[t * n + j] = A.h_mode == MHC_H_RAW ? v * av * (1.0f - av) : v;
+          } else {  // dP_i
+            const float pq = s_par[nn + n + i];
+            A.dpost_tok[t * n + i] = A.h_mode == MHC_H_RAW ? v * pq * (1.0f - 0.5f * pq) : v;
+          }
+        } else {
+          s_acc[i * NE + j] += v;
+        }
       }
     }
   }
   __syncthreads();
-  if (!A.M_ts)
-    for (int k = threadIdx.x; k < K; k += blockDim.x) prow[A.Cp + k] = s_acc[k];
+  if (!A.M_ts) {
+    // [Cp | dM n*n | dA n | dP n]
+    for (int k = threadIdx.x; k < nn + 2 * n; k += blockDim.x) {
+      float v;
+      if (k < nn) v = s_acc[(k / n) * NE + (k % n)];
+      else if (k < nn + n) v = s_acc[n * NE + (k - nn)];
+      else v = s_acc[(k - nn - n) * NE + n];
+      prow[A.Cp + k] = v;
+    }
+  }
 }
 
 // post-combine / stream_mix_add forward: out_i = p_i (y_i + sum_j M_ij a_j x_j)
@@ -275,7 +344,10 @@ int gen_fused_fwd(const GenArgs& A, int xd, int od, hipStream_t s) {
     using XT = std::remove_pointer_t<decltype(xp)>;
     return by_pair<XT>(od, [&](auto* op) {
       using OT = std::remove_pointer_t<decltype(op)>;
-      hipLaunchKernelGGL((gen_fwd_kernel<XT, OT>), dim3((unsigned)blocks), dim3(kGenThreads), 0, s, A);
+      if (A.n <= 32)
+        hipLaunchKernelGGL((gen_fwd_kernel<XT, OT, 32>), dim3((unsigned)blocks), dim3(kGenThreads), 0, s, A);
+      else
+        hipLaunchKernelGGL((gen_fwd_kernel<XT, OT, 64>), dim3((unsigned)blocks), dim3(kGenThreads), 0, s, A);
       MHC_CHECK_LAUNCH("gen_fwd_kernel");
       return MHC_OK;
     });
@@ -289,7 +361,10 @@ int gen_fused_bwd(const GenArgs& A, int xd, int gd, hipStream_t s, int64_t* num_
     using XT = std::remove_pointer_t<decltype(xp)>;
     return by_pair<XT>(gd, [&](auto* gp) {
       using GT = std::remove_pointer_t<decltype(gp)>;
-      hipLaunchKernelGGL((gen_bwd_kernel<XT, GT>), dim3((unsigned)blocks), dim3(kGenThreads), 0, s, A);
+      if (A.n <= 32)
+        hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 32>), dim3((unsigned)blocks), dim3(kGenThreads), 0, s, A);
+      else
+        hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 64>), dim3((unsigned)blocks), dim3(kGenThreads), 0, s, A);
       MHC_CHECK_LAUNCH("gen_bwd_kernel");
       return MHC_OK;
     });
