@@ -241,12 +241,20 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs A) {
   }
 }
 
-// post-combine / stream_mix_add forward: out_i = p_i (y_i + sum_j M_ij a_j x_j)
-template <typename XT, typename YT, typename OT>
+// post-combine / stream_mix_add forward: out_i = p_i (y_i + sum_j M_ij a_j x_j).
+// The n values of x at a (token, channel) item sit in registers (NMAX slots,
+// the unused ones zero) against float4 rows of Mf_ij = M_ij a_j in LDS.
+template <typename XT, typename YT, typename OT, int NMAX>
 __global__ __launch_bounds__(kGenThreads) void gen_mix_fwd_kernel(GenArgs A) {
   __shared__ float s_par[kGenMaxPar];
+  __shared__ __align__(16) float s_Mf[NMAX * NMAX];
   const int n = A.n, C = A.C, nn = n * n;
   gen_stage(s_par, A.M, A.hpre, A.hpost, n, A.h_mode);
+  __syncthreads();
+  for (int k = threadIdx.x; k < NMAX * NMAX; k += blockDim.x) {
+    const int i = k / NMAX, j = k % NMAX;
+    s_Mf[k] = (i < n && j < n) ? s_par[i * n + j] * s_par[nn + j] : 0.0f;
+  }
   __syncthreads();
   const XT* X = (const XT*)A.x;
   const YT* Y = (const YT*)A.y;
@@ -257,10 +265,20 @@ __global__ __launch_bounds__(kGenThreads) void gen_mix_fwd_kernel(GenArgs A) {
     const int64_t t = item / C;
     const int c = (int)(item - t * C);
     const int64_t base = t * n * C + c;
+    float xv[NMAX];
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) xv[j] = j < n ? load1<XT>(X + base + (int64_t)j * C) : 0.0f;
     for (int i = 0; i < n; ++i) {
+      const float4* Mi = reinterpret_cast<const float4*>(s_Mf + i * NMAX);
       float acc = 0.0f;
-      for (int j = 0; j < n; ++j)
-        acc = fmaf(s_par[i * n + j] * s_par[nn + j], load1<XT>(X + base + (int64_t)j * C), acc);
+#pragma unroll
+      for (int j4 = 0; j4 < NMAX / 4; ++j4) {
+        const float4 m = Mi[j4];
+        acc = fmaf(m.x, xv[4 * j4], acc);
+        acc = fmaf(m.y, xv[4 * j4 + 1], acc);
+        acc = fmaf(m.z, xv[4 * j4 + 2], acc);
+        acc = fmaf(m.w, xv[4 * j4 + 3], acc);
+      }
       const float yv = Y ? load1<YT>(Y + base + (int64_t)i * C) : 0.0f;
       store1<OT>(O + base + (int64_t)i * C, s_par[nn + n + i] * (yv + acc));
     }
@@ -269,47 +287,96 @@ __global__ __launch_bounds__(kGenThreads) void gen_mix_fwd_kernel(GenArgs A) {
 
 // post-combine VJP: dx_j = a_j sum_i M_ij p_i g_i, dy_i = p_i g_i and the
 // sums S_ij = sum g_i x_j, Yd_i = sum g_i y_i (one partial row per workgroup).
-template <typename XT, typename YT, typename GT>
+// dx runs from g in registers against rows of (M^T p) a in LDS.  S and Yd
+// are taken per token in 4 x 4 blocks of rows g_i and columns x_j (column n:
+// y_i of the same row), one block per wavefront at a time with the lanes
+// over consecutive channels; each entry belongs to one wavefront, so the
+// LDS sums have a fixed order.
+template <typename XT, typename YT, typename GT, int NMAX>
 __global__ __launch_bounds__(kGenThreads) void gen_mix_bwd_kernel(GenArgs A) {
+  constexpr int NE = NMAX + 1;
   __shared__ float s_par[kGenMaxPar];
-  __shared__ float s_acc[MHC_MAX_N * MHC_MAX_N + MHC_MAX_N];
+  __shared__ __align__(16) float s_W[NMAX * NMAX];  // s_W[j][i] = a_j M_ij p_i
+  __shared__ float s_acc[NMAX * NE];
   const int n = A.n, C = A.C, nn = n * n, K = nn + n;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   gen_stage(s_par, A.M, A.hpre, A.hpost, n, A.h_mode);
-  for (int k = threadIdx.x; k < K; k += blockDim.x) s_acc[k] = 0.0f;
+  for (int k = threadIdx.x; k < NMAX * NE; k += blockDim.x) s_acc[k] = 0.0f;
+  __syncthreads();
+  for (int k = threadIdx.x; k < NMAX * NMAX; k += blockDim.x) {
+    const int j = k / NMAX, i = k % NMAX;
+    s_W[k] = (i < n && j < n) ? s_par[nn + j] * s_par[i * n + j] * s_par[nn + n + i] : 0.0f;
+  }
   __syncthreads();
   const XT* X = (const XT*)A.x;
   const YT* Y = (const YT*)A.y;
   const GT* Gd = (const GT*)A.g;
   XT* DX = (XT*)A.out;
   YT* DY = (YT*)A.dy;
+  const int nbr = (n + 3) / 4, nbc = (n + 1 + 3) / 4;  // row blocks, column blocks (column n: y)
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x) {
     const int64_t tb = t * n * C;
     for (int c = threadIdx.x; c < C; c += blockDim.x) {
+      float gv[NMAX];
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) gv[i] = i < n ? load1<GT>(Gd + tb + (int64_t)i * C + c) : 0.0f;
       for (int j = 0; j < n; ++j) {
+        const float4* Wj = reinterpret_cast<const float4*>(s_W + j * NMAX);
         float acc = 0.0f;
-        for (int i = 0; i < n; ++i)
-          acc = fmaf(s_par[nn + n + i] * s_par[i * n + j], load1<GT>(Gd + tb + (int64_t)i * C + c), acc);
-        store1<XT>(DX + tb + (int64_t)j * C + c, s_par[nn + j] * acc);
-        if (DY) store1<YT>(DY + tb + (int64_t)j * C + c, s_par[nn + n + j] * load1<GT>(Gd + tb + (int64_t)j * C + c));
+#pragma unroll
+        for (int i4 = 0; i4 < NMAX / 4; ++i4) {
+          const float4 m = Wj[i4];
+          acc = fmaf(m.x, gv[4 * i4], acc);
+          acc = fmaf(m.y, gv[4 * i4 + 1], acc);
+          acc = fmaf(m.z, gv[4 * i4 + 2], acc);
+          acc = fmaf(m.w, gv[4 * i4 + 3], acc);
+        }
+        store1<XT>(DX + tb + (int64_t)j * C + c, acc);
+      }
+      if (DY) {
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i)
+          if (i < n) store1<YT>(DY + tb + (int64_t)i * C + c, s_par[nn + n + i] * gv[i]);
       }
     }
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-      float s = 0.0f;
-      if (k < nn) {
-        const int i = k / n, j = k % n;
-        for (int c = 0; c < C; ++c)
-          s = fmaf(load1<GT>(Gd + tb + (int64_t)i * C + c), load1<XT>(X + tb + (int64_t)j * C + c), s);
-      } else if (Y) {
-        const int i = k - nn;
-        for (int c = 0; c < C; ++c)
-          s = fmaf(load1<GT>(Gd + tb + (int64_t)i * C + c), load1<YT>(Y + tb + (int64_t)i * C + c), s);
+    for (int blk = wave; blk < nbr * nbc; blk += nwaves) {
+      const int r0 = (blk / nbc) * 4, c0 = (blk % nbc) * 4;
+      float acc[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+      for (int c = lane; c < C; c += 64) {
+        float rv[4], cv[4], yv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int ri = r0 + e, cj = c0 + e;
+          rv[e] = ri < n ? load1<GT>(Gd + tb + (int64_t)ri * C + c) : 0.0f;
+          cv[e] = cj < n ? load1<XT>(X + tb + (int64_t)cj * C + c) : 0.0f;
+          yv[e] = (Y && c0 + 3 >= n && ri < n) ? load1<YT>(Y + tb + (int64_t)ri * C + c) : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int f = e & 3;
+          const float col = (c0 + f == n) ? yv[e >> 2] : cv[f];
+          acc[e] = fmaf(rv[e >> 2], col, acc[e]);
+        }
       }
-      s_acc[k] += s;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = wave_sum(acc[e]);
+        const int i = r0 + (e >> 2), j = c0 + (e & 3);
+        if (lane == 0 && i < n && j <= n) s_acc[i * NE + j] += v;
+      }
     }
   }
   __syncthreads();
   float* prow = A.part + (int64_t)blockIdx.x * A.P;
-  for (int k = threadIdx.x; k < A.P; k += blockDim.x) prow[k] = k < K ? s_acc[k] : 0.0f;
+  // [S n*n | Yd n], then zero padding
+  for (int k = threadIdx.x; k < A.P; k += blockDim.x) {
+    float v = 0.0f;
+    if (k < nn) v = s_acc[(k / n) * NE + (k % n)];
+    else if (k < K) v = s_acc[(k - nn) * NE + n];
+    prow[k] = v;
+  }
 }
 
 template <typename F>
@@ -380,8 +447,12 @@ int gen_mix_fwd(const GenArgs& A, int xd, int yd, int od, hipStream_t s) {
       using YT = std::remove_pointer_t<decltype(yp)>;
       return by_pair<XT>(od, [&](auto* op) {
         using OT = std::remove_pointer_t<decltype(op)>;
-        hipLaunchKernelGGL((gen_mix_fwd_kernel<XT, YT, OT>), dim3((unsigned)blocks), dim3(kGenThreads), 0,
-                           s, A);
+        if (A.n <= 32)
+          hipLaunchKernelGGL((gen_mix_fwd_kernel<XT, YT, OT, 32>), dim3((unsigned)blocks), dim3(kGenThreads), 0,
+                             s, A);
+        else
+          hipLaunchKernelGGL((gen_mix_fwd_kernel<XT, YT, OT, 64>), dim3((unsigned)blocks), dim3(kGenThreads), 0,
+                             s, A);
         MHC_CHECK_LAUNCH("gen_mix_fwd_kernel");
         return MHC_OK;
       });
@@ -396,8 +467,12 @@ int gen_mix_bwd(const GenArgs& A, int xd, int yd, int gd, hipStream_t s, int64_t
       using YT = std::remove_pointer_t<decltype(yp)>;
       return by_pair<XT>(gd, [&](auto* gp) {
         using GT = std::remove_pointer_t<decltype(gp)>;
-        hipLaunchKernelGGL((gen_mix_bwd_kernel<XT, YT, GT>), dim3((unsigned)blocks), dim3(kGenThreads), 0,
-                           s, A);
+        if (A.n <= 32)
+          hipLaunchKernelGGL((gen_mix_bwd_kernel<XT, YT, GT, 32>), dim3((unsigned)blocks), dim3(kGenThreads), 0,
+                             s, A);
+        else
+          hipLaunchKernelGGL((gen_mix_bwd_kernel<XT, YT, GT, 64>), dim3((unsigned)blocks), dim3(kGenThreads), 0,
+                             s, A);
         MHC_CHECK_LAUNCH("gen_mix_bwd_kernel");
         return MHC_OK;
       });
