@@ -13,7 +13,7 @@ import torch
 from oracle import mhc_oracle as O
 from tests._helpers import dev_tensor, np_of, params, rel_err, rng, to_dtype_np
 
-from mhc_mlx_amd import MHCLayer, _lib
+from mhc_mlx_amd import MHCLayer, MHCRewire, _lib
 
 pytestmark = pytest.mark.gpu
 
@@ -163,6 +163,46 @@ def test_determinism_and_state_dict():
     assert list(a.state_dict().keys()) == ["H_pre_raw", "H_post_raw", "H_res_raw", "rms_weight"]
     x = torch.randn(1, 16, 64, device="cuda")
     assert torch.equal(a(x), b(x))
+
+
+@pytest.mark.parametrize("T,n,C", [(300, 16, 512), (70, 32, 96), (40, 24, 48), (20, 64, 32)])
+def test_backward_bitwise_reproducible(T, n, C):
+    """Fixed-order sums: two fwd+bwd runs give bitwise equal gradients (n = 16 layer-wide MFMA
+    backward; the 16 < n <= 64 kernels, whose outer-product blocks each belong to one wavefront)."""
+    torch.manual_seed(T + n + C)
+    layer = MHCLayer(n=n, C=C, eps=1e-6, identity_init=False).cuda()
+    with torch.no_grad():
+        for p in (layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw):
+            p.normal_()
+    x = torch.randn(T, n, C, device="cuda", dtype=torch.bfloat16).requires_grad_(True)
+    g = torch.randn(T, n, C, device="cuda", dtype=torch.bfloat16)
+    params = list(layer.parameters())
+    runs = []
+    for _ in range(2):
+        out = layer(x, return_dtype=torch.bfloat16)
+        runs.append([out] + list(torch.autograd.grad(out, [x] + params, g)))
+    for a, b in zip(*runs):
+        assert torch.isfinite(a.float()).all()
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("n", [32, 20])
+def test_rewire_backward_bitwise_reproducible(n):
+    """The post-combine VJP for 16 < n <= 64 (MHCRewire's default n = 32) is run-to-run exact."""
+    torch.manual_seed(n)
+    dims = 40 * n
+    inner = torch.nn.Linear(dims, dims, bias=False).cuda()
+    m = MHCRewire(inner, dims=dims, n=n, identity_init=False).cuda()
+    with torch.no_grad():
+        for p in (m.mhc.H_pre_raw, m.mhc.H_post_raw, m.mhc.H_res_raw):
+            p.normal_()
+    x = torch.randn(50, dims, device="cuda").requires_grad_(True)
+    g = torch.randn(50, dims, device="cuda")
+    prm = [x, inner.weight, m.mhc.H_pre_raw, m.mhc.H_post_raw, m.mhc.H_res_raw]
+    a = torch.autograd.grad(m(x), prm, g)
+    b = torch.autograd.grad(m(x), prm, g)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
 
 
 def test_mixing_matrix_doubly_stochastic_and_bomb():
