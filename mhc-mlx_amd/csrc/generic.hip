@@ -13,6 +13,12 @@ namespace mhc {
 namespace {
 
 constexpr int kGenThreads = 256;
+// The layer backward takes its parameter sums one 4 x 4 block per wavefront;
+// at n <= 32 its registers allow 512-thread workgroups (at most 256 VGPRs),
+// which measured 4.7 -> 3.0 ms at n = 32.  The post-combine VJP measured
+// slower with 1024 threads (0.97 -> 1.24 ms) and keeps kGenThreads.
+constexpr int gen_bwd_threads(int nmax) { return nmax <= 32 ? 512 : 256; }
+constexpr int kGenMaxWaves = 8;
 constexpr int kGenMaxPar = MHC_MAX_N * MHC_MAX_N + 2 * MHC_MAX_N;
 
 // params for token t: M [n*n], a [n], p [n] (activated), compact n-indexing
@@ -118,12 +124,12 @@ __global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(GenArgs A) {
 //          layer-wide parameters, or straight to the per-token outputs.
 //          Each entry belongs to one wavefront, so the order is fixed.
 template <typename XT, typename GT, int NMAX>
-__global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs A) {
+__global__ __launch_bounds__(gen_bwd_threads(NMAX)) void gen_bwd_kernel(GenArgs A) {
   constexpr int NE = NMAX + 1;  // extended rows / columns
   __shared__ float s_par[kGenMaxPar];
   __shared__ __align__(16) float s_MT[NMAX * NMAX];
   __shared__ float s_acc[NE * NE];
-  __shared__ float s_red[2][2][kGenThreads / 64];
+  __shared__ float s_red[2][2][kGenMaxWaves];
   const int n = A.n, C = A.C, nn = n * n;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   const int nb = (n + 1 + 3) / 4;  // 4-wide blocks of the n + 1 rows (and columns)
@@ -429,9 +435,11 @@ int gen_fused_bwd(const GenArgs& A, int xd, int gd, hipStream_t s, int64_t* num_
     return by_pair<XT>(gd, [&](auto* gp) {
       using GT = std::remove_pointer_t<decltype(gp)>;
       if (A.n <= 32)
-        hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 32>), dim3((unsigned)blocks), dim3(kGenThreads), 0, s, A);
+        hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 32>), dim3((unsigned)blocks), dim3(gen_bwd_threads(32)), 0, s,
+                           A);
       else
-        hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 64>), dim3((unsigned)blocks), dim3(kGenThreads), 0, s, A);
+        hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 64>), dim3((unsigned)blocks), dim3(gen_bwd_threads(64)), 0, s,
+                           A);
       MHC_CHECK_LAUNCH("gen_bwd_kernel");
       return MHC_OK;
     });
