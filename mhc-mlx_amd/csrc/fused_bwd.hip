@@ -1008,8 +1008,10 @@ constexpr int kMf16MaxWaves = 8;
 // dA and dP are then added into per-thread sums across the workgroup's
 // tokens and end in its partial row after the dw slice, unactivated (the
 // reduction applies the activation chain to the totals).
-template <typename XT, int SPW, bool RAW, bool LW>
-__global__ __launch_bounds__(SPW == 2 ? 256 : 512) __attribute__((amdgpu_waves_per_eu(2)))
+// WIDE: two slabs per wave with up to 8 waves, C up to 2048 (one workgroup
+// per CU: its staged slabs take ~140 KB of LDS).
+template <typename XT, int SPW, bool RAW, bool LW, bool WIDE = false>
+__global__ __launch_bounds__(SPW == 2 && !WIDE ? 256 : 512) __attribute__((amdgpu_waves_per_eu(2)))
 void fused_bwd_mfma16_kernel(BwdArgs A) {
   constexpr int N = 16;
   constexpr int64_t PS = LW ? 0 : 16;   // parameter strides per token
@@ -1021,12 +1023,12 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
   for (int e = 0; e < KPT; ++e) lw_acc[e] = 0.0f;
   constexpr int SLAB = 2 * N * kMf16Row;  // 16-bit elements of one staged slab (x rows, then g rows)
   extern __shared__ uint16_t mf_lds[];
-  constexpr int MW = SPW == 2 ? 4 : kMf16MaxWaves;  // waves per workgroup at most
+  constexpr int MW = SPW == 2 && !WIDE ? 4 : kMf16MaxWaves;  // waves per workgroup at most
   __shared__ float s_red[2][2][MW];
   __shared__ float s_dm[MW][256];
   __shared__ float s_ap[MW][32];
   __shared__ float s_act[2][32];  // activated a, p of the token (parity-buffered)
-  __shared__ __align__(16) float s_w[1024];
+  __shared__ __align__(16) float s_w[WIDE ? 2048 : 1024];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -1516,12 +1518,34 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
 // Per-token n == 16 with 16-bit x == dout and C a multiple of 256 up to 1024
 // (fused_bwd_pt16_kernel).  Returns 1 when the shape is not covered.
 // n == 16 on MFMA (fused_bwd_mfma16_kernel), per-token or (LW) layer-wide
-// parameters: 16-bit x == dout, C a multiple of 128 up to 1024 (two
-// 128-channel slabs per wave when C / 128 is even, else one), 16-byte aligned
-// operands.  Returns 1 when the shape is not covered.
+// parameters: 16-bit x == dout, C a multiple of 128 up to 1024, or up to
+// 2048 with two slabs per wave (two 128-channel slabs per wave when C / 128
+// is even, else one), 16-byte aligned operands.  Returns 1 when the shape is
+// not covered.
+template <typename XT, int SPW, bool LW, bool WIDE>
+int launch_mf16_variant(BwdArgs A, const BwdLayout& L, int waves, int64_t* num_partials, hipStream_t stream) {
+  const size_t smem = (size_t)waves * SPW * 2 * 16 * kMf16Row * sizeof(uint16_t);
+  const bool raw = A.h_mode == MHC_H_RAW;
+  const void* kfn = raw ? (const void*)fused_bwd_mfma16_kernel<XT, SPW, true, LW, WIDE>
+                        : (const void*)fused_bwd_mfma16_kernel<XT, SPW, false, LW, WIDE>;
+  const int occ = occupancy_blocks(kfn, waves * 64, smem);
+  if (occ <= 0) return 1;
+  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
+  const int grid_pref = env_int("MHC_BWD_GRID", 0);
+  if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+  set_rows(A, L);
+  const dim3 g((unsigned)blocks), b(waves * 64);
+  if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, SPW, true, LW, WIDE>), g, b, smem, stream, A);
+  else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, SPW, false, LW, WIDE>), g, b, smem, stream, A);
+  MHC_CHECK_LAUNCH("fused_bwd_mfma16_kernel");
+  *num_partials = blocks;
+  return MHC_OK;
+}
+
 template <typename XT, bool LW>
 int launch_bwd_mfma16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
-  if (A.n != 16 || A.C % 128 != 0 || A.C > 1024) return 1;
+  if (A.n != 16 || A.C % 128 != 0 || A.C > 2048) return 1;
   if (LW && L.P != L.Cp + 256 + 32) return 1;
   if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.dx, 16) || !aligned(A.M, 16) ||
       !aligned(A.hpre, 16) || !aligned(A.hpost, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
@@ -1532,31 +1556,13 @@ int launch_bwd_mfma16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipS
   if (spw != 1 && spw != 2) spw = 1;
   if (S % spw != 0) spw = 1;
   const int waves = S / spw;
-  if (waves > (spw == 2 ? 4 : kMf16MaxWaves)) return 1;
-  const size_t smem = (size_t)waves * spw * 2 * 16 * kMf16Row * sizeof(uint16_t);
-  const bool raw = A.h_mode == MHC_H_RAW;
-  const void* kfn = spw == 2 ? (raw ? (const void*)fused_bwd_mfma16_kernel<XT, 2, true, LW>
-                                    : (const void*)fused_bwd_mfma16_kernel<XT, 2, false, LW>)
-                             : (raw ? (const void*)fused_bwd_mfma16_kernel<XT, 1, true, LW>
-                                    : (const void*)fused_bwd_mfma16_kernel<XT, 1, false, LW>);
-  const int occ = occupancy_blocks(kfn, waves * 64, smem);
-  if (occ <= 0) return 1;
-  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
-  const int grid_pref = env_int("MHC_BWD_GRID", 0);
-  if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
-  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
-  set_rows(A, L);
-  const dim3 g((unsigned)blocks), b(waves * 64);
-  if (spw == 2) {
-    if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 2, true, LW>), g, b, smem, stream, A);
-    else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 2, false, LW>), g, b, smem, stream, A);
-  } else {
-    if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 1, true, LW>), g, b, smem, stream, A);
-    else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, 1, false, LW>), g, b, smem, stream, A);
+  if (spw == 1) {
+    if (waves > kMf16MaxWaves) return 1;
+    return launch_mf16_variant<XT, 1, LW, false>(A, L, waves, num_partials, stream);
   }
-  MHC_CHECK_LAUNCH("fused_bwd_mfma16_kernel");
-  *num_partials = blocks;
-  return MHC_OK;
+  if (waves <= 4) return launch_mf16_variant<XT, 2, LW, false>(A, L, waves, num_partials, stream);
+  if (waves > kMf16MaxWaves) return 1;
+  return launch_mf16_variant<XT, 2, LW, true>(A, L, waves, num_partials, stream);
 }
 
 template <typename XT>

@@ -83,7 +83,8 @@ def test_config1_forward_bf16():
 
 @pytest.mark.parametrize("T,n,C,dt", [(300, 4, 1024, "bf16"), (300, 4, 1024, "f32"), (300, 8, 512, "bf16"),
                                       (600, 4, 1024, "bf16"), (40, 4, 2048, "f16"),
-                                      (700, 16, 1024, "bf16"), (300, 16, 512, "f16"), (50, 16, 128, "bf16")])
+                                      (700, 16, 1024, "bf16"), (300, 16, 512, "f16"), (50, 16, 128, "bf16"),
+                                      (300, 16, 2048, "bf16")])
 def test_full_tile_paths_fwd_bwd(T, n, C, dt):
     """T >= CU count (two chunks per thread), C a multiple of the tile, > 64 partial rows."""
     g = rng(T + n + C)
@@ -278,7 +279,9 @@ def test_config4_rewire_linear_full_size():
 
 
 @pytest.mark.parametrize("T,C,dt", [(300, 1024, "bf16"), (40, 256, "bf16"), (70, 512, "f16"), (3, 1024, "bf16"),
-                                   (50, 384, "bf16"), (20, 128, "f16"), (9, 768, "bf16"), (1500, 256, "bf16")])
+                                   (50, 384, "bf16"), (20, 128, "f16"), (9, 768, "bf16"), (1500, 256, "bf16"),
+                                   # two slabs per wave with 5-8 waves (C up to 2048)
+                                   (300, 2048, "bf16"), (40, 1280, "f16")])
 def test_per_token_n16_mfma_path(T, C, dt):
     """Per-token n=16 with C a multiple of 128 (the MFMA kernels: one or two 128-channel slabs per wave;
     T = 1500 exceeds the persistent backward grid, so workgroups walk several tokens), all gradients."""
