@@ -526,8 +526,13 @@ struct LwCfg {
 
 template <int NMAX, typename XT, typename GT>
 constexpr int lw_vec() {
-  return (NMAX <= 4 ? 16 : 8) / LwCfg<XT, GT>::kElem;
+  return 16 / LwCfg<XT, GT>::kElem;
 }
+
+// Largest workgroup of the layer-wide backward.  n <= 4 keeps a 1024-thread
+// bound (128 VGPRs).  n = 8 (64 dM sums per thread) is bounded at 512
+// threads, so it gets 256 VGPRs without spilling and 16-byte chunks.
+constexpr int lw_max_threads(int nmax) { return nmax <= 4 ? 1024 : 512; }
 
 template <typename T>
 MHC_DEV float dot2_acc(uint32_t g, uint32_t x, float acc);
@@ -553,7 +558,8 @@ MHC_DEV void reg_fence(uint32_t& w) { asm volatile("" : "+v"(w)); }
 #endif
 
 template <int NMAX, typename XT, typename GT, int CHK, bool FULL>
-__global__ __attribute__((amdgpu_flat_work_group_size(64, 1024), amdgpu_waves_per_eu(MHC_BWD_WPE)))
+__global__ __attribute__((amdgpu_flat_work_group_size(64, lw_max_threads(NMAX)),
+                          amdgpu_waves_per_eu(NMAX <= 4 ? MHC_BWD_WPE : 2)))
 void fused_bwd_lw_kernel(BwdArgs A) {
   constexpr int V = lw_vec<NMAX, XT, GT>();
   constexpr int K = NMAX * NMAX + 2 * NMAX;
@@ -1495,7 +1501,7 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
   constexpr int V = lw_vec<NMAX, XT, GT>();
   A.nchunks = (int)ceil_div(A.C, V);
   const int tpb = std::max(64, round_up(A.nchunks, 64));
-  if (tpb > 1024) return 1;
+  if (tpb > lw_max_threads(NMAX)) return 1;
   const bool full = A.n == NMAX && A.vec && A.C % V == 0 && A.nchunks == tpb;
   // Grid: the workspace's full row budget (8 workgroups per CU) streams
   // faster than one resident wave of workgroups (562 vs 576 us at config 2);
