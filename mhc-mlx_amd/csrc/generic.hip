@@ -1,7 +1,10 @@
-// Runtime-n kernels for 16 < n <= 64 (the reference allows n up to 64:
-// metal.py:71).  Compact code with runtime loops over streams; one workgroup
-// per token (persistent), threads over channels.  The register-tiled kernels
-// in fused_fwd.hip / fused_bwd.hip / stream_mix.hip cover n <= 16.
+// Kernels for 16 < n <= 64 (the reference allows n up to 64: metal.py:71),
+// templated on NMAX = 32 or 64 register slots per channel with runtime n.
+// A persistent workgroup walks tokens; threads own channels, keep a
+// channel's n values in registers and mix them against rows of M broadcast
+// from LDS; parameter-gradient sums are 4 x 4 outer-product blocks, one per
+// wavefront.  The kernels in fused_fwd.hip / fused_bwd.hip / stream_mix.hip
+// cover n <= 16.
 #include "mhc_device.hpp"
 #include "mhc_generic.hpp"
 #include "mhc_host.hpp"
