@@ -84,7 +84,9 @@ def test_config1_forward_bf16():
 @pytest.mark.parametrize("T,n,C,dt", [(300, 4, 1024, "bf16"), (300, 4, 1024, "f32"), (300, 8, 512, "bf16"),
                                       (600, 4, 1024, "bf16"), (40, 4, 2048, "f16"),
                                       (700, 16, 1024, "bf16"), (300, 16, 512, "f16"), (50, 16, 128, "bf16"),
-                                      (300, 16, 2048, "bf16")])
+                                      (300, 16, 2048, "bf16"),
+                                      # n = 8 with 16-byte chunks: 512-thread workgroups at C = 4096
+                                      (200, 8, 4096, "bf16"), (100, 8, 2048, "f16")])
 def test_full_tile_paths_fwd_bwd(T, n, C, dt):
     """T >= CU count (two chunks per thread), C a multiple of the tile, > 64 partial rows."""
     g = rng(T + n + C)
