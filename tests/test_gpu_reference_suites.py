@@ -194,7 +194,7 @@ def test_multiprocess_fwd_bwd():
         for p in procs:
             p.start()
         for p in procs:
-            p.join(timeout=100)
+            p.join(timeout=240)  # each child imports torch first
         for p in procs:
             assert p.exitcode == 0, p.exitcode
         results = dict(q.get(timeout=5) for _ in procs)
