@@ -557,7 +557,12 @@ MHC_DEV void reg_fence(uint32_t& w) { asm volatile("" : "+v"(w)); }
 #define MHC_BWD_WPE 4
 #endif
 
-template <int NMAX, typename XT, typename GT, int CHK, bool FULL>
+// PT: per-token parameters (M_ts = n*n, h_ts = n).  The token's M, a and p
+// are loaded at the top of each token, and its dM, dA and dP sums go through
+// the same wave + LDS reduction at the end of each token to the per-token
+// outputs (dA and dP through the activation chain when RAW); only dw stays
+// in registers across tokens.
+template <int NMAX, typename XT, typename GT, int CHK, bool FULL, bool PT = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(64, lw_max_threads(NMAX)),
                           amdgpu_waves_per_eu(NMAX <= 4 ? MHC_BWD_WPE : 2)))
 void fused_bwd_lw_kernel(BwdArgs A) {
@@ -580,22 +585,25 @@ void fused_bwd_lw_kernel(BwdArgs A) {
   float* prow = A.part + (int64_t)blockIdx.x * A.P;
 
   float Ms[NMAX * NMAX], as[NMAX], ps[NMAX];
+  auto load_params = [&](const float* Mt, const float* hp, const float* hq) {
 #pragma unroll
-  for (int i = 0; i < NMAX; ++i) {
-    float av = 0.0f, pq = 0.0f;
-    if (i < n) {
-      av = A.hpre[i];
-      pq = A.hpost[i];
-      if (A.h_mode == MHC_H_RAW) {
-        av = sigmoidf_(av);
-        pq = 2.0f * sigmoidf_(pq);
+    for (int i = 0; i < NMAX; ++i) {
+      float av = 0.0f, pq = 0.0f;
+      if (i < n) {
+        av = hp[i];
+        pq = hq[i];
+        if (A.h_mode == MHC_H_RAW) {
+          av = sigmoidf_(av);
+          pq = 2.0f * sigmoidf_(pq);
+        }
       }
-    }
-    as[i] = uniform_f(av);
-    ps[i] = uniform_f(pq);
+      as[i] = uniform_f(av);
+      ps[i] = uniform_f(pq);
 #pragma unroll
-    for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = uniform_f((i < n && j < n) ? A.M[i * n + j] : 0.0f);
-  }
+      for (int j = 0; j < NMAX; ++j) Ms[i * NMAX + j] = uniform_f((i < n && j < n) ? Mt[i * n + j] : 0.0f);
+    }
+  };
+  if constexpr (!PT) load_params(A.M, A.hpre, A.hpost);
 
   int c0[CHK], valid[CHK];
   float wv[CHK][V], dwv[CHK][V];
@@ -623,6 +631,7 @@ void fused_bwd_lw_kernel(BwdArgs A) {
     XT* dxt = DX + t * nC;
     Vec<XT, V> xr[CHK][NMAX];
     Vec<GT, V> gr[CHK][NMAX];
+    if constexpr (PT) load_params(A.M + t * A.M_ts, A.hpre + t * A.h_ts, A.hpost + t * A.h_ts);
 #pragma unroll
     for (int k = 0; k < CHK; ++k) {
 #pragma unroll
@@ -739,6 +748,45 @@ void fused_bwd_lw_kernel(BwdArgs A) {
         }
       }
     }
+    if constexpr (PT) {
+      // the token's parameter sums: wave sums, then the waves in order
+#pragma unroll
+      for (int k = 0; k < NMAX * NMAX; ++k) {
+        const float v = wave_sum(accM[k]);
+        accM[k] = 0.0f;
+        if (lane == 0) s_acc[wave][k] = v;
+      }
+#pragma unroll
+      for (int k = 0; k < NMAX; ++k) {
+        const float va = wave_sum(accA[k]), vp = wave_sum(accP[k]);
+        accA[k] = accP[k] = 0.0f;
+        if (lane == 0) {
+          s_acc[wave][NMAX * NMAX + k] = va;
+          s_acc[wave][NMAX * NMAX + NMAX + k] = vp;
+        }
+      }
+      __syncthreads();
+      for (int k = tid; k < K; k += blockDim.x) {
+        float sum = 0.0f;
+        for (int w = 0; w < nwaves; ++w) sum += s_acc[w][k];
+        if (k < NMAX * NMAX) {
+          const int i = k / NMAX, j = k % NMAX;
+          if (i < n && j < n) A.dM_tok[t * n * n + i * n + j] = sum;
+        } else if (k < NMAX * NMAX + NMAX) {
+          const int j = k - NMAX * NMAX;
+          if (j < n) {
+            const float av = as[j];
+            A.dpre_tok[t * n + j] = A.h_mode == MHC_H_RAW ? sum * av * (1.0f - av) : sum;
+          }
+        } else {
+          const int i = k - NMAX * NMAX - NMAX;
+          if (i < n) {
+            const float pq = ps[i];
+            A.dpost_tok[t * n + i] = A.h_mode == MHC_H_RAW ? sum * pq * (1.0f - 0.5f * pq) : sum;
+          }
+        }
+      }
+    }
   }
 
   // ---- this workgroup's partial row: dw slice, then wave and block sums
@@ -750,6 +798,7 @@ void fused_bwd_lw_kernel(BwdArgs A) {
   }
   if (tid == 0)
     for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
+  if constexpr (PT) return;  // per-token sums are already out; the row is dw only
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const float v = k < NMAX * NMAX ? accM[k] : (k < NMAX * NMAX + NMAX ? accA[k - NMAX * NMAX]
@@ -1496,7 +1545,7 @@ void set_rows(BwdArgs& A, const BwdLayout& L) {
 // Layer-wide n <= 8 (fused_bwd_lw_kernel).  Returns 1 when the shape is not
 // covered (C too large for one chunk per thread), so the caller falls back
 // to fused_bwd_kernel.
-template <int NMAX, typename XT, typename GT>
+template <int NMAX, typename XT, typename GT, bool PT>
 int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
   constexpr int V = lw_vec<NMAX, XT, GT>();
   A.nchunks = (int)ceil_div(A.C, V);
@@ -1513,9 +1562,9 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
   set_rows(A, L);
   const dim3 g((unsigned)blocks), b(tpb);
   if (full)
-    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, true>), g, b, 0, stream, A);
+    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, true, PT>), g, b, 0, stream, A);
   else
-    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, false>), g, b, 0, stream, A);
+    hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, false, PT>), g, b, 0, stream, A);
   MHC_CHECK_LAUNCH("fused_bwd_lw_kernel");
   *num_partials = blocks;
   return MHC_OK;
@@ -1600,10 +1649,10 @@ int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t
     rc = launch_bwd_pt16<XT>(A, L, num_partials, stream);
     if (rc != 1) return rc;
   }
-  if constexpr (!PT && NMAX <= 8) {
+  if constexpr (NMAX <= 8) {
     static const int legacy = env_int("MHC_BWD_LEGACY", 0);
     if (!legacy) {
-      const int rc = launch_bwd_lw<NMAX, XT, GT>(A, L, num_partials, stream);
+      const int rc = launch_bwd_lw<NMAX, XT, GT, PT>(A, L, num_partials, stream);
       if (rc != 1) return rc;
     }
   }
