@@ -7,34 +7,87 @@ Forward semantics (layer.py:1-12):
   out = stream_mix(x, M) + H_post_act * rms_norm(sum_i H_pre_act[i] x[:, i], w)
 
 Paths:
-* accelerated (default, ``use_metal=True``): one autograd Function per call
-  (Sinkhorn + fused kernel forward; fused backward + reduction + Sinkhorn
-  VJP), all in libmhc_hip.  GPU tensors are required; errors raise.
-* reference (``use_metal=False`` or ``MHC_MLX_DISABLE_METAL=1`` /
-  ``MHC_HIP_DISABLE=1``): the torch restatement in reference.py, as the
-  reference layer does (layer.py:122-126, 423-431).
+* accelerated (default, ``use_metal=True`` on a host with a GPU): one
+  autograd Function per call (Sinkhorn + fused kernel forward; fused
+  backward + reduction + Sinkhorn VJP), all in libmhc_hip.
+* reference: the torch restatement in reference.py.  It runs when
+  ``use_metal=False``, when ``MHC_MLX_DISABLE_METAL=1`` / ``MHC_HIP_DISABLE=1``,
+  or when no GPU is visible (``metal_available`` is False), as the reference
+  layer does when Metal is absent (layer.py:122-126).
+
+Failures of the accelerated path follow the reference (layer.py:28-29,
+158-173, 306-330, 408-422): a RuntimeError raised by the library (a HIP
+error, an allocation failure) or inputs that the HIP path cannot take (CPU
+tensors) are reported once through ``warnings.warn`` and the module flag
+``_METAL_FAILED``, and that call runs the reference path.  A GPU host whose
+libmhc_hip.so is missing or unloadable is an installation error: the
+constructor raises RuntimeError naming the build command instead of
+degrading silently.  Argument errors (ValueError) always propagate.
 
 The reference's dispatch-policy knobs are accepted with the same validation
-and the same predicates (``_should_avoid_fused`` etc.).  On MI355X every
-branch they select is served by the HIP kernels: the reference used them to
-route around slow Metal shapes, which this library does not have.
+and the same predicates (``_should_avoid_fused`` etc.).  The policy routes
+the reference to its MLX path for shapes its Metal kernels handled badly;
+libmhc_hip serves every n <= 64 shape with its own kernels, so here the
+predicates are informational and every such call stays on the HIP path.
 """
 
 from __future__ import annotations
 
 import os
+import warnings
 
 import torch
 import torch.nn as nn
 
-from . import ops
+from . import _lib, ops
 from . import reference as ref
 
-__all__ = ["MHCLayer", "MHCRewire"]
+__all__ = ["MHCLayer", "MHCRewire", "hip_available"]
+
+# Set once the accelerated path has handed a call to the reference path
+# (layer.py:28-29); the warning is issued only the first time.
+_METAL_FAILED = False
+
+_HIP_AVAILABLE: bool | None = None
 
 
 def _disabled_by_env() -> bool:
     return os.getenv("MHC_MLX_DISABLE_METAL", "0") == "1" or os.getenv("MHC_HIP_DISABLE", "0") == "1"
+
+
+def hip_available() -> bool:
+    """Whether the HIP path can run here: a GPU is visible and libmhc_hip.so loads.
+
+    The analogue of the reference's ``hasattr(mx.fast, "metal_kernel")``
+    (layer.py:122).  False when torch sees no GPU.  With a GPU visible the
+    library must load: a missing or broken build raises RuntimeError (naming
+    the build command) rather than reporting False.
+    """
+    global _HIP_AVAILABLE
+    if _HIP_AVAILABLE is None:
+        if not torch.cuda.is_available():
+            _HIP_AVAILABLE = False
+        else:
+            _lib.load()
+            _HIP_AVAILABLE = True
+    return _HIP_AVAILABLE
+
+
+def _fallback_warning(where: str, err) -> None:
+    """Warn once per process that the accelerated path handed a call to the reference path."""
+    global _METAL_FAILED
+    if not _METAL_FAILED:
+        warnings.warn(f"HIP kernel execution failed{where}, falling back to reference path. Error: {err}",
+                      RuntimeWarning, stacklevel=3)
+        _METAL_FAILED = True
+
+
+def _off_gpu(*ts) -> str | None:
+    """None when every tensor is on a GPU, else a reason naming the first that is not."""
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            return f"the HIP path needs GPU tensors (got a tensor on {t.device})"
+    return None
 
 
 class MHCLayer(nn.Module):
@@ -103,8 +156,12 @@ class MHCLayer(nn.Module):
         self.mix_kernel = str(mix_kernel)
         accel = bool(use_metal) if use_hip is None else bool(use_hip)
         # layer.py:121-126 (Metal availability is HIP availability here)
-        self.metal_available = True
-        self.use_metal = False if _disabled_by_env() else accel
+        if _disabled_by_env() or not accel:
+            self.metal_available = torch.cuda.is_available() and _lib.LIB_PATH.exists()
+            self.use_metal = False
+        else:
+            self.metal_available = hip_available()
+            self.use_metal = self.metal_available
         self.threads_per_group = None if threads_per_group is None else int(threads_per_group)
         self.identity_init = bool(identity_init)
         if compile_reference is None:
@@ -193,9 +250,15 @@ class MHCLayer(nn.Module):
     # ---- API
     def mixing_matrix(self) -> torch.Tensor:
         """Current mixing matrix M = sinkhorn(exp(H_res_raw)) (layer.py:155-173)."""
-        if self.use_metal and self.H_res_raw.is_cuda and not _disabled_by_env():
-            return ops.sinkhorn_knopp_hip_autograd(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps,
-                                                   threads_per_group=self.threads_per_group)
+        if self.use_metal and not _disabled_by_env():
+            why = _off_gpu(self.H_res_raw)
+            if why is None:
+                try:
+                    return ops.sinkhorn_knopp_hip_autograd(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps,
+                                                           threads_per_group=self.threads_per_group)
+                except RuntimeError as e:
+                    why = e
+            _fallback_warning(" in mixing_matrix", why)
         return ref.mixing_matrix_from_logits(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps)
 
     def _reference_forward(self, x, H_pre_raw, H_post_raw, H_res_raw, rms_weight):
@@ -209,11 +272,20 @@ class MHCLayer(nn.Module):
         fp32 out as in the reference; ``return_dtype`` (extension) casts it, and a half type equal to
         x's dtype is written by the kernel directly.
         """
+        out = None
         if self.use_metal and not _disabled_by_env():
-            kdt = self._kernel_out_dtype(x_reshaped, return_dtype)
-            out = ops.post_combine(x_reshaped, y_inner_reshaped, self.H_pre_raw, self.H_post_raw, self.H_res_raw,
-                                   sinkhorn_iters=self.sinkhorn_iters, eps=self.eps, output_dtype=kdt)
-        else:
+            why = _off_gpu(x_reshaped, y_inner_reshaped, self.H_pre_raw, self.H_post_raw, self.H_res_raw)
+            if why is None:
+                kdt = self._kernel_out_dtype(x_reshaped, return_dtype)
+                try:
+                    out = ops.post_combine(x_reshaped, y_inner_reshaped, self.H_pre_raw, self.H_post_raw,
+                                           self.H_res_raw, sinkhorn_iters=self.sinkhorn_iters, eps=self.eps,
+                                           output_dtype=kdt)
+                except RuntimeError as e:
+                    why = e
+            if out is None:
+                _fallback_warning(" in post_combine", why)
+        if out is None:
             H_pre_act, H_post_act = ref.activate_pre_post(self.H_pre_raw, self.H_post_raw)
             M = ref.mixing_matrix_from_logits(self.H_res_raw, iters=self.sinkhorn_iters, eps=self.eps)
             M_final = M * H_pre_act.reshape(1, -1)
@@ -243,11 +315,19 @@ class MHCLayer(nn.Module):
     def forward(self, x_expanded: torch.Tensor, *, return_dtype: torch.dtype | None = None) -> torch.Tensor:
         """Run the mHC layer on x_expanded [B, n, C] (layer.py:339-435)."""
         B, n, C = self._check(x_expanded)
+        out = None
         if self._should_use_metal(B, n, C):
-            out = ops.mhc_layer_forward(x_expanded, self.H_pre_raw, self.H_post_raw, self.H_res_raw, self.rms_weight,
-                                        sinkhorn_iters=self.sinkhorn_iters, eps=self.eps,
-                                        output_dtype=self._kernel_out_dtype(x_expanded, return_dtype))
-        else:
+            why = _off_gpu(x_expanded, self.H_pre_raw, self.H_post_raw, self.H_res_raw, self.rms_weight)
+            if why is None:
+                try:
+                    out = ops.mhc_layer_forward(x_expanded, self.H_pre_raw, self.H_post_raw, self.H_res_raw,
+                                                self.rms_weight, sinkhorn_iters=self.sinkhorn_iters, eps=self.eps,
+                                                output_dtype=self._kernel_out_dtype(x_expanded, return_dtype))
+                except RuntimeError as e:
+                    why = e
+            if out is None:
+                _fallback_warning("", why)
+        if out is None:
             out = self._reference_forward(x_expanded, self.H_pre_raw, self.H_post_raw, self.H_res_raw,
                                           self.rms_weight)
         if return_dtype is not None and out.dtype != return_dtype:
@@ -265,11 +345,20 @@ class MHCLayer(nn.Module):
             raise ValueError(f"H_pre_raw / H_post_raw must be [B, n]=[{B}, {n}]")
         if tuple(H_res_raw.shape) != (B, n, n):
             raise ValueError(f"H_res_raw must be [B, n, n]=[{B}, {n}, {n}], got {tuple(H_res_raw.shape)}")
+        out = None
         if self._should_use_metal(B, n, C):
-            out = ops.mhc_layer_forward_dynamic(x_expanded, H_pre_raw, H_post_raw, H_res_raw, self.rms_weight,
-                                                sinkhorn_iters=self.sinkhorn_iters, eps=self.eps,
-                                                output_dtype=self._kernel_out_dtype(x_expanded, return_dtype))
-        else:
+            why = _off_gpu(x_expanded, H_pre_raw, H_post_raw, H_res_raw, self.rms_weight)
+            if why is None:
+                try:
+                    out = ops.mhc_layer_forward_dynamic(x_expanded, H_pre_raw, H_post_raw, H_res_raw,
+                                                        self.rms_weight, sinkhorn_iters=self.sinkhorn_iters,
+                                                        eps=self.eps,
+                                                        output_dtype=self._kernel_out_dtype(x_expanded, return_dtype))
+                except RuntimeError as e:
+                    why = e
+            if out is None:
+                _fallback_warning(" in forward_dynamic", why)
+        if out is None:
             out = self._reference_forward(x_expanded, H_pre_raw, H_post_raw, H_res_raw, self.rms_weight)
         if return_dtype is not None and out.dtype != return_dtype:
             out = out.to(return_dtype)
@@ -302,10 +391,17 @@ class MHCRewire(nn.Module):
             raise ValueError(f"input dims {dims} must be divisible by n={self.n}")
         C = dims // self.n
         x3 = x.reshape(-1, self.n, C)
-        hip = self.mhc.use_metal and not _disabled_by_env()
-        if hip:
-            x_pre = ops.stream_scale(x3, self.mhc.H_pre_raw)
-        else:
+        x_pre = None
+        if self.mhc.use_metal and not _disabled_by_env():
+            why = _off_gpu(x3, self.mhc.H_pre_raw)
+            if why is None:
+                try:
+                    x_pre = ops.stream_scale(x3, self.mhc.H_pre_raw)
+                except RuntimeError as e:
+                    why = e
+            if x_pre is None:
+                _fallback_warning(" in the MHCRewire pre-scale", why)
+        if x_pre is None:
             H_pre_act, _ = ref.activate_pre_post(self.mhc.H_pre_raw, self.mhc.H_post_raw)
             x_pre = x3 * H_pre_act.reshape(1, self.n, 1).to(x3.dtype)
         y_inner = self.inner(x_pre.reshape(x.shape))

@@ -29,3 +29,24 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(autouse=True)
+def _hip_path_did_not_fall_back(request):
+    """A GPU test must not pass on the module's reference fallback.
+
+    MHCLayer / MHCRewire hand a call to the torch reference path (with one
+    warning) when the HIP path raises or gets CPU tensors; the module flag
+    records it.  Every test marked ``gpu`` starts with the flag clear and
+    fails if it is set at the end, so parity evidence always comes from the
+    library.  A test that exercises the fallback on purpose restores the
+    flag with ``monkeypatch`` (undone before this check runs).
+    """
+    if "gpu" not in request.keywords:
+        yield
+        return
+    from mhc_mlx_amd import layer as L
+
+    L._METAL_FAILED = False
+    yield
+    assert not L._METAL_FAILED, "the HIP path fell back to the torch reference path during this GPU test"

@@ -121,6 +121,40 @@ def test_hip_path_is_the_one_that_runs(monkeypatch):
     assert "mhc_layer_fwd" in calls and "mhc_layer_bwd" in calls
 
 
+def test_gpu_layer_reports_hip_available():
+    from mhc_mlx_amd import layer as L
+
+    layer = MHCLayer(n=4, C=64)
+    assert L.hip_available() is True and layer.metal_available is True and layer.use_metal is True
+
+
+def test_library_failure_falls_back_once_on_gpu(monkeypatch):
+    """A RuntimeError from the library runs the reference path on the same GPU tensors, warned once."""
+    from mhc_mlx_amd import layer as L
+
+    monkeypatch.setattr(L, "_METAL_FAILED", False)  # restored before the session guard checks it
+    orig = _lib.call
+
+    def failing(name, *args):
+        if name == "mhc_layer_fwd":
+            raise _lib.MHCError("mhc_layer_fwd: HIP error 98: injected by the test")
+        return orig(name, *args)
+
+    monkeypatch.setattr(_lib, "call", failing)
+    g = rng(11)
+    B, n, C = 3, 4, 128
+    hpre, hpost, hres, w = params(g, n, C)
+    x = g.standard_normal((B, n, C)).astype(np.float32)
+    layer = MHCLayer(n=n, C=C).cuda()
+    _set(layer, hpre, hpost, hres, w)
+    with pytest.warns(RuntimeWarning, match="injected by the test") as rec:
+        y1 = layer(dev_tensor(x))
+        y2 = layer(dev_tensor(x))
+    assert len(rec) == 1 and L._METAL_FAILED is True
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=layer.eps)
+    assert rel_err(np_of(y1), ref) < 1e-5 and torch.equal(y1, y2)
+
+
 def test_timed_path_uses_the_same_kernels(monkeypatch):
     """Under kernel_timer the layer splits its calls per kernel; results are bitwise equal."""
     from mhc_mlx_amd import kernel_timer
