@@ -52,6 +52,26 @@ int mhc_abi_version(void);
 const char* mhc_last_error(void);
 
 /* --------------------------------------------------------------------- */
+/* Launch-shape knobs                                                      */
+/* --------------------------------------------------------------------- */
+
+/* The library picks its launch shapes itself; a few integer choices
+ * (workgroups per CU of a grid, slabs per wave, columns per lane, ...) can be
+ * overridden by name ("MHC_RES_GRID", "MHC_BWD_GRID", ...).  Every knob
+ * starts from the environment variable of the same name, read once when the
+ * library is loaded; afterwards only these calls change it.  The table is
+ * process-wide and its entries are atomics: a change made on one thread
+ * applies to launches that start after it on any thread.  This is the
+ * storage behind the reference's tuning file (metal.py:21-36: a JSON file of
+ * per-kernel threadgroup sizes read at import); the Python package applies
+ * such a file here.  Results never depend on a knob beyond fp32 rounding. */
+int mhc_knob_count(void);
+const char* mhc_knob_name(int index);                  /* NULL outside [0, count) */
+int mhc_set_knob(const char* name, int value);         /* MHC_ERR_INVALID_ARG: unknown name */
+int mhc_unset_knob(const char* name);                  /* back to the built-in choice */
+int mhc_get_knob(const char* name, int* value);        /* 1: set (*value written), 0: unset */
+
+/* --------------------------------------------------------------------- */
 /* Sinkhorn-Knopp projection                                               */
 /* --------------------------------------------------------------------- */
 
@@ -83,8 +103,8 @@ int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlogits, int64
  * backward; the results are those of mhc_sinkhorn_fwd / mhc_sinkhorn_bwd.
  *
  * Bytes of the state buffer for this shape; 0 when no recorded path exists
- * (n != 16, or the n == 16 kernels are switched off with MHC_SK16=0): then
- * use mhc_sinkhorn_fwd / mhc_sinkhorn_bwd. */
+ * (n != 16, or the knob MHC_SK16 or MHC_SK16_RECORD is 0): then use
+ * mhc_sinkhorn_fwd / mhc_sinkhorn_bwd. */
 size_t mhc_sinkhorn_state_bytes(int64_t batch, int n, int iters);
 
 /* mhc_sinkhorn_fwd that also writes the state to `state` (state_bytes >=

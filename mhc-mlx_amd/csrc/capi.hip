@@ -1,4 +1,6 @@
-// C ABI plumbing: version, per-thread error text, cached device queries.
+// C ABI plumbing: version, per-thread error text, the launch-shape knob
+// table, cached device properties.
+#include <climits>
 #include <atomic>
 #include <mutex>
 #include <unordered_map>
@@ -71,13 +73,81 @@ int occupancy_blocks(const void* kernel, int tpb, size_t smem) {
   return blocks;
 }
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  if (v == nullptr || *v == '\0') return dflt;
-  return atoi(v);
+// ---------------------------------------------------------------------------
+// Knobs: one process-wide table of integer launch-shape choices.  Each entry
+// starts from its environment variable, read once when the library is
+// loaded (static initialisation, before any thread can launch); afterwards
+// only mhc_set_knob / mhc_unset_knob change it.  Values are atomics, so a
+// setter racing a launch on another thread is well defined (the launch sees
+// the old or the new value).  INT_MIN marks an unset knob.
+// ---------------------------------------------------------------------------
+
+namespace {
+constexpr int kUnset = INT_MIN;
+const char* const kKnobNames[kNumKnobs] = {
+    "MHC_FWD_MFMA", "MHC_FWD_SPW", "MHC_FWD_CH", "MHC_FWD_TPB", "MHC_FWD_GRID", "MHC_FWD_SKF",
+    "MHC_BWD_GRID", "MHC_BWD_MFMA", "MHC_BWD_SPW", "MHC_BWD_LEGACY", "MHC_BWD_TPB",
+    "MHC_SK16", "MHC_SK16_CPL", "MHC_SK16_RECORD",
+    "MHC_RES_GRID", "MHC_MIX_FWD_GRID", "MHC_MIX_BWD_GRID", "MHC_SCALE_FWD_GRID", "MHC_SCALE_BWD_GRID",
+};
+std::atomic<int> g_knobs[kNumKnobs];
+
+int knob_index(const char* name) {
+  if (name == nullptr) return -1;
+  for (int i = 0; i < kNumKnobs; ++i)
+    if (strcmp(name, kKnobNames[i]) == 0) return i;
+  return -1;
+}
+
+struct KnobInit {
+  KnobInit() {
+    for (int i = 0; i < kNumKnobs; ++i) {
+      const char* v = getenv(kKnobNames[i]);
+      g_knobs[i].store(v != nullptr && *v != '\0' ? atoi(v) : kUnset, std::memory_order_relaxed);
+    }
+  }
+} g_knob_init;
+}  // namespace
+
+int knob(Knob k, int dflt) {
+  const int v = g_knobs[k].load(std::memory_order_relaxed);
+  return v == kUnset ? dflt : v;
 }
 
 }  // namespace mhc
+
+extern "C" int mhc_knob_count(void) { return mhc::kNumKnobs; }
+
+extern "C" const char* mhc_knob_name(int index) {
+  return index >= 0 && index < mhc::kNumKnobs ? mhc::kKnobNames[index] : nullptr;
+}
+
+extern "C" int mhc_set_knob(const char* name, int value) {
+  mhc::clear_error();
+  const int i = mhc::knob_index(name);
+  MHC_CHECK_ARG(i >= 0, "unknown knob %s", name ? name : "(null)");
+  MHC_CHECK_ARG(value != mhc::kUnset, "knob value %d is reserved", value);
+  mhc::g_knobs[i].store(value, std::memory_order_relaxed);
+  return MHC_OK;
+}
+
+extern "C" int mhc_unset_knob(const char* name) {
+  mhc::clear_error();
+  const int i = mhc::knob_index(name);
+  MHC_CHECK_ARG(i >= 0, "unknown knob %s", name ? name : "(null)");
+  mhc::g_knobs[i].store(mhc::kUnset, std::memory_order_relaxed);
+  return MHC_OK;
+}
+
+extern "C" int mhc_get_knob(const char* name, int* value) {
+  mhc::clear_error();
+  const int i = mhc::knob_index(name);
+  MHC_CHECK_ARG(i >= 0, "unknown knob %s", name ? name : "(null)");
+  const int v = mhc::g_knobs[i].load(std::memory_order_relaxed);
+  if (v == mhc::kUnset) return 0;
+  if (value != nullptr) *value = v;
+  return 1;
+}
 
 extern "C" int mhc_abi_version(void) { return MHC_ABI_VERSION; }
 

@@ -1556,7 +1556,7 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
   // faster than one resident wave of workgroups (562 vs 576 us at config 2);
   // MHC_BWD_GRID overrides the count.
   int64_t blocks = L.gmax;
-  const int grid_pref = env_int("MHC_BWD_GRID", 0);
+  const int grid_pref = knob(kKnobBwdGrid, 0);
   if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
   set_rows(A, L);
@@ -1586,7 +1586,7 @@ int launch_mf16_variant(BwdArgs A, const BwdLayout& L, int waves, int64_t* num_p
   const int occ = occupancy_blocks(kfn, waves * 64, smem);
   if (occ <= 0) return 1;
   int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
-  const int grid_pref = env_int("MHC_BWD_GRID", 0);
+  const int grid_pref = knob(kKnobBwdGrid, 0);
   if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
   set_rows(A, L);
@@ -1605,9 +1605,9 @@ int launch_bwd_mfma16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipS
   if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.dx, 16) || !aligned(A.M, 16) ||
       !aligned(A.hpre, 16) || !aligned(A.hpost, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
     return 1;
-  if (env_int("MHC_BWD_MFMA", 1) == 0) return 1;
+  if (knob(kKnobBwdMfma, 1) == 0) return 1;
   const int S = A.C / 128;
-  int spw = env_int("MHC_BWD_SPW", S % 2 == 0 ? 2 : 1);
+  int spw = knob(kKnobBwdSpw, S % 2 == 0 ? 2 : 1);
   if (spw != 1 && spw != 2) spw = 1;
   if (S % spw != 0) spw = 1;
   const int waves = S / spw;
@@ -1650,7 +1650,7 @@ int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t
     if (rc != 1) return rc;
   }
   if constexpr (NMAX <= 8) {
-    static const int legacy = env_int("MHC_BWD_LEGACY", 0);
+    const int legacy = knob(kKnobBwdLegacy, 0);
     if (!legacy) {
       const int rc = launch_bwd_lw<NMAX, XT, GT, PT>(A, L, num_partials, stream);
       if (rc != 1) return rc;
@@ -1661,7 +1661,7 @@ int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t
   constexpr int KP = NMAX * NMAX + 2 * NMAX;
   constexpr int NBLK = (KP + 63) / 64;
   A.nchunks = (int)ceil_div(A.C, V);
-  static const int tpb_pref = env_int("MHC_BWD_TPB", 0);
+  const int tpb_pref = knob(kKnobBwdTpb, 0);
   const ThreadPlan tp = plan_threads(A.nchunks, 1, tpb_pref);
   A.reload = tp.reload;
   const int nwaves = tp.tpb / 64;

@@ -552,9 +552,9 @@ int launch_fwd_mfma16(FwdArgs A, hipStream_t stream) {
   } else {
     if (A.n != 16 || !A.vec || A.C % 128 != 0) return 1;
     if (!aligned(A.M, 16) || !aligned(A.hpre, 16) || !aligned(A.hpost, 16) || !aligned(A.w, 16)) return 1;
-    if (env_int("MHC_FWD_MFMA", 1) == 0) return 1;
+    if (knob(kKnobFwdMfma, 1) == 0) return 1;
     const int S = A.C / 128;
-    int spw = env_int("MHC_FWD_SPW", S % 2 == 0 && S >= 8 ? 2 : 1);
+    int spw = knob(kKnobFwdSpw, S % 2 == 0 && S >= 8 ? 2 : 1);
     if (spw != 1 && spw != 2) spw = 1;
     if (S % spw != 0) spw = 1;
     const int waves = S / spw;
@@ -587,7 +587,7 @@ int launch_fwd_full(FwdArgs A, hipStream_t stream) {
   // with one chunk per thread against 380 us with two; bf16 -> fp32
   // (4-channel chunks) 566 us with two against 625 us with one (1024 threads).
   int ch = nchunks <= 512 ? 1 : 2;
-  const int ch_pref = env_int("MHC_FWD_CH", 0);
+  const int ch_pref = knob(kKnobFwdCh, 0);
   if (ch_pref == 1 || ch_pref == 2) ch = ch_pref;
   if (nchunks % (64 * ch) != 0) ch = 1;
   if (nchunks % 64 != 0 || nchunks / ch > 1024) return 1;
@@ -620,7 +620,7 @@ int launch_fwd(FwdArgs A, hipStream_t stream) {
     if (rc != 1) return rc;
   }
   A.nchunks = (int)ceil_div(A.C, V);
-  const ThreadPlan tp = plan_threads(A.nchunks, CH, env_int("MHC_FWD_TPB", 0));
+  const ThreadPlan tp = plan_threads(A.nchunks, CH, knob(kKnobFwdTpb, 0));
   A.ch = tp.ch;
   A.reload = tp.reload;
   const bool par_lds = PT || NMAX > 8;
@@ -631,7 +631,7 @@ int launch_fwd(FwdArgs A, hipStream_t stream) {
     return set_error(MHC_ERR_INVALID_ARG, "fused_fwd: no occupancy for %d threads (n=%d C=%d)",
                      tp.tpb, A.n, A.C);
   // Persistent grid (per-token parameters are staged one token ahead).
-  const int grid_per_cu = env_int("MHC_FWD_GRID", 0);
+  const int grid_per_cu = knob(kKnobFwdGrid, 0);
   int64_t blocks = (int64_t)device_cu_count() * (grid_per_cu > 0 ? grid_per_cu : occ);
   blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, blocks));
   hipLaunchKernelGGL((fused_fwd_kernel<NMAX, XT, OT, PT>), dim3((unsigned)blocks), dim3(tp.tpb),
@@ -726,7 +726,7 @@ int launch_fwd_full_skf(FwdArgs A, hipStream_t stream) {
 }
 
 int layer_fwd_single_launch(const FwdArgs& A, int xd, int od, hipStream_t s) {
-  if (env_int("MHC_FWD_SKF", 1) == 0 || A.T < 1 || A.T > device_cu_count()) return 1;
+  if (knob(kKnobFwdSkf, 1) == 0 || A.T < 1 || A.T > device_cu_count()) return 1;
   if (xd == MHC_DTYPE_BF16 && od == MHC_DTYPE_BF16) {
     if (A.n == 4) return launch_fwd_full_skf<4, __bf16, __bf16>(A, s);
     if (A.n == 8) return launch_fwd_full_skf<8, __bf16, __bf16>(A, s);

@@ -74,8 +74,18 @@ inline ThreadPlan plan_threads(int nchunks, int chmax, int tpb_pref) {
 // Resident blocks per CU for a kernel at a block size (cached).
 int occupancy_blocks(const void* kernel, int tpb, size_t smem);
 
-// Integer tuning override from the environment (0 when unset).
-int env_int(const char* name, int dflt);
+// Launch-shape tuning knobs (names in capi.hip; set through mhc_set_knob,
+// initialised from the environment once at load).
+enum Knob : int {
+  kKnobFwdMfma, kKnobFwdSpw, kKnobFwdCh, kKnobFwdTpb, kKnobFwdGrid, kKnobFwdSkf,
+  kKnobBwdGrid, kKnobBwdMfma, kKnobBwdSpw, kKnobBwdLegacy, kKnobBwdTpb,
+  kKnobSk16, kKnobSk16Cpl, kKnobSk16Record,
+  kKnobResGrid, kKnobMixFwdGrid, kKnobMixBwdGrid, kKnobScaleFwdGrid, kKnobScaleBwdGrid,
+  kNumKnobs
+};
+
+// The knob's value, or `dflt` when it is unset.
+int knob(Knob k, int dflt);
 
 // Upper bound on a one-dimensional grid; larger token counts are covered by
 // the kernels' grid-stride loops.

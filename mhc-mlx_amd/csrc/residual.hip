@@ -217,7 +217,7 @@ constexpr int kResBwdGroup = 4;
 // at that many blocks per CU (tuning override).
 int64_t res_fwd_grid(int64_t items, int cus) {
   const int64_t g = ceil_div(items, kResThreads);
-  const int per_cu = env_int("MHC_RES_GRID", -1);
+  const int per_cu = knob(kKnobResGrid, -1);
   if (per_cu < 0) return std::max<int64_t>(1, std::min<int64_t>(g, kMaxGrid));
   return std::max<int64_t>(1, std::min<int64_t>(g, (int64_t)cus * std::max(per_cu, 1)));
 }

@@ -390,12 +390,12 @@ namespace {
 
 // The n == 16 kernels need 16-byte aligned matrices; MHC_SK16=0 turns them off.
 bool use_sk16(int n, const void* a, const void* b, const void* c) {
-  if (n != 16 || env_int("MHC_SK16", 1) == 0) return false;
+  if (n != 16 || knob(kKnobSk16, 1) == 0) return false;
   return aligned(a, 16) && aligned(b, 16) && (c == nullptr || aligned(c, 16));
 }
 
 // MHC_SK16_CPL (2 or 4) selects the columns per lane (tuning override).
-int sk16_cpl() { return env_int("MHC_SK16_CPL", 4) == 2 ? 2 : 4; }
+int sk16_cpl() { return knob(kKnobSk16Cpl, 4) == 2 ? 2 : 4; }
 
 int64_t sk16_blocks(int64_t batch, int cpl) {
   return ceil_div(batch, (int64_t)(cpl == 4 ? Sk16<4>::MPW : Sk16<2>::MPW) * (kSk16Threads / 64));
@@ -586,7 +586,7 @@ float* sk16_state_ptr(const void* state, size_t state_bytes, int64_t batch, int 
 }  // namespace
 
 extern "C" size_t mhc_sinkhorn_state_bytes(int64_t batch, int n, int iters) {
-  if (n != 16 || batch <= 0 || iters < 0 || env_int("MHC_SK16", 1) == 0) return 0;
+  if (n != 16 || batch <= 0 || iters < 0 || knob(kKnobSk16, 1) == 0 || knob(kKnobSk16Record, 1) == 0) return 0;
   return sk16_state_bytes(batch, iters) + 256;
 }
 

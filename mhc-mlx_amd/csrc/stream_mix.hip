@@ -669,19 +669,19 @@ int mix_vec_width(int nmax, std::initializer_list<int> dtype_sizes) {
 
 // Grid of a grid-stride kernel over `work` items: at most `per_cu`
 // workgroups per CU (per_cu < 0: one item per thread, up to kMaxGrid).
-// `env` names a tuning override of per_cu.
-int64_t mix_grid(int64_t work, int cus, const char* env = "MHC_MIX_GRID", int per_cu = 8) {
-  per_cu = env_int(env, per_cu);
+// `k` names the tuning knob that overrides per_cu.
+int64_t mix_grid(int64_t work, int cus, Knob k, int per_cu = 8) {
+  per_cu = knob(k, per_cu);
   int64_t g = ceil_div(work, kMixThreads);
   g = std::min<int64_t>(g, per_cu < 0 ? kMaxGrid : (int64_t)cus * std::max(per_cu, 1));
   return std::max<int64_t>(g, 1);
 }
 
 // Workgroups along x of the per-stream scale kernels (grid.y = n): at most
-// 8 per CU over all streams by default; `env` overrides the per-CU count
-// (< 0: one item per thread).
-int64_t scale_grid(int64_t T, int n, int C, const char* env) {
-  const int per_cu = env_int(env, 8);
+// 8 per CU over all streams by default; the knob `k` overrides the per-CU
+// count (< 0: one item per thread).
+int64_t scale_grid(int64_t T, int n, int C, Knob k) {
+  const int per_cu = knob(k, 8);
   const int64_t g = ceil_div(T * ceil_div(C, 8), kMixThreads);
   const int64_t cap = per_cu < 0 ? kMaxGrid : (int64_t)device_cu_count() * std::max(per_cu, 1) / n + 1;
   return std::max<int64_t>(1, std::min<int64_t>(g, cap));
@@ -756,7 +756,7 @@ extern "C" int mhc_stream_mix_add_fwd(const void* x, int x_dtype, const void* y,
   A.nchunks = (int)ceil_div(C, V);
   A.vec = io_vec_ok(C, V, {{x, dtype_bytes(x_dtype)}, {y, y ? dtype_bytes(y_dtype) : 4},
                            {out, dtype_bytes(out_dtype)}});
-  const int64_t blocks = mix_grid(T * A.nchunks, device_cu_count(), "MHC_MIX_FWD_GRID", 8);
+  const int64_t blocks = mix_grid(T * A.nchunks, device_cu_count(), kKnobMixFwdGrid, 8);
   hipStream_t s = (hipStream_t)stream;
   const int ydt = y ? y_dtype : x_dtype;
   if (nmax_for(n) == 0) {
@@ -791,7 +791,7 @@ extern "C" size_t mhc_stream_mix_add_bwd_workspace_bytes(int64_t T, int n, int C
   if (T <= 0 || n < 1 || n > MHC_MAX_N || C < 1) return 0;
   // the narrowest item (fp32 operands) gives the most items and so the largest grid
   const int V = mix_vec_width(nmax_for(n), {4});
-  const int64_t G = mix_grid(T * ceil_div(C, V), device_cu_count(), "MHC_MIX_BWD_GRID", 8);
+  const int64_t G = mix_grid(T * ceil_div(C, V), device_cu_count(), kKnobMixBwdGrid, 8);
   return (size_t)(G + kMixSplit) * (size_t)mix_rows(n) * sizeof(float);
 }
 
@@ -817,7 +817,7 @@ extern "C" int mhc_stream_mix_add_bwd(const void* x, int x_dtype, const void* y,
   MHC_CHECK_ARG(dtype_bytes(ydt), "unknown dtype code");
   const int V = mix_vec_width(nmax_for(n), {dtype_bytes(x_dtype), dtype_bytes(ydt), dtype_bytes(dout_dtype)});
   const int nch = (int)ceil_div(C, V);
-  const int64_t G = mix_grid(T * nch, device_cu_count(), "MHC_MIX_BWD_GRID", 8);
+  const int64_t G = mix_grid(T * nch, device_cu_count(), kKnobMixBwdGrid, 8);
   const int P = mix_rows(n);
   const size_t need = (size_t)(G + kMixSplit) * P * sizeof(float);
   MHC_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
@@ -887,7 +887,7 @@ extern "C" int mhc_stream_scale_fwd(const void* x, int x_dtype, const float* h_p
   A.x = x; A.out = out; A.hpre = h_pre; A.T = T; A.n = n; A.C = C; A.h_mode = h_mode;
   A.nchunks = (int)ceil_div(C, 8);
   A.vec = io_vec_ok(C, 8, {{x, dtype_bytes(x_dtype)}, {out, dtype_bytes(out_dtype)}});
-  const int64_t bx = scale_grid(T, n, C, "MHC_SCALE_FWD_GRID");
+  const int64_t bx = scale_grid(T, n, C, kKnobScaleFwdGrid);
   hipStream_t s = (hipStream_t)stream;
   return by_dtype(x_dtype, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
@@ -906,7 +906,7 @@ extern "C" int mhc_stream_scale_fwd(const void* x, int x_dtype, const float* h_p
 }
 
 namespace {
-int64_t scale_bwd_grid(int64_t T, int n, int C) { return scale_grid(T, n, C, "MHC_SCALE_BWD_GRID"); }
+int64_t scale_bwd_grid(int64_t T, int n, int C) { return scale_grid(T, n, C, kKnobScaleBwdGrid); }
 }  // namespace
 
 extern "C" size_t mhc_stream_scale_bwd_workspace_bytes(int64_t T, int n, int C) {

@@ -34,6 +34,11 @@ _PI64 = ctypes.POINTER(ctypes.c_int64)
 SIGNATURES = {
     "mhc_abi_version": ([], _I32),
     "mhc_last_error": ([], ctypes.c_char_p),
+    "mhc_knob_count": ([], _I32),
+    "mhc_knob_name": ([_I32], ctypes.c_char_p),
+    "mhc_set_knob": ([ctypes.c_char_p, _I32], _I32),
+    "mhc_unset_knob": ([ctypes.c_char_p], _I32),
+    "mhc_get_knob": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)], _I32),
     "mhc_sinkhorn_fwd": ([_VP, _VP, _I64, _I32, _I32, _F32, _VP], _I32),
     "mhc_sinkhorn_bwd_workspace_bytes": ([_I64, _I32, _I32], _SZ),
     "mhc_sinkhorn_bwd": ([_VP, _VP, _VP, _I64, _I32, _I32, _F32, _VP, _SZ, _VP], _I32),
@@ -73,6 +78,8 @@ SIGNATURES = {
 
 _lock = threading.Lock()
 _lib = None
+# knob settings made before the library is loaded: name -> value (None: unset)
+_pending_knobs: dict[str, int | None] = {}
 
 
 class MHCError(RuntimeError):
@@ -101,8 +108,48 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         if lib.mhc_abi_version() != 1:
             raise RuntimeError(f"{p}: unexpected ABI version {lib.mhc_abi_version()}")
         if path is None:
+            for name, value in _pending_knobs.items():
+                rc = lib.mhc_unset_knob(name.encode()) if value is None else lib.mhc_set_knob(name.encode(), value)
+                if rc != 0:
+                    raise ValueError(f"knob {name}: {lib.mhc_last_error().decode()}")
+            _pending_knobs.clear()
             _lib = lib
         return lib
+
+
+def knob_names() -> list[str]:
+    """Names of the library's launch-shape knobs (mhc_knob_name)."""
+    lib = load()
+    return [lib.mhc_knob_name(i).decode() for i in range(lib.mhc_knob_count())]
+
+
+def set_knob(name: str, value: int | None) -> None:
+    """Set a launch-shape knob (None: back to the library's own choice).
+
+    Applied at once when the library is loaded, else when it loads.
+    """
+    if value is not None and (isinstance(value, bool) or not isinstance(value, int)):
+        raise ValueError(f"knob {name} must be an integer, got {value!r}")
+    with _lock:
+        if _lib is None:
+            _pending_knobs[name] = value
+            return
+    if value is None:
+        check(_lib.mhc_unset_knob(name.encode()), f"mhc_unset_knob({name})")
+    else:
+        check(_lib.mhc_set_knob(name.encode(), int(value)), f"mhc_set_knob({name})")
+
+
+def get_knob(name: str) -> int | None:
+    """A knob's value, or None while it is unset (the library's own choice)."""
+    with _lock:
+        if _lib is None and name in _pending_knobs:
+            return _pending_knobs[name]
+    lib = load()
+    v = ctypes.c_int(0)
+    rc = lib.mhc_get_knob(name.encode(), ctypes.byref(v))
+    check(min(rc, 0), f"mhc_get_knob({name})")
+    return v.value if rc == 1 else None
 
 
 def last_error() -> str:

@@ -26,7 +26,6 @@ op requires GPU tensors and the built library; there is no silent fallback.
 from __future__ import annotations
 
 import ctypes
-import os
 
 import torch
 
@@ -415,13 +414,11 @@ def _layer_bwd(x, g, hpre, hpost, hres, M, w, iters, eps, per_token):
 def _sk_state_bytes(B: int, n: int, iters: int) -> int:
     """Bytes of the Sinkhorn state a per-token forward records for its backward.
 
-    0 when the library has no recorded path for n, or when MHC_SK16_RECORD=0
-    (then the VJP recomputes the forward iterations and needs no saved
-    state: 256 bytes per token and iteration less memory between forward and
-    backward).
+    0 when the library has no recorded path for n, or when the knob
+    MHC_SK16_RECORD is 0 (then the VJP recomputes the forward iterations and
+    needs no saved state: 256 bytes per token and iteration less memory
+    between forward and backward).
     """
-    if os.environ.get("MHC_SK16_RECORD", "1") == "0":
-        return 0
     return int(_lib.query("mhc_sinkhorn_state_bytes", B, n, iters))
 
 

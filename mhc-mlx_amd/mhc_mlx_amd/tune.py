@@ -3,7 +3,8 @@
     python -m mhc_mlx_amd.tune [--out mhc_tuning.json] [--scale 1.0]
 
 The gfx950 counterpart of the reference's ``scripts/tune.py`` (tune.py:50-103):
-for every op in ``tuning.KNOBS`` each candidate value of its knob is set, the
+for every op in ``tuning.KNOBS`` each candidate value of its knob is set in
+the library's knob table (``mhc_set_knob``), the
 op's representative workload is timed with HIP events on the current stream
 (warm-up, then the mean of timed calls, as tune.py:12-24), and the fastest
 value is kept.  The file is written in the format ``tuning.load`` reads;
@@ -14,12 +15,11 @@ from __future__ import annotations
 
 import argparse
 import json
-import os
 import sys
 
 import torch
 
-from . import ops
+from . import _lib, ops
 from .tuning import KNOBS
 
 
@@ -112,18 +112,15 @@ def tune(scale: float = 1.0, only: list[str] | None = None, log=print) -> dict:
     for op, (env, candidates) in KNOBS.items():
         if only and op not in only:
             continue
-        prev = os.environ.get(env)
+        prev = _lib.get_knob(env)
         times = {}
         try:
             for v in candidates:
-                os.environ[env] = str(v)
+                _lib.set_knob(env, v)
                 times[v] = _time_us(runs[op])
                 log(f"  {op:20s} {env}={v:<5d} {times[v]:10.1f} us")
         finally:
-            if prev is None:
-                os.environ.pop(env, None)
-            else:
-                os.environ[env] = prev
+            _lib.set_knob(env, prev)
         best = min(times, key=times.get)
         log(f"  -> {op}: {env}={best}")
         result[op] = {env: best}

@@ -6,25 +6,30 @@ import from ``mhc_tuning.json`` (working directory) and
 (mhc_mlx/metal.py:21-36); ``scripts/tune.py`` writes it (tune.py:50-103).
 
 Here the same files are read the same way.  libmhc_hip chooses its
-launch shapes itself and exposes its tunable choices as environment
-variables that it reads at every launch (``MHC_RES_GRID`` and so on, listed
-in ``KNOBS``).  A tuning entry of this library maps an op name to the
+launch shapes itself and exposes its tunable choices as named integer
+knobs (``MHC_RES_GRID`` and so on; the tuned ones are listed in ``KNOBS``),
+held in a process-wide table inside the library (``mhc_set_knob``).  Each
+knob starts from the environment variable of the same name, read once when
+the library loads.  A tuning entry of this library maps an op name to the
 values of its knobs::
 
     {"residual_add_agg": {"MHC_RES_GRID": -1}, "sinkhorn_16": {"MHC_SK16_CPL": 4}}
 
 Keys starting with ``_`` hold metadata (device, timings).
-``load()`` (run at import) exports such values, unless the variable is
-already set in the environment, so an explicit setting always wins.  Integer
-entries written for the reference (Metal threadgroup sizes) are kept for
-``_get_tuned_tpg`` and otherwise ignored.  ``python -m mhc_mlx_amd.tune``
-measures the candidates and writes the file.
+``load()`` (run at import) sets such values in the library's table, except
+for knobs whose environment variable is set, so an explicit setting always
+wins; the environment itself is never written.  Integer entries written for
+the reference (Metal threadgroup sizes) are kept for ``_get_tuned_tpg`` and
+otherwise ignored.  ``python -m mhc_mlx_amd.tune`` measures the candidates
+and writes the file.
 """
 
 from __future__ import annotations
 
 import json
 import os
+
+from . import _lib
 
 __all__ = ["KNOBS", "CONFIG_PATHS", "load", "apply", "tuning_config", "_get_tuned_tpg"]
 
@@ -33,8 +38,8 @@ CONFIG_PATHS = [
     os.path.join(os.path.expanduser("~"), ".cache", "mhc-mlx", "tuning.json"),
 ]
 
-# op name -> (environment variable, candidate values).  The library reads each
-# variable at every launch; the first candidate is its built-in default.
+# op name -> (knob name, candidate values).  The first candidate is the
+# library's built-in choice.
 KNOBS: dict[str, tuple[str, list[int]]] = {
     # workgroups per CU of the residual add + aggregate grid (-1: one item per thread)
     "residual_add_agg": ("MHC_RES_GRID", [-1, 4, 8, 16]),
@@ -65,12 +70,11 @@ def tuning_config() -> dict:
 
 
 def apply(config: dict, override: bool = False) -> dict:
-    """Export the knob values of `config` ({op: {ENV: value}}); returns what was set.
+    """Set the knob values of `config` ({op: {KNOB: value}}) in the library; returns what was set.
 
-    A variable already present in the environment is left alone unless
-    `override` is true.  Unknown names and non-integer values raise
-    ValueError before anything is exported, so a corrupt file cannot pass
-    silently or apply in part.
+    A knob whose environment variable is set is left alone unless `override`
+    is true.  Unknown names and non-integer values raise ValueError before
+    anything is set, so a corrupt file cannot pass silently or apply in part.
     """
     values = {}
     for op, entry in config.items():
@@ -82,11 +86,11 @@ def apply(config: dict, override: bool = False) -> dict:
             if isinstance(value, bool) or not isinstance(value, int):
                 raise ValueError(f"tuning entry {op!r}: {env} must be an integer, got {value!r}")
             values[env] = value
-    # all entries are valid: export them
+    # all entries are valid: set them
     done = {}
     for env, value in values.items():
         if override or env not in os.environ:
-            os.environ[env] = str(value)
+            _lib.set_knob(env, value)
             done[env] = value
     return done
 

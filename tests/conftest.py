@@ -50,3 +50,17 @@ def _hip_path_did_not_fall_back(request):
     L._METAL_FAILED = False
     yield
     assert not L._METAL_FAILED, "the HIP path fell back to the torch reference path during this GPU test"
+
+
+@pytest.fixture
+def knobs():
+    """Set libmhc_hip launch-shape knobs for one test: ``knobs(name, value)``.
+
+    Every knob of the library's table is restored when the test ends.
+    """
+    from mhc_mlx_amd import _lib
+
+    saved = {name: _lib.get_knob(name) for name in _lib.knob_names()}
+    yield _lib.set_knob
+    for name, value in saved.items():
+        _lib.set_knob(name, value)

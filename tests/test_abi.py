@@ -112,13 +112,16 @@ def test_residual_add_agg_rejects_bad_arguments_on_the_host(lib):
                                         None, 0, 4, 4, 8, None) == -1
 
 
-def test_sinkhorn_state_is_for_n16_only_and_checked_on_the_host(lib, monkeypatch):
+def test_sinkhorn_state_is_for_n16_only_and_checked_on_the_host(lib, knobs):
     assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 8 * 20 * 256 + 256
     assert lib.mhc_sinkhorn_state_bytes(8, 4, 20) == 0
     assert lib.mhc_sinkhorn_state_bytes(0, 16, 20) == 0
-    monkeypatch.setenv("MHC_SK16", "0")
+    knobs("MHC_SK16", 0)
     assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 0
-    monkeypatch.delenv("MHC_SK16")
+    knobs("MHC_SK16", None)
+    knobs("MHC_SK16_RECORD", 0)
+    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 0
+    knobs("MHC_SK16_RECORD", None)
     fake = ctypes.c_void_p(4096)  # never dereferenced: every call below is rejected on the host
     eps = ctypes.c_float(1e-6)
     assert lib.mhc_sinkhorn_fwd_record(fake, fake, fake, 1 << 20, 8, 4, 20, eps, None) == -1

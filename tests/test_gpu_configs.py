@@ -343,7 +343,7 @@ def test_per_token_n16_activated_c_abi(dt):
 
 
 @pytest.mark.parametrize("T,C", [(300, 1024), (37, 256)])
-def test_per_token_n16_recorded_sinkhorn_state(monkeypatch, T, C):
+def test_per_token_n16_recorded_sinkhorn_state(T, C, knobs):
     """Per-token n = 16 with gradients records the Sinkhorn VJP state in the forward
     (mhc_sinkhorn_fwd_record) and the backward uses it (mhc_sinkhorn_bwd_recorded); with
     MHC_SK16_RECORD=0 the backward recomputes it.  Both give bitwise the same output and gradients."""
@@ -356,7 +356,7 @@ def test_per_token_n16_recorded_sinkhorn_state(monkeypatch, T, C):
     hpre, hpost, hres, w = params(g, n, C, per_token_B=T)
     results = []
     for rec in ("1", "0"):
-        monkeypatch.setenv("MHC_SK16_RECORD", rec)
+        knobs("MHC_SK16_RECORD", int(rec))
         ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
         xt = dev_tensor(x, "bf16").requires_grad_(True)
         out = ops.mhc_layer_forward_dynamic(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
@@ -367,7 +367,7 @@ def test_per_token_n16_recorded_sinkhorn_state(monkeypatch, T, C):
     refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, np_of(dout), sinkhorn_iters=20, eps=EPS)
     assert rel_err(np_of(results[0][4]), refs[3]) < 1e-4
     # without gradients nothing is recorded: the forward is the plain one (and identical)
-    monkeypatch.setenv("MHC_SK16_RECORD", "1")
+    knobs("MHC_SK16_RECORD", 1)
     with torch.no_grad():
         ps = [dev_tensor(v) for v in (hpre, hpost, hres, w)]
         out_ng = ops.mhc_layer_forward_dynamic(dev_tensor(x, "bf16"), *ps, sinkhorn_iters=20, eps=EPS,
@@ -375,11 +375,11 @@ def test_per_token_n16_recorded_sinkhorn_state(monkeypatch, T, C):
     assert torch.equal(out_ng, results[0][0])
 
 
-def test_per_token_n16_valu_fallback(monkeypatch):
+def test_per_token_n16_valu_fallback(knobs):
     """The VALU kernels that serve n = 16 when the MFMA kernels decline (here forced off through
-    their environment switches, read at every launch) give the same parity."""
-    monkeypatch.setenv("MHC_FWD_MFMA", "0")
-    monkeypatch.setenv("MHC_BWD_MFMA", "0")
+    their knobs) give the same parity."""
+    knobs("MHC_FWD_MFMA", 0)
+    knobs("MHC_BWD_MFMA", 0)
     T, n, C, dt = 40, 16, 512, "bf16"
     g = rng(7200)
     x = to_dtype_np(g.standard_normal((T, n, C)), dt)

@@ -61,11 +61,11 @@ def test_post_combine_bf16_with_bf16_or_fp32_grad(gdt):
 
 
 @pytest.mark.parametrize("gdt", ["bf16", "f32"])
-def test_rewire_kernels_walk_several_items_per_thread(monkeypatch, gdt):
+def test_rewire_kernels_walk_several_items_per_thread(gdt, knobs):
     """One workgroup per CU: each thread walks many (token, chunk) items and, with three
     chunks per token (C = 24), the chunk index wraps between the items of a thread."""
     for env in ("MHC_MIX_FWD_GRID", "MHC_MIX_BWD_GRID", "MHC_SCALE_FWD_GRID", "MHC_SCALE_BWD_GRID"):
-        monkeypatch.setenv(env, "1")
+        knobs(env, 1)
     B, n, C = 30000, 4, 24
     g = rng(48)
     x = to_dtype_np(g.standard_normal((B, n, C)), "bf16")

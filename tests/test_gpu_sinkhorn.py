@@ -220,7 +220,7 @@ def test_sinkhorn16_vjp_in_place_c_abi():
 
 @pytest.mark.parametrize("B,iters,cpl_fwd,cpl_bwd", [(200, 20, "4", "4"), (33, 1, "4", "2"), (65, 0, "2", "4"),
                                                    (1000, 20, "2", "2")])
-def test_sinkhorn16_recorded_state_matches_recompute(monkeypatch, B, iters, cpl_fwd, cpl_bwd):
+def test_sinkhorn16_recorded_state_matches_recompute(B, iters, cpl_fwd, cpl_bwd, knobs):
     """mhc_sinkhorn_fwd_record / mhc_sinkhorn_bwd_recorded give bitwise the results of
     mhc_sinkhorn_fwd / mhc_sinkhorn_bwd (the same iterations, recorded in the forward instead of
     recomputed in the VJP) when both use the same lanes per matrix.  With different widths the
@@ -239,7 +239,7 @@ def test_sinkhorn16_recorded_state_matches_recompute(monkeypatch, B, iters, cpl_
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     eps = ctypes.c_float(1e-5)
     Ht = dev_tensor(H)
-    monkeypatch.setenv("MHC_SK16_CPL", cpl_fwd)
+    knobs("MHC_SK16_CPL", int(cpl_fwd))
     M_plain = torch.empty_like(Ht)
     _lib.call("mhc_sinkhorn_fwd", P(Ht), P(M_plain), B, 16, iters, eps, s)
     nst = _lib.query("mhc_sinkhorn_state_bytes", B, 16, iters)
@@ -249,7 +249,7 @@ def test_sinkhorn16_recorded_state_matches_recompute(monkeypatch, B, iters, cpl_
     M_rec = torch.empty_like(Ht)
     _lib.call("mhc_sinkhorn_fwd_record", P(Ht), P(M_rec), P(st), nst, B, 16, iters, eps, s)
     assert torch.equal(M_rec, M_plain)
-    monkeypatch.setenv("MHC_SK16_CPL", cpl_bwd)
+    knobs("MHC_SK16_CPL", int(cpl_bwd))
     d_rec = dev_tensor(dM)
     _lib.call("mhc_sinkhorn_bwd_recorded", P(Ht), P(d_rec), P(d_rec), P(st), nst, B, 16, iters, eps, s)
     nb = _lib.query("mhc_sinkhorn_bwd_workspace_bytes", B, 16, iters)

@@ -2,17 +2,16 @@
 candidate values, and results do not depend on the launch shape chosen."""
 
 import json
-import os
 
 import pytest
 import torch
 
-from mhc_mlx_amd import ops, tune, tuning
+from mhc_mlx_amd import _lib, ops, tune, tuning
 
 pytestmark = pytest.mark.gpu
 
 
-def test_tuner_writes_a_loadable_file(tmp_path, monkeypatch):
+def test_tuner_writes_a_loadable_file(tmp_path, monkeypatch, knobs):
     out = tmp_path / "mhc_tuning.json"
     assert tune.main(["--out", str(out), "--scale", "0.05", "--only", "residual_add_agg", "sinkhorn_16"]) == 0
     cfg = json.loads(out.read_text())
@@ -22,12 +21,13 @@ def test_tuner_writes_a_loadable_file(tmp_path, monkeypatch):
         assert set(cfg["_timings_us"][op]) == {str(c) for c in cands}
     for env, _ in tuning.KNOBS.values():
         monkeypatch.delenv(env, raising=False)
+        knobs(env, None)
     tuning.load([str(out)])
-    assert os.environ["MHC_RES_GRID"] == str(cfg["residual_add_agg"]["MHC_RES_GRID"])
+    assert _lib.get_knob("MHC_RES_GRID") == cfg["residual_add_agg"]["MHC_RES_GRID"]
 
 
 @pytest.mark.parametrize("op", ["residual_add_agg", "stream_mix_add", "mhc_fused_n16", "sinkhorn_16"])
-def test_results_do_not_depend_on_the_knob(op, monkeypatch):
+def test_results_do_not_depend_on_the_knob(op, knobs):
     runs = {}
     env, cands = tuning.KNOBS[op]
     g = torch.Generator("cuda").manual_seed(1)
@@ -45,7 +45,7 @@ def test_results_do_not_depend_on_the_knob(op, monkeypatch):
              torch.randn(200, 16, 16, device="cuda", generator=g), torch.ones(1024, device="cuda")]
         fn = lambda: (ops.mhc_layer_forward_dynamic(x, *p),)  # noqa: E731
     for v in cands:
-        monkeypatch.setenv(env, str(v))
+        knobs(env, v)
         with torch.no_grad():
             runs[v] = [t.clone() for t in fn()]
     ref = runs[cands[0]]
