@@ -13,8 +13,11 @@ Timed regions (all on the stream the library launches on):
 Extras: forward latency at B=32, C=2048 (config 1) and B=1, C=4096 (eager
 calls); config 3 (per-token H, n=16) fwd+bwd; config 4
 (MHCRewire around Linear(4096, 4096)) with mHC kernel time reported apart
-from the GEMM; residual_add_agg at config 2's shape.  cpu_baseline: the numpy oracle in fp32 on one core over a
-bounded token sample of config 2.
+from the GEMM; residual_add_agg at config 2's shape.  cpu_baseline: the
+package's torch restatement of reference.py (MHCLayer(use_metal=False), the
+analogue of the reference's MHC_MLX_DISABLE_METAL=1 path) fwd+bwd on CPU
+tensors over a bounded token sample of config 2, on every host core this
+process may use; the one-core numpy oracle figure is reported beside it.
 
 Prints one JSON line.
 """
@@ -204,8 +207,60 @@ def _residual(dev, steps, warmup):
             "hbm_frac": nbytes / (st["mean_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS}
 
 
-def _cpu_baseline(n, C, budget_s=12.0, chunk=64):
-    """Oracle (numpy fp32 restatement of reference.py + its VJP) on token chunks, one core."""
+def _cpu_baseline(n, C, budget_s=15.0, chunk=256):
+    """MHCLayer's torch reference path (use_metal=False) fwd+bwd on CPU tensors, all host cores.
+
+    Timing follows the reference harness (mhc_mlx/benchmark.py:72-97): a
+    warm-up call, then repeated calls; the median step gives the rate, with
+    p10 / p90 beside it.
+    """
+    import numpy as np
+    import torch
+
+    from mhc_mlx_amd import MHCLayer
+
+    cores = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        hpre, hpost, hres, w = _params(np.random.default_rng(0), n, C)
+        layer = MHCLayer(n=n, C=C, sinkhorn_iters=20, eps=EPS, use_metal=False)
+        with torch.no_grad():
+            for prm, v in zip((layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight),
+                              (hpre, hpost, hres, w)):
+                prm.copy_(torch.from_numpy(v))
+        gen = torch.Generator().manual_seed(0)
+        x = torch.randn(chunk, n, C, generator=gen).to(torch.bfloat16).requires_grad_(True)
+        dout = torch.randn(chunk, n, C, generator=gen).to(torch.bfloat16)
+        params = [x] + list(layer.parameters())
+
+        def step():
+            out = layer(x, return_dtype=torch.bfloat16)
+            torch.autograd.grad(out, params, dout)
+
+        step()
+        ts = []
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget_s or len(ts) < 3:
+            s = time.perf_counter()
+            step()
+            ts.append(time.perf_counter() - s)
+    finally:
+        torch.set_num_threads(prev)
+    ts.sort()
+    med = statistics.median(ts)
+    pct = lambda q: ts[min(len(ts) - 1, int(q * len(ts)))]  # noqa: E731
+    return {"value": chunk / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{len(ts)} steps of {chunk} config-2 tokens (n={n}, C={C}, bf16 x and dout, bf16 out), "
+                      f"fwd+bwd of MHCLayer(use_metal=False) on CPU tensors (torch eager, "
+                      f"torch.set_num_threads({cores})); median {med * 1e3:.1f} ms per step "
+                      f"(p10 {pct(0.1) * 1e3:.1f}, p90 {pct(0.9) * 1e3:.1f}); the reference's MLX path "
+                      f"cannot run here (MLX absent)",
+            "numpy_oracle_1core": _cpu_oracle_1core(n, C)}
+
+
+def _cpu_oracle_1core(n, C, budget_s=6.0, chunk=64):
+    """The numpy oracle (fp32 restatement of reference.py + its VJP) on token chunks, one core."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
@@ -223,9 +278,9 @@ def _cpu_baseline(n, C, budget_s=12.0, chunk=64):
             O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, 20, EPS, dtype=np.float32)
             done += chunk
     dt = time.perf_counter() - t0
-    return {"value": done / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{done} tokens of config 2 ({chunk}-token chunks, n={n}, C={C}, bf16-rounded "
-                      f"inputs, fp32 numpy fwd+bwd incl. 20-iteration Sinkhorn VJP) in {dt:.1f}s"}
+    return {"value": done / dt, "unit": "tokens/s", "cores": 1,
+            "sample": f"{done} tokens of config 2 ({chunk}-token chunks, bf16-rounded inputs, fp32 numpy "
+                      f"fwd+bwd incl. the 20-iteration Sinkhorn VJP) in {dt:.1f}s"}
 
 
 def _traffic():

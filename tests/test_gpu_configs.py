@@ -133,6 +133,14 @@ def _param_grads_f64(x, g, a, p, M, w, chunk=2048):
     return dM.cpu().numpy(), dA.cpu().numpy(), dP.cpu().numpy(), dw.cpu().numpy()
 
 
+def _bf16_bound(got, ref):
+    """|got - ref| <= 2^-8 |ref| + 1e-6 everywhere: the error of one bf16 rounding (2^-9 relative) with
+    a factor of two for the fp32 arithmetic before it, plus an absolute floor for values near zero."""
+    err = np.abs(got - ref)
+    bound = 2.0 ** -8 * np.abs(ref) + 1e-6
+    assert (err <= bound).all(), float((err / bound).max())
+
+
 def _sample(T, k, seed):
     return np.sort(np.random.default_rng(seed).choice(T, size=k, replace=False))
 
@@ -159,6 +167,9 @@ def test_config2_full_size_fwd_bwd():
     assert rel_err(np_of(out[idx]), ref) < 2e-2
     rdx = O.mhc_backward_reference(xs, hpre, hpost, hres, w, gs, sinkhorn_iters=20, eps=EPS)[0]
     assert rel_err(np_of(dx[idx]), rdx) < 2e-2
+    # one bf16 rounding of an fp32 result, element by element
+    _bf16_bound(np_of(out[idx]), ref)
+    _bf16_bound(np_of(dx[idx]), rdx)
 
     # layer-wide sums vs float64 on the GPU, chained through the oracle
     a, p = O.activate_pre_post(hpre, hpost)
@@ -209,6 +220,8 @@ def test_config3_full_size_dynamic_fwd_bwd():
     assert rel_err(np_of(out[idx]), ref) < 2e-2
     refs = O.mhc_backward_reference(xs, hp, hq, hr, w, gs, sinkhorn_iters=20, eps=EPS)
     assert rel_err(np_of(dx[idx]), refs[0]) < 2e-2
+    _bf16_bound(np_of(out[idx]), ref)
+    _bf16_bound(np_of(dx[idx]), refs[0])
     assert rel_err(np_of(d_pre[idx]), refs[1]) < 1e-4
     assert rel_err(np_of(d_post[idx]), refs[2]) < 1e-4
     assert rel_err(np_of(d_res[idx]), refs[3]) < 1e-4
@@ -257,7 +270,8 @@ def test_config4_rewire_linear_full_size():
     gx, gw, gpre, gpost, gres = torch.autograd.grad(
         out, [x, inner.weight, m.mhc.H_pre_raw, m.mhc.H_post_raw, m.mhc.H_res_raw], g)
 
-    # explicit fp32 formulation with the same bf16 GEMM
+    # explicit fp32 formulation with the same bf16 GEMM; M is a leaf so its gradient can be
+    # chained through the oracle's Sinkhorn VJP
     xr = x.detach().clone().requires_grad_(True)
     hp = m.mhc.H_pre_raw.detach().clone().requires_grad_(True)
     hq = m.mhc.H_post_raw.detach().clone().requires_grad_(True)
@@ -268,16 +282,19 @@ def test_config4_rewire_linear_full_size():
     x_pre = (x3 * a[None, :, None]).to(torch.bfloat16).reshape(T, dims)
     y = torch.nn.functional.linear(x_pre, inner.weight).float().reshape(T, n, dims // n)
     M = torch.from_numpy(O.mixing_matrix_from_logits(hr.cpu().numpy(), iters=20, eps=EPS)).float().cuda()
+    M.requires_grad_(True)
     Mf = M * a[None, :]
     mixed = (Mf[None, :, :, None] * x3[:, None, :, :]).sum(2)
     ref = ((y + mixed) * p[None, :, None]).reshape(T, dims)
     assert out.dtype == torch.float32
     assert rel_err(np_of(out), np_of(ref)) < 1e-2
-    rgx, rpre, rpost = torch.autograd.grad(ref, [xr, hp, hq], g)
+    rgx, rpre, rpost, rM, rgw = torch.autograd.grad(ref, [xr, hp, hq, M, inner.weight], g)
     assert rel_err(np_of(gx), np_of(rgx)) < 2e-2
     assert rel_err(np_of(gpre), np_of(rpre)) < 1e-2
     assert rel_err(np_of(gpost), np_of(rpost)) < 1e-2
-    assert torch.isfinite(gw).all() and torch.isfinite(gres).all()
+    rres = O.sinkhorn_knopp_vjp(hr.cpu().numpy(), np_of(rM), iters=20, eps=EPS)
+    assert rel_err(np_of(gres), rres) < 1e-2
+    assert rel_err(np_of(gw), np_of(rgw)) < 2e-2
 
 
 @pytest.mark.parametrize("T,C,dt", [(300, 1024, "bf16"), (40, 256, "bf16"), (70, 512, "f16"), (3, 1024, "bf16"),

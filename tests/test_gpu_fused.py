@@ -147,7 +147,9 @@ def test_layer_backward_raw_matches_oracle(B, n, C, xdt):
 
 
 @pytest.mark.parametrize("B,n,C", [(6, 4, 96), (5, 16, 64), (4, 8, 33), (3, 24, 40), (3, 3, 16), (4, 16, 256),
-                                   (3, 16, 1024)])
+                                   (3, 16, 1024),
+                                   # C beyond the layer-wide kernel's one chunk per thread: the general kernel
+                                   (2, 4, 20000), (2, 8, 5000)])
 @pytest.mark.parametrize("xdt", ["f32", "bf16", "f16"])
 def test_dynamic_per_token_matches_oracle(B, n, C, xdt):
     """Per-token H_pre/H_post [B, n] and H_res [B, n, n] (forward and all gradients)."""
@@ -164,6 +166,34 @@ def test_dynamic_per_token_matches_oracle(B, n, C, xdt):
     for name, got, r in zip(["dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], gots, ref):
         tol = _grad_tol(xdt) if name == "dx" else 1e-4
         assert rel_err(got, r) < tol, (name, B, n, C, xdt, rel_err(got, r))
+
+
+@pytest.mark.parametrize("B,n,C,xdt,gdt", [(64, 4, 4096, "bf16", "bf16"), (48, 8, 2048, "bf16", "bf16"),
+                                           (40, 4, 1024, "bf16", "f32"), (30, 8, 512, "f16", "f32"),
+                                           (25, 3, 200, "f32", "f32")])
+@pytest.mark.parametrize("legacy", [0, 1])
+def test_per_token_backward_with_many_tokens_per_workgroup(B, n, C, xdt, gdt, legacy, knobs):
+    """Per-token n <= 8 with MHC_BWD_GRID = 3: every workgroup walks many tokens, so the per-token reset
+    of the parameter sums and the reuse of the LDS reduction run.  n = 4, C = 4096 bf16 is the full-tile
+    variant of the benchmarked shape; fp32 dout comes with the default fp32 output.  MHC_BWD_LEGACY = 1
+    sends the same shapes to the general backward kernel.  A second run is bitwise identical."""
+    knobs("MHC_BWD_GRID", 3)
+    knobs("MHC_BWD_LEGACY", legacy)
+    x, dout, hpre, hpost, hres, w = _bwd_case(B, n, C, xdt, gdt, 1700 + B + n + C, per_token=True)
+    runs = []
+    for _ in range(2):
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        xt = dev_tensor(x, xdt).requires_grad_(True)
+        out = ops.mhc_layer_forward_dynamic(xt, *ps, sinkhorn_iters=20, eps=1e-5,
+                                            output_dtype=xt.dtype if gdt == xdt and xdt != "f32" else None)
+        out.backward(dev_tensor(dout, gdt))
+        runs.append([xt.grad.clone()] + [t.grad.clone() for t in ps])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    ref = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=1e-5)
+    for name, got, r in zip(["dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], runs[0], ref):
+        tol = _grad_tol(xdt) if name == "dx" else 1e-4
+        assert rel_err(np_of(got), r) < tol, (name, rel_err(np_of(got), r))
 
 
 def test_backward_is_deterministic():
