@@ -208,6 +208,23 @@ int mhc_layer_bwd(const void* x, int x_dtype, const void* dout, int dout_dtype,
                   size_t workspace_bytes, int64_t T, int n, int C, int per_token, int iters,
                   float eps, void* stream);
 
+/* mhc_layer_bwd without a workspace argument: the workspace is a fixed
+ * device array inside the library (64 MiB per GPU, reserved on a GPU by the
+ * first call there and held until the process ends), so this call allocates
+ * nothing.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Shapes whose mhc_layer_bwd_workspace_bytes
+ * exceed 64 MiB are rejected with MHC_ERR_INVALID_ARG (e.g. layer-wide n = 4,
+ * C = 4096 needs about 35 MB on a 256-CU GPU; per-token n = 16 needs its
+ * Sinkhorn VJP state too).  All calls on one GPU share its array: calls that
+ * overlap on one GPU (different streams, or threads on different streams)
+ * race; calls on one stream are ordered by it. */
+int mhc_layer_bwd_noalloc(const void* x, int x_dtype, const void* dout, int dout_dtype,
+                          const float* h_pre_raw, const float* h_post_raw, const float* h_res_raw,
+                          const float* M, const float* rms_weight, void* dx, float* d_h_pre_raw,
+                          float* d_h_post_raw, float* d_h_res_raw, float* d_rms_weight, int64_t T, int n,
+                          int C, int per_token, int iters, float eps, void* stream);
+
 /* Second stage of mhc_layer_bwd on its own: after mhc_fused_bwd_partials
  * (h_mode MHC_H_RAW, the first mhc_fused_bwd_workspace_bytes() bytes of this
  * workspace, per-token dM / dh written into d_h_res_raw / d_h_pre_raw /

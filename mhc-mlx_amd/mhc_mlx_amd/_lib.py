@@ -59,6 +59,8 @@ SIGNATURES = {
     "mhc_layer_bwd_workspace_bytes": ([_I64, _I32, _I32, _I32, _I32], _SZ),
     "mhc_layer_bwd": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I64,
                        _I32, _I32, _I32, _I32, _F32, _VP], _I32),
+    "mhc_layer_bwd_noalloc": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I32,
+                               _I32, _I32, _I32, _F32, _VP], _I32),
     "mhc_layer_bwd_reduce": ([_VP, _SZ, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I32, _I32, _I32, _I32,
                               _F32, _VP], _I32),
     "mhc_stream_mix_add_fwd": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP, _I32, _VP, _I32, _I64, _I32, _I32,
