@@ -22,6 +22,7 @@
 
 #include "mhc_device.hpp"
 #include "mhc_generic.hpp"
+#include "mhc_mfma32.hpp"
 #include "mhc_host.hpp"
 #include "mhc_plan.hpp"
 #include "mhc_reduce.hpp"
@@ -1759,6 +1760,12 @@ extern "C" int mhc_fused_bwd_partials(const void* x, int x_dtype, const void* do
   MHC_CHECK_ARG(dout_dtype == MHC_DTYPE_F32 || dout_dtype == x_dtype,
                 "dout_dtype (%d) must be fp32 or x_dtype (%d)", dout_dtype, x_dtype);
   if (nmax_for(n) == 0) {
+    Mf32Args F{};
+    F.x = x; F.g = dout; F.out = dx; F.M = M; F.hpre = h_pre; F.hpost = h_post; F.w = rms_weight;
+    F.part = (float*)workspace; F.T = T; F.M_ts = M_token_stride; F.h_ts = h_token_stride; F.n = n; F.C = C;
+    F.Cp = L.Cp; F.P = L.P; F.h_mode = h_mode; F.eps = eps;
+    const int rc = mf32_fused_bwd(F, x_dtype, dout_dtype, L.gmax, (hipStream_t)stream, num_partials);
+    if (rc != 1) return rc;
     GenArgs G{};
     G.x = x; G.g = dout; G.out = dx; G.M = M; G.hpre = h_pre; G.hpost = h_post; G.w = rms_weight;
     G.part = (float*)workspace;

@@ -16,6 +16,7 @@
 
 #include "mhc_device.hpp"
 #include "mhc_generic.hpp"
+#include "mhc_mfma32.hpp"
 #include "mhc_host.hpp"
 #include "mhc_plan.hpp"
 #include "mhc_sinkhorn.hpp"
@@ -692,6 +693,11 @@ extern "C" int mhc_fused_fwd(const void* x, int x_dtype, const float* M, int64_t
   MHC_CHECK_ARG(out_dtype == MHC_DTYPE_F32 || out_dtype == x_dtype,
                 "out_dtype (%d) must be fp32 or x_dtype (%d)", out_dtype, x_dtype);
   if (nmax_for(n) == 0) {
+    Mf32Args F{};
+    F.x = x; F.out = out; F.inv_rms = inv_rms; F.M = M; F.hpre = h_pre; F.hpost = h_post; F.w = rms_weight;
+    F.T = T; F.M_ts = M_token_stride; F.h_ts = h_token_stride; F.n = n; F.C = C; F.h_mode = h_mode; F.eps = eps;
+    const int rc = mf32_fused_fwd(F, x_dtype, out_dtype, (hipStream_t)stream);
+    if (rc != 1) return rc;
     GenArgs G{};
     G.x = x; G.out = out; G.M = M; G.hpre = h_pre; G.hpost = h_post; G.w = rms_weight;
     G.inv_rms = inv_rms; G.T = T; G.M_ts = M_token_stride; G.h_ts = h_token_stride; G.n = n;

@@ -1,0 +1,570 @@
+// Fused mHC forward and backward for 16 < n <= 32 on MFMA (gfx950
+// v_mfma_f32_16x16x32, bf16 / fp16: exact 16-bit products, fp32 sums).
+//
+// At n = 32 the stream mix is 1024 FMAs per channel, far more VALU issue
+// time than the channel's HBM time, so every contraction over streams runs on
+// the matrix cores with the fp32 parameters split into three 16-bit terms
+// (split3: for bf16 they sum exactly to the fp32 value, so the MFMA forms the
+// products of the fp32 parameters with the 16-bit data):
+//   forward   y = a^T X,  out = M X + p (y inv w)
+//   backward  y = a^T X,  dyn = p^T G,  dx = M^T G + a dy,  dM = G X^T
+// n is padded to 32 with zero parameters; streams >= n are neither loaded
+// nor stored.
+//
+// Lane layout (q = lane >> 4, r = lane & 15).  A wave owns 128-channel
+// slabs; in a slab the lane loads streams 8q .. 8q+7 of channels
+// [8r, 8r + 8) (eight 16-byte loads).  Transposed in registers, channel v of
+// that range gives the B operand "streams 8q .. 8q+7 of column r", i.e. the K
+// index of the MFMA runs over (q, element) = stream, and the columns are the
+// 16 channels 8r + v of the 16 lanes r.  The A operand of lane (q, r) is row
+// r of a 16-row block of the parameter matrix at the same streams, and D
+// holds rows 4q .. 4q+3 of column r: out (or dx) of streams 16I + 4q + k at
+// channel 8r + v.  Over v = 0..7 the lane so collects 8 contiguous channels
+// of 8 output streams, stored as 16-byte rows.
+//
+// dM = G X^T contracts over channels instead: each wave stages its slab of x
+// and g in LDS as one row per stream, and A (rows of g) and B (rows of x)
+// are read back as 16-byte row pieces, 32 channels per MFMA.
+#include "mhc_device.hpp"
+#include "mhc_host.hpp"
+#include "mhc_mfma32.hpp"
+#include "mhc_plan.hpp"
+
+namespace mhc {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// D += A B for one 16 x 16 x 32 block; operands are eight 16-bit elements,
+// element e of word m at half (e & 1) of word e >> 1.
+template <typename T>
+MHC_DEV f32x4 mfma32k(u32x4 a, u32x4 b, f32x4 c);
+template <>
+MHC_DEV f32x4 mfma32k<__bf16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+template <>
+MHC_DEV f32x4 mfma32k<_Float16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+
+// split3 of eight values as three packed operands (term e of v[0..7]).
+template <typename T>
+MHC_DEV void split3x8(const float (&v)[8], u32x4 (&out)[3]) {
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    float a = v[2 * h], b = v[2 * h + 1];
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+      const uint32_t wd = pack2<T>(a, b);
+      a -= lo16<T>(wd);
+      b -= hi16<T>(wd);
+      out[e][h] = wd;
+    }
+  }
+}
+
+// Eight streams x eight channels (stream e in rows[e], channel v at element
+// v) -> per channel v the operand "streams 0..7 of channel v".
+template <typename T>
+MHC_DEV void transpose8(const Vec<T, 8> (&rows)[8], u32x4 (&b)[8]) {
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const int wd = v >> 1;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      b[v][m] = (v & 1) ? pack_hi16<T>(rows[2 * m].w[wd], rows[2 * m + 1].w[wd])
+                        : pack_lo16<T>(rows[2 * m].w[wd], rows[2 * m + 1].w[wd]);
+  }
+}
+
+// D = sum_e A_e B over the three split terms, smallest first.
+template <typename T>
+MHC_DEV f32x4 mfma_split3(const u32x4 (&a)[3], u32x4 b, f32x4 acc) {
+#pragma unroll
+  for (int e = 2; e >= 0; --e) acc = mfma32k<T>(a[e], b, acc);
+  return acc;
+}
+
+// Four output rows of eight channels, filled a channel pair (p = 0..3) at a
+// time: 16-bit rows as packed words (one conversion per pair), fp32 rows as
+// the values themselves; stored as 16-byte pieces.
+template <typename OT>
+struct OutRows {
+  static constexpr bool kHalf = ElemTraits<OT>::kBytes == 2;
+  uint32_t w[4][kHalf ? 4 : 8];
+  MHC_DEV void put(int p, f32x4 even, f32x4 odd) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (kHalf) {
+        w[k][p] = pack2<OT>(even[k], odd[k]);
+      } else {
+        // through scalars: a bit_cast of an ext-vector element reads element 0
+        const float e0 = even[k], e1 = odd[k];
+        w[k][2 * p] = __builtin_bit_cast(uint32_t, e0);
+        w[k][2 * p + 1] = __builtin_bit_cast(uint32_t, e1);
+      }
+    }
+  }
+  MHC_DEV void store(int k, OT* dst) const {
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+    if constexpr (kHalf) {
+      st_nt(d, w[k][0], w[k][1], w[k][2], w[k][3]);
+    } else {
+      st16<false>(d, w[k][0], w[k][1], w[k][2], w[k][3]);
+      st16<false>(d + 4, w[k][4], w[k][5], w[k][6], w[k][7]);
+    }
+  }
+};
+
+template <bool RAW>
+MHC_DEV float act_pre(float h) { return RAW ? sigmoid_fast(h) : h; }
+template <bool RAW>
+MHC_DEV float act_post(float h) { return RAW ? 2.0f * sigmoid_fast(h) : h; }
+
+// ---------------------------------------------------------------------------
+// Forward.  One token at a time per workgroup of S / SPW waves (S = C / 128
+// slabs); the grid strides over tokens, so layer-wide parameters are split
+// once per workgroup.  Before the RMS barrier only y = a^T X runs; the mix
+// runs after it, slab by slab, straight into the output rows.
+// ---------------------------------------------------------------------------
+
+template <typename XT, typename OT, int SPW, bool PT, bool RAW>
+__global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
+  __shared__ float s_red[2][16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int n = A.n, C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  int cb[SPW];
+#pragma unroll
+  for (int s = 0; s < SPW; ++s) cb[s] = (wave * SPW + s) * 128 + 8 * r;
+
+  // a of streams 8q+e (the A operand of y), M rows 16I + r at streams 8q+e
+  // (the A operands of the mix), p of the output rows 16I + 4q + k
+  u32x4 aa[3], am[2][3];
+  float pv[2][4];
+  auto load_params = [&](int64_t t) {
+    const float* M = A.M + t * A.M_ts;
+    const float* hp = A.hpre + t * A.h_ts;
+    const float* hq = A.hpost + t * A.h_ts;
+    float av[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) av[e] = 8 * q + e < n ? act_pre<RAW>(hp[8 * q + e]) : 0.0f;
+    split3x8<XT>(av, aa);
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      const int row = 16 * I + r;
+      float mv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mv[e] = (row < n && 8 * q + e < n) ? M[row * n + 8 * q + e] : 0.0f;
+      split3x8<XT>(mv, am[I]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int o = 16 * I + 4 * q + k;
+        pv[I][k] = o < n ? act_post<RAW>(hq[o]) : 0.0f;
+      }
+    }
+  };
+  if constexpr (!PT) load_params(0);
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const XT* xt = (const XT*)A.x + t * nC;
+    OT* ot = (OT*)A.out + t * nC;
+    u32x4 bx[SPW][8];
+    {
+      Vec<XT, 8> xr[SPW][8];
+#pragma unroll
+      for (int s = 0; s < SPW; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (8 * q + e < n) xr[s][e].load(xt + (int64_t)(8 * q + e) * C + cb[s]);
+          else xr[s][e].zero();
+        }
+      if constexpr (PT) load_params(t);
+#pragma unroll
+      for (int s = 0; s < SPW; ++s) transpose8<XT>(xr[s], bx[s]);
+    }
+    float y[SPW][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const f32x4 acc = mfma_split3<XT>(aa, bx[s][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        y[s][v] = acc[0];
+        ss = fmaf(acc[0], acc[0], ss);
+      }
+    // the four lane groups q hold the same y: count it once
+    ss = q == 0 ? ss : 0.0f;
+    ss = wave_sum(ss);
+    if (lane == 0) s_red[it & 1][wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < nwaves; ++w) tot += s_red[it & 1][w];
+    const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
+    if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      const float4 w0 = *reinterpret_cast<const float4*>(A.w + cb[s]);
+      const float4 w1 = *reinterpret_cast<const float4*>(A.w + cb[s] + 4);
+      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      float yn[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) yn[v] = (y[s][v] * inv) * wv[v];
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        // four output rows of this lane, converted a channel pair at a time
+        OutRows<OT> rows;
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = mfma_split3<XT>(am[I], bx[s][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc[k] = fmaf(yn[v], pv[I][k], acc[k]);
+          if (v & 1) rows.put(v >> 1, even, acc);
+          else even = acc;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int row = 16 * I + 4 * q + k;
+          if (row < n) rows.store(k, ot + (int64_t)row * C + cb[s]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, layer-wide parameters.  A persistent workgroup of C / 128 waves
+// walks tokens t = b, b + G, ...; per token and slab:
+//   before the RMS barrier: y = a^T X, dyn = p^T G (MFMA), the two per-token
+//     sums, and dM += G X^T over the slab staged in LDS (MFMA);
+//   after it: dy, yn and the dw contribution per channel; dx = M^T G + a dy
+//     (MFMA, a dy as the accumulator input) stored as 16-byte rows; dA and
+//     dP as lane partials from x and g read back from the staged slab.
+// dM, dA, dP and dw stay in registers across the workgroup's tokens and end
+// in its partial row, the waves' parts added in wave order.
+// ---------------------------------------------------------------------------
+
+constexpr int kMf32Row = 128 + 8;                 // LDS row: 16-bit elements (68 dwords, 4 mod 64 banks)
+constexpr int kMf32Slab = 2 * 32 * kMf32Row;      // x rows then g rows
+constexpr int kMf32MaxWaves = 8;                  // C <= 1024
+constexpr int kMf32Par = 32 * 32 + 2 * 32;
+
+template <typename XT, bool RAW>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_kernel(Mf32Args A) {
+  extern __shared__ __align__(16) uint16_t mf32_lds[];
+  __shared__ float s_red[2][2][kMf32MaxWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int n = A.n, C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  uint16_t* xs = mf32_lds + (size_t)wave * kMf32Slab;
+  uint16_t* gs = xs + 32 * kMf32Row;
+  const int cb = wave * 128 + 8 * r;
+
+  // parameters: a, p of streams 8q+e (A operands of y, dyn); column 16J + r
+  // of M at rows 8q+e (A operand of M^T); a of the dx rows 16J + 4q + k
+  u32x4 aa[3], ap[3], amt[2][3];
+  float a4[2][4];
+  {
+    float av[8], pv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = 8 * q + e;
+      av[e] = i < n ? act_pre<RAW>(A.hpre[i]) : 0.0f;
+      pv[e] = i < n ? act_post<RAW>(A.hpost[i]) : 0.0f;
+    }
+    split3x8<XT>(av, aa);
+    split3x8<XT>(pv, ap);
+#pragma unroll
+    for (int J = 0; J < 2; ++J) {
+      const int col = 16 * J + r;
+      float mv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mv[e] = (col < n && 8 * q + e < n) ? A.M[(8 * q + e) * n + col] : 0.0f;
+      split3x8<XT>(mv, amt[J]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = 16 * J + 4 * q + k;
+        a4[J][k] = j < n ? act_pre<RAW>(A.hpre[j]) : 0.0f;
+      }
+    }
+  }
+  float wv[8];
+  {
+    const float4 w0 = *reinterpret_cast<const float4*>(A.w + cb);
+    const float4 w1 = *reinterpret_cast<const float4*>(A.w + cb + 4);
+    wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+    wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+  }
+  f32x4 dm[2][2];
+#pragma unroll
+  for (int I = 0; I < 2; ++I)
+#pragma unroll
+    for (int J = 0; J < 2; ++J) dm[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float dA[8], dP[8], dwv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dA[e] = dP[e] = dwv[e] = 0.0f;
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const XT* xt = (const XT*)A.x + t * nC;
+    const XT* gt = (const XT*)A.g + t * nC;
+    float y[8], dyn[8];
+    float ss = 0.0f, sr = 0.0f;
+    {
+      Vec<XT, 8> xr[8], gr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (8 * q + e < n) {
+          xr[e].load(xt + (int64_t)(8 * q + e) * C + cb);
+          gr[e].load(gt + (int64_t)(8 * q + e) * C + cb);
+        } else {
+          xr[e].zero();
+          gr[e].zero();
+        }
+      }
+      // stage the slab (one LDS row per stream; zero rows for streams >= n)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        *reinterpret_cast<u32x4*>(&xs[(8 * q + e) * kMf32Row + 8 * r]) =
+            u32x4{xr[e].w[0], xr[e].w[1], xr[e].w[2], xr[e].w[3]};
+        *reinterpret_cast<u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]) =
+            u32x4{gr[e].w[0], gr[e].w[1], gr[e].w[2], gr[e].w[3]};
+      }
+      u32x4 bx[8], bg[8];
+      transpose8<XT>(xr, bx);
+      transpose8<XT>(gr, bg);
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const f32x4 ay = mfma_split3<XT>(aa, bx[v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        const f32x4 ad = mfma_split3<XT>(ap, bg[v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        y[v] = ay[0];
+        dyn[v] = ad[0];
+        ss = fmaf(ay[0], ay[0], ss);
+        sr = fmaf(ad[0] * ay[0], wv[v], sr);
+      }
+    }
+    // dM over the slab: A = g rows 16I + r, B = x rows 16J + r, 32 channels per step
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      u32x4 ga[2], xb[2];
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        ga[I] = *reinterpret_cast<const u32x4*>(&gs[(16 * I + r) * kMf32Row + 32 * kk + 8 * q]);
+        xb[I] = *reinterpret_cast<const u32x4*>(&xs[(16 * I + r) * kMf32Row + 32 * kk + 8 * q]);
+      }
+#pragma unroll
+      for (int I = 0; I < 2; ++I)
+#pragma unroll
+        for (int J = 0; J < 2; ++J) dm[I][J] = mfma32k<XT>(ga[I], xb[J], dm[I][J]);
+    }
+    // the four lane groups q hold the same y and dyn: count them once
+    ss = q == 0 ? ss : 0.0f;
+    sr = q == 0 ? sr : 0.0f;
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    lds_barrier();
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+
+    float dyv[8], ynv[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const float yi = y[v] * inv;
+      dyv[v] = dyn[v] * inv * wv[v] - kf * y[v];
+      ynv[v] = yi * wv[v];
+      dwv[v] = fmaf(dyn[v], yi, dwv[v]);
+    }
+    XT* dxt = (XT*)A.out + t * nC;
+    {
+      // g back from the slab: dx = M^T g + a dy, and dP
+      Vec<XT, 8> gr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]);
+        gr[e].w[0] = u[0]; gr[e].w[1] = u[1]; gr[e].w[2] = u[2]; gr[e].w[3] = u[3];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) dP[e] = fmaf(gr[e].get(v), ynv[v], dP[e]);
+      u32x4 bg[8];
+      transpose8<XT>(gr, bg);
+#pragma unroll
+      for (int J = 0; J < 2; ++J) {
+        uint32_t ow[4][4];
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = {a4[J][0] * dyv[v], a4[J][1] * dyv[v], a4[J][2] * dyv[v], a4[J][3] * dyv[v]};
+          acc = mfma_split3<XT>(amt[J], bg[v], acc);
+          if (v & 1) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ow[k][v >> 1] = pack2<XT>(even[k], acc[k]);
+          } else {
+            even = acc;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int j = 16 * J + 4 * q + k;
+          if (j < n)
+            st_nt(reinterpret_cast<uint32_t*>(dxt + (int64_t)j * C + cb), ow[k][0], ow[k][1], ow[k][2], ow[k][3]);
+        }
+      }
+    }
+    {
+      // x back from the slab: dA
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        Vec<XT, 8> xv;
+        const u32x4 u = *reinterpret_cast<const u32x4*>(&xs[(8 * q + e) * kMf32Row + 8 * r]);
+        xv.w[0] = u[0]; xv.w[1] = u[1]; xv.w[2] = u[2]; xv.w[3] = u[3];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) dA[e] = fmaf(dyv[v], xv.get(v), dA[e]);
+      }
+    }
+  }
+
+  // ---- the workgroup's partial row [dw C | 0 .. Cp | dM n*n | dA n | dP n | 0 .. P]
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  if (q == 0) {
+    *reinterpret_cast<float4*>(prow + cb) = make_float4(dwv[0], dwv[1], dwv[2], dwv[3]);
+    *reinterpret_cast<float4*>(prow + cb + 4) = make_float4(dwv[4], dwv[5], dwv[6], dwv[7]);
+  }
+  if (tid == 0)
+    for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
+  // dA, dP: sums over the 16 lanes of a group, then the waves in order
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    dA[e] = group_sum<16>(dA[e]);
+    dP[e] = group_sum<16>(dP[e]);
+  }
+  __syncthreads();  // every wave is done with its slab: reuse the LDS for the cross-wave sums
+  float* s_fin = reinterpret_cast<float*>(mf32_lds);  // [wave][kMf32Par]
+  float* mine = s_fin + wave * kMf32Par;
+#pragma unroll
+  for (int I = 0; I < 2; ++I)
+#pragma unroll
+    for (int J = 0; J < 2; ++J)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) mine[(16 * I + 4 * q + k) * 32 + 16 * J + r] = dm[I][J][k];
+  if (r == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      mine[1024 + 8 * q + e] = dA[e];
+      mine[1024 + 32 + 8 * q + e] = dP[e];
+    }
+  }
+  __syncthreads();
+  const int nn = n * n;
+  for (int k = tid; k < nn + 2 * n; k += blockDim.x) {
+    int src;
+    if (k < nn) src = (k / n) * 32 + (k % n);
+    else if (k < nn + n) src = 1024 + (k - nn);
+    else src = 1024 + 32 + (k - nn - n);
+    float sum = 0.0f;
+    for (int w = 0; w < nwaves; ++w) sum += s_fin[w * kMf32Par + src];
+    prow[A.Cp + k] = sum;
+  }
+  if (tid == 0)
+    for (int c = A.Cp + nn + 2 * n; c < A.P; ++c) prow[c] = 0.0f;
+}
+
+template <typename F>
+int by_half(int code, F&& f) {
+  if (code == MHC_DTYPE_BF16) return f((__bf16*)nullptr);
+  if (code == MHC_DTYPE_F16) return f((_Float16*)nullptr);
+  return 1;
+}
+
+}  // namespace
+
+int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
+  if (A.n <= 16 || A.n > 32 || A.C % 128 != 0 || A.C > 2048) return 1;
+  if (od != MHC_DTYPE_F32 && od != xd) return 1;
+  if (!aligned(A.x, 16) || !aligned(A.out, 16) || !aligned(A.w, 16)) return 1;
+  if (knob(kKnobFwdMfma, 1) == 0) return 1;
+  const int S = A.C / 128;
+  const int spw = S <= 8 ? 1 : 2;
+  if (S % spw != 0) return 1;
+  const int waves = S / spw;
+  const bool pt = A.M_ts != 0, raw = A.h_mode == MHC_H_RAW;
+  const int per_cu = knob(kKnobFwdGrid, 8);
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * std::max(per_cu, 1)));
+  const dim3 g((unsigned)blocks), b(waves * 64);
+  return by_half(xd, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    auto go = [&](auto* op) {
+      using OT = std::remove_pointer_t<decltype(op)>;
+#define MF32_FWD(SPW_, PT_, RAW_) hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, PT_, RAW_>), g, b, 0, s, A)
+      if (spw == 1) {
+        if (pt) { if (raw) MF32_FWD(1, true, true); else MF32_FWD(1, true, false); }
+        else { if (raw) MF32_FWD(1, false, true); else MF32_FWD(1, false, false); }
+      } else {
+        if (pt) { if (raw) MF32_FWD(2, true, true); else MF32_FWD(2, true, false); }
+        else { if (raw) MF32_FWD(2, false, true); else MF32_FWD(2, false, false); }
+      }
+#undef MF32_FWD
+      MHC_CHECK_LAUNCH("mf32_fwd_kernel");
+      return MHC_OK;
+    };
+    return od == MHC_DTYPE_F32 ? go((float*)nullptr) : go((XT*)nullptr);
+  });
+}
+
+int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
+  if (A.n <= 16 || A.n > 32 || A.M_ts != 0 || A.C % 128 != 0 || A.C > 128 * kMf32MaxWaves) return 1;
+  if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
+  if (A.P != A.Cp + round_up(A.n * A.n + 2 * A.n, 4)) return 1;
+  if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.out, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
+    return 1;
+  if (knob(kKnobBwdMfma, 1) == 0) return 1;
+  const int waves = A.C / 128;
+  const size_t smem = std::max<size_t>((size_t)waves * kMf32Slab * sizeof(uint16_t),
+                                       (size_t)waves * kMf32Par * sizeof(float));
+  const bool raw = A.h_mode == MHC_H_RAW;
+  return by_half(xd, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    const void* kfn = raw ? (const void*)mf32_bwd_kernel<XT, true> : (const void*)mf32_bwd_kernel<XT, false>;
+    const int occ = occupancy_blocks(kfn, waves * 64, smem);
+    if (occ <= 0) return 1;
+    int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
+    const int grid_pref = knob(kKnobBwdGrid, 0);
+    if (grid_pref > 0) blocks = std::min<int64_t>(gmax, grid_pref);
+    blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+    const dim3 g((unsigned)blocks), b(waves * 64);
+    if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true>), g, b, smem, s, A);
+    else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false>), g, b, smem, s, A);
+    MHC_CHECK_LAUNCH("mf32_bwd_kernel");
+    *num_partials = blocks;
+    return MHC_OK;
+  });
+}
+
+}  // namespace mhc

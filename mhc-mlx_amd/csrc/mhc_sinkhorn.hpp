@@ -321,4 +321,210 @@ MHC_DEV void sk_bwd_group_reg(const float* __restrict__ H, const float* __restri
   }
 }
 
+// ---------------------------------------------------------------------------
+// Block layout: one NP x NP matrix per wavefront, NP in {16, 32, 64}.  Lane
+// (R = lane >> 3, Q = lane & 7) holds the B x B block (B = NP / 8) at rows
+// R*B .. R*B+B-1 and columns Q*B .. Q*B+B-1.  A row sum adds B values in the
+// lane and then the 8 lanes of R (lane ^ 1, 2, 4: DPP); a column sum adds B
+// values in the lane and then the 8 lanes of Q (lane ^ 8: DPP, lane ^ 16 and
+// ^ 32: ds_bpermute).  Per iteration that is 3B + 3B cross-lane steps,
+// against 5 per element for the one-row-per-lane-pair layout of SkLayout
+// (NP = 32: 24 against 80), which bounds a single matrix's latency.
+// Same semantics and arithmetic per element as sk_fwd_group / sk_bwd_group;
+// only the association of each row or column sum differs.
+// ---------------------------------------------------------------------------
+
+template <int NP>
+MHC_DEV void sk_fwd_blk(const float* __restrict__ H, float* __restrict__ out, int n, int iters, float eps,
+                        int lane) {
+  constexpr int B = NP / 8;
+  const int r0 = (lane >> 3) * B, c0 = (lane & 7) * B;
+  float P[B][B];
+#pragma unroll
+  for (int a = 0; a < B; ++a) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const bool v = r0 + a < n && c0 + b < n;
+      P[a][b] = v ? H[(r0 + a) * n + c0 + b] : -INFINITY;
+      mx = fmaxf(mx, P[a][b]);
+    }
+    mx = group_max<8>(mx);
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const bool v = r0 + a < n && c0 + b < n;
+      P[a][b] = v ? expf(P[a][b] - mx) : 0.0f;
+    }
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int a = 0; a < B; ++a) {
+      float s = 0.0f;
+#pragma unroll
+      for (int b = 0; b < B; ++b) s += P[a][b];
+      s = group_sum<8>(s);
+      const float rsc = (r0 + a < n && s > eps) ? sk_rcp(s) : 1.0f;
+#pragma unroll
+      for (int b = 0; b < B; ++b) P[a][b] *= rsc;
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      float cs = 0.0f;
+#pragma unroll
+      for (int a = 0; a < B; ++a) cs += P[a][b];
+      cs = strided_sum<8, 64>(cs);
+      const float csc = (c0 + b < n && cs > eps) ? sk_rcp(cs) : 0.0f;
+#pragma unroll
+      for (int a = 0; a < B; ++a) P[a][b] *= csc;
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < B; ++a)
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+      if (r0 + a < n && c0 + b < n) out[(r0 + a) * n + c0 + b] = P[a][b];
+}
+
+// Floats of VJP state per matrix in the block layout: per iteration the row
+// sums, cumulative row scales, column sums and cumulative column scales.
+__host__ __device__ inline int64_t sk_blk_state_floats(int np, int iters) {
+  return (int64_t)4 * np * (iters > 0 ? iters : 1);
+}
+
+// VJP of sk_fwd_blk: dH = d/dH <dM, SK(H)>.  st: this wavefront's state,
+// [iters][rs | R | cs | C][NP] (LDS or global memory); every lane writes the
+// entries of its rows and columns (the lanes sharing a row or column write
+// the same value) and reads back only its own.
+template <int NP>
+MHC_DEV void sk_bwd_blk(const float* __restrict__ H, const float* __restrict__ dM, float* __restrict__ dH, int n,
+                        int iters, float eps, float* st, int lane) {
+  constexpr int B = NP / 8;
+  static_assert(B * B <= 64, "tie mask holds one bit per element");
+  const int r0 = (lane >> 3) * B, c0 = (lane & 7) * B;
+  float K[B][B], Gd[B][B];
+  uint64_t tie = 0;  // bit a*B+b: H at the row maximum
+#pragma unroll
+  for (int a = 0; a < B; ++a) {
+    float hv[B];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const bool v = r0 + a < n && c0 + b < n;
+      hv[b] = v ? H[(r0 + a) * n + c0 + b] : -INFINITY;
+      mx = fmaxf(mx, hv[b]);
+    }
+    mx = group_max<8>(mx);
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const bool v = r0 + a < n && c0 + b < n;
+      K[a][b] = v ? expf(hv[b] - mx) : 0.0f;
+      if (v && hv[b] == mx) tie |= (uint64_t)1 << (a * B + b);
+      Gd[a][b] = K[a][b];  // the forward's P
+    }
+  }
+  // forward recompute, recording sums and cumulative scales
+  float Rc[B], Cc[B];
+#pragma unroll
+  for (int a = 0; a < B; ++a) Rc[a] = Cc[a] = 1.0f;
+  for (int it = 0; it < iters; ++it) {
+    float* sti = st + (int64_t)it * 4 * NP;
+#pragma unroll
+    for (int a = 0; a < B; ++a) {
+      float s = 0.0f;
+#pragma unroll
+      for (int b = 0; b < B; ++b) s += Gd[a][b];
+      s = group_sum<8>(s);
+      const float rsc = (r0 + a < n && s > eps) ? sk_rcp(s) : 1.0f;
+#pragma unroll
+      for (int b = 0; b < B; ++b) Gd[a][b] *= rsc;
+      Rc[a] *= rsc;
+      sti[r0 + a] = s;
+      sti[NP + r0 + a] = Rc[a];
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      float cs = 0.0f;
+#pragma unroll
+      for (int a = 0; a < B; ++a) cs += Gd[a][b];
+      cs = strided_sum<8, 64>(cs);
+      const float csc = (c0 + b < n && cs > eps) ? sk_rcp(cs) : 0.0f;
+#pragma unroll
+      for (int a = 0; a < B; ++a) Gd[a][b] *= csc;
+      Cc[b] *= csc;
+      sti[2 * NP + c0 + b] = cs;
+      sti[3 * NP + c0 + b] = Cc[b];
+    }
+  }
+  // reverse sweep
+#pragma unroll
+  for (int a = 0; a < B; ++a)
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const bool v = r0 + a < n && c0 + b < n;
+      Gd[a][b] = v ? dM[(r0 + a) * n + c0 + b] : 0.0f;
+    }
+  for (int it = iters - 1; it >= 0; --it) {
+    const float* sti = st + (int64_t)it * 4 * NP;
+    const float* stp = st + (int64_t)(it > 0 ? it - 1 : 0) * 4 * NP;
+    float Rk[B], Rp[B], Cp[B];
+#pragma unroll
+    for (int a = 0; a < B; ++a) {
+      Rk[a] = sti[NP + r0 + a];
+      Rp[a] = it > 0 ? stp[NP + r0 + a] : 1.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) Cp[b] = it > 0 ? stp[3 * NP + c0 + b] : 1.0f;
+    // column step: input R_k K C_{k-1}
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int a = 0; a < B; ++a) dot += Gd[a][b] * (Rk[a] * K[a][b] * Cp[b]);
+      dot = strided_sum<8, 64>(dot);
+      const float cs = sti[2 * NP + c0 + b];
+      if (c0 + b < n && cs > eps) {
+        const float sc = sk_rcp(cs);
+#pragma unroll
+        for (int a = 0; a < B; ++a) Gd[a][b] = sc * Gd[a][b] - sc * sc * dot;
+      } else {
+#pragma unroll
+        for (int a = 0; a < B; ++a) Gd[a][b] = 0.0f;
+      }
+    }
+    // row step: input R_{k-1} K C_{k-1}
+#pragma unroll
+    for (int a = 0; a < B; ++a) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int b = 0; b < B; ++b) dot += Gd[a][b] * (Rp[a] * K[a][b] * Cp[b]);
+      dot = group_sum<8>(dot);
+      const float rs = sti[r0 + a];
+      if (r0 + a < n && rs > eps) {
+        const float sc = sk_rcp(rs);
+#pragma unroll
+        for (int b = 0; b < B; ++b) Gd[a][b] = sc * Gd[a][b] - sc * sc * dot;
+      }
+    }
+  }
+  // through exp and the row-max shift (the gradient of the max split evenly
+  // among tied maxima; it is zero in exact arithmetic)
+#pragma unroll
+  for (int a = 0; a < B; ++a) {
+    float tot = 0.0f, cnt = 0.0f;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      Gd[a][b] *= K[a][b];  // K is 0 outside the matrix
+      tot += Gd[a][b];
+      cnt += (tie >> (a * B + b)) & 1 ? 1.0f : 0.0f;
+    }
+    tot = group_sum<8>(tot);
+    cnt = group_sum<8>(cnt);
+    const float corr = cnt > 0.0f ? tot / cnt : 0.0f;
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+      if (r0 + a < n && c0 + b < n)
+        dH[(r0 + a) * n + c0 + b] = Gd[a][b] - ((tie >> (a * B + b)) & 1 ? corr : 0.0f);
+  }
+}
+
 }  // namespace mhc

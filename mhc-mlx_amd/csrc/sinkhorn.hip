@@ -67,6 +67,36 @@ __global__ __launch_bounds__(kSkThreads) void sinkhorn_bwd_kernel(
   }
 }
 
+// One matrix per wavefront in the block layout (mhc_sinkhorn.hpp), for
+// 16 < n <= 64: a single layer-wide matrix is latency-bound, and this layout
+// needs a third of the cross-lane steps per iteration.
+template <int NP>
+__global__ __launch_bounds__(kSkThreads) void sinkhorn_blk_fwd_kernel(const float* __restrict__ logits,
+                                                                      float* __restrict__ out, int64_t batch,
+                                                                      int n, int iters, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wpb = blockDim.x >> 6;
+  const int64_t nn = (int64_t)n * n;
+  for (int64_t m = (int64_t)blockIdx.x * wpb + wave; m < batch; m += (int64_t)gridDim.x * wpb)
+    sk_fwd_blk<NP>(logits + m * nn, out + m * nn, n, iters, eps, lane);
+}
+
+template <int NP, bool GLOBAL_STATE>
+__global__ __launch_bounds__(kSkThreads) void sinkhorn_blk_bwd_kernel(
+    const float* __restrict__ logits, const float* __restrict__ dM, float* __restrict__ dlogits, int64_t batch,
+    int n, int iters, float eps, float* __restrict__ gstate) {
+  extern __shared__ float sk_smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wpb = blockDim.x >> 6;
+  const int64_t nn = (int64_t)n * n;
+  const int64_t per_wave = sk_blk_state_floats(NP, iters);
+  float* st = GLOBAL_STATE ? gstate + ((int64_t)blockIdx.x * wpb + wave) * per_wave : sk_smem + wave * per_wave;
+  for (int64_t m = (int64_t)blockIdx.x * wpb + wave; m < batch; m += (int64_t)gridDim.x * wpb)
+    sk_bwd_blk<NP>(logits + m * nn, dM + m * nn, dlogits + m * nn, n, iters, eps, st, lane);
+}
+
 // ---------------------------------------------------------------------------
 // n == 16, batched (per-token mappings, config 3): four lanes per matrix.
 //
@@ -446,6 +476,41 @@ SkPlan plan_bwd(int64_t batch, int n, int iters, int cus) {
   return p;
 }
 
+// Block-layout kernels (16 < n <= 64): one wave per matrix, VJP state in
+// LDS when it fits the budget, else in the workspace.
+SkPlan plan_blk(int64_t batch, int n, int iters, int cus) {
+  SkPlan p{};
+  p.np = next_pow2(n);
+  p.wpb = (int)std::min<int64_t>(kSkThreads / 64, batch);
+  if (p.wpb < 1) p.wpb = 1;
+  p.blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(batch, p.wpb), (int64_t)cus * 16));
+  const size_t per_wave = (size_t)sk_blk_state_floats(p.np, iters) * sizeof(float);
+  p.global_state = per_wave * (size_t)p.wpb > (size_t)kSkLdsBudget;
+  p.lds_bytes = p.global_state ? 0 : per_wave * (size_t)p.wpb;
+  p.ws_bytes = p.global_state ? per_wave * (size_t)p.wpb * (size_t)p.blocks : 0;
+  return p;
+}
+
+bool use_blk(int n) { return n > 16; }
+
+template <int NP>
+void launch_blk_fwd(const SkPlan& p, const float* logits, float* M, int64_t batch, int n, int iters, float eps,
+                    hipStream_t s) {
+  hipLaunchKernelGGL(sinkhorn_blk_fwd_kernel<NP>, dim3((unsigned)p.blocks), dim3(p.wpb * 64), 0, s, logits, M,
+                     batch, n, iters, eps);
+}
+
+template <int NP>
+void launch_blk_bwd(const SkPlan& p, const float* logits, const float* dM, float* dlogits, int64_t batch, int n,
+                    int iters, float eps, float* ws, hipStream_t s) {
+  if (p.global_state)
+    hipLaunchKernelGGL((sinkhorn_blk_bwd_kernel<NP, true>), dim3((unsigned)p.blocks), dim3(p.wpb * 64), 0, s,
+                       logits, dM, dlogits, batch, n, iters, eps, ws);
+  else
+    hipLaunchKernelGGL((sinkhorn_blk_bwd_kernel<NP, false>), dim3((unsigned)p.blocks), dim3(p.wpb * 64),
+                       p.lds_bytes, s, logits, dM, dlogits, batch, n, iters, eps, ws);
+}
+
 template <int NP>
 void launch_fwd(const float* logits, float* M, int64_t batch, int n, int iters, float eps,
                 hipStream_t stream, int cus) {
@@ -494,6 +559,13 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
     MHC_CHECK_LAUNCH("sinkhorn16_fwd_kernel");
     return MHC_OK;
   }
+  if (use_blk(n)) {
+    const SkPlan p = plan_blk(batch, n, iters, cus);
+    if (p.np == 32) launch_blk_fwd<32>(p, logits, M, batch, n, iters, eps, s);
+    else launch_blk_fwd<64>(p, logits, M, batch, n, iters, eps, s);
+    MHC_CHECK_LAUNCH("sinkhorn_blk_fwd_kernel");
+    return MHC_OK;
+  }
   switch (next_pow2(n)) {
     case 1: launch_fwd<1>(logits, M, batch, n, iters, eps, s, cus); break;
     case 2: launch_fwd<2>(logits, M, batch, n, iters, eps, s, cus); break;
@@ -516,6 +588,7 @@ size_t sk16_state_bytes(int64_t batch, int iters) {
 
 extern "C" size_t mhc_sinkhorn_bwd_workspace_bytes(int64_t batch, int n, int iters) {
   if (n < 1 || n > MHC_MAX_N || batch <= 0 || iters < 0) return 0;
+  if (use_blk(n)) return plan_blk(batch, n, iters, device_cu_count()).ws_bytes;
   const size_t gen = plan_bwd(batch, n, iters, device_cu_count()).ws_bytes;
   if (n == 16) return std::max(gen, sk16_state_bytes(batch, iters) + 256);
   return gen;
@@ -551,6 +624,15 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
       MHC_CHECK_LAUNCH("sinkhorn16_bwd_kernel");
       return MHC_OK;
     }
+  }
+  if (use_blk(n)) {
+    const SkPlan p = plan_blk(batch, n, iters, device_cu_count());
+    MHC_CHECK_ARG(workspace_bytes >= p.ws_bytes && (p.ws_bytes == 0 || workspace != nullptr),
+                  "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, p.ws_bytes);
+    if (p.np == 32) launch_blk_bwd<32>(p, logits, dM, dlogits, batch, n, iters, eps, (float*)workspace, s);
+    else launch_blk_bwd<64>(p, logits, dM, dlogits, batch, n, iters, eps, (float*)workspace, s);
+    MHC_CHECK_LAUNCH("sinkhorn_blk_bwd_kernel");
+    return MHC_OK;
   }
   const SkPlan p = plan_bwd(batch, n, iters, device_cu_count());
   MHC_CHECK_ARG(workspace_bytes >= p.ws_bytes && (p.ws_bytes == 0 || workspace != nullptr),

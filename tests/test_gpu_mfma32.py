@@ -1,0 +1,98 @@
+"""GPU parity of the 16 < n <= 32 MFMA kernels (csrc/mfma32.hip) against the float64 oracle.
+
+The forward covers n = 17, 24 and 32, C from one 128-channel slab to 2048 (one and two slabs per wave),
+16-bit x with 16-bit or fp32 output, layer-wide and per-token parameters; the backward covers
+layer-wide parameters with 16-bit x and dout up to C = 1024.  With the grid knobs at a few
+workgroups every workgroup walks many tokens.  Shapes outside these ranges (odd C, fp32 x, fp32
+dout, per-token backward) take the generic kernels and are covered by tests/test_gpu_fused.py.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mhc_oracle as O
+from tests._helpers import TOL, dev_tensor, np_of, params, rel_err, rng, to_dtype_np
+
+from mhc_mlx_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-5
+
+
+def _ulp_bound(got, ref, dt):
+    """One rounding to the output dtype (2^-9 / 2^-12 relative) with a factor of two, plus a floor."""
+    ulp = {"bf16": 2.0 ** -8, "f16": 2.0 ** -11}[dt]
+    err = np.abs(got - ref)
+    bound = ulp * np.abs(ref) + 1e-6
+    assert (err <= bound).all(), float((err / bound).max())
+
+
+@pytest.mark.parametrize("T,n,C", [(5, 32, 128), (40, 32, 512), (7, 24, 384), (9, 17, 256), (3, 32, 1024),
+                                   (4, 32, 2048), (6, 20, 1280)])
+@pytest.mark.parametrize("xdt,odt", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
+@pytest.mark.parametrize("per_token", [False, True])
+def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
+    knobs("MHC_FWD_GRID", 1)  # fewer workgroups than tokens: each walks several
+    g = rng(3200 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), xdt)
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T if per_token else None)
+    xt = dev_tensor(x, xdt)
+    ps = [dev_tensor(v) for v in (hpre, hpost, hres, w)]
+    fn = ops.mhc_layer_forward_dynamic if per_token else ops.mhc_layer_forward
+    with torch.no_grad():
+        out = fn(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=None if odt == "f32" else xt.dtype)
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    got = np_of(out)
+    assert rel_err(got, ref) < (1e-5 if odt == "f32" else TOL[odt]), rel_err(got, ref)
+    if odt != "f32":
+        _ulp_bound(got, ref, odt)
+
+
+@pytest.mark.parametrize("T,n,C", [(5, 32, 128), (300, 32, 512), (40, 24, 256), (33, 17, 640), (7, 32, 1024),
+                                   (64, 28, 384)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_mfma32_backward_layer_wide(T, n, C, dt, knobs):
+    knobs("MHC_BWD_GRID", 3)
+    g = rng(3300 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C)
+    runs = []
+    for _ in range(2):
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        xt = dev_tensor(x, dt).requires_grad_(True)
+        out = ops.mhc_layer_forward(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+        out.backward(dev_tensor(dout, dt))
+        runs.append([out.detach(), xt.grad] + [p.grad for p in ps])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    ref_out = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    _ulp_bound(np_of(runs[0][0]), ref_out, dt)
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    _ulp_bound(np_of(runs[0][1]), refs[0], dt)
+    for name, got, r in zip(["dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], runs[0][2:], refs[1:]):
+        assert rel_err(np_of(got), r) < 1e-4, (name, rel_err(np_of(got), r))
+
+
+def test_mfma32_matches_the_generic_kernels(knobs):
+    """The MFMA kernels and the VALU kernels they replace agree to rounding on the same inputs."""
+    T, n, C = 64, 32, 512
+    g = rng(3400)
+    x = dev_tensor(to_dtype_np(g.standard_normal((T, n, C)), "bf16"), "bf16")
+    dout = dev_tensor(to_dtype_np(g.standard_normal((T, n, C)), "bf16"), "bf16")
+    hpre, hpost, hres, w = params(g, n, C)
+    res = {}
+    for mf in (1, 0):
+        knobs("MHC_FWD_MFMA", mf)
+        knobs("MHC_BWD_MFMA", mf)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        xt = x.clone().requires_grad_(True)
+        out = ops.mhc_layer_forward(xt, *ps, eps=EPS, output_dtype=torch.bfloat16)
+        out.backward(dout)
+        res[mf] = [out.detach(), xt.grad] + [p.grad for p in ps]
+    for name, a, b in zip(["out", "dx", "dpre", "dpost", "dres", "dw"], res[1], res[0]):
+        # out and dx: one bf16 rounding of fp32 values that differ in the last bits
+        tol = 2.0 ** -8 if name in ("out", "dx") else 2e-5
+        assert rel_err(np_of(a), np_of(b)) < tol, (name, rel_err(np_of(a), np_of(b)))
