@@ -82,6 +82,18 @@ MHC_DEV void transpose8(const Vec<T, 8> (&rows)[8], u32x4 (&b)[8]) {
   }
 }
 
+// One channel of eight stream rows: the operand "streams 0..7 of channel v".
+template <typename T>
+MHC_DEV u32x4 column8(const Vec<T, 8> (&rows)[8], int v) {
+  const int wd = v >> 1;
+  u32x4 b;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    b[m] = (v & 1) ? pack_hi16<T>(rows[2 * m].w[wd], rows[2 * m + 1].w[wd])
+                   : pack_lo16<T>(rows[2 * m].w[wd], rows[2 * m + 1].w[wd]);
+  return b;
+}
+
 // D = sum_e A_e B over the three split terms, smallest first.
 template <typename T>
 MHC_DEV f32x4 mfma_split3(const u32x4 (&a)[3], u32x4 b, f32x4 acc) {
@@ -133,7 +145,9 @@ MHC_DEV float act_post(float h) { return RAW ? 2.0f * sigmoid_fast(h) : h; }
 // runs after it, slab by slab, straight into the output rows.
 // ---------------------------------------------------------------------------
 
-template <typename XT, typename OT, int SPW, bool PT, bool RAW>
+// FULL: n == 32, so no stream index is ever out of range (no per-stream
+// branches in the load, store and parameter code).
+template <typename XT, typename OT, int SPW, bool PT, bool RAW, bool FULL>
 __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
   __shared__ float s_red[2][16];
   const int tid = threadIdx.x;
@@ -141,7 +155,8 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
   const int wave = tid >> 6;
   const int nwaves = blockDim.x >> 6;
   const int q = lane >> 4, r = lane & 15;
-  const int n = A.n, C = A.C;
+  const int n = FULL ? 32 : A.n;
+  const int C = A.C;
   const int64_t nC = (int64_t)n * C;
   int cb[SPW];
 #pragma unroll
@@ -260,7 +275,7 @@ constexpr int kMf32Slab = 2 * 32 * kMf32Row;      // x rows then g rows
 constexpr int kMf32MaxWaves = 8;                  // C <= 1024
 constexpr int kMf32Par = 32 * 32 + 2 * 32;
 
-template <typename XT, bool RAW>
+template <typename XT, bool RAW, bool FULL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_kernel(Mf32Args A) {
   extern __shared__ __align__(16) uint16_t mf32_lds[];
   __shared__ float s_red[2][2][kMf32MaxWaves];
@@ -269,40 +284,60 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   const int wave = tid >> 6;
   const int nwaves = blockDim.x >> 6;
   const int q = lane >> 4, r = lane & 15;
-  const int n = A.n, C = A.C;
+  const int n = FULL ? 32 : A.n;
+  const int C = A.C;
   const int64_t nC = (int64_t)n * C;
   uint16_t* xs = mf32_lds + (size_t)wave * kMf32Slab;
   uint16_t* gs = xs + 32 * kMf32Row;
   const int cb = wave * 128 + 8 * r;
 
-  // parameters: a, p of streams 8q+e (A operands of y, dyn); column 16J + r
-  // of M at rows 8q+e (A operand of M^T); a of the dx rows 16J + 4q + k
-  u32x4 aa[3], ap[3], amt[2][3];
-  float a4[2][4];
-  {
-    float av[8], pv[8];
+  // parameters, split once by wave 0 into LDS and read per token (registers
+  // are kept for the next token's loads): a, p of streams 8q+e (A operands
+  // of y, dyn), column 16J + r of M at rows 8q+e (the A operand of M^T, per
+  // lane) and a of the dx rows 16J + 4q + k
+  __shared__ u32x4 s_amt[2][3][64];
+  __shared__ float4 s_a4[2][4];
+  __shared__ u32x4 s_aa[3][4], s_ap[3][4];
+  if (wave == 0) {
+    if (r == 0) {
+      float av[8], pv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int i = 8 * q + e;
-      av[e] = i < n ? act_pre<RAW>(A.hpre[i]) : 0.0f;
-      pv[e] = i < n ? act_post<RAW>(A.hpost[i]) : 0.0f;
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * q + e;
+        av[e] = i < n ? act_pre<RAW>(A.hpre[i]) : 0.0f;
+        pv[e] = i < n ? act_post<RAW>(A.hpost[i]) : 0.0f;
+      }
+      u32x4 aa[3], ap[3];
+      split3x8<XT>(av, aa);
+      split3x8<XT>(pv, ap);
+#pragma unroll
+      for (int e = 0; e < 3; ++e) {
+        s_aa[e][q] = aa[e];
+        s_ap[e][q] = ap[e];
+      }
     }
-    split3x8<XT>(av, aa);
-    split3x8<XT>(pv, ap);
 #pragma unroll
     for (int J = 0; J < 2; ++J) {
       const int col = 16 * J + r;
       float mv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) mv[e] = (col < n && 8 * q + e < n) ? A.M[(8 * q + e) * n + col] : 0.0f;
-      split3x8<XT>(mv, amt[J]);
+      u32x4 amt[3];
+      split3x8<XT>(mv, amt);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int j = 16 * J + 4 * q + k;
-        a4[J][k] = j < n ? act_pre<RAW>(A.hpre[j]) : 0.0f;
+      for (int e = 0; e < 3; ++e) s_amt[J][e][lane] = amt[e];
+      if (r == 0) {
+        float a4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int j = 16 * J + 4 * q + k;
+          a4[k] = j < n ? act_pre<RAW>(A.hpre[j]) : 0.0f;
+        }
+        s_a4[J][q] = make_float4(a4[0], a4[1], a4[2], a4[3]);
       }
     }
   }
+  __syncthreads();
   float wv[8];
   {
     const float4 w0 = *reinterpret_cast<const float4*>(A.w + cb);
@@ -319,24 +354,37 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 #pragma unroll
   for (int e = 0; e < 8; ++e) dA[e] = dP[e] = dwv[e] = 0.0f;
 
-  int it = 0;
-  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+  // The token's x and g rows are loaded one token ahead: the next token's
+  // loads are issued as soon as this token's registers are staged, so they
+  // are in flight during the dM, barrier and dx phases and go out before this
+  // token's dx stores (a wait for them then never waits for those stores).
+  Vec<XT, 8> xr[8], gr[8];
+  auto load_token = [&](int64_t t) {
     const XT* xt = (const XT*)A.x + t * nC;
     const XT* gt = (const XT*)A.g + t * nC;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (8 * q + e < n) {
+        xr[e].load(xt + (int64_t)(8 * q + e) * C + cb);
+        gr[e].load(gt + (int64_t)(8 * q + e) * C + cb);
+      } else {
+        xr[e].zero();
+        gr[e].zero();
+      }
+    }
+  };
+  // (n < 32: loads at the top of each token instead; the per-stream
+  // branches leave no registers for the next token's rows)
+  if constexpr (FULL) {
+    if ((int64_t)blockIdx.x < A.T) load_token(blockIdx.x);
+  }
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
     float y[8], dyn[8];
     float ss = 0.0f, sr = 0.0f;
+    if constexpr (!FULL) load_token(t);
     {
-      Vec<XT, 8> xr[8], gr[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (8 * q + e < n) {
-          xr[e].load(xt + (int64_t)(8 * q + e) * C + cb);
-          gr[e].load(gt + (int64_t)(8 * q + e) * C + cb);
-        } else {
-          xr[e].zero();
-          gr[e].zero();
-        }
-      }
       // stage the slab (one LDS row per stream; zero rows for streams >= n)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -345,18 +393,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
         *reinterpret_cast<u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]) =
             u32x4{gr[e].w[0], gr[e].w[1], gr[e].w[2], gr[e].w[3]};
       }
-      u32x4 bx[8], bg[8];
-      transpose8<XT>(xr, bx);
-      transpose8<XT>(gr, bg);
+      const u32x4 aa[3] = {s_aa[0][q], s_aa[1][q], s_aa[2][q]};
+      const u32x4 ap[3] = {s_ap[0][q], s_ap[1][q], s_ap[2][q]};
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
-        const f32x4 ay = mfma_split3<XT>(aa, bx[v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-        const f32x4 ad = mfma_split3<XT>(ap, bg[v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        const f32x4 ay = mfma_split3<XT>(aa, column8<XT>(xr, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        const f32x4 ad = mfma_split3<XT>(ap, column8<XT>(gr, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f});
         y[v] = ay[0];
         dyn[v] = ad[0];
         ss = fmaf(ay[0], ay[0], ss);
         sr = fmaf(ad[0] * ay[0], wv[v], sr);
       }
+      if constexpr (FULL) {
+        if (t + gridDim.x < A.T) load_token(t + gridDim.x);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     // dM over the slab: A = g rows 16I + r, B = x rows 16J + r, 32 channels per step
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -401,28 +452,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
       dwv[v] = fmaf(dyn[v], yi, dwv[v]);
     }
     XT* dxt = (XT*)A.out + t * nC;
+    __builtin_amdgcn_sched_barrier(0);
     {
       // g back from the slab: dx = M^T g + a dy, and dP
-      Vec<XT, 8> gr[8];
+      Vec<XT, 8> gr2[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const u32x4 u = *reinterpret_cast<const u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]);
-        gr[e].w[0] = u[0]; gr[e].w[1] = u[1]; gr[e].w[2] = u[2]; gr[e].w[3] = u[3];
+        gr2[e].w[0] = u[0]; gr2[e].w[1] = u[1]; gr2[e].w[2] = u[2]; gr2[e].w[3] = u[3];
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e)
 #pragma unroll
-        for (int v = 0; v < 8; ++v) dP[e] = fmaf(gr[e].get(v), ynv[v], dP[e]);
-      u32x4 bg[8];
-      transpose8<XT>(gr, bg);
+        for (int v = 0; v < 8; ++v) dP[e] = fmaf(gr2[e].get(v), ynv[v], dP[e]);
 #pragma unroll
       for (int J = 0; J < 2; ++J) {
+        const u32x4 amt[3] = {s_amt[J][0][lane], s_amt[J][1][lane], s_amt[J][2][lane]};
+        const float4 a4 = s_a4[J][q];
         uint32_t ow[4][4];
         f32x4 even;
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
-          f32x4 acc = {a4[J][0] * dyv[v], a4[J][1] * dyv[v], a4[J][2] * dyv[v], a4[J][3] * dyv[v]};
-          acc = mfma_split3<XT>(amt[J], bg[v], acc);
+          const u32x4 bg = column8<XT>(gr2, v);
+          f32x4 acc = {a4.x * dyv[v], a4.y * dyv[v], a4.z * dyv[v], a4.w * dyv[v]};
+          acc = mfma_split3<XT>(amt, bg, acc);
           if (v & 1) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) ow[k][v >> 1] = pack2<XT>(even[k], acc[k]);
@@ -438,6 +491,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
         }
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
     {
       // x back from the slab: dA
 #pragma unroll
@@ -514,7 +568,7 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
   const int spw = S <= 8 ? 1 : 2;
   if (S % spw != 0) return 1;
   const int waves = S / spw;
-  const bool pt = A.M_ts != 0, raw = A.h_mode == MHC_H_RAW;
+  const bool pt = A.M_ts != 0, raw = A.h_mode == MHC_H_RAW, full = A.n == 32;
   const int per_cu = knob(kKnobFwdGrid, 8);
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * std::max(per_cu, 1)));
   const dim3 g((unsigned)blocks), b(waves * 64);
@@ -522,7 +576,11 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
     using XT = std::remove_pointer_t<decltype(xp)>;
     auto go = [&](auto* op) {
       using OT = std::remove_pointer_t<decltype(op)>;
-#define MF32_FWD(SPW_, PT_, RAW_) hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, PT_, RAW_>), g, b, 0, s, A)
+#define MF32_FWD(SPW_, PT_, RAW_)                                                                 \
+  do {                                                                                             \
+    if (full) hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, PT_, RAW_, true>), g, b, 0, s, A);  \
+    else hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, PT_, RAW_, false>), g, b, 0, s, A);      \
+  } while (0)
       if (spw == 1) {
         if (pt) { if (raw) MF32_FWD(1, true, true); else MF32_FWD(1, true, false); }
         else { if (raw) MF32_FWD(1, false, true); else MF32_FWD(1, false, false); }
@@ -551,7 +609,9 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   const bool raw = A.h_mode == MHC_H_RAW;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
-    const void* kfn = raw ? (const void*)mf32_bwd_kernel<XT, true> : (const void*)mf32_bwd_kernel<XT, false>;
+    const bool full = A.n == 32;
+    const void* kfn = full ? (raw ? (const void*)mf32_bwd_kernel<XT, true, true> : (const void*)mf32_bwd_kernel<XT, false, true>)
+                           : (raw ? (const void*)mf32_bwd_kernel<XT, true, false> : (const void*)mf32_bwd_kernel<XT, false, false>);
     const int occ = occupancy_blocks(kfn, waves * 64, smem);
     if (occ <= 0) return 1;
     int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
@@ -559,8 +619,13 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     if (grid_pref > 0) blocks = std::min<int64_t>(gmax, grid_pref);
     blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
     const dim3 g((unsigned)blocks), b(waves * 64);
-    if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true>), g, b, smem, s, A);
-    else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false>), g, b, smem, s, A);
+    if (full) {
+      if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true, true>), g, b, smem, s, A);
+      else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false, true>), g, b, smem, s, A);
+    } else {
+      if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true, false>), g, b, smem, s, A);
+      else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false, false>), g, b, smem, s, A);
+    }
     MHC_CHECK_LAUNCH("mf32_bwd_kernel");
     *num_partials = blocks;
     return MHC_OK;
