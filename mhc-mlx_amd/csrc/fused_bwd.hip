@@ -563,10 +563,21 @@ MHC_DEV void reg_fence(uint32_t& w) { asm volatile("" : "+v"(w)); }
 // the same wave + LDS reduction at the end of each token to the per-token
 // outputs (dA and dP through the activation chain when RAW); only dw stays
 // in registers across tokens.
-template <int NMAX, typename XT, typename GT, int CHK, bool FULL, bool PT = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(64, lw_max_threads(NMAX)),
-                          amdgpu_waves_per_eu(NMAX <= 4 ? MHC_BWD_WPE : 2)))
+//
+// PIPE (layer-wide full tiles, n == 4): the next token's x and g are loaded
+// right after this token's phase A, into a second set of registers, so they
+// are in flight across the barrier and phase B and are issued before this
+// token's dx stores.  On gfx9 a vmcnt wait counts stores as well: loads
+// issued after the stores would make the next token's first wait also wait
+// for this token's stores.  The second register set (32 VGPRs) bounds the
+// workgroup at 512 threads and three waves per SIMD, i.e. one workgroup per
+// CU, which the overlap more than pays for (config 2: 565 -> 559 us at one
+// workgroup per CU against two).
+template <int NMAX, typename XT, typename GT, int CHK, bool FULL, bool PT = false, bool PIPE = false>
+__global__ __attribute__((amdgpu_flat_work_group_size(64, PIPE ? 512 : lw_max_threads(NMAX)),
+                          amdgpu_waves_per_eu(PIPE ? 3 : (NMAX <= 4 ? MHC_BWD_WPE : 2))))
 void fused_bwd_lw_kernel(BwdArgs A) {
+  static_assert(!PIPE || (FULL && !PT), "pipelined loads for layer-wide full tiles only");
   constexpr int V = lw_vec<NMAX, XT, GT>();
   constexpr int K = NMAX * NMAX + 2 * NMAX;
   constexpr bool DOT = std::is_same<XT, GT>::value && ElemTraits<XT>::kBytes == 2;
@@ -625,30 +636,37 @@ void fused_bwd_lw_kernel(BwdArgs A) {
 #pragma unroll
   for (int k = 0; k < NMAX; ++k) accA[k] = accP[k] = 0.0f;
 
-  int it = 0;
-  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+  auto load_tok = [&](Vec<XT, V> (&xa)[CHK][NMAX], Vec<GT, V> (&ga)[CHK][NMAX], int64_t t) {
     const XT* xt = X + t * nC;
     const GT* gt = Gr + t * nC;
-    XT* dxt = DX + t * nC;
-    Vec<XT, V> xr[CHK][NMAX];
-    Vec<GT, V> gr[CHK][NMAX];
-    if constexpr (PT) load_params(A.M + t * A.M_ts, A.hpre + t * A.h_ts, A.hpost + t * A.h_ts);
 #pragma unroll
     for (int k = 0; k < CHK; ++k) {
 #pragma unroll
       for (int i = 0; i < NMAX; ++i) {
         if (FULL || (i < n && valid[k] == V && A.vec)) {
-          xr[k][i].load(xt + (int64_t)i * C + c0[k]);
-          gr[k][i].load(gt + (int64_t)i * C + c0[k]);
+          xa[k][i].load(xt + (int64_t)i * C + c0[k]);
+          ga[k][i].load(gt + (int64_t)i * C + c0[k]);
         } else if (i < n && valid[k] > 0) {
-          xr[k][i].load_partial(xt + (int64_t)i * C + c0[k], valid[k]);
-          gr[k][i].load_partial(gt + (int64_t)i * C + c0[k], valid[k]);
+          xa[k][i].load_partial(xt + (int64_t)i * C + c0[k], valid[k]);
+          ga[k][i].load_partial(gt + (int64_t)i * C + c0[k], valid[k]);
         } else {
-          xr[k][i].zero();
-          gr[k][i].zero();
+          xa[k][i].zero();
+          ga[k][i].zero();
         }
       }
     }
+  };
+  Vec<XT, V> xr[CHK][NMAX];
+  Vec<GT, V> gr[CHK][NMAX];
+  if constexpr (PIPE) {
+    if ((int64_t)blockIdx.x < A.T) load_tok(xr, gr, blockIdx.x);
+  }
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    XT* dxt = DX + t * nC;
+    if constexpr (PT) load_params(A.M + t * A.M_ts, A.hpre + t * A.h_ts, A.hpost + t * A.h_ts);
+    if constexpr (!PIPE) load_tok(xr, gr, t);
     // ---- phase A: y, dyn and the per-token sums  sum y^2, sum dyn*y*w
     float y[CHK][V], dyn[CHK][V];
     float ss = 0.0f, sr = 0.0f;
@@ -673,6 +691,11 @@ void fused_bwd_lw_kernel(BwdArgs A) {
     if (lane == 0) {
       s_red[it & 1][0][wave] = ss;
       s_red[it & 1][1][wave] = sr;
+    }
+    Vec<XT, V> xn[CHK][NMAX];
+    Vec<GT, V> gn[CHK][NMAX];
+    if constexpr (PIPE) {
+      if (t + gridDim.x < A.T) load_tok(xn, gn, t + gridDim.x);
     }
     lds_barrier();
     float tss = 0.0f, tsr = 0.0f;
@@ -787,6 +810,15 @@ void fused_bwd_lw_kernel(BwdArgs A) {
           }
         }
       }
+    }
+    if constexpr (PIPE) {
+#pragma unroll
+      for (int k = 0; k < CHK; ++k)
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          xr[k][i] = xn[k][i];
+          gr[k][i] = gn[k][i];
+        }
     }
   }
 
@@ -1066,7 +1098,12 @@ constexpr int kMf16MaxWaves = 8;
 // reduction applies the activation chain to the totals).
 // WIDE: two slabs per wave with up to 8 waves, C up to 2048 (one workgroup
 // per CU: its staged slabs take ~140 KB of LDS).
-template <typename XT, int SPW, bool RAW, bool LW, bool WIDE = false>
+// PIPE: the next token's x and g are loaded once this token's slabs are
+// staged (the registers are free then), so the loads are in flight across
+// the RMS barrier and the dx pass, and are issued before this token's dx
+// stores (a vmcnt wait counts stores too: loads issued after them would
+// wait for them).
+template <typename XT, int SPW, bool RAW, bool LW, bool WIDE = false, bool PIPE = false>
 __global__ __launch_bounds__(SPW == 2 && !WIDE ? 256 : 512) __attribute__((amdgpu_waves_per_eu(2)))
 void fused_bwd_mfma16_kernel(BwdArgs A) {
   constexpr int N = 16;
@@ -1116,26 +1153,32 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
     const float* M0 = A.M + t0 * MS + (4 * q) * 16 + r;
     nm = make_float4(M0[0], M0[16], M0[32], M0[48]);
   }
+  Vec<XT, 8> xr[SPW][4], gr[SPW][4];
+  auto load_tok = [&](int64_t t) {
+    const XT* xt = (const XT*)A.x + t * nC;
+    const XT* gt = (const XT*)A.g + t * nC;
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        xr[s][k].load(xt + (int64_t)(4 * q + k) * C + cb[s]);
+        gr[s][k].load(gt + (int64_t)(4 * q + k) * C + cb[s]);
+      }
+  };
+  if constexpr (PIPE) {
+    if ((int64_t)blockIdx.x < A.T) load_tok(blockIdx.x);
+  }
   __syncthreads();
 
   int it = 0;
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
-    const XT* xt = (const XT*)A.x + t * nC;
-    const XT* gt = (const XT*)A.g + t * nC;
     const float4 h4 = nh, g4 = ng, m4 = nm;
     float y[SPW][8], dyn[SPW][8];
     float ss = 0.0f, sr = 0.0f;
     f32x4 dm = {0.0f, 0.0f, 0.0f, 0.0f};
     float av[4];
     {
-      Vec<XT, 8> xr[SPW][4], gr[SPW][4];
-#pragma unroll
-      for (int s = 0; s < SPW; ++s)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          xr[s][k].load(xt + (int64_t)(4 * q + k) * C + cb[s]);
-          gr[s][k].load(gt + (int64_t)(4 * q + k) * C + cb[s]);
-        }
+      if constexpr (!PIPE) load_tok(t);
       {
         const int64_t tn = t + gridDim.x;
         if (tn < A.T) {
@@ -1212,6 +1255,9 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
           dm = mfma16<XT>(a, b, dm);
         }
       }
+    }
+    if constexpr (PIPE) {
+      if (t + gridDim.x < A.T) load_tok(t + gridDim.x);
     }
     // the four lanes of a column hold the same y and dyn: count them once
     ss = q == 0 ? ss : 0.0f;
@@ -1556,12 +1602,25 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
   // Grid: the workspace's full row budget (8 workgroups per CU) streams
   // faster than one resident wave of workgroups (562 vs 576 us at config 2);
   // MHC_BWD_GRID overrides the count.
-  int64_t blocks = L.gmax;
+  // The pipelined variant (n == 4 full tiles up to 512 threads, MHC_BWD_PIPE
+  // != 0) holds one workgroup per CU; two per CU keep the CUs busy while
+  // one drains (config 2: 0.929 ms step at 512 workgroups vs 0.955 at the
+  // non-pipelined default).
+  const bool pipe = NMAX == 4 && !PT && full && tpb <= 512 && knob(kKnobBwdPipe, 1) != 0;
+  int64_t blocks = pipe ? std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * 2) : L.gmax;
   const int grid_pref = knob(kKnobBwdGrid, 0);
   if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
   set_rows(A, L);
   const dim3 g((unsigned)blocks), b(tpb);
+  if constexpr (NMAX == 4 && !PT) {
+    if (pipe) {
+      hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, true, false, true>), g, b, 0, stream, A);
+      MHC_CHECK_LAUNCH("fused_bwd_lw_kernel");
+      *num_partials = blocks;
+      return MHC_OK;
+    }
+  }
   if (full)
     hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, true, PT>), g, b, 0, stream, A);
   else
@@ -1571,19 +1630,17 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
   return MHC_OK;
 }
 
-// Per-token n == 16 with 16-bit x == dout and C a multiple of 256 up to 1024
-// (fused_bwd_pt16_kernel).  Returns 1 when the shape is not covered.
 // n == 16 on MFMA (fused_bwd_mfma16_kernel), per-token or (LW) layer-wide
 // parameters: 16-bit x == dout, C a multiple of 128 up to 1024, or up to
 // 2048 with two slabs per wave (two 128-channel slabs per wave when C / 128
 // is even, else one), 16-byte aligned operands.  Returns 1 when the shape is
 // not covered.
-template <typename XT, int SPW, bool LW, bool WIDE>
+template <typename XT, int SPW, bool LW, bool WIDE, bool PIPE>
 int launch_mf16_variant(BwdArgs A, const BwdLayout& L, int waves, int64_t* num_partials, hipStream_t stream) {
   const size_t smem = (size_t)waves * SPW * 2 * 16 * kMf16Row * sizeof(uint16_t);
   const bool raw = A.h_mode == MHC_H_RAW;
-  const void* kfn = raw ? (const void*)fused_bwd_mfma16_kernel<XT, SPW, true, LW, WIDE>
-                        : (const void*)fused_bwd_mfma16_kernel<XT, SPW, false, LW, WIDE>;
+  const void* kfn = raw ? (const void*)fused_bwd_mfma16_kernel<XT, SPW, true, LW, WIDE, PIPE>
+                        : (const void*)fused_bwd_mfma16_kernel<XT, SPW, false, LW, WIDE, PIPE>;
   const int occ = occupancy_blocks(kfn, waves * 64, smem);
   if (occ <= 0) return 1;
   int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
@@ -1592,11 +1649,24 @@ int launch_mf16_variant(BwdArgs A, const BwdLayout& L, int waves, int64_t* num_p
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
   set_rows(A, L);
   const dim3 g((unsigned)blocks), b(waves * 64);
-  if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, SPW, true, LW, WIDE>), g, b, smem, stream, A);
-  else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, SPW, false, LW, WIDE>), g, b, smem, stream, A);
+  if (raw) hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, SPW, true, LW, WIDE, PIPE>), g, b, smem, stream, A);
+  else hipLaunchKernelGGL((fused_bwd_mfma16_kernel<XT, SPW, false, LW, WIDE, PIPE>), g, b, smem, stream, A);
   MHC_CHECK_LAUNCH("fused_bwd_mfma16_kernel");
   *num_partials = blocks;
   return MHC_OK;
+}
+
+// Pipelined loads (MHC_BWD_PIPE, default on) hold the next token's x and g
+// (32 VGPRs per slab) through the dx pass; with two slabs per wave and the
+// layer-wide sums in registers that would spill, so that variant keeps its
+// loads at the top of the token.
+template <typename XT, int SPW, bool LW, bool WIDE>
+int launch_mf16_pick(BwdArgs A, const BwdLayout& L, int waves, int64_t* num_partials, hipStream_t stream) {
+  if constexpr (!(LW && SPW == 2)) {
+    if (knob(kKnobBwdPipe, 1) != 0)
+      return launch_mf16_variant<XT, SPW, LW, WIDE, true>(A, L, waves, num_partials, stream);
+  }
+  return launch_mf16_variant<XT, SPW, LW, WIDE, false>(A, L, waves, num_partials, stream);
 }
 
 template <typename XT, bool LW>
@@ -1614,12 +1684,15 @@ int launch_bwd_mfma16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipS
   const int waves = S / spw;
   if (spw == 1) {
     if (waves > kMf16MaxWaves) return 1;
-    return launch_mf16_variant<XT, 1, LW, false>(A, L, waves, num_partials, stream);
+    return launch_mf16_pick<XT, 1, LW, false>(A, L, waves, num_partials, stream);
   }
-  if (waves <= 4) return launch_mf16_variant<XT, 2, LW, false>(A, L, waves, num_partials, stream);
+  if (waves <= 4) return launch_mf16_pick<XT, 2, LW, false>(A, L, waves, num_partials, stream);
   if (waves > kMf16MaxWaves) return 1;
-  return launch_mf16_variant<XT, 2, LW, true>(A, L, waves, num_partials, stream);
+  return launch_mf16_pick<XT, 2, LW, true>(A, L, waves, num_partials, stream);
 }
+
+// Per-token n == 16 with 16-bit x == dout and C a multiple of 256 up to 1024
+// (fused_bwd_pt16_kernel).  Returns 1 when the shape is not covered.
 
 template <typename XT>
 int launch_bwd_pt16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {

@@ -196,6 +196,37 @@ def test_per_token_backward_with_many_tokens_per_workgroup(B, n, C, xdt, gdt, le
         assert rel_err(np_of(got), r) < tol, (name, rel_err(np_of(got), r))
 
 
+@pytest.mark.parametrize("B,n,C,xdt,per_token,spw", [
+    (64, 4, 4096, "bf16", False, None), (5, 4, 4096, "bf16", False, None), (1, 4, 2048, "f16", False, None),
+    (37, 16, 1024, "bf16", True, None), (37, 16, 1024, "bf16", True, 1), (9, 16, 2048, "f16", True, None),
+    (21, 16, 512, "bf16", False, 1), (21, 16, 512, "f16", False, None)])
+@pytest.mark.parametrize("grid", [3, 100])
+def test_pipelined_loads_match_unpipelined(B, n, C, xdt, per_token, spw, grid, knobs):
+    """MHC_BWD_PIPE = 1 (the next token's x and dout loaded during this token's dx pass) against 0 at one
+    grid: the same sums in the same order, so every gradient is bitwise equal.  Grid 3 walks many tokens per
+    workgroup; grid 100 leaves workgroups without a token when B < 100."""
+    knobs("MHC_BWD_GRID", grid)
+    if spw is not None:
+        knobs("MHC_BWD_SPW", spw)
+    x, dout, hpre, hpost, hres, w = _bwd_case(B, n, C, xdt, xdt, 2100 + B + n + C, per_token=per_token)
+    runs = []
+    for pipe in (1, 0):
+        knobs("MHC_BWD_PIPE", pipe)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        xt = dev_tensor(x, xdt).requires_grad_(True)
+        fwd = ops.mhc_layer_forward_dynamic if per_token else ops.mhc_layer_forward
+        out = fwd(xt, *ps, sinkhorn_iters=20, eps=1e-5, output_dtype=xt.dtype)
+        out.backward(dev_tensor(dout, xdt))
+        runs.append([xt.grad.clone()] + [t.grad.clone() for t in ps])
+    for name, a, b in zip(["dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], *runs):
+        assert torch.equal(a, b), name
+    if B * n * C <= 64 * 16 * 1024:
+        ref = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=1e-5)
+        for name, got, r in zip(["dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], runs[0], ref):
+            tol = _grad_tol(xdt) if name == "dx" else 1e-4
+            assert rel_err(np_of(got), r) < tol, (name, rel_err(np_of(got), r))
+
+
 def test_backward_is_deterministic():
     B, n, C = 64, 4, 1024
     x, dout, hpre, hpost, hres, w = _bwd_case(B, n, C, "bf16", "bf16", 77)
