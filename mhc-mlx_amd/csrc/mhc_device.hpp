@@ -326,6 +326,8 @@ MHC_DEV void wave_reduce_scatter(float (&v)[64 * R], int lane) {
 // expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]; vmcnt and expcnt left
 // at their maximum).
 constexpr int kWaitLgkm0 = 0xC07F;
+// s_waitcnt immediate for vmcnt(0) alone.
+constexpr int kWaitVm0 = 0x0F70;
 
 // Workgroup barrier for data exchanged through LDS only.  __syncthreads()
 // is a workgroup-scope release/acquire fence and waits for every

@@ -12,6 +12,7 @@
 #include "mhc_device.hpp"
 #include "mhc_generic.hpp"
 #include "mhc_host.hpp"
+#include "mhc_mix32.hpp"
 #include "mhc_plan.hpp"
 #include "mhc_reduce.hpp"
 
@@ -435,7 +436,10 @@ MHC_DEV void col_sums4(const float* __restrict__ part2, int S, int P, int c0, in
   for (int e = 0; e < 4; ++e) v[e] = wave_sum(v[e]);
 }
 
-// Final: sum S partial rows, then dM / dh_pre / dh_post (one block).
+// Final: sum S partial rows, then dM / dh_pre / dh_post (one block).  One
+// thread per column adds the S rows in row order (coalesced across the
+// threads); M and the activated a, p are staged in LDS first, so the n-long
+// dot products below read LDS only.
 __global__ __launch_bounds__(256) void mix_final_kernel(const float* __restrict__ part2, int S,
                                                         int P, int n, int h_mode,
                                                         const float* __restrict__ M,
@@ -444,47 +448,55 @@ __global__ __launch_bounds__(256) void mix_final_kernel(const float* __restrict_
                                                         float* __restrict__ dM,
                                                         float* __restrict__ dpre,
                                                         float* __restrict__ dpost) {
-  extern __shared__ float s_sum[];  // [n*n + n]: S then Yd
+  extern __shared__ float s_sum[];  // [n*n + n]: S then Yd; then M [n*n], a [n], p [n]
   const int K = n * n + n;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-  for (int c0 = 4 * wave; c0 < K; c0 += 4 * nwaves) {
-    float v[4];
-    col_sums4(part2, S, P, c0, K, lane, v);
-    if (lane == 0)
-      for (int e = 0; e < 4 && c0 + e < K; ++e) s_sum[c0 + e] = v[e];
+  float* s_M = s_sum + K;
+  float* s_a = s_M + n * n;
+  float* s_p = s_a + n;
+  for (int c = threadIdx.x; c < K; c += blockDim.x) {
+    const float* src = part2 + c;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int r = 0; r < S; ++r) acc += src[(int64_t)r * P];
+    s_sum[c] = acc;
+  }
+  for (int k = threadIdx.x; k < n * n; k += blockDim.x) s_M[k] = M[k];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    float a = 1.0f, p = 1.0f;
+    if (h_mode == MHC_H_RAW) {
+      a = sigmoidf_(hpre[i]);
+      p = 2.0f * sigmoidf_(hpost[i]);
+    } else if (h_mode == MHC_H_ACTIVATED) {
+      a = hpre[i];
+      p = hpost[i];
+    }
+    s_a[i] = a;
+    s_p[i] = p;
   }
   __syncthreads();
-  auto a_of = [&](int j) {
-    if (h_mode == MHC_H_NONE) return 1.0f;
-    return h_mode == MHC_H_RAW ? sigmoidf_(hpre[j]) : hpre[j];
-  };
-  auto p_of = [&](int i) {
-    if (h_mode == MHC_H_NONE) return 1.0f;
-    return h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(hpost[i]) : hpost[i];
-  };
   for (int k = threadIdx.x; k < n * n; k += blockDim.x) {
     const int i = k / n, j = k % n;
-    dM[k] = h_mode == MHC_H_NONE ? s_sum[k] : p_of(i) * s_sum[k] * a_of(j);
+    dM[k] = h_mode == MHC_H_NONE ? s_sum[k] : s_p[i] * s_sum[k] * s_a[j];
   }
   if (h_mode == MHC_H_NONE) return;
   for (int j = threadIdx.x; j < n; j += blockDim.x) {
-    float s = 0.0f;
-    for (int i = 0; i < n; ++i) s = fmaf(p_of(i) * M[i * n + j], s_sum[i * n + j], s);
+    float acc = 0.0f;
+    for (int i = 0; i < n; ++i) acc = fmaf(s_p[i] * s_M[i * n + j], s_sum[i * n + j], acc);
     if (h_mode == MHC_H_RAW) {
-      const float a = sigmoidf_(hpre[j]);
-      s *= a * (1.0f - a);
+      const float a = s_a[j];
+      acc *= a * (1.0f - a);
     }
-    dpre[j] = s;
+    dpre[j] = acc;
   }
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    float s = 0.0f;
-    for (int j = 0; j < n; ++j) s = fmaf(M[i * n + j] * a_of(j), s_sum[i * n + j], s);
-    s += s_sum[n * n + i];
+    float acc = 0.0f;
+    for (int j = 0; j < n; ++j) acc = fmaf(s_M[i * n + j] * s_a[j], s_sum[i * n + j], acc);
+    acc += s_sum[n * n + i];
     if (h_mode == MHC_H_RAW) {
-      const float sg = sigmoidf_(hpost[i]);
-      s *= 2.0f * sg * (1.0f - sg);
+      const float sg = 0.5f * s_p[i];
+      acc *= 2.0f * sg * (1.0f - sg);
     }
-    dpost[i] = s;
+    dpost[i] = acc;
   }
 }
 
@@ -760,6 +772,11 @@ extern "C" int mhc_stream_mix_add_fwd(const void* x, int x_dtype, const void* y,
   hipStream_t s = (hipStream_t)stream;
   const int ydt = y ? y_dtype : x_dtype;
   if (nmax_for(n) == 0) {
+    Mix32Args F{};
+    F.x = x; F.y = y; F.out = out; F.M = M; F.hpre = h_pre; F.hpost = h_post; F.T = T; F.n = n; F.C = C;
+    F.h_mode = h_mode;
+    const int rc = mix32_fwd(F, x_dtype, ydt, out_dtype, s);
+    if (rc != 1) return rc;
     GenArgs G{};
     G.x = x; G.y = y; G.out = out; G.M = M; G.hpre = h_pre; G.hpost = h_post; G.T = T; G.n = n;
     G.C = C; G.h_mode = h_mode;
@@ -829,12 +846,20 @@ extern "C" int mhc_stream_mix_add_bwd(const void* x, int x_dtype, const void* y,
                            {dout, dtype_bytes(dout_dtype)}, {dy, dtype_bytes(ydt)}});
   hipStream_t s = (hipStream_t)stream;
   int rc;
+  int64_t rows = G;  // partial rows written (the MFMA kernel may write fewer)
   if (nmax_for(n) == 0) {
-    GenArgs Gg{};
-    Gg.x = x; Gg.y = y; Gg.g = dout; Gg.out = dx; Gg.dy = dy; Gg.M = M; Gg.hpre = h_pre;
-    Gg.hpost = h_post; Gg.part = (float*)workspace; Gg.T = T; Gg.n = n; Gg.C = C; Gg.P = P;
-    Gg.h_mode = h_mode;
-    rc = gen_mix_bwd(Gg, x_dtype, ydt, dout_dtype, s, G);
+    Mix32Args F{};
+    F.x = x; F.y = y; F.g = dout; F.out = dx; F.dy = dy; F.M = M; F.hpre = h_pre; F.hpost = h_post;
+    F.part = (float*)workspace; F.T = T; F.n = n; F.C = C; F.h_mode = h_mode; F.P = P;
+    rc = mix32_bwd(F, x_dtype, ydt, dout_dtype, G, s, &rows);
+    if (rc == 1) {
+      GenArgs Gg{};
+      Gg.x = x; Gg.y = y; Gg.g = dout; Gg.out = dx; Gg.dy = dy; Gg.M = M; Gg.hpre = h_pre;
+      Gg.hpost = h_post; Gg.part = (float*)workspace; Gg.T = T; Gg.n = n; Gg.C = C; Gg.P = P;
+      Gg.h_mode = h_mode;
+      rows = G;
+      rc = gen_mix_bwd(Gg, x_dtype, ydt, dout_dtype, s, G);
+    }
   } else rc = by_nmax(n, [&](auto nm) {
     constexpr int NM = decltype(nm)::value;
     return by_dtype(x_dtype, [&](auto* xp) {
@@ -861,13 +886,15 @@ extern "C" int mhc_stream_mix_add_bwd(const void* x, int x_dtype, const void* y,
   });
   if (rc != MHC_OK) return rc;
   float* part2 = (float*)workspace + (size_t)G * P;
-  const int S = (int)std::min<int64_t>(kMixSplit, G);
-  const int rows = (int)ceil_div(G, S);
-  const int S_used = (int)ceil_div(G, rows);
+  // about 64 rows per split: the split sums run in parallel workgroups, and
+  // mix_final_kernel (one workgroup) then adds few rows per column
+  const int S = (int)std::min<int64_t>(kMixSplit, ceil_div(rows, 64));
+  const int per = (int)ceil_div(rows, S);
+  const int S_used = (int)ceil_div(rows, per);
   hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)ceil_div(P / 4, 256), (unsigned)S_used),
-                     dim3(256), 0, s, (const float*)workspace, part2, G, P, rows);
+                     dim3(256), 0, s, (const float*)workspace, part2, rows, P, per);
   MHC_CHECK_LAUNCH("reduce_rows_kernel");
-  hipLaunchKernelGGL(mix_final_kernel, dim3(1), dim3(256), (size_t)(n * n + n) * sizeof(float), s,
+  hipLaunchKernelGGL(mix_final_kernel, dim3(1), dim3(256), (size_t)(2 * n * n + 3 * n) * sizeof(float), s,
                      part2, S_used, P, n, h_mode, M, h_pre, h_post, dM, dh_pre, dh_post);
   MHC_CHECK_LAUNCH("mix_final_kernel");
   return MHC_OK;

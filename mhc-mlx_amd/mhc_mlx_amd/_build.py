@@ -23,7 +23,7 @@ LIB_PATH = PKG_DIR / LIB_NAME
 OFFLOAD_ARCH = os.environ.get("MHC_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["capi.hip", "sinkhorn.hip", "fused_fwd.hip", "fused_bwd.hip", "stream_mix.hip", "generic.hip", "residual.hip",
-           "mfma32.hip", "noalloc.hip"]
+           "mfma32.hip", "mix32.hip", "noalloc.hip"]
 
 # Packed-FP32 VALU forms are disabled for every device pass (hipcc only; the
 # host pass prints a harmless "not a recognized feature" warning).

@@ -95,7 +95,68 @@ def test_rewire_kernels_walk_several_items_per_thread(gdt, knobs):
     assert rel_err(np_of(ht.grad), np.einsum("bic,bic->i", d16, x) * a * (1 - a)) < 1e-4
 
 
-@pytest.mark.parametrize("n,C", [(4, 64), (16, 16), (32, 8), (3, 9)])
+def _post_combine_run(x, y, dout, hpre, hpost, hres, xdt, gdt, odt):
+    xt = dev_tensor(x, xdt).requires_grad_(True)
+    yt = dev_tensor(y, xdt).requires_grad_(True)
+    ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres)]
+    out = ops.post_combine(xt, yt, *ps, sinkhorn_iters=20, eps=1e-5,
+                           output_dtype=None if odt == "f32" else xt.dtype)
+    out.backward(dev_tensor(dout, gdt).to(out.dtype))
+    return [out.detach().clone(), xt.grad.clone(), yt.grad.clone()] + [t.grad.clone() for t in ps]
+
+
+@pytest.mark.parametrize("B,n,C", [(5, 32, 128), (3, 24, 64), (2, 17, 192), (4, 32, 1024)])
+@pytest.mark.parametrize("xdt,gdt,odt", [("bf16", "f32", "f32"), ("bf16", "bf16", "bf16"), ("f16", "f32", "f32"),
+                                         ("f32", "f32", "f32")])
+def test_post_combine_mfma_above_16_streams(B, n, C, xdt, gdt, odt, knobs):
+    """16 < n <= 32 with C a multiple of 64 runs on the fp32 matrix cores (mix32.hip): forward and every
+    gradient against the float64 oracle, per element for the 16-bit outputs (one rounding of the fp32
+    result), and against the generic kernels (MHC_MIX32 = 0) to fp32 rounding."""
+    g = rng(600 + B + n + C)
+    x = to_dtype_np(g.standard_normal((B, n, C)), xdt)
+    y = to_dtype_np(g.standard_normal((B, n, C)), xdt)
+    dout = to_dtype_np(g.standard_normal((B, n, C)), gdt if odt == "f32" else odt)
+    hpre, hpost, hres, _ = params(g, n, C)
+    got = _post_combine_run(x, y, dout, hpre, hpost, hres, xdt, gdt, odt)
+    ref_out = O.post_combine(x, y, hpre, hpost, hres, 20, 1e-5)
+    refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    names = ["out", "dx", "dy", "dH_pre", "dH_post", "dH_res"]
+    for name, t, r in zip(names, got, [ref_out] + list(refs)):
+        v = np_of(t)
+        if name in ("out", "dx", "dy") and t.dtype != torch.float32:
+            ulp = 2.0 ** -8 if t.dtype == torch.bfloat16 else 2.0 ** -11
+            assert (np.abs(v - r) <= ulp * np.abs(r) + 1e-5 * np.abs(r).max()).all(), name
+        else:
+            assert rel_err(v, r) < (1e-5 if name in ("out", "dx", "dy") else 1e-4), (name, rel_err(v, r))
+    knobs("MHC_MIX32", 0)
+    gen = _post_combine_run(x, y, dout, hpre, hpost, hres, xdt, gdt, odt)
+    for name, a, b in zip(names, got, gen):
+        assert rel_err(np_of(a), np_of(b)) < (1e-2 if a.dtype != torch.float32 else 1e-5), name
+
+
+@pytest.mark.parametrize("gdt", ["bf16", "f32"])
+def test_post_combine_mfma_walks_several_items_per_wave(gdt, knobs):
+    """One workgroup per CU for the n = 32 MFMA post-combine: each wave walks several (token, slab) items,
+    so the backward's S / Yd sums run across items; a second run is bitwise identical."""
+    knobs("MHC_MIX_FWD_GRID", 1)
+    knobs("MHC_MIX_BWD_GRID", 1)
+    B, n, C = 3000, 32, 128
+    g = rng(49)
+    x = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    y = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    dout = to_dtype_np(g.standard_normal((B, n, C)), gdt)
+    hpre, hpost, hres, _ = params(g, n, C)
+    runs = [_post_combine_run(x, y, dout, hpre, hpost, hres, "bf16", gdt, "f32") for _ in range(2)]
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    assert rel_err(np_of(runs[0][0]), O.post_combine(x, y, hpre, hpost, hres, 20, 1e-5)) < 1e-5
+    for name, t, r in zip(["dx", "dy", "dH_pre", "dH_post", "dH_res"], runs[0][1:], refs):
+        tol = 1e-2 if name in ("dx", "dy") else 1e-4
+        assert rel_err(np_of(t), r) < tol, (name, rel_err(np_of(t), r))
+
+
+@pytest.mark.parametrize("n,C", [(4, 64), (16, 16), (32, 8), (3, 9), (32, 64), (20, 128)])
 def test_stream_mix_add_matches_reference_semantics(n, C):
     """stream_mix_add_metal: out = M x + y_dist (fp32); VJP dx = M^T g, dM = sum g x^T, dy = g."""
     B = 3
@@ -130,7 +191,7 @@ def test_stream_scale_matches_oracle(n, C):
     assert rel_err(np_of(ht.grad), ref_dh) < 1e-5
 
 
-@pytest.mark.parametrize("dims,n,T", [(64, 4, 3), (256, 16, 2), (512, 32, 2), (4096, 4, 16)])
+@pytest.mark.parametrize("dims,n,T", [(64, 4, 3), (256, 16, 2), (512, 32, 2), (4096, 4, 16), (4096, 32, 8)])
 def test_rewire_linear_matches_oracle(dims, n, T):
     g = rng(dims + n)
     torch.manual_seed(dims)
