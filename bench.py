@@ -13,7 +13,11 @@ Timed regions (all on the stream the library launches on):
 Extras: forward latency at B=32, C=2048 (config 1) and B=1, C=4096 (eager
 calls); config 3 (per-token H, n=16) fwd+bwd; config 4
 (MHCRewire around Linear(4096, 4096)) with mHC kernel time reported apart
-from the GEMM; residual_add_agg at config 2's shape.  cpu_baseline: the
+from the GEMM; residual_add_agg at config 2's shape; n=32 training steps
+(MHCLayer at 8192 x 32 x 512, MHCRewire(Linear(4096, 4096)) at n=32); the
+reference's own benchmark scenarios (scripts/record_benchmarks.py: n=32
+forward latency at B=1 and throughput at B=32, MHCLayer and MHCRewire) with
+its published Apple-silicon figures beside them.  cpu_baseline: the
 package's torch restatement of reference.py (MHCLayer(use_metal=False), the
 analogue of the reference's MHC_MLX_DISABLE_METAL=1 path) fwd+bwd on CPU
 tensors over a bounded token sample of config 2, on every host core this
@@ -183,6 +187,129 @@ def _config4(dev, steps, warmup):
             "gemm_and_other_ms_per_step": ms_t - mhc_ms}
 
 
+# The reference's own benchmark scenarios (scripts/record_benchmarks.py:12-23, 54-88): MHCLayer and MHCRewire
+# forward in inference mode at n=32, x of shape (B, 1, n*C) bf16; latency = median wall time of 50 synchronised
+# calls, throughput = mean of 50 unsynchronised calls.  Published figures (BENCHMARKS.csv:2-20, Apple silicon,
+# context only) are kept beside each row.
+_REF_SCENARIOS = [(1, 256, "latency"), (1, 512, "latency"), (1, 1024, "latency"), (1, 2048, "latency"),
+                  (1, 4096, "latency"), (32, 512, "throughput"), (32, 2048, "throughput"), (32, 4096, "throughput")]
+_REF_PUBLISHED_US = {  # (B, C, mode) -> (MHCLayer, MHCRewire) from BENCHMARKS.csv (latest rows)
+    (1, 256, "latency"): (513.25, 3171.46), (1, 512, "latency"): (445.21, 11771.79),
+    (1, 1024, "latency"): (436.62, 46445.42), (1, 2048, "latency"): (577.96, None),
+    (1, 4096, "latency"): (406.88, None), (32, 512, "throughput"): (117.73, 17480.19),
+    (32, 2048, "throughput"): (1529.09, None), (32, 4096, "throughput"): (2078.89, None)}
+
+
+def _wall_us(fn, mode, iters=50, warmup=10):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    if mode == "latency":
+        ts = []
+        for _ in range(iters):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts) * 1e6
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / iters * 1e6
+
+
+def _reference_scenarios(dev):
+    """The reference's BENCHMARKS.csv rows (n=32, forward, inference) on this GPU."""
+    import torch
+
+    from mhc_mlx_amd import MHCLayer, MHCRewire
+
+    rows = []
+    n = 32
+    for B, C, mode in _REF_SCENARIOS:
+        dims = n * C
+        torch.manual_seed(B * 7 + C)
+        x = torch.randn(B, 1, dims, device=dev, dtype=torch.bfloat16)
+        layer = MHCLayer(n=n, C=C, identity_init=False).to(dev).eval()
+        with torch.no_grad():
+            t_layer = _wall_us(lambda: layer(x.reshape(B, n, C)), mode)
+        ref_layer, ref_rewire = _REF_PUBLISHED_US[(B, C, mode)]
+        row = {"B": B, "n": n, "C": C, "mode": mode, "MHCLayer_us": round(t_layer, 2),
+               "reference_MHCLayer_us": ref_layer}
+        if C <= 1024:
+            lin = torch.nn.Linear(dims, dims, bias=False, device=dev, dtype=torch.bfloat16)
+            with torch.no_grad():
+                lin.weight.zero_()
+            rewire = MHCRewire(lin, dims=dims, n=n, identity_init=False).to(dev).eval()
+            with torch.no_grad():
+                row["MHCRewire_us"] = round(_wall_us(lambda: rewire(x), mode), 2)
+            row["reference_MHCRewire_us"] = ref_rewire
+            del lin, rewire
+        rows.append(row)
+        del layer, x
+        torch.cuda.empty_cache()
+    return {"source": "scripts/record_benchmarks.py scenarios; reference figures from BENCHMARKS.csv "
+                      "(Apple silicon, context only)", "rows": rows}
+
+
+def _n32_training(dev, steps=20, warmup=20):
+    """n=32 training steps: MHCLayer fwd+bwd at 8192 x 32 x 512 bf16 and MHCRewire(Linear(4096,4096)) at n=32."""
+    import numpy as np
+    import torch
+
+    from mhc_mlx_amd import MHCRewire, kernel_timer
+
+    T, n, C = 8192, 32, 512
+    layer = _layer(n, C, dev, np.random.default_rng(6))
+    gen = torch.Generator(dev).manual_seed(6)
+    x = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen).requires_grad_(True)
+    dout = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen)
+    params = [layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight]
+
+    def step():
+        out = layer(x, return_dtype=torch.bfloat16)
+        return torch.autograd.grad(out, [x] + params, dout)
+
+    for _ in range(warmup):
+        step()
+    ms = _time_loop(step, steps)
+    with kernel_timer() as kt:
+        _time_loop(step, steps)
+        st = kt.stats()
+    e = T * n * C * 2
+    layer_row = {"workload": "MHCLayer fwd+bwd, 8192 tokens, n=32, C=512, bf16 I/O", "ms_per_step": ms,
+                 "tokens_per_s": T / (ms / 1e3), "step_hbm_frac": 5 * e / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+                 "kernels_us": {k: round(v["mean_ms"] * 1e3, 1) for k, v in st.items()}}
+    del x, dout, layer
+    torch.cuda.empty_cache()
+
+    dims = 4096
+    torch.manual_seed(7)
+    inner = torch.nn.Linear(dims, dims, bias=False).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        inner.weight.normal_(0.0, 0.02)
+    m = MHCRewire(inner, dims=dims, n=n, eps=EPS, identity_init=False).to(dev)
+    xr = torch.randn(T, dims, device=dev, dtype=torch.bfloat16).requires_grad_(True)
+    g = torch.randn(T, dims, device=dev, dtype=torch.float32)
+    prm = [xr, inner.weight, m.mhc.H_pre_raw, m.mhc.H_post_raw, m.mhc.H_res_raw]
+
+    def rstep():
+        return torch.autograd.grad(m(xr), prm, g)
+
+    for _ in range(warmup):
+        rstep()
+    rms = _time_loop(rstep, steps)
+    with kernel_timer() as kt:
+        _time_loop(rstep, steps)
+        rst = kt.stats()
+    rewire_row = {"workload": "MHCRewire(Linear(4096,4096)), n=32 (C=128), 8192 tokens, bf16, fwd+bwd",
+                  "ms_per_step": rms, "mhc_kernels_us": {k: round(v["mean_ms"] * 1e3, 1) for k, v in rst.items()}}
+    return {"layer": layer_row, "rewire": rewire_row}
+
+
 def _residual(dev, steps, warmup):
     """residual_add_agg (utils.py:4-24) at config 2's shape: x, res [32768, 4, 4096] bf16 -> out bf16, y_agg fp32."""
     import torch
@@ -321,7 +448,8 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-latency", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip configs 3 and 4")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip configs 3 and 4, residual_add_agg, the n=32 rows and the reference scenarios")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain fp32 copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -404,6 +532,10 @@ def main() -> int:
         result["config4"] = _config4(dev, 20, 20)
         torch.cuda.empty_cache()
         result["residual_add_agg"] = _residual(dev, 10, 3)
+        torch.cuda.empty_cache()
+        result["n32"] = _n32_training(dev)
+        torch.cuda.empty_cache()
+        result["reference_scenarios"] = _reference_scenarios(dev)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(n, C)

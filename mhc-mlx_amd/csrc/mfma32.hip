@@ -147,7 +147,10 @@ MHC_DEV float act_post(float h) { return RAW ? 2.0f * sigmoid_fast(h) : h; }
 
 // FULL: n == 32, so no stream index is ever out of range (no per-stream
 // branches in the load, store and parameter code).
-template <typename XT, typename OT, int SPW, bool PT, bool RAW, bool FULL>
+// RELOAD (C above 2048: SPW = C / 1024 slabs per wave): the transposed
+// slabs do not stay in registers across the RMS barrier; the lane reads its
+// x again for the mix (from the caches: the token was read just before).
+template <typename XT, typename OT, int SPW, bool PT, bool RAW, bool FULL, bool RELOAD = false>
 __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
   __shared__ float s_red[2][16];
   const int tid = threadIdx.x;
@@ -194,8 +197,20 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
     const XT* xt = (const XT*)A.x + t * nC;
     OT* ot = (OT*)A.out + t * nC;
-    u32x4 bx[SPW][8];
-    {
+    // one slab of x (streams 8q .. 8q+7), transposed into the B operands
+    auto load_slab = [&](int s, u32x4 (&b)[8]) {
+      Vec<XT, 8> xr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (8 * q + e < n) xr[e].load(xt + (int64_t)(8 * q + e) * C + cb[s]);
+        else xr[e].zero();
+      }
+      transpose8<XT>(xr, b);
+    };
+    u32x4 bx[RELOAD ? 1 : SPW][8];
+    float y[SPW][8];
+    float ss = 0.0f;
+    if constexpr (!RELOAD) {
       Vec<XT, 8> xr[SPW][8];
 #pragma unroll
       for (int s = 0; s < SPW; ++s)
@@ -207,17 +222,19 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
       if constexpr (PT) load_params(t);
 #pragma unroll
       for (int s = 0; s < SPW; ++s) transpose8<XT>(xr[s], bx[s]);
+    } else {
+      if constexpr (PT) load_params(t);
     }
-    float y[SPW][8];
-    float ss = 0.0f;
 #pragma unroll
-    for (int s = 0; s < SPW; ++s)
+    for (int s = 0; s < SPW; ++s) {
+      if constexpr (RELOAD) load_slab(s, bx[0]);
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
-        const f32x4 acc = mfma_split3<XT>(aa, bx[s][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-        y[s][v] = acc[0];
+        const f32x4 acc = mfma_split3<XT>(aa, bx[RELOAD ? 0 : s][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        if constexpr (!RELOAD) y[s][v] = acc[0];
         ss = fmaf(acc[0], acc[0], ss);
       }
+    }
     // the four lane groups q hold the same y: count it once
     ss = q == 0 ? ss : 0.0f;
     ss = wave_sum(ss);
@@ -229,6 +246,13 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
     if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
+      // RELOAD: y of the slab recomputed from the reloaded x (the same MFMAs,
+      // so bitwise the value the sum of squares used)
+      if constexpr (RELOAD) {
+        load_slab(s, bx[0]);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) y[s][v] = mfma_split3<XT>(aa, bx[0][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f})[0];
+      }
       const float4 w0 = *reinterpret_cast<const float4*>(A.w + cb[s]);
       const float4 w1 = *reinterpret_cast<const float4*>(A.w + cb[s] + 4);
       const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -242,7 +266,7 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
         f32x4 even;
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
-          f32x4 acc = mfma_split3<XT>(am[I], bx[s][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+          f32x4 acc = mfma_split3<XT>(am[I], bx[RELOAD ? 0 : s][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
           for (int k = 0; k < 4; ++k) acc[k] = fmaf(yn[v], pv[I][k], acc[k]);
           if (v & 1) rows.put(v >> 1, even, acc);
@@ -560,15 +584,19 @@ int by_half(int code, F&& f) {
 }  // namespace
 
 int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
-  if (A.n <= 16 || A.n > 32 || A.C % 128 != 0 || A.C > 2048) return 1;
+  if (A.n <= 16 || A.n > 32 || A.C % 128 != 0 || A.C > 4096) return 1;
   if (od != MHC_DTYPE_F32 && od != xd) return 1;
   if (!aligned(A.x, 16) || !aligned(A.out, 16) || !aligned(A.w, 16)) return 1;
   if (knob(kKnobFwdMfma, 1) == 0) return 1;
   const int S = A.C / 128;
-  const int spw = S <= 8 ? 1 : 2;
+  // two slabs per wave up to C = 2048 (in registers across the RMS barrier),
+  // four above it (read again after the barrier)
+  // (n == 32 only: with per-stream conditions the four-slab variant spills)
+  const int spw = S <= 8 ? 1 : (S <= 16 ? 2 : 4);
   if (S % spw != 0) return 1;
   const int waves = S / spw;
   const bool pt = A.M_ts != 0, raw = A.h_mode == MHC_H_RAW, full = A.n == 32;
+  if (spw == 4 && !full) return 1;
   const int per_cu = knob(kKnobFwdGrid, 8);
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * std::max(per_cu, 1)));
   const dim3 g((unsigned)blocks), b(waves * 64);
@@ -581,14 +609,20 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
     if (full) hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, PT_, RAW_, true>), g, b, 0, s, A);  \
     else hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, PT_, RAW_, false>), g, b, 0, s, A);      \
   } while (0)
+#define MF32_FWD_RELOAD(PT_, RAW_) \
+  hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, 4, PT_, RAW_, true, true>), g, b, 0, s, A)
       if (spw == 1) {
         if (pt) { if (raw) MF32_FWD(1, true, true); else MF32_FWD(1, true, false); }
         else { if (raw) MF32_FWD(1, false, true); else MF32_FWD(1, false, false); }
-      } else {
+      } else if (spw == 2) {
         if (pt) { if (raw) MF32_FWD(2, true, true); else MF32_FWD(2, true, false); }
         else { if (raw) MF32_FWD(2, false, true); else MF32_FWD(2, false, false); }
+      } else {
+        if (pt) { if (raw) MF32_FWD_RELOAD(true, true); else MF32_FWD_RELOAD(true, false); }
+        else { if (raw) MF32_FWD_RELOAD(false, true); else MF32_FWD_RELOAD(false, false); }
       }
 #undef MF32_FWD
+#undef MF32_FWD_RELOAD
       MHC_CHECK_LAUNCH("mf32_fwd_kernel");
       return MHC_OK;
     };

@@ -30,7 +30,10 @@ def _ulp_bound(got, ref, dt):
 
 
 @pytest.mark.parametrize("T,n,C", [(5, 32, 128), (40, 32, 512), (7, 24, 384), (9, 17, 256), (3, 32, 1024),
-                                   (4, 32, 2048), (6, 20, 1280)])
+                                   (4, 32, 2048), (6, 20, 1280),
+                                   # C above 2048 at n = 32: four slabs per wave, x read again after the
+                                   # RMS barrier; n < 32 there goes to the generic kernel
+                                   (3, 32, 4096), (300, 32, 3072), (2, 24, 4096)])
 @pytest.mark.parametrize("xdt,odt", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
 @pytest.mark.parametrize("per_token", [False, True])
 def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
