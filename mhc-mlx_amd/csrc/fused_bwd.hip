@@ -660,6 +660,11 @@ void fused_bwd_lw_kernel(BwdArgs A) {
   Vec<GT, V> gr[CHK][NMAX];
   if constexpr (PIPE) {
     if ((int64_t)blockIdx.x < A.T) load_tok(xr, gr, blockIdx.x);
+    // wait for the first token here: entering the loop with its loads pending
+    // (no stores issued after them) would make the loop-top waits of every
+    // token as strict as the first one's, i.e. wait for the previous token's
+    // dx stores
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
   }
 
   int it = 0;

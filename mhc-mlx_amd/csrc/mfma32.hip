@@ -401,6 +401,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   // branches leave no registers for the next token's rows)
   if constexpr (FULL) {
     if ((int64_t)blockIdx.x < A.T) load_token(blockIdx.x);
+    // the first token's loads are waited for before the loop: pending at the
+    // loop entry (with no stores after them) they would make every token's
+    // loop-top wait also wait for the previous token's dx stores
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
   }
 
   int it = 0;
