@@ -239,6 +239,29 @@ MHC_DEV float uniform_f(float v) {
 
 MHC_DEV float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
 
+// One all-reduce step across lane ^ 16 or lane ^ 32 on gfx950's permlane
+// swaps (v_permlane16_swap / v_permlane32_swap: VALU, no LDS round trip as
+// with ds_bpermute).  Swapping a value with itself leaves the lower and the
+// upper member of each lane pair in the two results, in the same order on
+// both lanes, so op(lo, hi) is bitwise the same on both partners (and equal
+// to op(v, partner) for a commutative op).
+template <int M, typename Op>
+MHC_DEV float xor_allreduce(float v, Op op) {
+  static_assert(M == 16 || M == 32, "permlane swaps exchange 16- or 32-lane halves");
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  unsigned lo, hi;
+  if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    lo = r[0];  // vector elements copied to scalars before any bit cast
+    hi = r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    lo = r[0];
+    hi = r[1];
+  }
+  return op(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
+}
+
 template <int CTRL>
 MHC_DEV float dpp_mov(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
@@ -265,6 +288,8 @@ MHC_DEV float group_reduce(float v, Op op) {
   if constexpr (Lanes >= 4) v = op(v, dpp_mov<kDppXor2>(v));
   if constexpr (Lanes >= 8) v = op(v, dpp_mov<kDppHalfMirror>(v));
   if constexpr (Lanes >= 16) v = op(v, dpp_mov<kDppMirror>(v));
+  // (ds_bpermute here: the permlane form below made the n = 4 forward, whose
+  // per-token wave_sum sits on every workgroup's path, 5% slower)
   if constexpr (Lanes >= 32) v = op(v, shfl_xor(v, 16));
   if constexpr (Lanes >= 64) v = op(v, shfl_xor(v, 32));
   return v;
@@ -289,8 +314,8 @@ MHC_DEV float strided_sum(float v) {
   } else if constexpr (Stride <= 4 && Span == 8) {
     v += shfl_xor(v, 4);
   }
-  if constexpr (Stride <= 16 && Span >= 32) v += shfl_xor(v, 16);
-  if constexpr (Stride <= 32 && Span >= 64) v += shfl_xor(v, 32);
+  if constexpr (Stride <= 16 && Span >= 32) v = xor_allreduce<16>(v, SumOp{});
+  if constexpr (Stride <= 32 && Span >= 64) v = xor_allreduce<32>(v, SumOp{});
   return v;
 }
 
