@@ -299,6 +299,106 @@ constexpr int kMf32Slab = 2 * 32 * kMf32Row;      // x rows then g rows
 constexpr int kMf32MaxWaves = 8;                  // C <= 1024
 constexpr int kMf32Par = 32 * 32 + 2 * 32;
 
+// The backward's parameters, split once (by wave 0) into LDS: a, p of streams
+// 8q+e (the A operands of y, dyn; per lane group q), column 16J + r of M at
+// rows 8q+e (the A operand of M^T, per lane) and a of the dx rows
+// 16J + 4q + k (per lane group q).
+struct Mf32BwdPar {
+  u32x4 amt[2][3][64];
+  float4 a4[2][4];
+  u32x4 aa[3][4], ap[3][4];
+};
+
+template <typename XT, bool RAW>
+MHC_DEV void mf32_bwd_params(const Mf32Args& A, int n, Mf32BwdPar& P) {
+  const int lane = threadIdx.x & 63;
+  const int q = lane >> 4, r = lane & 15;
+  if (r == 0) {
+    float av[8], pv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = 8 * q + e;
+      av[e] = i < n ? act_pre<RAW>(A.hpre[i]) : 0.0f;
+      pv[e] = i < n ? act_post<RAW>(A.hpost[i]) : 0.0f;
+    }
+    u32x4 aa[3], ap[3];
+    split3x8<XT>(av, aa);
+    split3x8<XT>(pv, ap);
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+      P.aa[e][q] = aa[e];
+      P.ap[e][q] = ap[e];
+    }
+  }
+#pragma unroll
+  for (int J = 0; J < 2; ++J) {
+    const int col = 16 * J + r;
+    float mv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mv[e] = (col < n && 8 * q + e < n) ? A.M[(8 * q + e) * n + col] : 0.0f;
+    u32x4 amt[3];
+    split3x8<XT>(mv, amt);
+#pragma unroll
+    for (int e = 0; e < 3; ++e) P.amt[J][e][lane] = amt[e];
+    if (r == 0) {
+      float a4[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = 16 * J + 4 * q + k;
+        a4[k] = j < n ? act_pre<RAW>(A.hpre[j]) : 0.0f;
+      }
+      P.a4[J][q] = make_float4(a4[0], a4[1], a4[2], a4[3]);
+    }
+  }
+}
+
+// The workgroup's dM, dA and dP after its partial row's dw slice: dA and dP
+// summed over the 16 lanes of a group, then every wave's part added in wave
+// order through LDS (the staged slabs are no longer read by then).
+MHC_DEV void mf32_bwd_param_sums(const Mf32Args& A, float* prow, uint16_t* lds, int n, const f32x4 (&dm)[2][2],
+                                 float (&dA)[8], float (&dP)[8]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  // dA, dP: sums over the 16 lanes of a group, then the waves in order
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    dA[e] = group_sum<16>(dA[e]);
+    dP[e] = group_sum<16>(dP[e]);
+  }
+  __syncthreads();  // every wave is done with its slab: reuse the LDS for the cross-wave sums
+  float* s_fin = reinterpret_cast<float*>(lds);  // [wave][kMf32Par]
+  float* mine = s_fin + wave * kMf32Par;
+#pragma unroll
+  for (int I = 0; I < 2; ++I)
+#pragma unroll
+    for (int J = 0; J < 2; ++J)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) mine[(16 * I + 4 * q + k) * 32 + 16 * J + r] = dm[I][J][k];
+  if (r == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      mine[1024 + 8 * q + e] = dA[e];
+      mine[1024 + 32 + 8 * q + e] = dP[e];
+    }
+  }
+  __syncthreads();
+  const int nn = n * n;
+  for (int k = tid; k < nn + 2 * n; k += blockDim.x) {
+    int src;
+    if (k < nn) src = (k / n) * 32 + (k % n);
+    else if (k < nn + n) src = 1024 + (k - nn);
+    else src = 1024 + 32 + (k - nn - n);
+    float sum = 0.0f;
+    for (int w = 0; w < nwaves; ++w) sum += s_fin[w * kMf32Par + src];
+    prow[A.Cp + k] = sum;
+  }
+  if (tid == 0)
+    for (int c = A.Cp + nn + 2 * n; c < A.P; ++c) prow[c] = 0.0f;
+}
+
 template <typename XT, bool RAW, bool FULL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_kernel(Mf32Args A) {
   extern __shared__ __align__(16) uint16_t mf32_lds[];
@@ -316,51 +416,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   const int cb = wave * 128 + 8 * r;
 
   // parameters, split once by wave 0 into LDS and read per token (registers
-  // are kept for the next token's loads): a, p of streams 8q+e (A operands
-  // of y, dyn), column 16J + r of M at rows 8q+e (the A operand of M^T, per
-  // lane) and a of the dx rows 16J + 4q + k
-  __shared__ u32x4 s_amt[2][3][64];
-  __shared__ float4 s_a4[2][4];
-  __shared__ u32x4 s_aa[3][4], s_ap[3][4];
-  if (wave == 0) {
-    if (r == 0) {
-      float av[8], pv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = 8 * q + e;
-        av[e] = i < n ? act_pre<RAW>(A.hpre[i]) : 0.0f;
-        pv[e] = i < n ? act_post<RAW>(A.hpost[i]) : 0.0f;
-      }
-      u32x4 aa[3], ap[3];
-      split3x8<XT>(av, aa);
-      split3x8<XT>(pv, ap);
-#pragma unroll
-      for (int e = 0; e < 3; ++e) {
-        s_aa[e][q] = aa[e];
-        s_ap[e][q] = ap[e];
-      }
-    }
-#pragma unroll
-    for (int J = 0; J < 2; ++J) {
-      const int col = 16 * J + r;
-      float mv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mv[e] = (col < n && 8 * q + e < n) ? A.M[(8 * q + e) * n + col] : 0.0f;
-      u32x4 amt[3];
-      split3x8<XT>(mv, amt);
-#pragma unroll
-      for (int e = 0; e < 3; ++e) s_amt[J][e][lane] = amt[e];
-      if (r == 0) {
-        float a4[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int j = 16 * J + 4 * q + k;
-          a4[k] = j < n ? act_pre<RAW>(A.hpre[j]) : 0.0f;
-        }
-        s_a4[J][q] = make_float4(a4[0], a4[1], a4[2], a4[3]);
-      }
-    }
-  }
+  // are kept for the next token's loads)
+  __shared__ Mf32BwdPar s_par;
+  if (wave == 0) mf32_bwd_params<XT, RAW>(A, n, s_par);
   __syncthreads();
   float wv[8];
   {
@@ -421,8 +479,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
         *reinterpret_cast<u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]) =
             u32x4{gr[e].w[0], gr[e].w[1], gr[e].w[2], gr[e].w[3]};
       }
-      const u32x4 aa[3] = {s_aa[0][q], s_aa[1][q], s_aa[2][q]};
-      const u32x4 ap[3] = {s_ap[0][q], s_ap[1][q], s_ap[2][q]};
+      const u32x4 aa[3] = {s_par.aa[0][q], s_par.aa[1][q], s_par.aa[2][q]};
+      const u32x4 ap[3] = {s_par.ap[0][q], s_par.ap[1][q], s_par.ap[2][q]};
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
         const f32x4 ay = mfma_split3<XT>(aa, column8<XT>(xr, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f});
@@ -495,8 +553,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
         for (int v = 0; v < 8; ++v) dP[e] = fmaf(gr2[e].get(v), ynv[v], dP[e]);
 #pragma unroll
       for (int J = 0; J < 2; ++J) {
-        const u32x4 amt[3] = {s_amt[J][0][lane], s_amt[J][1][lane], s_amt[J][2][lane]};
-        const float4 a4 = s_a4[J][q];
+        const u32x4 amt[3] = {s_par.amt[J][0][lane], s_par.amt[J][1][lane], s_par.amt[J][2][lane]};
+        const float4 a4 = s_par.a4[J][q];
         uint32_t ow[4][4];
         f32x4 even;
 #pragma unroll
@@ -541,41 +599,240 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   }
   if (tid == 0)
     for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
-  // dA, dP: sums over the 16 lanes of a group, then the waves in order
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    dA[e] = group_sum<16>(dA[e]);
-    dP[e] = group_sum<16>(dP[e]);
-  }
-  __syncthreads();  // every wave is done with its slab: reuse the LDS for the cross-wave sums
-  float* s_fin = reinterpret_cast<float*>(mf32_lds);  // [wave][kMf32Par]
-  float* mine = s_fin + wave * kMf32Par;
+  mf32_bwd_param_sums(A, prow, mf32_lds, n, dm, dA, dP);
+}
+
+// ---------------------------------------------------------------------------
+// Backward at n = 32 above C = 1024 (layer-wide): SPW = 2 or 4 slabs per
+// wave, up to 8 waves.  A token's slabs do not fit in registers across the
+// RMS barrier, so the work splits around it:
+//   before: per slab, y and dyn (MFMA), the two per-token sums and
+//     dM += G X^T over the slab staged in LDS;
+//   after: per slab, last first, x and g are read again (from the caches:
+//     the token was just read, and those first reads leave it cached) for
+//     dx = M^T G + a dy (MFMA), dA and dP.
+// Of y and dyn only the pair of channels 8r + 2q, 8r + 2q + 1 stays with
+// lane group q across the barrier (the four groups hold the same values);
+// the lane's eight are gathered back from the groups afterwards.  dw of those
+// two channels is kept by the same group.
+// Token rows are addressed through buffer resources: one lane offset for all
+// rows and slabs, the row and slab parts as uniform offsets.
+// ---------------------------------------------------------------------------
+MHC_DEV void load_w8(const float* p, float (&wv)[8]) {
+  const float4 w0 = *reinterpret_cast<const float4*>(p);
+  const float4 w1 = *reinterpret_cast<const float4*>(p + 4);
+  wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+  wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+}
+
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw, 32-bit data)
+constexpr int kBufNt = 2;               // buffer access cache policy: non-temporal
+
+template <typename T>
+MHC_DEV __amdgpu_buffer_rsrc_t rows_rsrc(const T* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, (int)bytes, kRsrcWord3);
+}
+
+template <int AUX, typename T>
+MHC_DEV void buf_load(Vec<T, 8>& v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, AUX);
+  v.w[0] = u.x; v.w[1] = u.y; v.w[2] = u.z; v.w[3] = u.w;
+}
+
+// v[2 grp + k] for a lane-dependent grp in 0..3, as bit selects (a select
+// chain on these values was turned into branches)
+MHC_DEV float pick_pair(const float (&v)[8], int grp, int k) {
+  const uint32_t m1 = 0u - (uint32_t)(grp & 1), m2 = 0u - (uint32_t)((grp >> 1) & 1);
+  const uint32_t a = __builtin_bit_cast(uint32_t, v[k]), b = __builtin_bit_cast(uint32_t, v[2 + k]);
+  const uint32_t c = __builtin_bit_cast(uint32_t, v[4 + k]), d = __builtin_bit_cast(uint32_t, v[6 + k]);
+  const uint32_t lo = (a & ~m1) | (b & m1), hi = (c & ~m1) | (d & m1);
+  return __builtin_bit_cast(float, (lo & ~m2) | (hi & m2));
+}
+
+template <typename XT, bool RAW, int SPW>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_wide_kernel(Mf32Args A) {
+  extern __shared__ __align__(16) uint16_t mf32_lds[];
+  __shared__ float s_red[2][2][kMf32MaxWaves];
+  __shared__ Mf32BwdPar s_par;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  constexpr int n = 32;
+  constexpr uint32_t kEs = sizeof(XT);
+  const int C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  uint16_t* xs = mf32_lds + (size_t)wave * kMf32Slab;
+  uint16_t* gs = xs + 32 * kMf32Row;
+  const int slab0 = wave * SPW * 128;
+  const uint32_t rowb = (uint32_t)C * kEs;                      // one stream row
+  const uint32_t slabb = (uint32_t)slab0 * kEs;                 // the wave's first slab
+  const uint32_t lane_in = (uint32_t)(8 * q * C + 8 * r) * kEs;  // stream 8q (+ e rows)
+  const uint32_t lane_dx = (uint32_t)(4 * q * C + 8 * r) * kEs;  // stream 4q (+ 16 J + k rows)
+  const uint32_t tokb = (uint32_t)(nC * kEs);
+
+  if (wave == 0) mf32_bwd_params<XT, RAW>(A, n, s_par);
+  __syncthreads();
+  f32x4 dm[2][2];
 #pragma unroll
   for (int I = 0; I < 2; ++I)
 #pragma unroll
-    for (int J = 0; J < 2; ++J)
+    for (int J = 0; J < 2; ++J) dm[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float dA[8], dP[8], dwv[SPW][2];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) mine[(16 * I + 4 * q + k) * 32 + 16 * J + r] = dm[I][J][k];
-  if (r == 0) {
+  for (int e = 0; e < 8; ++e) dA[e] = dP[e] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      mine[1024 + 8 * q + e] = dA[e];
-      mine[1024 + 32 + 8 * q + e] = dP[e];
+  for (int s = 0; s < SPW; ++s) dwv[s][0] = dwv[s][1] = 0.0f;
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const auto rx = rows_rsrc((const XT*)A.x + t * nC, tokb);
+    const auto rg = rows_rsrc((const XT*)A.g + t * nC, tokb);
+    float yk[SPW][2], dk[SPW][2];
+    float ss = 0.0f, sr = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t sb = slabb + (uint32_t)s * 128 * kEs;
+      Vec<XT, 8> xr[8], gr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        buf_load<0>(xr[e], rx, lane_in, sb + (uint32_t)e * rowb);
+        buf_load<0>(gr[e], rg, lane_in, sb + (uint32_t)e * rowb);
+      }
+      float wv[8];
+      load_w8(A.w + slab0 + s * 128 + 8 * r, wv);
+      // stage the slab for dM (the previous slab's reads of the buffer were
+      // issued first, and one wave's LDS accesses complete in order)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        *reinterpret_cast<u32x4*>(&xs[(8 * q + e) * kMf32Row + 8 * r]) =
+            u32x4{xr[e].w[0], xr[e].w[1], xr[e].w[2], xr[e].w[3]};
+        *reinterpret_cast<u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]) =
+            u32x4{gr[e].w[0], gr[e].w[1], gr[e].w[2], gr[e].w[3]};
+      }
+      const u32x4 aa[3] = {s_par.aa[0][q], s_par.aa[1][q], s_par.aa[2][q]};
+      const u32x4 ap[3] = {s_par.ap[0][q], s_par.ap[1][q], s_par.ap[2][q]};
+      float y[8], dyn[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const f32x4 ay = mfma_split3<XT>(aa, column8<XT>(xr, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        const f32x4 ad = mfma_split3<XT>(ap, column8<XT>(gr, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        y[v] = ay[0];
+        dyn[v] = ad[0];
+        ss = fmaf(ay[0], ay[0], ss);
+        sr = fmaf(ad[0] * ay[0], wv[v], sr);
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        yk[s][k] = pick_pair(y, q, k);
+        dk[s][k] = pick_pair(dyn, q, k);
+        // selected here, not at the uses after the barrier (sunk there, the
+        // selects would keep all eight values of every slab live across it)
+        asm volatile("" : "+v"(yk[s][k]), "+v"(dk[s][k]));
+      }
+      // dM over the slab: A = g rows 16I + r, B = x rows 16J + r, 32 channels per step
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        u32x4 ga[2], xb[2];
+#pragma unroll
+        for (int I = 0; I < 2; ++I) {
+          ga[I] = *reinterpret_cast<const u32x4*>(&gs[(16 * I + r) * kMf32Row + 32 * kk + 8 * q]);
+          xb[I] = *reinterpret_cast<const u32x4*>(&xs[(16 * I + r) * kMf32Row + 32 * kk + 8 * q]);
+        }
+#pragma unroll
+        for (int I = 0; I < 2; ++I)
+#pragma unroll
+          for (int J = 0; J < 2; ++J) dm[I][J] = mfma32k<XT>(ga[I], xb[J], dm[I][J]);
+      }
+    }
+    // the four lane groups q hold the same y and dyn: count them once
+    ss = q == 0 ? ss : 0.0f;
+    sr = q == 0 ? sr : 0.0f;
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    lds_barrier();
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+
+    const auto rdx = rows_rsrc((const XT*)A.out + t * nC, tokb);
+#pragma unroll
+    for (int s = SPW - 1; s >= 0; --s) {
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t sb = slabb + (uint32_t)s * 128 * kEs;
+      Vec<XT, 8> gr[8], xr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) buf_load<kBufNt>(gr[e], rg, lane_in, sb + (uint32_t)e * rowb);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) buf_load<kBufNt>(xr[e], rx, lane_in, sb + (uint32_t)e * rowb);
+      float wv[8];
+      load_w8(A.w + slab0 + s * 128 + 8 * r, wv);
+      // y and dyn of the lane's 8 channels back from the four lane groups
+      float dyv[8], ynv[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int src = 16 * (v >> 1) + r;
+        const float yv = __shfl(yk[s][v & 1], src);
+        const float dn = __shfl(dk[s][v & 1], src);
+        dyv[v] = dn * inv * wv[v] - kf * yv;
+        ynv[v] = (yv * inv) * wv[v];
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k) dwv[s][k] = fmaf(dk[s][k], yk[s][k] * inv, dwv[s][k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) dP[e] = fmaf(gr[e].get(v), ynv[v], dP[e]);
+#pragma unroll
+      for (int J = 0; J < 2; ++J) {
+        const u32x4 amt[3] = {s_par.amt[J][0][lane], s_par.amt[J][1][lane], s_par.amt[J][2][lane]};
+        const float4 a4 = s_par.a4[J][q];
+        uint32_t ow[4][4];
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const u32x4 bg = column8<XT>(gr, v);
+          f32x4 acc = {a4.x * dyv[v], a4.y * dyv[v], a4.z * dyv[v], a4.w * dyv[v]};
+          acc = mfma_split3<XT>(amt, bg, acc);
+          if (v & 1) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ow[k][v >> 1] = pack2<XT>(even[k], acc[k]);
+          } else {
+            even = acc;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx, lane_dx,
+                                                 sb + (uint32_t)(16 * J + k) * rowb, kBufNt);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) dA[e] = fmaf(dyv[v], xr[e].get(v), dA[e]);
     }
   }
-  __syncthreads();
-  const int nn = n * n;
-  for (int k = tid; k < nn + 2 * n; k += blockDim.x) {
-    int src;
-    if (k < nn) src = (k / n) * 32 + (k % n);
-    else if (k < nn + n) src = 1024 + (k - nn);
-    else src = 1024 + 32 + (k - nn - n);
-    float sum = 0.0f;
-    for (int w = 0; w < nwaves; ++w) sum += s_fin[w * kMf32Par + src];
-    prow[A.Cp + k] = sum;
-  }
+
+  // ---- the workgroup's partial row [dw C | 0 .. Cp | dM n*n | dA n | dP n | 0 .. P]
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+#pragma unroll
+  for (int s = 0; s < SPW; ++s)
+    *reinterpret_cast<float2*>(prow + slab0 + s * 128 + 8 * r + 2 * q) = make_float2(dwv[s][0], dwv[s][1]);
   if (tid == 0)
-    for (int c = A.Cp + nn + 2 * n; c < A.P; ++c) prow[c] = 0.0f;
+    for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
+  mf32_bwd_param_sums(A, prow, mf32_lds, n, dm, dA, dP);
 }
 
 template <typename F>
@@ -635,21 +892,33 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
 }
 
 int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
-  if (A.n <= 16 || A.n > 32 || A.M_ts != 0 || A.C % 128 != 0 || A.C > 128 * kMf32MaxWaves) return 1;
+  if (A.n <= 16 || A.n > 32 || A.M_ts != 0 || A.C % 128 != 0) return 1;
   if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
   if (A.P != A.Cp + round_up(A.n * A.n + 2 * A.n, 4)) return 1;
   if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.out, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
     return 1;
   if (knob(kKnobBwdMfma, 1) == 0) return 1;
-  const int waves = A.C / 128;
+  const int S = A.C / 128;
+  // one slab per wave up to C = 1024; above it (n == 32 only) two or four,
+  // with g read again after the RMS barrier
+  const int spw = S <= kMf32MaxWaves ? 1 : (S <= 2 * kMf32MaxWaves ? 2 : 4);
+  if (S % spw != 0 || S / spw > kMf32MaxWaves) return 1;
+  const bool full = A.n == 32;
+  if (spw > 1 && !full) return 1;
+  const int waves = S / spw;
   const size_t smem = std::max<size_t>((size_t)waves * kMf32Slab * sizeof(uint16_t),
                                        (size_t)waves * kMf32Par * sizeof(float));
   const bool raw = A.h_mode == MHC_H_RAW;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
-    const bool full = A.n == 32;
-    const void* kfn = full ? (raw ? (const void*)mf32_bwd_kernel<XT, true, true> : (const void*)mf32_bwd_kernel<XT, false, true>)
-                           : (raw ? (const void*)mf32_bwd_kernel<XT, true, false> : (const void*)mf32_bwd_kernel<XT, false, false>);
+    const void* kfn;
+    if (spw == 1)
+      kfn = full ? (raw ? (const void*)mf32_bwd_kernel<XT, true, true> : (const void*)mf32_bwd_kernel<XT, false, true>)
+                 : (raw ? (const void*)mf32_bwd_kernel<XT, true, false> : (const void*)mf32_bwd_kernel<XT, false, false>);
+    else if (spw == 2)
+      kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, 2> : (const void*)mf32_bwd_wide_kernel<XT, false, 2>;
+    else
+      kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, 4> : (const void*)mf32_bwd_wide_kernel<XT, false, 4>;
     const int occ = occupancy_blocks(kfn, waves * 64, smem);
     if (occ <= 0) return 1;
     int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
@@ -657,12 +926,20 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     if (grid_pref > 0) blocks = std::min<int64_t>(gmax, grid_pref);
     blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
     const dim3 g((unsigned)blocks), b(waves * 64);
-    if (full) {
-      if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true, true>), g, b, smem, s, A);
-      else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false, true>), g, b, smem, s, A);
+    if (spw == 1) {
+      if (full) {
+        if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true, true>), g, b, smem, s, A);
+        else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false, true>), g, b, smem, s, A);
+      } else {
+        if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true, false>), g, b, smem, s, A);
+        else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false, false>), g, b, smem, s, A);
+      }
+    } else if (spw == 2) {
+      if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, 2>), g, b, smem, s, A);
+      else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, 2>), g, b, smem, s, A);
     } else {
-      if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true, false>), g, b, smem, s, A);
-      else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false, false>), g, b, smem, s, A);
+      if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, 4>), g, b, smem, s, A);
+      else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, 4>), g, b, smem, s, A);
     }
     MHC_CHECK_LAUNCH("mf32_bwd_kernel");
     *num_partials = blocks;

@@ -2,7 +2,8 @@
 
 The forward covers n = 17, 24 and 32, C from one 128-channel slab to 2048 (one and two slabs per wave),
 16-bit x with 16-bit or fp32 output, layer-wide and per-token parameters; the backward covers
-layer-wide parameters with 16-bit x and dout up to C = 1024.  With the grid knobs at a few
+layer-wide parameters with 16-bit x and dout up to C = 1024, and at n = 32 up to C = 4096 (two or
+four slabs per wave, x and g read again after the RMS barrier).  With the grid knobs at a few
 workgroups every workgroup walks many tokens.  Shapes outside these ranges (odd C, fp32 x, fp32
 dout, per-token backward) take the generic kernels and are covered by tests/test_gpu_fused.py.
 """
@@ -54,7 +55,11 @@ def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
 
 
 @pytest.mark.parametrize("T,n,C", [(5, 32, 128), (300, 32, 512), (40, 24, 256), (33, 17, 640), (7, 32, 1024),
-                                   (64, 28, 384)])
+                                   (64, 28, 384),
+                                   # n = 32 above C = 1024: two slabs per wave (6 and 8 waves), four
+                                   # (5, 6 and 8 waves); n < 32 there takes the generic kernel
+                                   (9, 32, 1536), (4, 32, 2048), (5, 32, 2560), (17, 32, 3072), (3, 32, 4096),
+                                   (4, 24, 2048)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_mfma32_backward_layer_wide(T, n, C, dt, knobs):
     knobs("MHC_BWD_GRID", 3)
