@@ -102,6 +102,22 @@ MHC_DEV f32x4 mfma_split3(const u32x4 (&a)[3], u32x4 b, f32x4 acc) {
   return acc;
 }
 
+// Token rows through buffer resources: one lane offset serves every row and
+// slab, the row and slab parts go in as uniform offsets.
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw, 32-bit data)
+constexpr int kBufNt = 2;               // buffer access cache policy: non-temporal
+
+template <typename T>
+MHC_DEV __amdgpu_buffer_rsrc_t rows_rsrc(const T* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, (int)bytes, kRsrcWord3);
+}
+
+template <int AUX, typename T>
+MHC_DEV void buf_load(Vec<T, 8>& v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, AUX);
+  v.w[0] = u.x; v.w[1] = u.y; v.w[2] = u.z; v.w[3] = u.w;
+}
+
 // Four output rows of eight channels, filled a channel pair (p = 0..3) at a
 // time: 16-bit rows as packed words (one conversion per pair), fp32 rows as
 // the values themselves; stored as 16-byte pieces.
@@ -138,6 +154,14 @@ MHC_DEV float act_pre(float h) { return RAW ? sigmoid_fast(h) : h; }
 template <bool RAW>
 MHC_DEV float act_post(float h) { return RAW ? 2.0f * sigmoid_fast(h) : h; }
 
+// Eight consecutive RMS weights.
+MHC_DEV void load_w8(const float* p, float (&wv)[8]) {
+  const float4 w0 = *reinterpret_cast<const float4*>(p);
+  const float4 w1 = *reinterpret_cast<const float4*>(p + 4);
+  wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+  wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+}
+
 // ---------------------------------------------------------------------------
 // Forward.  One token at a time per workgroup of S / SPW waves (S = C / 128
 // slabs); the grid strides over tokens, so layer-wide parameters are split
@@ -145,11 +169,23 @@ MHC_DEV float act_post(float h) { return RAW ? 2.0f * sigmoid_fast(h) : h; }
 // runs after it, slab by slab, straight into the output rows.
 // ---------------------------------------------------------------------------
 
+// v[2 grp + k] for a lane-dependent grp in 0..3, as bit selects (a select
+// chain on these values was turned into branches)
+MHC_DEV float pick_pair(const float (&v)[8], int grp, int k) {
+  const uint32_t m1 = 0u - (uint32_t)(grp & 1), m2 = 0u - (uint32_t)((grp >> 1) & 1);
+  const uint32_t a = __builtin_bit_cast(uint32_t, v[k]), b = __builtin_bit_cast(uint32_t, v[2 + k]);
+  const uint32_t c = __builtin_bit_cast(uint32_t, v[4 + k]), d = __builtin_bit_cast(uint32_t, v[6 + k]);
+  const uint32_t lo = (a & ~m1) | (b & m1), hi = (c & ~m1) | (d & m1);
+  return __builtin_bit_cast(float, (lo & ~m2) | (hi & m2));
+}
+
 // FULL: n == 32, so no stream index is ever out of range (no per-stream
 // branches in the load, store and parameter code).
 // RELOAD (C above 2048: SPW = C / 1024 slabs per wave): the transposed
 // slabs do not stay in registers across the RMS barrier; the lane reads its
 // x again for the mix (from the caches: the token was read just before).
+// Of y only channels 8r + 2q, 8r + 2q + 1 stay with lane group q (the four
+// groups hold the same values), gathered back after the barrier.
 template <typename XT, typename OT, int SPW, bool PT, bool RAW, bool FULL, bool RELOAD = false>
 __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
   __shared__ float s_red[2][16];
@@ -208,7 +244,9 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
       transpose8<XT>(xr, b);
     };
     u32x4 bx[RELOAD ? 1 : SPW][8];
-    float y[SPW][8];
+    float y[RELOAD ? 1 : SPW][8];
+    // RELOAD: y of channels 8r + 2q, 8r + 2q + 1 kept by lane group q
+    float yk[RELOAD ? SPW : 1][2];
     float ss = 0.0f;
     if constexpr (!RELOAD) {
       Vec<XT, 8> xr[SPW][8];
@@ -231,8 +269,16 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
         const f32x4 acc = mfma_split3<XT>(aa, bx[RELOAD ? 0 : s][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-        if constexpr (!RELOAD) y[s][v] = acc[0];
+        y[RELOAD ? 0 : s][v] = acc[0];
         ss = fmaf(acc[0], acc[0], ss);
+      }
+      if constexpr (RELOAD) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          yk[s][k] = pick_pair(y[0], q, k);
+          // selected here, not at the uses after the barrier
+          asm volatile("" : "+v"(yk[s][k]));
+        }
       }
     }
     // the four lane groups q hold the same y: count it once
@@ -246,19 +292,19 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
     if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
-      // RELOAD: y of the slab recomputed from the reloaded x (the same MFMAs,
-      // so bitwise the value the sum of squares used)
+      // RELOAD: x of the slab read again; y of the lane's eight channels
+      // gathered back from the four lane groups
       if constexpr (RELOAD) {
         load_slab(s, bx[0]);
 #pragma unroll
-        for (int v = 0; v < 8; ++v) y[s][v] = mfma_split3<XT>(aa, bx[0][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f})[0];
+        for (int v = 0; v < 8; ++v) y[0][v] = __shfl(yk[s][v & 1], 16 * (v >> 1) + r);
       }
       const float4 w0 = *reinterpret_cast<const float4*>(A.w + cb[s]);
       const float4 w1 = *reinterpret_cast<const float4*>(A.w + cb[s] + 4);
       const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
       float yn[8];
 #pragma unroll
-      for (int v = 0; v < 8; ++v) yn[v] = (y[s][v] * inv) * wv[v];
+      for (int v = 0; v < 8; ++v) yn[v] = (y[RELOAD ? 0 : s][v] * inv) * wv[v];
 #pragma unroll
       for (int I = 0; I < 2; ++I) {
         // four output rows of this lane, converted a channel pair at a time
@@ -615,40 +661,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 // lane group q across the barrier (the four groups hold the same values);
 // the lane's eight are gathered back from the groups afterwards.  dw of those
 // two channels is kept by the same group.
-// Token rows are addressed through buffer resources: one lane offset for all
-// rows and slabs, the row and slab parts as uniform offsets.
 // ---------------------------------------------------------------------------
-MHC_DEV void load_w8(const float* p, float (&wv)[8]) {
-  const float4 w0 = *reinterpret_cast<const float4*>(p);
-  const float4 w1 = *reinterpret_cast<const float4*>(p + 4);
-  wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
-  wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
-}
-
-constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw, 32-bit data)
-constexpr int kBufNt = 2;               // buffer access cache policy: non-temporal
-
-template <typename T>
-MHC_DEV __amdgpu_buffer_rsrc_t rows_rsrc(const T* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, (int)bytes, kRsrcWord3);
-}
-
-template <int AUX, typename T>
-MHC_DEV void buf_load(Vec<T, 8>& v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
-  const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, AUX);
-  v.w[0] = u.x; v.w[1] = u.y; v.w[2] = u.z; v.w[3] = u.w;
-}
-
-// v[2 grp + k] for a lane-dependent grp in 0..3, as bit selects (a select
-// chain on these values was turned into branches)
-MHC_DEV float pick_pair(const float (&v)[8], int grp, int k) {
-  const uint32_t m1 = 0u - (uint32_t)(grp & 1), m2 = 0u - (uint32_t)((grp >> 1) & 1);
-  const uint32_t a = __builtin_bit_cast(uint32_t, v[k]), b = __builtin_bit_cast(uint32_t, v[2 + k]);
-  const uint32_t c = __builtin_bit_cast(uint32_t, v[4 + k]), d = __builtin_bit_cast(uint32_t, v[6 + k]);
-  const uint32_t lo = (a & ~m1) | (b & m1), hi = (c & ~m1) | (d & m1);
-  return __builtin_bit_cast(float, (lo & ~m2) | (hi & m2));
-}
-
 template <typename XT, bool RAW, int SPW>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_wide_kernel(Mf32Args A) {
   extern __shared__ __align__(16) uint16_t mf32_lds[];
