@@ -255,16 +255,16 @@ def _reference_scenarios(dev):
                       "(Apple silicon, context only)", "rows": rows}
 
 
-def _n32_training(dev, steps=20, warmup=20):
-    """n=32 training steps: MHCLayer fwd+bwd at 8192 x 32 x 512 bf16 and MHCRewire(Linear(4096,4096)) at n=32."""
+def _n32_layer_row(dev, T, C, steps, warmup, seed):
+    """One MHCLayer fwd+bwd row at n=32, bf16 I/O, layer-wide parameters."""
     import numpy as np
     import torch
 
-    from mhc_mlx_amd import MHCRewire, kernel_timer
+    from mhc_mlx_amd import kernel_timer
 
-    T, n, C = 8192, 32, 512
-    layer = _layer(n, C, dev, np.random.default_rng(6))
-    gen = torch.Generator(dev).manual_seed(6)
+    n = 32
+    layer = _layer(n, C, dev, np.random.default_rng(seed))
+    gen = torch.Generator(dev).manual_seed(seed)
     x = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen).requires_grad_(True)
     dout = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen)
     params = [layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight]
@@ -280,11 +280,24 @@ def _n32_training(dev, steps=20, warmup=20):
         _time_loop(step, steps)
         st = kt.stats()
     e = T * n * C * 2
-    layer_row = {"workload": "MHCLayer fwd+bwd, 8192 tokens, n=32, C=512, bf16 I/O", "ms_per_step": ms,
-                 "tokens_per_s": T / (ms / 1e3), "step_hbm_frac": 5 * e / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
-                 "kernels_us": {k: round(v["mean_ms"] * 1e3, 1) for k, v in st.items()}}
+    row = {"workload": f"MHCLayer fwd+bwd, {T} tokens, n=32, C={C}, bf16 I/O", "ms_per_step": ms,
+           "tokens_per_s": T / (ms / 1e3), "step_hbm_frac": 5 * e / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+           "kernels_us": {k: round(v["mean_ms"] * 1e3, 1) for k, v in st.items()}}
     del x, dout, layer
     torch.cuda.empty_cache()
+    return row
+
+
+def _n32_training(dev, steps=20, warmup=20):
+    """n=32 training steps: MHCLayer fwd+bwd at 8192 x 32 x 512 and 2048 x 32 x 4096 (the same bytes) bf16, and
+    MHCRewire(Linear(4096,4096)) at n=32."""
+    import torch
+
+    from mhc_mlx_amd import MHCRewire, kernel_timer
+
+    T, n = 8192, 32
+    layer_row = _n32_layer_row(dev, T, 512, steps, warmup, 6)
+    wide_row = _n32_layer_row(dev, 2048, 4096, steps, warmup, 8)
 
     dims = 4096
     torch.manual_seed(7)
@@ -307,7 +320,7 @@ def _n32_training(dev, steps=20, warmup=20):
         rst = kt.stats()
     rewire_row = {"workload": "MHCRewire(Linear(4096,4096)), n=32 (C=128), 8192 tokens, bf16, fwd+bwd",
                   "ms_per_step": rms, "mhc_kernels_us": {k: round(v["mean_ms"] * 1e3, 1) for k, v in rst.items()}}
-    return {"layer": layer_row, "rewire": rewire_row}
+    return {"layer": layer_row, "layer_c4096": wide_row, "rewire": rewire_row}
 
 
 def _residual(dev, steps, warmup):
