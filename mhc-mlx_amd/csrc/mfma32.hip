@@ -848,6 +848,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   mf32_bwd_param_sums(A, prow, mf32_lds, n, dm, dA, dP);
 }
 
+constexpr int kMf32MaxSpw = 8;  // slabs per wave of the wide backward (C <= 8 waves x 8 x 128)
+
+// f(std::integral_constant<int, spw>) for spw in 2 .. kMf32MaxSpw.
+template <typename F>
+void with_spw(int spw, F&& f) {
+  switch (spw) {
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 3: f(std::integral_constant<int, 3>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    case 5: f(std::integral_constant<int, 5>{}); break;
+    case 6: f(std::integral_constant<int, 6>{}); break;
+    case 7: f(std::integral_constant<int, 7>{}); break;
+    case 8: f(std::integral_constant<int, 8>{}); break;
+    default: break;
+  }
+}
+
 template <typename F>
 int by_half(int code, F&& f) {
   if (code == MHC_DTYPE_BF16) return f((__bf16*)nullptr);
@@ -912,10 +929,22 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     return 1;
   if (knob(kKnobBwdMfma, 1) == 0) return 1;
   const int S = A.C / 128;
-  // one slab per wave up to C = 1024; above it (n == 32 only) two or four,
-  // with g read again after the RMS barrier
-  const int spw = S <= kMf32MaxWaves ? 1 : (S <= 2 * kMf32MaxWaves ? 2 : 4);
-  if (S % spw != 0 || S / spw > kMf32MaxWaves) return 1;
+  // one slab per wave up to C = 1024; above it (n == 32 only) SPW = 2 .. 8
+  // slabs per wave, with x and g read again after the RMS barrier: the wave
+  // count nearest MHC_MF32_WAVES (default 8) among those that divide S.
+  // Measured (2048 tokens, bf16): C = 3072 on 8 waves 268 us, on 4 (two
+  // workgroups per CU) 284 us; C = 4096 400 against 384 us; C = 2048 355
+  // against 358 us.
+  int spw = 1;
+  if (S > kMf32MaxWaves) {
+    const int target = std::max(1, knob(kKnobMf32Waves, kMf32MaxWaves));
+    spw = 0;
+    for (int c = 2; c <= kMf32MaxSpw; ++c) {
+      if (S % c != 0 || S / c > kMf32MaxWaves) continue;
+      if (spw == 0 || std::abs(S / c - target) < std::abs(S / spw - target)) spw = c;
+    }
+    if (spw == 0) return 1;
+  }
   const bool full = A.n == 32;
   if (spw > 1 && !full) return 1;
   const int waves = S / spw;
@@ -924,14 +953,16 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   const bool raw = A.h_mode == MHC_H_RAW;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
-    const void* kfn;
-    if (spw == 1)
+    const void* kfn = nullptr;
+    if (spw == 1) {
       kfn = full ? (raw ? (const void*)mf32_bwd_kernel<XT, true, true> : (const void*)mf32_bwd_kernel<XT, false, true>)
                  : (raw ? (const void*)mf32_bwd_kernel<XT, true, false> : (const void*)mf32_bwd_kernel<XT, false, false>);
-    else if (spw == 2)
-      kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, 2> : (const void*)mf32_bwd_wide_kernel<XT, false, 2>;
-    else
-      kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, 4> : (const void*)mf32_bwd_wide_kernel<XT, false, 4>;
+    } else {
+      with_spw(spw, [&](auto c) {
+        kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, decltype(c)::value>
+                  : (const void*)mf32_bwd_wide_kernel<XT, false, decltype(c)::value>;
+      });
+    }
     const int occ = occupancy_blocks(kfn, waves * 64, smem);
     if (occ <= 0) return 1;
     int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
@@ -947,12 +978,12 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
         if (raw) hipLaunchKernelGGL((mf32_bwd_kernel<XT, true, false>), g, b, smem, s, A);
         else hipLaunchKernelGGL((mf32_bwd_kernel<XT, false, false>), g, b, smem, s, A);
       }
-    } else if (spw == 2) {
-      if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, 2>), g, b, smem, s, A);
-      else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, 2>), g, b, smem, s, A);
     } else {
-      if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, 4>), g, b, smem, s, A);
-      else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, 4>), g, b, smem, s, A);
+      with_spw(spw, [&](auto c) {
+        constexpr int SPW = decltype(c)::value;
+        if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, SPW>), g, b, smem, s, A);
+        else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, SPW>), g, b, smem, s, A);
+      });
     }
     MHC_CHECK_LAUNCH("mf32_bwd_kernel");
     *num_partials = blocks;

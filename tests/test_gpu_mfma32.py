@@ -2,8 +2,8 @@
 
 The forward covers n = 17, 24 and 32, C from one 128-channel slab to 2048 (one and two slabs per wave),
 16-bit x with 16-bit or fp32 output, layer-wide and per-token parameters; the backward covers
-layer-wide parameters with 16-bit x and dout up to C = 1024, and at n = 32 up to C = 4096 (two or
-four slabs per wave, x and g read again after the RMS barrier).  With the grid knobs at a few
+layer-wide parameters with 16-bit x and dout up to C = 1024, and at n = 32 up to C = 8192 (2 to 8
+slabs per wave, x and g read again after the RMS barrier).  With the grid knobs at a few
 workgroups every workgroup walks many tokens.  Shapes outside these ranges (odd C, fp32 x, fp32
 dout, per-token backward) take the generic kernels and are covered by tests/test_gpu_fused.py.
 """
@@ -56,12 +56,25 @@ def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
 
 @pytest.mark.parametrize("T,n,C", [(5, 32, 128), (300, 32, 512), (40, 24, 256), (33, 17, 640), (7, 32, 1024),
                                    (64, 28, 384),
-                                   # n = 32 above C = 1024: two slabs per wave (6 and 8 waves), four
-                                   # (5, 6 and 8 waves); n < 32 there takes the generic kernel
-                                   (9, 32, 1536), (4, 32, 2048), (5, 32, 2560), (17, 32, 3072), (3, 32, 4096),
-                                   (4, 24, 2048)])
+                                   # n = 32 above C = 1024: 2 .. 8 slabs per wave on 3 to 8 waves (the
+                                   # largest wave count up to 8 that divides C / 128; C = 1408 has none;
+                                   # above C = 4096 the forward runs on the generic kernel); n < 32 there
+                                   # takes the generic kernel
+                                   (3, 32, 1152), (9, 32, 1536), (2, 32, 1408), (4, 32, 2048), (5, 32, 2560),
+                                   (17, 32, 3072), (2, 32, 3584), (3, 32, 4096), (2, 32, 8192), (4, 24, 2048)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_mfma32_backward_layer_wide(T, n, C, dt, knobs):
+    _backward_layer_wide(T, n, C, dt, knobs)
+
+
+@pytest.mark.parametrize("T,C,waves", [(6, 2048, 4), (5, 4096, 4), (4, 3072, 2)])
+def test_mfma32_backward_wave_counts(T, C, waves, knobs):
+    """Other splits of the same shapes (MHC_MF32_WAVES): 4 waves of 4 or 8 slabs, 3 waves of 8."""
+    knobs("MHC_MF32_WAVES", waves)
+    _backward_layer_wide(T, 32, C, "bf16", knobs)
+
+
+def _backward_layer_wide(T, n, C, dt, knobs):
     knobs("MHC_BWD_GRID", 3)
     g = rng(3300 + T + n + C)
     x = to_dtype_np(g.standard_normal((T, n, C)), dt)
