@@ -848,7 +848,262 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   mf32_bwd_param_sums(A, prow, mf32_lds, n, dm, dA, dP);
 }
 
-constexpr int kMf32MaxSpw = 8;  // slabs per wave of the wide backward (C <= 8 waves x 8 x 128)
+// ---------------------------------------------------------------------------
+// The same backward with each slab step's x and g loaded one step ahead (the
+// default; MHC_BWD_PIPE=0 selects the kernel above).  A step stages its x and
+// g registers in the wave's LDS slab buffer, issues the next step's loads
+// into the freed registers and computes from the staged copy, so a slab's
+// loads are in flight during the previous slab's MFMAs.  Steps per token:
+// before the RMS barrier slabs 0 .. SPW-1; after it SPW-1 (still staged from
+// the last step before the barrier, so not read again), then SPW-2 .. 0.
+// The last step loads the next token's first slab, before its dx stores.
+// ---------------------------------------------------------------------------
+template <typename XT, bool RAW, int SPW>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_pipe_kernel(Mf32Args A) {
+  extern __shared__ __align__(16) uint16_t mf32_lds[];
+  __shared__ float s_red[2][2][kMf32MaxWaves];
+  __shared__ Mf32BwdPar s_par;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  constexpr int n = 32;
+  constexpr uint32_t kEs = sizeof(XT);
+  const int C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  uint16_t* xs = mf32_lds + (size_t)wave * kMf32Slab;
+  uint16_t* gs = xs + 32 * kMf32Row;
+  const int slab0 = wave * SPW * 128;
+  const uint32_t rowb = (uint32_t)C * kEs;                      // one stream row
+  const uint32_t slabb = (uint32_t)slab0 * kEs;                 // the wave's first slab
+  const uint32_t lane_in = (uint32_t)(8 * q * C + 8 * r) * kEs;  // stream 8q (+ e rows)
+  const uint32_t lane_dx = (uint32_t)(4 * q * C + 8 * r) * kEs;  // stream 4q (+ 16 J + k rows)
+  const uint32_t tokb = (uint32_t)(nC * kEs);
+
+  if (wave == 0) mf32_bwd_params<XT, RAW>(A, n, s_par);
+  __syncthreads();
+  f32x4 dm[2][2];
+#pragma unroll
+  for (int I = 0; I < 2; ++I)
+#pragma unroll
+    for (int J = 0; J < 2; ++J) dm[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float dA[8], dP[8], dwv[SPW][2];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dA[e] = dP[e] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < SPW; ++s) dwv[s][0] = dwv[s][1] = 0.0f;
+
+  // the step's x and g rows (streams 8q + e, channels 8r .. 8r + 7 of a slab)
+  Vec<XT, 8> xr[8], gr[8];
+  using Cached = std::integral_constant<int, 0>;
+  using Stream = std::integral_constant<int, kBufNt>;
+  auto load = [&](auto aux, int64_t t, int s) {
+    const auto rx = rows_rsrc((const XT*)A.x + t * nC, tokb);
+    const auto rg = rows_rsrc((const XT*)A.g + t * nC, tokb);
+    const uint32_t sb = slabb + (uint32_t)s * 128 * kEs;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      buf_load<decltype(aux)::value>(xr[e], rx, lane_in, sb + (uint32_t)e * rowb);
+      buf_load<decltype(aux)::value>(gr[e], rg, lane_in, sb + (uint32_t)e * rowb);
+    }
+  };
+  // one LDS row per stream (the previous step's reads of the buffer were
+  // issued first, and one wave's LDS accesses complete in order)
+  auto stage = [&]() {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      *reinterpret_cast<u32x4*>(&xs[(8 * q + e) * kMf32Row + 8 * r]) =
+          u32x4{xr[e].w[0], xr[e].w[1], xr[e].w[2], xr[e].w[3]};
+      *reinterpret_cast<u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]) =
+          u32x4{gr[e].w[0], gr[e].w[1], gr[e].w[2], gr[e].w[3]};
+    }
+  };
+  // the lane's own rows back from the staged slab
+  auto rows_back = [&](const uint16_t* buf, Vec<XT, 8>(&rows)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const u32x4 u = *reinterpret_cast<const u32x4*>(&buf[(8 * q + e) * kMf32Row + 8 * r]);
+      rows[e].w[0] = u[0]; rows[e].w[1] = u[1]; rows[e].w[2] = u[2]; rows[e].w[3] = u[3];
+    }
+  };
+
+  load(Cached{}, blockIdx.x, 0);
+  // the first token's loads are waited for before the loop: pending at the
+  // loop entry they would make every token's first wait also wait for the
+  // previous token's dx stores
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    float yk[SPW][2], dk[SPW][2];
+    float ss = 0.0f, sr = 0.0f;
+    float wlast[8];  // w of slab SPW - 1, used again right after the barrier
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      // w first: a wait for a load also waits for every load issued before it
+      float wv[8];
+      load_w8(A.w + slab0 + s * 128 + 8 * r, wv);
+      if (s == SPW - 1) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) wlast[v] = wv[v];
+      }
+      stage();
+      // next: slab s + 1; after the last slab, the second step after the barrier (SPW - 2)
+      if (s + 1 < SPW) load(Cached{}, t, s + 1);
+      else load(Stream{}, t, SPW - 2);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      __builtin_amdgcn_wave_barrier();
+      float y[8], dyn[8];
+      {
+        Vec<XT, 8> rows[8];
+        rows_back(xs, rows);
+        const u32x4 aa[3] = {s_par.aa[0][q], s_par.aa[1][q], s_par.aa[2][q]};
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          y[v] = mfma_split3<XT>(aa, column8<XT>(rows, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f})[0];
+          ss = fmaf(y[v], y[v], ss);
+        }
+      }
+      {
+        Vec<XT, 8> rows[8];
+        rows_back(gs, rows);
+        const u32x4 ap[3] = {s_par.ap[0][q], s_par.ap[1][q], s_par.ap[2][q]};
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          dyn[v] = mfma_split3<XT>(ap, column8<XT>(rows, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f})[0];
+          sr = fmaf(dyn[v] * y[v], wv[v], sr);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        yk[s][k] = pick_pair(y, q, k);
+        dk[s][k] = pick_pair(dyn, q, k);
+        // selected here, not at the uses after the barrier (sunk there, the
+        // selects would keep all eight values of every slab live across it)
+        asm volatile("" : "+v"(yk[s][k]), "+v"(dk[s][k]));
+      }
+      // dM over the slab: A = g rows 16I + r, B = x rows 16J + r, 32 channels per step
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        u32x4 ga[2], xb[2];
+#pragma unroll
+        for (int I = 0; I < 2; ++I) {
+          ga[I] = *reinterpret_cast<const u32x4*>(&gs[(16 * I + r) * kMf32Row + 32 * kk + 8 * q]);
+          xb[I] = *reinterpret_cast<const u32x4*>(&xs[(16 * I + r) * kMf32Row + 32 * kk + 8 * q]);
+        }
+#pragma unroll
+        for (int I = 0; I < 2; ++I)
+#pragma unroll
+          for (int J = 0; J < 2; ++J) dm[I][J] = mfma32k<XT>(ga[I], xb[J], dm[I][J]);
+      }
+    }
+    // the four lane groups q hold the same y and dyn: count them once
+    ss = q == 0 ? ss : 0.0f;
+    sr = q == 0 ? sr : 0.0f;
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    lds_barrier();
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+
+    const auto rdx = rows_rsrc((const XT*)A.out + t * nC, tokb);
+    const int64_t tn = t + gridDim.x < A.T ? t + gridDim.x : t;  // the next token (this one again at the end)
+#pragma unroll
+    for (int s = SPW - 1; s >= 0; --s) {
+      __builtin_amdgcn_sched_barrier(0);
+      float wv[8];
+      if (s == SPW - 1) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) wv[v] = wlast[v];
+      } else {
+        load_w8(A.w + slab0 + s * 128 + 8 * r, wv);
+      }
+      // slab SPW - 1 is still staged; the others are staged from the registers
+      if (s < SPW - 1) {
+        stage();
+        if (s > 0) load(Stream{}, t, s - 1);
+        else load(Cached{}, tn, 0);
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        __builtin_amdgcn_wave_barrier();
+      }
+      const uint32_t sb = slabb + (uint32_t)s * 128 * kEs;
+      // y and dyn of the lane's 8 channels back from the four lane groups
+      float dyv[8], ynv[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int src = 16 * (v >> 1) + r;
+        const float yv = __shfl(yk[s][v & 1], src);
+        const float dn = __shfl(dk[s][v & 1], src);
+        dyv[v] = dn * inv * wv[v] - kf * yv;
+        ynv[v] = (yv * inv) * wv[v];
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k) dwv[s][k] = fmaf(dk[s][k], yk[s][k] * inv, dwv[s][k]);
+      {
+        Vec<XT, 8> rows[8];
+        rows_back(gs, rows);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+          for (int v = 0; v < 8; ++v) dP[e] = fmaf(rows[e].get(v), ynv[v], dP[e]);
+#pragma unroll
+        for (int J = 0; J < 2; ++J) {
+          const u32x4 amt[3] = {s_par.amt[J][0][lane], s_par.amt[J][1][lane], s_par.amt[J][2][lane]};
+          const float4 a4 = s_par.a4[J][q];
+          uint32_t ow[4][4];
+          f32x4 even;
+#pragma unroll
+          for (int v = 0; v < 8; ++v) {
+            f32x4 acc = {a4.x * dyv[v], a4.y * dyv[v], a4.z * dyv[v], a4.w * dyv[v]};
+            acc = mfma_split3<XT>(amt, column8<XT>(rows, v), acc);
+            if (v & 1) {
+#pragma unroll
+              for (int k = 0; k < 4; ++k) ow[k][v >> 1] = pack2<XT>(even[k], acc[k]);
+            } else {
+              even = acc;
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx, lane_dx,
+                                                   sb + (uint32_t)(16 * J + k) * rowb, kBufNt);
+        }
+      }
+      {
+        Vec<XT, 8> rows[8];
+        rows_back(xs, rows);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+          for (int v = 0; v < 8; ++v) dA[e] = fmaf(dyv[v], rows[e].get(v), dA[e]);
+      }
+    }
+  }
+
+  // ---- the workgroup's partial row [dw C | 0 .. Cp | dM n*n | dA n | dP n | 0 .. P]
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+#pragma unroll
+  for (int s = 0; s < SPW; ++s)
+    *reinterpret_cast<float2*>(prow + slab0 + s * 128 + 8 * r + 2 * q) = make_float2(dwv[s][0], dwv[s][1]);
+  if (tid == 0)
+    for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
+  mf32_bwd_param_sums(A, prow, mf32_lds, n, dm, dA, dP);
+}
+
+constexpr int kMf32MaxSpw = 8;      // slabs per wave of the wide backward (C <= 8 waves x 8 x 128)
+constexpr int kMf32PipeMaxSpw = 5;  // and of its pipelined variant (6 and more spill)
+constexpr int kMf32PipeMaxS = 24;   // slabs per token up to which the pipelined variant is used
 
 // f(std::integral_constant<int, spw>) for spw in 2 .. kMf32MaxSpw.
 template <typename F>
@@ -931,13 +1186,14 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   const int S = A.C / 128;
   // one slab per wave up to C = 1024; above it (n == 32 only) SPW = 2 .. 8
   // slabs per wave, with x and g read again after the RMS barrier: the wave
-  // count nearest MHC_MF32_WAVES (default 8) among those that divide S.
-  // Measured (2048 tokens, bf16): C = 3072 on 8 waves 268 us, on 4 (two
-  // workgroups per CU) 284 us; C = 4096 400 against 384 us; C = 2048 355
-  // against 358 us.
+  // count nearest MHC_MF32_WAVES among those that divide S.  Default 8 waves
+  // up to C = 3072 and 4 above (two workgroups per CU).  Measured, 2048 tokens
+  // (4096 at C = 2048), bf16, pipelined / not: C = 2048 on 8 waves 327 / 354
+  // us, on 4 341 us; C = 3072 on 8 waves 252 / 268 us; C = 4096 on 8 waves
+  // 423 / 400 us, on 4 (eight slabs, not pipelined) 383 us.
   int spw = 1;
   if (S > kMf32MaxWaves) {
-    const int target = std::max(1, knob(kKnobMf32Waves, kMf32MaxWaves));
+    const int target = std::max(1, knob(kKnobMf32Waves, S <= kMf32PipeMaxS ? kMf32MaxWaves : 4));
     spw = 0;
     for (int c = 2; c <= kMf32MaxSpw; ++c) {
       if (S % c != 0 || S / c > kMf32MaxWaves) continue;
@@ -951,6 +1207,8 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   const size_t smem = std::max<size_t>((size_t)waves * kMf32Slab * sizeof(uint16_t),
                                        (size_t)waves * kMf32Par * sizeof(float));
   const bool raw = A.h_mode == MHC_H_RAW;
+  // the pipelined kernel up to C = 3072 and kMf32PipeMaxSpw slabs per wave
+  const bool pipe = knob(kKnobBwdPipe, 1) != 0 && spw <= kMf32PipeMaxSpw && S <= kMf32PipeMaxS;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
     const void* kfn = nullptr;
@@ -959,8 +1217,14 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
                  : (raw ? (const void*)mf32_bwd_kernel<XT, true, false> : (const void*)mf32_bwd_kernel<XT, false, false>);
     } else {
       with_spw(spw, [&](auto c) {
-        kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, decltype(c)::value>
-                  : (const void*)mf32_bwd_wide_kernel<XT, false, decltype(c)::value>;
+        constexpr int SPW = decltype(c)::value;
+        if constexpr (SPW <= kMf32PipeMaxSpw) {
+          if (pipe)
+            kfn = raw ? (const void*)mf32_bwd_pipe_kernel<XT, true, SPW>
+                      : (const void*)mf32_bwd_pipe_kernel<XT, false, SPW>;
+        }
+        if (kfn == nullptr)
+          kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, SPW> : (const void*)mf32_bwd_wide_kernel<XT, false, SPW>;
       });
     }
     const int occ = occupancy_blocks(kfn, waves * 64, smem);
@@ -981,8 +1245,18 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     } else {
       with_spw(spw, [&](auto c) {
         constexpr int SPW = decltype(c)::value;
-        if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, SPW>), g, b, smem, s, A);
-        else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, SPW>), g, b, smem, s, A);
+        bool launched = false;
+        if constexpr (SPW <= kMf32PipeMaxSpw) {
+          if (pipe) {
+            if (raw) hipLaunchKernelGGL((mf32_bwd_pipe_kernel<XT, true, SPW>), g, b, smem, s, A);
+            else hipLaunchKernelGGL((mf32_bwd_pipe_kernel<XT, false, SPW>), g, b, smem, s, A);
+            launched = true;
+          }
+        }
+        if (!launched) {
+          if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, SPW>), g, b, smem, s, A);
+          else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, SPW>), g, b, smem, s, A);
+        }
       });
     }
     MHC_CHECK_LAUNCH("mf32_bwd_kernel");

@@ -56,10 +56,10 @@ def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
 
 @pytest.mark.parametrize("T,n,C", [(5, 32, 128), (300, 32, 512), (40, 24, 256), (33, 17, 640), (7, 32, 1024),
                                    (64, 28, 384),
-                                   # n = 32 above C = 1024: 2 .. 8 slabs per wave on 3 to 8 waves (the
-                                   # largest wave count up to 8 that divides C / 128; C = 1408 has none;
-                                   # above C = 4096 the forward runs on the generic kernel); n < 32 there
-                                   # takes the generic kernel
+                                   # n = 32 above C = 1024: 2 .. 8 slabs per wave on 3 to 8 waves, the
+                                   # one-slab-ahead variant up to C = 3072 (C = 1408 has no split; above
+                                   # C = 4096 the forward runs on the generic kernel); n < 32 there takes
+                                   # the generic kernel
                                    (3, 32, 1152), (9, 32, 1536), (2, 32, 1408), (4, 32, 2048), (5, 32, 2560),
                                    (17, 32, 3072), (2, 32, 3584), (3, 32, 4096), (2, 32, 8192), (4, 24, 2048)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
@@ -67,10 +67,14 @@ def test_mfma32_backward_layer_wide(T, n, C, dt, knobs):
     _backward_layer_wide(T, n, C, dt, knobs)
 
 
-@pytest.mark.parametrize("T,C,waves", [(6, 2048, 4), (5, 4096, 4), (4, 3072, 2)])
-def test_mfma32_backward_wave_counts(T, C, waves, knobs):
-    """Other splits of the same shapes (MHC_MF32_WAVES): 4 waves of 4 or 8 slabs, 3 waves of 8."""
-    knobs("MHC_MF32_WAVES", waves)
+@pytest.mark.parametrize("T,C,settings", [(6, 2048, {"MHC_MF32_WAVES": 4}), (5, 4096, {"MHC_MF32_WAVES": 8}),
+                                           (4, 3072, {"MHC_MF32_WAVES": 2}), (6, 2048, {"MHC_BWD_PIPE": 0}),
+                                           (7, 3072, {"MHC_BWD_PIPE": 0})])
+def test_mfma32_backward_other_splits(T, C, settings, knobs):
+    """Other splits of the same shapes: 4 waves of 4 slabs (pipelined), 8 of 4 and 3 of 8 (not pipelined), and
+    the unpipelined kernel at 2 and 3 slabs per wave (MHC_BWD_PIPE = 0)."""
+    for name, value in settings.items():
+        knobs(name, value)
     _backward_layer_wide(T, 32, C, "bf16", knobs)
 
 
