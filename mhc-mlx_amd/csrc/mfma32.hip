@@ -1137,12 +1137,10 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
   const int S = A.C / 128;
   // two slabs per wave up to C = 2048 (in registers across the RMS barrier),
   // four above it (read again after the barrier)
-  // (n == 32 only: with per-stream conditions the four-slab variant spills)
   const int spw = S <= 8 ? 1 : (S <= 16 ? 2 : 4);
   if (S % spw != 0) return 1;
   const int waves = S / spw;
   const bool pt = A.M_ts != 0, raw = A.h_mode == MHC_H_RAW, full = A.n == 32;
-  if (spw == 4 && !full) return 1;
   const int per_cu = knob(kKnobFwdGrid, 8);
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * std::max(per_cu, 1)));
   const dim3 g((unsigned)blocks), b(waves * 64);
@@ -1155,8 +1153,11 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
     if (full) hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, PT_, RAW_, true>), g, b, 0, s, A);  \
     else hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, PT_, RAW_, false>), g, b, 0, s, A);      \
   } while (0)
-#define MF32_FWD_RELOAD(PT_, RAW_) \
-  hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, 4, PT_, RAW_, true, true>), g, b, 0, s, A)
+#define MF32_FWD_RELOAD(PT_, RAW_)                                                                 \
+  do {                                                                                             \
+    if (full) hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, 4, PT_, RAW_, true, true>), g, b, 0, s, A);  \
+    else hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, 4, PT_, RAW_, false, true>), g, b, 0, s, A);      \
+  } while (0)
       if (spw == 1) {
         if (pt) { if (raw) MF32_FWD(1, true, true); else MF32_FWD(1, true, false); }
         else { if (raw) MF32_FWD(1, false, true); else MF32_FWD(1, false, false); }

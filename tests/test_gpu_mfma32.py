@@ -1,6 +1,6 @@
 """GPU parity of the 16 < n <= 32 MFMA kernels (csrc/mfma32.hip) against the float64 oracle.
 
-The forward covers n = 17, 24 and 32, C from one 128-channel slab to 2048 (one and two slabs per wave),
+The forward covers n = 17 to 32, C from one 128-channel slab to 4096 (one, two and four slabs per wave),
 16-bit x with 16-bit or fp32 output, layer-wide and per-token parameters; the backward covers
 layer-wide parameters with 16-bit x and dout up to C = 1024, and at n = 32 up to C = 8192 (2 to 8
 slabs per wave, x and g read again after the RMS barrier).  With the grid knobs at a few
@@ -32,9 +32,8 @@ def _ulp_bound(got, ref, dt):
 
 @pytest.mark.parametrize("T,n,C", [(5, 32, 128), (40, 32, 512), (7, 24, 384), (9, 17, 256), (3, 32, 1024),
                                    (4, 32, 2048), (6, 20, 1280),
-                                   # C above 2048 at n = 32: four slabs per wave, x read again after the
-                                   # RMS barrier; n < 32 there goes to the generic kernel
-                                   (3, 32, 4096), (300, 32, 3072), (2, 24, 4096)])
+                                   # C above 2048: four slabs per wave, x read again after the RMS barrier
+                                   (3, 32, 4096), (300, 32, 3072), (2, 24, 4096), (5, 20, 3072)])
 @pytest.mark.parametrize("xdt,odt", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
 @pytest.mark.parametrize("per_token", [False, True])
 def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
