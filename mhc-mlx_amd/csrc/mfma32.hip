@@ -649,8 +649,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 }
 
 // ---------------------------------------------------------------------------
-// Backward at n = 32 above C = 1024 (layer-wide): SPW = 2 or 4 slabs per
-// wave, up to 8 waves.  A token's slabs do not fit in registers across the
+// Backward for 16 < n <= 32 above C = 1024 (layer-wide): SPW slabs per wave,
+// up to 8 waves.  A token's slabs do not fit in registers across the
 // RMS barrier, so the work splits around it:
 //   before: per slab, y and dyn (MFMA), the two per-token sums and
 //     dM += G X^T over the slab staged in LDS;
@@ -661,8 +661,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 // lane group q across the barrier (the four groups hold the same values);
 // the lane's eight are gathered back from the groups afterwards.  dw of those
 // two channels is kept by the same group.
+// n < 32 (!FULL): a row's offset goes in the lane offset, which the buffer
+// range check covers, so rows beyond n load as zero and their stores are
+// dropped (the resource spans the token's n rows); at n = 32 the row part is
+// a uniform offset.
 // ---------------------------------------------------------------------------
-template <typename XT, bool RAW, int SPW>
+template <typename XT, bool RAW, int SPW, bool FULL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_wide_kernel(Mf32Args A) {
   extern __shared__ __align__(16) uint16_t mf32_lds[];
   __shared__ float s_red[2][2][kMf32MaxWaves];
@@ -672,7 +676,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nwaves = blockDim.x >> 6;
   const int q = lane >> 4, r = lane & 15;
-  constexpr int n = 32;
+  const int n = FULL ? 32 : A.n;
   constexpr uint32_t kEs = sizeof(XT);
   const int C = A.C;
   const int64_t nC = (int64_t)n * C;
@@ -711,8 +715,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
       Vec<XT, 8> xr[8], gr[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        buf_load<0>(xr[e], rx, lane_in, sb + (uint32_t)e * rowb);
-        buf_load<0>(gr[e], rg, lane_in, sb + (uint32_t)e * rowb);
+        buf_load<0>(xr[e], rx, FULL ? lane_in : lane_in + (uint32_t)e * rowb, FULL ? sb + (uint32_t)e * rowb : sb);
+        buf_load<0>(gr[e], rg, FULL ? lane_in : lane_in + (uint32_t)e * rowb, FULL ? sb + (uint32_t)e * rowb : sb);
       }
       float wv[8];
       load_w8(A.w + slab0 + s * 128 + 8 * r, wv);
@@ -787,9 +791,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
       const uint32_t sb = slabb + (uint32_t)s * 128 * kEs;
       Vec<XT, 8> gr[8], xr[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) buf_load<kBufNt>(gr[e], rg, lane_in, sb + (uint32_t)e * rowb);
+      for (int e = 0; e < 8; ++e) buf_load<kBufNt>(gr[e], rg, FULL ? lane_in : lane_in + (uint32_t)e * rowb, FULL ? sb + (uint32_t)e * rowb : sb);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) buf_load<kBufNt>(xr[e], rx, lane_in, sb + (uint32_t)e * rowb);
+      for (int e = 0; e < 8; ++e) buf_load<kBufNt>(xr[e], rx, FULL ? lane_in : lane_in + (uint32_t)e * rowb, FULL ? sb + (uint32_t)e * rowb : sb);
       float wv[8];
       load_w8(A.w + slab0 + s * 128 + 8 * r, wv);
       // y and dyn of the lane's 8 channels back from the four lane groups
@@ -828,8 +832,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx, lane_dx,
-                                                 sb + (uint32_t)(16 * J + k) * rowb, kBufNt);
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx,
+                                                 FULL ? lane_dx : lane_dx + (uint32_t)(16 * J + k) * rowb,
+                                                 FULL ? sb + (uint32_t)(16 * J + k) * rowb : sb, kBufNt);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e)
@@ -858,7 +863,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 // the last step before the barrier, so not read again), then SPW-2 .. 0.
 // The last step loads the next token's first slab, before its dx stores.
 // ---------------------------------------------------------------------------
-template <typename XT, bool RAW, int SPW>
+template <typename XT, bool RAW, int SPW, bool FULL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_pipe_kernel(Mf32Args A) {
   extern __shared__ __align__(16) uint16_t mf32_lds[];
   __shared__ float s_red[2][2][kMf32MaxWaves];
@@ -868,7 +873,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nwaves = blockDim.x >> 6;
   const int q = lane >> 4, r = lane & 15;
-  constexpr int n = 32;
+  const int n = FULL ? 32 : A.n;
   constexpr uint32_t kEs = sizeof(XT);
   const int C = A.C;
   const int64_t nC = (int64_t)n * C;
@@ -904,8 +909,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
     const uint32_t sb = slabb + (uint32_t)s * 128 * kEs;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      buf_load<decltype(aux)::value>(xr[e], rx, lane_in, sb + (uint32_t)e * rowb);
-      buf_load<decltype(aux)::value>(gr[e], rg, lane_in, sb + (uint32_t)e * rowb);
+      buf_load<decltype(aux)::value>(xr[e], rx, FULL ? lane_in : lane_in + (uint32_t)e * rowb, FULL ? sb + (uint32_t)e * rowb : sb);
+      buf_load<decltype(aux)::value>(gr[e], rg, FULL ? lane_in : lane_in + (uint32_t)e * rowb, FULL ? sb + (uint32_t)e * rowb : sb);
     }
   };
   // one LDS row per stream (the previous step's reads of the buffer were
@@ -1076,8 +1081,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
           }
 #pragma unroll
           for (int k = 0; k < 4; ++k)
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx, lane_dx,
-                                                   sb + (uint32_t)(16 * J + k) * rowb, kBufNt);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx,
+                                                   FULL ? lane_dx : lane_dx + (uint32_t)(16 * J + k) * rowb,
+                                                   FULL ? sb + (uint32_t)(16 * J + k) * rowb : sb, kBufNt);
         }
       }
       {
@@ -1118,6 +1124,13 @@ void with_spw(int spw, F&& f) {
     case 8: f(std::integral_constant<int, 8>{}); break;
     default: break;
   }
+}
+
+// f(std::true_type) for n == 32 (no stream beyond n), else f(std::false_type).
+template <typename F>
+void with_full(bool full, F&& f) {
+  if (full) f(std::true_type{});
+  else f(std::false_type{});
 }
 
 template <typename F>
@@ -1192,24 +1205,26 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   // (4096 at C = 2048), bf16, pipelined / not: C = 2048 on 8 waves 327 / 354
   // us, on 4 341 us; C = 3072 on 8 waves 252 / 268 us; C = 4096 on 8 waves
   // 423 / 400 us, on 4 (eight slabs, not pipelined) 383 us.
+  // (n < 32 up to kMf32PipeMaxSpw slabs per wave: the per-row offsets of the
+  // range-checked rows cost registers)
+  const bool full = A.n == 32;
   int spw = 1;
   if (S > kMf32MaxWaves) {
     const int target = std::max(1, knob(kKnobMf32Waves, S <= kMf32PipeMaxS ? kMf32MaxWaves : 4));
+    const int max_spw = full ? kMf32MaxSpw : kMf32PipeMaxSpw;
     spw = 0;
-    for (int c = 2; c <= kMf32MaxSpw; ++c) {
+    for (int c = 2; c <= max_spw; ++c) {
       if (S % c != 0 || S / c > kMf32MaxWaves) continue;
       if (spw == 0 || std::abs(S / c - target) < std::abs(S / spw - target)) spw = c;
     }
     if (spw == 0) return 1;
   }
-  const bool full = A.n == 32;
-  if (spw > 1 && !full) return 1;
   const int waves = S / spw;
   const size_t smem = std::max<size_t>((size_t)waves * kMf32Slab * sizeof(uint16_t),
                                        (size_t)waves * kMf32Par * sizeof(float));
   const bool raw = A.h_mode == MHC_H_RAW;
   // the pipelined kernel up to C = 3072 and kMf32PipeMaxSpw slabs per wave
-  const bool pipe = knob(kKnobBwdPipe, 1) != 0 && spw <= kMf32PipeMaxSpw && S <= kMf32PipeMaxS;
+  const bool pipe = full && knob(kKnobBwdPipe, 1) != 0 && spw <= kMf32PipeMaxSpw && S <= kMf32PipeMaxS;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
     const void* kfn = nullptr;
@@ -1219,13 +1234,19 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     } else {
       with_spw(spw, [&](auto c) {
         constexpr int SPW = decltype(c)::value;
-        if constexpr (SPW <= kMf32PipeMaxSpw) {
-          if (pipe)
-            kfn = raw ? (const void*)mf32_bwd_pipe_kernel<XT, true, SPW>
-                      : (const void*)mf32_bwd_pipe_kernel<XT, false, SPW>;
-        }
-        if (kfn == nullptr)
-          kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, SPW> : (const void*)mf32_bwd_wide_kernel<XT, false, SPW>;
+        with_full(full, [&](auto fc) {
+          constexpr bool F = decltype(fc)::value;
+          if constexpr (F && SPW <= kMf32PipeMaxSpw) {
+            if (pipe)
+              kfn = raw ? (const void*)mf32_bwd_pipe_kernel<XT, true, SPW, F>
+                        : (const void*)mf32_bwd_pipe_kernel<XT, false, SPW, F>;
+          }
+          if constexpr (F || SPW <= kMf32PipeMaxSpw) {
+            if (kfn == nullptr)
+              kfn = raw ? (const void*)mf32_bwd_wide_kernel<XT, true, SPW, F>
+                        : (const void*)mf32_bwd_wide_kernel<XT, false, SPW, F>;
+          }
+        });
       });
     }
     const int occ = occupancy_blocks(kfn, waves * 64, smem);
@@ -1246,18 +1267,23 @@ int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     } else {
       with_spw(spw, [&](auto c) {
         constexpr int SPW = decltype(c)::value;
-        bool launched = false;
-        if constexpr (SPW <= kMf32PipeMaxSpw) {
-          if (pipe) {
-            if (raw) hipLaunchKernelGGL((mf32_bwd_pipe_kernel<XT, true, SPW>), g, b, smem, s, A);
-            else hipLaunchKernelGGL((mf32_bwd_pipe_kernel<XT, false, SPW>), g, b, smem, s, A);
-            launched = true;
+        with_full(full, [&](auto fc) {
+          constexpr bool F = decltype(fc)::value;
+          bool launched = false;
+          if constexpr (F && SPW <= kMf32PipeMaxSpw) {
+            if (pipe) {
+              if (raw) hipLaunchKernelGGL((mf32_bwd_pipe_kernel<XT, true, SPW, F>), g, b, smem, s, A);
+              else hipLaunchKernelGGL((mf32_bwd_pipe_kernel<XT, false, SPW, F>), g, b, smem, s, A);
+              launched = true;
+            }
           }
-        }
-        if (!launched) {
-          if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, SPW>), g, b, smem, s, A);
-          else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, SPW>), g, b, smem, s, A);
-        }
+          if constexpr (F || SPW <= kMf32PipeMaxSpw) {
+            if (!launched) {
+              if (raw) hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, true, SPW, F>), g, b, smem, s, A);
+              else hipLaunchKernelGGL((mf32_bwd_wide_kernel<XT, false, SPW, F>), g, b, smem, s, A);
+            }
+          }
+        });
       });
     }
     MHC_CHECK_LAUNCH("mf32_bwd_kernel");

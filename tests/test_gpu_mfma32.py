@@ -2,8 +2,8 @@
 
 The forward covers n = 17 to 32, C from one 128-channel slab to 4096 (one, two and four slabs per wave),
 16-bit x with 16-bit or fp32 output, layer-wide and per-token parameters; the backward covers
-layer-wide parameters with 16-bit x and dout up to C = 1024, and at n = 32 up to C = 8192 (2 to 8
-slabs per wave, x and g read again after the RMS barrier).  With the grid knobs at a few
+layer-wide parameters with 16-bit x and dout up to C = 1024, and above it up to C = 8192 at n = 32
+(2 to 8 slabs per wave, x and g read again after the RMS barrier) and 5120 below n = 32.  With the grid knobs at a few
 workgroups every workgroup walks many tokens.  Shapes outside these ranges (odd C, fp32 x, fp32
 dout, per-token backward) take the generic kernels and are covered by tests/test_gpu_fused.py.
 """
@@ -57,10 +57,11 @@ def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
                                    (64, 28, 384),
                                    # n = 32 above C = 1024: 2 .. 8 slabs per wave on 3 to 8 waves, the
                                    # one-slab-ahead variant up to C = 3072 (C = 1408 has no split; above
-                                   # C = 4096 the forward runs on the generic kernel); n < 32 there takes
-                                   # the generic kernel
+                                   # C = 4096 the forward runs on the generic kernel); n < 32 there: up to
+                                   # 5 slabs per wave, rows beyond n through the buffer range check
                                    (3, 32, 1152), (9, 32, 1536), (2, 32, 1408), (4, 32, 2048), (5, 32, 2560),
-                                   (17, 32, 3072), (2, 32, 3584), (3, 32, 4096), (2, 32, 8192), (4, 24, 2048)])
+                                   (17, 32, 3072), (2, 32, 3584), (3, 32, 4096), (2, 32, 8192), (4, 24, 2048),
+                                   (11, 20, 3072), (3, 17, 4096), (5, 28, 1536)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_mfma32_backward_layer_wide(T, n, C, dt, knobs):
     _backward_layer_wide(T, n, C, dt, knobs)
