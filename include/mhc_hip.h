@@ -97,18 +97,20 @@ int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlogits, int64
                      void* stream);
 
 /* Recorded state: the forward keeps what the VJP would otherwise recompute
- * (per iteration the cumulative row/column scales and the row/column sums,
- * 256 bytes per matrix).  This splits _sinkhorn_autograd_fn's forward and
- * VJP (metal.py:2712-2758) the way an autograd function saves tensors for
+ * (per iteration the cumulative row/column scales and the row/column sums
+ * or scales: 256 bytes per matrix at n = 16, 6 * next_pow2(n) * 4 bytes for
+ * 16 < n <= 64).  This splits _sinkhorn_autograd_fn's forward and VJP
+ * (metal.py:2712-2758) the way an autograd function saves tensors for
  * backward; the results are those of mhc_sinkhorn_fwd / mhc_sinkhorn_bwd.
  *
  * Bytes of the state buffer for this shape; 0 when no recorded path exists
- * (n != 16, or the knob MHC_SK16 or MHC_SK16_RECORD is 0): then use
- * mhc_sinkhorn_fwd / mhc_sinkhorn_bwd. */
+ * (n < 16, or the knob MHC_SK16 or MHC_SK16_RECORD is 0 at n = 16, or
+ * MHC_SK_BLK_RECORD is 0 for 16 < n <= 64): then use mhc_sinkhorn_fwd /
+ * mhc_sinkhorn_bwd. */
 size_t mhc_sinkhorn_state_bytes(int64_t batch, int n, int iters);
 
 /* mhc_sinkhorn_fwd that also writes the state to `state` (state_bytes >=
- * mhc_sinkhorn_state_bytes; logits and M 16-byte aligned). */
+ * mhc_sinkhorn_state_bytes; at n = 16 logits and M 16-byte aligned). */
 int mhc_sinkhorn_fwd_record(const float* logits, float* M, void* state, size_t state_bytes,
                             int64_t batch, int n, int iters, float eps, void* stream);
 

@@ -322,87 +322,63 @@ MHC_DEV void sk_bwd_group_reg(const float* __restrict__ H, const float* __restri
 }
 
 // ---------------------------------------------------------------------------
-// Block layout: one NP x NP matrix per wavefront, NP in {16, 32, 64}.  Lane
+// Block layout: one NP x NP matrix per wavefront, NP in {32, 64}.  Lane
 // (R = lane >> 3, Q = lane & 7) holds the B x B block (B = NP / 8) at rows
 // R*B .. R*B+B-1 and columns Q*B .. Q*B+B-1.  A row sum adds B values in the
 // lane and then the 8 lanes of R (lane ^ 1, 2, 4: DPP); a column sum adds B
 // values in the lane and then the 8 lanes of Q (lane ^ 8: DPP, lane ^ 16 and
-// ^ 32: ds_bpermute).  Per iteration that is 3B + 3B cross-lane steps,
+// ^ 32: permlane swaps).  Per iteration that is 3B + 3B cross-lane steps,
 // against 5 per element for the one-row-per-lane-pair layout of SkLayout
 // (NP = 32: 24 against 80), which bounds a single matrix's latency.
-// Same semantics and arithmetic per element as sk_fwd_group / sk_bwd_group;
-// only the association of each row or column sum differs.
+// Same semantics and arithmetic per element as sk_fwd_group; only the
+// association of each row or column sum differs.
+//
+// VJP state, per iteration k (6 * NP floats, each entry a multiple of 16
+// bytes from the start of the matrix's state):
+//   [0]   R_k     cumulative row scale after the row step
+//   [1]   C_k-1   cumulative column scale before the column step
+//   [2]   rsc_k   row scale applied (1 for a masked row)
+//   [3]   rf_k    R_k-1 * rsc_k^2 (0 for a masked row)
+//   [4]   csc_k   column scale applied (0 for a masked column)
+//   [5]   cf_k    C_k-1 * csc_k^2 (0 for a masked column)
+// A masked row or column is one past n or whose sum is <= eps.  With these
+// the VJP of iteration k needs no reciprocal and no mask test.
 // ---------------------------------------------------------------------------
 
-template <int NP>
-MHC_DEV void sk_fwd_blk(const float* __restrict__ H, float* __restrict__ out, int n, int iters, float eps,
-                        int lane) {
-  constexpr int B = NP / 8;
-  const int r0 = (lane >> 3) * B, c0 = (lane & 7) * B;
-  float P[B][B];
-#pragma unroll
-  for (int a = 0; a < B; ++a) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const bool v = r0 + a < n && c0 + b < n;
-      P[a][b] = v ? H[(r0 + a) * n + c0 + b] : -INFINITY;
-      mx = fmaxf(mx, P[a][b]);
-    }
-    mx = group_max<8>(mx);
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const bool v = r0 + a < n && c0 + b < n;
-      P[a][b] = v ? expf(P[a][b] - mx) : 0.0f;
-    }
-  }
-  for (int it = 0; it < iters; ++it) {
-#pragma unroll
-    for (int a = 0; a < B; ++a) {
-      float s = 0.0f;
-#pragma unroll
-      for (int b = 0; b < B; ++b) s += P[a][b];
-      s = group_sum<8>(s);
-      const float rsc = (r0 + a < n && s > eps) ? sk_rcp(s) : 1.0f;
-#pragma unroll
-      for (int b = 0; b < B; ++b) P[a][b] *= rsc;
-    }
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      float cs = 0.0f;
-#pragma unroll
-      for (int a = 0; a < B; ++a) cs += P[a][b];
-      cs = strided_sum<8, 64>(cs);
-      const float csc = (c0 + b < n && cs > eps) ? sk_rcp(cs) : 0.0f;
-#pragma unroll
-      for (int a = 0; a < B; ++a) P[a][b] *= csc;
-    }
-  }
-#pragma unroll
-  for (int a = 0; a < B; ++a)
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-      if (r0 + a < n && c0 + b < n) out[(r0 + a) * n + c0 + b] = P[a][b];
-}
+constexpr int kSkBlkStateVecs = 6;
 
-// Floats of VJP state per matrix in the block layout: per iteration the row
-// sums, cumulative row scales, column sums and cumulative column scales.
 __host__ __device__ inline int64_t sk_blk_state_floats(int np, int iters) {
-  return (int64_t)4 * np * (iters > 0 ? iters : 1);
+  return (int64_t)kSkBlkStateVecs * np * (iters > 0 ? iters : 1);
 }
 
-// VJP of sk_fwd_blk: dH = d/dH <dM, SK(H)>.  st: this wavefront's state,
-// [iters][rs | R | cs | C][NP] (LDS or global memory); every lane writes the
-// entries of its rows and columns (the lanes sharing a row or column write
-// the same value) and reads back only its own.
-template <int NP>
-MHC_DEV void sk_bwd_blk(const float* __restrict__ H, const float* __restrict__ dM, float* __restrict__ dH, int n,
-                        int iters, float eps, float* st, int lane) {
+// B contiguous floats of a 16-byte aligned state row.
+template <int B>
+MHC_DEV void sk_blk_st_store(float* p, const float (&v)[B]) {
+#pragma unroll
+  for (int i = 0; i < B; i += 4)
+    *reinterpret_cast<float4*>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+}
+
+template <int B>
+MHC_DEV void sk_blk_st_load(const float* p, float (&v)[B]) {
+#pragma unroll
+  for (int i = 0; i < B; i += 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p + i);
+    v[i] = t.x;
+    v[i + 1] = t.y;
+    v[i + 2] = t.z;
+    v[i + 3] = t.w;
+  }
+}
+
+// exp(H - rowmax) of the lane's block (0 outside the matrix); with TIE, also
+// the mask of elements at their row's maximum (bit a*B+b).  Reads are
+// in-bounds for every lane (index 0 for padding elements), then selected.
+template <int NP, bool TIE>
+MHC_DEV uint64_t sk_blk_load_exp(const float* __restrict__ H, int n, int lane, float (&K)[NP / 8][NP / 8]) {
   constexpr int B = NP / 8;
-  static_assert(B * B <= 64, "tie mask holds one bit per element");
   const int r0 = (lane >> 3) * B, c0 = (lane & 7) * B;
-  float K[B][B], Gd[B][B];
-  uint64_t tie = 0;  // bit a*B+b: H at the row maximum
+  uint64_t tie = 0;
 #pragma unroll
   for (int a = 0; a < B; ++a) {
     float hv[B];
@@ -410,7 +386,8 @@ MHC_DEV void sk_bwd_blk(const float* __restrict__ H, const float* __restrict__ d
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       const bool v = r0 + a < n && c0 + b < n;
-      hv[b] = v ? H[(r0 + a) * n + c0 + b] : -INFINITY;
+      const float h = H[v ? (r0 + a) * n + c0 + b : 0];
+      hv[b] = v ? h : -INFINITY;
       mx = fmaxf(mx, hv[b]);
     }
     mx = group_max<8>(mx);
@@ -418,93 +395,176 @@ MHC_DEV void sk_bwd_blk(const float* __restrict__ H, const float* __restrict__ d
     for (int b = 0; b < B; ++b) {
       const bool v = r0 + a < n && c0 + b < n;
       K[a][b] = v ? expf(hv[b] - mx) : 0.0f;
-      if (v && hv[b] == mx) tie |= (uint64_t)1 << (a * B + b);
-      Gd[a][b] = K[a][b];  // the forward's P
+      if (TIE && v && hv[b] == mx) tie |= (uint64_t)1 << (a * B + b);
     }
   }
-  // forward recompute, recording sums and cumulative scales
+  return tie;
+}
+
+// `iters` Sinkhorn iterations on the lane's block P.  With REC, iteration k's
+// state goes to st + k * 6 * NP (16-byte aligned).  Every lane writes the
+// entries of its own rows and columns (the lanes sharing a row or column
+// write the same values), so a lane that reads the state back reads only
+// what it wrote itself.
+template <int NP, bool REC>
+MHC_DEV void sk_blk_iterate(float (&P)[NP / 8][NP / 8], int n, int iters, float eps, int lane, float* st) {
+  constexpr int B = NP / 8;
+  const int r0 = (lane >> 3) * B, c0 = (lane & 7) * B;
   float Rc[B], Cc[B];
 #pragma unroll
   for (int a = 0; a < B; ++a) Rc[a] = Cc[a] = 1.0f;
   for (int it = 0; it < iters; ++it) {
-    float* sti = st + (int64_t)it * 4 * NP;
+    float rsc[B], rf[B], csc[B], cf[B], Cp[B];
 #pragma unroll
     for (int a = 0; a < B; ++a) {
-      float s = 0.0f;
+      float s = P[a][0];
 #pragma unroll
-      for (int b = 0; b < B; ++b) s += Gd[a][b];
+      for (int b = 1; b < B; ++b) s += P[a][b];
       s = group_sum<8>(s);
-      const float rsc = (r0 + a < n && s > eps) ? sk_rcp(s) : 1.0f;
+      const bool ok = r0 + a < n && s > eps;
+      rsc[a] = ok ? sk_rcp(s) : 1.0f;
 #pragma unroll
-      for (int b = 0; b < B; ++b) Gd[a][b] *= rsc;
-      Rc[a] *= rsc;
-      sti[r0 + a] = s;
-      sti[NP + r0 + a] = Rc[a];
+      for (int b = 0; b < B; ++b) P[a][b] *= rsc[a];
+      if (REC) {
+        rf[a] = ok ? Rc[a] * rsc[a] * rsc[a] : 0.0f;
+        Rc[a] *= rsc[a];
+      }
     }
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      float cs = 0.0f;
+      float cs = P[0][b];
 #pragma unroll
-      for (int a = 0; a < B; ++a) cs += Gd[a][b];
+      for (int a = 1; a < B; ++a) cs += P[a][b];
       cs = strided_sum<8, 64>(cs);
-      const float csc = (c0 + b < n && cs > eps) ? sk_rcp(cs) : 0.0f;
+      const bool ok = c0 + b < n && cs > eps;
+      csc[b] = ok ? sk_rcp(cs) : 0.0f;
 #pragma unroll
-      for (int a = 0; a < B; ++a) Gd[a][b] *= csc;
-      Cc[b] *= csc;
-      sti[2 * NP + c0 + b] = cs;
-      sti[3 * NP + c0 + b] = Cc[b];
+      for (int a = 0; a < B; ++a) P[a][b] *= csc[b];
+      if (REC) {
+        Cp[b] = Cc[b];
+        cf[b] = ok ? Cc[b] * csc[b] * csc[b] : 0.0f;
+        Cc[b] *= csc[b];
+      }
+    }
+    if (REC) {
+      float* sti = st + (int64_t)it * kSkBlkStateVecs * NP;
+      sk_blk_st_store<B>(sti + r0, Rc);
+      sk_blk_st_store<B>(sti + NP + c0, Cp);
+      sk_blk_st_store<B>(sti + 2 * NP + r0, rsc);
+      sk_blk_st_store<B>(sti + 3 * NP + r0, rf);
+      sk_blk_st_store<B>(sti + 4 * NP + c0, csc);
+      sk_blk_st_store<B>(sti + 5 * NP + c0, cf);
     }
   }
-  // reverse sweep
+}
+
+// Forward of one matrix; with REC the VJP state also goes to st.
+template <int NP, bool REC>
+MHC_DEV void sk_fwd_blk(const float* __restrict__ H, float* __restrict__ out, int n, int iters, float eps,
+                        int lane, float* st) {
+  constexpr int B = NP / 8;
+  const int r0 = (lane >> 3) * B, c0 = (lane & 7) * B;
+  float P[B][B];
+  sk_blk_load_exp<NP, false>(H, n, lane, P);
+  sk_blk_iterate<NP, REC>(P, n, iters, eps, lane, st);
+#pragma unroll
+  for (int a = 0; a < B; ++a)
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+      if (r0 + a < n && c0 + b < n) out[(r0 + a) * n + c0 + b] = P[a][b];
+}
+
+// One reverse-sweep iteration's state for this lane's rows and columns.
+template <int B>
+struct SkBlkRev {
+  float Rk[B], Cp[B], rsc[B], rf[B], csc[B], cf[B];
+};
+
+template <int NP, int B>
+MHC_DEV void sk_blk_rev_load(const float* st, int it, int r0, int c0, SkBlkRev<B>& s) {
+  const float* sti = st + (int64_t)it * kSkBlkStateVecs * NP;
+  sk_blk_st_load<B>(sti + r0, s.Rk);
+  sk_blk_st_load<B>(sti + NP + c0, s.Cp);
+  sk_blk_st_load<B>(sti + 2 * NP + r0, s.rsc);
+  sk_blk_st_load<B>(sti + 3 * NP + r0, s.rf);
+  sk_blk_st_load<B>(sti + 4 * NP + c0, s.csc);
+  sk_blk_st_load<B>(sti + 5 * NP + c0, s.cf);
+}
+
+// VJP of one Sinkhorn iteration (column step, then row step) on the lane's
+// block Gd.  Column step, input R_k K C_k-1:
+//   Gd = csc Gd - cf * sum_rows(Gd K R_k);
+// row step, input R_k-1 K C_k-1:
+//   Gd = rsc Gd - rf * sum_cols(Gd K C_k-1).
+template <int B>
+MHC_DEV void sk_blk_rev_step(float (&Gd)[B][B], const float (&K)[B][B], const SkBlkRev<B>& s) {
+  float GK[B][B];
+#pragma unroll
+  for (int a = 0; a < B; ++a)
+#pragma unroll
+    for (int b = 0; b < B; ++b) GK[a][b] = Gd[a][b] * K[a][b];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    float dot = GK[0][b] * s.Rk[0];
+#pragma unroll
+    for (int a = 1; a < B; ++a) dot += GK[a][b] * s.Rk[a];
+    const float sub = strided_sum<8, 64>(dot) * s.cf[b];
+#pragma unroll
+    for (int a = 0; a < B; ++a) Gd[a][b] = s.csc[b] * Gd[a][b] - sub;
+  }
+#pragma unroll
+  for (int a = 0; a < B; ++a) {
+    float KC[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) KC[b] = K[a][b] * s.Cp[b];
+    float dot = Gd[a][0] * KC[0];
+#pragma unroll
+    for (int b = 1; b < B; ++b) dot += Gd[a][b] * KC[b];
+    const float sub = group_sum<8>(dot) * s.rf[a];
+#pragma unroll
+    for (int b = 0; b < B; ++b) Gd[a][b] = s.rsc[a] * Gd[a][b] - sub;
+  }
+}
+
+// VJP of sk_fwd_blk: dH = d/dH <dM, SK(H)>.  st holds the matrix's state
+// (recorded by the forward, or written here first when RECOMPUTE).  The
+// reverse sweep reads each iteration's state one iteration ahead, into two
+// alternating sets, so the reads are in flight during the previous
+// iteration's arithmetic.
+template <int NP, bool RECOMPUTE>
+MHC_DEV void sk_bwd_blk(const float* __restrict__ H, const float* __restrict__ dM, float* __restrict__ dH, int n,
+                        int iters, float eps, float* st, int lane) {
+  constexpr int B = NP / 8;
+  static_assert(B * B <= 64, "tie mask holds one bit per element");
+  const int r0 = (lane >> 3) * B, c0 = (lane & 7) * B;
+  float K[B][B], Gd[B][B];
+  const uint64_t tie = sk_blk_load_exp<NP, true>(H, n, lane, K);  // bit a*B+b: H at the row maximum
+  if (RECOMPUTE) {
+#pragma unroll
+    for (int a = 0; a < B; ++a)
+#pragma unroll
+      for (int b = 0; b < B; ++b) Gd[a][b] = K[a][b];
+    sk_blk_iterate<NP, true>(Gd, n, iters, eps, lane, st);
+  }
 #pragma unroll
   for (int a = 0; a < B; ++a)
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       const bool v = r0 + a < n && c0 + b < n;
-      Gd[a][b] = v ? dM[(r0 + a) * n + c0 + b] : 0.0f;
+      const float g = dM[v ? (r0 + a) * n + c0 + b : 0];
+      Gd[a][b] = v ? g : 0.0f;
     }
-  for (int it = iters - 1; it >= 0; --it) {
-    const float* sti = st + (int64_t)it * 4 * NP;
-    const float* stp = st + (int64_t)(it > 0 ? it - 1 : 0) * 4 * NP;
-    float Rk[B], Rp[B], Cp[B];
-#pragma unroll
-    for (int a = 0; a < B; ++a) {
-      Rk[a] = sti[NP + r0 + a];
-      Rp[a] = it > 0 ? stp[NP + r0 + a] : 1.0f;
+  if (iters > 0) {
+    SkBlkRev<B> sa, sb;
+    sk_blk_rev_load<NP>(st, iters - 1, r0, c0, sa);
+    int it = iters - 1;
+    for (; it >= 1; it -= 2) {
+      sk_blk_rev_load<NP>(st, it - 1, r0, c0, sb);
+      sk_blk_rev_step<B>(Gd, K, sa);
+      sk_blk_rev_load<NP>(st, it >= 2 ? it - 2 : 0, r0, c0, sa);
+      sk_blk_rev_step<B>(Gd, K, sb);
     }
-#pragma unroll
-    for (int b = 0; b < B; ++b) Cp[b] = it > 0 ? stp[3 * NP + c0 + b] : 1.0f;
-    // column step: input R_k K C_{k-1}
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      float dot = 0.0f;
-#pragma unroll
-      for (int a = 0; a < B; ++a) dot += Gd[a][b] * (Rk[a] * K[a][b] * Cp[b]);
-      dot = strided_sum<8, 64>(dot);
-      const float cs = sti[2 * NP + c0 + b];
-      if (c0 + b < n && cs > eps) {
-        const float sc = sk_rcp(cs);
-#pragma unroll
-        for (int a = 0; a < B; ++a) Gd[a][b] = sc * Gd[a][b] - sc * sc * dot;
-      } else {
-#pragma unroll
-        for (int a = 0; a < B; ++a) Gd[a][b] = 0.0f;
-      }
-    }
-    // row step: input R_{k-1} K C_{k-1}
-#pragma unroll
-    for (int a = 0; a < B; ++a) {
-      float dot = 0.0f;
-#pragma unroll
-      for (int b = 0; b < B; ++b) dot += Gd[a][b] * (Rp[a] * K[a][b] * Cp[b]);
-      dot = group_sum<8>(dot);
-      const float rs = sti[r0 + a];
-      if (r0 + a < n && rs > eps) {
-        const float sc = sk_rcp(rs);
-#pragma unroll
-        for (int b = 0; b < B; ++b) Gd[a][b] = sc * Gd[a][b] - sc * sc * dot;
-      }
-    }
+    if (it == 0) sk_blk_rev_step<B>(Gd, K, sa);
   }
   // through exp and the row-max shift (the gradient of the max split evenly
   // among tied maxima; it is zero in exact arithmetic)

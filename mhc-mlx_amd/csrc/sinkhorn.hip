@@ -69,32 +69,66 @@ __global__ __launch_bounds__(kSkThreads) void sinkhorn_bwd_kernel(
 
 // One matrix per wavefront in the block layout (mhc_sinkhorn.hpp), for
 // 16 < n <= 64: a single layer-wide matrix is latency-bound, and this layout
-// needs a third of the cross-lane steps per iteration.
-template <int NP>
+// needs a third of the cross-lane steps per iteration.  With REC the forward
+// also writes each matrix's VJP state to `rec` (sk_blk_state_floats per
+// matrix, 16-byte aligned).
+template <int NP, bool REC>
 __global__ __launch_bounds__(kSkThreads) void sinkhorn_blk_fwd_kernel(const float* __restrict__ logits,
                                                                       float* __restrict__ out, int64_t batch,
-                                                                      int n, int iters, float eps) {
+                                                                      int n, int iters, float eps,
+                                                                      float* __restrict__ rec) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wpb = blockDim.x >> 6;
   const int64_t nn = (int64_t)n * n;
+  const int64_t per_matrix = sk_blk_state_floats(NP, iters);
   for (int64_t m = (int64_t)blockIdx.x * wpb + wave; m < batch; m += (int64_t)gridDim.x * wpb)
-    sk_fwd_blk<NP>(logits + m * nn, out + m * nn, n, iters, eps, lane);
+    sk_fwd_blk<NP, REC>(logits + m * nn, out + m * nn, n, iters, eps, lane, REC ? rec + m * per_matrix : nullptr);
 }
 
-template <int NP, bool GLOBAL_STATE>
+// Where the block-layout VJP finds its state.
+enum SkBlkState : int {
+  kSkBlkLds = 0,        // recomputed into the wave's LDS
+  kSkBlkWs = 1,         // recomputed into the wave's slice of the workspace
+  kSkBlkRecLds = 2,     // recorded by the forward, copied to the wave's LDS first
+  kSkBlkRecGlobal = 3,  // recorded by the forward, read where it lies
+};
+
+template <int NP, int STATE>
 __global__ __launch_bounds__(kSkThreads) void sinkhorn_blk_bwd_kernel(
     const float* __restrict__ logits, const float* __restrict__ dM, float* __restrict__ dlogits, int64_t batch,
     int n, int iters, float eps, float* __restrict__ gstate) {
-  extern __shared__ float sk_smem[];
+  extern __shared__ float4 sk_smem4[];
+  float* sk_smem = reinterpret_cast<float*>(sk_smem4);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wpb = blockDim.x >> 6;
   const int64_t nn = (int64_t)n * n;
   const int64_t per_wave = sk_blk_state_floats(NP, iters);
-  float* st = GLOBAL_STATE ? gstate + ((int64_t)blockIdx.x * wpb + wave) * per_wave : sk_smem + wave * per_wave;
-  for (int64_t m = (int64_t)blockIdx.x * wpb + wave; m < batch; m += (int64_t)gridDim.x * wpb)
-    sk_bwd_blk<NP>(logits + m * nn, dM + m * nn, dlogits + m * nn, n, iters, eps, st, lane);
+  float* const lds = sk_smem + wave * per_wave;
+  for (int64_t m = (int64_t)blockIdx.x * wpb + wave; m < batch; m += (int64_t)gridDim.x * wpb) {
+    float* st;
+    if constexpr (STATE == kSkBlkLds) {
+      st = lds;
+    } else if constexpr (STATE == kSkBlkWs) {
+      st = gstate + ((int64_t)blockIdx.x * wpb + wave) * per_wave;
+    } else if constexpr (STATE == kSkBlkRecLds) {
+      // the matrix's record, 16 bytes per lane and step, read out before any
+      // of it is written (no lane reads what another lane has yet to copy)
+      const float4* src = reinterpret_cast<const float4*>(gstate + m * per_wave);
+      float4* dst = reinterpret_cast<float4*>(lds);
+      const int64_t n4 = per_wave / 4;
+      for (int64_t i = lane; i < n4; i += 64) dst[i] = src[i];
+      // every lane's LDS writes complete before any lane reads the state
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
+      st = lds;
+    } else {
+      st = gstate + m * per_wave;
+    }
+    sk_bwd_blk<NP, STATE == kSkBlkLds || STATE == kSkBlkWs>(logits + m * nn, dM + m * nn, dlogits + m * nn, n,
+                                                            iters, eps, st, lane);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -477,38 +511,60 @@ SkPlan plan_bwd(int64_t batch, int n, int iters, int cus) {
 }
 
 // Block-layout kernels (16 < n <= 64): one wave per matrix, VJP state in
-// LDS when it fits the budget, else in the workspace.
+// LDS when one wave's fits the budget (as many waves per block as fit, up to
+// 4), else in the workspace (which then starts at its first 256-byte
+// boundary, hence 256 bytes more).
 SkPlan plan_blk(int64_t batch, int n, int iters, int cus) {
   SkPlan p{};
   p.np = next_pow2(n);
-  p.wpb = (int)std::min<int64_t>(kSkThreads / 64, batch);
-  if (p.wpb < 1) p.wpb = 1;
-  p.blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(batch, p.wpb), (int64_t)cus * 16));
   const size_t per_wave = (size_t)sk_blk_state_floats(p.np, iters) * sizeof(float);
-  p.global_state = per_wave * (size_t)p.wpb > (size_t)kSkLdsBudget;
+  const int64_t fit = (int64_t)(kSkLdsBudget / per_wave);
+  p.global_state = fit < 1;
+  p.wpb = (int)std::max<int64_t>(1, std::min<int64_t>({kSkThreads / 64, batch, p.global_state ? 4 : fit}));
+  p.blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(batch, p.wpb), (int64_t)cus * 16));
   p.lds_bytes = p.global_state ? 0 : per_wave * (size_t)p.wpb;
-  p.ws_bytes = p.global_state ? per_wave * (size_t)p.wpb * (size_t)p.blocks : 0;
+  p.ws_bytes = p.global_state ? per_wave * (size_t)p.wpb * (size_t)p.blocks + 256 : 0;
   return p;
 }
 
 bool use_blk(int n) { return n > 16; }
 
-template <int NP>
-void launch_blk_fwd(const SkPlan& p, const float* logits, float* M, int64_t batch, int n, int iters, float eps,
-                    hipStream_t s) {
-  hipLaunchKernelGGL(sinkhorn_blk_fwd_kernel<NP>, dim3((unsigned)p.blocks), dim3(p.wpb * 64), 0, s, logits, M,
-                     batch, n, iters, eps);
+// The first 256-byte boundary at or after p.
+template <typename T>
+T* align256(void* p) {
+  const uintptr_t b = reinterpret_cast<uintptr_t>(p);
+  return reinterpret_cast<T*>(b + (256 - b % 256) % 256);
 }
 
 template <int NP>
-void launch_blk_bwd(const SkPlan& p, const float* logits, const float* dM, float* dlogits, int64_t batch, int n,
-                    int iters, float eps, float* ws, hipStream_t s) {
-  if (p.global_state)
-    hipLaunchKernelGGL((sinkhorn_blk_bwd_kernel<NP, true>), dim3((unsigned)p.blocks), dim3(p.wpb * 64), 0, s,
-                       logits, dM, dlogits, batch, n, iters, eps, ws);
+void launch_blk_fwd(const SkPlan& p, const float* logits, float* M, int64_t batch, int n, int iters, float eps,
+                    float* rec, hipStream_t s) {
+  if (rec != nullptr)
+    hipLaunchKernelGGL((sinkhorn_blk_fwd_kernel<NP, true>), dim3((unsigned)p.blocks), dim3(p.wpb * 64), 0, s,
+                       logits, M, batch, n, iters, eps, rec);
   else
-    hipLaunchKernelGGL((sinkhorn_blk_bwd_kernel<NP, false>), dim3((unsigned)p.blocks), dim3(p.wpb * 64),
-                       p.lds_bytes, s, logits, dM, dlogits, batch, n, iters, eps, ws);
+    hipLaunchKernelGGL((sinkhorn_blk_fwd_kernel<NP, false>), dim3((unsigned)p.blocks), dim3(p.wpb * 64), 0, s,
+                       logits, M, batch, n, iters, eps, nullptr);
+}
+
+// rec: the forward's recorded state (16-byte aligned), or nullptr to
+// recompute it (in LDS, or in ws when the plan says so).
+template <int NP>
+void launch_blk_bwd(const SkPlan& p, const float* logits, const float* dM, float* dlogits, int64_t batch, int n,
+                    int iters, float eps, float* ws, float* rec, hipStream_t s) {
+  const dim3 g((unsigned)p.blocks), b(p.wpb * 64);
+  if (rec != nullptr && !p.global_state)
+    hipLaunchKernelGGL((sinkhorn_blk_bwd_kernel<NP, kSkBlkRecLds>), g, b, p.lds_bytes, s, logits, dM, dlogits,
+                       batch, n, iters, eps, rec);
+  else if (rec != nullptr)
+    hipLaunchKernelGGL((sinkhorn_blk_bwd_kernel<NP, kSkBlkRecGlobal>), g, b, 0, s, logits, dM, dlogits, batch, n,
+                       iters, eps, rec);
+  else if (p.global_state)
+    hipLaunchKernelGGL((sinkhorn_blk_bwd_kernel<NP, kSkBlkWs>), g, b, 0, s, logits, dM, dlogits, batch, n, iters,
+                       eps, align256<float>(ws));
+  else
+    hipLaunchKernelGGL((sinkhorn_blk_bwd_kernel<NP, kSkBlkLds>), g, b, p.lds_bytes, s, logits, dM, dlogits, batch,
+                       n, iters, eps, nullptr);
 }
 
 template <int NP>
@@ -561,8 +617,8 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
   }
   if (use_blk(n)) {
     const SkPlan p = plan_blk(batch, n, iters, cus);
-    if (p.np == 32) launch_blk_fwd<32>(p, logits, M, batch, n, iters, eps, s);
-    else launch_blk_fwd<64>(p, logits, M, batch, n, iters, eps, s);
+    if (p.np == 32) launch_blk_fwd<32>(p, logits, M, batch, n, iters, eps, nullptr, s);
+    else launch_blk_fwd<64>(p, logits, M, batch, n, iters, eps, nullptr, s);
     MHC_CHECK_LAUNCH("sinkhorn_blk_fwd_kernel");
     return MHC_OK;
   }
@@ -629,8 +685,8 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
     const SkPlan p = plan_blk(batch, n, iters, device_cu_count());
     MHC_CHECK_ARG(workspace_bytes >= p.ws_bytes && (p.ws_bytes == 0 || workspace != nullptr),
                   "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, p.ws_bytes);
-    if (p.np == 32) launch_blk_bwd<32>(p, logits, dM, dlogits, batch, n, iters, eps, (float*)workspace, s);
-    else launch_blk_bwd<64>(p, logits, dM, dlogits, batch, n, iters, eps, (float*)workspace, s);
+    if (p.np == 32) launch_blk_bwd<32>(p, logits, dM, dlogits, batch, n, iters, eps, (float*)workspace, nullptr, s);
+    else launch_blk_bwd<64>(p, logits, dM, dlogits, batch, n, iters, eps, (float*)workspace, nullptr, s);
     MHC_CHECK_LAUNCH("sinkhorn_blk_bwd_kernel");
     return MHC_OK;
   }
@@ -657,34 +713,52 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
 // ---------------------------------------------------------------------------
 
 namespace {
+// Bytes of recorded state per layout: n == 16 (batched kernels) and
+// 16 < n <= 64 (block layout, MHC_SK_BLK_RECORD=0 turns its recording off).
+size_t sk_record_bytes(int64_t batch, int n, int iters) {
+  if (n == 16) return sk16_state_bytes(batch, iters);
+  return (size_t)batch * (size_t)sk_blk_state_floats(next_pow2(n), iters) * sizeof(float);
+}
+
 // The state starts at the first 256-byte boundary of the caller's buffer
 // (the same offset for the forward that writes it and the VJP that reads it).
-float* sk16_state_ptr(const void* state, size_t state_bytes, int64_t batch, int iters) {
+float* sk_state_ptr(const void* state, size_t state_bytes, int64_t batch, int n, int iters) {
   const uintptr_t base = reinterpret_cast<uintptr_t>(state);
   const size_t pad = (size_t)((256 - base % 256) % 256);
-  if (state == nullptr || state_bytes < sk16_state_bytes(batch, iters) + pad) return nullptr;
+  if (state == nullptr || state_bytes < sk_record_bytes(batch, n, iters) + pad) return nullptr;
   return reinterpret_cast<float*>(base + pad);
 }
 }  // namespace
 
 extern "C" size_t mhc_sinkhorn_state_bytes(int64_t batch, int n, int iters) {
-  if (n != 16 || batch <= 0 || iters < 0 || knob(kKnobSk16, 1) == 0 || knob(kKnobSk16Record, 1) == 0) return 0;
-  return sk16_state_bytes(batch, iters) + 256;
+  if (batch <= 0 || iters < 0) return 0;
+  if (n == 16 && (knob(kKnobSk16, 1) == 0 || knob(kKnobSk16Record, 1) == 0)) return 0;
+  if (n > 16 && n <= MHC_MAX_N && knob(kKnobSkBlkRecord, 1) == 0) return 0;
+  if (n < 16 || n > MHC_MAX_N) return 0;
+  return sk_record_bytes(batch, n, iters) + 256;
 }
 
 extern "C" int mhc_sinkhorn_fwd_record(const float* logits, float* M, void* state, size_t state_bytes,
                                        int64_t batch, int n, int iters, float eps, void* stream) {
   clear_error();
-  MHC_CHECK_ARG(n == 16, "a recorded Sinkhorn state exists for n == 16 only (n=%d)", n);
+  MHC_CHECK_ARG(n >= 16 && n <= MHC_MAX_N, "a recorded Sinkhorn state exists for 16 <= n <= %d only (n=%d)",
+                MHC_MAX_N, n);
   MHC_CHECK_ARG(batch >= 0, "batch=%lld must be >= 0", (long long)batch);
   MHC_CHECK_ARG(iters >= 0, "iters=%d must be >= 0", iters);
   if (batch == 0) return MHC_OK;
   MHC_CHECK_ARG(logits != nullptr && M != nullptr, "null pointer argument");
-  MHC_CHECK_ARG(aligned(logits, 16) && aligned(M, 16), "logits and M must be 16-byte aligned");
-  float* st = sk16_state_ptr(state, state_bytes, batch, iters);
+  MHC_CHECK_ARG(n != 16 || (aligned(logits, 16) && aligned(M, 16)), "logits and M must be 16-byte aligned");
+  float* st = sk_state_ptr(state, state_bytes, batch, n, iters);
   MHC_CHECK_ARG(st != nullptr, "state of %zu bytes is smaller than the %zu bytes required", state_bytes,
-                sk16_state_bytes(batch, iters) + 256);
+                sk_record_bytes(batch, n, iters) + 256);
   hipStream_t s = (hipStream_t)stream;
+  if (n > 16) {
+    const SkPlan p = plan_blk(batch, n, iters, device_cu_count());
+    if (p.np == 32) launch_blk_fwd<32>(p, logits, M, batch, n, iters, eps, st, s);
+    else launch_blk_fwd<64>(p, logits, M, batch, n, iters, eps, st, s);
+    MHC_CHECK_LAUNCH("sinkhorn_blk_fwd_kernel");
+    return MHC_OK;
+  }
   const int cpl = sk16_cpl();
   const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
   if (cpl == 4)
@@ -699,17 +773,25 @@ extern "C" int mhc_sinkhorn_bwd_recorded(const float* logits, const float* dM, f
                                          size_t state_bytes, int64_t batch, int n, int iters, float eps,
                                          void* stream) {
   clear_error();
-  MHC_CHECK_ARG(n == 16, "a recorded Sinkhorn state exists for n == 16 only (n=%d)", n);
+  MHC_CHECK_ARG(n >= 16 && n <= MHC_MAX_N, "a recorded Sinkhorn state exists for 16 <= n <= %d only (n=%d)",
+                MHC_MAX_N, n);
   MHC_CHECK_ARG(batch >= 0, "batch=%lld must be >= 0", (long long)batch);
   MHC_CHECK_ARG(iters >= 0, "iters=%d must be >= 0", iters);
   if (batch == 0) return MHC_OK;
   MHC_CHECK_ARG(logits != nullptr && dM != nullptr && dlogits != nullptr, "null pointer argument");
-  MHC_CHECK_ARG(aligned(logits, 16) && aligned(dM, 16) && aligned(dlogits, 16),
+  MHC_CHECK_ARG(n != 16 || (aligned(logits, 16) && aligned(dM, 16) && aligned(dlogits, 16)),
                 "logits, dM and dlogits must be 16-byte aligned");
-  float* st = sk16_state_ptr(state, state_bytes, batch, iters);
+  float* st = sk_state_ptr(state, state_bytes, batch, n, iters);
   MHC_CHECK_ARG(st != nullptr, "state of %zu bytes is smaller than the %zu bytes required", state_bytes,
-                sk16_state_bytes(batch, iters) + 256);
+                sk_record_bytes(batch, n, iters) + 256);
   hipStream_t s = (hipStream_t)stream;
+  if (n > 16) {
+    const SkPlan p = plan_blk(batch, n, iters, device_cu_count());
+    if (p.np == 32) launch_blk_bwd<32>(p, logits, dM, dlogits, batch, n, iters, eps, nullptr, st, s);
+    else launch_blk_bwd<64>(p, logits, dM, dlogits, batch, n, iters, eps, nullptr, st, s);
+    MHC_CHECK_LAUNCH("sinkhorn_blk_bwd_kernel");
+    return MHC_OK;
+  }
   const int cpl = sk16_cpl();
   const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
   if (cpl == 4)

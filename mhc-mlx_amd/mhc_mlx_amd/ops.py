@@ -168,21 +168,33 @@ def _sk_shape(H: torch.Tensor) -> tuple[int, int]:
     raise ValueError(f"H_res_raw must be square [n, n], got shape {tuple(H.shape)}")
 
 
-def _sinkhorn_fwd(H: torch.Tensor, iters: int, eps: float) -> torch.Tensor:
+def _sinkhorn_fwd(H: torch.Tensor, iters: int, eps: float, state: torch.Tensor | None = None) -> torch.Tensor:
+    """M = SK(exp(H)); with `state`, the forward also records its VJP state there."""
     batch, n = _sk_shape(H)
     _validate_n(n)
     Hf = _f32(H)
     M = torch.empty_like(Hf)
     with timed("sinkhorn_fwd"):
-        _lib.call("mhc_sinkhorn_fwd", _p(Hf), _p(M), batch, n, int(iters), float(eps), _stream(Hf))
+        if state is None:
+            _lib.call("mhc_sinkhorn_fwd", _p(Hf), _p(M), batch, n, int(iters), float(eps), _stream(Hf))
+        else:
+            _lib.call("mhc_sinkhorn_fwd_record", _p(Hf), _p(M), _p(state), state.numel(), batch, n, int(iters),
+                      float(eps), _stream(Hf))
     return M
 
 
-def _sinkhorn_bwd(H: torch.Tensor, dM: torch.Tensor, iters: int, eps: float) -> torch.Tensor:
+def _sinkhorn_bwd(H: torch.Tensor, dM: torch.Tensor, iters: int, eps: float,
+                  state: torch.Tensor | None = None) -> torch.Tensor:
+    """dH of <dM, SK(exp(H))>, from a recorded state when one is given."""
     batch, n = _sk_shape(H)
     Hf = _f32(H)
     dMf = _f32(dM)
     dH = torch.empty_like(Hf)
+    if state is not None:
+        with timed("sinkhorn_bwd"):
+            _lib.call("mhc_sinkhorn_bwd_recorded", _p(Hf), _p(dMf), _p(dH), _p(state), state.numel(), batch, n,
+                      int(iters), float(eps), _stream(Hf))
+        return dH
     nb = _lib.query("mhc_sinkhorn_bwd_workspace_bytes", batch, n, int(iters))
     ws = _ws(nb, Hf.device)
     with timed("sinkhorn_bwd"):
@@ -191,17 +203,34 @@ def _sinkhorn_bwd(H: torch.Tensor, dM: torch.Tensor, iters: int, eps: float) -> 
     return dH
 
 
+def _sk_record_buffer(H: torch.Tensor, batch: int, n: int, iters: int) -> torch.Tensor | None:
+    """A buffer for the Sinkhorn forward to record its VJP state in, or None.
+
+    The library records for n = 16 (16-byte aligned logits) and 16 < n <= 64,
+    unless the knob MHC_SK16_RECORD / MHC_SK_BLK_RECORD is 0; the backward
+    then reads the state instead of recomputing the forward iterations.
+    """
+    if batch <= 0 or (n == 16 and _f32(H).data_ptr() % 16 != 0):
+        return None
+    nb = _sk_state_bytes(batch, n, iters)
+    return torch.empty(nb, dtype=torch.uint8, device=H.device) if nb > 0 else None
+
+
 class SinkhornFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, H_res_raw, iters, eps):
-        ctx.save_for_backward(H_res_raw)
+        state = None
+        if ctx.needs_input_grad[0]:
+            batch, n = _sk_shape(H_res_raw)
+            state = _sk_record_buffer(H_res_raw, batch, n, iters)
+        ctx.save_for_backward(H_res_raw, state)
         ctx.iters, ctx.eps = iters, eps
-        return _sinkhorn_fwd(H_res_raw, iters, eps)
+        return _sinkhorn_fwd(H_res_raw, iters, eps, state)
 
     @staticmethod
     def backward(ctx, dM):
-        (H,) = ctx.saved_tensors
-        return _sinkhorn_bwd(H, dM, ctx.iters, ctx.eps).to(H.dtype), None, None
+        H, state = ctx.saved_tensors
+        return _sinkhorn_bwd(H, dM, ctx.iters, ctx.eps, state).to(H.dtype), None, None
 
 
 def sinkhorn_knopp_hip(H_res_raw, iters: int = 20, eps: float = 1e-5, threads_per_group=None,
@@ -412,18 +441,17 @@ def _layer_bwd(x, g, hpre, hpost, hres, M, w, iters, eps, per_token):
 
 
 def _sk_state_bytes(B: int, n: int, iters: int) -> int:
-    """Bytes of the Sinkhorn state a per-token forward records for its backward.
+    """Bytes of the Sinkhorn state a forward records for its backward (B matrices).
 
     0 when the library has no recorded path for n, or when the knob
-    MHC_SK16_RECORD is 0 (then the VJP recomputes the forward iterations and
-    needs no saved state: 256 bytes per token and iteration less memory
-    between forward and backward).
+    MHC_SK16_RECORD (n = 16) or MHC_SK_BLK_RECORD (16 < n <= 64) is 0: then
+    the VJP recomputes the forward iterations and needs no saved state.
     """
     return int(_lib.query("mhc_sinkhorn_state_bytes", B, n, iters))
 
 
-def _layer_fwd_recorded(x, hpre, hpost, hres, w, iters, eps, out_dtype, state):
-    """Per-token forward that records the Sinkhorn VJP state in `state`. Returns (out, M)."""
+def _layer_fwd_recorded(x, hpre, hpost, hres, w, iters, eps, out_dtype, state, per_token):
+    """Layer forward that records the Sinkhorn VJP state in `state`. Returns (out, M)."""
     B, n, C = x.shape
     xc = x if x.is_contiguous() else x.contiguous()
     hp, hq, hr, wc = _f32(hpre), _f32(hpost), _f32(hres), _f32(w)
@@ -431,16 +459,16 @@ def _layer_fwd_recorded(x, hpre, hpost, hres, w, iters, eps, out_dtype, state):
     out = torch.empty((B, n, C), dtype=out_dtype, device=x.device)
     s = _stream(xc)
     with timed("sinkhorn_fwd"):
-        _lib.call("mhc_sinkhorn_fwd_record", _p(hr), _p(M), _p(state), state.numel(), B, n, int(iters), float(eps),
-                  s)
+        _lib.call("mhc_sinkhorn_fwd_record", _p(hr), _p(M), _p(state), state.numel(), B if per_token else 1, n,
+                  int(iters), float(eps), s)
     with timed("fused_fwd"):
-        _lib.call("mhc_fused_fwd", _p(xc), _code(xc.dtype), _p(M), n * n, _p(hp), _p(hq), n, _lib.H_RAW, _p(wc),
-                  _p(out), _code(out_dtype), None, B, n, C, float(eps), s)
+        _lib.call("mhc_fused_fwd", _p(xc), _code(xc.dtype), _p(M), n * n if per_token else 0, _p(hp), _p(hq),
+                  n if per_token else 0, _lib.H_RAW, _p(wc), _p(out), _code(out_dtype), None, B, n, C, float(eps), s)
     return out, M
 
 
-def _layer_bwd_recorded(x, g, hpre, hpost, hres, M, w, iters, eps, state):
-    """Per-token backward from a recorded Sinkhorn state: (dx, dH_pre_raw, dH_post_raw, dH_res_raw, d_w)."""
+def _layer_bwd_recorded(x, g, hpre, hpost, hres, M, w, iters, eps, state, per_token):
+    """Backward from a recorded Sinkhorn state: (dx, dH_pre_raw, dH_post_raw, dH_res_raw, d_w)."""
     B, n, C = (int(s) for s in x.shape)
     dev = x.device
     xc = x.detach().contiguous()
@@ -452,20 +480,26 @@ def _layer_bwd_recorded(x, g, hpre, hpost, hres, M, w, iters, eps, state):
     dpost = torch.empty_like(hq)
     dres = torch.empty_like(hr)
     dw = torch.empty((C,), dtype=torch.float32, device=dev)
-    nb = _lib.query("mhc_fused_bwd_workspace_bytes", B, n, C, 1)
+    # layer-wide: the reduced dM, input of the Sinkhorn VJP; per token the
+    # partials pass writes each token's dM to dres and the VJP runs in place
+    dM = dres if per_token else torch.empty((n, n), dtype=torch.float32, device=dev)
+    nb = _lib.query("mhc_fused_bwd_workspace_bytes", B, n, C, int(per_token))
     ws = _ws(nb, dev)
     s = _stream(xc)
     np_ = ctypes.c_int64(0)
+    pt = per_token
     with timed("fused_bwd"):
-        # per-token dM goes to dres, the activated-H chain is applied in the kernel
-        _lib.call("mhc_fused_bwd_partials", _p(xc), _code(xc.dtype), _p(gc), _code(gc.dtype), _p(Mc), n * n,
-                  _p(hp), _p(hq), n, _lib.H_RAW, _p(wc), _p(dx), _code(xc.dtype), _p(dres), _p(dpre), _p(dpost),
+        # the activated-H chain is applied in the kernel (per token) or the reduction (layer-wide)
+        _lib.call("mhc_fused_bwd_partials", _p(xc), _code(xc.dtype), _p(gc), _code(gc.dtype), _p(Mc),
+                  n * n if pt else 0, _p(hp), _p(hq), n if pt else 0, _lib.H_RAW, _p(wc), _p(dx), _code(xc.dtype),
+                  _p(dres) if pt else None, _p(dpre) if pt else None, _p(dpost) if pt else None,
                   _p(ws), nb, B, n, C, float(eps), ctypes.byref(np_), s)
     with timed("layer_bwd_reduce"):
-        _lib.call("mhc_reduce_param_grads", _p(ws), nb, np_.value, n, C, 1, None, None, _lib.H_RAW, None, None,
-                  None, _p(dw), s)
-        _lib.call("mhc_sinkhorn_bwd_recorded", _p(hr), _p(dres), _p(dres), _p(state), state.numel(), B, n,
-                  int(iters), float(eps), s)
+        _lib.call("mhc_reduce_param_grads", _p(ws), nb, np_.value, n, C, int(pt), None if pt else _p(hp),
+                  None if pt else _p(hq), _lib.H_RAW, None if pt else _p(dM), None if pt else _p(dpre),
+                  None if pt else _p(dpost), _p(dw), s)
+        _lib.call("mhc_sinkhorn_bwd_recorded", _p(hr), _p(dM), _p(dres), _p(state), state.numel(),
+                  B if pt else 1, n, int(iters), float(eps), s)
     return dx, dpre, dpost, dres, dw
 
 
@@ -479,22 +513,23 @@ class MHCLayerFn(torch.autograd.Function):
     VJP).  Parameters are layer-wide ([n], [n], [n, n]) or per token
     ([B, n], [B, n], [B, n, n]).  Per token at n = 16, when a gradient is
     needed, the Sinkhorn forward also records the VJP's state (saved for
-    backward like an activation, 256 bytes per token and iteration), so the
-    backward skips recomputing the forward iterations.
+    backward like an activation, 256 bytes per token and iteration), and so
+    does the layer-wide or per-token forward for 16 < n <= 64 (6 * 32 * 4
+    bytes per matrix and iteration at n = 32): the backward then skips
+    recomputing the forward iterations.
     """
 
     @staticmethod
     def forward(ctx, x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype):
         per_token = H_res_raw.ndim == 3
-        # per-token n = 16 with gradients: the Sinkhorn forward records the VJP state
+        n = int(x.shape[1])
+        # with gradients (per token at n = 16, or n > 16): the Sinkhorn forward records the VJP state
         state = None
-        if per_token and any(ctx.needs_input_grad[:5]) and x.shape[0] > 0:
-            nb = _sk_state_bytes(int(x.shape[0]), int(x.shape[1]), iters)
-            if nb > 0:
-                state = torch.empty(nb, dtype=torch.uint8, device=x.device)
+        if (per_token or n > 16) and any(ctx.needs_input_grad[:5]) and x.shape[0] > 0:
+            state = _sk_record_buffer(H_res_raw, int(x.shape[0]) if per_token else 1, n, iters)
         if state is not None:
             out, M = _layer_fwd_recorded(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype,
-                                         state)
+                                         state, per_token)
         else:
             out, M = _layer_fwd(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, iters, eps, out_dtype, per_token)
         ctx.save_for_backward(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, M, state)
@@ -506,7 +541,7 @@ class MHCLayerFn(torch.autograd.Function):
         x, hpre, hpost, hres, w, M, state = ctx.saved_tensors
         if state is not None:
             dx, dpre, dpost, dres, dw = _layer_bwd_recorded(x, dout, hpre, hpost, hres, M, w, ctx.iters, ctx.eps,
-                                                            state)
+                                                            state, ctx.per_token)
         else:
             dx, dpre, dpost, dres, dw = _layer_bwd(x, dout, hpre, hpost, hres, M, w, ctx.iters, ctx.eps,
                                                    ctx.per_token)

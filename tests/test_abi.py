@@ -112,21 +112,34 @@ def test_residual_add_agg_rejects_bad_arguments_on_the_host(lib):
                                         None, 0, 4, 4, 8, None) == -1
 
 
-def test_sinkhorn_state_is_for_n16_only_and_checked_on_the_host(lib, knobs):
+def test_sinkhorn_state_is_for_n16_to_64_and_checked_on_the_host(lib, knobs):
     assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 8 * 20 * 256 + 256
+    # block layout (16 < n <= 64): six vectors of next_pow2(n) floats per matrix and iteration
+    assert lib.mhc_sinkhorn_state_bytes(8, 32, 20) == 8 * 20 * 6 * 32 * 4 + 256
+    assert lib.mhc_sinkhorn_state_bytes(3, 24, 7) == 3 * 7 * 6 * 32 * 4 + 256
+    assert lib.mhc_sinkhorn_state_bytes(1, 64, 0) == 1 * 1 * 6 * 64 * 4 + 256
     assert lib.mhc_sinkhorn_state_bytes(8, 4, 20) == 0
+    assert lib.mhc_sinkhorn_state_bytes(8, 65, 20) == 0
     assert lib.mhc_sinkhorn_state_bytes(0, 16, 20) == 0
     knobs("MHC_SK16", 0)
     assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 0
     knobs("MHC_SK16", None)
     knobs("MHC_SK16_RECORD", 0)
     assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 0
+    assert lib.mhc_sinkhorn_state_bytes(8, 32, 20) > 0
     knobs("MHC_SK16_RECORD", None)
+    knobs("MHC_SK_BLK_RECORD", 0)
+    assert lib.mhc_sinkhorn_state_bytes(8, 32, 20) == 0
+    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) > 0
+    knobs("MHC_SK_BLK_RECORD", None)
     fake = ctypes.c_void_p(4096)  # never dereferenced: every call below is rejected on the host
     eps = ctypes.c_float(1e-6)
     assert lib.mhc_sinkhorn_fwd_record(fake, fake, fake, 1 << 20, 8, 4, 20, eps, None) == -1
-    assert b"n == 16" in lib.mhc_last_error()
+    assert b"16 <= n <= 64" in lib.mhc_last_error()
+    assert lib.mhc_sinkhorn_bwd_recorded(fake, fake, fake, fake, 1 << 20, 8, 65, 20, eps, None) == -1
     assert lib.mhc_sinkhorn_fwd_record(fake, fake, fake, 100, 8, 16, 20, eps, None) == -1
+    assert b"smaller" in lib.mhc_last_error()
+    assert lib.mhc_sinkhorn_fwd_record(fake, fake, fake, 8 * 20 * 768 - 1, 8, 32, 20, eps, None) == -1
     assert b"smaller" in lib.mhc_last_error()
     assert lib.mhc_sinkhorn_bwd_recorded(fake, fake, fake, None, 1 << 20, 8, 16, 20, eps, None) == -1
     assert lib.mhc_sinkhorn_bwd_recorded(fake, fake, fake, fake, 1 << 20, 8, 16, -1, eps, None) == -1

@@ -262,6 +262,51 @@ def test_sinkhorn16_recorded_state_matches_recompute(B, iters, cpl_fwd, cpl_bwd,
     assert np.abs(np_of(d_rec) - rg).max() < 1e-4 * max(1.0, np.abs(rg).max())
 
 
+@pytest.mark.parametrize("B,n,iters", [(1, 32, 20), (1, 24, 20), (5, 32, 3), (1, 64, 20), (3, 48, 1), (9, 17, 0),
+                                       (1, 32, 90), (700, 32, 20)])
+def test_sinkhorn_blk_recorded_state_matches_recompute(B, n, iters):
+    """16 < n <= 64: mhc_sinkhorn_fwd_record / mhc_sinkhorn_bwd_recorded give bitwise the results of
+    mhc_sinkhorn_fwd / mhc_sinkhorn_bwd (the forward records the same state the VJP otherwise
+    recomputes into LDS or its workspace: 90 iterations at n = 32 and n = 64 exceed one wave's LDS
+    share), and both match the oracle.  The state buffer is deliberately not 256-byte aligned; masked
+    rows and columns included; the VJP runs in place (dM aliasing dH) as the layer's per-token
+    backward calls it."""
+    import ctypes
+
+    from mhc_mlx_amd import _lib
+
+    g = rng(4400 + B + n + iters)
+    H = (2.0 * g.standard_normal((B, n, n))).astype(np.float32)
+    H[::3, :, 1] = -40.0
+    dM = g.standard_normal((B, n, n)).astype(np.float32)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    eps = ctypes.c_float(1e-5)
+    Ht = dev_tensor(H)
+    M_plain = torch.empty_like(Ht)
+    _lib.call("mhc_sinkhorn_fwd", P(Ht), P(M_plain), B, n, iters, eps, s)
+    nst = _lib.query("mhc_sinkhorn_state_bytes", B, n, iters)
+    npow = 32 if n <= 32 else 64
+    assert nst == B * max(iters, 1) * 6 * npow * 4 + 256
+    st_buf = torch.empty(nst + 64, dtype=torch.uint8, device="cuda")
+    st = st_buf[48:]
+    M_rec = torch.empty_like(Ht)
+    _lib.call("mhc_sinkhorn_fwd_record", P(Ht), P(M_rec), P(st), nst, B, n, iters, eps, s)
+    assert torch.equal(M_rec, M_plain)
+    d_rec = dev_tensor(dM)
+    _lib.call("mhc_sinkhorn_bwd_recorded", P(Ht), P(d_rec), P(d_rec), P(st), nst, B, n, iters, eps, s)
+    nb = _lib.query("mhc_sinkhorn_bwd_workspace_bytes", B, n, iters)
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+    d_plain = torch.empty_like(Ht)
+    _lib.call("mhc_sinkhorn_bwd", P(Ht), P(dev_tensor(dM)), P(d_plain), B, n, iters, eps, P(ws), nb, s)
+    torch.cuda.synchronize()
+    assert torch.equal(d_rec, d_plain)
+    rm = O.mixing_matrix_from_logits(H.astype(np.float64), iters=iters, eps=1e-5)
+    assert np.abs(np_of(M_rec) - rm).max() < 1e-5 * max(1.0, np.abs(rm).max())
+    rg = O.sinkhorn_knopp_vjp(H.astype(np.float64), dM, iters=iters, eps=1e-5)
+    assert np.abs(np_of(d_rec) - rg).max() < 1e-4 * max(1.0, np.abs(rg).max())
+
+
 def test_sinkhorn16_identity_init_and_bomb():
     n = 16
     Hi = (np.full((n, n), -12.0) + np.eye(n) * 12.0).astype(np.float32)
