@@ -690,16 +690,20 @@ class PostCombineFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, y_inner, H_pre_raw, H_post_raw, H_res_raw, iters, eps, out_dtype):
-        M = _sinkhorn_fwd(H_res_raw, iters, eps)
-        ctx.save_for_backward(x, y_inner, H_pre_raw, H_post_raw, H_res_raw, M)
+        # with a gradient for H_res_raw the Sinkhorn forward records its VJP state (n >= 16)
+        state = None
+        if ctx.needs_input_grad[4]:
+            state = _sk_record_buffer(H_res_raw, 1, int(H_res_raw.shape[-1]), iters)
+        M = _sinkhorn_fwd(H_res_raw, iters, eps, state)
+        ctx.save_for_backward(x, y_inner, H_pre_raw, H_post_raw, H_res_raw, M, state)
         ctx.iters, ctx.eps = iters, eps
         return _mix_fwd(x, y_inner, M, H_pre_raw, H_post_raw, _lib.H_RAW, out_dtype)
 
     @staticmethod
     def backward(ctx, dout):
-        x, y, hpre, hpost, hres, M = ctx.saved_tensors
+        x, y, hpre, hpost, hres, M, state = ctx.saved_tensors
         dx, dy, dM, dpre, dpost = _mix_bwd(x, y, dout, M, hpre, hpost, _lib.H_RAW, want_dy=True)
-        dres = _sinkhorn_bwd(hres, dM, ctx.iters, ctx.eps)
+        dres = _sinkhorn_bwd(hres, dM, ctx.iters, ctx.eps, state)
         return (dx, dy.to(y.dtype), dpre.to(hpre.dtype), dpost.to(hpost.dtype), dres.to(hres.dtype), None,
                 None, None)
 

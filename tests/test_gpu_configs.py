@@ -392,6 +392,33 @@ def test_per_token_n16_recorded_sinkhorn_state(T, C, knobs):
     assert torch.equal(out_ng, results[0][0])
 
 
+@pytest.mark.parametrize("T,n,C,per_token", [(300, 32, 512, False), (64, 24, 1024, False), (40, 48, 256, False),
+                                             (37, 32, 256, True), (20, 20, 384, True)])
+def test_block_sinkhorn_recorded_state_in_the_layer(T, n, C, per_token, knobs):
+    """16 < n <= 64 with gradients: the layer's Sinkhorn forward records the VJP state and the
+    backward reads it (layer-wide: partial sums, reduction, recorded VJP); with MHC_SK_BLK_RECORD=0
+    the backward is mhc_layer_bwd, which recomputes it.  Both give bitwise the same output and
+    gradients, and dH_res_raw matches the oracle."""
+    g = rng(7400 + T + n)
+    x = to_dtype_np(g.standard_normal((T, n, C)), "bf16")
+    dout = dev_tensor(to_dtype_np(g.standard_normal((T, n, C)), "bf16"), "bf16")
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T if per_token else None)
+    fn = ops.mhc_layer_forward_dynamic if per_token else ops.mhc_layer_forward
+    results = []
+    for rec in (1, 0):
+        knobs("MHC_SK_BLK_RECORD", rec)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        xt = dev_tensor(x, "bf16").requires_grad_(True)
+        out = fn(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+        out.backward(dout)
+        results.append([out.detach(), xt.grad] + [p.grad for p in ps])
+    knobs("MHC_SK_BLK_RECORD", None)
+    for name, a, b in zip(["out", "dx", "dH_pre_raw", "dH_post_raw", "dH_res_raw", "d_w"], *results):
+        assert torch.equal(a, b), name
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, np_of(dout), sinkhorn_iters=20, eps=EPS)
+    assert rel_err(np_of(results[0][4]), refs[3]) < 1e-4
+
+
 def test_per_token_n16_valu_fallback(knobs):
     """The VALU kernels that serve n = 16 when the MFMA kernels decline (here forced off through
     their knobs) give the same parity."""
