@@ -11,7 +11,9 @@ Timed regions (all on the stream the library launches on):
   2. K steps with per-kernel HIP events          -> roofline of the dominant
      kernel (the backward partial-sums pass) and of the forward kernel
 Extras: forward latency at B=32, C=2048 (config 1) and B=1, C=4096 (eager
-calls); config 3 (per-token H, n=16) fwd+bwd; config 4
+calls, and replays of a HIP graph of the C ABI's forward); fwd+bwd latency
+of a 32-token batch (eager module against a graph of the C ABI's forward and
+allocation-free backward); config 3 (per-token H, n=16) fwd+bwd; config 4
 (MHCRewire around Linear(4096, 4096)) with mHC kernel time reported apart
 from the GEMM; residual_add_agg at config 2's shape; n=32 training steps
 (MHCLayer at 8192 x 32 x 512, MHCRewire(Linear(4096, 4096)) at n=32); the
@@ -112,7 +114,72 @@ def _fwd_latency(n, C, B, dev, reps=200):
     # layer-wide n in {4, 8} with at most one token per CU: the Sinkhorn projection runs inside the
     # forward kernel (one launch); otherwise Sinkhorn and the fused forward are two launches
     one = n in (4, 8) and B <= torch.cuda.get_device_properties(dev).multi_processor_count
-    return {"eager_us": round(eager, 2), "kernel_launches": 1 if one else 2}
+    graph = _graph_abi(layer, x, with_backward=False)
+    return {"eager_us": round(eager, 2), "graph_us": round(_median_us(graph.replay, reps), 2),
+            "kernel_launches": 1 if one else 2}
+
+
+def _graph_abi(layer, x, with_backward, dout=None):
+    """A HIP graph of the C ABI's mhc_layer_fwd (and mhc_layer_bwd_noalloc) on buffers allocated
+    outside the capture, after eager warm-up calls on the capturing stream."""
+    import ctypes
+
+    import torch
+
+    from mhc_mlx_amd import _lib
+
+    T, n, C = (int(v) for v in x.shape)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    hp, hq, hr, w = (p.detach().float().contiguous() for p in
+                     (layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight))
+    out, M = torch.empty_like(x), torch.empty_like(hr)
+    dx = torch.empty_like(x)
+    grads = [torch.empty_like(hp), torch.empty_like(hq), torch.empty_like(hr), torch.empty_like(w)]
+    bf16, it, eps = _lib.DTYPE_BF16, int(layer.sinkhorn_iters), ctypes.c_float(layer.eps)
+
+    def launch():
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.call("mhc_layer_fwd", P(x), bf16, P(hp), P(hq), P(hr), P(w), P(out), bf16, P(M), T, n, C, 0, it, eps,
+                  s)
+        if with_backward:
+            _lib.call("mhc_layer_bwd_noalloc", P(x), bf16, P(dout), bf16, P(hp), P(hq), P(hr), P(M), P(w), P(dx),
+                      *(P(t) for t in grads), T, n, C, 0, it, eps, s)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        launch()
+    graph.buffers = (hp, hq, hr, w, out, M, dx, grads)  # kept alive with the graph
+    return graph
+
+
+def _small_step_latency(dev, T=32, n=4, C=2048, reps=200):
+    """fwd+bwd of a small batch (host-bound when eager): the module through autograd against a HIP graph of
+    the C ABI's forward and allocation-free backward (µs, medians of event-bracketed calls)."""
+    import numpy as np
+    import torch
+
+    layer = _layer(n, C, dev, np.random.default_rng(2))
+    x = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16).requires_grad_(True)
+    dout = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16)
+    params = [layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight]
+
+    def step():
+        out = layer(x, return_dtype=torch.bfloat16)
+        return torch.autograd.grad(out, [x] + params, dout)
+
+    for _ in range(20):
+        step()
+    eager = _median_us(step, reps)
+    graph = _graph_abi(layer, x.detach(), with_backward=True, dout=dout)
+    return {"workload": f"MHCLayer fwd+bwd, {T} tokens, n={n}, C={C}, bf16", "eager_us": round(eager, 2),
+            "graph_us": round(_median_us(graph.replay, reps), 2)}
 
 
 def _config3(dev, steps, warmup):
@@ -537,6 +604,7 @@ def main() -> int:
     if not args.no_latency:
         result["fwd_latency"] = {"config1_B32_C2048": _fwd_latency(4, 2048, 32, dev),
                                  "B1_C4096": _fwd_latency(4, 4096, 1, dev)}
+        result["small_step_latency"] = _small_step_latency(dev)
     if not args.no_extra:
         # 20 warmup steps: the first ~20 steps after a change of workload run a few percent slow
         # (config 3: 0.56-0.61 ms against 0.545 ms from then on)
