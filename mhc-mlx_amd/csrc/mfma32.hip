@@ -147,6 +147,15 @@ struct OutRows {
       st16<false>(d + 4, w[k][4], w[k][5], w[k][6], w[k][7]);
     }
   }
+  // row k through a buffer resource (lane offset voff, uniform offset soff)
+  MHC_DEV void store_buf(int k, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) const {
+    if constexpr (kHalf) {
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}, rs, voff, soff, kBufNt);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}, rs, voff, soff, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[k][4], w[k][5], w[k][6], w[k][7]}, rs, voff, soff + 16, 0);
+    }
+  }
 };
 
 template <bool RAW>
@@ -322,6 +331,170 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
         for (int k = 0; k < 4; ++k) {
           const int row = 16 * I + 4 * q + k;
           if (row < n) rows.store(k, ot + (int64_t)row * C + cb[s]);
+        }
+      }
+    }
+  }
+}
+
+// Largest C of the forward: the loop variant's y buffer (512 bytes per slab)
+// stays within 64 KiB of LDS.
+constexpr int kMf32FwdMaxC = 16384;
+
+// Forward above C = 2048 (LOOP): W waves per workgroup walk SPW = S / W slabs
+// each in a runtime loop, one slab in registers at a time, so the kernel
+// needs the registers of the one-slab variant whatever C is and several
+// workgroups share a CU.  Before the RMS barrier the lane loads its slab for
+// y = a^T X and the token's sum of y^2, and lane group 0 writes the slab's y
+// to LDS (512 bytes per slab); after it the lane loads the slab again (from
+// the caches: the token was read just before) and reads its channels' y
+// back for the mix.  Each wave reads back only the y it wrote itself.
+template <typename XT, typename OT, bool PT, bool RAW, bool FULL>
+__global__ __launch_bounds__(512) void mf32_fwd_loop_kernel(Mf32Args A, int spw) {
+  extern __shared__ float4 s_y4[];  // [S][16 r][8 channels]
+  float* const s_y = reinterpret_cast<float*>(s_y4);
+  __shared__ float s_red[2][16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int n = FULL ? 32 : A.n;
+  const int C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  // token rows through buffer resources: a 32-bit lane offset for the lane's
+  // first row, the row and slab parts as uniform offsets (n < 32: the row part
+  // in the lane offset, so rows past n fall outside the resource, which reads
+  // them as zero and drops their stores)
+  constexpr uint32_t kEs = sizeof(XT), kOs = sizeof(OT);
+  const uint32_t rowb = (uint32_t)C * kEs, orowb = (uint32_t)C * kOs;
+  const uint32_t lane_in = (uint32_t)(8 * q * C + 8 * r) * kEs;   // stream 8q (+ e rows)
+  const uint32_t lane_out = (uint32_t)(4 * q * C + 8 * r) * kOs;  // stream 4q (+ 16 I + k rows)
+  const uint32_t tokb = (uint32_t)(nC * kEs), otokb = (uint32_t)(nC * kOs);
+
+  u32x4 aa[3], am[2][3];
+  float pv[2][4];
+  auto load_params = [&](int64_t t) {
+    const float* M = A.M + t * A.M_ts;
+    const float* hp = A.hpre + t * A.h_ts;
+    const float* hq = A.hpost + t * A.h_ts;
+    float av[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) av[e] = 8 * q + e < n ? act_pre<RAW>(hp[8 * q + e]) : 0.0f;
+    split3x8<XT>(av, aa);
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      const int row = 16 * I + r;
+      float mv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mv[e] = (row < n && 8 * q + e < n) ? M[row * n + 8 * q + e] : 0.0f;
+      split3x8<XT>(mv, am[I]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int o = 16 * I + 4 * q + k;
+        pv[I][k] = o < n ? act_post<RAW>(hq[o]) : 0.0f;
+      }
+    }
+  };
+  // layer-wide: the split operands (36 words per lane, the same for every
+  // wave) are staged in LDS once and read back at each use, which keeps
+  // the kernel at two 8-wave workgroups per CU
+  __shared__ u32x4 s_aa[3][64], s_am[2][3][64];
+  if constexpr (!PT) {
+    load_params(0);
+    if (wave == 0) {
+#pragma unroll
+      for (int e = 0; e < 3; ++e) {
+        s_aa[e][lane] = aa[e];
+        s_am[0][e][lane] = am[0][e];
+        s_am[1][e][lane] = am[1][e];
+      }
+    }
+    __syncthreads();
+  }
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const auto rx = rows_rsrc((const XT*)A.x + t * nC, tokb);
+    const auto ro = rows_rsrc((OT*)A.out + t * nC, otokb);
+    // streams 8q .. 8q+7 of the slab's channels 8r .. 8r+7, transposed into
+    // the B operands (the first read cached, the second non-temporal)
+    auto load_slab = [&](auto aux, int slab, u32x4 (&b)[8]) {
+      const uint32_t sb = (uint32_t)slab * 128 * kEs;
+      Vec<XT, 8> xr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        buf_load<decltype(aux)::value>(xr[e], rx, FULL ? lane_in : lane_in + (uint32_t)e * rowb,
+                                       FULL ? sb + (uint32_t)e * rowb : sb);
+      transpose8<XT>(xr, b);
+    };
+    if constexpr (PT) load_params(t);
+    float ss = 0.0f;
+    for (int s = 0; s < spw; ++s) {
+      const int slab = wave * spw + s;
+      u32x4 bx[8];
+      load_slab(std::integral_constant<int, 0>{}, slab, bx);
+      if constexpr (!PT) {
+        asm volatile("" ::: "memory");  // read at each use, not held in registers across the loop
+#pragma unroll
+        for (int e = 0; e < 3; ++e) aa[e] = s_aa[e][lane];
+      }
+      float y[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const f32x4 acc = mfma_split3<XT>(aa, bx[v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        y[v] = acc[0];
+        ss = fmaf(acc[0], acc[0], ss);
+      }
+      // the four lane groups q hold the same y: group 0 keeps it
+      if (q == 0) {
+        float4* dst = reinterpret_cast<float4*>(s_y + (slab * 16 + r) * 8);
+        dst[0] = make_float4(y[0], y[1], y[2], y[3]);
+        dst[1] = make_float4(y[4], y[5], y[6], y[7]);
+      }
+    }
+    ss = q == 0 ? ss : 0.0f;
+    ss = wave_sum(ss);
+    if (lane == 0) s_red[it & 1][wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < nwaves; ++w) tot += s_red[it & 1][w];
+    const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
+    if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
+    for (int s = 0; s < spw; ++s) {
+      const int slab = wave * spw + s;
+      u32x4 bx[8];
+      load_slab(std::integral_constant<int, kBufNt>{}, slab, bx);
+      const float4* src = reinterpret_cast<const float4*>(s_y + (slab * 16 + r) * 8);
+      const float4 y0 = src[0], y1 = src[1];
+      const float y[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+      float wv[8];
+      load_w8(A.w + slab * 128 + 8 * r, wv);
+      float yn[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) yn[v] = (y[v] * inv) * wv[v];
+      const uint32_t sob = (uint32_t)slab * 128 * kOs;
+      if constexpr (!PT) asm volatile("" ::: "memory");
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        if constexpr (!PT) {
+#pragma unroll
+          for (int e = 0; e < 3; ++e) am[I][e] = s_am[I][e][lane];
+        }
+        OutRows<OT> rows;
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = mfma_split3<XT>(am[I], bx[v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc[k] = fmaf(yn[v], pv[I][k], acc[k]);
+          if (v & 1) rows.put(v >> 1, even, acc);
+          else even = acc;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t ro_row = (uint32_t)(16 * I + k) * orowb;
+          rows.store_buf(k, ro, FULL ? lane_out : lane_out + ro_row, FULL ? sob + ro_row : sob);
         }
       }
     }
@@ -1142,12 +1315,19 @@ int by_half(int code, F&& f) {
 
 }  // namespace
 
+int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s);
+
 int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
-  if (A.n <= 16 || A.n > 32 || A.C % 128 != 0 || A.C > 4096) return 1;
+  if (A.n <= 16 || A.n > 32 || A.C % 128 != 0 || A.C > kMf32FwdMaxC) return 1;
   if (od != MHC_DTYPE_F32 && od != xd) return 1;
   if (!aligned(A.x, 16) || !aligned(A.out, 16) || !aligned(A.w, 16)) return 1;
   if (knob(kKnobFwdMfma, 1) == 0) return 1;
   const int S = A.C / 128;
+  // above C = 2048 the runtime slab loop (above C = 4096 the only variant);
+  // MHC_MF32_FWD_LOOP=0 keeps the register variants up to C = 4096, 2 takes
+  // the loop at every C
+  const int loop = knob(kKnobFwdLoop, 1);
+  if (S > 32 || (S > 16 && loop != 0) || loop == 2) return mf32_fused_fwd_loop(A, xd, od, s);
   // two slabs per wave up to C = 2048 (in registers across the RMS barrier),
   // four above it (read again after the barrier)
   const int spw = S <= 8 ? 1 : (S <= 16 ? 2 : 4);
@@ -1184,6 +1364,41 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
 #undef MF32_FWD
 #undef MF32_FWD_RELOAD
       MHC_CHECK_LAUNCH("mf32_fwd_kernel");
+      return MHC_OK;
+    };
+    return od == MHC_DTYPE_F32 ? go((float*)nullptr) : go((XT*)nullptr);
+  });
+}
+
+// The runtime-loop forward: the wave count nearest MHC_MF32_FWD_WAVES (default
+// 8) that divides the slab count, one token per workgroup at a time.
+int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s) {
+  const int S = A.C / 128;
+  const int target = std::min(kMf32MaxWaves, std::max(1, knob(kKnobMf32FwdWaves, 8)));
+  int waves = 1;
+  for (int w = 1; w <= kMf32MaxWaves; ++w)
+    if (S % w == 0 && std::abs(w - target) < std::abs(waves - target)) waves = w;
+  const int spw = S / waves;
+  const size_t smem = (size_t)S * 16 * 8 * sizeof(float);
+  const bool pt = A.M_ts != 0, raw = A.h_mode == MHC_H_RAW, full = A.n == 32;
+  const int per_cu = knob(kKnobFwdGrid, 8);
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * std::max(per_cu, 1)));
+  const dim3 g((unsigned)blocks), b(waves * 64);
+  return by_half(xd, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    auto go = [&](auto* op) {
+      using OT = std::remove_pointer_t<decltype(op)>;
+      with_full(full, [&](auto fc) {
+        constexpr bool F = decltype(fc)::value;
+        if (pt) {
+          if (raw) hipLaunchKernelGGL((mf32_fwd_loop_kernel<XT, OT, true, true, F>), g, b, smem, s, A, spw);
+          else hipLaunchKernelGGL((mf32_fwd_loop_kernel<XT, OT, true, false, F>), g, b, smem, s, A, spw);
+        } else {
+          if (raw) hipLaunchKernelGGL((mf32_fwd_loop_kernel<XT, OT, false, true, F>), g, b, smem, s, A, spw);
+          else hipLaunchKernelGGL((mf32_fwd_loop_kernel<XT, OT, false, false, F>), g, b, smem, s, A, spw);
+        }
+      });
+      MHC_CHECK_LAUNCH("mf32_fwd_loop_kernel");
       return MHC_OK;
     };
     return od == MHC_DTYPE_F32 ? go((float*)nullptr) : go((XT*)nullptr);

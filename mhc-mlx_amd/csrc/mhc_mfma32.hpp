@@ -28,7 +28,7 @@ struct Mf32Args {
 };
 
 // Forward (out = M x + p * rms_norm(a^T x) w) for 16 < n <= 32, 16-bit x,
-// out fp32 or x's dtype, C a multiple of 128 up to 4096, layer-wide or
+// out fp32 or x's dtype, C a multiple of 128 up to 16384, layer-wide or
 // per-token parameters.  Returns 1 when the shape is not covered.
 int mf32_fused_fwd(const Mf32Args& A, int x_dtype, int out_dtype, hipStream_t s);
 

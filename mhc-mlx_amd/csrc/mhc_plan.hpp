@@ -81,7 +81,7 @@ enum Knob : int {
   kKnobBwdGrid, kKnobBwdMfma, kKnobBwdSpw, kKnobBwdLegacy, kKnobBwdTpb,
   kKnobSk16, kKnobSk16Cpl, kKnobSk16Record,
   kKnobResGrid, kKnobMixFwdGrid, kKnobMixBwdGrid, kKnobScaleFwdGrid, kKnobScaleBwdGrid,
-  kKnobBwdPipe, kKnobMix32, kKnobMf32Waves, kKnobSkBlkRecord,
+  kKnobBwdPipe, kKnobMix32, kKnobMf32Waves, kKnobSkBlkRecord, kKnobFwdLoop, kKnobMf32FwdWaves,
   kNumKnobs
 };
 

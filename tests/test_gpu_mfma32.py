@@ -32,8 +32,10 @@ def _ulp_bound(got, ref, dt):
 
 @pytest.mark.parametrize("T,n,C", [(5, 32, 128), (40, 32, 512), (7, 24, 384), (9, 17, 256), (3, 32, 1024),
                                    (4, 32, 2048), (6, 20, 1280),
-                                   # C above 2048: four slabs per wave, x read again after the RMS barrier
-                                   (3, 32, 4096), (300, 32, 3072), (2, 24, 4096), (5, 20, 3072)])
+                                   # C above 2048: a runtime loop over each wave's slabs, x read again after
+                                   # the RMS barrier, y kept in LDS; 17 and 18 slabs split over 1 and 3 waves
+                                   (3, 32, 4096), (300, 32, 3072), (2, 24, 4096), (5, 20, 3072), (2, 32, 8192),
+                                   (3, 24, 6144), (1, 32, 16384), (4, 32, 2176), (3, 20, 2304)])
 @pytest.mark.parametrize("xdt,odt", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
 @pytest.mark.parametrize("per_token", [False, True])
 def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
@@ -53,12 +55,26 @@ def test_mfma32_forward(T, n, C, xdt, odt, per_token, knobs):
         _ulp_bound(got, ref, odt)
 
 
+@pytest.mark.parametrize("T,n,C,settings", [(3, 32, 4096, {"MHC_MF32_FWD_LOOP": 0}),
+                                            (5, 24, 3072, {"MHC_MF32_FWD_LOOP": 0}),
+                                            (4, 32, 4096, {"MHC_MF32_FWD_WAVES": 8}),
+                                            (3, 32, 3072, {"MHC_MF32_FWD_WAVES": 1}),
+                                            (2, 20, 8192, {"MHC_MF32_FWD_WAVES": 2})])
+@pytest.mark.parametrize("odt", ["bf16", "f32"])
+def test_mfma32_forward_other_splits(T, n, C, settings, odt, knobs):
+    """C above 2048 with the four-slab register variant (MHC_MF32_FWD_LOOP=0, C <= 4096) and with the
+    runtime-loop variant on 8, 1 and 2 waves per workgroup."""
+    for k, v in settings.items():
+        knobs(k, v)
+    test_mfma32_forward(T, n, C, "bf16", odt, True, knobs)
+    test_mfma32_forward(T, n, C, "bf16", odt, False, knobs)
+
+
 @pytest.mark.parametrize("T,n,C", [(5, 32, 128), (300, 32, 512), (40, 24, 256), (33, 17, 640), (7, 32, 1024),
                                    (64, 28, 384),
                                    # n = 32 above C = 1024: 2 .. 8 slabs per wave on 3 to 8 waves, the
-                                   # one-slab-ahead variant up to C = 3072 (C = 1408 has no split; above
-                                   # C = 4096 the forward runs on the generic kernel); n < 32 there: up to
-                                   # 5 slabs per wave, rows beyond n through the buffer range check
+                                   # one-slab-ahead variant up to C = 3072 (C = 1408 has no split); n < 32
+                                   # there: up to 5 slabs per wave, rows beyond n through the buffer range check
                                    (3, 32, 1152), (9, 32, 1536), (2, 32, 1408), (4, 32, 2048), (5, 32, 2560),
                                    (17, 32, 3072), (2, 32, 3584), (3, 32, 4096), (2, 32, 8192), (4, 24, 2048),
                                    (11, 20, 3072), (3, 17, 4096), (5, 28, 1536)])

@@ -1,7 +1,8 @@
 """Run-to-run determinism of every kernel family on its main shapes.
 
 Each path (the n = 4 and n = 8 layer-wide full tiles, n = 4 per-token, the n = 16 MFMA kernels per-token and
-layer-wide, the n = 32 MFMA kernels at one, two and four slabs per wave, n = 24, and MHCRewire's post-combine
+layer-wide, the n = 32 MFMA kernels at one, two and four slabs per wave and the runtime-loop forward above C = 2048
+(C = 4096, 8192, and per-token n = 24 at C = 3072), n = 24, and MHCRewire's post-combine
 at n = 4 and n = 32) runs forward and backward five times on the same inputs; every output and gradient must
 be bitwise equal to the first run's.  The kernels use fixed-order reductions, so any difference is a defect:
 a race, or a register or memory hazard that depends on timing.  Parity with the oracle is covered by the
@@ -31,7 +32,8 @@ def _assert_reruns_equal(run):
 @pytest.mark.parametrize("T,n,C,per_token", [(4096, 4, 4096, False), (4096, 4, 4096, True), (2048, 8, 2048, False),
                                              (2048, 16, 1024, True), (2048, 16, 2048, False),
                                              (2048, 32, 512, False), (512, 32, 2048, False),
-                                             (512, 32, 4096, False), (512, 24, 1024, False)])
+                                             (512, 32, 4096, False), (256, 32, 8192, False), (512, 24, 1024, False),
+                                             (300, 24, 3072, True)])
 def test_layer_reruns_are_bitwise_equal(T, n, C, per_token):
     g = rng(7100 + T + n + C)
     x = to_dtype_np(g.standard_normal((T, n, C)), "bf16")
