@@ -50,6 +50,8 @@ _METAL_FAILED = False
 
 _HIP_AVAILABLE: bool | None = None
 
+_HALF = (torch.float16, torch.bfloat16)
+
 
 def _disabled_by_env() -> bool:
     return os.getenv("MHC_MLX_DISABLE_METAL", "0") == "1" or os.getenv("MHC_HIP_DISABLE", "0") == "1"
@@ -312,8 +314,35 @@ class MHCLayer(nn.Module):
             return return_dtype
         return None
 
+    def _forward_nograd(self, x, return_dtype):
+        """The HIP forward of a call that needs no gradient (inference, torch.no_grad), with the fewest
+        host steps: a single-token forward is launch-bound, so its latency is mostly this code.  Returns
+        None whenever the general path has something to decide (a shape error, CPU tensors, the torch
+        path, a gradient, a library error), and forward() then takes that path."""
+        if not self.use_metal or x.ndim != 3 or x.shape[1] != self.n or x.shape[2] != self.C:
+            return None
+        ps = self._parameters
+        hp, hq, hr, w = ps.get("H_pre_raw"), ps.get("H_post_raw"), ps.get("H_res_raw"), ps.get("rms_weight")
+        if hp is None or hq is None or hr is None or w is None or _disabled_by_env():
+            return None
+        if torch.is_grad_enabled() and (x.requires_grad or hp.requires_grad or hq.requires_grad
+                                        or hr.requires_grad or w.requires_grad):
+            return None
+        xdt = x.dtype
+        kdt = return_dtype if return_dtype is xdt and xdt in _HALF else torch.float32
+        try:
+            out = ops.layer_forward_nograd(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, kdt)
+        except RuntimeError:
+            return None
+        if out is not None and return_dtype is not None and out.dtype != return_dtype:
+            out = out.to(return_dtype)
+        return out
+
     def forward(self, x_expanded: torch.Tensor, *, return_dtype: torch.dtype | None = None) -> torch.Tensor:
         """Run the mHC layer on x_expanded [B, n, C] (layer.py:339-435)."""
+        out = self._forward_nograd(x_expanded, return_dtype)
+        if out is not None:
+            return out
         B, n, C = self._check(x_expanded)
         out = None
         if self._should_use_metal(B, n, C):

@@ -403,6 +403,37 @@ def _layer_fwd(x, hpre, hpost, hres, w, iters, eps, out_dtype, per_token):
     return out, M
 
 
+_F32 = torch.float32
+
+
+def layer_forward_nograd(x, hpre, hpost, hres, w, iters: int, eps: float, out_dtype):
+    """mhc_layer_fwd for a call that needs no gradient, with the fewest host steps (small-batch latency).
+
+    Takes only what the library can consume as is: x contiguous on a GPU in fp32/bf16/fp16, the four
+    layer-wide parameters contiguous fp32 on x's device, no kernel timer active.  Returns None when any
+    of that does not hold, and the caller takes the general path (mhc_layer_forward); raises on a
+    library error like every op here.  out_dtype: torch.float32, or x's dtype when that is 16-bit.
+    """
+    xcode = _DTYPE_CODE.get(x.dtype)
+    if xcode is None or not x.is_cuda or not x.is_contiguous() or profiling._active is not None:
+        return None
+    dev = x.get_device()
+    for p in (hpre, hpost, hres, w):
+        if p.dtype is not _F32 or not p.is_contiguous() or p.get_device() != dev:
+            return None
+    B, n, C = x.shape
+    if hpre.numel() != n or hpost.numel() != n or hres.numel() != n * n or w.numel() != C:
+        return None
+    out = torch.empty_like(x) if out_dtype is x.dtype else torch.empty((B, n, C), dtype=out_dtype, device=x.device)
+    M = torch.empty_like(hres)
+    rc = _lib.load().mhc_layer_fwd(x.data_ptr(), xcode, hpre.data_ptr(), hpost.data_ptr(), hres.data_ptr(),
+                                   w.data_ptr(), out.data_ptr(), _DTYPE_CODE[out_dtype], M.data_ptr(), B, n, C, 0,
+                                   iters, eps, _stream(x))
+    if rc:
+        _lib.check(rc, "mhc_layer_fwd")
+    return out
+
+
 def _layer_bwd(x, g, hpre, hpost, hres, M, w, iters, eps, per_token):
     """mhc_layer_bwd: (dx, dH_pre_raw, dH_post_raw, dH_res_raw, d_rms_weight)."""
     B, n, C = (int(s) for s in x.shape)

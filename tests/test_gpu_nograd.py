@@ -1,0 +1,127 @@
+"""GPU tests of MHCLayer's no-gradient forward (inference, torch.no_grad).
+
+A call that needs no gradient goes straight to mhc_layer_fwd with the fewest
+host steps (``MHCLayer._forward_nograd`` -> ``ops.layer_forward_nograd``).
+It must give bitwise the results of the general op path and match the
+oracle (reference.py:164-184), and hand every case it does not take (views,
+fp64 parameters, a library error) to the general path unchanged.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mhc_oracle as O
+from tests._helpers import TOL, dev_tensor, np_of, params, rel_err, rng, to_dtype_np
+
+from mhc_mlx_amd import MHCLayer, _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(n, C, g):
+    hpre, hpost, hres, w = params(g, n, C)
+    layer = MHCLayer(n=n, C=C, eps=1e-6).cuda()
+    with torch.no_grad():
+        for p, v in zip((layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight),
+                        (hpre, hpost, hres, w)):
+            p.copy_(torch.from_numpy(v))
+    return layer, (hpre, hpost, hres, w)
+
+
+@pytest.fixture
+def fast_calls(monkeypatch):
+    """Counts the fast path's calls that returned a result."""
+    calls = []
+    real = ops.layer_forward_nograd
+
+    def wrapped(*a, **k):
+        out = real(*a, **k)
+        calls.append(out is not None)
+        return out
+
+    monkeypatch.setattr(ops, "layer_forward_nograd", wrapped)
+    return calls
+
+
+@pytest.mark.parametrize("B,n,C,dt,ret", [
+    (1, 4, 4096, "bf16", torch.bfloat16),   # the B = 1 latency shape (single launch)
+    (32, 4, 2048, "bf16", torch.bfloat16),  # config 1
+    (32, 4, 2048, "bf16", None),            # fp32 out (the reference's default)
+    (3, 8, 520, "f16", torch.float16),      # ragged C
+    (300, 4, 256, "f32", None),             # more tokens than CUs: Sinkhorn launch + fused forward
+    (2, 16, 1024, "bf16", torch.bfloat16),
+    (1, 32, 4096, "bf16", torch.bfloat16),  # the reference's n = 32 latency rows
+    (4, 2, 96, "bf16", torch.float32),      # fp32 out requested explicitly
+])
+def test_nograd_forward_matches_general_path_and_oracle(B, n, C, dt, ret, fast_calls):
+    g = rng(300 + n + B)
+    layer, (hpre, hpost, hres, w) = _layer(n, C, g)
+    x = to_dtype_np(g.standard_normal((B, n, C)), dt)
+    xt = dev_tensor(x, dt)
+    with torch.no_grad():
+        out = layer(xt, return_dtype=ret)
+        assert fast_calls == [True]
+        kdt = ret if ret is xt.dtype and ret in (torch.bfloat16, torch.float16) else None
+        ref = ops.mhc_layer_forward(xt, layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight,
+                                    sinkhorn_iters=20, eps=1e-6, output_dtype=kdt)
+        if ret is not None:
+            ref = ref.to(ret)
+    torch.cuda.synchronize()
+    assert out.dtype == (ret or torch.float32) and out.shape == (B, n, C)
+    assert torch.equal(out, ref)
+    oracle = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=1e-6)
+    tol = TOL["bf16" if out.dtype == torch.bfloat16 else "f16" if out.dtype == torch.float16 else dt]
+    assert rel_err(np_of(out), oracle) < max(tol, 1e-5)
+
+
+def test_inference_mode_and_frozen_parameters_take_the_fast_path(fast_calls):
+    g = rng(11)
+    layer, _ = _layer(4, 512, g)
+    xt = torch.randn(8, 4, 512, device="cuda", dtype=torch.bfloat16)
+    with torch.inference_mode():
+        a = layer(xt, return_dtype=torch.bfloat16)
+    for p in layer.parameters():
+        p.requires_grad_(False)
+    b = layer(xt, return_dtype=torch.bfloat16)  # grad mode on, nothing needs a gradient
+    assert fast_calls == [True, True]
+    assert torch.equal(a, b)
+
+
+def test_gradient_calls_skip_the_fast_path(fast_calls):
+    g = rng(12)
+    layer, _ = _layer(4, 256, g)
+    xt = torch.randn(4, 4, 256, device="cuda", dtype=torch.bfloat16)
+    out = layer(xt, return_dtype=torch.bfloat16)
+    assert out.requires_grad and fast_calls == []
+    out.float().sum().backward()
+    assert layer.H_res_raw.grad is not None
+
+
+def test_cases_the_fast_path_declines_run_the_general_path(fast_calls):
+    g = rng(13)
+    layer, _ = _layer(4, 256, g)
+    base = torch.randn(4, 4, 512, device="cuda", dtype=torch.bfloat16)
+    view = base[:, :, :256]  # not contiguous
+    with torch.no_grad():
+        a = layer(view, return_dtype=torch.bfloat16)
+        b = layer(view.contiguous(), return_dtype=torch.bfloat16)
+    assert fast_calls == [False, True]
+    assert torch.equal(a, b)
+    with torch.no_grad(), pytest.raises(ValueError):
+        layer(torch.randn(4, 5, 256, device="cuda", dtype=torch.bfloat16))
+
+
+def test_library_error_in_the_fast_path_goes_to_the_general_path(monkeypatch):
+    g = rng(14)
+    layer, _ = _layer(4, 256, g)
+    xt = torch.randn(4, 4, 256, device="cuda", dtype=torch.bfloat16)
+
+    def failing(*a, **k):
+        raise _lib.MHCError("mhc_layer_fwd: HIP error 2: injected")
+
+    with torch.no_grad():
+        want = layer(xt, return_dtype=torch.bfloat16)
+        monkeypatch.setattr(ops, "layer_forward_nograd", failing)
+        got = layer(xt, return_dtype=torch.bfloat16)
+    assert torch.equal(got, want)

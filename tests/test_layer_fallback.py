@@ -147,3 +147,16 @@ def test_env_disable_is_silent(fresh_flag, monkeypatch):
         warnings.simplefilter("error")
         y = layer(x)
     assert rel_err(np_of(y), _ref_out(layer, x)) < 1e-5
+
+
+def test_nograd_cpu_call_takes_the_general_path(fresh_flag):
+    """The no-gradient fast path takes GPU tensors only; a CPU call under no_grad still falls back once."""
+    layer = _accelerated(MHCLayer(n=4, C=16, identity_init=False))
+    _randomise(layer, 4)
+    x = torch.randn(2, 4, 16)
+    assert ops.layer_forward_nograd(x, layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight,
+                                    20, 1e-5, torch.float32) is None
+    with torch.no_grad(), pytest.warns(RuntimeWarning, match="falling back to reference path") as rec:
+        y = layer(x)
+    assert len(rec) == 1 and L._METAL_FAILED is True
+    assert rel_err(np_of(y), _ref_out(layer, x)) < 1e-5
