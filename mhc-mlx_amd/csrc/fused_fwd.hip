@@ -314,7 +314,10 @@ constexpr int full_vec() {
 }
 
 template <int NMAX, typename XT, typename OT, int CH, bool RAW, bool SKF = false>
-__global__ __launch_bounds__(1024) MHC_FWD_FULL_ATTR void fused_fwd_full_kernel(FwdArgs A) {
+// (n = 8 with two chunks per thread holds 128 fp32 values of x per thread: bounded at 512 threads, so
+// 256 VGPRs, where the 1024-thread bound spilled)
+__global__ __launch_bounds__(NMAX == 8 && CH == 2 ? 512 : 1024) MHC_FWD_FULL_ATTR
+void fused_fwd_full_kernel(FwdArgs A) {
   constexpr int V = full_vec<XT, OT>();
   __shared__ float s_red[2][16];
   const int tid = threadIdx.x;
@@ -591,7 +594,7 @@ int launch_fwd_full(FwdArgs A, hipStream_t stream) {
   const int ch_pref = knob(kKnobFwdCh, 0);
   if (ch_pref == 1 || ch_pref == 2) ch = ch_pref;
   if (nchunks % (64 * ch) != 0) ch = 1;
-  if (nchunks % 64 != 0 || nchunks / ch > 1024) return 1;
+  if (nchunks % 64 != 0 || nchunks / ch > (NMAX == 8 && ch == 2 ? 512 : 1024)) return 1;
   const int tpb = nchunks / ch;
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, kMaxGrid));
   const dim3 g((unsigned)blocks), b(tpb);

@@ -24,8 +24,9 @@ FWD_SHAPES = [
     (2, 4, 128), (2, 4, 129), (1, 4, 512), (3, 3, 64), (2, 1, 40), (2, 2, 24), (2, 8, 128),
     (2, 5, 72), (2, 16, 64), (2, 16, 256), (1, 32, 256), (2, 24, 40), (1, 64, 64), (2, 4, 20000),
     # full-tile forward with two chunks per thread (more than 512 chunks: 4-channel chunks
-    # with fp32 output at C = 3072 / 4096, 8-channel chunks at C = 8192)
-    (2, 4, 4096), (2, 8, 3072), (1, 4, 8192),
+    # with fp32 output at C = 3072 / 4096, 8-channel chunks at C = 8192); n = 8 with two chunks
+    # per thread is bounded at 512 threads, so C = 16384 with 16-bit output takes the general kernel
+    (2, 4, 4096), (2, 8, 3072), (1, 4, 8192), (2, 8, 8192), (1, 8, 16384),
     # n = 16 with C a multiple of 128: the MFMA forward (one or two 128-channel slabs per wave)
     (3, 16, 128), (2, 16, 384), (2, 16, 1024), (1, 16, 2048),
 ]
