@@ -778,6 +778,14 @@ extern "C" int mhc_layer_fwd(const void* x, int x_dtype, const float* h_pre_raw,
     const int rc = layer_fwd_single_launch(A, x_dtype, out_dtype, (hipStream_t)stream);
     if (rc != 1) return rc;
   }
+  if (!per_token && n > 16 && n <= 32 && T >= 1 && iters >= 0 && x && h_pre_raw && h_post_raw && rms_weight &&
+      out && (out_dtype == MHC_DTYPE_F32 || out_dtype == x_dtype) && dtype_bytes(x_dtype) == 2) {
+    Mf32Args F{};
+    F.x = x; F.out = out; F.M = M_out; F.hpre = h_pre_raw; F.hpost = h_post_raw; F.w = rms_weight; F.T = T;
+    F.n = n; F.C = C; F.h_mode = MHC_H_RAW; F.eps = eps; F.hres = h_res_raw; F.M_out = M_out; F.iters = iters;
+    const int rc = mf32_layer_fwd_single_launch(F, x_dtype, out_dtype, (hipStream_t)stream);
+    if (rc != 1) return rc;
+  }
   const int64_t batch = per_token ? T : 1;
   if (batch > 0) {
     const int rc = mhc_sinkhorn_fwd(h_res_raw, M_out, batch, n, iters, eps, stream);

@@ -29,6 +29,7 @@
 #include "mhc_host.hpp"
 #include "mhc_mfma32.hpp"
 #include "mhc_plan.hpp"
+#include "mhc_sinkhorn.hpp"
 
 namespace mhc {
 
@@ -171,6 +172,18 @@ MHC_DEV void load_w8(const float* p, float (&wv)[8]) {
   wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
 }
 
+// The layer-wide projection inside a forward workgroup: wave 0 runs the
+// block Sinkhorn (sk_fwd_blk, the arithmetic of mhc_sinkhorn_fwd's kernel
+// for one matrix, so M is bitwise the same) into s_M ([n][n], LDS); after the
+// barrier every wave reads its parameters from there, and workgroup 0 also
+// writes M for the caller (kept for the backward).
+MHC_DEV void mf32_project_into_lds(const Mf32Args& A, float* s_M, int n, int wave, int lane) {
+  if (wave == 0) sk_fwd_blk<32, false>(A.hres, s_M, n, A.iters, A.eps, lane, nullptr);
+  __syncthreads();
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < n * n; i += blockDim.x) A.M_out[i] = s_M[i];
+}
+
 // ---------------------------------------------------------------------------
 // Forward.  One token at a time per workgroup of S / SPW waves (S = C / 128
 // slabs); the grid strides over tokens, so layer-wide parameters are split
@@ -195,9 +208,13 @@ MHC_DEV float pick_pair(const float (&v)[8], int grp, int k) {
 // x again for the mix (from the caches: the token was read just before).
 // Of y only channels 8r + 2q, 8r + 2q + 1 stay with lane group q (the four
 // groups hold the same values), gathered back after the barrier.
-template <typename XT, typename OT, int SPW, bool PT, bool RAW, bool FULL, bool RELOAD = false>
+// SKF (layer-wide, raw logits): the Sinkhorn projection runs in the kernel
+// (mf32_project_into_lds) instead of a launch of its own.
+template <typename XT, typename OT, int SPW, bool PT, bool RAW, bool FULL, bool RELOAD = false, bool SKF = false>
 __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
+  static_assert(!SKF || (!PT && RAW), "the in-kernel projection takes layer-wide raw logits");
   __shared__ float s_red[2][16];
+  __shared__ float s_M[SKF ? 32 * 32 : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -215,7 +232,7 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
   u32x4 aa[3], am[2][3];
   float pv[2][4];
   auto load_params = [&](int64_t t) {
-    const float* M = A.M + t * A.M_ts;
+    const float* M = SKF ? s_M : A.M + t * A.M_ts;
     const float* hp = A.hpre + t * A.h_ts;
     const float* hq = A.hpost + t * A.h_ts;
     float av[8];
@@ -236,6 +253,7 @@ __global__ __launch_bounds__(512) void mf32_fwd_kernel(Mf32Args A) {
       }
     }
   };
+  if constexpr (SKF) mf32_project_into_lds(A, s_M, n, wave, lane);
   if constexpr (!PT) load_params(0);
 
   int it = 0;
@@ -349,11 +367,13 @@ constexpr int kMf32FwdMaxC = 16384;
 // to LDS (512 bytes per slab); after it the lane loads the slab again (from
 // the caches: the token was read just before) and reads its channels' y
 // back for the mix.  Each wave reads back only the y it wrote itself.
-template <typename XT, typename OT, bool PT, bool RAW, bool FULL>
+template <typename XT, typename OT, bool PT, bool RAW, bool FULL, bool SKF = false>
 __global__ __launch_bounds__(512) void mf32_fwd_loop_kernel(Mf32Args A, int spw) {
+  static_assert(!SKF || (!PT && RAW), "the in-kernel projection takes layer-wide raw logits");
   extern __shared__ float4 s_y4[];  // [S][16 r][8 channels]
   float* const s_y = reinterpret_cast<float*>(s_y4);
   __shared__ float s_red[2][16];
+  __shared__ float s_M[SKF ? 32 * 32 : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -375,7 +395,7 @@ __global__ __launch_bounds__(512) void mf32_fwd_loop_kernel(Mf32Args A, int spw)
   u32x4 aa[3], am[2][3];
   float pv[2][4];
   auto load_params = [&](int64_t t) {
-    const float* M = A.M + t * A.M_ts;
+    const float* M = SKF ? s_M : A.M + t * A.M_ts;
     const float* hp = A.hpre + t * A.h_ts;
     const float* hq = A.hpost + t * A.h_ts;
     float av[8];
@@ -400,6 +420,7 @@ __global__ __launch_bounds__(512) void mf32_fwd_loop_kernel(Mf32Args A, int spw)
   // wave) are staged in LDS once and read back at each use, which keeps
   // the kernel at two 8-wave workgroups per CU
   __shared__ u32x4 s_aa[3][64], s_am[2][3][64];
+  if constexpr (SKF) mf32_project_into_lds(A, s_M, n, wave, lane);
   if constexpr (!PT) {
     load_params(0);
     if (wave == 0) {
@@ -1315,10 +1336,12 @@ int by_half(int code, F&& f) {
 
 }  // namespace
 
-int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s);
+int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s, bool skf);
 
-int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
+// skf: the single-launch layer forward (A.hres, A.M_out, A.iters; layer-wide raw parameters)
+int mf32_fused_fwd_impl(const Mf32Args& A, int xd, int od, hipStream_t s, bool skf) {
   if (A.n <= 16 || A.n > 32 || A.C % 128 != 0 || A.C > kMf32FwdMaxC) return 1;
+  if (skf && (A.M_ts != 0 || A.h_mode != MHC_H_RAW || A.hres == nullptr || A.M_out == nullptr)) return 1;
   if (od != MHC_DTYPE_F32 && od != xd) return 1;
   if (!aligned(A.x, 16) || !aligned(A.out, 16) || !aligned(A.w, 16)) return 1;
   if (knob(kKnobFwdMfma, 1) == 0) return 1;
@@ -1327,7 +1350,7 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
   // MHC_MF32_FWD_LOOP=0 keeps the register variants up to C = 4096, 2 takes
   // the loop at every C
   const int loop = knob(kKnobFwdLoop, 1);
-  if (S > 32 || (S > 16 && loop != 0) || loop == 2) return mf32_fused_fwd_loop(A, xd, od, s);
+  if (S > 32 || (S > 16 && loop != 0) || loop == 2) return mf32_fused_fwd_loop(A, xd, od, s, skf);
   // two slabs per wave up to C = 2048 (in registers across the RMS barrier),
   // four above it (read again after the barrier)
   const int spw = S <= 8 ? 1 : (S <= 16 ? 2 : 4);
@@ -1351,7 +1374,16 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
     if (full) hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, 4, PT_, RAW_, true, true>), g, b, 0, s, A);  \
     else hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, 4, PT_, RAW_, false, true>), g, b, 0, s, A);      \
   } while (0)
-      if (spw == 1) {
+#define MF32_FWD_SKF(SPW_, RELOAD_)                                                                          \
+  do {                                                                                                       \
+    if (full) hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, false, true, true, RELOAD_, true>), g, b, 0, s, A); \
+    else hipLaunchKernelGGL((mf32_fwd_kernel<XT, OT, SPW_, false, true, false, RELOAD_, true>), g, b, 0, s, A);     \
+  } while (0)
+      if (skf) {
+        if (spw == 1) MF32_FWD_SKF(1, false);
+        else if (spw == 2) MF32_FWD_SKF(2, false);
+        else MF32_FWD_SKF(4, true);
+      } else if (spw == 1) {
         if (pt) { if (raw) MF32_FWD(1, true, true); else MF32_FWD(1, true, false); }
         else { if (raw) MF32_FWD(1, false, true); else MF32_FWD(1, false, false); }
       } else if (spw == 2) {
@@ -1363,6 +1395,7 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
       }
 #undef MF32_FWD
 #undef MF32_FWD_RELOAD
+#undef MF32_FWD_SKF
       MHC_CHECK_LAUNCH("mf32_fwd_kernel");
       return MHC_OK;
     };
@@ -1372,7 +1405,7 @@ int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
 
 // The runtime-loop forward: the wave count nearest MHC_MF32_FWD_WAVES (default
 // 8) that divides the slab count, one token per workgroup at a time.
-int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s) {
+int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s, bool skf) {
   const int S = A.C / 128;
   const int target = std::min(kMf32MaxWaves, std::max(1, knob(kKnobMf32FwdWaves, 8)));
   int waves = 1;
@@ -1390,7 +1423,9 @@ int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s) {
       using OT = std::remove_pointer_t<decltype(op)>;
       with_full(full, [&](auto fc) {
         constexpr bool F = decltype(fc)::value;
-        if (pt) {
+        if (skf) {
+          hipLaunchKernelGGL((mf32_fwd_loop_kernel<XT, OT, false, true, F, true>), g, b, smem, s, A, spw);
+        } else if (pt) {
           if (raw) hipLaunchKernelGGL((mf32_fwd_loop_kernel<XT, OT, true, true, F>), g, b, smem, s, A, spw);
           else hipLaunchKernelGGL((mf32_fwd_loop_kernel<XT, OT, true, false, F>), g, b, smem, s, A, spw);
         } else {
@@ -1403,6 +1438,13 @@ int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s) {
     };
     return od == MHC_DTYPE_F32 ? go((float*)nullptr) : go((XT*)nullptr);
   });
+}
+
+int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) { return mf32_fused_fwd_impl(A, xd, od, s, false); }
+
+int mf32_layer_fwd_single_launch(const Mf32Args& A, int xd, int od, hipStream_t s) {
+  if (knob(kKnobFwdSkf, 1) == 0 || A.T < 1 || A.T > device_cu_count()) return 1;
+  return mf32_fused_fwd_impl(A, xd, od, s, true);
 }
 
 int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {

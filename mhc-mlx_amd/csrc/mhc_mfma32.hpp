@@ -25,12 +25,23 @@ struct Mf32Args {
   int P;
   int h_mode;
   float eps;
+  // forward with the Sinkhorn projection in the kernel (layer-wide, at most one token per CU): the raw
+  // logits, the iteration count and M written by workgroup 0 (null: M is read from M)
+  const float* hres;
+  float* M_out;
+  int iters;
 };
 
 // Forward (out = M x + p * rms_norm(a^T x) w) for 16 < n <= 32, 16-bit x,
 // out fp32 or x's dtype, C a multiple of 128 up to 16384, layer-wide or
 // per-token parameters.  Returns 1 when the shape is not covered.
 int mf32_fused_fwd(const Mf32Args& A, int x_dtype, int out_dtype, hipStream_t s);
+
+// The layer forward from raw parameters in one launch (A.hres, A.M_out, A.iters set; raw h, layer-wide,
+// 16 < n <= 32, at most one token per CU): every workgroup projects the logits in its wave 0 (the block
+// Sinkhorn, so M is bitwise that of mhc_sinkhorn_fwd) and workgroup 0 writes M.  Returns 1 when the
+// shape is not covered.
+int mf32_layer_fwd_single_launch(const Mf32Args& A, int x_dtype, int out_dtype, hipStream_t s);
 
 // Backward partial-sums pass for 16 < n <= 32 with layer-wide parameters,
 // 16-bit x and dout of one dtype, C a multiple of 128 up to 1024: dx, and one

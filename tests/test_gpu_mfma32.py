@@ -137,3 +137,28 @@ def test_mfma32_matches_the_generic_kernels(knobs):
         # out and dx: one bf16 rounding of fp32 values that differ in the last bits
         tol = 2.0 ** -8 if name in ("out", "dx") else 2e-5
         assert rel_err(np_of(a), np_of(b)) < tol, (name, rel_err(np_of(a), np_of(b)))
+
+
+@pytest.mark.parametrize("T,n,C", [(1, 32, 256), (1, 32, 4096), (32, 32, 512), (32, 32, 2048), (256, 32, 1024),
+                                   (1, 24, 8192), (7, 20, 3072), (2, 17, 128)])
+@pytest.mark.parametrize("xdt,odt", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
+def test_single_launch_layer_forward_matches_two_launches(T, n, C, xdt, odt, knobs):
+    """Layer-wide 16 < n <= 32 with at most one token per CU: the Sinkhorn projection runs inside the
+    forward kernel (one launch, M written by workgroup 0).  Out and M are bitwise those of the
+    projection kernel followed by the forward (MHC_FWD_SKF=0), and match the oracle."""
+    g = rng(3300 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), xdt)
+    hpre, hpost, hres, w = params(g, n, C)
+    xt = dev_tensor(x, xdt)
+    ps = [dev_tensor(v) for v in (hpre, hpost, hres, w)]
+    odtype = torch.float32 if odt == "f32" else xt.dtype
+    res = []
+    for skf in (1, 0):
+        knobs("MHC_FWD_SKF", skf)
+        out, M = ops._layer_fwd(xt, *ps, 20, EPS, odtype, False)
+        res.append((out, M))
+    torch.cuda.synchronize()
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    assert rel_err(np_of(res[0][0]), ref) < (1e-5 if odt == "f32" else TOL[odt])
+    assert rel_err(np_of(res[0][1]), O.mixing_matrix_from_logits(hres, iters=20, eps=EPS)) < 1e-5
