@@ -313,11 +313,15 @@ constexpr int full_vec() {
   return 16 / (ElemTraits<XT>::kBytes > ElemTraits<OT>::kBytes ? ElemTraits<XT>::kBytes : ElemTraits<OT>::kBytes);
 }
 
-template <int NMAX, typename XT, typename OT, int CH, bool RAW, bool SKF = false>
+// PIPE (persistent grid): the next token's loads are issued before this
+// token's RMS barrier, into a second register set, so they are in flight
+// across the barrier and the stores (the barrier waits for LDS only).
+template <int NMAX, typename XT, typename OT, int CH, bool RAW, bool SKF = false, bool PIPE = false>
 // (n = 8 with two chunks per thread holds 128 fp32 values of x per thread: bounded at 512 threads, so
 // 256 VGPRs, where the 1024-thread bound spilled)
 __global__ __launch_bounds__(NMAX == 8 && CH == 2 ? 512 : 1024) MHC_FWD_FULL_ATTR
 void fused_fwd_full_kernel(FwdArgs A) {
+  static_assert(!(PIPE && SKF), "the pipelined forward reads M");
   constexpr int V = full_vec<XT, OT>();
   __shared__ float s_red[2][16];
   const int tid = threadIdx.x;
@@ -334,24 +338,10 @@ void fused_fwd_full_kernel(FwdArgs A) {
   // (after the first token's loads are issued); block 0 stores M for the backward.
   float Mk[SKF ? NMAX * NMAX : 1];
 
-  int it = 0;
-  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
-    // the token's loads go out first; parameters and w are read while they fly
-    const XT* xt = (const XT*)A.x + t * nC;
-    OT* ot = (OT*)A.out + t * nC;
-    Vec<XT, V> xr[CH][NMAX];
-#pragma unroll
-    for (int k = 0; k < CH; ++k)
-#pragma unroll
-      for (int i = 0; i < NMAX; ++i) xr[k][i].load(xt + i * C + c0[k]);
-    if constexpr (SKF) {
-      if (it == 0) {
-        float mine;
-        sk_fwd_wave<NMAX>(A.hres, A.iters, A.eps, lane, Mk, mine);
-        if (blockIdx.x == 0 && tid < NMAX * NMAX) A.M_out[tid] = mine;
-      }
-    }
-    float Ms[NMAX * NMAX], as[NMAX], ps[NMAX];
+  // parameters and the lane's rms weights: per token (PIPE: once, before the first token's loads are waited
+  // for, since a load issued after a token's stores would wait for those stores too)
+  float Ms[NMAX * NMAX], as[NMAX], ps[NMAX], wv[CH][V];
+  auto load_params = [&]() {
 #pragma unroll
     for (int i = 0; i < NMAX; ++i) {
       float av = A.hpre[i], pv = A.hpost[i];
@@ -367,11 +357,39 @@ void fused_fwd_full_kernel(FwdArgs A) {
         else Ms[i * NMAX + j] = uniform_f(A.M[i * NMAX + j]);
       }
     }
-    float wv[CH][V];
 #pragma unroll
     for (int k = 0; k < CH; ++k)
 #pragma unroll
       for (int v = 0; v < V; ++v) wv[k][v] = A.w[c0[k] + v];
+  };
+  Vec<XT, V> xr[CH][NMAX];
+  auto load_tok = [&](Vec<XT, V> (&xa)[CH][NMAX], int64_t t) {
+    const XT* xt = (const XT*)A.x + t * nC;
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) xa[k][i].load(xt + i * C + c0[k]);
+  };
+  if constexpr (PIPE) {
+    if ((int64_t)blockIdx.x < A.T) load_tok(xr, blockIdx.x);
+    load_params();
+    // enter the loop with no loads pending (else every token's first wait would be as strict as this one)
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  }
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    // the token's loads go out first; parameters and w are read while they fly
+    OT* ot = (OT*)A.out + t * nC;
+    if constexpr (!PIPE) load_tok(xr, t);
+    if constexpr (SKF) {
+      if (it == 0) {
+        float mine;
+        sk_fwd_wave<NMAX>(A.hres, A.iters, A.eps, lane, Mk, mine);
+        if (blockIdx.x == 0 && tid < NMAX * NMAX) A.M_out[tid] = mine;
+      }
+    }
+    if constexpr (!PIPE) load_params();
 
     float y[CH][V];
     float ss = 0.0f;
@@ -388,7 +406,13 @@ void fused_fwd_full_kernel(FwdArgs A) {
     }
     ss = wave_sum(ss);
     if (lane == 0) s_red[it & 1][wave] = ss;
-    __syncthreads();
+    Vec<XT, V> xn[PIPE ? CH : 1][NMAX];
+    if constexpr (PIPE) {
+      if (t + gridDim.x < A.T) load_tok(xn, t + gridDim.x);
+      lds_barrier();
+    } else {
+      __syncthreads();
+    }
     float tot = 0.0f;
     for (int w = 0; w < nwaves; ++w) tot += s_red[it & 1][w];
     const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
@@ -410,6 +434,12 @@ void fused_fwd_full_kernel(FwdArgs A) {
         }
         store_vec<OT, V>(ot + i * C + c0[k], o);
       }
+    }
+    if constexpr (PIPE) {
+#pragma unroll
+      for (int k = 0; k < CH; ++k)
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) xr[k][i] = xn[k][i];
     }
   }
 }
@@ -596,9 +626,21 @@ int launch_fwd_full(FwdArgs A, hipStream_t stream) {
   if (nchunks % (64 * ch) != 0) ch = 1;
   if (nchunks % 64 != 0 || nchunks / ch > (NMAX == 8 && ch == 2 ? 512 : 1024)) return 1;
   const int tpb = nchunks / ch;
+  const bool raw = A.h_mode == MHC_H_RAW;
+  // n = 4: MHC_FWD_PIPE > 0 takes the pipelined kernel on a persistent grid of that many workgroups per
+  // CU.  Alone it ran config 2's forward 7-10 us faster at one workgroup per CU (two to four: slower),
+  // but the training step moved by -10, +2.5 and +0.8 us on three boxes, so it is not the default.
+  const int pipe = knob(kKnobFwdPipe, 0);
+  if (pipe > 0 && NMAX == 4 && ch == 1 && raw) {
+    // persistent pipelined grid: `pipe` workgroups per CU
+    const int64_t pb = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * pipe));
+    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1, true, false, true>), dim3((unsigned)pb), dim3(tpb), 0,
+                       stream, A);
+    MHC_CHECK_LAUNCH("fused_fwd_full_kernel");
+    return MHC_OK;
+  }
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, kMaxGrid));
   const dim3 g((unsigned)blocks), b(tpb);
-  const bool raw = A.h_mode == MHC_H_RAW;
   if (ch == 2) {
     if (raw) hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 2, true>), g, b, 0, stream, A);
     else hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 2, false>), g, b, 0, stream, A);

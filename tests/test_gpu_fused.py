@@ -254,3 +254,25 @@ def test_fused_rejects_bad_arguments():
         ops.mhc_forward_fused_hip(x, M, h, h, w, output_dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU tensors"):
         ops.mhc_forward_fused_hip(x.cpu(), M, h, h, w)
+
+
+@pytest.mark.parametrize("T,C", [(1000, 4096), (700, 1024), (300, 2048), (257, 512)])
+@pytest.mark.parametrize("xdt,odt", [("bf16", "bf16"), ("f16", "f16"), ("bf16", "f32")])
+def test_pipelined_forward_matches_per_token_workgroups(T, C, xdt, odt, knobs):
+    """n = 4 full tiles: the pipelined forward (MHC_FWD_PIPE: persistent grid, the next token's loads
+    issued before the RMS barrier) is bitwise the one-token-per-workgroup kernel, with one and three
+    workgroups per CU (several tokens per workgroup), and matches the oracle."""
+    n = 4
+    x, hpre, hpost, hres, w = _inputs(T, n, C, xdt, 4400 + T + C)
+    a, p = O.activate_pre_post(hpre, hpost, np.float32)
+    M = O.mixing_matrix_from_logits(hres, iters=20, eps=1e-5, dtype=np.float32)
+    xt = dev_tensor(x, xdt)
+    outs = []
+    for pipe in (0, 1, 3):
+        knobs("MHC_FWD_PIPE", pipe)
+        outs.append(ops.mhc_forward_fused_hip(xt, dev_tensor(M), dev_tensor(a), dev_tensor(p), dev_tensor(w),
+                                              eps=1e-5, output_dtype=None if odt == "f32" else xt.dtype))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    ref = O.mhc_forward_fused_reference(x, M, a, p, w, eps=1e-5)
+    assert rel_err(np_of(outs[1]), ref) < TOL[odt]
