@@ -557,6 +557,29 @@ __global__ __launch_bounds__(kMixThreads) void scale_fwd_kernel(MixArgs A) {
   }
 }
 
+// The pre-scale over the tensor as one flat array (whole 16-byte chunks,
+// aligned): chunk c lies in row c / nchunks, i.e. stream (c / nchunks) % n,
+// so consecutive lanes and workgroups stream consecutive memory as a plain
+// elementwise kernel does, one chunk per thread.
+template <typename XT, typename OT>
+__global__ __launch_bounds__(kMixThreads) void scale_fwd_flat_kernel(MixArgs A, uint32_t total) {
+  constexpr int V = 16 / (ElemTraits<XT>::kBytes > ElemTraits<OT>::kBytes ? ElemTraits<XT>::kBytes
+                                                                             : ElemTraits<OT>::kBytes);
+  const uint32_t c = blockIdx.x * (uint32_t)blockDim.x + threadIdx.x;
+  if (c >= total) return;
+  const XT* __restrict__ X = (const XT*)A.x;
+  OT* __restrict__ O = (OT*)A.out;
+  Vec<XT, V> xr;
+  xr.load(X + (int64_t)c * V);
+  const uint32_t i = (c / (uint32_t)A.nchunks) % (uint32_t)A.n;
+  const float hv = A.hpre[i];
+  const float a = A.h_mode == MHC_H_RAW ? sigmoidf_(hv) : hv;
+  float o[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) o[v] = a * xr.get(v);
+  store_vec<OT, V>(O + (int64_t)c * V, o);
+}
+
 // pre-scale VJP: dx_i = a_i g_i (+ acc), Sa_i = sum g_i x_i.  grid.y = stream
 // i; block (bx, i) writes column i of partial row bx.
 template <typename XT, typename GT, bool FULL>
@@ -916,11 +939,20 @@ extern "C" int mhc_stream_scale_fwd(const void* x, int x_dtype, const float* h_p
   A.vec = io_vec_ok(C, 8, {{x, dtype_bytes(x_dtype)}, {out, dtype_bytes(out_dtype)}});
   const int64_t bx = scale_grid(T, n, C, kKnobScaleFwdGrid);
   hipStream_t s = (hipStream_t)stream;
+  const int vf = 16 / std::max(dtype_bytes(x_dtype), dtype_bytes(out_dtype));
+  const int64_t flat_chunks = T * n * (int64_t)(C / vf);
+  const bool flat = knob(kKnobScaleFwdFlat, 1) != 0 && C % vf == 0 && flat_chunks < (int64_t)UINT32_MAX - kMixThreads &&
+                    io_vec_ok(C, vf, {{x, dtype_bytes(x_dtype)}, {out, dtype_bytes(out_dtype)}});
   return by_dtype(x_dtype, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
     return by_pair<XT>(out_dtype, [&](auto* op) {
       using OT = std::remove_pointer_t<decltype(op)>;
-      if (A.vec)
+      if (flat) {
+        MixArgs F = A;
+        F.nchunks = C / vf;
+        hipLaunchKernelGGL((scale_fwd_flat_kernel<XT, OT>), dim3((unsigned)ceil_div(flat_chunks, kMixThreads)),
+                           dim3(kMixThreads), 0, s, F, (uint32_t)flat_chunks);
+      } else if (A.vec)
         hipLaunchKernelGGL((scale_fwd_kernel<XT, OT, true>), dim3((unsigned)bx, (unsigned)n),
                            dim3(kMixThreads), 0, s, A);
       else

@@ -252,3 +252,29 @@ def test_rewire_shapes_and_errors():
         bad(torch.randn(1, dims, device="cuda"))
     blk = MHCRewire(torch.nn.Sequential(torch.nn.RMSNorm(1024), torch.nn.Linear(1024, 1024)), dims=1024, n=32).cuda()
     assert blk(torch.randn(1, 16, 1024, device="cuda")).shape == (1, 16, 1024)
+
+
+@pytest.mark.parametrize("T,n,C,xdt,odt", [(300, 4, 1024, "bf16", "bf16"), (7, 32, 128, "bf16", "f32"),
+                                           (5, 3, 24, "f16", "f16"), (9, 4, 64, "f32", "f32"),
+                                           (4, 5, 12, "bf16", "bf16")])
+def test_stream_scale_flat_matches_per_stream(T, n, C, xdt, odt, knobs):
+    """The pre-scale as one flat elementwise pass (16-byte chunks, the stream of each chunk from its row;
+    the default for whole aligned chunks) is bitwise the per-stream kernel (MHC_SCALE_FWD_FLAT=0), and both
+    match x * sigmoid(h).  C = 12 at 16-bit (not a whole number of 8-channel chunks) takes the per-stream
+    kernel either way."""
+    g = rng(7700 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), xdt)
+    hpre = g.standard_normal(n).astype(np.float32)
+    xt, ht = dev_tensor(x, xdt), dev_tensor(hpre)
+    outs = []
+    for flat in (1, 0):
+        knobs("MHC_SCALE_FWD_FLAT", flat)
+        with torch.no_grad():
+            o = ops.stream_scale(xt, ht)
+            if odt == "f32" and o.dtype != torch.float32:
+                o = o.float()
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    ref = x * O.sigmoid(hpre)[None, :, None]
+    assert rel_err(np_of(outs[0]), ref) < {"bf16": 2 ** -8, "f16": 2 ** -11, "f32": 1e-6}[xdt]
