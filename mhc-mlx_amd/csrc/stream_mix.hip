@@ -669,6 +669,65 @@ __global__ __launch_bounds__(kMixThreads) void scale_bwd_kernel(MixArgs A) {
   }
 }
 
+// The pre-scale VJP as a flat pass: 16-bit x and dout of one dtype, whole
+// aligned 8-channel chunks, no accumulator, nchunks a multiple of 64 and
+// n * nchunks of 256.  The grid's thread count is a multiple of n * nchunks,
+// so each thread's chunks lie in one stream and each wave's in one row;
+// block b adds its waves' sums into its partial row in wave order.
+template <typename XT>
+__global__ __launch_bounds__(kMixThreads) void scale_bwd_flat_kernel(MixArgs A, uint32_t total) {
+  constexpr int V = 8;
+  __shared__ float s_stage[kMixThreads / 64];
+  const uint32_t first = blockIdx.x * (uint32_t)kMixThreads + threadIdx.x;
+  const uint32_t stride = gridDim.x * (uint32_t)kMixThreads;
+  const uint32_t nch = (uint32_t)A.nchunks, n = (uint32_t)A.n;
+  const int i = (int)((first / nch) % n);
+  const float hv = A.hpre[i];
+  const float a = A.h_mode == MHC_H_RAW ? sigmoidf_(hv) : hv;
+  const XT* __restrict__ X = (const XT*)A.x;
+  const XT* __restrict__ Gd = (const XT*)A.g;
+  XT* __restrict__ DX = (XT*)A.out;
+  float acc = 0.0f;
+  for (uint32_t c = first; c < total; c += kScaleU * stride) {
+    Vec<XT, V> xr[kScaleU], gr[kScaleU];
+    bool on[kScaleU];
+#pragma unroll
+    for (int u = 0; u < kScaleU; ++u) {
+      const uint32_t cu = c + u * stride;
+      on[u] = cu < total;
+      if (on[u]) {
+        xr[u].load(X + (int64_t)cu * V);
+        gr[u].load(Gd + (int64_t)cu * V);
+      } else {
+        xr[u].zero();
+        gr[u].zero();
+      }
+    }
+    issue_fence();
+#pragma unroll
+    for (int u = 0; u < kScaleU; ++u) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc = fmaf(gr[u].get(v), xr[u].get(v), acc);
+      if (!on[u]) continue;
+      float o[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) o[v] = a * gr[u].get(v);
+      store_vec<XT, V>(DX + (int64_t)(c + u * stride) * V, o);
+    }
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) s_stage[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float* prow = A.part + (int64_t)blockIdx.x * A.P;
+    for (int j = 0; j < A.P; ++j) prow[j] = 0.0f;
+    for (int w = 0; w < kMixThreads / 64; ++w) {
+      const uint32_t cw = blockIdx.x * (uint32_t)kMixThreads + 64u * (uint32_t)w;
+      prow[(cw / nch) % n] += s_stage[w];
+    }
+  }
+}
+
 __global__ __launch_bounds__(64) void scale_final_kernel(const float* __restrict__ part2, int S,
                                                          int P, int n, int h_mode,
                                                          const float* __restrict__ hpre,
@@ -998,7 +1057,29 @@ extern "C" int mhc_stream_scale_bwd(const void* x, int x_dtype, const void* dout
   A.vec = io_vec_ok(C, 8, {{x, dtype_bytes(x_dtype)}, {dout, dtype_bytes(dout_dtype)},
                            {dx_accum, dtype_bytes(x_dtype)}, {dx, dtype_bytes(x_dtype)}});
   hipStream_t s = (hipStream_t)stream;
-  int rc = by_dtype(x_dtype, [&](auto* xp) {
+  // flat pass: a grid of whole multiples of n * nchunks / 256 workgroups, within the workspace's rows
+  const int64_t total = T * n * (int64_t)A.nchunks;
+  const int64_t m = (int64_t)n * A.nchunks / kMixThreads;
+  int64_t Gf = 0;
+  if (knob(kKnobScaleBwdFlat, 1) != 0 && A.vec && !dx_accum && x_dtype == dout_dtype && dtype_bytes(x_dtype) == 2 &&
+      C % 8 == 0 && A.nchunks % 64 == 0 && ((int64_t)n * A.nchunks) % kMixThreads == 0 && total < INT32_MAX)
+    Gf = std::min<int64_t>(G, total / kMixThreads) / m * m;
+  int64_t rows_used = G;
+  int rc;
+  if (Gf > 0) {
+    rows_used = Gf;
+    rc = by_dtype(x_dtype, [&](auto* xp) {
+      using XT = std::remove_pointer_t<decltype(xp)>;
+      if constexpr (ElemTraits<XT>::kBytes == 2) {
+        hipLaunchKernelGGL((scale_bwd_flat_kernel<XT>), dim3((unsigned)Gf), dim3(kMixThreads), 0, s, A,
+                           (uint32_t)total);
+        MHC_CHECK_LAUNCH("scale_bwd_flat_kernel");
+        return MHC_OK;
+      } else {
+        return set_error(MHC_ERR_INVALID_ARG, "flat pre-scale VJP needs 16-bit data");
+      }
+    });
+  } else rc = by_dtype(x_dtype, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
     return by_pair<XT>(dout_dtype, [&](auto* gp) {
       using GT = std::remove_pointer_t<decltype(gp)>;
@@ -1014,11 +1095,11 @@ extern "C" int mhc_stream_scale_bwd(const void* x, int x_dtype, const void* dout
   });
   if (rc != MHC_OK) return rc;
   float* part2 = (float*)workspace + (size_t)G * P;
-  const int S = (int)std::min<int64_t>(kMixSplit, G);
-  const int rows = (int)ceil_div(G, S);
-  const int S_used = (int)ceil_div(G, rows);
+  const int S = (int)std::min<int64_t>(kMixSplit, rows_used);
+  const int rows = (int)ceil_div(rows_used, S);
+  const int S_used = (int)ceil_div(rows_used, rows);
   hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)ceil_div(P / 4, 256), (unsigned)S_used),
-                     dim3(256), 0, s, (const float*)workspace, part2, G, P, rows);
+                     dim3(256), 0, s, (const float*)workspace, part2, rows_used, P, rows);
   MHC_CHECK_LAUNCH("reduce_rows_kernel");
   hipLaunchKernelGGL(scale_final_kernel, dim3(1), dim3(64), 0, s, part2, S_used, P, n, h_mode, h_pre,
                      dh_pre);

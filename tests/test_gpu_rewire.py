@@ -278,3 +278,29 @@ def test_stream_scale_flat_matches_per_stream(T, n, C, xdt, odt, knobs):
     assert torch.equal(outs[0], outs[1])
     ref = x * O.sigmoid(hpre)[None, :, None]
     assert rel_err(np_of(outs[0]), ref) < {"bf16": 2 ** -8, "f16": 2 ** -11, "f32": 1e-6}[xdt]
+
+
+@pytest.mark.parametrize("T,n,C,xdt", [(300, 4, 1024, "bf16"), (64, 2, 1024, "f16"), (33, 8, 512, "bf16"),
+                                       (20, 4, 2048, "bf16"), (5, 3, 128, "bf16")])
+def test_stream_scale_vjp_flat_matches_per_stream(T, n, C, xdt, knobs):
+    """The pre-scale VJP as a flat pass (16-bit x and dout, 8-channel chunks, each thread's chunks in one
+    stream) gives dx bitwise equal to the per-stream kernel's (MHC_SCALE_BWD_FLAT=0) and dH_pre within
+    fp32 summation order of it; both match the oracle.  The last shape (8 chunks per row) takes the
+    per-stream kernel either way."""
+    g = rng(7800 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), xdt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), xdt)
+    hpre = g.standard_normal(n).astype(np.float32)
+    res = []
+    for flat in (1, 0):
+        knobs("MHC_SCALE_BWD_FLAT", flat)
+        xt, ht = dev_tensor(x, xdt).requires_grad_(True), dev_tensor(hpre).requires_grad_(True)
+        ops.stream_scale(xt, ht).backward(dev_tensor(dout, xdt))
+        res.append((xt.grad, ht.grad))
+    torch.cuda.synchronize()
+    assert torch.equal(res[0][0], res[1][0])
+    assert rel_err(np_of(res[0][1]), np_of(res[1][1])) < 1e-5
+    a = O.sigmoid(hpre)
+    ref_dh = np.einsum("bic,bic->i", dout.astype(np.float64), x.astype(np.float64)) * a * (1 - a)
+    assert rel_err(np_of(res[0][1]), ref_dh) < 1e-5
+    assert rel_err(np_of(res[0][0]), dout * a[None, :, None]) < {"bf16": 2 ** -8, "f16": 2 ** -11}[xdt]
