@@ -523,6 +523,166 @@ __global__ __launch_bounds__(512) void mf32_fwd_loop_kernel(Mf32Args A, int spw)
 }
 
 // ---------------------------------------------------------------------------
+// Forward for 32 < n <= 64, layer-wide parameters: the loop kernel above
+// with the streams in two halves of 32.  Per slab the lane loads streams
+// 32h + 8q .. 32h + 8q + 7 (h = 0, 1) of channels 8r .. 8r + 7 and
+// transposes each half into B operands, so every contraction over streams
+// is two chained MFMAs (K = 32 each): y = a^T X as before, and the mix in
+// four 16-row blocks of M (rows 16I + r as the A operand, output rows
+// 16I + 4q + k in D).  The split operands of a, M (two halves, four row
+// blocks: 30 words of 16 bytes per lane) live in LDS and are read at each
+// use.  For n < 64 the row part of each stream's offset is in the lane
+// offset, so rows past n read as zero and their stores are dropped.
+// ---------------------------------------------------------------------------
+template <typename XT, typename OT, bool RAW, bool FULL>
+__global__ __launch_bounds__(512) void mf64_fwd_loop_kernel(Mf32Args A, int spw) {
+  extern __shared__ float4 s_y4[];  // [S][16 r][8 channels]
+  float* const s_y = reinterpret_cast<float*>(s_y4);
+  __shared__ float s_red[2][16];
+  __shared__ u32x4 s_aa[2][3][64], s_am[4][2][3][64];
+  __shared__ float s_pv[64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int n = FULL ? 64 : A.n;
+  const int C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  constexpr uint32_t kEs = sizeof(XT), kOs = sizeof(OT);
+  const uint32_t rowb = (uint32_t)C * kEs, orowb = (uint32_t)C * kOs;
+  const uint32_t lane_in = (uint32_t)(8 * q * C + 8 * r) * kEs;   // stream 8q (+ 32 h + e rows)
+  const uint32_t lane_out = (uint32_t)(4 * q * C + 8 * r) * kOs;  // stream 4q (+ 16 I + k rows)
+  const uint32_t tokb = (uint32_t)(nC * kEs), otokb = (uint32_t)(nC * kOs);
+
+  // split operands, written by wave 0 (one (h) or (I, h) block at a time)
+  if (wave == 0) {
+    u32x4 sp[3];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float av[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = 32 * h + 8 * q + e;
+        av[e] = j < n ? act_pre<RAW>(A.hpre[j]) : 0.0f;
+      }
+      split3x8<XT>(av, sp);
+#pragma unroll
+      for (int e = 0; e < 3; ++e) s_aa[h][e][lane] = sp[e];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const int row = 16 * I + r;
+        float mv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = 32 * h + 8 * q + e;
+          mv[e] = (row < n && j < n) ? A.M[row * n + j] : 0.0f;
+        }
+        split3x8<XT>(mv, sp);
+#pragma unroll
+        for (int e = 0; e < 3; ++e) s_am[I][h][e][lane] = sp[e];
+      }
+    }
+    s_pv[lane] = lane < n ? act_post<RAW>(A.hpost[lane]) : 0.0f;
+  }
+  __syncthreads();
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const auto rx = rows_rsrc((const XT*)A.x + t * nC, tokb);
+    const auto ro = rows_rsrc((OT*)A.out + t * nC, otokb);
+    // half h of the slab: streams 32h + 8q .. + 7 of channels 8r .. 8r+7, transposed into B operands
+    auto load_half = [&](auto aux, int slab, int h, u32x4 (&b)[8]) {
+      const uint32_t sb = (uint32_t)slab * 128 * kEs;
+      const uint32_t hb = (uint32_t)(32 * h) * rowb;
+      Vec<XT, 8> xr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        buf_load<decltype(aux)::value>(xr[e], rx, FULL ? lane_in : lane_in + hb + (uint32_t)e * rowb,
+                                       FULL ? sb + hb + (uint32_t)e * rowb : sb);
+      transpose8<XT>(xr, b);
+    };
+    float ss = 0.0f;
+    for (int s = 0; s < spw; ++s) {
+      const int slab = wave * spw + s;
+      u32x4 bx[2][8];
+      load_half(std::integral_constant<int, 0>{}, slab, 0, bx[0]);
+      load_half(std::integral_constant<int, 0>{}, slab, 1, bx[1]);
+      asm volatile("" ::: "memory");  // split operands read at each use
+      u32x4 aa[2][3];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 3; ++e) aa[h][e] = s_aa[h][e][lane];
+      float y[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        f32x4 acc = mfma_split3<XT>(aa[0], bx[0][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        acc = mfma_split3<XT>(aa[1], bx[1][v], acc);
+        y[v] = acc[0];
+        ss = fmaf(acc[0], acc[0], ss);
+      }
+      if (q == 0) {
+        float4* dst = reinterpret_cast<float4*>(s_y + (slab * 16 + r) * 8);
+        dst[0] = make_float4(y[0], y[1], y[2], y[3]);
+        dst[1] = make_float4(y[4], y[5], y[6], y[7]);
+      }
+    }
+    ss = q == 0 ? ss : 0.0f;
+    ss = wave_sum(ss);
+    if (lane == 0) s_red[it & 1][wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < nwaves; ++w) tot += s_red[it & 1][w];
+    const float inv = 1.0f / sqrtf(tot / (float)C + A.eps);
+    if (A.inv_rms != nullptr && tid == 0) A.inv_rms[t] = inv;
+    for (int s = 0; s < spw; ++s) {
+      const int slab = wave * spw + s;
+      u32x4 bx[2][8];
+      load_half(std::integral_constant<int, kBufNt>{}, slab, 0, bx[0]);
+      load_half(std::integral_constant<int, kBufNt>{}, slab, 1, bx[1]);
+      const float4* src = reinterpret_cast<const float4*>(s_y + (slab * 16 + r) * 8);
+      const float4 y0 = src[0], y1 = src[1];
+      const float y[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+      float wv[8];
+      load_w8(A.w + slab * 128 + 8 * r, wv);
+      float yn[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) yn[v] = (y[v] * inv) * wv[v];
+      const uint32_t sob = (uint32_t)slab * 128 * kOs;
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        u32x4 am[2][3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 3; ++e) am[h][e] = s_am[I][h][e][lane];
+        float pv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pv[k] = s_pv[16 * I + 4 * q + k];
+        OutRows<OT> rows;
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = mfma_split3<XT>(am[0], bx[0][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+          acc = mfma_split3<XT>(am[1], bx[1][v], acc);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc[k] = fmaf(yn[v], pv[k], acc[k]);
+          if (v & 1) rows.put(v >> 1, even, acc);
+          else even = acc;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t ro_row = (uint32_t)(16 * I + k) * orowb;
+          rows.store_buf(k, ro, FULL ? lane_out : lane_out + ro_row, FULL ? sob + ro_row : sob);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Backward, layer-wide parameters.  A persistent workgroup of C / 128 waves
 // walks tokens t = b, b + G, ...; per token and slab:
 //   before the RMS barrier: y = a^T X, dyn = p^T G (MFMA), the two per-token
@@ -1440,7 +1600,44 @@ int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s, bool s
   });
 }
 
-int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) { return mf32_fused_fwd_impl(A, xd, od, s, false); }
+// 32 < n <= 64, layer-wide parameters: mf64_fwd_loop_kernel (W waves near MHC_MF32_FWD_WAVES walking
+// the slabs, C a multiple of 128 up to 8192: the y buffer and the split operands fit in LDS).
+int mf64_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
+  if (A.n <= 32 || A.n > 64 || A.C % 128 != 0 || A.C > 8192 || A.M_ts != 0) return 1;
+  if (od != MHC_DTYPE_F32 && od != xd) return 1;
+  if (!aligned(A.x, 16) || !aligned(A.out, 16) || !aligned(A.w, 16)) return 1;
+  if (knob(kKnobFwdMfma, 1) == 0) return 1;
+  const int S = A.C / 128;
+  const int target = std::min(kMf32MaxWaves, std::max(1, knob(kKnobMf32FwdWaves, 8)));
+  int waves = 1;
+  for (int w = 1; w <= kMf32MaxWaves; ++w)
+    if (S % w == 0 && std::abs(w - target) < std::abs(waves - target)) waves = w;
+  const int spw = S / waves;
+  const size_t smem = (size_t)S * 16 * 8 * sizeof(float);
+  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;
+  const int per_cu = knob(kKnobFwdGrid, 8);
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * std::max(per_cu, 1)));
+  const dim3 g((unsigned)blocks), b(waves * 64);
+  return by_half(xd, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    auto go = [&](auto* op) {
+      using OT = std::remove_pointer_t<decltype(op)>;
+      with_full(full, [&](auto fc) {
+        constexpr bool F = decltype(fc)::value;
+        if (raw) hipLaunchKernelGGL((mf64_fwd_loop_kernel<XT, OT, true, F>), g, b, smem, s, A, spw);
+        else hipLaunchKernelGGL((mf64_fwd_loop_kernel<XT, OT, false, F>), g, b, smem, s, A, spw);
+      });
+      MHC_CHECK_LAUNCH("mf64_fwd_loop_kernel");
+      return MHC_OK;
+    };
+    return od == MHC_DTYPE_F32 ? go((float*)nullptr) : go((XT*)nullptr);
+  });
+}
+
+int mf32_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
+  if (A.n > 32) return mf64_fused_fwd(A, xd, od, s);
+  return mf32_fused_fwd_impl(A, xd, od, s, false);
+}
 
 int mf32_layer_fwd_single_launch(const Mf32Args& A, int xd, int od, hipStream_t s) {
   if (knob(kKnobFwdSkf, 1) == 0 || A.T < 1 || A.T > device_cu_count()) return 1;

@@ -162,3 +162,28 @@ def test_single_launch_layer_forward_matches_two_launches(T, n, C, xdt, odt, kno
     ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
     assert rel_err(np_of(res[0][0]), ref) < (1e-5 if odt == "f32" else TOL[odt])
     assert rel_err(np_of(res[0][1]), O.mixing_matrix_from_logits(hres, iters=20, eps=EPS)) < 1e-5
+
+
+@pytest.mark.parametrize("T,n,C", [(5, 64, 128), (40, 64, 512), (7, 48, 384), (9, 33, 256), (3, 64, 1024),
+                                   (4, 64, 2048), (2, 40, 4096), (1, 64, 8192), (300, 64, 256), (6, 56, 1280)])
+@pytest.mark.parametrize("xdt,odt", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
+@pytest.mark.parametrize("grid", [None, 1])
+def test_mfma64_forward(T, n, C, xdt, odt, grid, knobs):
+    """32 < n <= 64 with layer-wide parameters on MFMA (mf64_fwd_loop_kernel: two 32-stream halves chained
+    per contraction, four 16-row blocks of M), C a multiple of 128 up to 8192, against the oracle; with
+    MHC_FWD_GRID=1 every workgroup walks several tokens."""
+    if grid is not None:
+        knobs("MHC_FWD_GRID", grid)
+    g = rng(6400 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), xdt)
+    hpre, hpost, hres, w = params(g, n, C)
+    xt = dev_tensor(x, xdt)
+    ps = [dev_tensor(v) for v in (hpre, hpost, hres, w)]
+    with torch.no_grad():
+        out = ops.mhc_layer_forward(xt, *ps, sinkhorn_iters=20, eps=EPS,
+                                    output_dtype=None if odt == "f32" else xt.dtype)
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    got = np_of(out)
+    assert rel_err(got, ref) < (1e-5 if odt == "f32" else TOL[odt]), rel_err(got, ref)
+    if odt != "f32":
+        _ulp_bound(got, ref, odt)
