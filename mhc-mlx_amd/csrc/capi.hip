@@ -90,7 +90,7 @@ const char* const kKnobNames[kNumKnobs] = {
     "MHC_SK16", "MHC_SK16_CPL", "MHC_SK16_RECORD",
     "MHC_RES_GRID", "MHC_MIX_FWD_GRID", "MHC_MIX_BWD_GRID", "MHC_SCALE_FWD_GRID", "MHC_SCALE_BWD_GRID",
     "MHC_BWD_PIPE", "MHC_MIX32", "MHC_MF32_WAVES", "MHC_SK_BLK_RECORD", "MHC_MF32_FWD_LOOP",
-    "MHC_MF32_FWD_WAVES", "MHC_FWD_PIPE", "MHC_SCALE_FWD_FLAT", "MHC_SCALE_BWD_FLAT",
+    "MHC_MF32_FWD_WAVES", "MHC_FWD_PIPE", "MHC_SCALE_FWD_FLAT", "MHC_SCALE_BWD_FLAT", "MHC_GEN_MFMA",
 };
 std::atomic<int> g_knobs[kNumKnobs];
 

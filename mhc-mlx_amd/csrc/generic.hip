@@ -5,6 +5,8 @@
 // from LDS; parameter-gradient sums are 4 x 4 outer-product blocks, one per
 // wavefront.  The kernels in fused_fwd.hip / fused_bwd.hip / stream_mix.hip
 // cover n <= 16.
+#include <type_traits>
+
 #include "mhc_device.hpp"
 #include "mhc_generic.hpp"
 #include "mhc_host.hpp"
@@ -126,8 +128,41 @@ __global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(GenArgs A) {
 //          the wave sums into the block's entries: in LDS across tokens for
 //          layer-wide parameters, or straight to the per-token outputs.
 //          Each entry belongs to one wavefront, so the order is fixed.
-template <typename XT, typename GT, int NMAX>
+// 16 x 16 x 32 MFMA of 16-bit operands (eight elements per lane), fp32 accumulation.
+typedef __bf16 gen_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 gen_f16x8 __attribute__((ext_vector_type(8)));
+template <typename T>
+MHC_DEV f32x4 gen_mfma(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (std::is_same<T, __bf16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gen_bf16x8, a), __builtin_bit_cast(gen_bf16x8, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(gen_f16x8, a), __builtin_bit_cast(gen_f16x8, b), c,
+                                                  0, 0, 0);
+}
+
+// MF (16-bit x and dout of one dtype, C a multiple of 32, 16-byte aligned
+// rows): pass 3's dM = G X^T runs on MFMA in 16 x 16 blocks of (stream i,
+// stream j), each block owned by one wavefront for the whole kernel (at most
+// kGenMfBlk per wave), K = 32 channels per v_mfma_f32_16x16x32: lane
+// (q = lane >> 4, r = lane & 15) reads channels 32k + 8q .. + 7 of g row
+// 16I + r and of x row 16J + r (rows past n as zero) and holds dM entries
+// (16I + 4q + e, 16J + r).  The rows were just read by passes 1 and 2, so
+// these reads come from the caches.  dA and dP (the extended row and column
+// of the outer product) are dot products over the channels, one wavefront
+// each.  Every sum has one owner, so the order is fixed.
+template <int NMAX>
+constexpr int gen_mf_blocks() {
+  return ((NMAX / 16) * (NMAX / 16) + gen_bwd_threads(NMAX) / 64 - 1) / (gen_bwd_threads(NMAX) / 64);
+}
+
+template <typename XT, typename GT, int NMAX, bool MF = false>
 __global__ __launch_bounds__(gen_bwd_threads(NMAX)) void gen_bwd_kernel(GenArgs A) {
+  static_assert(!MF || (std::is_same<XT, GT>::value && sizeof(XT) == 2), "MFMA pass 3 takes 16-bit x == dout");
+  constexpr int kMfBlk = gen_mf_blocks<NMAX>();
+  f32x4 dmb[MF ? kMfBlk : 1];
+#pragma unroll
+  for (int b = 0; b < (MF ? kMfBlk : 1); ++b) dmb[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   constexpr int NE = NMAX + 1;  // extended rows / columns
   __shared__ float s_par[kGenMaxPar];
   __shared__ __align__(16) float s_MT[NMAX * NMAX];
@@ -200,6 +235,60 @@ __global__ __launch_bounds__(gen_bwd_threads(NMAX)) void gen_bwd_kernel(GenArgs 
       }
     }
     __syncthreads();  // sdy / syn visible to the workgroup
+    if constexpr (MF) {
+      const int q = lane >> 4, r = lane & 15;
+      const int nbk = (n + 15) / 16;
+#pragma unroll
+      for (int b = 0; b < kMfBlk; ++b) {
+        const int blk = wave + b * nwaves;
+        if (blk >= nbk * nbk) break;
+        const int I = blk / nbk, J = blk % nbk;
+        const int gi = 16 * I + r, xj = 16 * J + r;
+        const XT* grow = (const XT*)gt + (int64_t)(gi < n ? gi : 0) * C + 8 * q;
+        const XT* xrow = xt + (int64_t)(xj < n ? xj : 0) * C + 8 * q;
+        f32x4 acc = A.M_ts ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : dmb[b];
+        for (int k = 0; k < C; k += 32) {
+          const u32x4 zero = {0u, 0u, 0u, 0u};
+          const u32x4 ga = gi < n ? *reinterpret_cast<const u32x4*>(grow + k) : zero;
+          const u32x4 xb = xj < n ? *reinterpret_cast<const u32x4*>(xrow + k) : zero;
+          acc = gen_mfma<XT>(ga, xb, acc);
+        }
+        if (A.M_ts) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = 16 * I + 4 * q + e, j = 16 * J + r;
+            if (i < n && j < n) A.dM_tok[t * nn + i * n + j] = acc[e];
+          }
+        } else {
+          dmb[b] = acc;
+        }
+      }
+      // dA_j = sum dy x_j (e < n), dP_i = sum g_i yn (e >= n): one wavefront per dot product
+      for (int e = wave; e < 2 * n; e += nwaves) {
+        const bool da = e < n;
+        const int j = da ? e : e - n;
+        float acc = 0.0f;
+        for (int c = lane; c < C; c += 64)
+          acc = da ? fmaf(sdy[c], load1<XT>(xt + (int64_t)j * C + c), acc)
+                   : fmaf(load1<GT>(gt + (int64_t)j * C + c), syn[c], acc);
+        const float v = wave_sum(acc);
+        if (lane != 0) continue;
+        if (A.M_ts) {
+          if (da) {
+            const float av = s_par[nn + j];
+            A.dpre_tok[t * n + j] = A.h_mode == MHC_H_RAW ? v * av * (1.0f - av) : v;
+          } else {
+            const float pq = s_par[nn + n + j];
+            A.dpost_tok[t * n + j] = A.h_mode == MHC_H_RAW ? v * pq * (1.0f - 0.5f * pq) : v;
+          }
+        } else if (da) {
+          s_acc[n * NE + j] += v;
+        } else {
+          s_acc[j * NE + n] += v;
+        }
+      }
+      continue;
+    }
     for (int blk = wave; blk < nb * nb; blk += nwaves) {
       const int r0 = (blk / nb) * 4, c0 = (blk % nb) * 4;
       float acc[16];
@@ -233,6 +322,24 @@ __global__ __launch_bounds__(gen_bwd_threads(NMAX)) void gen_bwd_kernel(GenArgs 
           }
         } else {
           s_acc[i * NE + j] += v;
+        }
+      }
+    }
+  }
+  if constexpr (MF) {
+    // the blocks of dM into s_acc (each entry written by its one owner)
+    if (!A.M_ts) {
+      const int q = lane >> 4, r = lane & 15;
+      const int nbk = (n + 15) / 16;
+#pragma unroll
+      for (int b = 0; b < kMfBlk; ++b) {
+        const int blk = wave + b * nwaves;
+        if (blk >= nbk * nbk) break;
+        const int I = blk / nbk, J = blk % nbk;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * I + 4 * q + e, j = 16 * J + r;
+          if (i < n && j < n) s_acc[i * NE + j] = dmb[b][e];
         }
       }
     }
@@ -437,12 +544,33 @@ int gen_fused_bwd(const GenArgs& A, int xd, int gd, hipStream_t s, int64_t* num_
     using XT = std::remove_pointer_t<decltype(xp)>;
     return by_pair<XT>(gd, [&](auto* gp) {
       using GT = std::remove_pointer_t<decltype(gp)>;
-      if (A.n <= 32)
+      // pass 3 on MFMA: 16-bit x == dout, C a multiple of 32, 16-byte aligned rows
+      bool mf = false;
+      if constexpr (std::is_same<XT, GT>::value && sizeof(XT) == 2)
+        mf = knob(kKnobGenMfma, 1) != 0 && A.C % 32 == 0 && aligned(A.x, 16) && aligned(A.g, 16);
+      if (A.n <= 32) {
+        if constexpr (std::is_same<XT, GT>::value && sizeof(XT) == 2) {
+          if (mf) {
+            hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 32, true>), dim3((unsigned)blocks), dim3(gen_bwd_threads(32)),
+                               0, s, A);
+            MHC_CHECK_LAUNCH("gen_bwd_kernel");
+            return MHC_OK;
+          }
+        }
         hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 32>), dim3((unsigned)blocks), dim3(gen_bwd_threads(32)), 0, s,
                            A);
-      else
+      } else {
+        if constexpr (std::is_same<XT, GT>::value && sizeof(XT) == 2) {
+          if (mf) {
+            hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 64, true>), dim3((unsigned)blocks), dim3(gen_bwd_threads(64)),
+                               0, s, A);
+            MHC_CHECK_LAUNCH("gen_bwd_kernel");
+            return MHC_OK;
+          }
+        }
         hipLaunchKernelGGL((gen_bwd_kernel<XT, GT, 64>), dim3((unsigned)blocks), dim3(gen_bwd_threads(64)), 0, s,
                            A);
+      }
       MHC_CHECK_LAUNCH("gen_bwd_kernel");
       return MHC_OK;
     });

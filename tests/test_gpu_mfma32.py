@@ -187,3 +187,36 @@ def test_mfma64_forward(T, n, C, xdt, odt, grid, knobs):
     assert rel_err(got, ref) < (1e-5 if odt == "f32" else TOL[odt]), rel_err(got, ref)
     if odt != "f32":
         _ulp_bound(got, ref, odt)
+
+
+@pytest.mark.parametrize("T,n,C,per_token", [(50, 64, 256, False), (20, 48, 512, False), (33, 33, 96, False),
+                                             (300, 40, 128, False), (16, 24, 160, True), (9, 64, 64, True),
+                                             (12, 32, 256, True), (7, 20, 40, False)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_generic_backward_mfma_parameter_sums(T, n, C, per_token, dt, knobs):
+    """The generic backward (n > 32, per-token n > 16, and C that the n <= 32 MFMA kernels do not take)
+    forms dM = G X^T on MFMA for 16-bit x == dout with C a multiple of 32 (MHC_GEN_MFMA=0: the VALU
+    outer-product blocks).  dx is bitwise the same either way (the dx pass is shared), every parameter
+    gradient agrees to fp32 summation order, and both match the oracle."""
+    g = rng(6500 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T if per_token else None)
+    fn = ops.mhc_layer_forward_dynamic if per_token else ops.mhc_layer_forward
+    res = []
+    for mf in (1, 0):
+        knobs("MHC_GEN_MFMA", mf)
+        knobs("MHC_SK_BLK_RECORD", 0)  # the same (recomputing) Sinkhorn VJP both times
+        xt = dev_tensor(x, dt).requires_grad_(True)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        out = fn(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+        out.backward(dev_tensor(dout, dt))
+        res.append([xt.grad] + [p.grad for p in ps])
+    torch.cuda.synchronize()
+    assert torch.equal(res[0][0], res[1][0])
+    for a, b in zip(res[0][1:], res[1][1:]):
+        assert rel_err(np_of(a), np_of(b)) < 1e-5
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    assert rel_err(np_of(res[0][0]), refs[0]) < TOL[dt]
+    for got, ref in zip(res[0][1:], refs[1:]):
+        assert rel_err(np_of(got), ref) < 1e-4
