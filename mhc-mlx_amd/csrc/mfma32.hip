@@ -1003,6 +1003,303 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 }
 
 // ---------------------------------------------------------------------------
+// Backward for 32 < n <= 64, layer-wide parameters, 16-bit x == dout, C a
+// multiple of 128 up to 4096.  A persistent workgroup of W waves walks
+// tokens; each wave takes SPW slabs of 128 channels.  Per token:
+//   A (per slab): x and g as two 32-stream halves, transposed into B
+//     operands; y = a^T X and dyn = p^T G on MFMA (two chained halves, split3
+//     parameters); the token sums sum y^2 and sum dyn y w; y and dyn of the
+//     slab's channels to LDS.
+//   RMS barrier.
+//   B (per slab): dy and yn per channel (overwriting y and dyn in LDS), the
+//     dw term added to the workgroup's partial row, g read again and
+//     dx = M^T G + a dy on MFMA in four 16-row blocks, stored as 16-byte rows.
+//   barrier, then C: dM = G X^T in 16 x 16 blocks owned by the waves for the
+//     whole kernel (operands read as 16-byte pieces of the token's rows, from
+//     the caches), and dA_j = sum dy x_j, dP_i = sum g_i yn as lane partial
+//     sums, one wave per (row, kind), kept across the tokens.
+// Every sum has one owner and a fixed order.  Rows past n (n < 64) read as
+// zero and their stores are dropped (the row part of the offset is in the
+// lane offset, which the buffer range check covers).
+// ---------------------------------------------------------------------------
+constexpr int kMf64BwdMaxC = 4096;
+
+template <typename XT, bool RAW, bool FULL>
+__global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
+  extern __shared__ float4 s_yd4[];  // [2][S][16 r][8]: y then dyn (phase B: dy then yn)
+  float* const s_y = reinterpret_cast<float*>(s_yd4);
+  __shared__ float s_red[2][2][16];
+  __shared__ u32x4 s_aa[2][3][64], s_ap[2][3][64], s_amt[4][2][3][64];
+  __shared__ float s_a[64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int n = FULL ? 64 : A.n;
+  const int C = A.C;
+  const int S = C / 128;
+  float* const s_d = s_y + S * 128;
+  const int64_t nC = (int64_t)n * C;
+  constexpr uint32_t kEs = sizeof(XT);
+  const uint32_t rowb = (uint32_t)C * kEs;
+  const uint32_t lane_in = (uint32_t)(8 * q * C + 8 * r) * kEs;   // stream 8q (+ 32 h + e rows)
+  const uint32_t lane_out = (uint32_t)(4 * q * C + 8 * r) * kEs;  // stream 4q (+ 16 J + k rows)
+  const uint32_t tokb = (uint32_t)(nC * kEs);
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+
+  // parameters, split once by wave 0
+  if (wave == 0) {
+    u32x4 sp[3];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float av[8], pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 32 * h + 8 * q + e;
+        av[e] = i < n ? act_pre<RAW>(A.hpre[i]) : 0.0f;
+        pv[e] = i < n ? act_post<RAW>(A.hpost[i]) : 0.0f;
+      }
+      split3x8<XT>(av, sp);
+#pragma unroll
+      for (int e = 0; e < 3; ++e) s_aa[h][e][lane] = sp[e];
+      split3x8<XT>(pv, sp);
+#pragma unroll
+      for (int e = 0; e < 3; ++e) s_ap[h][e][lane] = sp[e];
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        const int j = 16 * J + r;
+        float mv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 32 * h + 8 * q + e;
+          mv[e] = (i < n && j < n) ? A.M[i * n + j] : 0.0f;
+        }
+        split3x8<XT>(mv, sp);
+#pragma unroll
+        for (int e = 0; e < 3; ++e) s_amt[J][h][e][lane] = sp[e];
+      }
+    }
+    s_a[lane] = lane < n ? act_pre<RAW>(A.hpre[lane]) : 0.0f;
+  }
+  for (int c = tid; c < A.P; c += blockDim.x) prow[c] = 0.0f;  // dw accumulates here across tokens
+  __syncthreads();
+
+  // phase C ownership: dM blocks wave + b * nwaves (16 blocks, at most 4 per wave: nwaves >= 4) in
+  // registers; dot products e = wave + k * nwaves (2n), added per token into s_dap (one owner each)
+  constexpr int kBlkW = 4;
+  f32x4 dmb[kBlkW];
+  const int nblk_w = (16 - wave + nwaves - 1) / nwaves;
+#pragma unroll
+  for (int b = 0; b < kBlkW; ++b) dmb[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  __shared__ float s_dap[128];
+  for (int e = tid; e < 128; e += blockDim.x) s_dap[e] = 0.0f;
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const XT* xt = (const XT*)A.x + t * nC;
+    const XT* gt = (const XT*)A.g + t * nC;
+    const auto rx = rows_rsrc(xt, tokb);
+    const auto rg = rows_rsrc(gt, tokb);
+    const auto rdx = rows_rsrc((XT*)A.out + t * nC, tokb);
+    auto load_half = [&](auto aux, const __amdgpu_buffer_rsrc_t& rs, int slab, int h, u32x4 (&b)[8]) {
+      const uint32_t sb = (uint32_t)slab * 128 * kEs;
+      const uint32_t hb = (uint32_t)(32 * h) * rowb;
+      Vec<XT, 8> xr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        buf_load<decltype(aux)::value>(xr[e], rs, FULL ? lane_in : lane_in + hb + (uint32_t)e * rowb,
+                                       FULL ? sb + hb + (uint32_t)e * rowb : sb);
+      transpose8<XT>(xr, b);
+    };
+    // ---- phase A
+    float ss = 0.0f, sr = 0.0f;
+    for (int s = 0; s < spw; ++s) {
+      const int slab = wave * spw + s;
+      float y[8], dyn[8];
+      {
+        u32x4 bx[2][8];
+        load_half(std::integral_constant<int, 0>{}, rx, slab, 0, bx[0]);
+        load_half(std::integral_constant<int, 0>{}, rx, slab, 1, bx[1]);
+        asm volatile("" ::: "memory");
+        u32x4 aa[2][3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 3; ++e) aa[h][e] = s_aa[h][e][lane];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = mfma_split3<XT>(aa[0], bx[0][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+          acc = mfma_split3<XT>(aa[1], bx[1][v], acc);
+          y[v] = acc[0];
+        }
+      }
+      {
+        u32x4 bg[2][8];
+        load_half(std::integral_constant<int, 0>{}, rg, slab, 0, bg[0]);
+        load_half(std::integral_constant<int, 0>{}, rg, slab, 1, bg[1]);
+        asm volatile("" ::: "memory");
+        u32x4 ap[2][3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 3; ++e) ap[h][e] = s_ap[h][e][lane];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = mfma_split3<XT>(ap[0], bg[0][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+          acc = mfma_split3<XT>(ap[1], bg[1][v], acc);
+          dyn[v] = acc[0];
+        }
+      }
+      float wv[8];
+      load_w8(A.w + slab * 128 + 8 * r, wv);
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        ss = fmaf(y[v], y[v], ss);
+        sr = fmaf(dyn[v] * y[v], wv[v], sr);
+      }
+      if (q == 0) {
+        float4* dy4 = reinterpret_cast<float4*>(s_y + (slab * 16 + r) * 8);
+        float4* dd4 = reinterpret_cast<float4*>(s_d + (slab * 16 + r) * 8);
+        dy4[0] = make_float4(y[0], y[1], y[2], y[3]);
+        dy4[1] = make_float4(y[4], y[5], y[6], y[7]);
+        dd4[0] = make_float4(dyn[0], dyn[1], dyn[2], dyn[3]);
+        dd4[1] = make_float4(dyn[4], dyn[5], dyn[6], dyn[7]);
+      }
+    }
+    // the four lane groups q hold the same y and dyn: count them once
+    ss = q == 0 ? ss : 0.0f;
+    sr = q == 0 ? sr : 0.0f;
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    __syncthreads();
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+    // ---- phase B
+    for (int s = 0; s < spw; ++s) {
+      const int slab = wave * spw + s;
+      float* yp = s_y + (slab * 16 + r) * 8;
+      float* dp = s_d + (slab * 16 + r) * 8;
+      const float4 y0 = reinterpret_cast<const float4*>(yp)[0], y1 = reinterpret_cast<const float4*>(yp)[1];
+      const float4 d0 = reinterpret_cast<const float4*>(dp)[0], d1 = reinterpret_cast<const float4*>(dp)[1];
+      const float y[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+      const float dyn[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      float wv[8];
+      load_w8(A.w + slab * 128 + 8 * r, wv);
+      float dy[8], yn[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const float yi = y[v] * inv;
+        dy[v] = dyn[v] * inv * wv[v] - kf * y[v];
+        yn[v] = yi * wv[v];
+      }
+      if (q == 0) {
+        float* pw = prow + slab * 128 + 8 * r;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) pw[v] = fmaf(dyn[v], y[v] * inv, pw[v]);
+        reinterpret_cast<float4*>(yp)[0] = make_float4(dy[0], dy[1], dy[2], dy[3]);
+        reinterpret_cast<float4*>(yp)[1] = make_float4(dy[4], dy[5], dy[6], dy[7]);
+        reinterpret_cast<float4*>(dp)[0] = make_float4(yn[0], yn[1], yn[2], yn[3]);
+        reinterpret_cast<float4*>(dp)[1] = make_float4(yn[4], yn[5], yn[6], yn[7]);
+      }
+      u32x4 bg[2][8];
+      load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 0, bg[0]);
+      load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 1, bg[1]);
+      const uint32_t sob = (uint32_t)slab * 128 * kEs;
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        u32x4 amt[2][3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 3; ++e) amt[h][e] = s_amt[J][h][e][lane];
+        float a4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a4[k] = s_a[16 * J + 4 * q + k];
+        OutRows<XT> rows;
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = {a4[0] * dy[v], a4[1] * dy[v], a4[2] * dy[v], a4[3] * dy[v]};
+          acc = mfma_split3<XT>(amt[0], bg[0][v], acc);
+          acc = mfma_split3<XT>(amt[1], bg[1][v], acc);
+          if (v & 1) rows.put(v >> 1, even, acc);
+          else even = acc;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t row = (uint32_t)(16 * J + k) * rowb;
+          rows.store_buf(k, rdx, FULL ? lane_out : lane_out + row, FULL ? sob + row : sob);
+        }
+      }
+    }
+    __syncthreads();  // dy and yn of every slab in LDS
+    // ---- phase C: dM blocks
+#pragma unroll
+    for (int b = 0; b < kBlkW; ++b) {
+      if (b >= nblk_w) break;
+      const int blk = wave + b * nwaves;
+      const int I = blk >> 2, J = blk & 3;
+      const int gi = 16 * I + r, xj = 16 * J + r;
+      const XT* grow = gt + (int64_t)(gi < n ? gi : 0) * C + 8 * q;
+      const XT* xrow = xt + (int64_t)(xj < n ? xj : 0) * C + 8 * q;
+      f32x4 acc = dmb[b];
+      for (int k = 0; k < C; k += 32) {
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        const u32x4 ga = gi < n ? *reinterpret_cast<const u32x4*>(grow + k) : zero;
+        const u32x4 xb = xj < n ? *reinterpret_cast<const u32x4*>(xrow + k) : zero;
+        acc = mfma32k<XT>(ga, xb, acc);
+      }
+      dmb[b] = acc;
+    }
+    // dA_j (e < n) and dP_i (e >= n): wave sums over the channels, added into s_dap by their owner
+    for (int e = wave; e < 2 * n; e += nwaves) {
+      const bool da = e < n;
+      const int j = da ? e : e - n;
+      const XT* row = (da ? xt : gt) + (int64_t)j * C;
+      const float* other = da ? s_y : s_d;
+      float acc = 0.0f;
+      for (int c = 8 * lane; c < C; c += 512) {  // eight channels per lane: one 16-byte load
+        Vec<XT, 8> xv;
+        xv.load(row + c);
+        const float4 o0 = *reinterpret_cast<const float4*>(other + c);
+        const float4 o1 = *reinterpret_cast<const float4*>(other + c + 4);
+        const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+#pragma unroll
+        for (int v = 0; v < 8; ++v) acc = fmaf(ov[v], xv.get(v), acc);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) s_dap[e] += acc;
+    }
+    __syncthreads();  // phase C done with dy / yn before the next token's phase A writes y / dyn
+  }
+
+  // ---- partial row: [dw C | 0 .. Cp | dM n*n | dA n | dP n | 0 .. P]
+#pragma unroll
+  for (int b = 0; b < kBlkW; ++b) {
+    if (b >= nblk_w) break;
+    const int blk = wave + b * nwaves;
+    const int I = blk >> 2, J = blk & 3;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = 16 * I + 4 * q + k, j = 16 * J + r;
+      if (i < n && j < n) prow[A.Cp + i * n + j] = dmb[b][k];
+    }
+  }
+  for (int e = tid; e < 2 * n; e += blockDim.x) prow[A.Cp + n * n + e] = s_dap[e];  // dA, then dP
+}
+
+// ---------------------------------------------------------------------------
 // Backward for 16 < n <= 32 above C = 1024 (layer-wide): SPW slabs per wave,
 // up to 8 waves.  A token's slabs do not fit in registers across the
 // RMS barrier, so the work splits around it:
@@ -1644,7 +1941,48 @@ int mf32_layer_fwd_single_launch(const Mf32Args& A, int xd, int od, hipStream_t 
   return mf32_fused_fwd_impl(A, xd, od, s, true);
 }
 
+// 32 < n <= 64 (mf64_bwd_kernel): the wave count nearest MHC_MF32_WAVES (default 8) dividing the slab
+// count, two workgroups per CU when they fit.
+int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
+  if (A.n <= 32 || A.n > 64 || A.M_ts != 0 || A.C % 128 != 0 || A.C > kMf64BwdMaxC) return 1;
+  if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
+  if (A.P != A.Cp + round_up(A.n * A.n + 2 * A.n, 4)) return 1;
+  if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.out, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
+    return 1;
+  if (knob(kKnobBwdMfma, 1) == 0) return 1;
+  const int S = A.C / 128;
+  const int target = std::min(kMf32MaxWaves, std::max(4, knob(kKnobMf32Waves, 8)));
+  int waves = 0;
+  for (int w = 4; w <= kMf32MaxWaves; ++w)
+    if (S % w == 0 && (waves == 0 || std::abs(w - target) < std::abs(waves - target))) waves = w;
+  if (waves == 0) return 1;  // fewer than four slabs, or no split into 4 to 8 waves
+  const int spw = S / waves;
+  const size_t smem = (size_t)2 * S * 128 * sizeof(float);
+  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;
+  return by_half(xd, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    const void* kfn = full ? (raw ? (const void*)mf64_bwd_kernel<XT, true, true> : (const void*)mf64_bwd_kernel<XT, false, true>)
+                           : (raw ? (const void*)mf64_bwd_kernel<XT, true, false> : (const void*)mf64_bwd_kernel<XT, false, false>);
+    const int occ = occupancy_blocks(kfn, waves * 64, smem);
+    if (occ <= 0) return 1;
+    int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
+    const int grid_pref = knob(kKnobBwdGrid, 0);
+    if (grid_pref > 0) blocks = std::min<int64_t>(gmax, grid_pref);
+    blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+    const dim3 g((unsigned)blocks), b(waves * 64);
+    with_full(full, [&](auto fc) {
+      constexpr bool F = decltype(fc)::value;
+      if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, F>), g, b, smem, s, A, spw);
+      else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, F>), g, b, smem, s, A, spw);
+    });
+    MHC_CHECK_LAUNCH("mf64_bwd_kernel");
+    *num_partials = blocks;
+    return MHC_OK;
+  });
+}
+
 int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
+  if (A.n > 32) return mf64_fused_bwd(A, xd, gd, gmax, s, num_partials);
   if (A.n <= 16 || A.n > 32 || A.M_ts != 0 || A.C % 128 != 0) return 1;
   if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
   if (A.P != A.Cp + round_up(A.n * A.n + 2 * A.n, 4)) return 1;

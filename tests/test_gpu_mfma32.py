@@ -220,3 +220,43 @@ def test_generic_backward_mfma_parameter_sums(T, n, C, per_token, dt, knobs):
     assert rel_err(np_of(res[0][0]), refs[0]) < TOL[dt]
     for got, ref in zip(res[0][1:], refs[1:]):
         assert rel_err(np_of(got), ref) < 1e-4
+
+
+@pytest.mark.parametrize("T,n,C", [(64, 64, 512), (300, 64, 1024), (20, 48, 512), (9, 33, 2048), (5, 64, 4096),
+                                   (40, 40, 768)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("grid", [None, 2])
+def test_mfma64_backward(T, n, C, dt, grid, knobs):
+    """32 < n <= 64 layer-wide backward on MFMA (mf64_bwd_kernel: y, dyn and dx = M^T G on MFMA in two
+    32-stream halves, dM = G X^T in wave-owned 16 x 16 blocks, dA and dP as wave dot products), C a
+    multiple of 128 from 512 to 4096 (4 to 8 waves), against the oracle for every gradient and against
+    the generic backward (MHC_BWD_MFMA=0); with MHC_BWD_GRID=2 each workgroup walks many tokens.  Two
+    runs are bitwise equal."""
+    if grid is not None:
+        knobs("MHC_BWD_GRID", grid)
+    knobs("MHC_SK_BLK_RECORD", 0)
+    g = rng(6600 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C)
+
+    def run():
+        xt = dev_tensor(x, dt).requires_grad_(True)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        out = ops.mhc_layer_forward(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+        out.backward(dev_tensor(dout, dt))
+        return [xt.grad] + [p.grad for p in ps]
+
+    a, b = run(), run()
+    knobs("MHC_BWD_MFMA", 0)
+    gen = run()
+    torch.cuda.synchronize()
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    assert rel_err(np_of(a[0]), refs[0]) < TOL[dt]
+    _ulp_bound(np_of(a[0]), refs[0], dt)
+    for got, ref in zip(a[1:], refs[1:]):
+        assert rel_err(np_of(got), ref) < 1e-4
+    for got, other in zip(a[1:], gen[1:]):
+        assert rel_err(np_of(got), np_of(other)) < 1e-5
