@@ -26,7 +26,8 @@ P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
 
 
 @pytest.mark.parametrize("T,n,C,per_token", [(32, 4, 2048, False), (300, 4, 1024, False), (9, 16, 64, True),
-                                             (64, 32, 512, False), (1, 4, 4096, False)])
+                                             (64, 32, 512, False), (1, 4, 4096, False), (1, 32, 4096, False),
+                                             (40, 64, 512, False)])
 def test_graph_replays_of_the_c_abi_match_eager(T, n, C, per_token):
     print("graph case", T, n, C, per_token, flush=True)
     g = rng(9300 + T + n + C)

@@ -62,6 +62,7 @@ PAIRS = [
     ((4096, 4, 4096, "bf16", False), (300, 4, 1000, "bf16", False)),
     ((2000, 16, 1024, "bf16", True), (37, 8, 256, "f32", True)),
     ((1000, 32, 512, "bf16", False), (5, 4, 64, "f32", False)),
+    ((500, 64, 1024, "bf16", False), (7, 48, 512, "bf16", False)),
 ]
 
 
