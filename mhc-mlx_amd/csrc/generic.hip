@@ -408,8 +408,36 @@ __global__ __launch_bounds__(kGenThreads) void gen_mix_fwd_kernel(GenArgs A) {
 // y_i of the same row), one block per wavefront at a time with the lanes
 // over consecutive channels; each entry belongs to one wavefront, so the
 // LDS sums have a fixed order.
-template <typename XT, typename YT, typename GT, int NMAX>
+// Eight floats as three packed 16-bit operands whose sum is the fp32 value (split3).
+template <typename T>
+MHC_DEV void gen_split3x8(const float (&v)[8], u32x4 (&out)[3]) {
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    float a = v[2 * h], b = v[2 * h + 1];
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+      const uint32_t wd = pack2<T>(a, b);
+      a -= lo16<T>(wd);
+      b -= hi16<T>(wd);
+      out[e][h] = wd;
+    }
+  }
+}
+
+// MF (16-bit x, dout of x's dtype or fp32, C a multiple of 32, 16-byte
+// aligned rows): the sums S = G X^T run on MFMA in 16 x 16 blocks owned by
+// the waves for the whole kernel (as in gen_bwd_kernel), an fp32 dout split
+// into three 16-bit terms per element (three MFMAs, fp32-accurate products);
+// Yd_i = sum G_i Y_i is a dot product per row, one wavefront each, over
+// 16-byte pieces.
+template <typename XT, typename YT, typename GT, int NMAX, bool MF = false>
 __global__ __launch_bounds__(kGenThreads) void gen_mix_bwd_kernel(GenArgs A) {
+  static_assert(!MF || (sizeof(XT) == 2 && (std::is_same<GT, XT>::value || std::is_same<GT, float>::value)),
+                "MFMA sums take 16-bit x and dout of x's dtype or fp32");
+  constexpr int kMfBlk = ((NMAX / 16) * (NMAX / 16) + kGenThreads / 64 - 1) / (kGenThreads / 64);
+  f32x4 smb[MF ? kMfBlk : 1];
+#pragma unroll
+  for (int b = 0; b < (MF ? kMfBlk : 1); ++b) smb[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   constexpr int NE = NMAX + 1;
   __shared__ float s_par[kGenMaxPar];
   __shared__ __align__(16) float s_W[NMAX * NMAX];  // s_W[j][i] = a_j M_ij p_i
@@ -430,9 +458,15 @@ __global__ __launch_bounds__(kGenThreads) void gen_mix_bwd_kernel(GenArgs A) {
   XT* DX = (XT*)A.out;
   YT* DY = (YT*)A.dy;
   const int nbr = (n + 3) / 4, nbc = (n + 1 + 3) / 4;  // row blocks, column blocks (column n: y)
-  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x) {
-    const int64_t tb = t * n * C;
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+  // tokens in groups of tpi (several per pass when C is below the workgroup size, so every thread has a
+  // channel of the dx pass); the sums then take the group's tokens in order
+  const int tpi = MF && C < (int)blockDim.x ? (int)blockDim.x / C : 1;
+  for (int64_t t0 = blockIdx.x; t0 < A.T; t0 += (int64_t)gridDim.x * tpi) {
+    for (int idx = threadIdx.x; idx < tpi * C; idx += blockDim.x) {
+      const int u = idx / C, c = idx - u * C;
+      const int64_t t = t0 + (int64_t)u * gridDim.x;
+      if (t >= A.T) continue;
+      const int64_t tb = t * n * C;
       float gv[NMAX];
 #pragma unroll
       for (int i = 0; i < NMAX; ++i) gv[i] = i < n ? load1<GT>(Gd + tb + (int64_t)i * C + c) : 0.0f;
@@ -455,32 +489,110 @@ __global__ __launch_bounds__(kGenThreads) void gen_mix_bwd_kernel(GenArgs A) {
           if (i < n) store1<YT>(DY + tb + (int64_t)i * C + c, s_par[nn + n + i] * gv[i]);
       }
     }
-    for (int blk = wave; blk < nbr * nbc; blk += nwaves) {
-      const int r0 = (blk / nbc) * 4, c0 = (blk % nbc) * 4;
-      float acc[16];
+    for (int u = 0; u < tpi; ++u) {
+      const int64_t t = t0 + (int64_t)u * gridDim.x;
+      if (t >= A.T) break;
+      const int64_t tb = t * n * C;
+      if constexpr (MF) {
+        const int q = lane >> 4, r = lane & 15;
+        const int nbk = (n + 15) / 16;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-      for (int c = lane; c < C; c += 64) {
-        float rv[4], cv[4], yv[4];
+        for (int b = 0; b < kMfBlk; ++b) {
+          const int blk = wave + b * nwaves;
+          if (blk >= nbk * nbk) break;
+          const int I = blk / nbk, J = blk % nbk;
+          const int gi = 16 * I + r, xj = 16 * J + r;
+          const GT* grow = Gd + tb + (int64_t)(gi < n ? gi : 0) * C + 8 * q;
+          const XT* xrow = X + tb + (int64_t)(xj < n ? xj : 0) * C + 8 * q;
+          f32x4 acc = smb[b];
+          for (int k = 0; k < C; k += 32) {
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            const u32x4 xb = xj < n ? *reinterpret_cast<const u32x4*>(xrow + k) : zero;
+            if constexpr (std::is_same<GT, XT>::value) {
+              const u32x4 ga = gi < n ? *reinterpret_cast<const u32x4*>(grow + k) : zero;
+              acc = gen_mfma<XT>(ga, xb, acc);
+            } else {
+              float gv8[8];
+              if (gi < n) {
+                const float4 g0 = *reinterpret_cast<const float4*>(grow + k);
+                const float4 g1 = *reinterpret_cast<const float4*>(grow + k + 4);
+                gv8[0] = g0.x; gv8[1] = g0.y; gv8[2] = g0.z; gv8[3] = g0.w;
+                gv8[4] = g1.x; gv8[5] = g1.y; gv8[6] = g1.z; gv8[7] = g1.w;
+              } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int ri = r0 + e, cj = c0 + e;
-          rv[e] = ri < n ? load1<GT>(Gd + tb + (int64_t)ri * C + c) : 0.0f;
-          cv[e] = cj < n ? load1<XT>(X + tb + (int64_t)cj * C + c) : 0.0f;
-          yv[e] = (Y && c0 + 3 >= n && ri < n) ? load1<YT>(Y + tb + (int64_t)ri * C + c) : 0.0f;
+                for (int e = 0; e < 8; ++e) gv8[e] = 0.0f;
+              }
+              u32x4 ga[3];
+              gen_split3x8<XT>(gv8, ga);
+#pragma unroll
+              for (int e = 2; e >= 0; --e) acc = gen_mfma<XT>(ga[e], xb, acc);
+            }
+          }
+          smb[b] = acc;
+        }
+        // Yd_i = sum G_i Y_i: one wavefront per row, 8 channels per lane
+        if (Y) {
+          for (int i = wave; i < n; i += nwaves) {
+            const GT* grow = Gd + tb + (int64_t)i * C;
+            const YT* yrow = Y + tb + (int64_t)i * C;
+            float acc = 0.0f;
+            for (int c = 8 * lane; c < C; c += 512) {
+              Vec<GT, 8> gv;
+              Vec<YT, 8> yv;
+              gv.load(grow + c);
+              yv.load(yrow + c);
+#pragma unroll
+              for (int v = 0; v < 8; ++v) acc = fmaf(gv.get(v), yv.get(v), acc);
+            }
+            acc = wave_sum(acc);
+            if (lane == 0) s_acc[i * NE + n] += acc;
+          }
+        }
+        continue;
+      }
+      for (int blk = wave; blk < nbr * nbc; blk += nwaves) {
+        const int r0 = (blk / nbc) * 4, c0 = (blk % nbc) * 4;
+        float acc[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+        for (int c = lane; c < C; c += 64) {
+          float rv[4], cv[4], yv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int ri = r0 + e, cj = c0 + e;
+            rv[e] = ri < n ? load1<GT>(Gd + tb + (int64_t)ri * C + c) : 0.0f;
+            cv[e] = cj < n ? load1<XT>(X + tb + (int64_t)cj * C + c) : 0.0f;
+            yv[e] = (Y && c0 + 3 >= n && ri < n) ? load1<YT>(Y + tb + (int64_t)ri * C + c) : 0.0f;
+          }
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int f = e & 3;
+            const float col = (c0 + f == n) ? yv[e >> 2] : cv[f];
+            acc[e] = fmaf(rv[e >> 2], col, acc[e]);
+          }
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int f = e & 3;
-          const float col = (c0 + f == n) ? yv[e >> 2] : cv[f];
-          acc[e] = fmaf(rv[e >> 2], col, acc[e]);
+          const float v = wave_sum(acc[e]);
+          const int i = r0 + (e >> 2), j = c0 + (e & 3);
+          if (lane == 0 && i < n && j <= n) s_acc[i * NE + j] += v;
         }
       }
+
+    }
+  }
+  if constexpr (MF) {
+    const int q = lane >> 4, r = lane & 15;
+    const int nbk = (n + 15) / 16;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float v = wave_sum(acc[e]);
-        const int i = r0 + (e >> 2), j = c0 + (e & 3);
-        if (lane == 0 && i < n && j <= n) s_acc[i * NE + j] += v;
+    for (int b = 0; b < kMfBlk; ++b) {
+      const int blk = wave + b * nwaves;
+      if (blk >= nbk * nbk) break;
+      const int I = blk / nbk, J = blk % nbk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 16 * I + 4 * q + e, j = 16 * J + r;
+        if (i < n && j < n) s_acc[i * NE + j] = smb[b][e];
       }
     }
   }
@@ -606,6 +718,20 @@ int gen_mix_bwd(const GenArgs& A, int xd, int yd, int gd, hipStream_t s, int64_t
       using YT = std::remove_pointer_t<decltype(yp)>;
       return by_pair<XT>(gd, [&](auto* gp) {
         using GT = std::remove_pointer_t<decltype(gp)>;
+        if constexpr (sizeof(XT) == 2 && (std::is_same<GT, XT>::value || std::is_same<GT, float>::value)) {
+          // the sums on MFMA: C a multiple of 32, 16-byte aligned rows (Y's 8-channel pieces too)
+          if (knob(kKnobGenMfma, 1) != 0 && A.C % 32 == 0 && aligned(A.x, 16) && aligned(A.g, 16) &&
+              (A.y == nullptr || aligned(A.y, 16))) {
+            if (A.n <= 32)
+              hipLaunchKernelGGL((gen_mix_bwd_kernel<XT, YT, GT, 32, true>), dim3((unsigned)blocks),
+                                 dim3(kGenThreads), 0, s, A);
+            else
+              hipLaunchKernelGGL((gen_mix_bwd_kernel<XT, YT, GT, 64, true>), dim3((unsigned)blocks),
+                                 dim3(kGenThreads), 0, s, A);
+            MHC_CHECK_LAUNCH("gen_mix_bwd_kernel");
+            return MHC_OK;
+          }
+        }
         if (A.n <= 32)
           hipLaunchKernelGGL((gen_mix_bwd_kernel<XT, YT, GT, 32>), dim3((unsigned)blocks), dim3(kGenThreads), 0,
                              s, A);

@@ -304,3 +304,33 @@ def test_stream_scale_vjp_flat_matches_per_stream(T, n, C, xdt, knobs):
     ref_dh = np.einsum("bic,bic->i", dout.astype(np.float64), x.astype(np.float64)) * a * (1 - a)
     assert rel_err(np_of(res[0][1]), ref_dh) < 1e-5
     assert rel_err(np_of(res[0][0]), dout * a[None, :, None]) < {"bf16": 2 ** -8, "f16": 2 ** -11}[xdt]
+
+
+@pytest.mark.parametrize("B,n,C", [(4, 64, 64), (3, 48, 128), (2, 40, 96), (5, 64, 256), (3, 33, 32)])
+@pytest.mark.parametrize("xdt,gdt,odt", [("bf16", "bf16", "bf16"), ("bf16", "f32", "f32"), ("f16", "f16", "f16"),
+                                         ("f16", "f32", "f32")])
+def test_post_combine_generic_mfma_sums(B, n, C, xdt, gdt, odt, knobs):
+    """32 < n <= 64 (the generic post-combine kernels): with 16-bit x and dout of x's dtype or fp32 and C a
+    multiple of 32, the VJP's sums S = G X^T run on MFMA (fp32 dout split into three 16-bit terms) and
+    Yd as wave dot products.  Every gradient matches the oracle, and the VALU sums (MHC_GEN_MFMA=0) to
+    fp32 summation order; dx and dy are bitwise the same either way."""
+    g = rng(650 + B + n + C)
+    x = to_dtype_np(g.standard_normal((B, n, C)), xdt)
+    y = to_dtype_np(g.standard_normal((B, n, C)), xdt)
+    dout = to_dtype_np(g.standard_normal((B, n, C)), gdt if odt == "f32" else odt)
+    hpre, hpost, hres, _ = params(g, n, C)
+    got = _post_combine_run(x, y, dout, hpre, hpost, hres, xdt, gdt, odt)
+    refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    names = ["dx", "dy", "dH_pre", "dH_post", "dH_res"]
+    for name, t, r in zip(names, got[1:], refs):
+        v = np_of(t)
+        if name in ("dx", "dy") and t.dtype != torch.float32:
+            ulp = 2.0 ** -8 if t.dtype == torch.bfloat16 else 2.0 ** -11
+            assert (np.abs(v - r) <= ulp * np.abs(r) + 1e-5 * np.abs(r).max()).all(), name
+        else:
+            assert rel_err(v, r) < (1e-5 if name in ("dx", "dy") else 1e-4), (name, rel_err(v, r))
+    knobs("MHC_GEN_MFMA", 0)
+    valu = _post_combine_run(x, y, dout, hpre, hpost, hres, xdt, gdt, odt)
+    assert torch.equal(got[1], valu[1]) and torch.equal(got[2], valu[2])
+    for name, a, b in zip(names[2:], got[3:], valu[3:]):
+        assert rel_err(np_of(a), np_of(b)) < 1e-5, name
