@@ -306,7 +306,8 @@ def test_stream_scale_vjp_flat_matches_per_stream(T, n, C, xdt, knobs):
     assert rel_err(np_of(res[0][0]), dout * a[None, :, None]) < {"bf16": 2 ** -8, "f16": 2 ** -11}[xdt]
 
 
-@pytest.mark.parametrize("B,n,C", [(4, 64, 64), (3, 48, 128), (2, 40, 96), (5, 64, 256), (3, 33, 32)])
+@pytest.mark.parametrize("B,n,C", [(4, 64, 64), (3, 48, 128), (2, 40, 96), (5, 64, 256), (3, 33, 32), (2, 36, 45),
+                                   (3, 64, 2)])
 @pytest.mark.parametrize("xdt,gdt,odt", [("bf16", "bf16", "bf16"), ("bf16", "f32", "f32"), ("f16", "f16", "f16"),
                                          ("f16", "f32", "f32")])
 def test_post_combine_generic_mfma_sums(B, n, C, xdt, gdt, odt, knobs):
@@ -320,6 +321,14 @@ def test_post_combine_generic_mfma_sums(B, n, C, xdt, gdt, odt, knobs):
     dout = to_dtype_np(g.standard_normal((B, n, C)), gdt if odt == "f32" else odt)
     hpre, hpost, hres, _ = params(g, n, C)
     got = _post_combine_run(x, y, dout, hpre, hpost, hres, xdt, gdt, odt)
+    # the forward too (generic kernel, one channel per thread)
+    fwd = O.post_combine(x, y, hpre, hpost, hres, 20, 1e-5)
+    o = np_of(got[0])
+    if got[0].dtype == torch.float32:
+        assert rel_err(o, fwd) < 1e-5
+    else:
+        ulp = 2.0 ** -8 if got[0].dtype == torch.bfloat16 else 2.0 ** -11
+        assert (np.abs(o - fwd) <= ulp * np.abs(fwd) + 1e-5 * np.abs(fwd).max()).all()
     refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
     names = ["dx", "dy", "dH_pre", "dH_post", "dH_res"]
     for name, t, r in zip(names, got[1:], refs):
