@@ -670,11 +670,13 @@ __global__ __launch_bounds__(kMixThreads) void scale_bwd_kernel(MixArgs A) {
 }
 
 // The pre-scale VJP as a flat pass: 16-bit x and dout of one dtype, whole
-// aligned 8-channel chunks, no accumulator, nchunks a multiple of 64 and
-// n * nchunks of 256.  The grid's thread count is a multiple of n * nchunks,
-// so each thread's chunks lie in one stream and each wave's in one row;
-// block b adds its waves' sums into its partial row in wave order.
-template <typename XT>
+// aligned 8-channel chunks, nchunks a multiple of 64 and n * nchunks of 256.
+// The grid's thread count is a multiple of n * nchunks, so each thread's
+// chunks lie in one stream and each wave's in one row; block b adds its
+// waves' sums into its partial row in wave order.  ACC: dx = a g + dx_accum
+// (the accumulator in dx's dtype, read in the same pass; it may be dx itself:
+// each element is read before the store that depends on it).
+template <typename XT, bool ACC>
 __global__ __launch_bounds__(kMixThreads) void scale_bwd_flat_kernel(MixArgs A, uint32_t total) {
   constexpr int V = 8;
   __shared__ float s_stage[kMixThreads / 64];
@@ -686,10 +688,11 @@ __global__ __launch_bounds__(kMixThreads) void scale_bwd_flat_kernel(MixArgs A, 
   const float a = A.h_mode == MHC_H_RAW ? sigmoidf_(hv) : hv;
   const XT* __restrict__ X = (const XT*)A.x;
   const XT* __restrict__ Gd = (const XT*)A.g;
-  XT* __restrict__ DX = (XT*)A.out;
+  const XT* ACCP = (const XT*)A.acc;
+  XT* DX = (XT*)A.out;
   float acc = 0.0f;
   for (uint32_t c = first; c < total; c += kScaleU * stride) {
-    Vec<XT, V> xr[kScaleU], gr[kScaleU];
+    Vec<XT, V> xr[kScaleU], gr[kScaleU], ar[ACC ? kScaleU : 1];
     bool on[kScaleU];
 #pragma unroll
     for (int u = 0; u < kScaleU; ++u) {
@@ -698,9 +701,11 @@ __global__ __launch_bounds__(kMixThreads) void scale_bwd_flat_kernel(MixArgs A, 
       if (on[u]) {
         xr[u].load(X + (int64_t)cu * V);
         gr[u].load(Gd + (int64_t)cu * V);
+        if constexpr (ACC) ar[u].load(ACCP + (int64_t)cu * V);
       } else {
         xr[u].zero();
         gr[u].zero();
+        if constexpr (ACC) ar[u].zero();
       }
     }
     issue_fence();
@@ -711,7 +716,10 @@ __global__ __launch_bounds__(kMixThreads) void scale_bwd_flat_kernel(MixArgs A, 
       if (!on[u]) continue;
       float o[V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) o[v] = a * gr[u].get(v);
+      for (int v = 0; v < V; ++v) {
+        if constexpr (ACC) o[v] = fmaf(a, gr[u].get(v), ar[u].get(v));
+        else o[v] = a * gr[u].get(v);
+      }
       store_vec<XT, V>(DX + (int64_t)(c + u * stride) * V, o);
     }
   }
@@ -1061,7 +1069,7 @@ extern "C" int mhc_stream_scale_bwd(const void* x, int x_dtype, const void* dout
   const int64_t total = T * n * (int64_t)A.nchunks;
   const int64_t m = (int64_t)n * A.nchunks / kMixThreads;
   int64_t Gf = 0;
-  if (knob(kKnobScaleBwdFlat, 1) != 0 && A.vec && !dx_accum && x_dtype == dout_dtype && dtype_bytes(x_dtype) == 2 &&
+  if (knob(kKnobScaleBwdFlat, 1) != 0 && A.vec && x_dtype == dout_dtype && dtype_bytes(x_dtype) == 2 &&
       C % 8 == 0 && A.nchunks % 64 == 0 && ((int64_t)n * A.nchunks) % kMixThreads == 0 && total < INT32_MAX)
     Gf = std::min<int64_t>(G, total / kMixThreads) / m * m;
   int64_t rows_used = G;
@@ -1071,8 +1079,12 @@ extern "C" int mhc_stream_scale_bwd(const void* x, int x_dtype, const void* dout
     rc = by_dtype(x_dtype, [&](auto* xp) {
       using XT = std::remove_pointer_t<decltype(xp)>;
       if constexpr (ElemTraits<XT>::kBytes == 2) {
-        hipLaunchKernelGGL((scale_bwd_flat_kernel<XT>), dim3((unsigned)Gf), dim3(kMixThreads), 0, s, A,
-                           (uint32_t)total);
+        if (dx_accum)
+          hipLaunchKernelGGL((scale_bwd_flat_kernel<XT, true>), dim3((unsigned)Gf), dim3(kMixThreads), 0, s, A,
+                             (uint32_t)total);
+        else
+          hipLaunchKernelGGL((scale_bwd_flat_kernel<XT, false>), dim3((unsigned)Gf), dim3(kMixThreads), 0, s, A,
+                             (uint32_t)total);
         MHC_CHECK_LAUNCH("scale_bwd_flat_kernel");
         return MHC_OK;
       } else {

@@ -319,7 +319,7 @@ class MHCLayer(nn.Module):
         host steps: a single-token forward is launch-bound, so its latency is mostly this code.  Returns
         None whenever the general path has something to decide (a shape error, CPU tensors, the torch
         path, a gradient, a library error), and forward() then takes that path."""
-        if not self.use_metal or x.ndim != 3 or x.shape[1] != self.n or x.shape[2] != self.C:
+        if not self.use_metal or self.n > _lib.MAX_N or x.ndim != 3 or x.shape[1] != self.n or x.shape[2] != self.C:
             return None
         ps = self._parameters
         hp, hq, hr, w = ps.get("H_pre_raw"), ps.get("H_post_raw"), ps.get("H_res_raw"), ps.get("rms_weight")
@@ -425,7 +425,9 @@ class MHCRewire(nn.Module):
             why = _off_gpu(x3, self.mhc.H_pre_raw)
             if why is None:
                 try:
-                    x_pre = ops.stream_scale(x3, self.mhc.H_pre_raw)
+                    # x3 comes back through the pre-scale node, whose VJP then adds the post-combine's
+                    # x gradient into its own dx pass
+                    x_pre, x3 = ops.stream_scale_and_pass(x3, self.mhc.H_pre_raw)
                 except RuntimeError as e:
                     why = e
             if x_pre is None:

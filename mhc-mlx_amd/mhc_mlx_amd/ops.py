@@ -43,6 +43,7 @@ __all__ = [
     "mhc_layer_forward_dynamic",
     "post_combine",
     "stream_scale",
+    "stream_scale_and_pass",
     "residual_add_agg_hip",
     "suggest_threads_per_group",
 ]
@@ -752,10 +753,16 @@ def post_combine(x, y_inner, H_pre_raw, H_post_raw, H_res_raw, sinkhorn_iters: i
 
 
 class StreamScaleFn(torch.autograd.Function):
-    """x_pre = sigmoid(H_pre_raw)_i * x_i (layer.py:476-480)."""
+    """x_pre = sigmoid(H_pre_raw)_i * x_i (layer.py:476-480).
+
+    With ``passthrough`` the Function also returns x itself (sharing its storage) for the caller's other
+    use of x, MHCRewire's post-combine.  Both x-gradient contributions then arrive at this node, and the
+    VJP writes dx = a_i g_i + g_pass in the same pass that reads g and x (the library's dx accumulator)
+    instead of leaving their sum to a separate elementwise add.
+    """
 
     @staticmethod
-    def forward(ctx, x, H_pre_raw):
+    def forward(ctx, x, H_pre_raw, passthrough):
         B, n, C = (int(s) for s in x.shape)
         xc = x.detach().contiguous()
         hp = _f32(H_pre_raw)
@@ -764,15 +771,19 @@ class StreamScaleFn(torch.autograd.Function):
             _lib.call("mhc_stream_scale_fwd", _p(xc), _code(xc.dtype), _p(hp), _lib.H_RAW, _p(out),
                       _code(xc.dtype), B, n, C, _stream(xc))
         ctx.save_for_backward(x, H_pre_raw)
-        return out
+        ctx.set_materialize_grads(False)
+        return (out, x) if passthrough else out
 
     @staticmethod
-    def backward(ctx, dout):
+    def backward(ctx, dout, dpass=None):
         x, hpre = ctx.saved_tensors
+        if dout is None:
+            return dpass, None, None
         B, n, C = (int(s) for s in x.shape)
         xc = x.detach().contiguous()
         gdt = dout.dtype if dout.dtype in (torch.float32, xc.dtype) else torch.float32
         gc = dout.detach().to(gdt).contiguous()
+        acc = None if dpass is None else dpass.detach().to(xc.dtype).contiguous()
         hp = _f32(hpre)
         dx = torch.empty_like(xc)
         dpre = torch.empty((n,), dtype=torch.float32, device=xc.device)
@@ -780,17 +791,28 @@ class StreamScaleFn(torch.autograd.Function):
         ws = _ws(nb, xc.device)
         with timed("stream_scale_bwd"):
             _lib.call("mhc_stream_scale_bwd", _p(xc), _code(xc.dtype), _p(gc), _code(gc.dtype), _p(hp),
-                      _lib.H_RAW, None, _p(dx), _code(xc.dtype), _p(dpre), _p(ws), nb, B, n, C, _stream(xc))
-        return dx, dpre.to(hpre.dtype)
+                      _lib.H_RAW, _p(acc), _p(dx), _code(xc.dtype), _p(dpre), _p(ws), nb, B, n, C, _stream(xc))
+        return dx, dpre.to(hpre.dtype), None
 
 
-def stream_scale(x, H_pre_raw):
-    """Pre-scale of MHCRewire: [B, n, C] * sigmoid(H_pre_raw)[n]."""
+def _stream_scale_check(x, H_pre_raw):
     if x.ndim != 3 or H_pre_raw.ndim != 1 or H_pre_raw.shape[0] != x.shape[1]:
         raise ValueError(f"x must be [B, n, C] and H_pre_raw [n], got {tuple(x.shape)}, {tuple(H_pre_raw.shape)}")
     _validate_n(int(x.shape[1]))
     _require_gpu(x, H_pre_raw)
-    return StreamScaleFn.apply(x, H_pre_raw)
+
+
+def stream_scale(x, H_pre_raw):
+    """Pre-scale of MHCRewire: [B, n, C] * sigmoid(H_pre_raw)[n]."""
+    _stream_scale_check(x, H_pre_raw)
+    return StreamScaleFn.apply(x, H_pre_raw, False)
+
+
+def stream_scale_and_pass(x, H_pre_raw):
+    """(stream_scale(x, H_pre_raw), x): the second output is x for a second use (MHCRewire's
+    post-combine) whose gradient the pre-scale's VJP adds into dx in its own pass."""
+    _stream_scale_check(x, H_pre_raw)
+    return StreamScaleFn.apply(x, H_pre_raw, True)
 
 
 # --------------------------------------------------------------------------

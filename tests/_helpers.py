@@ -30,11 +30,15 @@ def np_of(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def rel_err(got, ref) -> float:
-    """max |got - ref| / max(max |ref|, tiny)  (the reference tests' relative metric)."""
+def rel_err(got, ref, floor: float = 1e-30) -> float:
+    """max |got - ref| / max(max |ref|, floor)  (the reference tests' relative metric).
+
+    ``floor`` turns the metric into an absolute one for references whose
+    largest element is below it (a gradient that is zero or nearly so).
+    """
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
-    den = max(float(np.abs(ref).max()) if ref.size else 0.0, 1e-30)
+    den = max(float(np.abs(ref).max()) if ref.size else 0.0, floor)
     return float(np.abs(got - ref).max()) / den if ref.size else 0.0
 
 
@@ -44,6 +48,14 @@ def max_abs(got, ref) -> float:
 
 # tolerance per output dtype (reference tests: fp32 1e-5, fp16 5e-3, bf16 2e-2)
 TOL = {"f32": 1e-5, "f16": 5e-3, "bf16": 2e-2}
+
+# Parameter gradients (dH_pre, dH_post, dH_res, d_rms_weight, dM) for every input dtype: the oracle
+# sees the inputs already rounded to their I/O dtype, so the two sides differ only by fp32 rounding
+# in the products and in fixed-order partial sums.  For zero-mean products summed as partial sums of
+# depth d the expected relative error is about 2^-24 sqrt(d); the deepest sums tested (config 2: 64
+# tokens x 8 channels per thread before a fixed tree) give ~1.3e-6 by that estimate and measure
+# 9.5e-7, so the fp32 bar of the reference tests, 1e-5, holds with margin at every size.
+GRAD_TOL = 1e-5
 
 
 def params(g: np.random.Generator, n: int, C: int, per_token_B: int | None = None):

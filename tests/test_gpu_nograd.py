@@ -125,3 +125,27 @@ def test_library_error_in_the_fast_path_goes_to_the_general_path(monkeypatch):
         monkeypatch.setattr(ops, "layer_forward_nograd", failing)
         got = layer(xt, return_dtype=torch.bfloat16)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("grad_mode", ["no_grad", "inference_mode", "frozen"])
+def test_nograd_n_above_64_takes_the_reference_path(grad_mode, fast_calls):
+    """n > 64 is beyond the library (metal.py:827-834): like the reference layer (layer.py:175-185), the
+    module runs its torch path for it, also when no gradient is needed, and never calls the library."""
+    n, C, B = 65, 48, 3
+    g = rng(365)
+    layer, (hpre, hpost, hres, w) = _layer(n, C, g)
+    x = torch.from_numpy(g.standard_normal((B, n, C)).astype(np.float32)).cuda()
+    if grad_mode == "no_grad":
+        with torch.no_grad():
+            out = layer(x)
+    elif grad_mode == "inference_mode":
+        with torch.inference_mode():
+            out = layer(x)
+    else:
+        for p in layer.parameters():
+            p.requires_grad_(False)
+        out = layer(x)
+    assert fast_calls == []
+    ref = O.mhc_forward_reference(np_of(x), hpre, hpost, hres, w, sinkhorn_iters=20, eps=1e-6)
+    assert out.dtype == torch.float32 and out.is_cuda
+    assert rel_err(np_of(out), ref) < 1e-5

@@ -2,8 +2,8 @@
 
 Each path (the n = 4 and n = 8 layer-wide full tiles, n = 4 per-token, the n = 16 MFMA kernels per-token and
 layer-wide, the n = 32 MFMA kernels at one, two and four slabs per wave and the runtime-loop forward above C = 2048
-(C = 4096, 8192, and per-token n = 24 at C = 3072), n = 24, and MHCRewire's post-combine
-at n = 4 and n = 32) runs forward and backward five times on the same inputs; every output and gradient must
+(C = 4096, 8192, and per-token n = 24 at C = 3072), n = 24, the 32 < n <= 64 MFMA kernels at n = 48 and 64,
+and MHCRewire's post-combine at n = 4, 32 and 64) runs forward and backward five times on the same inputs; every output and gradient must
 be bitwise equal to the first run's.  The kernels use fixed-order reductions, so any difference is a defect:
 a race, or a register or memory hazard that depends on timing.  Parity with the oracle is covered by the
 other test files; this file checks that the values do not move between runs.
@@ -26,14 +26,17 @@ def _assert_reruns_equal(run):
     for rep in range(1, REPS):
         cur = run()
         diff = [i for i, (a, b) in enumerate(zip(first, cur)) if not torch.equal(a, b)]
-        assert not diff, f"run {rep}: outputs {diff} differ from run 0"
+        assert not diff, f"run {rep}: outputs {diff} differ from run 0"  # stops at the first mismatching run
 
 
 @pytest.mark.parametrize("T,n,C,per_token", [(4096, 4, 4096, False), (4096, 4, 4096, True), (2048, 8, 2048, False),
                                              (2048, 16, 1024, True), (2048, 16, 2048, False),
                                              (2048, 32, 512, False), (512, 32, 2048, False),
                                              (512, 32, 4096, False), (256, 32, 8192, False), (512, 24, 1024, False),
-                                             (300, 24, 3072, True)])
+                                             (300, 24, 3072, True),
+                                             # 32 < n <= 64 on MFMA (mf64_fwd_loop_kernel, mf64_bwd_kernel)
+                                             (4096, 64, 512, False), (1024, 64, 2048, False),
+                                             (2048, 48, 1024, False)])
 def test_layer_reruns_are_bitwise_equal(T, n, C, per_token):
     g = rng(7100 + T + n + C)
     x = to_dtype_np(g.standard_normal((T, n, C)), "bf16")
@@ -51,9 +54,10 @@ def test_layer_reruns_are_bitwise_equal(T, n, C, per_token):
     _assert_reruns_equal(run)
 
 
-@pytest.mark.parametrize("n", [4, 32])
-def test_rewire_reruns_are_bitwise_equal(n):
-    dims, T = 4096, 2048
+@pytest.mark.parametrize("n,T", [(4, 2048), (32, 2048), (64, 8192)])
+def test_rewire_reruns_are_bitwise_equal(n, T):
+    """MHCRewire(Linear(4096, 4096)): n = 64 runs the post-combine's generic MFMA sums at C = 64."""
+    dims = 4096
     dev = torch.device("cuda")
     torch.manual_seed(7200 + n)
     inner = torch.nn.Linear(dims, dims, bias=False).to(dev).to(torch.bfloat16)

@@ -6,6 +6,8 @@ import json
 import pytest
 import torch
 
+from tests._helpers import np_of, rel_err
+
 from mhc_mlx_amd import _lib, ops, tune, tuning
 
 pytestmark = pytest.mark.gpu
@@ -52,7 +54,9 @@ def test_results_do_not_depend_on_the_knob(op, knobs):
     for v, got in runs.items():
         for a, b in zip(got, ref):
             if op in ("sinkhorn_16", "mhc_fused_n16"):
-                # other lane layouts: sums associate differently, equal to within rounding
-                assert (a.float() - b.float()).abs().max() <= 1e-2 * b.float().abs().max(), v
+                # other lane layouts: the Sinkhorn sums associate differently, so M and the fp32
+                # output agree to fp32 rounding
+                assert a.dtype == torch.float32
+                assert rel_err(np_of(a), np_of(b)) < 1e-6, v
             else:
                 assert torch.equal(a, b), v
