@@ -447,6 +447,391 @@ __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_bwd_kernel(const floa
 }
 
 // ---------------------------------------------------------------------------
+// n == 16, batched, block layout (the default for n == 16): one 16-lane DPP
+// row per matrix, four matrices per wave, so a batch of B matrices fills
+// B / 4 waves (four per SIMD at config 3's 16384 matrices, against one for the
+// four-lanes-per-matrix kernels above).
+//
+// Lane l = 4 rb + cb of the matrix's row holds a 4 x 4 block, rotated:
+// register [s][t] is element (4 rb + ((cb + s) & 3), 4 cb + ((rb + t) & 3)).
+// Slot 0 is the lane's own row 4 rb + cb and own column 4 cb + rb; every row
+// and column has exactly one owner, and the rotation makes every cross-lane
+// step a uniform DPP read:
+//  * the owner of a row adds the partial sums of its quad (quad lane cb + u
+//    holds the row in slot (-u) & 3; quad_perm rotations), the owner of a
+//    column those of lanes l + 4u (slot (-u) & 3 again; row_ror rotations):
+//    three DPP adds per sum, computed once, by the owner;
+//  * per-row and per-column scalars (scales, cumulative R and C) live on the
+//    owner and are read back by the same rotations.
+//
+// The iterate is P_k = diag(R_k) K diag(C_k) (reference.py:35-46 scales P
+// itself; the same products, associated differently): the row sums of
+// P_{k-1} are R_{k-1} (K C_{k-1}) and the column sums after the row step are
+// C_{k-1} (R_k K), so an iteration costs two FMAs per element and the matrix
+// is formed once at the end.  The recorded state has the format of the
+// kernels above ([iters][R | rs | C | cs][16]).
+//
+// Without a record (MHC_SK16_RECORD=0, or the plain mhc_sinkhorn_bwd) the
+// VJP keeps its per-iteration state (R_k, rs_k, C_k, cs_k of the lane's own
+// row and column) in registers, kSk16bSeg iterations at a time.  The
+// segments are aligned to the end (the first one is the short one); the
+// forward runs once to the last segment's start, keeping each segment's
+// starting scales in LDS, then each segment, last first, is recomputed into
+// registers and swept in reverse: 2 iters - kSk16bSeg forward iterations in
+// all (31 at 20 iterations) and no memory traffic beyond the matrices.  At
+// 16384 matrices of 20 iterations the recorded pair (forward 19.9 us, VJP
+// 32.5 us) still beats it (14.5 + 41.5 us), so the layer records by default.
+// ---------------------------------------------------------------------------
+
+constexpr int kSk16bThreads = 256;
+constexpr int kSk16bSeg = 9;  // with 4 waves per SIMD (128 VGPRs), no spills
+constexpr int kSk16bMaxSeg = 32;  // VJP checkpoints: 512 bytes of LDS per wave and segment
+
+// A DPP read of another lane's v.  Every read here stays inside the lane's
+// quad or 16-lane row, so no source lane is ever out of range: bound_ctrl on,
+// and no "old" value for the compiler to materialise.
+template <int CTRL>
+MHC_DEV float sk16b_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v),
+                                                               __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// v of quad lane (c + U) & 3, c this lane's position in its quad
+template <int U>
+MHC_DEV float sk16b_quad(float v) {
+  if constexpr ((U & 3) == 0) return v;
+  else return sk16b_dpp<(U & 3) | (((U + 1) & 3) << 2) | (((U + 2) & 3) << 4) | (((U + 3) & 3) << 6)>(v);
+}
+
+// v of lane (l + 4 U) mod 16 of this lane's DPP row (row_ror:k reads lane (l - k) mod 16)
+template <int U>
+MHC_DEV float sk16b_col(float v) {
+  if constexpr ((U & 3) == 0) return v;
+  else return sk16b_dpp<0x120 + ((16 - 4 * U) & 15)>(v);
+}
+
+template <typename Op>
+MHC_DEV float sk16b_row_own(const float (&p)[4], Op op) {
+  return op(op(op(p[0], sk16b_quad<1>(p[3])), sk16b_quad<2>(p[2])), sk16b_quad<3>(p[1]));
+}
+template <typename Op>
+MHC_DEV float sk16b_col_own(const float (&p)[4], Op op) {
+  return op(op(op(p[0], sk16b_col<1>(p[3])), sk16b_col<2>(p[2])), sk16b_col<3>(p[1]));
+}
+MHC_DEV void sk16b_row_bcast(float v, float (&o)[4]) {
+  o[0] = v;
+  o[1] = sk16b_quad<1>(v);
+  o[2] = sk16b_quad<2>(v);
+  o[3] = sk16b_quad<3>(v);
+}
+MHC_DEV void sk16b_col_bcast(float v, float (&o)[4]) {
+  o[0] = v;
+  o[1] = sk16b_col<1>(v);
+  o[2] = sk16b_col<2>(v);
+  o[3] = sk16b_col<3>(v);
+}
+
+// The lane's block of a row-major 16 x 16 matrix: row slot s is one float4 of
+// columns 4 cb .. 4 cb + 3, rotated left by rb into the column slots.
+MHC_DEV void sk16b_load(const float* __restrict__ A, int rb, int cb, float (&E)[4][4]) {
+  const bool b1 = (rb & 1) != 0, b2 = (rb & 2) != 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const float4 f = *reinterpret_cast<const float4*>(A + (4 * rb + ((cb + s) & 3)) * 16 + 4 * cb);
+    const float v[4] = {f.x, f.y, f.z, f.w};
+    float a[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) a[t] = b1 ? v[(t + 1) & 3] : v[t];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) E[s][t] = b2 ? a[(t + 2) & 3] : a[t];
+  }
+}
+
+MHC_DEV void sk16b_store(float* A, int rb, int cb, const float (&E)[4][4]) {
+  const bool b1 = (rb & 1) != 0, b2 = (rb & 2) != 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    float a[4], v[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) a[x] = b2 ? E[s][(x + 2) & 3] : E[s][x];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) v[x] = b1 ? a[(x + 3) & 3] : a[x];
+    *reinterpret_cast<float4*>(A + (4 * rb + ((cb + s) & 3)) * 16 + 4 * cb) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// E <- exp(E - rowmax) (reference.py:67); mx: the row maxima of the lane's row slots
+MHC_DEV void sk16b_exp(float (&E)[4][4], float (&mx)[4]) {
+  float pm[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) pm[s] = fmaxf(fmaxf(E[s][0], E[s][1]), fmaxf(E[s][2], E[s][3]));
+  sk16b_row_bcast(sk16b_row_own(pm, MaxOp{}), mx);
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) E[s][t] = sk16_exp(E[s][t] - mx[s]);
+}
+
+struct Sk16bScales {
+  float R, C;          // cumulative scale of the lane's own row / own column
+  float Rs[4], Cs[4];  // ... of its row slots / column slots
+};
+
+MHC_DEV void sk16b_scales(Sk16bScales& S, float R, float C) {
+  S.R = R;
+  S.C = C;
+  sk16b_row_bcast(R, S.Rs);
+  sk16b_col_bcast(C, S.Cs);
+}
+
+// One iteration (row step, then column step, with the reference's eps masks);
+// rs / cs: the sums of the lane's own row / column that the steps divided by.
+MHC_DEV void sk16b_iter(const float (&K)[4][4], Sk16bScales& S, float eps, float& rs, float& cs) {
+  float p[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    float a = K[s][0] * S.Cs[0];
+    a = fmaf(K[s][1], S.Cs[1], a);
+    a = fmaf(K[s][2], S.Cs[2], a);
+    p[s] = fmaf(K[s][3], S.Cs[3], a);
+  }
+  rs = S.R * sk16b_row_own(p, SumOp{});
+  S.R *= rs > eps ? sk_rcp(rs) : 1.0f;
+  sk16b_row_bcast(S.R, S.Rs);
+  float q[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    float a = S.Rs[0] * K[0][t];
+    a = fmaf(S.Rs[1], K[1][t], a);
+    a = fmaf(S.Rs[2], K[2][t], a);
+    q[t] = fmaf(S.Rs[3], K[3][t], a);
+  }
+  cs = S.C * sk16b_col_own(q, SumOp{});
+  S.C *= cs > eps ? sk_rcp(cs) : 0.0f;
+  sk16b_col_bcast(S.C, S.Cs);
+}
+
+// Reverse of iteration k: G holds dL/dP_k on entry and dL/dP_{k-1} on exit.
+// Rk, rs, cs: the lane's own-row R_k and sums of iteration k; Rp, Cp: its
+// own-row R_{k-1} and own-column C_{k-1}.  For a step x -> s x with s = 1/sum:
+// d_in = s g - s^2 <g, in> (the reference's autograd of reference.py:37-46);
+// a masked column passes no gradient, a masked row passes it unchanged.
+MHC_DEV void sk16b_vjp_step(float (&G)[4][4], const float (&K)[4][4], float Rk, float rs, float cs, float Rp,
+                            float Cp, float eps) {
+  float Rkb[4];
+  sk16b_row_bcast(Rk, Rkb);
+  // column step: its input is diag(R_k) K diag(C_{k-1}); the column's scale C_{k-1} factors out of
+  // its dot product and is applied once, by the column's owner
+  float d[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    float a = (G[0][t] * K[0][t]) * Rkb[0];
+#pragma unroll
+    for (int s = 1; s < 4; ++s) a = fmaf(G[s][t] * K[s][t], Rkb[s], a);
+    d[t] = a;
+  }
+  const float dot = Cp * sk16b_col_own(d, SumOp{});
+  const float csc = cs > eps ? sk_rcp(cs) : 0.0f;
+  float scb[4], s2b[4];
+  sk16b_col_bcast(csc, scb);
+  sk16b_col_bcast(csc * csc * dot, s2b);
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) G[s][t] = fmaf(scb[t], G[s][t], -s2b[t]);
+  // row step: its input is diag(R_{k-1}) K diag(C_{k-1})
+  float Cpb[4];
+  sk16b_col_bcast(Cp, Cpb);
+  float e[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    float a = G[s][0] * (K[s][0] * Cpb[0]);
+    a = fmaf(G[s][1], K[s][1] * Cpb[1], a);
+    a = fmaf(G[s][2], K[s][2] * Cpb[2], a);
+    e[s] = fmaf(G[s][3], K[s][3] * Cpb[3], a);
+  }
+  const float rdot = Rp * sk16b_row_own(e, SumOp{});
+  const bool on = rs > eps;
+  const float rsc = on ? sk_rcp(rs) : 1.0f;
+  float rsb[4], r2b[4];
+  sk16b_row_bcast(rsc, rsb);
+  sk16b_row_bcast(on ? rsc * rsc * rdot : 0.0f, r2b);
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) G[s][t] = fmaf(rsb[s], G[s][t], -r2b[s]);
+}
+
+struct Sk16bLane {
+  int rb, cb, ro, co;  // block coordinates; own row and own column
+  int64_t m;           // matrix
+  bool valid;          // m < batch (lanes past the batch work on matrix 0 and store nothing)
+};
+
+MHC_DEV Sk16bLane sk16b_lane(int64_t batch) {
+  const int lane = threadIdx.x & 63;
+  Sk16bLane L;
+  L.rb = (lane >> 2) & 3;
+  L.cb = lane & 3;
+  L.ro = 4 * L.rb + L.cb;
+  L.co = 4 * L.cb + L.rb;
+  L.m = ((int64_t)blockIdx.x * (kSk16bThreads / 64) + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  L.valid = L.m < batch;
+  return L;
+}
+
+// REC: also record the VJP state ([batch][iters][R | rs | C | cs][16] floats at st).
+template <bool REC>
+__global__ __launch_bounds__(kSk16bThreads) void sinkhorn16b_fwd_kernel(const float* __restrict__ logits,
+                                                                        float* __restrict__ out, int64_t batch,
+                                                                        int iters, float eps,
+                                                                        float* __restrict__ st) {
+  const Sk16bLane L = sk16b_lane(batch);
+  const int64_t mm = L.valid ? L.m : 0;
+  float K[4][4], mx[4];
+  sk16b_load(logits + mm * 256, L.rb, L.cb, K);
+  sk16b_exp(K, mx);
+  Sk16bScales S;
+  sk16b_scales(S, 1.0f, 1.0f);
+  float* rec = REC ? st + mm * (int64_t)iters * 64 : nullptr;
+  for (int it = 0; it < iters; ++it) {
+    float rs, cs;
+    sk16b_iter(K, S, eps, rs, cs);
+    if constexpr (REC) {
+      if (L.valid) {
+        float* r = rec + (int64_t)it * 64;
+        r[L.ro] = S.R;
+        r[16 + L.ro] = rs;
+        r[32 + L.co] = S.C;
+        r[48 + L.co] = cs;
+      }
+    }
+  }
+  if (L.valid) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) K[s][t] = (S.Rs[s] * K[s][t]) * S.Cs[t];
+    sk16b_store(out + mm * 256, L.rb, L.cb, K);
+  }
+}
+
+// RECORDED: st holds the forward's record for these logits; otherwise the
+// iterations are recomputed (LDS: kSk16bThreads / 64 * nseg * 512 bytes).
+// dM may alias dlogits: each lane reads and writes only its own block.
+template <bool RECORDED>
+__global__ __launch_bounds__(kSk16bThreads) __attribute__((amdgpu_waves_per_eu(4))) void sinkhorn16b_bwd_kernel(const float* __restrict__ logits,
+                                                                        const float* dM, float* dlogits,
+                                                                        int64_t batch, int iters, float eps,
+                                                                        const float* __restrict__ st) {
+  extern __shared__ float2 sk16b_ck[];
+  const Sk16bLane L = sk16b_lane(batch);
+  const int64_t mm = L.valid ? L.m : 0;
+  float K[4][4], G[4][4];
+  {
+    float mx[4];
+    sk16b_load(logits + mm * 256, L.rb, L.cb, K);
+    sk16b_exp(K, mx);
+  }
+  sk16b_load(dM + mm * 256, L.rb, L.cb, G);
+  // segment sg covers iterations [first + (sg - 1) S, first + sg S) (sg >= 1) and segment 0 [0, first)
+  const int nseg = (iters + kSk16bSeg - 1) / kSk16bSeg;
+  const int first = iters - (nseg - 1) * kSk16bSeg;
+  const float* rec = RECORDED ? st + mm * (int64_t)iters * 64 : nullptr;
+  float2* ck = sk16b_ck + (int64_t)(threadIdx.x >> 6) * nseg * 64 + (threadIdx.x & 63);
+  if constexpr (!RECORDED) {
+    // the scales at each segment's start, lane-private (no cross-lane LDS use)
+    Sk16bScales S;
+    sk16b_scales(S, 1.0f, 1.0f);
+    for (int sg = 0; sg < nseg; ++sg) {
+      ck[sg * 64] = make_float2(S.R, S.C);
+      if (sg == nseg - 1) break;
+      const int len = sg == 0 ? first : kSk16bSeg;
+      for (int j = 0; j < len; ++j) {
+        float rs, cs;
+        sk16b_iter(K, S, eps, rs, cs);
+      }
+    }
+  }
+  for (int sg = nseg - 1; sg >= 0; --sg) {
+    const int it0 = sg == 0 ? 0 : first + (sg - 1) * kSk16bSeg;
+    const int len = sg == 0 ? first : kSk16bSeg;
+    float R0 = 1.0f, C0 = 1.0f;
+    float sR[kSk16bSeg], srs[kSk16bSeg], sC[kSk16bSeg], scs[kSk16bSeg];
+    if constexpr (RECORDED) {
+      if (it0 > 0) {
+        const float* r0 = rec + (int64_t)(it0 - 1) * 64;
+        R0 = r0[L.ro];
+        C0 = r0[32 + L.co];
+      }
+#pragma unroll
+      for (int j = 0; j < kSk16bSeg; ++j) {
+        if (j < len) {
+          const float* r = rec + (int64_t)(it0 + j) * 64;
+          sR[j] = r[L.ro];
+          srs[j] = r[16 + L.ro];
+          sC[j] = r[32 + L.co];
+          scs[j] = r[48 + L.co];
+        }
+      }
+    } else {
+      const float2 c = ck[sg * 64];
+      R0 = c.x;
+      C0 = c.y;
+      Sk16bScales S;
+      sk16b_scales(S, R0, C0);
+#pragma unroll
+      for (int j = 0; j < kSk16bSeg; ++j) {
+        if (j < len) {
+          sk16b_iter(K, S, eps, srs[j], scs[j]);
+          sR[j] = S.R;
+          sC[j] = S.C;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = kSk16bSeg - 1; j >= 0; --j) {
+      if (j < len) sk16b_vjp_step(G, K, sR[j], srs[j], scs[j], j > 0 ? sR[j - 1] : R0, j > 0 ? sC[j - 1] : C0, eps);
+    }
+  }
+  // through exp and the row-max shift: the max's gradient split evenly among
+  // tied maxima (zero in exact arithmetic)
+  float Hr[4][4], mx[4];
+  sk16b_load(logits + mm * 256, L.rb, L.cb, Hr);
+  {
+    float pm[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) pm[s] = fmaxf(fmaxf(Hr[s][0], Hr[s][1]), fmaxf(Hr[s][2], Hr[s][3]));
+    sk16b_row_bcast(sk16b_row_own(pm, MaxOp{}), mx);
+  }
+  float tot[4], cnt[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    float a = 0.0f, c = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      G[s][t] *= K[s][t];
+      a += G[s][t];
+      c += Hr[s][t] == mx[s] ? 1.0f : 0.0f;
+    }
+    tot[s] = a;
+    cnt[s] = c;
+  }
+  float totb[4], cntb[4];
+  sk16b_row_bcast(sk16b_row_own(tot, SumOp{}), totb);
+  sk16b_row_bcast(sk16b_row_own(cnt, SumOp{}), cntb);
+  if (L.valid) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float corr = cntb[s] > 0.0f ? totb[s] / cntb[s] : 0.0f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) G[s][t] -= Hr[s][t] == mx[s] ? corr : 0.0f;
+    }
+    sk16b_store(dlogits + mm * 256, L.rb, L.cb, G);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
@@ -458,8 +843,19 @@ bool use_sk16(int n, const void* a, const void* b, const void* c) {
   return aligned(a, 16) && aligned(b, 16) && (c == nullptr || aligned(c, 16));
 }
 
-// MHC_SK16_CPL (2 or 4) selects the columns per lane (tuning override).
-int sk16_cpl() { return knob(kKnobSk16Cpl, 4) == 2 ? 2 : 4; }
+// MHC_SK16_CPL selects the n == 16 batched layout: 0 (default) the block
+// layout (16 lanes per matrix), 4 or 2 the kernels with that many columns per
+// lane (4 or 8 lanes per matrix).
+int sk16_cpl() {
+  const int v = knob(kKnobSk16Cpl, 0);
+  return v == 2 ? 2 : v == 4 ? 4 : 0;
+}
+
+// The block layout's VJP keeps a checkpoint per kSk16bSeg iterations in LDS.
+int sk16b_nseg(int iters) { return (int)ceil_div((int64_t)iters, (int64_t)kSk16bSeg); }
+bool sk16b_vjp_ok(int iters) { return sk16b_nseg(iters) <= kSk16bMaxSeg; }
+size_t sk16b_lds_bytes(int iters) { return (size_t)(kSk16bThreads / 64) * sk16b_nseg(iters) * 64 * sizeof(float2); }
+int64_t sk16b_blocks(int64_t batch) { return ceil_div(batch, (int64_t)4 * (kSk16bThreads / 64)); }
 
 int64_t sk16_blocks(int64_t batch, int cpl) {
   return ceil_div(batch, (int64_t)(cpl == 4 ? Sk16<4>::MPW : Sk16<2>::MPW) * (kSk16Threads / 64));
@@ -607,6 +1003,12 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
   hipStream_t s = (hipStream_t)stream;
   if (use_sk16(n, logits, M, nullptr)) {
     const int cpl = sk16_cpl();
+    if (cpl == 0) {
+      hipLaunchKernelGGL((sinkhorn16b_fwd_kernel<false>), dim3((unsigned)sk16b_blocks(batch)), dim3(kSk16bThreads),
+                         0, s, logits, M, batch, iters, eps, nullptr);
+      MHC_CHECK_LAUNCH("sinkhorn16b_fwd_kernel");
+      return MHC_OK;
+    }
     const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
     if (cpl == 4)
       hipLaunchKernelGGL((sinkhorn16_fwd_kernel<4, false>), g, b, 0, s, logits, M, batch, iters, eps, nullptr);
@@ -646,7 +1048,8 @@ extern "C" size_t mhc_sinkhorn_bwd_workspace_bytes(int64_t batch, int n, int ite
   if (n < 1 || n > MHC_MAX_N || batch <= 0 || iters < 0) return 0;
   if (use_blk(n)) return plan_blk(batch, n, iters, device_cu_count()).ws_bytes;
   const size_t gen = plan_bwd(batch, n, iters, device_cu_count()).ws_bytes;
-  if (n == 16) return std::max(gen, sk16_state_bytes(batch, iters) + 256);
+  // n == 16: the block layout needs none; the other layouts keep their state there
+  if (n == 16 && !(sk16_cpl() == 0 && sk16b_vjp_ok(iters))) return std::max(gen, sk16_state_bytes(batch, iters) + 256);
   return gen;
 }
 
@@ -660,6 +1063,12 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
   if (batch == 0) return MHC_OK;
   MHC_CHECK_ARG(logits != nullptr && dM != nullptr && dlogits != nullptr, "null pointer argument");
   hipStream_t s = (hipStream_t)stream;
+  if (use_sk16(n, logits, dM, dlogits) && sk16_cpl() == 0 && sk16b_vjp_ok(iters)) {
+    hipLaunchKernelGGL((sinkhorn16b_bwd_kernel<false>), dim3((unsigned)sk16b_blocks(batch)), dim3(kSk16bThreads),
+                       sk16b_lds_bytes(iters), s, logits, dM, dlogits, batch, iters, eps, nullptr);
+    MHC_CHECK_LAUNCH("sinkhorn16b_bwd_kernel");
+    return MHC_OK;
+  }
   if (use_sk16(n, logits, dM, dlogits) && workspace != nullptr) {
     // The recorded state starts at the first 256-byte boundary of the workspace:
     // each matrix's records (256 bytes per iteration) then fill whole cache
@@ -669,7 +1078,7 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
     const size_t need = sk16_state_bytes(batch, iters);
     if (workspace_bytes >= need + pad) {
       float* st = reinterpret_cast<float*>(base + pad);
-      const int cpl = sk16_cpl();
+      const int cpl = sk16_cpl() == 2 ? 2 : 4;
       const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
       if (cpl == 4)
         hipLaunchKernelGGL((sinkhorn16_bwd_kernel<4, false>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps,
@@ -760,6 +1169,12 @@ extern "C" int mhc_sinkhorn_fwd_record(const float* logits, float* M, void* stat
     return MHC_OK;
   }
   const int cpl = sk16_cpl();
+  if (cpl == 0) {
+    hipLaunchKernelGGL((sinkhorn16b_fwd_kernel<true>), dim3((unsigned)sk16b_blocks(batch)), dim3(kSk16bThreads), 0,
+                       s, logits, M, batch, iters, eps, st);
+    MHC_CHECK_LAUNCH("sinkhorn16b_fwd_kernel");
+    return MHC_OK;
+  }
   const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
   if (cpl == 4)
     hipLaunchKernelGGL((sinkhorn16_fwd_kernel<4, true>), g, b, 0, s, logits, M, batch, iters, eps, st);
@@ -793,6 +1208,12 @@ extern "C" int mhc_sinkhorn_bwd_recorded(const float* logits, const float* dM, f
     return MHC_OK;
   }
   const int cpl = sk16_cpl();
+  if (cpl == 0) {
+    hipLaunchKernelGGL((sinkhorn16b_bwd_kernel<true>), dim3((unsigned)sk16b_blocks(batch)), dim3(kSk16bThreads), 0,
+                       s, logits, dM, dlogits, batch, iters, eps, st);
+    MHC_CHECK_LAUNCH("sinkhorn16b_bwd_kernel");
+    return MHC_OK;
+  }
   const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
   if (cpl == 4)
     hipLaunchKernelGGL((sinkhorn16_bwd_kernel<4, true>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);

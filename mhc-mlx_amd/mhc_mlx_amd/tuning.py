@@ -52,8 +52,8 @@ KNOBS: dict[str, tuple[str, list[int]]] = {
     # 128-channel slabs per wave of the n = 16 MFMA kernels
     "mhc_fused_n16": ("MHC_FWD_SPW", [2, 1]),
     "mhc_fused_bwd_n16": ("MHC_BWD_SPW", [2, 1]),
-    # columns per lane of the batched n = 16 Sinkhorn kernels
-    "sinkhorn_16": ("MHC_SK16_CPL", [4, 2]),
+    # batched n = 16 Sinkhorn layout: 0 the 4 x 4-block layout (16 lanes per matrix), 4 / 2 columns per lane
+    "sinkhorn_16": ("MHC_SK16_CPL", [0, 4, 2]),
     # 8-channel chunks per thread of the layer-wide n <= 8 forward (1 unless C needs 2)
     "mhc_fused": ("MHC_FWD_CH", [1, 2]),
     # persistent workgroups of the layer-wide backward (0: the library's choice)

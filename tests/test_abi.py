@@ -113,7 +113,11 @@ def test_residual_add_agg_rejects_bad_arguments_on_the_host(lib):
 
 
 def test_sinkhorn_state_is_for_n16_to_64_and_checked_on_the_host(lib, knobs):
+    # n = 16: the same record format for the block layout (default) and the lanes-per-matrix layouts
     assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 8 * 20 * 256 + 256
+    knobs("MHC_SK16_CPL", 4)
+    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 8 * 20 * 256 + 256
+    knobs("MHC_SK16_CPL", None)
     # block layout (16 < n <= 64): six vectors of next_pow2(n) floats per matrix and iteration
     assert lib.mhc_sinkhorn_state_bytes(8, 32, 20) == 8 * 20 * 6 * 32 * 4 + 256
     assert lib.mhc_sinkhorn_state_bytes(3, 24, 7) == 3 * 7 * 6 * 32 * 4 + 256
@@ -144,3 +148,12 @@ def test_sinkhorn_state_is_for_n16_to_64_and_checked_on_the_host(lib, knobs):
     assert lib.mhc_sinkhorn_bwd_recorded(fake, fake, fake, None, 1 << 20, 8, 16, 20, eps, None) == -1
     assert lib.mhc_sinkhorn_bwd_recorded(fake, fake, fake, fake, 1 << 20, 8, 16, -1, eps, None) == -1
     assert lib.mhc_sinkhorn_fwd_record(fake, fake, fake, 0, 0, 16, 20, eps, None) == 0  # empty batch
+
+
+def test_torch_binding_loads_and_exports_the_layer_calls():
+    """_mhc_torch.so (csrc/torch_ext.cpp) loads after libmhc_hip.so and exports MHCLayer's two calls."""
+    from mhc_mlx_amd import _ext
+
+    mod = _ext.load()
+    assert callable(mod.layer_apply) and callable(mod.layer_forward_nograd)
+    assert _ext.load() is mod

@@ -159,7 +159,8 @@ def test_sinkhorn_rejects_bad_shapes():
 
 
 # ------------------------------------------------ n = 16 batched kernels
-# (four lanes per matrix, 16 matrices per wave, VJP state in the workspace)
+# (default: the 4 x 4-block layout, 16 lanes per matrix, VJP state recomputed in registers in segments of
+# 9 iterations; MHC_SK16_CPL = 4 / 2: four / eight lanes per matrix, VJP state in the workspace)
 
 @pytest.mark.parametrize("batch", [1, 15, 17, 64, 65, 1000])
 def test_sinkhorn16_batches_and_tails(batch):
@@ -218,14 +219,18 @@ def test_sinkhorn16_vjp_in_place_c_abi():
 
 
 @pytest.mark.parametrize("B,iters,cpl_fwd,cpl_bwd", [(200, 20, "4", "4"), (33, 1, "4", "2"), (65, 0, "2", "4"),
-                                                   (1000, 20, "2", "2")])
+                                                   (1000, 20, "2", "2"), (200, 20, "0", "0"), (1000, 20, "0", "0"),
+                                                   (77, 19, "0", "0"), (50, 37, "0", "0"), (33, 1, "0", "4"),
+                                                   (65, 9, "4", "0")])
 def test_sinkhorn16_recorded_state_matches_recompute(B, iters, cpl_fwd, cpl_bwd, knobs):
     """mhc_sinkhorn_fwd_record / mhc_sinkhorn_bwd_recorded give bitwise the results of
     mhc_sinkhorn_fwd / mhc_sinkhorn_bwd (the same iterations, recorded in the forward instead of
-    recomputed in the VJP) when both use the same lanes per matrix.  With different widths the
-    recorded row sums were added in another order (last-bit differences), so that case is held to
-    the oracle's tolerance.  The state buffer is deliberately not 256-byte aligned; masked rows and
-    columns included."""
+    recomputed in the VJP) when both use the same layout (MHC_SK16_CPL 0: the block layout, whose VJP
+    recomputes its segments from LDS checkpoints; 4 / 2 lanes-per-matrix layouts).  Across layouts
+    the sums associate differently (last-bit differences), so those cases are held to the oracle's
+    tolerance.  The state buffer is deliberately not 256-byte aligned; masked rows and columns
+    included."""
+    knobs("MHC_SK16_RECORD", 1)
     import ctypes
 
     from mhc_mlx_amd import _lib
@@ -259,6 +264,44 @@ def test_sinkhorn16_recorded_state_matches_recompute(B, iters, cpl_fwd, cpl_bwd,
         assert torch.equal(d_rec, d_plain)
     rg = O.sinkhorn_knopp_vjp(H.astype(np.float64), dM, iters=iters, eps=1e-5)
     assert rel_err(np_of(d_rec), rg, 1.0) < 1e-5
+
+
+@pytest.mark.parametrize("iters", [0, 1, 8, 9, 10, 17, 18, 19, 20, 28, 37, 300])
+def test_sinkhorn16_block_layout_iteration_counts(iters):
+    """The block layout's VJP at iteration counts around its 9-iteration segments (segments aligned to the
+    end, the first one shorter), with masked columns; 300 iterations need more than its 32 checkpoints and
+    take the four-lanes-per-matrix VJP instead.  Forward and VJP against the oracle; the VJP of 300
+    iterations is a long product of steps and is held at 1e-4."""
+    B = 37
+    g = rng(4500 + iters)
+    H = (2.0 * g.standard_normal((B, 16, 16))).astype(np.float32)
+    H[::4, :, 2] = -40.0
+    dM = g.standard_normal((B, 16, 16)).astype(np.float32)
+    got = _fwd(H, iters, 1e-5)
+    assert rel_err(got, O.mixing_matrix_from_logits(H.astype(np.float64), iters=iters, eps=1e-5), 1.0) < 1e-5
+    Ht = dev_tensor(H).requires_grad_(True)
+    ops.sinkhorn_knopp_hip_autograd(Ht, iters=iters, eps=1e-5).backward(dev_tensor(dM))
+    rg = O.sinkhorn_knopp_vjp(H.astype(np.float64), dM, iters=iters, eps=1e-5)
+    assert rel_err(np_of(Ht.grad), rg, 1.0) < (1e-4 if iters > 100 else 1e-5)
+
+
+@pytest.mark.parametrize("cpl", [4, 2])
+def test_sinkhorn16_layouts_agree(cpl, knobs):
+    """The block layout (default) and the lanes-per-matrix layouts compute the same iterations with the sums
+    associated differently: M and the VJP agree to fp32 rounding."""
+    B = 300
+    g = rng(4600 + cpl)
+    H = (2.0 * g.standard_normal((B, 16, 16))).astype(np.float32)
+    dM = g.standard_normal((B, 16, 16)).astype(np.float32)
+    res = {}
+    for layout in (0, cpl):
+        knobs("MHC_SK16_CPL", layout)
+        Ht = dev_tensor(H).requires_grad_(True)
+        M = ops.sinkhorn_knopp_hip_autograd(Ht, iters=20, eps=1e-6)
+        M.backward(dev_tensor(dM))
+        res[layout] = (np_of(M), np_of(Ht.grad))
+    assert rel_err(res[0][0], res[cpl][0], 1.0) < 2e-6
+    assert rel_err(res[0][1], res[cpl][1], 1.0) < 1e-5
 
 
 @pytest.mark.parametrize("B,n,iters", [(1, 32, 20), (1, 24, 20), (5, 32, 3), (1, 64, 20), (3, 48, 1), (9, 17, 0),
