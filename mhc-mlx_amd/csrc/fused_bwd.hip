@@ -1865,7 +1865,7 @@ extern "C" int mhc_fused_bwd_partials(const void* x, int x_dtype, const void* do
 namespace mhc {
 namespace {
 
-// Reduce `G` partial rows: reduce_rows_kernel then param_finish_kernel.
+// Reduce `G` partial rows: reduce_rows_kernel (when G > kReduceSplit) then param_finish_kernel.
 // With hres != NULL the Sinkhorn VJP of the reduced dM runs in the second
 // launch; returns 1 when that fusion is not possible (per-token parameters,
 // n > 8, or VJP state beyond the LDS budget).
@@ -1891,14 +1891,20 @@ int launch_param_reduce(const void* workspace, size_t workspace_bytes, int64_t G
     MHC_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                   "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
     MHC_CHECK_ARG(aligned(workspace, 16), "workspace must be 16-byte aligned");
-    const int S0 = (int)std::min<int64_t>(kReduceSplit, G);
-    const int rows = (int)ceil_div(G, S0);
-    R.S = (int)ceil_div(G, rows);
-    float* part2 = (float*)workspace + G * (int64_t)R.P;
-    hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)ceil_div(R.P / 4, 256), (unsigned)R.S), dim3(256), 0,
-                       s, (const float*)workspace, part2, G, R.P, rows);
-    MHC_CHECK_LAUNCH("reduce_rows_kernel");
-    R.part2 = part2;
+    if (G <= kReduceSplit) {
+      // at most kReduceSplit rows: reduce_rows_kernel would copy them unchanged (one row per output
+      // row), so param_finish_kernel reads them where they lie; one launch fewer at small batch
+      R.S = (int)G;
+      R.part2 = (const float*)workspace;
+    } else {
+      const int rows = (int)ceil_div(G, (int64_t)kReduceSplit);
+      R.S = (int)ceil_div(G, rows);
+      float* part2 = (float*)workspace + G * (int64_t)R.P;
+      hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)ceil_div(R.P / 4, 256), (unsigned)R.S), dim3(256), 0,
+                         s, (const float*)workspace, part2, G, R.P, rows);
+      MHC_CHECK_LAUNCH("reduce_rows_kernel");
+      R.part2 = part2;
+    }
   } else {
     R.S = 0;  // no rows: every sum is zero
     R.part2 = nullptr;

@@ -1,0 +1,197 @@
+// Torch binding of libmhc_hip for MHCLayer's hot calls (mhc_mlx/layer.py:339-435).
+//
+// The module's work per call is one or two library launches; at small batch
+// its latency is the host code around them.  This binding does that host code
+// in C++ over the same C ABI (include/mhc_hip.h): the layer's autograd
+// Function (forward: Sinkhorn projection + fused kernel; backward: partial
+// sums, fixed-order reduction, Sinkhorn VJP) and the no-gradient forward.
+// The backward therefore runs on the autograd engine's thread without Python.
+// Every launch goes to the current HIP stream of the input's device, as the
+// Python wrappers' do; arguments are validated by the Python caller
+// (mhc_mlx_amd/ops.py), and the library checks its own again.
+#include <torch/extension.h>
+
+#include <c10/hip/HIPStream.h>
+
+#include "mhc_hip.h"
+
+namespace {
+
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+int dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return MHC_DTYPE_F32;
+    case at::kBFloat16: return MHC_DTYPE_BF16;
+    case at::kHalf: return MHC_DTYPE_F16;
+    default: TORCH_CHECK_VALUE(false, "unsupported dtype ", t, "; expected float32, bfloat16 or float16");
+  }
+}
+
+void* stream_of(const at::Tensor& t) { return c10::hip::getCurrentHIPStream(t.get_device()).stream(); }
+
+// Library status -> exception: a rejected argument is a ValueError, a HIP
+// failure a RuntimeError (the Python wrappers' convention).
+void check(int rc, const char* what) {
+  if (rc == MHC_OK) return;
+  const char* msg = mhc_last_error();
+  TORCH_CHECK_VALUE(rc > 0, what, ": ", msg ? msg : "invalid argument");
+  TORCH_CHECK(false, what, " failed (hip error ", rc, "): ", msg ? msg : "");
+}
+
+at::Tensor f32(const at::Tensor& t) {
+  return t.scalar_type() == at::kFloat && t.is_contiguous() ? t : t.to(at::kFloat).contiguous();
+}
+
+// Every tensor on x's GPU (the kernels take raw device pointers).
+void check_device(const at::Tensor& x, std::initializer_list<const at::Tensor*> ps) {
+  TORCH_CHECK_VALUE(x.is_cuda(), "the HIP path needs GPU tensors (got x on ", x.device(), ")");
+  for (const at::Tensor* p : ps)
+    TORCH_CHECK_VALUE(p->device() == x.device(), "parameters must be on x's device ", x.device(), " (got ",
+                      p->device(), ")");
+}
+
+float* fp(const at::Tensor& t) { return t.defined() ? t.data_ptr<float>() : nullptr; }
+
+// mhc_layer_fwd: out [T, n, C] of out_dtype and M (Sinkhorn of the logits,
+// [n, n] or [T, n, n]); with `state` defined, the projection also records its
+// VJP state there (mhc_sinkhorn_fwd_record + mhc_fused_fwd).
+std::pair<at::Tensor, at::Tensor> layer_fwd(const at::Tensor& x, const at::Tensor& hp, const at::Tensor& hq,
+                                            const at::Tensor& hr, const at::Tensor& w, int64_t iters, double eps,
+                                            at::ScalarType out_dtype, bool per_token, const at::Tensor& state) {
+  const int64_t T = x.size(0);
+  const int n = (int)x.size(1), C = (int)x.size(2);
+  at::Tensor out = at::empty({T, n, C}, x.options().dtype(out_dtype));
+  at::Tensor M = at::empty_like(hr);
+  void* s = stream_of(x);
+  if (!state.defined()) {
+    check(mhc_layer_fwd(x.data_ptr(), dtype_code(x.scalar_type()), fp(hp), fp(hq), fp(hr), fp(w), out.data_ptr(),
+                        dtype_code(out_dtype), fp(M), T, n, C, per_token ? 1 : 0, (int)iters, (float)eps, s),
+          "mhc_layer_fwd");
+    return {out, M};
+  }
+  check(mhc_sinkhorn_fwd_record(fp(hr), fp(M), state.data_ptr(), (size_t)state.numel(), per_token ? T : 1, n,
+                                (int)iters, (float)eps, s),
+        "mhc_sinkhorn_fwd_record");
+  check(mhc_fused_fwd(x.data_ptr(), dtype_code(x.scalar_type()), fp(M), per_token ? (int64_t)n * n : 0, fp(hp),
+                      fp(hq), per_token ? n : 0, MHC_H_RAW, fp(w), out.data_ptr(), dtype_code(out_dtype), nullptr, T,
+                      n, C, (float)eps, s),
+        "mhc_fused_fwd");
+  return {out, M};
+}
+
+// VJP of layer_fwd: (dx, dH_pre_raw, dH_post_raw, dH_res_raw, d_rms_weight).
+variable_list layer_bwd(const at::Tensor& x, const at::Tensor& g_in, const at::Tensor& hp, const at::Tensor& hq,
+                        const at::Tensor& hr, const at::Tensor& M, const at::Tensor& w, int64_t iters, double eps,
+                        bool per_token, const at::Tensor& state) {
+  const int64_t T = x.size(0);
+  const int n = (int)x.size(1), C = (int)x.size(2);
+  const at::ScalarType gt = g_in.scalar_type() == at::kFloat || g_in.scalar_type() == x.scalar_type()
+                                ? g_in.scalar_type() : at::kFloat;
+  at::Tensor g = g_in.scalar_type() == gt ? g_in : g_in.to(gt);
+  if (!g.is_contiguous()) g = g.contiguous();
+  at::Tensor dx = at::empty_like(x);
+  // the four parameter gradients as views of one allocation (each contiguous with the parameter's shape,
+  // starting on a 256-byte boundary as a separate allocation would)
+  auto up = [](int64_t v) { return (v + 63) / 64 * 64; };
+  const int64_t o1 = up(hp.numel()), o2 = o1 + up(hq.numel()), o3 = o2 + up(hr.numel());
+  at::Tensor pg = at::empty({o3 + C}, w.options());
+  at::Tensor dpre = pg.narrow(0, 0, hp.numel()).view(hp.sizes());
+  at::Tensor dpost = pg.narrow(0, o1, hq.numel()).view(hq.sizes());
+  at::Tensor dres = pg.narrow(0, o2, hr.numel()).view(hr.sizes());
+  at::Tensor dw = pg.narrow(0, o3, C);
+  const int xc = dtype_code(x.scalar_type()), gc = dtype_code(gt);
+  void* s = stream_of(x);
+  const int pt = per_token ? 1 : 0;
+  if (!state.defined()) {
+    const size_t nb = mhc_layer_bwd_workspace_bytes(T, n, C, pt, (int)iters);
+    at::Tensor ws = at::empty({(int64_t)std::max<size_t>(nb, 1)}, x.options().dtype(at::kByte));
+    check(mhc_layer_bwd(x.data_ptr(), xc, g.data_ptr(), gc, fp(hp), fp(hq), fp(hr), fp(M), fp(w), dx.data_ptr(),
+                        fp(dpre), fp(dpost), fp(dres), fp(dw), ws.data_ptr(), nb, T, n, C, pt, (int)iters, (float)eps,
+                        s),
+          "mhc_layer_bwd");
+    return {dx, dpre, dpost, dres, dw};
+  }
+  // from the recorded Sinkhorn state: partial sums (per token: dM of each token into dres, the activated-H
+  // chain applied in the kernel), the reduction, then the recorded VJP (in place per token)
+  at::Tensor dM = per_token ? dres : at::empty({n, n}, hr.options());
+  const size_t nb = mhc_fused_bwd_workspace_bytes(T, n, C, pt);
+  at::Tensor ws = at::empty({(int64_t)std::max<size_t>(nb, 1)}, x.options().dtype(at::kByte));
+  int64_t np = 0;
+  check(mhc_fused_bwd_partials(x.data_ptr(), xc, g.data_ptr(), gc, fp(M), pt ? (int64_t)n * n : 0, fp(hp), fp(hq),
+                               pt ? n : 0, MHC_H_RAW, fp(w), dx.data_ptr(), xc, pt ? fp(dres) : nullptr,
+                               pt ? fp(dpre) : nullptr, pt ? fp(dpost) : nullptr, ws.data_ptr(), nb, T, n, C,
+                               (float)eps, &np, s),
+        "mhc_fused_bwd_partials");
+  check(mhc_reduce_param_grads(ws.data_ptr(), nb, np, n, C, pt, pt ? nullptr : fp(hp), pt ? nullptr : fp(hq),
+                               MHC_H_RAW, pt ? nullptr : fp(dM), pt ? nullptr : fp(dpre), pt ? nullptr : fp(dpost),
+                               fp(dw), s),
+        "mhc_reduce_param_grads");
+  check(mhc_sinkhorn_bwd_recorded(fp(hr), fp(dM), fp(dres), state.data_ptr(), (size_t)state.numel(), pt ? T : 1, n,
+                                  (int)iters, (float)eps, s),
+        "mhc_sinkhorn_bwd_recorded");
+  return {dx, dpre, dpost, dres, dw};
+}
+
+// MHCLayer forward/backward from raw parameters, as an autograd Function.
+// Inputs as the library takes them: x contiguous (fp32 / bf16 / fp16),
+// parameters fp32 contiguous on x's device.  With `record` the Sinkhorn
+// projection records its VJP state (n = 16 per token, 16 < n <= 64) when
+// the library has a recorded path for n.
+struct LayerFn : public torch::autograd::Function<LayerFn> {
+  static at::Tensor forward(AutogradContext* ctx, const at::Tensor& x, const at::Tensor& hpre,
+                            const at::Tensor& hpost, const at::Tensor& hres, const at::Tensor& w, int64_t iters,
+                            double eps, int64_t out_code, bool per_token, bool record) {
+    const at::ScalarType out_dtype = out_code == MHC_DTYPE_BF16 ? at::kBFloat16
+                                     : out_code == MHC_DTYPE_F16 ? at::kHalf : at::kFloat;
+    at::Tensor state;
+    // (the n = 16 batched kernels read 16-byte aligned logits: an offset view is projected without a record)
+    if (record && x.size(0) > 0 && (x.size(1) != 16 || reinterpret_cast<uintptr_t>(hres.data_ptr()) % 16 == 0)) {
+      const size_t nst = mhc_sinkhorn_state_bytes(per_token ? x.size(0) : 1, (int)x.size(1), (int)iters);
+      if (nst > 0) state = at::empty({(int64_t)nst}, x.options().dtype(at::kByte));
+    }
+    auto r = layer_fwd(x, hpre, hpost, hres, w, iters, eps, out_dtype, per_token, state);
+    ctx->save_for_backward({x, hpre, hpost, hres, w, r.second, state});
+    ctx->saved_data["iters"] = iters;
+    ctx->saved_data["eps"] = eps;
+    ctx->saved_data["per_token"] = per_token;
+    return r.first;
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const auto sv = ctx->get_saved_variables();
+    variable_list g = layer_bwd(sv[0], grads[0], sv[1], sv[2], sv[3], sv[5], sv[4], ctx->saved_data["iters"].toInt(),
+                                ctx->saved_data["eps"].toDouble(), ctx->saved_data["per_token"].toBool(), sv[6]);
+    return {g[0], g[1], g[2], g[3], g[4], at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
+  }
+};
+
+// Autograd entry: parameters are converted to contiguous fp32 here (a no-op
+// when they already are), with the conversion inside the autograd graph so
+// gradients reach the caller's tensors in their own dtype.
+at::Tensor layer_apply(const at::Tensor& x, const at::Tensor& hpre, const at::Tensor& hpost, const at::Tensor& hres,
+                       const at::Tensor& w, int64_t iters, double eps, int64_t out_code, bool per_token, bool record) {
+  check_device(x, {&hpre, &hpost, &hres, &w});
+  return LayerFn::apply(x.contiguous(), f32(hpre), f32(hpost), f32(hres), f32(w), iters, eps, out_code, per_token,
+                        record);
+}
+
+// The forward of a call that needs no gradient: out only.
+at::Tensor layer_forward_nograd(const at::Tensor& x, const at::Tensor& hpre, const at::Tensor& hpost,
+                                const at::Tensor& hres, const at::Tensor& w, int64_t iters, double eps,
+                                int64_t out_code, bool per_token) {
+  check_device(x, {&hpre, &hpost, &hres, &w});
+  const at::ScalarType out_dtype = out_code == MHC_DTYPE_BF16 ? at::kBFloat16
+                                   : out_code == MHC_DTYPE_F16 ? at::kHalf : at::kFloat;
+  return layer_fwd(x.contiguous(), f32(hpre), f32(hpost), f32(hres), f32(w), iters, eps, out_dtype, per_token,
+                   at::Tensor()).first;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "torch binding of libmhc_hip for MHCLayer's forward and backward";
+  m.def("layer_apply", &layer_apply, "MHCLayer forward with its backward as a C++ autograd Function");
+  m.def("layer_forward_nograd", &layer_forward_nograd, "MHCLayer forward without autograd");
+}

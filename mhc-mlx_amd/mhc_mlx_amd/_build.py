@@ -51,6 +51,42 @@ def _compile(hipcc: str, src: Path, obj: Path) -> None:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{msg}")
 
 
+EXT_NAME = "_mhc_torch"
+EXT_PATH = PKG_DIR / (EXT_NAME + ".so")
+
+
+def build_ext(verbose: bool = True) -> Path:
+    """Compile the torch binding (csrc/torch_ext.cpp) into _mhc_torch.so next to libmhc_hip.so.
+
+    A plain C++ torch extension (g++, torch's headers and c10_hip for the current HIP stream); its
+    calls into libmhc_hip resolve against the library, which _lib.load() opens with RTLD_GLOBAL
+    before the binding is imported.
+    """
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    from . import _lib
+
+    _lib.load()
+    t0 = time.time()
+    bdir = PKG_DIR.parent / "_build" / "torch_ext"
+    bdir.mkdir(parents=True, exist_ok=True)
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    ce.load(name=EXT_NAME, sources=[str(CSRC / "torch_ext.cpp")],
+            extra_include_paths=[str(INCLUDE), str(rocm / "include")],
+            extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__=1"],
+            extra_ldflags=[f"-L{torch_lib}", "-lc10_hip"],
+            build_directory=str(bdir), verbose=False, is_python_module=True)
+    built = bdir / (EXT_NAME + ".so")
+    tmp = EXT_PATH.with_suffix(".so.tmp")
+    shutil.copyfile(built, tmp)
+    os.replace(tmp, EXT_PATH)
+    if verbose:
+        print(f"[mhc_mlx_amd] built {EXT_PATH} in {time.time() - t0:.1f}s", file=sys.stderr)
+    return EXT_PATH
+
+
 def build(verbose: bool = True, jobs: int | None = None) -> Path:
     """Compile every HIP source for gfx950 and link libmhc_hip.so. Returns its path."""
     hipcc = _hipcc()
@@ -77,3 +113,4 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
 
 if __name__ == "__main__":
     build()
+    build_ext()

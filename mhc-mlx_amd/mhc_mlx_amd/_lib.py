@@ -102,7 +102,8 @@ def load(path: Path | None = None) -> ctypes.CDLL:
                 f"libmhc_hip.so not found at {p}; build it with "
                 "`python -c 'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)"
             )
-        lib = ctypes.CDLL(str(p))
+        # RTLD_GLOBAL: the torch binding (_mhc_torch.so) resolves its C-ABI calls against this library
+        lib = ctypes.CDLL(str(p), mode=ctypes.RTLD_GLOBAL)
         for name, (args, res) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = args

@@ -39,7 +39,7 @@ import warnings
 import torch
 import torch.nn as nn
 
-from . import _lib, ops
+from . import _lib, ops, profiling
 from . import reference as ref
 
 __all__ = ["MHCLayer", "MHCRewire", "hip_available"]
@@ -314,25 +314,27 @@ class MHCLayer(nn.Module):
             return return_dtype
         return None
 
-    def _forward_nograd(self, x, return_dtype):
-        """The HIP forward of a call that needs no gradient (inference, torch.no_grad), with the fewest
-        host steps: a single-token forward is launch-bound, so its latency is mostly this code.  Returns
-        None whenever the general path has something to decide (a shape error, CPU tensors, the torch
-        path, a gradient, a library error), and forward() then takes that path."""
+    def _forward_fast(self, x, return_dtype):
+        """The HIP forward with the fewest host steps: one call into the torch binding, which allocates
+        the output and, when a gradient is needed, records the C++ autograd node whose backward runs the
+        library's VJP.  At small batch the layer's latency is mostly this code.  Returns None whenever the
+        general path has something to decide (a shape error, tensors off the GPU, the torch path, a kernel
+        timer, a library error), and forward() then takes that path."""
         if not self.use_metal or self.n > _lib.MAX_N or x.ndim != 3 or x.shape[1] != self.n or x.shape[2] != self.C:
             return None
         ps = self._parameters
         hp, hq, hr, w = ps.get("H_pre_raw"), ps.get("H_post_raw"), ps.get("H_res_raw"), ps.get("rms_weight")
-        if hp is None or hq is None or hr is None or w is None or _disabled_by_env():
-            return None
-        if torch.is_grad_enabled() and (x.requires_grad or hp.requires_grad or hq.requires_grad
-                                        or hr.requires_grad or w.requires_grad):
+        if hp is None or hq is None or hr is None or w is None or profiling._active is not None or _disabled_by_env():
             return None
         xdt = x.dtype
         kdt = return_dtype if return_dtype is xdt and xdt in _HALF else torch.float32
         try:
-            out = ops.layer_forward_nograd(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, kdt)
-        except RuntimeError:
+            if torch.is_grad_enabled() and (x.requires_grad or hp.requires_grad or hq.requires_grad
+                                            or hr.requires_grad or w.requires_grad):
+                out = ops.layer_apply(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, kdt)
+            else:
+                out = ops.layer_forward_nograd(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, kdt)
+        except (RuntimeError, ValueError):
             return None
         if out is not None and return_dtype is not None and out.dtype != return_dtype:
             out = out.to(return_dtype)
@@ -340,7 +342,7 @@ class MHCLayer(nn.Module):
 
     def forward(self, x_expanded: torch.Tensor, *, return_dtype: torch.dtype | None = None) -> torch.Tensor:
         """Run the mHC layer on x_expanded [B, n, C] (layer.py:339-435)."""
-        out = self._forward_nograd(x_expanded, return_dtype)
+        out = self._forward_fast(x_expanded, return_dtype)
         if out is not None:
             return out
         B, n, C = self._check(x_expanded)

@@ -29,7 +29,7 @@ import ctypes
 
 import torch
 
-from . import _lib, profiling
+from . import _ext, _lib, profiling
 from .profiling import timed
 
 __all__ = [
@@ -100,6 +100,17 @@ def _needs_grad(*ts) -> bool:
     if not torch.is_grad_enabled():
         return False
     return any(t is not None and t.requires_grad for t in ts)
+
+
+_BINDING = None
+
+
+def _binding():
+    """The torch binding (_mhc_torch.so): MHCLayer's forward / backward in C++ over the same C ABI."""
+    global _BINDING
+    if _BINDING is None:
+        _BINDING = _ext.load()
+    return _BINDING
 
 
 def _ws(nbytes: int, dev) -> torch.Tensor | None:
@@ -404,35 +415,36 @@ def _layer_fwd(x, hpre, hpost, hres, w, iters, eps, out_dtype, per_token):
     return out, M
 
 
-_F32 = torch.float32
+def layer_apply(x, hpre, hpost, hres, w, iters: int, eps: float, out_dtype):
+    """MHCLayer's forward with autograd through the torch binding, with the fewest host steps.
+
+    Layer-wide parameters with the layer's shapes; x on a GPU in fp32/bf16/fp16.  Returns None when the
+    dtype is not one the library takes or a kernel timer is active (the caller takes the general path);
+    raises ValueError for tensors on another device and RuntimeError on a library error.  n > 16 records
+    the Sinkhorn VJP state, as mhc_layer_forward does.
+    """
+    if x.dtype not in _DTYPE_CODE or not x.is_cuda or profiling._active is not None:
+        return None
+    n = int(x.shape[1])
+    return _binding().layer_apply(x, hpre, hpost, hres, w, iters, eps, _DTYPE_CODE[out_dtype], False, n > 16)
 
 
 def layer_forward_nograd(x, hpre, hpost, hres, w, iters: int, eps: float, out_dtype):
     """mhc_layer_fwd for a call that needs no gradient, with the fewest host steps (small-batch latency).
 
-    Takes only what the library can consume as is: x contiguous on a GPU in fp32/bf16/fp16, the four
-    layer-wide parameters contiguous fp32 on x's device, no kernel timer active.  Returns None when any
-    of that does not hold, and the caller takes the general path (mhc_layer_forward); raises on a
-    library error like every op here.  out_dtype: torch.float32, or x's dtype when that is 16-bit.
+    One call into the torch binding, which allocates the output and launches on the current stream.
+    Takes x on a GPU in fp32/bf16/fp16 and the four layer-wide parameters with the layer's shapes on
+    x's device ([n], [n], [n, n], [C]); returns None when that does not hold or a kernel timer is
+    active, and the caller takes the general path (mhc_layer_forward).  Raises ValueError for tensors
+    on another device and RuntimeError on a library error.  out_dtype: torch.float32, or x's dtype
+    when that is 16-bit.
     """
-    xcode = _DTYPE_CODE.get(x.dtype)
-    if xcode is None or not x.is_cuda or not x.is_contiguous() or profiling._active is not None:
+    if x.dtype not in _DTYPE_CODE or not x.is_cuda or profiling._active is not None:
         return None
-    dev = x.get_device()
-    for p in (hpre, hpost, hres, w):
-        if p.dtype is not _F32 or not p.is_contiguous() or p.get_device() != dev:
-            return None
     B, n, C = x.shape
     if hpre.numel() != n or hpost.numel() != n or hres.numel() != n * n or w.numel() != C:
         return None
-    out = torch.empty_like(x) if out_dtype is x.dtype else torch.empty((B, n, C), dtype=out_dtype, device=x.device)
-    M = torch.empty_like(hres)
-    rc = _lib.load().mhc_layer_fwd(x.data_ptr(), xcode, hpre.data_ptr(), hpost.data_ptr(), hres.data_ptr(),
-                                   w.data_ptr(), out.data_ptr(), _DTYPE_CODE[out_dtype], M.data_ptr(), B, n, C, 0,
-                                   iters, eps, _stream(x))
-    if rc:
-        _lib.check(rc, "mhc_layer_fwd")
-    return out
+    return _binding().layer_forward_nograd(x, hpre, hpost, hres, w, iters, eps, _DTYPE_CODE[out_dtype], False)
 
 
 def _layer_bwd(x, g, hpre, hpost, hres, M, w, iters, eps, per_token):
@@ -596,6 +608,10 @@ def mhc_layer_forward(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, sinkhorn_
     if not _needs_grad(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight):
         return _layer_fwd(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, int(sinkhorn_iters), float(eps),
                           out_dtype, False)[0]
+    if profiling._active is None:
+        # the same Function in C++ (backward without Python); n > 16 records the Sinkhorn state
+        return _binding().layer_apply(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, int(sinkhorn_iters),
+                                      float(eps), _DTYPE_CODE[out_dtype], False, int(x.shape[1]) > 16)
     return MHCLayerFn.apply(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, int(sinkhorn_iters),
                             float(eps), out_dtype)
 
@@ -608,6 +624,9 @@ def mhc_layer_forward_dynamic(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, s
     _fused_shapes(x, H_res_raw, H_pre_raw, H_post_raw, rms_weight)
     out_dtype = _normalize_output_dtype(output_dtype, x.dtype)
     _require_gpu(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight)
+    if profiling._active is None and _needs_grad(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight):
+        return _binding().layer_apply(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, int(sinkhorn_iters),
+                                      float(eps), _DTYPE_CODE[out_dtype], True, True)
     return MHCLayerFn.apply(x, H_pre_raw, H_post_raw, H_res_raw, rms_weight, int(sinkhorn_iters),
                             float(eps), out_dtype)
 

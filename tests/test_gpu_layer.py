@@ -13,7 +13,7 @@ import torch
 from oracle import mhc_oracle as O
 from tests._helpers import GRAD_TOL, dev_tensor, np_of, params, rel_err, rng, to_dtype_np
 
-from mhc_mlx_amd import MHCLayer, MHCRewire, _lib
+from mhc_mlx_amd import MHCLayer, MHCRewire, _lib, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -105,20 +105,39 @@ def test_env_disable_forces_reference(monkeypatch):
     assert y.shape == (1, 4, 16)
 
 
+class _BindingSpy:
+    """Stands in for the torch binding (ops._BINDING): records each call, then makes it (or raises
+    ``fail`` for the names listed in ``failing``)."""
+
+    def __init__(self, real, failing=(), fail=None):
+        self.real, self.failing, self.fail, self.calls = real, set(failing), fail, []
+
+    def __getattr__(self, name):
+        fn = getattr(self.real, name)
+
+        def call(*args):
+            self.calls.append(name)
+            if name in self.failing:
+                raise self.fail
+            return fn(*args)
+
+        return call
+
+
 def test_hip_path_is_the_one_that_runs(monkeypatch):
-    """The accelerated layer must call the library (no silent torch path)."""
-    calls = []
-    orig = _lib.call
-
-    def spy(name, *args):
-        calls.append(name)
-        return orig(name, *args)
-
-    monkeypatch.setattr(_lib, "call", spy)
+    """The accelerated layer must call the library (no silent torch path): the forward with gradients
+    goes through the torch binding's autograd Function, whose backward runs the library's VJP."""
+    spy = _BindingSpy(ops._binding())
+    monkeypatch.setattr(ops, "_BINDING", spy)
     layer = MHCLayer(n=4, C=128).cuda()
     x = torch.randn(2, 4, 128, device="cuda", requires_grad=True)
-    layer(x).sum().backward()
-    assert "mhc_layer_fwd" in calls and "mhc_layer_bwd" in calls
+    out = layer(x)
+    assert spy.calls == ["layer_apply"] and out.grad_fn is not None
+    out.sum().backward()
+    assert x.grad is not None and layer.H_res_raw.grad is not None and layer.rms_weight.grad is not None
+    with torch.no_grad():
+        layer(x)
+    assert spy.calls == ["layer_apply", "layer_forward_nograd"]
 
 
 def test_gpu_layer_reports_hip_available():
@@ -133,14 +152,9 @@ def test_library_failure_falls_back_once_on_gpu(monkeypatch):
     from mhc_mlx_amd import layer as L
 
     monkeypatch.setattr(L, "_METAL_FAILED", False)  # restored before the session guard checks it
-    orig = _lib.call
-
-    def failing(name, *args):
-        if name == "mhc_layer_fwd":
-            raise _lib.MHCError("mhc_layer_fwd: HIP error 98: injected by the test")
-        return orig(name, *args)
-
-    monkeypatch.setattr(_lib, "call", failing)
+    spy = _BindingSpy(ops._binding(), failing=("layer_apply",),
+                      fail=RuntimeError("mhc_layer_fwd failed (hip error 98): injected by the test"))
+    monkeypatch.setattr(ops, "_BINDING", spy)
     g = rng(11)
     B, n, C = 3, 4, 128
     hpre, hpost, hres, w = params(g, n, C)

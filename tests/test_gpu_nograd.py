@@ -1,10 +1,10 @@
 """GPU tests of MHCLayer's no-gradient forward (inference, torch.no_grad).
 
 A call that needs no gradient goes straight to mhc_layer_fwd with the fewest
-host steps (``MHCLayer._forward_nograd`` -> ``ops.layer_forward_nograd``).
+host steps (``MHCLayer._forward_fast`` -> ``ops.layer_forward_nograd``).
 It must give bitwise the results of the general op path and match the
-oracle (reference.py:164-184), and hand every case it does not take (views,
-fp64 parameters, a library error) to the general path unchanged.
+oracle (reference.py:164-184), and hand every case it does not take (tensors
+on another device, a library error) to the general path unchanged.
 """
 
 import numpy as np
@@ -98,7 +98,9 @@ def test_gradient_calls_skip_the_fast_path(fast_calls):
     assert layer.H_res_raw.grad is not None
 
 
-def test_cases_the_fast_path_declines_run_the_general_path(fast_calls):
+def test_views_and_other_parameter_dtypes_take_the_fast_path(fast_calls):
+    """The binding copies a non-contiguous x and converts non-fp32 parameters itself (as the general path
+    does), so those calls stay on the fast path with the same results; a shape error still raises."""
     g = rng(13)
     layer, _ = _layer(4, 256, g)
     base = torch.randn(4, 4, 512, device="cuda", dtype=torch.bfloat16)
@@ -106,10 +108,30 @@ def test_cases_the_fast_path_declines_run_the_general_path(fast_calls):
     with torch.no_grad():
         a = layer(view, return_dtype=torch.bfloat16)
         b = layer(view.contiguous(), return_dtype=torch.bfloat16)
-    assert fast_calls == [False, True]
+    assert fast_calls == [True, True]
     assert torch.equal(a, b)
+    layer64, _ = _layer(4, 256, rng(13))
+    layer64.double()
+    with torch.no_grad():
+        c = layer64(view.contiguous(), return_dtype=torch.bfloat16)
+    assert fast_calls == [True, True, True] and torch.equal(c, b)
     with torch.no_grad(), pytest.raises(ValueError):
         layer(torch.randn(4, 5, 256, device="cuda", dtype=torch.bfloat16))
+
+
+def test_the_binding_refuses_tensors_off_the_gpu():
+    """The kernels take raw device pointers: the torch binding checks that every tensor is on x's GPU
+    before any launch (ValueError), with and without autograd."""
+    b = ops._binding()
+    x = torch.randn(2, 4, 64, device="cuda")
+    p = [torch.zeros(4, device="cuda"), torch.zeros(4, device="cuda"), torch.zeros(4, 4, device="cuda"),
+         torch.ones(64)]  # rms weight on the CPU
+    with pytest.raises(ValueError, match="device"):
+        b.layer_forward_nograd(x, *p, 20, 1e-6, 0, False)
+    with pytest.raises(ValueError, match="GPU"):
+        b.layer_forward_nograd(x.cpu(), *(t.cpu() for t in p), 20, 1e-6, 0, False)
+    with pytest.raises(ValueError, match="device"):
+        b.layer_apply(x.requires_grad_(True), *p, 20, 1e-6, 0, False, False)
 
 
 def test_library_error_in_the_fast_path_goes_to_the_general_path(monkeypatch):

@@ -63,6 +63,8 @@ PAIRS = [
     ((2000, 16, 1024, "bf16", True), (37, 8, 256, "f32", True)),
     ((1000, 32, 512, "bf16", False), (5, 4, 64, "f32", False)),
     ((500, 64, 1024, "bf16", False), (7, 48, 512, "bf16", False)),
+    # config 3 (per-token n = 16 at 16384 tokens): the block-layout Sinkhorn VJP needs no workspace
+    ((16384, 16, 1024, "bf16", True), (300, 16, 512, "bf16", True)),
 ]
 
 
@@ -85,10 +87,12 @@ def test_noalloc_matches_the_workspace_entry_point(first, second):
 
 
 def test_noalloc_rejects_shapes_beyond_its_array():
-    """Per-token n = 16 at 16384 tokens needs its Sinkhorn VJP state too: more than the 64 MiB array.
-    The call is rejected on the host before anything is launched."""
-    T, n, C = 16384, 16, 1024
-    assert _lib.query("mhc_layer_bwd_workspace_bytes", T, n, C, 1, ITERS) > 64 << 20
+    """Per-token n = 16 at 16384 tokens with 300 Sinkhorn iterations: more than the block layout's
+    32 VJP checkpoints, so the VJP keeps 256 bytes of state per matrix and iteration in its workspace,
+    1.2 GB, more than the 64 MiB array.  The call is rejected on the host before anything is launched.
+    (At 20 iterations config 3 needs no Sinkhorn workspace and fits.)"""
+    T, n, C, iters = 16384, 16, 1024, 300
+    assert _lib.query("mhc_layer_bwd_workspace_bytes", T, n, C, 1, iters) > 64 << 20
     # real buffers of the call's own sizes, so nothing out of bounds could be touched even if the host
     # check were missing; the call must still be rejected before any launch
     dev = "cuda"
@@ -102,7 +106,7 @@ def test_noalloc_rejects_shapes_beyond_its_array():
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     before = dx.clone()
     rc = _lib.load().mhc_layer_bwd_noalloc(P(x), 1, P(g), 1, P(hpre), P(hpost), P(hres), P(M), P(w), P(dx),
-                                           P(dpre), P(dpost), P(dres), P(dw), T, n, C, 1, ITERS,
+                                           P(dpre), P(dpost), P(dres), P(dw), T, n, C, 1, iters,
                                            ctypes.c_float(EPS), None)
     torch.cuda.synchronize()
     assert rc == -1
