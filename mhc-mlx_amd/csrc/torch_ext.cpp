@@ -44,12 +44,20 @@ at::Tensor f32(const at::Tensor& t) {
   return t.scalar_type() == at::kFloat && t.is_contiguous() ? t : t.to(at::kFloat).contiguous();
 }
 
-// Every tensor on x's GPU (the kernels take raw device pointers).
-void check_device(const at::Tensor& x, std::initializer_list<const at::Tensor*> ps) {
+// x [T, n, C] and the parameters on x's GPU (the kernels take raw device
+// pointers) with the element counts the kernels read: [n], [n], [n, n], [C],
+// or [T, n], [T, n], [T, n, n] per token.
+void check_inputs(const at::Tensor& x, const at::Tensor& hpre, const at::Tensor& hpost, const at::Tensor& hres,
+                  const at::Tensor& w, bool per_token) {
+  TORCH_CHECK_VALUE(x.dim() == 3, "x must be [B, n, C], got ", x.sizes());
   TORCH_CHECK_VALUE(x.is_cuda(), "the HIP path needs GPU tensors (got x on ", x.device(), ")");
-  for (const at::Tensor* p : ps)
+  for (const at::Tensor* p : {&hpre, &hpost, &hres, &w})
     TORCH_CHECK_VALUE(p->device() == x.device(), "parameters must be on x's device ", x.device(), " (got ",
                       p->device(), ")");
+  const int64_t T = x.size(0), n = x.size(1), C = x.size(2), k = per_token ? T : 1;
+  TORCH_CHECK_VALUE(hpre.numel() == k * n && hpost.numel() == k * n && hres.numel() == k * n * n &&
+                        w.numel() == C,
+                    "parameter sizes do not match x ", x.sizes());
 }
 
 float* fp(const at::Tensor& t) { return t.defined() ? t.data_ptr<float>() : nullptr; }
@@ -172,7 +180,7 @@ struct LayerFn : public torch::autograd::Function<LayerFn> {
 // gradients reach the caller's tensors in their own dtype.
 at::Tensor layer_apply(const at::Tensor& x, const at::Tensor& hpre, const at::Tensor& hpost, const at::Tensor& hres,
                        const at::Tensor& w, int64_t iters, double eps, int64_t out_code, bool per_token, bool record) {
-  check_device(x, {&hpre, &hpost, &hres, &w});
+  check_inputs(x, hpre, hpost, hres, w, per_token);
   return LayerFn::apply(x.contiguous(), f32(hpre), f32(hpost), f32(hres), f32(w), iters, eps, out_code, per_token,
                         record);
 }
@@ -181,7 +189,7 @@ at::Tensor layer_apply(const at::Tensor& x, const at::Tensor& hpre, const at::Te
 at::Tensor layer_forward_nograd(const at::Tensor& x, const at::Tensor& hpre, const at::Tensor& hpost,
                                 const at::Tensor& hres, const at::Tensor& w, int64_t iters, double eps,
                                 int64_t out_code, bool per_token) {
-  check_device(x, {&hpre, &hpost, &hres, &w});
+  check_inputs(x, hpre, hpost, hres, w, per_token);
   const at::ScalarType out_dtype = out_code == MHC_DTYPE_BF16 ? at::kBFloat16
                                    : out_code == MHC_DTYPE_F16 ? at::kHalf : at::kFloat;
   return layer_fwd(x.contiguous(), f32(hpre), f32(hpost), f32(hres), f32(w), iters, eps, out_dtype, per_token,

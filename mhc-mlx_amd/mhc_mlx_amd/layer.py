@@ -51,10 +51,16 @@ _METAL_FAILED = False
 _HIP_AVAILABLE: bool | None = None
 
 _HALF = (torch.float16, torch.bfloat16)
+_MAX_N = _lib.MAX_N
+# output dtype code of the fast path when return_dtype is x's half type (the kernel writes it directly)
+_OUT_CODE = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+
+
+_ENV = os.environ
 
 
 def _disabled_by_env() -> bool:
-    return os.getenv("MHC_MLX_DISABLE_METAL", "0") == "1" or os.getenv("MHC_HIP_DISABLE", "0") == "1"
+    return _ENV.get("MHC_MLX_DISABLE_METAL") == "1" or _ENV.get("MHC_HIP_DISABLE") == "1"
 
 
 def hip_available() -> bool:
@@ -315,28 +321,31 @@ class MHCLayer(nn.Module):
         return None
 
     def _forward_fast(self, x, return_dtype):
-        """The HIP forward with the fewest host steps: one call into the torch binding, which allocates
-        the output and, when a gradient is needed, records the C++ autograd node whose backward runs the
-        library's VJP.  At small batch the layer's latency is mostly this code.  Returns None whenever the
-        general path has something to decide (a shape error, tensors off the GPU, the torch path, a kernel
-        timer, a library error), and forward() then takes that path."""
-        if not self.use_metal or self.n > _lib.MAX_N or x.ndim != 3 or x.shape[1] != self.n or x.shape[2] != self.C:
+        """The HIP forward with the fewest host steps: one call into the torch binding, which checks the
+        tensors' devices, dtypes and sizes, allocates the output and, when a gradient is needed, records
+        the C++ autograd node whose backward runs the library's VJP.  At small batch the layer's latency
+        is mostly this code.  Returns None whenever the general path has something to decide (a shape
+        error, tensors off the GPU, the torch path, a kernel timer, a library error), and forward() then
+        takes that path."""
+        n = self.n
+        shp = x.shape
+        if not self.use_metal or n > _MAX_N or len(shp) != 3 or shp[1] != n or shp[2] != self.C:
             return None
         ps = self._parameters
         hp, hq, hr, w = ps.get("H_pre_raw"), ps.get("H_post_raw"), ps.get("H_res_raw"), ps.get("rms_weight")
         if hp is None or hq is None or hr is None or w is None or profiling._active is not None or _disabled_by_env():
             return None
-        xdt = x.dtype
-        kdt = return_dtype if return_dtype is xdt and xdt in _HALF else torch.float32
+        code = _OUT_CODE.get(return_dtype, 0) if return_dtype is x.dtype else 0
+        b = ops._BINDING or ops._binding()
         try:
             if torch.is_grad_enabled() and (x.requires_grad or hp.requires_grad or hq.requires_grad
                                             or hr.requires_grad or w.requires_grad):
-                out = ops.layer_apply(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, kdt)
+                out = b.layer_apply(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, code, False, n > 16)
             else:
-                out = ops.layer_forward_nograd(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, kdt)
+                out = b.layer_forward_nograd(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, code, False)
         except (RuntimeError, ValueError):
             return None
-        if out is not None and return_dtype is not None and out.dtype != return_dtype:
+        if return_dtype is not None and out.dtype is not return_dtype:
             out = out.to(return_dtype)
         return out
 

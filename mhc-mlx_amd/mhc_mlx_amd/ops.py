@@ -425,8 +425,8 @@ def layer_apply(x, hpre, hpost, hres, w, iters: int, eps: float, out_dtype):
     """
     if x.dtype not in _DTYPE_CODE or not x.is_cuda or profiling._active is not None:
         return None
-    n = int(x.shape[1])
-    return _binding().layer_apply(x, hpre, hpost, hres, w, iters, eps, _DTYPE_CODE[out_dtype], False, n > 16)
+    return _binding().layer_apply(x, hpre, hpost, hres, w, iters, eps, _DTYPE_CODE[out_dtype], False,
+                                  x.shape[1] > 16)
 
 
 def layer_forward_nograd(x, hpre, hpost, hres, w, iters: int, eps: float, out_dtype):
@@ -440,9 +440,6 @@ def layer_forward_nograd(x, hpre, hpost, hres, w, iters: int, eps: float, out_dt
     when that is 16-bit.
     """
     if x.dtype not in _DTYPE_CODE or not x.is_cuda or profiling._active is not None:
-        return None
-    B, n, C = x.shape
-    if hpre.numel() != n or hpost.numel() != n or hres.numel() != n * n or w.numel() != C:
         return None
     return _binding().layer_forward_nograd(x, hpre, hpost, hres, w, iters, eps, _DTYPE_CODE[out_dtype], False)
 

@@ -14,7 +14,7 @@ import torch
 from oracle import mhc_oracle as O
 from tests._helpers import TOL, dev_tensor, np_of, params, rel_err, rng, to_dtype_np
 
-from mhc_mlx_amd import MHCLayer, _lib, ops
+from mhc_mlx_amd import MHCLayer, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -29,18 +29,34 @@ def _layer(n, C, g):
     return layer, (hpre, hpost, hres, w)
 
 
-@pytest.fixture
-def fast_calls(monkeypatch):
-    """Counts the fast path's calls that returned a result."""
-    calls = []
-    real = ops.layer_forward_nograd
+class _Recorder:
+    """Stands in for the torch binding (ops._BINDING): records each no-gradient forward as True (a result)
+    or False (it raised, or ``fail`` was raised in its place); everything else passes through."""
 
-    def wrapped(*a, **k):
-        out = real(*a, **k)
-        calls.append(out is not None)
+    def __init__(self, real, calls, fail=None):
+        self.real, self.calls, self.fail = real, calls, fail
+
+    def __getattr__(self, name):
+        return getattr(self.real, name)
+
+    def layer_forward_nograd(self, *args):
+        if self.fail is not None:
+            self.calls.append(False)
+            raise self.fail
+        try:
+            out = self.real.layer_forward_nograd(*args)
+        except Exception:
+            self.calls.append(False)
+            raise
+        self.calls.append(True)
         return out
 
-    monkeypatch.setattr(ops, "layer_forward_nograd", wrapped)
+
+@pytest.fixture
+def fast_calls(monkeypatch):
+    """The module's no-gradient forwards through the binding: True for each that returned a result."""
+    calls = []
+    monkeypatch.setattr(ops, "_BINDING", _Recorder(ops._binding(), calls))
     return calls
 
 
@@ -135,18 +151,18 @@ def test_the_binding_refuses_tensors_off_the_gpu():
 
 
 def test_library_error_in_the_fast_path_goes_to_the_general_path(monkeypatch):
+    """A RuntimeError from the binding's forward hands the call to the general path (ops.py through
+    ctypes), which gives bitwise the same result."""
     g = rng(14)
     layer, _ = _layer(4, 256, g)
     xt = torch.randn(4, 4, 256, device="cuda", dtype=torch.bfloat16)
-
-    def failing(*a, **k):
-        raise _lib.MHCError("mhc_layer_fwd: HIP error 2: injected")
-
+    calls = []
     with torch.no_grad():
         want = layer(xt, return_dtype=torch.bfloat16)
-        monkeypatch.setattr(ops, "layer_forward_nograd", failing)
+        monkeypatch.setattr(ops, "_BINDING", _Recorder(ops._binding(), calls,
+                                                       fail=RuntimeError("mhc_layer_fwd failed: injected")))
         got = layer(xt, return_dtype=torch.bfloat16)
-    assert torch.equal(got, want)
+    assert calls == [False] and torch.equal(got, want)
 
 
 @pytest.mark.parametrize("grad_mode", ["no_grad", "inference_mode", "frozen"])
