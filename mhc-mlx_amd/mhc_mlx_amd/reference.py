@@ -2,9 +2,12 @@
 
 This is what ``MHCLayer(use_metal=False)`` / ``MHC_MLX_DISABLE_METAL=1`` run,
 as the reference's own layer does (layer.py:122-126, 423-431).  It is plain
-autograd-capable torch code on whatever device the inputs live on; the HIP
-path never falls back to it.  Function names and semantics follow
-reference.py:20-184 one for one.
+autograd-capable torch code on whatever device the inputs live on.  MHCLayer
+and MHCRewire also run it where the reference runs its MLX path: for n > 64,
+and, with one warning per process, for a call the HIP path cannot take (CPU
+tensors, a RuntimeError from the library).  The functions in ops.py never
+fall back to it.  Function names and semantics follow reference.py:20-184 one
+for one.
 """
 
 from __future__ import annotations

@@ -160,3 +160,39 @@ def test_nograd_cpu_call_takes_the_general_path(fresh_flag):
         y = layer(x)
     assert len(rec) == 1 and L._METAL_FAILED is True
     assert rel_err(np_of(y), _ref_out(layer, x)) < 1e-5
+
+
+def test_compile_reference_compiles_the_cpu_reference_once(fresh_flag, monkeypatch):
+    """compile_reference (layer.py:133-137, 291-300): the reference path of a CPU call runs
+    torch.compile of the restatement, built on the first such call and reused; without the flag
+    the restatement runs as is.  The real compiled runner is checked against the oracle."""
+    made = []
+    real_compile = torch.compile
+
+    def counting_compile(fn, *a, **k):
+        made.append(fn)
+        return real_compile(fn, *a, **k)
+
+    monkeypatch.setattr(torch, "compile", counting_compile)
+    plain = MHCLayer(n=4, C=16, identity_init=False, use_metal=False)
+    assert plain.compile_reference is False
+    _randomise(plain, 3)
+    x = torch.randn(3, 4, 16)
+    plain(x)
+    assert made == []
+
+    layer = MHCLayer(n=4, C=16, identity_init=False, use_metal=False, compile_reference=True)
+    _randomise(layer, 3)
+    with torch.no_grad():
+        y = layer(x)
+        y2 = layer(x)
+    assert len(made) == 1 and layer._get_reference_runner(x) is layer._compiled_reference
+    assert rel_err(np_of(y), _ref_out(layer, x)) < 1e-5 and torch.equal(y, y2)
+    hp = torch.randn(3, 4)
+    hr = torch.randn(3, 4, 4)
+    with torch.no_grad():
+        yd = layer.forward_dynamic(x, hp, hp, hr)
+    assert len(made) == 1
+    ref_d = O.mhc_forward_reference(np_of(x), np_of(hp), np_of(hp), np_of(hr), np_of(layer.rms_weight),
+                                    sinkhorn_iters=layer.sinkhorn_iters, eps=layer.eps)
+    assert rel_err(np_of(yd), ref_d) < 1e-5
