@@ -9,13 +9,12 @@
 //   dM_ij = sum g_i x_j   dA_j = sum dy x_j   dP_i = sum g_i y inv w
 //   dw_c  = sum_t dyn * y * inv
 //
-// Stage 1 (fused_bwd_kernel): persistent workgroups, one token at a time.
-// Each thread owns one chunk of V channels x n streams of x and g in
-// registers; one block reduction per token yields inv and d_r; then dx is
-// written and the parameter-gradient contributions are accumulated.  Each
-// workgroup finally writes one row of partial sums (dw over its tokens and,
-// for layer-wide parameters, dM/dA/dP).  Per-token parameter gradients are
-// reduced across the workgroup per token and written directly.
+// Stage 1 (bwd_tile_kernel and the specialised kernels): persistent
+// workgroups, one token at a time.  One block reduction per token yields inv
+// and d_r; then dx is written and the parameter-gradient contributions are
+// accumulated.  Each workgroup finally writes one row of partial sums (dw over
+// its tokens and, for layer-wide parameters, dM/dA/dP).  Per-token parameter
+// gradients are reduced across the workgroup per token and written directly.
 // Stage 2 (reduce kernels): fixed-order sum of the partial rows — the
 // result is bitwise reproducible for a given device and shape.
 #include <type_traits>
@@ -53,280 +52,232 @@ struct BwdArgs {
   int reload;
   int h_mode;
   int vec;
-  int rblk;  // butterfly blocks per cross-wave staging round
   float eps;
 };
 
-constexpr int kBwdStageBudget = 48 * 1024;
 constexpr int kReduceSplit = 64;
 
+// ---------------------------------------------------------------------------
+// Tile backward: every n <= 16 shape that the specialised kernels below do
+// not take (fp32 or mixed dtypes above n = 8, n that is not 4, 8 or 16, C
+// beyond the register-resident kernels, rows without 16-byte alignment).
+//
+// 256 threads, one token at a time (grid-stride).  Per token:
+//   A. one pass over the token's chunks (V channels per thread) for the two
+//      RMS sums, sum_c y^2 and sum_c dyn y w; a block reduction gives inv and
+//      kf.  A token of one tile (C <= CT) is staged in LDS by this pass.
+//   B. per tile of CT = 256 V channels:
+//      (a) each thread takes its chunk of every stream again (from LDS for a
+//          one-tile token, else from global memory) and forms y, dyn, dy, yn,
+//          its dw term and dx; it writes x and g as fp32 rows of the tile
+//          buffers, with yn and dy as one more row of each;
+//      (b) after a barrier, the parameter sums are accumulated from LDS as
+//          one product: [g; dy] [x; yn]^T holds dM (rows and columns < n),
+//          dA (the dy row) and dP (the yn column).  Each thread owns one 4x4
+//          block of that (NMAX+1)^2 matrix and one group of the tile's
+//          4-channel steps, so it holds 16 sums.
+// The sums run in a fixed order per thread and are then added over the
+// channel groups in group order: the result is bitwise reproducible for a
+// device and shape.  No NMAX needs scratch memory.
+// ---------------------------------------------------------------------------
 template <int NMAX>
-MHC_DEV void bwd_stage_params(float* buf, const BwdArgs& A, int64_t t) {
-  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
-  const int n = A.n;
-  const float* M = A.M + t * A.M_ts;
-  const float* hp = A.hpre + t * A.h_ts;
-  const float* hq = A.hpost + t * A.h_ts;
-  for (int idx = threadIdx.x; idx < NPAR; idx += blockDim.x) {
-    float v = 0.0f;
-    if (idx < NMAX * NMAX) {
-      const int i = idx / NMAX, j = idx % NMAX;
-      if (i < n && j < n) v = M[i * n + j];
-    } else if (idx < NMAX * NMAX + NMAX) {
-      const int i = idx - NMAX * NMAX;
-      if (i < n) v = A.h_mode == MHC_H_RAW ? sigmoidf_(hp[i]) : hp[i];
-    } else {
-      const int i = idx - NMAX * NMAX - NMAX;
-      if (i < n) v = A.h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(hq[i]) : hq[i];
-    }
-    buf[idx] = v;
-  }
-}
-
-// Parameters either in uniform registers (small layer-wide n) or in LDS.
-template <int NMAX, bool LDS>
-struct ParView {
-  const float* par;
-  float Ms[LDS ? 1 : NMAX * NMAX];
-  float as[LDS ? 1 : NMAX];
-  float ps[LDS ? 1 : NMAX];
-  MHC_DEV float a(int i) const {
-    if constexpr (LDS) return par[NMAX * NMAX + i]; else return as[i];
-  }
-  MHC_DEV float p(int i) const {
-    if constexpr (LDS) return par[NMAX * NMAX + NMAX + i]; else return ps[i];
-  }
-  MHC_DEV float m(int i, int j) const {
-    if constexpr (LDS) return par[i * NMAX + j]; else return Ms[i * NMAX + j];
-  }
+struct TileCfg {
+  static constexpr int V = NMAX == 16 ? 2 : 4;  // channels per thread and chunk
+  static constexpr int CT = 256 * V;            // channels per tile
+  static constexpr int RS = CT + 4;             // LDS row stride in floats: rows start 4 banks apart
+  static constexpr int ROWS = NMAX + 1;         // the streams, then yn (x buffer) or dy (g buffer)
+  static constexpr int NB = NMAX / 4 + 1;       // 4x4 blocks per side of the (NMAX+1)^2 sums
+  static constexpr int G = 256 / (NB * NB);     // channel groups per block
+  static constexpr int RED = 17;                // LDS stride of one thread's 16 sums in the final reduction
+  static_assert(256 * RED <= ROWS * RS, "reduction scratch must fit in one tile buffer");
 };
+constexpr int kTileThreads = 256;
 
-// Flattened per-token parameter-gradient index k (NMAX-padded):
-//   [0, NMAX^2)            dM[k / NMAX][k % NMAX]
-//   [NMAX^2, NMAX^2+NMAX)  dA[k - NMAX^2]
-//   [NMAX^2+NMAX, KP)      dP[k - NMAX^2 - NMAX]
-template <int NMAX, typename XT, typename GT, typename DT, bool PAR_LDS, bool REG_ACC, int NBLK>
-MHC_DEV void bwd_chunk_phase_b(const ParView<NMAX, PAR_LDS>& pv, const Vec<XT, BwdCfg<NMAX>::V> (&xr)[NMAX],
-                               const Vec<GT, BwdCfg<NMAX>::V> (&gr)[NMAX],
-                               const float (&y)[BwdCfg<NMAX>::V], const float (&dyn)[BwdCfg<NMAX>::V],
-                               const float (&wv)[BwdCfg<NMAX>::V], float (&dwv)[BwdCfg<NMAX>::V],
-                               float inv, float kf, int n, DT* dxt, int C, int c0, int valid, bool vec,
-                               float (&accM)[REG_ACC ? NMAX * NMAX : 1], float (&accA)[REG_ACC ? NMAX : 1],
-                               float (&accP)[REG_ACC ? NMAX : 1], float (&accL)[NBLK], int lane) {
-  constexpr int V = BwdCfg<NMAX>::V;
-  constexpr int KP = NMAX * NMAX + 2 * NMAX;
-  float dy[V], yn[V];
-#pragma unroll
-  for (int v = 0; v < V; ++v) {
-    const float yi = y[v] * inv;
-    dy[v] = dyn[v] * inv * wv[v] - kf * y[v];
-    yn[v] = yi * wv[v];
-    dwv[v] = fmaf(dyn[v], yi, dwv[v]);
-  }
-  // dx_j = sum_i M_ij g_i + a_j dy
-#pragma unroll
-  for (int j = 0; j < NMAX; ++j) {
-    if (j < n) {
-      float o[V];
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NMAX; ++i) acc = fmaf(pv.m(i, j), gr[i].get(v), acc);
-        o[v] = fmaf(pv.a(j), dy[v], acc);
-      }
-      DT* dst = dxt + (int64_t)j * C + c0;
-      if (vec && valid == V) store_vec<DT, V>(dst, o);
-      else store_partial<DT, V>(dst, o, valid);
-    }
-  }
-  if constexpr (REG_ACC) {
-#pragma unroll
-    for (int v = 0; v < V; ++v) {
-      float xv[NMAX], gv[NMAX];
-#pragma unroll
-      for (int i = 0; i < NMAX; ++i) {
-        xv[i] = xr[i].get(v);
-        gv[i] = gr[i].get(v);
-      }
-#pragma unroll
-      for (int i = 0; i < NMAX; ++i) {
-#pragma unroll
-        for (int j = 0; j < NMAX; ++j) accM[i * NMAX + j] = fmaf(gv[i], xv[j], accM[i * NMAX + j]);
-        accA[i] = fmaf(dy[v], xv[i], accA[i]);
-        accP[i] = fmaf(gv[i], yn[v], accP[i]);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int b = 0; b < NBLK; ++b) {
-      float pvv[64];
-#pragma unroll
-      for (int kk = 0; kk < 64; ++kk) {
-        const int k = 64 * b + kk;
-        float s = 0.0f;
-        if (k < NMAX * NMAX) {
-          const int i = k / NMAX, j = k % NMAX;
-#pragma unroll
-          for (int v = 0; v < V; ++v) s = fmaf(gr[i].get(v), xr[j].get(v), s);
-        } else if (k < NMAX * NMAX + NMAX) {
-          const int j = k - NMAX * NMAX;
-#pragma unroll
-          for (int v = 0; v < V; ++v) s = fmaf(dy[v], xr[j].get(v), s);
-        } else if (k < KP) {
-          const int i = k - NMAX * NMAX - NMAX;
-#pragma unroll
-          for (int v = 0; v < V; ++v) s = fmaf(gr[i].get(v), yn[v], s);
-        }
-        pvv[kk] = s;
-      }
-      wave_reduce_scatter<1>(pvv, lane);
-      accL[b] += pvv[0];
-    }
-  }
-}
-
-template <int NMAX, typename XT, typename GT, typename DT, bool PT>
-__global__ __launch_bounds__(1024) void fused_bwd_kernel(BwdArgs A) {
-  constexpr int V = BwdCfg<NMAX>::V;
-  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
-  constexpr bool PAR_LDS = PT || NMAX > 8;
-  constexpr bool REG_ACC = !PT && NMAX <= 8;
-  constexpr int KP = NMAX * NMAX + 2 * NMAX;
-  constexpr int NBLK = (KP + 63) / 64;
-  extern __shared__ float bwd_smem[];
-  __shared__ float s_red[2][2][16];
+template <int NMAX, typename XT, typename GT, bool PT>
+__global__ __launch_bounds__(kTileThreads) void bwd_tile_kernel(BwdArgs A) {
+  using Cfg = TileCfg<NMAX>;
+  constexpr int V = Cfg::V, CT = Cfg::CT, RS = Cfg::RS, ROWS = Cfg::ROWS, NB = Cfg::NB, G = Cfg::G;
+  constexpr int RED = Cfg::RED;
+  __shared__ __attribute__((aligned(16))) float s_x[ROWS * RS];  // x_j rows, then yn
+  __shared__ __attribute__((aligned(16))) float s_g[ROWS * RS];  // g_i rows, then dy
+  __shared__ float s_Mt[NMAX * NMAX];                               // s_Mt[j * NMAX + i] = M_ij
+  __shared__ float s_a[NMAX], s_p[NMAX];
+  __shared__ float s_sum[2][kTileThreads / 64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int nwaves = blockDim.x >> 6;
   const int n = A.n;
   const int C = A.C;
   const int64_t nC = (int64_t)n * C;
+  const int nchunks = A.nchunks;
+  const int ntiles = (C + CT - 1) / CT;
+  const bool resident = ntiles == 1;
+  const bool vec = A.vec != 0;
   const XT* __restrict__ X = (const XT*)A.x;
   const GT* __restrict__ Gr = (const GT*)A.g;
-  DT* __restrict__ DX = (DT*)A.dx;
+  XT* __restrict__ DX = (XT*)A.dx;
   const float* __restrict__ Wt = A.w;
-  float* s_par = bwd_smem;
-  float* s_stage = bwd_smem + (PAR_LDS ? (PT ? 3 : 1) * NPAR : 0);
   float* prow = A.part + (int64_t)blockIdx.x * A.P;
-  const int R = A.rblk;
 
-  ParView<NMAX, PAR_LDS> pv;
-  pv.par = s_par;
-  if constexpr (!PAR_LDS) {
+  // parameter-sum block (bi, bj) and channel group of this thread
+  const int blk = tid / G;
+  const int grp = tid - blk * G;
+  const bool owner = blk < NB * NB;
+  const int bi = owner ? blk / NB : 0;
+  const int bj = owner ? blk - bi * NB : 0;
+  float acc[16];
 #pragma unroll
-    for (int i = 0; i < NMAX; ++i) {
-      float av = 0.0f, pq = 0.0f;
-      if (i < n) {
-        av = A.hpre[i];
-        pq = A.hpost[i];
-        if (A.h_mode == MHC_H_RAW) {
-          av = sigmoidf_(av);
-          pq = 2.0f * sigmoidf_(pq);
-        }
+  for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
+  float dwr[V];  // dw of this thread's channels, one-tile tokens
+#pragma unroll
+  for (int v = 0; v < V; ++v) dwr[v] = 0.0f;
+
+  // rows n..NMAX-1 are never written and must read as zero
+  for (int k = tid; k < ROWS * RS; k += kTileThreads) {
+    s_x[k] = 0.0f;
+    s_g[k] = 0.0f;
+  }
+  if (!resident)
+    for (int c = tid; c < C; c += kTileThreads) prow[c] = 0.0f;
+
+  auto stage_params = [&](int64_t t) {
+    const float* Mp = A.M + t * A.M_ts;
+    const float* hp = A.hpre + t * A.h_ts;
+    const float* hq = A.hpost + t * A.h_ts;
+    for (int idx = tid; idx < NMAX * NMAX + 2 * NMAX; idx += kTileThreads) {
+      if (idx < NMAX * NMAX) {
+        const int j = idx / NMAX, i = idx - j * NMAX;
+        s_Mt[idx] = (i < n && j < n) ? Mp[i * n + j] : 0.0f;
+      } else if (idx < NMAX * NMAX + NMAX) {
+        const int i = idx - NMAX * NMAX;
+        float v = 0.0f;
+        if (i < n) v = A.h_mode == MHC_H_RAW ? sigmoidf_(hp[i]) : hp[i];
+        s_a[i] = v;
+      } else {
+        const int i = idx - NMAX * NMAX - NMAX;
+        float v = 0.0f;
+        if (i < n) v = A.h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(hq[i]) : hq[i];
+        s_p[i] = v;
       }
-      pv.as[i] = uniform_f(av);
-      pv.ps[i] = uniform_f(pq);
-#pragma unroll
-      for (int j = 0; j < NMAX; ++j) pv.Ms[i * NMAX + j] = (i < n && j < n) ? A.M[i * n + j] : 0.0f;
     }
-  } else {
-    if (PT) {
-      if ((int64_t)blockIdx.x < A.T) bwd_stage_params<NMAX>(s_par, A, blockIdx.x);
-    } else {
-      bwd_stage_params<NMAX>(s_par, A, 0);
-    }
-  }
+  };
 
-  // owned chunk (register path) and dw accumulators
-  const int q0 = tid;
-  const int c00 = q0 * V;
-  const bool act0 = !A.reload && q0 < A.nchunks;
-  const int valid0 = act0 ? min(V, C - c00) : 0;
-  float wv[V], dwv[V];
+  // the 16 sums of every thread added over the channel groups; emit(R, S, value) for each (R, S)
+  // of the (NMAX+1)^2 matrix.  Uses s_x as scratch and leaves it zero; brackets itself with barriers.
+  auto reduce_sums = [&](auto&& emit) {
+    __syncthreads();
 #pragma unroll
-  for (int v = 0; v < V; ++v) {
-    wv[v] = (act0 && c00 + v < C) ? Wt[c00 + v] : 0.0f;
-    dwv[v] = 0.0f;
-  }
-  if (A.reload) {
-    for (int c = tid; c < A.Cp; c += blockDim.x) prow[c] = 0.0f;
-  }
-  float accM[REG_ACC ? NMAX * NMAX : 1], accA[REG_ACC ? NMAX : 1], accP[REG_ACC ? NMAX : 1];
-  float accL[NBLK];
+    for (int k = 0; k < 16; ++k) {
+      s_x[tid * RED + k] = acc[k];
+      acc[k] = 0.0f;
+    }
+    __syncthreads();
+    for (int o = tid; o < NB * NB * 16; o += kTileThreads) {
+      const int b = o >> 4, k = o & 15;
+      float s = 0.0f;
+      for (int q = 0; q < G; ++q) s += s_x[(b * G + q) * RED + k];
+      const int bb = b / NB;
+      emit(4 * bb + (k >> 2), 4 * (b - bb * NB) + (k & 3), s);
+    }
+    __syncthreads();
 #pragma unroll
-  for (int k = 0; k < (REG_ACC ? NMAX * NMAX : 1); ++k) accM[k] = 0.0f;
-#pragma unroll
-  for (int k = 0; k < (REG_ACC ? NMAX : 1); ++k) {
-    accA[k] = 0.0f;
-    accP[k] = 0.0f;
-  }
-#pragma unroll
-  for (int b = 0; b < NBLK; ++b) accL[b] = 0.0f;
+    for (int k = 0; k < 16; ++k) s_x[tid * RED + k] = 0.0f;
+    __syncthreads();
+  };
+
+  if (!PT) stage_params(0);
   __syncthreads();
 
-  int it = 0;
-  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x) {
     if constexpr (PT) {
-      pv.par = s_par + (it % 3) * NPAR;
-      const int64_t tn = t + gridDim.x;
-      if (tn < A.T) bwd_stage_params<NMAX>(s_par + ((it + 1) % 3) * NPAR, A, tn);
-#pragma unroll
-      for (int b = 0; b < NBLK; ++b) accL[b] = 0.0f;
+      stage_params(t);
+      __syncthreads();
     }
     const XT* xt = X + t * nC;
     const GT* gt = Gr + t * nC;
-    DT* dxt = DX + t * nC;
+    XT* dxt = DX + t * nC;
 
-    // ---- phase A: y, dyn and the two per-token reductions
+    // ---- A: the RMS sums (cached loads: a token of several tiles is read again in B)
     float ss = 0.0f, sr = 0.0f;
-    Vec<XT, V> xr[NMAX];
-    Vec<GT, V> gr[NMAX];
-    float y[V], dyn[V];
-    if (!A.reload) {
+    for (int q = tid; q < nchunks; q += kTileThreads) {
+      const int c0 = q * V;
+      const int valid = min(V, C - c0);
+      float y[V], dyn[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) y[v] = dyn[v] = 0.0f;
 #pragma unroll
       for (int i = 0; i < NMAX; ++i) {
-        if (act0 && i < n) {
-          if (A.vec && valid0 == V) {
-            xr[i].load(xt + (int64_t)i * C + c00);
-            gr[i].load(gt + (int64_t)i * C + c00);
+        if (i < n) {
+          Vec<XT, V> xv;
+          Vec<GT, V> gv;
+          if (vec && valid == V) {
+            xv.template load<false>(xt + (int64_t)i * C + c0);
+            gv.template load<false>(gt + (int64_t)i * C + c0);
           } else {
-            xr[i].load_partial(xt + (int64_t)i * C + c00, valid0);
-            gr[i].load_partial(gt + (int64_t)i * C + c00, valid0);
+            xv.load_partial(xt + (int64_t)i * C + c0, valid);
+            gv.load_partial(gt + (int64_t)i * C + c0, valid);
           }
-        } else {
-          xr[i].zero();
-          gr[i].zero();
+          const float ai = s_a[i], pi = s_p[i];
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const float xf = xv.get(v), gf = gv.get(v);
+            y[v] = fmaf(ai, xf, y[v]);
+            dyn[v] = fmaf(pi, gf, dyn[v]);
+            if (resident) {
+              s_x[i * RS + c0 + v] = xf;
+              s_g[i * RS + c0 + v] = gf;
+            }
+          }
         }
       }
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        float ya = 0.0f, da = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NMAX; ++i) {
-          ya = fmaf(pv.a(i), xr[i].get(v), ya);
-          da = fmaf(pv.p(i), gr[i].get(v), da);
-        }
-        y[v] = ya;
-        dyn[v] = da;
-        ss = fmaf(ya, ya, ss);
-        sr = fmaf(da * ya, wv[v], sr);
+        const float wv = v < valid ? Wt[c0 + v] : 0.0f;
+        ss = fmaf(y[v], y[v], ss);
+        sr = fmaf(dyn[v] * y[v], wv, sr);
       }
-    } else {
-      for (int q = tid; q < A.nchunks; q += blockDim.x) {
-        const int c0 = q * V;
-        const int valid = min(V, C - c0);
-        float ya[V], da[V];
+    }
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_sum[0][wave] = ss;
+      s_sum[1][wave] = sr;
+    }
+    __syncthreads();
+    float tss = 0.0f, tsr = 0.0f;
 #pragma unroll
-        for (int v = 0; v < V; ++v) ya[v] = da[v] = 0.0f;
+    for (int w = 0; w < kTileThreads / 64; ++w) {
+      tss += s_sum[0][w];
+      tsr += s_sum[1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+
+    // ---- B: per tile, (a) dx, dw and the tile rows, (b) the parameter sums
+    for (int tl = 0; tl < ntiles; ++tl) {
+      const int cl = tid * V;
+      const int c0 = tl * CT + cl;
+      const int valid = max(0, min(V, C - c0));
+      float y[V], dyn[V], gr[NMAX][V];
 #pragma unroll
-        for (int i = 0; i < NMAX; ++i) {
-          if (i < n) {
+      for (int v = 0; v < V; ++v) y[v] = dyn[v] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        float xf[V], gf[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) xf[v] = gf[v] = 0.0f;
+        if (i < n && valid > 0) {
+          if (resident) {
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              xf[v] = s_x[i * RS + cl + v];
+              gf[v] = s_g[i * RS + cl + v];
+            }
+          } else {
             Vec<XT, V> xv;
             Vec<GT, V> gv;
-            if (A.vec && valid == V) {
+            if (vec && valid == V) {
               xv.load(xt + (int64_t)i * C + c0);
               gv.load(gt + (int64_t)i * C + c0);
             } else {
@@ -335,173 +286,114 @@ __global__ __launch_bounds__(1024) void fused_bwd_kernel(BwdArgs A) {
             }
 #pragma unroll
             for (int v = 0; v < V; ++v) {
-              ya[v] = fmaf(pv.a(i), xv.get(v), ya[v]);
-              da[v] = fmaf(pv.p(i), gv.get(v), da[v]);
+              xf[v] = xv.get(v);
+              gf[v] = gv.get(v);
             }
           }
         }
+        const float ai = s_a[i], pi = s_p[i];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-          const float wc = c0 + v < C ? Wt[c0 + v] : 0.0f;
-          ss = fmaf(ya[v], ya[v], ss);
-          sr = fmaf(da[v] * ya[v], wc, sr);
+          y[v] = fmaf(ai, xf[v], y[v]);
+          dyn[v] = fmaf(pi, gf[v], dyn[v]);
+          gr[i][v] = gf[v];
+        }
+        if (!resident && i < n) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            s_x[i * RS + cl + v] = xf[v];
+            s_g[i * RS + cl + v] = gf[v];
+          }
         }
       }
-    }
-    ss = wave_sum(ss);
-    sr = wave_sum(sr);
-    if (lane == 0) {
-      s_red[it & 1][0][wave] = ss;
-      s_red[it & 1][1][wave] = sr;
-    }
-    __syncthreads();
-    float tss = 0.0f, tsr = 0.0f;
-    for (int w = 0; w < nwaves; ++w) {
-      tss += s_red[it & 1][0][w];
-      tsr += s_red[it & 1][1][w];
-    }
-    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
-    const float kf = (inv * inv * inv / (float)C) * tsr;
-
-    // ---- phase B: dx, dw, parameter-gradient contributions
-    if (!A.reload) {
-      if (act0 || !REG_ACC) {
-        bwd_chunk_phase_b<NMAX, XT, GT, DT, PAR_LDS, REG_ACC, NBLK>(
-            pv, xr, gr, y, dyn, wv, dwv, inv, kf, act0 ? n : 0, dxt, C, c00, valid0, A.vec != 0,
-            accM, accA, accP, accL, lane);
-      }
-    } else {
-      // all lanes of a wave iterate together so the butterflies stay converged
-      const int nq = (int)ceil_div(A.nchunks, blockDim.x) * blockDim.x;
-      for (int q = tid; q < nq; q += blockDim.x) {
-        const bool act = q < A.nchunks;
-        const int c0 = q * V;
-        const int valid = act ? min(V, C - c0) : 0;
-        Vec<XT, V> xq[NMAX];
-        Vec<GT, V> gq[NMAX];
-        float yq[V], dq[V], wq[V], dwq[V];
+      float dy[V];
 #pragma unroll
-        for (int i = 0; i < NMAX; ++i) {
-          if (act && i < n) {
-            if (A.vec && valid == V) {
-              xq[i].load(xt + (int64_t)i * C + c0);
-              gq[i].load(gt + (int64_t)i * C + c0);
-            } else {
-              xq[i].load_partial(xt + (int64_t)i * C + c0, valid);
-              gq[i].load_partial(gt + (int64_t)i * C + c0, valid);
+      for (int v = 0; v < V; ++v) {
+        const float wv = v < valid ? Wt[c0 + v] : 0.0f;
+        const float yi = y[v] * inv;
+        dy[v] = dyn[v] * inv * wv - kf * y[v];
+        s_x[NMAX * RS + cl + v] = yi * wv;
+        s_g[NMAX * RS + cl + v] = dy[v];
+        const float dwt = dyn[v] * yi;
+        if (resident) dwr[v] += dwt;
+        else if (v < valid) prow[c0 + v] += dwt;
+      }
+      if (valid > 0) {
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+          if (j < n) {
+            float o[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              float s = 0.0f;
+#pragma unroll
+              for (int i = 0; i < NMAX; ++i) s = fmaf(s_Mt[j * NMAX + i], gr[i][v], s);
+              o[v] = fmaf(s_a[j], dy[v], s);
             }
-          } else {
-            xq[i].zero();
-            gq[i].zero();
+            XT* dst = dxt + (int64_t)j * C + c0;
+            if (vec && valid == V) store_vec<XT, V>(dst, o);
+            else store_partial<XT, V>(dst, o, valid);
           }
-        }
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          float ya = 0.0f, da = 0.0f;
-#pragma unroll
-          for (int i = 0; i < NMAX; ++i) {
-            ya = fmaf(pv.a(i), xq[i].get(v), ya);
-            da = fmaf(pv.p(i), gq[i].get(v), da);
-          }
-          yq[v] = ya;
-          dq[v] = da;
-          wq[v] = (act && c0 + v < C) ? Wt[c0 + v] : 0.0f;
-          dwq[v] = 0.0f;
-        }
-        bwd_chunk_phase_b<NMAX, XT, GT, DT, PAR_LDS, REG_ACC, NBLK>(
-            pv, xq, gq, yq, dq, wq, dwq, inv, kf, act ? n : 0, dxt, C, c0, valid, A.vec != 0, accM,
-            accA, accP, accL, lane);
-        if (act) {
-#pragma unroll
-          for (int v = 0; v < V; ++v)
-            if (v < valid) prow[c0 + v] += dwq[v];
         }
       }
+      __syncthreads();
+      if (owner) {
+        const int qend = (min(CT, C - tl * CT) + 3) >> 2;
+        for (int q = grp; q < qend; q += G) {
+          float4 gq[4], xq[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int R = 4 * bi + r;
+            gq[r] = R < ROWS ? *reinterpret_cast<const float4*>(&s_g[R * RS + 4 * q]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const int S = 4 * bj + r;
+            xq[r] = S < ROWS ? *reinterpret_cast<const float4*>(&s_x[S * RS + 4 * q]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              float a = acc[4 * r + s];
+              a = fmaf(gq[r].x, xq[s].x, a);
+              a = fmaf(gq[r].y, xq[s].y, a);
+              a = fmaf(gq[r].z, xq[s].z, a);
+              a = fmaf(gq[r].w, xq[s].w, a);
+              acc[4 * r + s] = a;
+            }
+        }
+      }
+      __syncthreads();
     }
 
-    // ---- per-token parameter gradients: cross-wave sum and write
     if constexpr (PT) {
-      const float* par = pv.par;
-      for (int b0 = 0; b0 < NBLK; b0 += R) {
-#pragma unroll
-        for (int b = 0; b < NBLK; ++b)
-          if (b >= b0 && b < b0 + R) s_stage[((wave * R) + (b - b0)) * 64 + lane] = accL[b];
-        __syncthreads();
-        const int cnt = min(R, NBLK - b0) * 64;
-        for (int idx = tid; idx < cnt; idx += blockDim.x) {
-          float s = 0.0f;
-          for (int w = 0; w < nwaves; ++w) s += s_stage[((w * R) + (idx >> 6)) * 64 + (idx & 63)];
-          const int k = b0 * 64 + idx;
-          if (k < NMAX * NMAX) {
-            const int i = k / NMAX, j = k % NMAX;
-            if (i < n && j < n) A.dM_tok[t * n * n + i * n + j] = s;
-          } else if (k < NMAX * NMAX + NMAX) {
-            const int j = k - NMAX * NMAX;
-            if (j < n) {
-              const float av = par[NMAX * NMAX + j];
-              A.dpre_tok[t * n + j] = A.h_mode == MHC_H_RAW ? s * av * (1.0f - av) : s;
-            }
-          } else if (k < KP) {
-            const int i = k - NMAX * NMAX - NMAX;
-            if (i < n) {
-              const float pq = par[NMAX * NMAX + NMAX + i];
-              A.dpost_tok[t * n + i] = A.h_mode == MHC_H_RAW ? s * pq * (1.0f - 0.5f * pq) : s;
-            }
-          }
+      reduce_sums([&](int R, int S, float s) {
+        if (R < n && S < n) {
+          A.dM_tok[t * n * n + R * n + S] = s;
+        } else if (R == NMAX && S < n) {
+          const float av = s_a[S];
+          A.dpre_tok[t * n + S] = A.h_mode == MHC_H_RAW ? s * av * (1.0f - av) : s;
+        } else if (R < n && S == NMAX) {
+          const float pq = s_p[R];
+          A.dpost_tok[t * n + R] = A.h_mode == MHC_H_RAW ? s * pq * (1.0f - 0.5f * pq) : s;
         }
-        if (b0 + R < NBLK) __syncthreads();
-      }
+      });
     }
   }
 
-  // ---- this workgroup's partial row
-  if (!A.reload && act0) {
+  // ---- this workgroup's partial row: dw, then (layer-wide) dM, dA, dP
+  if (resident) {
+    const int c0 = tid * V;
 #pragma unroll
     for (int v = 0; v < V; ++v)
-      if (v < valid0) prow[c00 + v] = dwv[v];
+      if (c0 + v < C) prow[c0 + v] = dwr[v];
   }
   if (tid == 0)
     for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
   if constexpr (!PT) {
-    if constexpr (REG_ACC) {
-#pragma unroll
-      for (int b = 0; b < NBLK; ++b) {
-        float pvv[64];
-#pragma unroll
-        for (int kk = 0; kk < 64; ++kk) {
-          const int k = 64 * b + kk;
-          pvv[kk] = k < NMAX * NMAX ? accM[k < NMAX * NMAX ? k : 0]
-                  : k < NMAX * NMAX + NMAX ? accA[(k - NMAX * NMAX) % NMAX]
-                  : k < KP ? accP[(k - NMAX * NMAX - NMAX) % NMAX] : 0.0f;
-        }
-        wave_reduce_scatter<1>(pvv, lane);
-        accL[b] = pvv[0];
-      }
-    }
-    __syncthreads();
-    for (int b0 = 0; b0 < NBLK; b0 += R) {
-#pragma unroll
-      for (int b = 0; b < NBLK; ++b)
-        if (b >= b0 && b < b0 + R) s_stage[((wave * R) + (b - b0)) * 64 + lane] = accL[b];
-      __syncthreads();
-      const int cnt = min(R, NBLK - b0) * 64;
-      for (int idx = tid; idx < cnt; idx += blockDim.x) {
-        float s = 0.0f;
-        for (int w = 0; w < nwaves; ++w) s += s_stage[((w * R) + (idx >> 6)) * 64 + (idx & 63)];
-        const int k = b0 * 64 + idx;
-        if (k < NMAX * NMAX) {
-          const int i = k / NMAX, j = k % NMAX;
-          if (i < n && j < n) prow[A.Cp + i * n + j] = s;
-        } else if (k < NMAX * NMAX + NMAX) {
-          const int j = k - NMAX * NMAX;
-          if (j < n) prow[A.Cp + n * n + j] = s;
-        } else if (k < KP) {
-          const int i = k - NMAX * NMAX - NMAX;
-          if (i < n) prow[A.Cp + n * n + n + i] = s;
-        }
-      }
-      __syncthreads();
-    }
+    reduce_sums([&](int R, int S, float s) {
+      if (R < n && S < n) prow[A.Cp + R * n + S] = s;
+      else if (R == NMAX && S < n) prow[A.Cp + n * n + S] = s;
+      else if (R < n && S == NMAX) prow[A.Cp + n * n + n + R] = s;
+    });
     if (tid == 0)
       for (int c = A.Cp + n * n + 2 * n; c < A.P; ++c) prow[c] = 0.0f;
   }
@@ -574,8 +466,8 @@ MHC_DEV void reg_fence(uint32_t& w) { asm volatile("" : "+v"(w)); }
 // CU, which the overlap more than pays for (config 2: 565 -> 559 us at one
 // workgroup per CU against two).
 template <int NMAX, typename XT, typename GT, int CHK, bool FULL, bool PT = false, bool PIPE = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(64, PIPE ? 512 : lw_max_threads(NMAX)),
-                          amdgpu_waves_per_eu(PIPE ? 3 : (NMAX <= 4 ? MHC_BWD_WPE : 2))))
+__global__ __attribute__((amdgpu_flat_work_group_size(64, (PIPE || !FULL) ? 512 : lw_max_threads(NMAX)),
+                          amdgpu_waves_per_eu(PIPE ? 3 : (NMAX <= 4 && FULL ? MHC_BWD_WPE : 2))))
 void fused_bwd_lw_kernel(BwdArgs A) {
   static_assert(!PIPE || (FULL && !PT), "pipelined loads for layer-wide full tiles only");
   constexpr int V = lw_vec<NMAX, XT, GT>();
@@ -1604,6 +1496,10 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
   const int tpb = std::max(64, round_up(A.nchunks, 64));
   if (tpb > lw_max_threads(NMAX)) return 1;
   const bool full = A.n == NMAX && A.vec && A.C % V == 0 && A.nchunks == tpb;
+  // Partial tiles (n below NMAX, a partial last chunk or workgroup) run here only at n <= 4 with
+  // vector-aligned rows, on at most 512 threads (the variant's 256-VGPR bound); the others take the
+  // tile kernel, whose narrower chunks need less alignment.
+  if (!full && (NMAX > 4 || !A.vec || tpb > 512)) return 1;
   // Grid: the workspace's full row budget (8 workgroups per CU) streams
   // faster than one resident wave of workgroups (562 vs 576 us at config 2);
   // MHC_BWD_GRID overrides the count.
@@ -1626,10 +1522,11 @@ int launch_bwd_lw(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStrea
       return MHC_OK;
     }
   }
-  if (full)
+  if (full) {
     hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, true, PT>), g, b, 0, stream, A);
-  else
+  } else if constexpr (NMAX <= 4) {
     hipLaunchKernelGGL((fused_bwd_lw_kernel<NMAX, XT, GT, 1, false, PT>), g, b, 0, stream, A);
+  }
   MHC_CHECK_LAUNCH("fused_bwd_lw_kernel");
   *num_partials = blocks;
   return MHC_OK;
@@ -1716,6 +1613,28 @@ int launch_bwd_pt16(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStr
   return MHC_OK;
 }
 
+// Tile backward (bwd_tile_kernel): every shape the kernels above do not take.
+template <int NMAX, typename XT, typename GT, bool PT>
+int launch_bwd_tile(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
+  constexpr int V = TileCfg<NMAX>::V;
+  A.nchunks = (int)ceil_div(A.C, V);
+  const int ax = std::min(16, V * ElemTraits<XT>::kBytes), ag = std::min(16, V * ElemTraits<GT>::kBytes);
+  A.vec = A.C % V == 0 && aligned(A.x, ax) && aligned(A.dx, ax) && aligned(A.g, ag) ? 1 : 0;
+  const void* kfn = (const void*)bwd_tile_kernel<NMAX, XT, GT, PT>;
+  const int occ = occupancy_blocks(kfn, kTileThreads, 0);
+  if (occ <= 0)
+    return set_error(MHC_ERR_INVALID_ARG, "fused_bwd: no occupancy for the tile kernel (n=%d C=%d)", A.n, A.C);
+  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
+  const int grid_pref = knob(kKnobBwdGrid, 0);
+  if (grid_pref > 0) blocks = std::min<int64_t>(L.gmax, grid_pref);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+  set_rows(A, L);
+  hipLaunchKernelGGL((bwd_tile_kernel<NMAX, XT, GT, PT>), dim3((unsigned)blocks), dim3(kTileThreads), 0, stream, A);
+  MHC_CHECK_LAUNCH("bwd_tile_kernel");
+  *num_partials = blocks;
+  return MHC_OK;
+}
+
 template <int NMAX, typename XT, typename GT, bool PT>
 int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t stream) {
   if constexpr (!PT && NMAX == 16 && std::is_same<XT, GT>::value && ElemTraits<XT>::kBytes == 2) {
@@ -1735,34 +1654,7 @@ int launch_bwd(BwdArgs A, const BwdLayout& L, int64_t* num_partials, hipStream_t
       if (rc != 1) return rc;
     }
   }
-  constexpr int V = BwdCfg<NMAX>::V;
-  constexpr int NPAR = NMAX * NMAX + 2 * NMAX;
-  constexpr int KP = NMAX * NMAX + 2 * NMAX;
-  constexpr int NBLK = (KP + 63) / 64;
-  A.nchunks = (int)ceil_div(A.C, V);
-  const int tpb_pref = knob(kKnobBwdTpb, 0);
-  const ThreadPlan tp = plan_threads(A.nchunks, 1, tpb_pref);
-  A.reload = tp.reload;
-  const int nwaves = tp.tpb / 64;
-  const bool par_lds = PT || NMAX > 8;
-  const size_t par_bytes = par_lds ? (size_t)(PT ? 3 : 1) * NPAR * sizeof(float) : 0;
-  int rblk = (int)((kBwdStageBudget - (int)par_bytes) / (nwaves * 64 * (int)sizeof(float)));
-  rblk = std::max(1, std::min(rblk, NBLK));
-  A.rblk = rblk;
-  const size_t smem = par_bytes + (size_t)nwaves * rblk * 64 * sizeof(float);
-  const void* kfn = (const void*)fused_bwd_kernel<NMAX, XT, GT, XT, PT>;
-  const int occ = occupancy_blocks(kfn, tp.tpb, smem);
-  if (occ <= 0)
-    return set_error(MHC_ERR_INVALID_ARG, "fused_bwd: no occupancy for %d threads (n=%d C=%d)",
-                     tp.tpb, A.n, A.C);
-  int64_t blocks = std::min<int64_t>(L.gmax, (int64_t)device_cu_count() * occ);
-  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
-  set_rows(A, L);
-  hipLaunchKernelGGL((fused_bwd_kernel<NMAX, XT, GT, XT, PT>), dim3((unsigned)blocks), dim3(tp.tpb),
-                     smem, stream, A);
-  MHC_CHECK_LAUNCH("fused_bwd_kernel");
-  *num_partials = blocks;
-  return MHC_OK;
+  return launch_bwd_tile<NMAX, XT, GT, PT>(A, L, num_partials, stream);
 }
 
 template <typename XT, typename GT, bool PT>

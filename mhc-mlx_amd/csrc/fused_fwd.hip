@@ -125,8 +125,10 @@ __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
     __syncthreads();
   }
 
-  // rms weight of the owned chunks (register-resident path)
-  float wv[CH][V];
+  // rms weight of the owned chunks (register-resident path), in this thread's LDS slots
+  // (s_w[(j * V + v) * blockDim.x + tid]): held in registers across the token loop they were what
+  // the loop spilled, and the scratch reloads waited for every load in flight
+  float* s_w = fwd_smem + (PAR_LDS ? (PT ? 3 : 1) * NPAR : 0);
   if (!A.reload) {
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
@@ -134,7 +136,8 @@ __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
       const int c0 = q * V;
       const bool act = (j < A.ch) && (q < A.nchunks);
 #pragma unroll
-      for (int v = 0; v < V; ++v) wv[j][v] = (act && c0 + v < C) ? Wt[c0 + v] : 0.0f;
+      for (int v = 0; v < V; ++v)
+        s_w[(j * V + v) * blockDim.x + tid] = (act && c0 + v < C) ? Wt[c0 + v] : 0.0f;
     }
   }
 
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(1024) void fused_fwd_kernel(FwdArgs A) {
         const int valid = min(V, C - c0);
         float yn[V];
 #pragma unroll
-        for (int v = 0; v < V; ++v) yn[v] = (y[j][v] * inv) * wv[j][v];
+        for (int v = 0; v < V; ++v) yn[v] = (y[j][v] * inv) * s_w[(j * V + v) * blockDim.x + tid];
 #pragma unroll
         for (int i = 0; i < NMAX; ++i) {
           if (i < n) {
@@ -634,14 +637,16 @@ int launch_fwd_full(FwdArgs A, hipStream_t stream) {
   // n = 4: MHC_FWD_PIPE > 0 takes the pipelined kernel on a persistent grid of that many workgroups per
   // CU.  Alone it ran config 2's forward 7-10 us faster at one workgroup per CU (two to four: slower),
   // but the training step moved by -10, +2.5 and +0.8 us on three boxes, so it is not the default.
-  const int pipe = knob(kKnobFwdPipe, 0);
-  if (pipe > 0 && NMAX == 4 && ch == 1 && raw) {
-    // persistent pipelined grid: `pipe` workgroups per CU
-    const int64_t pb = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * pipe));
-    hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1, true, false, true>), dim3((unsigned)pb), dim3(tpb), 0,
-                       stream, A);
-    MHC_CHECK_LAUNCH("fused_fwd_full_kernel");
-    return MHC_OK;
+  if constexpr (NMAX == 4) {
+    const int pipe = knob(kKnobFwdPipe, 0);
+    if (pipe > 0 && ch == 1 && raw) {
+      // persistent pipelined grid: `pipe` workgroups per CU
+      const int64_t pb = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * pipe));
+      hipLaunchKernelGGL((fused_fwd_full_kernel<NMAX, XT, OT, 1, true, false, true>), dim3((unsigned)pb), dim3(tpb),
+                         0, stream, A);
+      MHC_CHECK_LAUNCH("fused_fwd_full_kernel");
+      return MHC_OK;
+    }
   }
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, kMaxGrid));
   const dim3 g((unsigned)blocks), b(tpb);
@@ -670,11 +675,12 @@ int launch_fwd(FwdArgs A, hipStream_t stream) {
     if (rc != 1) return rc;
   }
   A.nchunks = (int)ceil_div(A.C, V);
-  const ThreadPlan tp = plan_threads(A.nchunks, CH, knob(kKnobFwdTpb, 0));
+  const ThreadPlan tp = plan_threads(A.nchunks, CH, knob(kKnobFwdTpb, 0), 1024);
   A.ch = tp.ch;
   A.reload = tp.reload;
   const bool par_lds = PT || NMAX > 8;
-  const size_t smem = par_lds ? (size_t)(PT ? 3 : 1) * NPAR * sizeof(float) : 0;
+  const size_t smem = (par_lds ? (size_t)(PT ? 3 : 1) * NPAR * sizeof(float) : 0) +
+                      (tp.reload ? 0 : (size_t)CH * V * tp.tpb * sizeof(float));
   const void* kfn = (const void*)fused_fwd_kernel<NMAX, XT, OT, PT>;
   const int occ = occupancy_blocks(kfn, tp.tpb, smem);
   if (occ <= 0)

@@ -953,6 +953,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
         for (int v = 0; v < 8; ++v) dP[e] = fmaf(gr2[e].get(v), ynv[v], dP[e]);
 #pragma unroll
       for (int J = 0; J < 2; ++J) {
+        // one 16-row half of dx at a time: the scheduler would otherwise overlap the halves'
+        // operands and spill
+        __builtin_amdgcn_sched_barrier(0);
         const u32x4 amt[3] = {s_par.amt[J][0][lane], s_par.amt[J][1][lane], s_par.amt[J][2][lane]};
         const float4 a4 = s_par.a4[J][q];
         uint32_t ow[4][4];
@@ -993,9 +996,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 
   // ---- the workgroup's partial row [dw C | 0 .. Cp | dM n*n | dA n | dP n | 0 .. P]
   float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  // the channel base again from the thread index (opaque to the optimiser): kept from before the
+  // token loop, it was the one value the loop spilled
+  int tid2 = tid;
+  asm volatile("" : "+v"(tid2));
+  const int cb2 = (tid2 >> 6) * 128 + 8 * (tid2 & 15);
   if (q == 0) {
-    *reinterpret_cast<float4*>(prow + cb) = make_float4(dwv[0], dwv[1], dwv[2], dwv[3]);
-    *reinterpret_cast<float4*>(prow + cb + 4) = make_float4(dwv[4], dwv[5], dwv[6], dwv[7]);
+    *reinterpret_cast<float4*>(prow + cb2) = make_float4(dwv[0], dwv[1], dwv[2], dwv[3]);
+    *reinterpret_cast<float4*>(prow + cb2 + 4) = make_float4(dwv[4], dwv[5], dwv[6], dwv[7]);
   }
   if (tid == 0)
     for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;

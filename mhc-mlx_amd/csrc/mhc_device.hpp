@@ -100,7 +100,9 @@ struct Vec {
   // the non-temporal hint.  Wider ones (a lane's 32 bytes as two 16-byte
   // loads, so each instruction reads every other 16 bytes of the wave's
   // span) stay cached: with the hint that pattern streams at 48% of HBM peak
-  // on gfx950, without it at 72% (1 GiB copy, read and write).
+  // on gfx950, without it at 72% (1 GiB copy, read and write).  NT = false
+  // drops the hint for data that is read again soon.
+  template <bool NT = true>
   MHC_DEV void load(const T* p) {
     const char* b = reinterpret_cast<const char*>(p);
     if constexpr (kBytes % 16 == 0) {
@@ -108,15 +110,17 @@ struct Vec {
       for (int k = 0; k < kBytes / 16; ++k) {
         const u32x4* a = reinterpret_cast<const u32x4*>(b) + k;
         u32x4 u;
-        if constexpr (kBytes == 16) u = __builtin_nontemporal_load(a);
+        if constexpr (kBytes == 16 && NT) u = __builtin_nontemporal_load(a);
         else u = *a;
         w[4 * k + 0] = u.x; w[4 * k + 1] = u.y; w[4 * k + 2] = u.z; w[4 * k + 3] = u.w;
       }
     } else if constexpr (kBytes == 8) {
-      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(b));
+      const u32x2* a = reinterpret_cast<const u32x2*>(b);
+      const u32x2 u = NT ? __builtin_nontemporal_load(a) : *a;
       w[0] = u.x; w[1] = u.y;
     } else if constexpr (kBytes == 4) {
-      w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(b));
+      const uint32_t* a = reinterpret_cast<const uint32_t*>(b);
+      w[0] = NT ? __builtin_nontemporal_load(a) : *a;
     } else {
       static_assert(kBytes == 2, "unsupported vector width");
       w[0] = (uint32_t)(*reinterpret_cast<const uint16_t*>(b));

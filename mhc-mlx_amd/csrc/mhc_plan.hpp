@@ -16,14 +16,10 @@ namespace mhc {
 // held in registers.  NMAX is n rounded up to {4, 8, 16, 32, 64}.
 template <int NMAX>
 struct FwdCfg {
-  static constexpr int V = NMAX <= 8 ? 8 : 64 / NMAX;
+  // n = 16 takes 2-channel chunks: with 4 the 16 streams' x (64 fp32 values) and the per-stream
+  // branches of a runtime n spilled at the 1024-thread bound (128 VGPRs)
+  static constexpr int V = NMAX <= 8 ? 8 : 32 / NMAX;
   static constexpr int CH = NMAX <= 4 ? 2 : 1;
-};
-
-// Backward tile: x and dout of one chunk per thread.
-template <int NMAX>
-struct BwdCfg {
-  static constexpr int V = NMAX <= 4 ? 8 : (NMAX == 8 ? 4 : (NMAX == 16 ? 2 : 1));
 };
 
 // Register-tiled kernels exist for NMAX in {4, 8, 16}; 0 selects the
@@ -47,24 +43,25 @@ struct ThreadPlan {
   int reload;  // 1: tile does not fit, two passes over the inputs
 };
 
-// Smallest block (multiple of 64, <= 1024) holding nchunks with at most
-// `chmax` chunks per thread; `tpb_pref` > 0 forces the block size.
-inline ThreadPlan plan_threads(int nchunks, int chmax, int tpb_pref) {
+// Smallest block (multiple of 64, <= max_tpb) holding nchunks with at most
+// `chmax` chunks per thread; `tpb_pref` > 0 forces the block size (capped at
+// max_tpb).  Above max_tpb * chmax chunks the kernel reloads (reload = 1).
+inline ThreadPlan plan_threads(int nchunks, int chmax, int tpb_pref, int max_tpb) {
   ThreadPlan p{};
   if (tpb_pref > 0) {
-    p.tpb = std::min(1024, std::max(64, round_up(tpb_pref, 64)));
+    p.tpb = std::min(max_tpb, std::max(64, round_up(tpb_pref, 64)));
     p.ch = (int)ceil_div(nchunks, p.tpb);
     p.reload = p.ch > chmax ? 1 : 0;
     if (p.reload) p.ch = 0;
     return p;
   }
   int tpb = round_up((int)ceil_div(nchunks, chmax), 64);
-  if (tpb <= 1024) {
+  if (tpb <= max_tpb) {
     p.tpb = std::max(64, tpb);
     p.ch = (int)ceil_div(nchunks, p.tpb);
     p.reload = 0;
   } else {
-    p.tpb = 1024;
+    p.tpb = max_tpb;
     p.ch = 0;
     p.reload = 1;
   }
