@@ -11,7 +11,11 @@
 // (mhc_mlx_amd/ops.py), and the library checks its own again.
 #include <torch/extension.h>
 
+#include <cstdlib>
+
 #include <c10/hip/HIPStream.h>
+#include <torch/csrc/Dtype.h>
+#include <torch/csrc/autograd/python_variable.h>
 
 #include "mhc_hip.h"
 
@@ -87,6 +91,26 @@ std::pair<at::Tensor, at::Tensor> layer_fwd(const at::Tensor& x, const at::Tenso
                       n, C, (float)eps, s),
         "mhc_fused_fwd");
   return {out, M};
+}
+
+// layer_fwd (layer-wide parameters, no record) for a call that needs no
+// gradient: out and the projection M share one allocation (out first, M at
+// the next 256-byte boundary), since only out is returned and one allocation
+// costs less host time than two.  out is a view of the whole buffer's first
+// T*n*C elements.
+at::Tensor layer_fwd_nograd(const at::Tensor& x, const at::Tensor& hp, const at::Tensor& hq, const at::Tensor& hr,
+                            const at::Tensor& w, int64_t iters, double eps, at::ScalarType out_dtype) {
+  const int64_t T = x.size(0);
+  const int n = (int)x.size(1), C = (int)x.size(2);
+  const int64_t elt = (int64_t)c10::elementSize(out_dtype), nout = T * n * C;
+  const int64_t m_off = (nout * elt + 255) / 256 * 256;  // bytes
+  const int64_t total = (m_off + (int64_t)n * n * 4 + elt - 1) / elt;
+  at::Tensor buf = at::empty({total}, x.options().dtype(out_dtype));
+  float* M = reinterpret_cast<float*>(static_cast<char*>(buf.data_ptr()) + m_off);
+  check(mhc_layer_fwd(x.data_ptr(), dtype_code(x.scalar_type()), fp(hp), fp(hq), fp(hr), fp(w), buf.data_ptr(),
+                      dtype_code(out_dtype), M, T, n, C, 0, (int)iters, (float)eps, stream_of(x)),
+        "mhc_layer_fwd");
+  return buf.narrow(0, 0, nout).view({T, n, C});
 }
 
 // VJP of layer_fwd: (dx, dH_pre_raw, dH_post_raw, dH_res_raw, d_rms_weight).
@@ -192,8 +216,91 @@ at::Tensor layer_forward_nograd(const at::Tensor& x, const at::Tensor& hpre, con
   check_inputs(x, hpre, hpost, hres, w, per_token);
   const at::ScalarType out_dtype = out_code == MHC_DTYPE_BF16 ? at::kBFloat16
                                    : out_code == MHC_DTYPE_F16 ? at::kHalf : at::kFloat;
+  if (!per_token) return layer_fwd_nograd(x.contiguous(), f32(hpre), f32(hpost), f32(hres), f32(w), iters, eps, out_dtype);
   return layer_fwd(x.contiguous(), f32(hpre), f32(hpost), f32(hres), f32(w), iters, eps, out_dtype, per_token,
                    at::Tensor()).first;
+}
+
+bool env_is_one(const char* name) {
+  const char* v = std::getenv(name);
+  return v != nullptr && v[0] == '1' && v[1] == '\0';
+}
+
+// MHCLayer's forward on the accelerated path, all of its host steps in one
+// call (mhc_mlx/layer.py:339-435): an undefined tensor (None in Python) when
+// MHC_MLX_DISABLE_METAL=1 or MHC_HIP_DISABLE=1 is set (read per call through
+// getenv, which sees os.environ's changes, as the reference reads its switch
+// per call, layer.py:176) or when the call is not one this path takes (x not
+// [B, n, C] for the layer's n and C, tensors off x's GPU, n > 64, a dtype the
+// kernels do not read), so that the module's general path decides and raises
+// the reference's errors.  Otherwise the output: the kernel writes
+// return_dtype directly when it is x's half type (layer.py:361-364), else fp32
+// cast to return_dtype; the autograd node is recorded when grad mode is on and
+// x or a parameter requires a gradient.
+at::Tensor module_forward(const at::Tensor& x, const at::Tensor& hpre, const at::Tensor& hpost,
+                          const at::Tensor& hres, const at::Tensor& w, int64_t n, int64_t C, int64_t iters,
+                          double eps, c10::optional<at::ScalarType> return_dtype) {
+  if (env_is_one("MHC_MLX_DISABLE_METAL") || env_is_one("MHC_HIP_DISABLE")) return at::Tensor();
+  if (n < 1 || n > MHC_MAX_N || x.dim() != 3 || x.size(1) != n || x.size(2) != C || !x.is_cuda()) return at::Tensor();
+  const at::ScalarType xt = x.scalar_type();
+  if (xt != at::kFloat && xt != at::kBFloat16 && xt != at::kHalf) return at::Tensor();
+  const at::Device dev = x.device();
+  for (const at::Tensor* p : {&hpre, &hpost, &hres, &w})
+    if (p->device() != dev) return at::Tensor();
+  if (hpre.numel() != n || hpost.numel() != n || hres.numel() != n * n || w.numel() != C) return at::Tensor();
+  const bool half_out = return_dtype.has_value() && *return_dtype == xt && xt != at::kFloat;
+  const int64_t code = half_out ? dtype_code(xt) : MHC_DTYPE_F32;
+  at::Tensor out;
+  if (at::GradMode::is_enabled() && (x.requires_grad() || hpre.requires_grad() || hpost.requires_grad() ||
+                                     hres.requires_grad() || w.requires_grad())) {
+    out = LayerFn::apply(x.contiguous(), f32(hpre), f32(hpost), f32(hres), f32(w), iters, eps, code, false, n > 16);
+  } else {
+    out = layer_fwd_nograd(x.contiguous(), f32(hpre), f32(hpost), f32(hres), f32(w), iters, eps,
+                           half_out ? xt : at::kFloat);
+  }
+  if (return_dtype.has_value() && out.scalar_type() != *return_dtype) out = out.to(*return_dtype);
+  return out;
+}
+
+// module_forward called with the module itself: its parameters, n, C,
+// sinkhorn_iters, eps and use_metal are read from the instance dict here, so
+// one call with three arguments carries MHCLayer.forward's whole fast path.
+// Anything unexpected there (a deleted or replaced-by-None parameter, an
+// attribute of another type) leaves the call to the general path.
+at::Tensor module_call(py::handle mod, py::handle x_obj, py::handle rd_obj) {
+  py::object dict_obj = py::reinterpret_steal<py::object>(PyObject_GetAttrString(mod.ptr(), "__dict__"));
+  if (!dict_obj) {
+    PyErr_Clear();
+    return at::Tensor();
+  }
+  PyObject* d = dict_obj.ptr();
+  if (!PyDict_Check(d) || PyDict_GetItemString(d, "use_metal") != Py_True) return at::Tensor();
+  PyObject* ps = PyDict_GetItemString(d, "_parameters");
+  PyObject* n_obj = PyDict_GetItemString(d, "n");
+  PyObject* c_obj = PyDict_GetItemString(d, "C");
+  PyObject* it_obj = PyDict_GetItemString(d, "sinkhorn_iters");
+  PyObject* eps_obj = PyDict_GetItemString(d, "eps");
+  if (ps == nullptr || !PyDict_Check(ps) || n_obj == nullptr || !PyLong_Check(n_obj) || c_obj == nullptr ||
+      !PyLong_Check(c_obj) || it_obj == nullptr || !PyLong_Check(it_obj) || eps_obj == nullptr ||
+      !PyFloat_Check(eps_obj) || !THPVariable_Check(x_obj.ptr()))
+    return at::Tensor();
+  PyObject* t[4] = {PyDict_GetItemString(ps, "H_pre_raw"), PyDict_GetItemString(ps, "H_post_raw"),
+                    PyDict_GetItemString(ps, "H_res_raw"), PyDict_GetItemString(ps, "rms_weight")};
+  for (PyObject* o : t)
+    if (o == nullptr || !THPVariable_Check(o)) return at::Tensor();
+  c10::optional<at::ScalarType> rd;
+  if (rd_obj.ptr() != Py_None) {
+    if (!THPDtype_Check(rd_obj.ptr())) return at::Tensor();
+    rd = reinterpret_cast<THPDtype*>(rd_obj.ptr())->scalar_type;
+  }
+  const long long n = PyLong_AsLongLong(n_obj), C = PyLong_AsLongLong(c_obj), iters = PyLong_AsLongLong(it_obj);
+  if (PyErr_Occurred()) {
+    PyErr_Clear();
+    return at::Tensor();
+  }
+  return module_forward(THPVariable_Unpack(x_obj.ptr()), THPVariable_Unpack(t[0]), THPVariable_Unpack(t[1]),
+                        THPVariable_Unpack(t[2]), THPVariable_Unpack(t[3]), n, C, iters,
+                        PyFloat_AS_DOUBLE(eps_obj), rd);
 }
 
 }  // namespace
@@ -202,4 +309,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "torch binding of libmhc_hip for MHCLayer's forward and backward";
   m.def("layer_apply", &layer_apply, "MHCLayer forward with its backward as a C++ autograd Function");
   m.def("layer_forward_nograd", &layer_forward_nograd, "MHCLayer forward without autograd");
+  m.def("module_forward", &module_forward, "MHCLayer.forward's accelerated path (None: take the general path)");
+  m.def("module_call", &module_call, "module_forward with the arguments read from the MHCLayer instance");
 }

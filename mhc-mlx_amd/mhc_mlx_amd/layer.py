@@ -52,10 +52,6 @@ _METAL_FAILED = False
 
 _HIP_AVAILABLE: bool | None = None
 
-_HALF = (torch.float16, torch.bfloat16)
-_MAX_N = _lib.MAX_N
-# output dtype code of the fast path when return_dtype is x's half type (the kernel writes it directly)
-_OUT_CODE = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
 
 
 _ENV = os.environ
@@ -339,40 +335,23 @@ class MHCLayer(nn.Module):
             return return_dtype
         return None
 
-    def _forward_fast(self, x, return_dtype):
-        """The HIP forward with the fewest host steps: one call into the torch binding, which checks the
-        tensors' devices, dtypes and sizes, allocates the output and, when a gradient is needed, records
-        the C++ autograd node whose backward runs the library's VJP.  At small batch the layer's latency
-        is mostly this code.  Returns None whenever the general path has something to decide (a shape
-        error, tensors off the GPU, the torch path, a kernel timer, a library error), and forward() then
-        takes that path."""
-        n = self.n
-        shp = x.shape
-        if not self.use_metal or n > _MAX_N or len(shp) != 3 or shp[1] != n or shp[2] != self.C:
-            return None
-        ps = self._parameters
-        hp, hq, hr, w = ps.get("H_pre_raw"), ps.get("H_post_raw"), ps.get("H_res_raw"), ps.get("rms_weight")
-        if hp is None or hq is None or hr is None or w is None or profiling._active is not None or _disabled_by_env():
-            return None
-        code = _OUT_CODE.get(return_dtype, 0) if return_dtype is x.dtype else 0
-        b = ops._BINDING or ops._binding()
-        try:
-            if torch.is_grad_enabled() and (x.requires_grad or hp.requires_grad or hq.requires_grad
-                                            or hr.requires_grad or w.requires_grad):
-                out = b.layer_apply(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, code, False, n > 16)
-            else:
-                out = b.layer_forward_nograd(x, hp, hq, hr, w, self.sinkhorn_iters, self.eps, code, False)
-        except (RuntimeError, ValueError):
-            return None
-        if return_dtype is not None and out.dtype is not return_dtype:
-            out = out.to(return_dtype)
-        return out
-
     def forward(self, x_expanded: torch.Tensor, *, return_dtype: torch.dtype | None = None) -> torch.Tensor:
-        """Run the mHC layer on x_expanded [B, n, C] (layer.py:339-435)."""
-        out = self._forward_fast(x_expanded, return_dtype)
-        if out is not None:
-            return out
+        """Run the mHC layer on x_expanded [B, n, C] (layer.py:339-435).
+
+        The accelerated path first makes one call into the torch binding (``module_call``): it reads the
+        disable switches, this layer's parameters and settings, checks the tensors' shapes, devices and
+        dtypes, allocates the output and, when a gradient is needed, records the C++ autograd node whose
+        backward runs the library's VJP.  At small batch the layer's latency is mostly this host code.
+        It returns None whenever the general path below has something to decide (a disable switch,
+        use_metal off, a shape error, tensors off the GPU, n > 64, a kernel timer, a library error).
+        """
+        if profiling._active is None:
+            try:
+                out = (ops._BINDING or ops._binding()).module_call(self, x_expanded, return_dtype)
+            except (RuntimeError, ValueError, TypeError):
+                out = None
+            if out is not None:
+                return out
         B, n, C = self._check(x_expanded)
         out = None
         if self._should_use_metal(B, n, C):

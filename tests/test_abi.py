@@ -155,5 +155,5 @@ def test_torch_binding_loads_and_exports_the_layer_calls():
     from mhc_mlx_amd import _ext
 
     mod = _ext.load()
-    assert callable(mod.layer_apply) and callable(mod.layer_forward_nograd)
+    assert callable(mod.layer_apply) and callable(mod.layer_forward_nograd) and callable(mod.module_forward) and callable(mod.module_call)
     assert _ext.load() is mod

@@ -132,12 +132,12 @@ def test_hip_path_is_the_one_that_runs(monkeypatch):
     layer = MHCLayer(n=4, C=128).cuda()
     x = torch.randn(2, 4, 128, device="cuda", requires_grad=True)
     out = layer(x)
-    assert spy.calls == ["layer_apply"] and out.grad_fn is not None
+    assert spy.calls == ["module_call"] and "LayerFn" in out.grad_fn.name()
     out.sum().backward()
     assert x.grad is not None and layer.H_res_raw.grad is not None and layer.rms_weight.grad is not None
     with torch.no_grad():
-        layer(x)
-    assert spy.calls == ["layer_apply", "layer_forward_nograd"]
+        y = layer(x)
+    assert spy.calls == ["module_call", "module_call"] and y.grad_fn is None
 
 
 def test_gpu_layer_reports_hip_available():
@@ -152,7 +152,7 @@ def test_library_failure_falls_back_once_on_gpu(monkeypatch):
     from mhc_mlx_amd import layer as L
 
     monkeypatch.setattr(L, "_METAL_FAILED", False)  # restored before the session guard checks it
-    spy = _BindingSpy(ops._binding(), failing=("layer_apply",),
+    spy = _BindingSpy(ops._binding(), failing=("module_call", "layer_apply"),
                       fail=RuntimeError("mhc_layer_fwd failed (hip error 98): injected by the test"))
     monkeypatch.setattr(ops, "_BINDING", spy)
     g = rng(11)

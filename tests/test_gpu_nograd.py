@@ -1,10 +1,11 @@
-"""GPU tests of MHCLayer's no-gradient forward (inference, torch.no_grad).
+"""GPU tests of MHCLayer's fast path, in particular its no-gradient forward (inference, torch.no_grad).
 
-A call that needs no gradient goes straight to mhc_layer_fwd with the fewest
-host steps (``MHCLayer._forward_fast`` -> ``ops.layer_forward_nograd``).
-It must give bitwise the results of the general op path and match the
-oracle (reference.py:164-184), and hand every case it does not take (tensors
-on another device, a library error) to the general path unchanged.
+Every accelerated module call makes one call into the torch binding
+(``MHCLayer.forward`` -> ``module_call``); a call that needs no
+gradient goes from there straight to mhc_layer_fwd.  It must give bitwise the
+results of the general op path and match the oracle (reference.py:164-184),
+and hand every case it does not take (tensors on another device, n > 64, a
+disable switch, a library error) to the general path unchanged.
 """
 
 import numpy as np
@@ -30,8 +31,9 @@ def _layer(n, C, g):
 
 
 class _Recorder:
-    """Stands in for the torch binding (ops._BINDING): records each no-gradient forward as True (a result)
-    or False (it raised, or ``fail`` was raised in its place); everything else passes through."""
+    """Stands in for the torch binding (ops._BINDING): records each module_call as True (a result
+    without an autograd node), "grad" (a result with one), None (the call was left to the general path) or
+    False (it raised, or ``fail`` was raised in its place); everything else passes through."""
 
     def __init__(self, real, calls, fail=None):
         self.real, self.calls, self.fail = real, calls, fail
@@ -39,22 +41,22 @@ class _Recorder:
     def __getattr__(self, name):
         return getattr(self.real, name)
 
-    def layer_forward_nograd(self, *args):
+    def module_call(self, *args):
         if self.fail is not None:
             self.calls.append(False)
             raise self.fail
         try:
-            out = self.real.layer_forward_nograd(*args)
+            out = self.real.module_call(*args)
         except Exception:
             self.calls.append(False)
             raise
-        self.calls.append(True)
+        self.calls.append(None if out is None else ("grad" if out.grad_fn is not None else True))
         return out
 
 
 @pytest.fixture
 def fast_calls(monkeypatch):
-    """The module's no-gradient forwards through the binding: True for each that returned a result."""
+    """The module's calls into the binding: True for each no-gradient forward that returned a result."""
     calls = []
     monkeypatch.setattr(ops, "_BINDING", _Recorder(ops._binding(), calls))
     return calls
@@ -104,14 +106,33 @@ def test_inference_mode_and_frozen_parameters_take_the_fast_path(fast_calls):
     assert torch.equal(a, b)
 
 
-def test_gradient_calls_skip_the_fast_path(fast_calls):
+def test_gradient_calls_record_the_autograd_node(fast_calls):
     g = rng(12)
     layer, _ = _layer(4, 256, g)
     xt = torch.randn(4, 4, 256, device="cuda", dtype=torch.bfloat16)
     out = layer(xt, return_dtype=torch.bfloat16)
-    assert out.requires_grad and fast_calls == []
+    assert out.requires_grad and fast_calls == ["grad"] and "LayerFn" in out.grad_fn.name()
     out.float().sum().backward()
     assert layer.H_res_raw.grad is not None
+
+
+def test_disable_switch_set_after_construction_takes_the_reference_path(fast_calls, monkeypatch):
+    """MHC_MLX_DISABLE_METAL=1 is read on every call (layer.py:176), also by the binding's fast path: set
+    after the layer was built, the call runs the torch path."""
+    g = rng(15)
+    layer, (hpre, hpost, hres, w) = _layer(4, 128, g)
+    x = torch.from_numpy(g.standard_normal((2, 4, 128)).astype(np.float32)).cuda()
+    for name in ("MHC_MLX_DISABLE_METAL", "MHC_HIP_DISABLE"):
+        monkeypatch.setenv(name, "1")
+        with torch.no_grad():
+            out = layer(x)
+        monkeypatch.delenv(name)
+        assert fast_calls[-1] is None
+        ref = O.mhc_forward_reference(np_of(x), hpre, hpost, hres, w, sinkhorn_iters=20, eps=1e-6)
+        assert rel_err(np_of(out), ref) < 1e-5
+    with torch.no_grad():
+        layer(x)
+    assert fast_calls == [None, None, True]
 
 
 def test_views_and_other_parameter_dtypes_take_the_fast_path(fast_calls):
@@ -148,6 +169,9 @@ def test_the_binding_refuses_tensors_off_the_gpu():
         b.layer_forward_nograd(x.cpu(), *(t.cpu() for t in p), 20, 1e-6, 0, False)
     with pytest.raises(ValueError, match="device"):
         b.layer_apply(x.requires_grad_(True), *p, 20, 1e-6, 0, False, False)
+    # the module's entry leaves such calls to the general path
+    assert b.module_forward(x, *p, 4, 64, 20, 1e-6, None) is None
+    assert b.module_forward(x.cpu(), *(t.cpu() for t in p), 4, 64, 20, 1e-6, None) is None
 
 
 def test_library_error_in_the_fast_path_goes_to_the_general_path(monkeypatch):
@@ -183,7 +207,7 @@ def test_nograd_n_above_64_takes_the_reference_path(grad_mode, fast_calls):
         for p in layer.parameters():
             p.requires_grad_(False)
         out = layer(x)
-    assert fast_calls == []
+    assert fast_calls == [None]
     ref = O.mhc_forward_reference(np_of(x), hpre, hpost, hres, w, sinkhorn_iters=20, eps=1e-6)
     assert out.dtype == torch.float32 and out.is_cuda
     assert rel_err(np_of(out), ref) < 1e-5
