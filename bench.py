@@ -570,9 +570,21 @@ def main() -> int:
                     help="skip configs 3 and 4, residual_add_agg, the n=32 rows and the reference scenarios")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain fp32 copy of this many MiB (counter calibration)")
+    ap.add_argument("--only", choices=["config3", "config4"], default=None,
+                    help="only run this extra workload (--steps timed steps after --warmup) and print its result, "
+                         "for profiling it on its own")
     args = ap.parse_args()
     if args.copy_probe_mib > 0:
         return _copy_probe(args.copy_probe_mib)
+    if args.only is not None:
+        import torch
+
+        from mhc_mlx_amd import _lib
+
+        _lib.load()
+        fn = _config3 if args.only == "config3" else _config4
+        print(json.dumps({args.only: fn(torch.device("cuda:0"), args.steps, args.warmup)}), flush=True)
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU per box; the mHC path shards by token "
