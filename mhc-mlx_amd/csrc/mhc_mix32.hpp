@@ -1,4 +1,4 @@
-// Post-combine (stream_mix_add) kernels for 16 < n <= 32 on MFMA (mix32.hip).
+// Post-combine (stream_mix_add) kernels for 16 < n <= 64 on MFMA (mix32.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -23,7 +23,7 @@ struct Mix32Args {
   int P;              // floats per partial row
 };
 
-// out = Mf X + p Y for 16 < n <= 32, C a multiple of 64, 16-byte aligned
+// out = Mf X + p Y for 16 < n <= 64, C a multiple of 64, 16-byte aligned
 // tensors; y and out fp32 or x's dtype.  Returns 1 when not covered.
 int mix32_fwd(const Mix32Args& A, int x_dtype, int y_dtype, int out_dtype, hipStream_t s);
 

@@ -1,5 +1,5 @@
 // MHCRewire post-combine (stream_mix_add, mhc_mlx/layer.py:302-337,
-// metal.py:954-1014) for 16 < n <= 32 on MFMA (v_mfma_f32_16x16x4_f32):
+// metal.py:954-1014) for 16 < n <= 64 on MFMA (v_mfma_f32_16x16x4_f32):
 //   forward   out = Mf X + p Y                   (Mf_ij = p_i M_ij a_j)
 //   backward  dx = Mf^T G,  dy = p G,  S = G X^T,  Yd_i = sum_c G_ic Y_ic
 // At n = 32 each of Mf X, Mf^T G and G X^T is 1024 FMAs per channel, far
@@ -410,6 +410,309 @@ void mix32_bwd_kernel(Mix32Args A) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 32 < n <= 64: the same contractions over 64 streams (zero past n).
+//
+// Forward: per item the lane loads streams 4m + q (m = 0..15) of channels
+// [4r, 4r + 4) and the y of its output rows; each of the four 16-row blocks
+// I of Mf X is, per channel column v, 16 chained MFMAs whose A operand (Mf
+// row 16I + r at streams 4m + q) is read from LDS, staged once per
+// workgroup as one float4 per (I, m / 4, lane) so that the wave reads
+// consecutive 16 bytes per lane.  Each block's rows are stored before the
+// next block is formed.
+//
+// Backward: per item and 32-channel half g, the lane loads G, X and Y of
+// streams 16I + r (I = 0..3), channels 32g + 8q .. +8 (the channel-contraction
+// layout of the n <= 32 kernel): Yd, dy = p G and S += G X^T (16 blocks of
+// 16 x 16 in registers across the wave's items).  For dx = Mf^T G the lane
+// then reads G again in the stream-contraction layout (streams 4m + q,
+// channels 4r .. 4r + 3; from the caches, the item was just read) with Mf^T
+// staged like the forward's A operand.  At the end the waves' S and Yd are
+// added in wave order through LDS into the workgroup's partial row.
+// ---------------------------------------------------------------------------
+
+constexpr int kMx64Par = 64 * 64 + 64;
+
+// Mf (row-block layout for the forward, column-block layout for the backward) and p into LDS:
+// fw[(I * 4 + j) * 64 + lane] = Mf[16I + r][4(4j + t) + q] (t = 0..3), bw the same with Mf^T.
+MHC_DEV void mx64_stage(float4* fw, float4* bw, float* s_p, const Mix32Args& A) {
+  const int n = A.n;
+  auto act_a = [&](int j) {
+    if (A.h_mode == MHC_H_NONE) return 1.0f;
+    return A.h_mode == MHC_H_RAW ? sigmoidf_(A.hpre[j]) : A.hpre[j];
+  };
+  auto act_p = [&](int i) {
+    if (A.h_mode == MHC_H_NONE) return 1.0f;
+    return A.h_mode == MHC_H_RAW ? 2.0f * sigmoidf_(A.hpost[i]) : A.hpost[i];
+  };
+  auto mf = [&](int i, int j) { return (i < n && j < n) ? act_p(i) * A.M[i * n + j] * act_a(j) : 0.0f; };
+  for (int idx = threadIdx.x; idx < 16 * 64; idx += blockDim.x) {
+    const int blk = idx >> 6, ln = idx & 63;  // blk = I * 4 + j
+    const int I = blk >> 2, j = blk & 3, q = ln >> 4, r = ln & 15;
+    float a[4], b[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int st = 4 * (4 * j + t) + q;
+      a[t] = mf(16 * I + r, st);
+      b[t] = mf(st, 16 * I + r);
+    }
+    if (fw != nullptr) fw[idx] = make_float4(a[0], a[1], a[2], a[3]);
+    if (bw != nullptr) bw[idx] = make_float4(b[0], b[1], b[2], b[3]);
+  }
+  for (int i = threadIdx.x; i < 64; i += blockDim.x) s_p[i] = i < n ? act_p(i) : 0.0f;
+}
+
+// Token rows through buffer resources (one per tensor and item): the lane's
+// 32-bit offset plus a uniform offset per row group.  With n == 64 (FULL)
+// the row part goes in the uniform offset; below it the row part goes in the
+// lane offset, which the range check covers, so rows past n read as zero and
+// their stores are dropped (the resource spans the token's n rows).
+constexpr int kMxRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw, 32-bit data)
+
+template <typename T>
+MHC_DEV __amdgpu_buffer_rsrc_t mx_rsrc(const T* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, (int)bytes, kMxRsrcWord3);
+}
+
+// four elements (16 or 8 bytes)
+template <typename T>
+MHC_DEV void mx_bload4(Vec<T, 4>& v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  if constexpr (ElemTraits<T>::kBytes == 4) {
+    const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+    v.w[0] = u.x; v.w[1] = u.y; v.w[2] = u.z; v.w[3] = u.w;
+  } else {
+    const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0);
+    v.w[0] = u.x; v.w[1] = u.y;
+  }
+}
+
+template <typename T>
+MHC_DEV void mx_bstore4(const float (&o)[4], __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  if constexpr (ElemTraits<T>::kBytes == 4) {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4{__builtin_bit_cast(uint32_t, o[0]), __builtin_bit_cast(uint32_t, o[1]),
+              __builtin_bit_cast(uint32_t, o[2]), __builtin_bit_cast(uint32_t, o[3])},
+        rs, voff, soff, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3])}, rs, voff, soff, 0);
+  }
+}
+
+// FULL: n == 64 and y present.
+template <typename XT, typename YT, typename OT, bool FULL>
+__global__ __launch_bounds__(kMxThreads) void mix64_fwd_kernel(Mix32Args A) {
+  __shared__ float4 s_fw[16 * 64];
+  __shared__ float s_p[64];
+  mx64_stage(s_fw, nullptr, s_p, A);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, r = lane & 15;
+  const int n = FULL ? 64 : A.n, C = A.C;
+  const int nslabs = C / kMxSlab;
+  const int64_t nC = (int64_t)n * C;
+  constexpr uint32_t xs = sizeof(XT), ys = sizeof(YT), os = sizeof(OT);
+  const bool hasy = FULL || A.y != nullptr;
+  const int64_t items = A.T * nslabs;
+  const int64_t stride = (int64_t)gridDim.x * kMxWaves;
+  for (SlabWalk w((int64_t)blockIdx.x * kMxWaves + wave, stride, items, nslabs, nC); w.valid(); w.advance()) {
+    const int64_t tok = w.t * nC;
+    const uint32_t ch = (uint32_t)(w.s * kMxSlab);
+    const auto rx = mx_rsrc((const XT*)A.x + tok, (uint32_t)(nC * xs));
+    const auto ry = mx_rsrc((const YT*)A.y + tok, hasy ? (uint32_t)(nC * ys) : 0u);
+    const auto ro = mx_rsrc((OT*)A.out + tok, (uint32_t)(nC * os));
+    // x: streams 4m + q, channels ch + 4r .. +4
+    Vec<XT, 4> x[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const uint32_t row = (uint32_t)((4 * m + (FULL ? 0 : q)) * C);
+      mx_bload4(x[m], rx, (uint32_t)(((FULL ? q * C : 0) + 4 * r) * xs) + (FULL ? 0u : row * xs),
+                (ch + (FULL ? row : 0u)) * xs);
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      // y of output rows 16I + 4q + k
+      Vec<YT, 4> y[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t row = (uint32_t)((16 * I + (FULL ? 0 : 4 * q) + k) * C);
+        if (hasy)
+          mx_bload4(y[k], ry, (uint32_t)(((FULL ? 4 * q * C : 0) + 4 * r) * ys) + (FULL ? 0u : row * ys),
+                    (ch + (FULL ? row : 0u)) * ys);
+        else
+          y[k].zero();
+      }
+      float am[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 u = s_fw[(I * 4 + j) * 64 + lane];
+        am[4 * j] = u.x; am[4 * j + 1] = u.y; am[4 * j + 2] = u.z; am[4 * j + 3] = u.w;
+      }
+      float o[4][4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < 16; ++m) acc = mfma4(am[m], x[m].get(v), acc);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k][v] = fmaf(s_p[16 * I + 4 * q + k], y[k].get(v), acc[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t row = (uint32_t)((16 * I + (FULL ? 0 : 4 * q) + k) * C);
+        mx_bstore4<OT>(o[k], ro, (uint32_t)(((FULL ? 4 * q * C : 0) + 4 * r) * os) + (FULL ? 0u : row * os),
+                       (ch + (FULL ? row : 0u)) * os);
+      }
+    }
+  }
+}
+
+// FULL: n == 64 with y and dy present (the only variant launched: below 64 the
+// per-row lane offsets take more registers than the kernel has).
+template <typename XT, typename YT, typename GT, bool FULL>
+__global__ __launch_bounds__(kMxThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void mix64_bwd_kernel(Mix32Args A) {
+  __shared__ float4 s_bw[16 * 64];
+  __shared__ float s_p[64];
+  __shared__ float s_red[kMx64Par];
+  mx64_stage(nullptr, s_bw, s_p, A);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, r = lane & 15;
+  const int n = FULL ? 64 : A.n, C = A.C;
+  const int nslabs = C / kMxSlab;
+  const int64_t nC = (int64_t)n * C;
+  constexpr uint32_t xs = sizeof(XT), ys = sizeof(YT), gs = sizeof(GT);
+  const bool hasy = FULL || A.y != nullptr, hasdy = FULL || A.dy != nullptr;
+  float pr[4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I) pr[I] = s_p[16 * I + r];
+
+  f32x4 sacc[4][4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int J = 0; J < 4; ++J) sacc[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float yd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t items = A.T * nslabs;
+  const int64_t stride = (int64_t)gridDim.x * kMxWaves;
+  for (SlabWalk w((int64_t)blockIdx.x * kMxWaves + wave, stride, items, nslabs, nC); w.valid(); w.advance()) {
+    const int64_t tok = w.t * nC;
+    const uint32_t ch = (uint32_t)(w.s * kMxSlab);
+    const auto rg = mx_rsrc((const GT*)A.g + tok, (uint32_t)(nC * gs));
+    const auto rx = mx_rsrc((const XT*)A.x + tok, (uint32_t)(nC * xs));
+    const auto ry = mx_rsrc((const YT*)A.y + tok, hasy ? (uint32_t)(nC * ys) : 0u);
+    const auto rdy = mx_rsrc((YT*)A.dy + tok, hasdy ? (uint32_t)(nC * ys) : 0u);
+    const auto rdx = mx_rsrc((XT*)A.out + tok, (uint32_t)(nC * xs));
+    // S, Yd, dy in quarters of 16 channels: streams 16I + r, channels ch + 16g + 4q .. +4
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      Vec<GT, 4> gg[4];
+      Vec<XT, 4> xx[4];
+      Vec<YT, 4> yy[4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const uint32_t row = (uint32_t)((16 * I + (FULL ? 0 : r)) * C);
+        const uint32_t lo = (uint32_t)((FULL ? r * C : 0) + 4 * q), co = ch + 16 * g;
+        mx_bload4(gg[I], rg, (lo + (FULL ? 0u : row)) * gs, (co + (FULL ? row : 0u)) * gs);
+        mx_bload4(xx[I], rx, (lo + (FULL ? 0u : row)) * xs, (co + (FULL ? row : 0u)) * xs);
+        if (hasy) mx_bload4(yy[I], ry, (lo + (FULL ? 0u : row)) * ys, (co + (FULL ? row : 0u)) * ys);
+        else yy[I].zero();
+      }
+      float gv[4][4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gv[I][e] = gg[I].get(e);
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yd[I] = fmaf(gv[I][e], yy[I].get(e), yd[I]);
+        if (hasdy) {
+          const uint32_t row = (uint32_t)((16 * I + (FULL ? 0 : r)) * C);
+          const uint32_t lo = (uint32_t)((FULL ? r * C : 0) + 4 * q), co = ch + 16 * g;
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = pr[I] * gv[I][e];
+          mx_bstore4<YT>(o, rdy, (lo + (FULL ? 0u : row)) * ys, (co + (FULL ? row : 0u)) * ys);
+        }
+      }
+      // S += G X^T: row block I (g rows), column block J (x rows), K = the four lane groups' channels
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+#pragma unroll
+          for (int J = 0; J < 4; ++J) sacc[I][J] = mfma4(gv[I][e], xx[J].get(e), sacc[I][J]);
+    }
+    // dx = Mf^T G: G again as streams 4m + q, channels ch + 4r .. +4 (from the caches)
+    Vec<GT, 4> gb[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const uint32_t row = (uint32_t)((4 * m + (FULL ? 0 : q)) * C);
+      mx_bload4(gb[m], rg, (uint32_t)(((FULL ? q * C : 0) + 4 * r) * gs) + (FULL ? 0u : row * gs),
+                (ch + (FULL ? row : 0u)) * gs);
+    }
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      float amt[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 u = s_bw[(J * 4 + j) * 64 + lane];
+        amt[4 * j] = u.x; amt[4 * j + 1] = u.y; amt[4 * j + 2] = u.z; amt[4 * j + 3] = u.w;
+      }
+      float o[4][4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < 16; ++m) acc = mfma4(amt[m], gb[m].get(v), acc);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k][v] = acc[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t row = (uint32_t)((16 * J + (FULL ? 0 : 4 * q) + k) * C);
+        mx_bstore4<XT>(o[k], rdx, (uint32_t)(((FULL ? 4 * q * C : 0) + 4 * r) * xs) + (FULL ? 0u : row * xs),
+                       (ch + (FULL ? row : 0u)) * xs);
+      }
+    }
+  }
+
+  // ---- the workgroup's partial row [S n*n | Yd n | zero pad]: the waves' sums added in wave order
+#pragma unroll
+  for (int I = 0; I < 4; ++I) yd[I] = strided_sum<16, 64>(yd[I]);
+  const int nwaves = blockDim.x >> 6;
+  for (int wv = 0; wv < nwaves; ++wv) {
+    if (wave == wv) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int J = 0; J < 4; ++J)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int idx = (16 * I + 4 * q + k) * 64 + 16 * J + r;
+            s_red[idx] = wv == 0 ? sacc[I][J][k] : s_red[idx] + sacc[I][J][k];
+          }
+      if (q == 0) {
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          const int idx = 64 * 64 + 16 * I + r;
+          s_red[idx] = wv == 0 ? yd[I] : s_red[idx] + yd[I];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  for (int k = threadIdx.x; k < A.P; k += blockDim.x) {
+    float v = 0.0f;
+    if (k < n * n) v = s_red[(k / n) * 64 + (k % n)];
+    else if (k < n * n + n) v = s_red[64 * 64 + (k - n * n)];
+    prow[k] = v;
+  }
+}
+
 template <typename F>
 int mx_by_dtype(int code, F&& f) {
   switch (code) {
@@ -431,7 +734,7 @@ int mx_by_pair(int code, F&& f) {
 }
 
 bool mx_covered(const Mix32Args& A, std::initializer_list<const void*> ptrs) {
-  if (A.n <= 16 || A.n > 32 || A.C % kMxSlab != 0 || A.T < 1) return false;
+  if (A.n <= 16 || A.n > 64 || A.C % kMxSlab != 0 || A.T < 1) return false;
   if (knob(kKnobMix32, 1) == 0) return false;
   for (const void* p : ptrs)
     if (p != nullptr && !aligned(p, 16)) return false;
@@ -453,6 +756,14 @@ int mix32_fwd(const Mix32Args& A, int x_dtype, int y_dtype, int out_dtype, hipSt
       using YT = std::remove_pointer_t<decltype(yp)>;
       return mx_by_pair<XT>(out_dtype, [&](auto* op) {
         using OT = std::remove_pointer_t<decltype(op)>;
+        if (A.n > 32) {
+          if (A.n == 64 && A.y)
+            hipLaunchKernelGGL((mix64_fwd_kernel<XT, YT, OT, true>), dim3((unsigned)blocks), dim3(kMxThreads), 0, s, A);
+          else
+            hipLaunchKernelGGL((mix64_fwd_kernel<XT, YT, OT, false>), dim3((unsigned)blocks), dim3(kMxThreads), 0, s, A);
+          MHC_CHECK_LAUNCH("mix64_fwd_kernel");
+          return (int)MHC_OK;
+        }
         if (A.n == 32 && A.y)
           hipLaunchKernelGGL((mix32_fwd_kernel<XT, YT, OT, true>), dim3((unsigned)blocks), dim3(kMxThreads), 0, s, A);
         else
@@ -467,6 +778,9 @@ int mix32_fwd(const Mix32Args& A, int x_dtype, int y_dtype, int out_dtype, hipSt
 int mix32_bwd(const Mix32Args& A, int x_dtype, int y_dtype, int g_dtype, int64_t gmax, hipStream_t s,
               int64_t* num_partials) {
   if (!mx_covered(A, {A.x, A.y, A.g, A.out, A.dy})) return 1;
+  // 32 < n < 64 (rows in the lane offsets, more registers than the kernel has) and calls without y or dy
+  // take the generic kernels
+  if (A.n > 32 && !(A.n == 64 && A.y && A.dy)) return 1;
   const int64_t items = A.T * (A.C / kMxSlab);
   return mx_by_dtype(x_dtype, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
@@ -475,20 +789,27 @@ int mix32_bwd(const Mix32Args& A, int x_dtype, int y_dtype, int g_dtype, int64_t
       return mx_by_pair<XT>(g_dtype, [&](auto* gp) {
         using GT = std::remove_pointer_t<decltype(gp)>;
         // one resident wave of workgroups (each ends in one partial row)
-        const bool full = A.n == 32 && A.y && A.dy;
-        const void* kfn = full ? (const void*)mix32_bwd_kernel<XT, YT, GT, true>
-                               : (const void*)mix32_bwd_kernel<XT, YT, GT, false>;
+        const bool wide = A.n > 32;
+        const bool full = A.n == (wide ? 64 : 32) && A.y && A.dy;
+        const void* kfn = wide ? (const void*)mix64_bwd_kernel<XT, YT, GT, true>
+                               : (full ? (const void*)mix32_bwd_kernel<XT, YT, GT, true>
+                                       : (const void*)mix32_bwd_kernel<XT, YT, GT, false>);
         const int occ = occupancy_blocks(kfn, kMxThreads, 0);
         if (occ <= 0) return 1;
         const int per_cu = knob(kKnobMixBwdGrid, occ);
         int64_t blocks = ceil_div(items, kMxWaves);
         if (per_cu > 0) blocks = std::min<int64_t>(blocks, (int64_t)device_cu_count() * per_cu);
         blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, gmax));
-        if (full)
+        if (wide) {
+          hipLaunchKernelGGL((mix64_bwd_kernel<XT, YT, GT, true>), dim3((unsigned)blocks), dim3(kMxThreads), 0, s, A);
+          MHC_CHECK_LAUNCH("mix64_bwd_kernel");
+        } else if (full) {
           hipLaunchKernelGGL((mix32_bwd_kernel<XT, YT, GT, true>), dim3((unsigned)blocks), dim3(kMxThreads), 0, s, A);
-        else
+          MHC_CHECK_LAUNCH("mix32_bwd_kernel");
+        } else {
           hipLaunchKernelGGL((mix32_bwd_kernel<XT, YT, GT, false>), dim3((unsigned)blocks), dim3(kMxThreads), 0, s, A);
-        MHC_CHECK_LAUNCH("mix32_bwd_kernel");
+          MHC_CHECK_LAUNCH("mix32_bwd_kernel");
+        }
         *num_partials = blocks;
         return (int)MHC_OK;
       });

@@ -136,6 +136,60 @@ def test_post_combine_mfma_above_16_streams(B, n, C, xdt, gdt, odt, knobs):
         assert rel_err(np_of(a), np_of(b)) < half_ulp, name
 
 
+@pytest.mark.parametrize("B,n,C", [(4, 64, 64), (3, 64, 128), (2, 64, 1024), (2, 48, 64), (3, 33, 128)])
+@pytest.mark.parametrize("xdt,gdt,odt", [("bf16", "f32", "f32"), ("bf16", "bf16", "bf16"), ("f16", "f32", "f32"),
+                                         ("f32", "f32", "f32")])
+def test_post_combine_mfma_above_32_streams(B, n, C, xdt, gdt, odt, knobs):
+    """32 < n <= 64 with C a multiple of 64: the forward runs on the fp32 matrix cores (mix64_fwd_kernel,
+    rows past n through the buffer range check), and at n = 64 the VJP too (mix64_bwd_kernel).  Forward
+    and every gradient against the float64 oracle (16-bit outputs per element, within one rounding of the
+    fp32 result), and against the generic kernels (MHC_MIX32 = 0) to fp32 rounding."""
+    g = rng(700 + B + n + C)
+    x = to_dtype_np(g.standard_normal((B, n, C)), xdt)
+    y = to_dtype_np(g.standard_normal((B, n, C)), xdt)
+    dout = to_dtype_np(g.standard_normal((B, n, C)), gdt if odt == "f32" else odt)
+    hpre, hpost, hres, _ = params(g, n, C)
+    got = _post_combine_run(x, y, dout, hpre, hpost, hres, xdt, gdt, odt)
+    ref_out = O.post_combine(x, y, hpre, hpost, hres, 20, 1e-5)
+    refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    names = ["out", "dx", "dy", "dH_pre", "dH_post", "dH_res"]
+    for name, t, r in zip(names, got, [ref_out] + list(refs)):
+        v = np_of(t)
+        if name in ("out", "dx", "dy") and t.dtype != torch.float32:
+            ulp = 2.0 ** -8 if t.dtype == torch.bfloat16 else 2.0 ** -11
+            assert (np.abs(v - r) <= ulp * np.abs(r) + 1e-5 * np.abs(r).max()).all(), name
+        else:
+            assert rel_err(v, r) < (1e-5 if name in ("out", "dx", "dy") else GRAD_TOL), (name, rel_err(v, r))
+    knobs("MHC_MIX32", 0)
+    gen = _post_combine_run(x, y, dout, hpre, hpost, hres, xdt, gdt, odt)
+    for name, a, b in zip(names, got, gen):
+        half_ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}.get(a.dtype, 1e-5)
+        assert rel_err(np_of(a), np_of(b)) < half_ulp, name
+
+
+@pytest.mark.parametrize("gdt", ["bf16", "f32"])
+def test_post_combine_mfma64_walks_several_items_per_wave(gdt, knobs):
+    """One workgroup per CU for the n = 64 MFMA post-combine: each wave walks several (token, slab) items,
+    so the VJP's S / Yd sums run across items and are added over the waves at the end; a second run is
+    bitwise identical."""
+    knobs("MHC_MIX_FWD_GRID", 1)
+    knobs("MHC_MIX_BWD_GRID", 1)
+    B, n, C = 1500, 64, 128
+    g = rng(51)
+    x = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    y = to_dtype_np(g.standard_normal((B, n, C)), "bf16")
+    dout = to_dtype_np(g.standard_normal((B, n, C)), gdt)
+    hpre, hpost, hres, _ = params(g, n, C)
+    runs = [_post_combine_run(x, y, dout, hpre, hpost, hres, "bf16", gdt, "f32") for _ in range(2)]
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    refs = O.post_combine_backward(x, y, hpre, hpost, hres, dout, 20, 1e-5)
+    assert rel_err(np_of(runs[0][0]), O.post_combine(x, y, hpre, hpost, hres, 20, 1e-5)) < 1e-5
+    for name, t, r in zip(["dx", "dy", "dH_pre", "dH_post", "dH_res"], runs[0][1:], refs):
+        tol = 1e-2 if name in ("dx", "dy") else GRAD_TOL
+        assert rel_err(np_of(t), r) < tol, (name, rel_err(np_of(t), r))
+
+
 @pytest.mark.parametrize("gdt", ["bf16", "f32"])
 def test_post_combine_mfma_walks_several_items_per_wave(gdt, knobs):
     """One workgroup per CU for the n = 32 MFMA post-combine: each wave walks several (token, slab) items,
@@ -345,10 +399,12 @@ def test_stream_scale_vjp_flat_matches_per_stream(T, n, C, xdt, knobs):
 @pytest.mark.parametrize("xdt,gdt,odt", [("bf16", "bf16", "bf16"), ("bf16", "f32", "f32"), ("f16", "f16", "f16"),
                                          ("f16", "f32", "f32")])
 def test_post_combine_generic_mfma_sums(B, n, C, xdt, gdt, odt, knobs):
-    """32 < n <= 64 (the generic post-combine kernels): with 16-bit x and dout of x's dtype or fp32 and C a
-    multiple of 32, the VJP's sums S = G X^T run on MFMA (fp32 dout split into three 16-bit terms) and
-    Yd as wave dot products.  Every gradient matches the oracle, and the VALU sums (MHC_GEN_MFMA=0) to
-    fp32 summation order; dx and dy are bitwise the same either way."""
+    """32 < n <= 64 on the generic post-combine kernels (MHC_MIX32 = 0: the MFMA mix kernels off): with
+    16-bit x and dout of x's dtype or fp32 and C a multiple of 32, the VJP's sums S = G X^T run on MFMA
+    (fp32 dout split into three 16-bit terms) and Yd as wave dot products.  Every gradient matches the
+    oracle, and the VALU sums (MHC_GEN_MFMA=0) to fp32 summation order; dx and dy are bitwise the same
+    either way."""
+    knobs("MHC_MIX32", 0)
     g = rng(650 + B + n + C)
     x = to_dtype_np(g.standard_normal((B, n, C)), xdt)
     y = to_dtype_np(g.standard_normal((B, n, C)), xdt)
