@@ -1252,7 +1252,8 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
       }
     }
     __syncthreads();  // dy and yn of every slab in LDS
-    // ---- phase C: dM blocks
+    // ---- phase C: dM blocks, each in rounds of eight 32-channel steps whose loads are issued before
+    // their MFMAs (one step per load-then-MFMA round had left each wave waiting on every load in turn)
 #pragma unroll
     for (int b = 0; b < kBlkW; ++b) {
       if (b >= nblk_w) break;
@@ -1261,33 +1262,55 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
       const int gi = 16 * I + r, xj = 16 * J + r;
       const XT* grow = gt + (int64_t)(gi < n ? gi : 0) * C + 8 * q;
       const XT* xrow = xt + (int64_t)(xj < n ? xj : 0) * C + 8 * q;
+      const u32x4 zero = {0u, 0u, 0u, 0u};
       f32x4 acc = dmb[b];
-      for (int k = 0; k < C; k += 32) {
-        const u32x4 zero = {0u, 0u, 0u, 0u};
-        const u32x4 ga = gi < n ? *reinterpret_cast<const u32x4*>(grow + k) : zero;
-        const u32x4 xb = xj < n ? *reinterpret_cast<const u32x4*>(xrow + k) : zero;
-        acc = mfma32k<XT>(ga, xb, acc);
+      for (int k0 = 0; k0 < C; k0 += 256) {
+        u32x4 ga[8], xb[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int k = k0 + 32 * u;
+          ga[u] = gi < n && k < C ? *reinterpret_cast<const u32x4*>(grow + k) : zero;
+          xb[u] = xj < n && k < C ? *reinterpret_cast<const u32x4*>(xrow + k) : zero;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (k0 + 32 * u < C) acc = mfma32k<XT>(ga[u], xb[u], acc);
       }
       dmb[b] = acc;
     }
-    // dA_j (e < n) and dP_i (e >= n): wave sums over the channels, added into s_dap by their owner
-    for (int e = wave; e < 2 * n; e += nwaves) {
-      const bool da = e < n;
-      const int j = da ? e : e - n;
-      const XT* row = (da ? xt : gt) + (int64_t)j * C;
-      const float* other = da ? s_y : s_d;
-      float acc = 0.0f;
-      for (int c = 8 * lane; c < C; c += 512) {  // eight channels per lane: one 16-byte load
-        Vec<XT, 8> xv;
-        xv.load(row + c);
-        const float4 o0 = *reinterpret_cast<const float4*>(other + c);
-        const float4 o1 = *reinterpret_cast<const float4*>(other + c + 4);
-        const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+    // dA_j (e < n) and dP_i (e >= n): wave sums over the channels, added into s_dap by their owner;
+    // the rows go four at a time, their loads issued before the sums
+    for (int e0 = wave; e0 < 2 * n; e0 += 4 * nwaves) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int c = 8 * lane; c < C; c += 512) {  // eight channels per lane: one 16-byte load per row
+        Vec<XT, 8> xv[4];
 #pragma unroll
-        for (int v = 0; v < 8; ++v) acc = fmaf(ov[v], xv.get(v), acc);
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u * nwaves;
+          if (e < 2 * n) {
+            const int j = e < n ? e : e - n;
+            xv[u].load((e < n ? xt : gt) + (int64_t)j * C + c);
+          } else {
+            xv[u].zero();
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u * nwaves;
+          const float* other = e < n ? s_y : s_d;
+          const float4 o0 = *reinterpret_cast<const float4*>(other + c);
+          const float4 o1 = *reinterpret_cast<const float4*>(other + c + 4);
+          const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+#pragma unroll
+          for (int v = 0; v < 8; ++v) acc[u] = fmaf(ov[v], xv[u].get(v), acc[u]);
+        }
       }
-      acc = wave_sum(acc);
-      if (lane == 0) s_dap[e] += acc;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = e0 + u * nwaves;
+        const float a = wave_sum(acc[u]);
+        if (lane == 0 && e < 2 * n) s_dap[e] += a;
+      }
     }
     __syncthreads();  // phase C done with dy / yn before the next token's phase A writes y / dyn
   }
