@@ -289,23 +289,17 @@ MHC_DEV void sk16_forward_record(float (&P)[16][CPL], int iters, float eps, int 
   }
 }
 
-// REC: also record the VJP state ([batch][iters][4][16] floats at st) for
-// sinkhorn16_bwd_kernel<CPL', true>.
-template <int CPL, bool REC>
+template <int CPL>
 __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_fwd_kernel(const float* __restrict__ logits,
                                                                       float* __restrict__ out, int64_t batch,
-                                                                      int iters, float eps, float* __restrict__ st) {
+                                                                      int iters, float eps) {
   int p;
   const int64_t m = sk16_matrix<CPL>(p);
   const bool mvalid = m < batch;
   float P[16][CPL];
   sk16_load_k<CPL>(logits + (mvalid ? m : 0) * 256, mvalid, p, P);
-  if constexpr (REC) {
-    sk16_forward_record<CPL>(P, iters, eps, p, mvalid, st + (mvalid ? m : 0) * (int64_t)iters * 64);
-  } else {
-    for (int it = 0; it < iters; ++it)
-      sk16_iter<CPL>(P, eps, [](int, float, float) {}, [](int, float, float) {});
-  }
+  for (int it = 0; it < iters; ++it)
+    sk16_iter<CPL>(P, eps, [](int, float, float) {}, [](int, float, float) {});
   if (mvalid) {
     float* O = out + m * 256;
 #pragma unroll
@@ -313,10 +307,10 @@ __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_fwd_kernel(const floa
   }
 }
 
-// st: [batch][iters][4][16] floats (R_k, rs_k, C_k, cs_k).  dM may alias dlogits.
-// RECORDED: st was written by sinkhorn16_fwd_kernel<CPL', true> for the same
-// logits; otherwise the forward is recomputed here and recorded first.
-template <int CPL, bool RECORDED>
+// st: the workspace, [batch][iters][4][16] floats (R_k, rs_k, C_k, cs_k),
+// written by the forward recomputed here and read back by the reverse sweep.
+// dM may alias dlogits.
+template <int CPL>
 __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_bwd_kernel(const float* __restrict__ logits,
                                                                       const float* dM, float* dlogits,
                                                                       int64_t batch, int iters, float eps,
@@ -329,8 +323,7 @@ __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_bwd_kernel(const floa
   float K[16][CPL];
   sk16_load_k<CPL>(logits + mm * 256, mvalid, p, K);
   float* sm = st + mm * (int64_t)iters * 64;
-
-  if constexpr (!RECORDED) {
+  {
     float P[16][CPL];
 #pragma unroll
     for (int i = 0; i < 16; ++i)
@@ -468,8 +461,17 @@ __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_bwd_kernel(const floa
 // itself; the same products, associated differently): the row sums of
 // P_{k-1} are R_{k-1} (K C_{k-1}) and the column sums after the row step are
 // C_{k-1} (R_k K), so an iteration costs two FMAs per element and the matrix
-// is formed once at the end.  The recorded state has the format of the
-// kernels above ([iters][R | rs | C | cs][16]).
+// is formed once at the end.
+//
+// The recorded state (mhc_sinkhorn_fwd_record, always this layout at n = 16)
+// is what the VJP cannot get cheaply: per iteration the row sums rs_k and
+// column sums cs_k (32 floats), and at the start of every VJP segment but the
+// first the cumulative scales R and C (32 floats), [iters][rs | cs][16] then
+// [nseg - 1][R | C][16] per matrix.  The VJP rebuilds R_k and C_k inside a
+// segment from its starting scales with the forward's own products
+// (R_k = R_{k-1} rcp(rs_k) unless masked, likewise C_k), so they are
+// bitwise the forward's: 128 bytes per iteration instead of the 256 of R_k,
+// rs_k, C_k, cs_k.
 //
 // Without a record (MHC_SK16_RECORD=0, or the plain mhc_sinkhorn_bwd) the
 // VJP keeps its per-iteration state (R_k, rs_k, C_k, cs_k of the lane's own
@@ -486,6 +488,18 @@ __global__ __launch_bounds__(kSk16Threads) void sinkhorn16_bwd_kernel(const floa
 constexpr int kSk16bThreads = 256;
 constexpr int kSk16bSeg = 9;  // with 4 waves per SIMD (128 VGPRs), no spills
 constexpr int kSk16bMaxSeg = 32;  // VJP checkpoints: 512 bytes of LDS per wave and segment
+// The VJP from a record holds two segments' sums (the one swept and the next
+// one's, loaded meanwhile) and the rebuilt scales: 5 iterations a segment keep
+// that within 128 VGPRs (9 spilled).  The record's checkpoints follow it.
+constexpr int kSk16bRecSeg = 5;
+
+// Floats of recorded state per matrix: 32 per iteration, 32 per VJP segment
+// after the first (at least 32, so that iters = 0 still has a record).
+__host__ __device__ inline int64_t sk16b_rec_floats(int iters) {
+  const int nseg = (iters + kSk16bRecSeg - 1) / kSk16bRecSeg;
+  const int64_t k = (int64_t)iters + (nseg > 0 ? nseg - 1 : 0);
+  return 32 * (k > 0 ? k : 1);
+}
 
 // A DPP read of another lane's v.  Every read here stays inside the lane's
 // quad or 16-lane row, so no source lane is ever out of range: bound_ctrl on,
@@ -680,7 +694,9 @@ MHC_DEV Sk16bLane sk16b_lane(int64_t batch) {
   return L;
 }
 
-// REC: also record the VJP state ([batch][iters][R | rs | C | cs][16] floats at st).
+// REC: also record the VJP state at st (sk16b_rec_floats(iters) floats per
+// matrix: the sums of every iteration, then the scales at the start of every
+// VJP segment but the first).
 template <bool REC>
 __global__ __launch_bounds__(kSk16bThreads) void sinkhorn16b_fwd_kernel(const float* __restrict__ logits,
                                                                         float* __restrict__ out, int64_t batch,
@@ -693,17 +709,28 @@ __global__ __launch_bounds__(kSk16bThreads) void sinkhorn16b_fwd_kernel(const fl
   sk16b_exp(K, mx);
   Sk16bScales S;
   sk16b_scales(S, 1.0f, 1.0f);
-  float* rec = REC ? st + mm * (int64_t)iters * 64 : nullptr;
+  float* rec = REC ? st + mm * sk16b_rec_floats(iters) : nullptr;
+  // the VJP's segment sg >= 1 starts after iteration first + (sg - 1) kSk16bRecSeg - 1
+  const int nseg = (iters + kSk16bRecSeg - 1) / kSk16bRecSeg;
+  const int first = iters - (nseg - 1) * kSk16bRecSeg;
+  int next_ck = first;  // completed iterations at the next checkpoint
+  float* ck = REC ? rec + (int64_t)iters * 32 : nullptr;
   for (int it = 0; it < iters; ++it) {
     float rs, cs;
     sk16b_iter(K, S, eps, rs, cs);
     if constexpr (REC) {
       if (L.valid) {
-        float* r = rec + (int64_t)it * 64;
-        r[L.ro] = S.R;
-        r[16 + L.ro] = rs;
-        r[32 + L.co] = S.C;
-        r[48 + L.co] = cs;
+        float* r = rec + (int64_t)it * 32;
+        r[L.ro] = rs;
+        r[16 + L.co] = cs;
+        if (it + 1 == next_ck && it + 1 < iters) {
+          ck[L.ro] = S.R;
+          ck[16 + L.co] = S.C;
+        }
+      }
+      if (it + 1 == next_ck && it + 1 < iters) {
+        ck += 32;
+        next_ck += kSk16bRecSeg;
       }
     }
   }
@@ -716,15 +743,18 @@ __global__ __launch_bounds__(kSk16bThreads) void sinkhorn16b_fwd_kernel(const fl
   }
 }
 
-// RECORDED: st holds the forward's record for these logits; otherwise the
-// iterations are recomputed (LDS: kSk16bThreads / 64 * nseg * 512 bytes).
-// dM may alias dlogits: each lane reads and writes only its own block.
+// RECORDED: st holds the forward's record for these logits (each segment's
+// sums and starting scales are loaded while the segment before it in the
+// sweep is processed); otherwise the iterations are recomputed (LDS:
+// kSk16bThreads / 64 * nseg * 512 bytes).  dM may alias dlogits: each lane
+// reads and writes only its own block.
 template <bool RECORDED>
 __global__ __launch_bounds__(kSk16bThreads) __attribute__((amdgpu_waves_per_eu(4))) void sinkhorn16b_bwd_kernel(const float* __restrict__ logits,
                                                                         const float* dM, float* dlogits,
                                                                         int64_t batch, int iters, float eps,
                                                                         const float* __restrict__ st) {
   extern __shared__ float2 sk16b_ck[];
+  constexpr int SEG = RECORDED ? kSk16bRecSeg : kSk16bSeg;
   const Sk16bLane L = sk16b_lane(batch);
   const int64_t mm = L.valid ? L.m : 0;
   float K[4][4], G[4][4];
@@ -735,10 +765,32 @@ __global__ __launch_bounds__(kSk16bThreads) __attribute__((amdgpu_waves_per_eu(4
   }
   sk16b_load(dM + mm * 256, L.rb, L.cb, G);
   // segment sg covers iterations [first + (sg - 1) S, first + sg S) (sg >= 1) and segment 0 [0, first)
-  const int nseg = (iters + kSk16bSeg - 1) / kSk16bSeg;
-  const int first = iters - (nseg - 1) * kSk16bSeg;
-  const float* rec = RECORDED ? st + mm * (int64_t)iters * 64 : nullptr;
+  const int nseg = (iters + SEG - 1) / SEG;
+  const int first = iters - (nseg - 1) * SEG;
+  const float* rec = RECORDED ? st + mm * sk16b_rec_floats(iters) : nullptr;
   float2* ck = sk16b_ck + (int64_t)(threadIdx.x >> 6) * nseg * 64 + (threadIdx.x & 63);
+  // RECORDED: segment sg's sums (own row, own column) and starting scales.
+  // The loads are unconditional, at addresses inside the matrix's record
+  // (iterations past the segment clamped to the last one, segment 0's
+  // checkpoint read from the last iteration's sums and replaced by 1 where it
+  // is used), so that no value merges with an older one and each load is
+  // waited for only where it is used.
+  auto load_seg = [&](int sg, float (&rs_)[SEG], float (&cs_)[SEG], float& R0_, float& C0_) {
+    const int it0 = sg == 0 ? 0 : first + (sg - 1) * SEG;
+    const float* c = rec + (int64_t)iters * 32 + (int64_t)(sg - 1) * 32;
+    R0_ = c[L.ro];
+    C0_ = c[16 + L.co];
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      const float* r = rec + (int64_t)min(it0 + j, iters - 1) * 32;
+      rs_[j] = r[L.ro];
+      cs_[j] = r[16 + L.co];
+    }
+  };
+  float nrs[SEG], ncs[SEG], nR0 = 1.0f, nC0 = 1.0f;
+  if constexpr (RECORDED) {
+    if (nseg > 0) load_seg(nseg - 1, nrs, ncs, nR0, nC0);
+  }
   if constexpr (!RECORDED) {
     // the scales at each segment's start, lane-private (no cross-lane LDS use)
     Sk16bScales S;
@@ -746,7 +798,7 @@ __global__ __launch_bounds__(kSk16bThreads) __attribute__((amdgpu_waves_per_eu(4
     for (int sg = 0; sg < nseg; ++sg) {
       ck[sg * 64] = make_float2(S.R, S.C);
       if (sg == nseg - 1) break;
-      const int len = sg == 0 ? first : kSk16bSeg;
+      const int len = sg == 0 ? first : SEG;
       for (int j = 0; j < len; ++j) {
         float rs, cs;
         sk16b_iter(K, S, eps, rs, cs);
@@ -754,24 +806,27 @@ __global__ __launch_bounds__(kSk16bThreads) __attribute__((amdgpu_waves_per_eu(4
     }
   }
   for (int sg = nseg - 1; sg >= 0; --sg) {
-    const int it0 = sg == 0 ? 0 : first + (sg - 1) * kSk16bSeg;
-    const int len = sg == 0 ? first : kSk16bSeg;
+    const int len = sg == 0 ? first : SEG;
     float R0 = 1.0f, C0 = 1.0f;
-    float sR[kSk16bSeg], srs[kSk16bSeg], sC[kSk16bSeg], scs[kSk16bSeg];
+    float sR[SEG], srs[SEG], sC[SEG], scs[SEG];
     if constexpr (RECORDED) {
-      if (it0 > 0) {
-        const float* r0 = rec + (int64_t)(it0 - 1) * 64;
-        R0 = r0[L.ro];
-        C0 = r0[32 + L.co];
-      }
+      R0 = sg > 0 ? nR0 : 1.0f;
+      C0 = sg > 0 ? nC0 : 1.0f;
 #pragma unroll
-      for (int j = 0; j < kSk16bSeg; ++j) {
+      for (int j = 0; j < SEG; ++j) {
+        srs[j] = nrs[j];
+        scs[j] = ncs[j];
+      }
+      if (sg > 0) load_seg(sg - 1, nrs, ncs, nR0, nC0);
+      // the forward's cumulative scales, rebuilt with its own products (sk16b_iter)
+      float R = R0, Cc = C0;
+#pragma unroll
+      for (int j = 0; j < SEG; ++j) {
         if (j < len) {
-          const float* r = rec + (int64_t)(it0 + j) * 64;
-          sR[j] = r[L.ro];
-          srs[j] = r[16 + L.ro];
-          sC[j] = r[32 + L.co];
-          scs[j] = r[48 + L.co];
+          R *= srs[j] > eps ? sk_rcp(srs[j]) : 1.0f;
+          Cc *= scs[j] > eps ? sk_rcp(scs[j]) : 0.0f;
+          sR[j] = R;
+          sC[j] = Cc;
         }
       }
     } else {
@@ -781,7 +836,7 @@ __global__ __launch_bounds__(kSk16bThreads) __attribute__((amdgpu_waves_per_eu(4
       Sk16bScales S;
       sk16b_scales(S, R0, C0);
 #pragma unroll
-      for (int j = 0; j < kSk16bSeg; ++j) {
+      for (int j = 0; j < SEG; ++j) {
         if (j < len) {
           sk16b_iter(K, S, eps, srs[j], scs[j]);
           sR[j] = S.R;
@@ -790,7 +845,7 @@ __global__ __launch_bounds__(kSk16bThreads) __attribute__((amdgpu_waves_per_eu(4
       }
     }
 #pragma unroll
-    for (int j = kSk16bSeg - 1; j >= 0; --j) {
+    for (int j = SEG - 1; j >= 0; --j) {
       if (j < len) sk16b_vjp_step(G, K, sR[j], srs[j], scs[j], j > 0 ? sR[j - 1] : R0, j > 0 ? sC[j - 1] : C0, eps);
     }
   }
@@ -1011,9 +1066,9 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
     }
     const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
     if (cpl == 4)
-      hipLaunchKernelGGL((sinkhorn16_fwd_kernel<4, false>), g, b, 0, s, logits, M, batch, iters, eps, nullptr);
+      hipLaunchKernelGGL((sinkhorn16_fwd_kernel<4>), g, b, 0, s, logits, M, batch, iters, eps);
     else
-      hipLaunchKernelGGL((sinkhorn16_fwd_kernel<2, false>), g, b, 0, s, logits, M, batch, iters, eps, nullptr);
+      hipLaunchKernelGGL((sinkhorn16_fwd_kernel<2>), g, b, 0, s, logits, M, batch, iters, eps);
     MHC_CHECK_LAUNCH("sinkhorn16_fwd_kernel");
     return MHC_OK;
   }
@@ -1038,8 +1093,8 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
 }
 
 namespace {
-// n == 16: 64 floats of recorded state per matrix and iteration.
-size_t sk16_state_bytes(int64_t batch, int iters) {
+// n == 16, lanes-per-matrix VJP: 64 floats of workspace per matrix and iteration.
+size_t sk16_ws_bytes(int64_t batch, int iters) {
   return (size_t)batch * (size_t)(iters > 0 ? iters : 1) * 64 * sizeof(float);
 }
 }  // namespace
@@ -1049,7 +1104,7 @@ extern "C" size_t mhc_sinkhorn_bwd_workspace_bytes(int64_t batch, int n, int ite
   if (use_blk(n)) return plan_blk(batch, n, iters, device_cu_count()).ws_bytes;
   const size_t gen = plan_bwd(batch, n, iters, device_cu_count()).ws_bytes;
   // n == 16: the block layout needs none; the other layouts keep their state there
-  if (n == 16 && !(sk16_cpl() == 0 && sk16b_vjp_ok(iters))) return std::max(gen, sk16_state_bytes(batch, iters) + 256);
+  if (n == 16 && !(sk16_cpl() == 0 && sk16b_vjp_ok(iters))) return std::max(gen, sk16_ws_bytes(batch, iters) + 256);
   return gen;
 }
 
@@ -1070,21 +1125,21 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
     return MHC_OK;
   }
   if (use_sk16(n, logits, dM, dlogits) && workspace != nullptr) {
-    // The recorded state starts at the first 256-byte boundary of the workspace:
-    // each matrix's records (256 bytes per iteration) then fill whole cache
+    // The recomputed state starts at the first 256-byte boundary of the workspace:
+    // each matrix's state (256 bytes per iteration) then fills whole cache
     // lines, none shared with a matrix that another wave or CU processes.
     const uintptr_t base = reinterpret_cast<uintptr_t>(workspace);
     const size_t pad = (size_t)((256 - base % 256) % 256);
-    const size_t need = sk16_state_bytes(batch, iters);
+    const size_t need = sk16_ws_bytes(batch, iters);
     if (workspace_bytes >= need + pad) {
       float* st = reinterpret_cast<float*>(base + pad);
       const int cpl = sk16_cpl() == 2 ? 2 : 4;
       const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
       if (cpl == 4)
-        hipLaunchKernelGGL((sinkhorn16_bwd_kernel<4, false>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps,
+        hipLaunchKernelGGL((sinkhorn16_bwd_kernel<4>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps,
                            st);
       else
-        hipLaunchKernelGGL((sinkhorn16_bwd_kernel<2, false>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps,
+        hipLaunchKernelGGL((sinkhorn16_bwd_kernel<2>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps,
                            st);
       MHC_CHECK_LAUNCH("sinkhorn16_bwd_kernel");
       return MHC_OK;
@@ -1122,10 +1177,11 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
 // ---------------------------------------------------------------------------
 
 namespace {
-// Bytes of recorded state per layout: n == 16 (batched kernels) and
+// Bytes of recorded state per layout: n == 16 (the block layout's compact
+// record, whatever MHC_SK16_CPL selects for the unrecorded calls) and
 // 16 < n <= 64 (block layout, MHC_SK_BLK_RECORD=0 turns its recording off).
 size_t sk_record_bytes(int64_t batch, int n, int iters) {
-  if (n == 16) return sk16_state_bytes(batch, iters);
+  if (n == 16) return (size_t)batch * (size_t)sk16b_rec_floats(iters) * sizeof(float);
   return (size_t)batch * (size_t)sk_blk_state_floats(next_pow2(n), iters) * sizeof(float);
 }
 
@@ -1168,19 +1224,9 @@ extern "C" int mhc_sinkhorn_fwd_record(const float* logits, float* M, void* stat
     MHC_CHECK_LAUNCH("sinkhorn_blk_fwd_kernel");
     return MHC_OK;
   }
-  const int cpl = sk16_cpl();
-  if (cpl == 0) {
-    hipLaunchKernelGGL((sinkhorn16b_fwd_kernel<true>), dim3((unsigned)sk16b_blocks(batch)), dim3(kSk16bThreads), 0,
-                       s, logits, M, batch, iters, eps, st);
-    MHC_CHECK_LAUNCH("sinkhorn16b_fwd_kernel");
-    return MHC_OK;
-  }
-  const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
-  if (cpl == 4)
-    hipLaunchKernelGGL((sinkhorn16_fwd_kernel<4, true>), g, b, 0, s, logits, M, batch, iters, eps, st);
-  else
-    hipLaunchKernelGGL((sinkhorn16_fwd_kernel<2, true>), g, b, 0, s, logits, M, batch, iters, eps, st);
-  MHC_CHECK_LAUNCH("sinkhorn16_fwd_kernel");
+  hipLaunchKernelGGL((sinkhorn16b_fwd_kernel<true>), dim3((unsigned)sk16b_blocks(batch)), dim3(kSk16bThreads), 0, s,
+                     logits, M, batch, iters, eps, st);
+  MHC_CHECK_LAUNCH("sinkhorn16b_fwd_kernel");
   return MHC_OK;
 }
 
@@ -1207,18 +1253,8 @@ extern "C" int mhc_sinkhorn_bwd_recorded(const float* logits, const float* dM, f
     MHC_CHECK_LAUNCH("sinkhorn_blk_bwd_kernel");
     return MHC_OK;
   }
-  const int cpl = sk16_cpl();
-  if (cpl == 0) {
-    hipLaunchKernelGGL((sinkhorn16b_bwd_kernel<true>), dim3((unsigned)sk16b_blocks(batch)), dim3(kSk16bThreads), 0,
-                       s, logits, dM, dlogits, batch, iters, eps, st);
-    MHC_CHECK_LAUNCH("sinkhorn16b_bwd_kernel");
-    return MHC_OK;
-  }
-  const dim3 g((unsigned)sk16_blocks(batch, cpl)), b(kSk16Threads);
-  if (cpl == 4)
-    hipLaunchKernelGGL((sinkhorn16_bwd_kernel<4, true>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);
-  else
-    hipLaunchKernelGGL((sinkhorn16_bwd_kernel<2, true>), g, b, 0, s, logits, dM, dlogits, batch, iters, eps, st);
-  MHC_CHECK_LAUNCH("sinkhorn16_bwd_kernel");
+  hipLaunchKernelGGL((sinkhorn16b_bwd_kernel<true>), dim3((unsigned)sk16b_blocks(batch)), dim3(kSk16bThreads), 0, s,
+                     logits, dM, dlogits, batch, iters, eps, st);
+  MHC_CHECK_LAUNCH("sinkhorn16b_bwd_kernel");
   return MHC_OK;
 }

@@ -113,10 +113,19 @@ def test_residual_add_agg_rejects_bad_arguments_on_the_host(lib):
 
 
 def test_sinkhorn_state_is_for_n16_to_64_and_checked_on_the_host(lib, knobs):
-    # n = 16: the same record format for the block layout (default) and the lanes-per-matrix layouts
-    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 8 * 20 * 256 + 256
+    # n = 16: the block layout's compact record whatever layout the unrecorded calls use: per matrix
+    # 32 floats per iteration (row and column sums) and 32 per 5-iteration VJP segment after the first
+    # (the scales at its start), at least 32
+    def rec16(B, iters):
+        nseg = -(-iters // 5)
+        return B * 32 * 4 * max(1, iters + max(nseg - 1, 0)) + 256
+
+    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == rec16(8, 20) == 8 * 23 * 128 + 256
+    assert lib.mhc_sinkhorn_state_bytes(3, 16, 7) == rec16(3, 7) == 3 * 8 * 128 + 256
+    assert lib.mhc_sinkhorn_state_bytes(2, 16, 5) == rec16(2, 5) == 2 * 5 * 128 + 256
+    assert lib.mhc_sinkhorn_state_bytes(2, 16, 0) == rec16(2, 0) == 2 * 128 + 256
     knobs("MHC_SK16_CPL", 4)
-    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == 8 * 20 * 256 + 256
+    assert lib.mhc_sinkhorn_state_bytes(8, 16, 20) == rec16(8, 20)
     knobs("MHC_SK16_CPL", None)
     # block layout (16 < n <= 64): six vectors of next_pow2(n) floats per matrix and iteration
     assert lib.mhc_sinkhorn_state_bytes(8, 32, 20) == 8 * 20 * 6 * 32 * 4 + 256
