@@ -1320,7 +1320,9 @@ void fused_bwd_mfma16_kernel(BwdArgs A) {
 }
 
 // ---------------------------------------------------------------------------
-// Stage 2: fixed-order column sums of the G partial rows, two launches.
+// Stage 2: fixed-order column sums of the G partial rows, two launches
+// (per-token parameters, where only d_w is left: one, col_sum_kernel in
+// mhc_reduce.hpp).
 //
 // reduce_rows_kernel (mhc_reduce.hpp) folds the G rows into S <= kReduceSplit
 // rows (part2); param_finish_kernel adds those S rows, writes the final sums
@@ -1757,7 +1759,9 @@ extern "C" int mhc_fused_bwd_partials(const void* x, int x_dtype, const void* do
 namespace mhc {
 namespace {
 
-// Reduce `G` partial rows: reduce_rows_kernel (when G > kReduceSplit) then param_finish_kernel.
+// Reduce `G` partial rows: per-token parameters (d_w only) in one col_sum_kernel
+// launch; otherwise reduce_rows_kernel (when G > kReduceSplit) then
+// param_finish_kernel.
 // With hres != NULL the Sinkhorn VJP of the reduced dM runs in the second
 // launch; returns 1 when that fusion is not possible (per-token parameters,
 // n > 8, or VJP state beyond the LDS budget).
@@ -1783,6 +1787,14 @@ int launch_param_reduce(const void* workspace, size_t workspace_bytes, int64_t G
     MHC_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                   "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
     MHC_CHECK_ARG(aligned(workspace, 16), "workspace must be 16-byte aligned");
+    if (per_token) {
+      // only d_w is left to sum (the token's parameter gradients are written by the partials pass): one
+      // launch, which takes the place of the two below
+      hipLaunchKernelGGL(col_sum_kernel, dim3((unsigned)ceil_div(R.Cp, 4 * kColSumCols)),
+                         dim3(kColSumCols * kColSumPhases), 0, s, (const float*)workspace, G, R.P, C, dw);
+      MHC_CHECK_LAUNCH("col_sum_kernel");
+      return MHC_OK;
+    }
     if (G <= kReduceSplit) {
       // at most kReduceSplit rows: reduce_rows_kernel would copy them unchanged (one row per output
       // row), so param_finish_kernel reads them where they lie; one launch fewer at small batch
