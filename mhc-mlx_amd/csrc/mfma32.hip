@@ -119,6 +119,15 @@ MHC_DEV void buf_load(Vec<T, 8>& v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, ui
   v.w[0] = u.x; v.w[1] = u.y; v.w[2] = u.z; v.w[3] = u.w;
 }
 
+// v, passed through an empty asm the compiler cannot see through: offsets
+// formed from the result are formed where they are used, instead of being
+// hoisted out of the token loop and held in registers for all of it (with the
+// row part in the lane offset, n < 64, that is one register per row).
+MHC_DEV uint32_t opaque_u32(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Four output rows of eight channels, filled a channel pair (p = 0..3) at a
 // time: 16-bit rows as packed words (one conversion per pair), fp32 rows as
 // the values themselves; stored as 16-byte pieces.
@@ -1022,19 +1031,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 //   B (per slab): dy and yn per channel (overwriting y and dyn in LDS), the
 //     dw term added to the workgroup's partial row, g read again and
 //     dx = M^T G + a dy on MFMA in four 16-row blocks, stored as 16-byte rows.
-//   barrier, then C: dM = G X^T in 16 x 16 blocks owned by the waves for the
-//     whole kernel (operands read as 16-byte pieces of the token's rows, from
-//     the caches), and dA_j = sum dy x_j, dP_i = sum g_i yn as lane partial
-//     sums, one wave per (row, kind), kept across the tokens.
-// Every sum has one owner and a fixed order.  Rows past n (n < 64) read as
-// zero and their stores are dropped (the row part of the offset is in the
-// lane offset, which the buffer range check covers).
+//   C (per slab, right after its B): the slab's part of dM = G X^T, all
+//     sixteen 16 x 16 blocks, per 32-channel chunk from eight 16-byte row
+//     pieces per lane (four 16-row blocks of G as A operands, four of X as
+//     B operands, each used by four MFMAs), read again from the caches (the
+//     slab was just read): the token's rows are read once here, not once per
+//     block row or column.  dA_j = sum dy x_j and dP_i = sum g_i yn come from
+//     the same operands (the slab's dy and yn from LDS), as lane partials.
+//   The dM blocks (in registers) and the dA, dP partials are the wave's over
+//   its slabs and every token; they are added in wave order at the end.
+// Every LDS value a wave reads after the RMS barrier is one it wrote itself,
+// so the RMS barrier is the token's only one.  Every sum has one owner and a
+// fixed order.  Rows past n (n < 64) read as zero and their stores are
+// dropped (the row part of the offset is in the lane offset, which the
+// buffer range check covers).
 // ---------------------------------------------------------------------------
 constexpr int kMf64BwdMaxC = 4096;
 
 template <typename XT, bool RAW, bool FULL>
 __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
-  extern __shared__ float4 s_yd4[];  // [2][S][16 r][8]: y then dyn (phase B: dy then yn)
+  extern __shared__ float4 s_yd4[];  // [2][S][16 r][8]: y then dyn (after the RMS barrier: dy then yn); dw [C]
   float* const s_y = reinterpret_cast<float*>(s_yd4);
   __shared__ float s_red[2][2][16];
   __shared__ u32x4 s_aa[2][3][64], s_ap[2][3][64], s_amt[4][2][3][64];
@@ -1048,6 +1064,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   const int C = A.C;
   const int S = C / 128;
   float* const s_d = s_y + S * 128;
+  float* const s_dw = s_d + S * 128;  // the workgroup's dw, one owner lane per channel
   const int64_t nC = (int64_t)n * C;
   constexpr uint32_t kEs = sizeof(XT);
   const uint32_t rowb = (uint32_t)C * kEs;
@@ -1093,15 +1110,17 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   for (int c = tid; c < A.P; c += blockDim.x) prow[c] = 0.0f;  // dw accumulates here across tokens
   __syncthreads();
 
-  // phase C ownership: dM blocks wave + b * nwaves (16 blocks, at most 4 per wave: nwaves >= 4) in
-  // registers; dot products e = wave + k * nwaves (2n), added per token into s_dap (one owner each)
-  constexpr int kBlkW = 4;
-  f32x4 dmb[kBlkW];
-  const int nblk_w = (16 - wave + nwaves - 1) / nwaves;
+  // phase C sums of the wave's slabs over every token: dM blocks [I][J] (rows 16 I + 4 q + k, column
+  // 16 J + r), dA of streams 16 J + r and dP of streams 16 I + r over the lane's channels
+  f32x4 dmb[4][4];
+  float dAp[4], dPp[4];
 #pragma unroll
-  for (int b = 0; b < kBlkW; ++b) dmb[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  __shared__ float s_dap[128];
-  for (int e = tid; e < 128; e += blockDim.x) s_dap[e] = 0.0f;
+  for (int I = 0; I < 4; ++I) {
+    dAp[I] = dPp[I] = 0.0f;
+#pragma unroll
+    for (int J = 0; J < 4; ++J) dmb[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  const uint32_t lane_c = (uint32_t)(r * C + 8 * q) * kEs;  // stream r (+ 16 I rows), channel 8q of a chunk
 
   int it = 0;
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
@@ -1113,10 +1132,11 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     auto load_half = [&](auto aux, const __amdgpu_buffer_rsrc_t& rs, int slab, int h, u32x4 (&b)[8]) {
       const uint32_t sb = (uint32_t)slab * 128 * kEs;
       const uint32_t hb = (uint32_t)(32 * h) * rowb;
+      const uint32_t li = FULL ? lane_in : opaque_u32(lane_in);
       Vec<XT, 8> xr[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        buf_load<decltype(aux)::value>(xr[e], rs, FULL ? lane_in : lane_in + hb + (uint32_t)e * rowb,
+        buf_load<decltype(aux)::value>(xr[e], rs, FULL ? li : li + hb + (uint32_t)e * rowb,
                                        FULL ? sb + hb + (uint32_t)e * rowb : sb);
       transpose8<XT>(xr, b);
     };
@@ -1192,7 +1212,8 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     }
     const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
     const float kf = (inv * inv * inv / (float)C) * tsr;
-    // ---- phase B
+    // ---- per slab: dy, yn and dw (B1), the slab's dM, dA, dP (C), then dx (B2): C's loads go out before
+    // B2's stores (a wait for a load issued after a store also waits for the store)
     for (int s = 0; s < spw; ++s) {
       const int slab = wave * spw + s;
       float* yp = s_y + (slab * 16 + r) * 8;
@@ -1219,6 +1240,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
         reinterpret_cast<float4*>(dp)[0] = make_float4(yn[0], yn[1], yn[2], yn[3]);
         reinterpret_cast<float4*>(dp)[1] = make_float4(yn[4], yn[5], yn[6], yn[7]);
       }
+      // ---- B2: dx = M^T G + a dy
       u32x4 bg[2][8];
       load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 0, bg[0]);
       load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 1, bg[1]);
@@ -1244,90 +1266,92 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
           if (v & 1) rows.put(v >> 1, even, acc);
           else even = acc;
         }
+        const uint32_t lo = FULL ? lane_out : opaque_u32(lane_out);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const uint32_t row = (uint32_t)(16 * J + k) * rowb;
-          rows.store_buf(k, rdx, FULL ? lane_out : lane_out + row, FULL ? sob + row : sob);
+          rows.store_buf(k, rdx, FULL ? lo : lo + row, FULL ? sob + row : sob);
         }
       }
-    }
-    __syncthreads();  // dy and yn of every slab in LDS
-    // ---- phase C: dM blocks, each in rounds of eight 32-channel steps whose loads are issued before
-    // their MFMAs (one step per load-then-MFMA round had left each wave waiting on every load in turn)
+      // ---- C: 32-channel chunks, each chunk's loads issued before its MFMAs
 #pragma unroll
-    for (int b = 0; b < kBlkW; ++b) {
-      if (b >= nblk_w) break;
-      const int blk = wave + b * nwaves;
-      const int I = blk >> 2, J = blk & 3;
-      const int gi = 16 * I + r, xj = 16 * J + r;
-      const XT* grow = gt + (int64_t)(gi < n ? gi : 0) * C + 8 * q;
-      const XT* xrow = xt + (int64_t)(xj < n ? xj : 0) * C + 8 * q;
-      const u32x4 zero = {0u, 0u, 0u, 0u};
-      f32x4 acc = dmb[b];
-      for (int k0 = 0; k0 < C; k0 += 256) {
-        u32x4 ga[8], xb[8];
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t cb = sob + (uint32_t)(32 * k) * kEs;
+        const uint32_t lc = FULL ? lane_c : opaque_u32(lane_c);
+        Vec<XT, 8> ga[4], xb[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int k = k0 + 32 * u;
-          ga[u] = gi < n && k < C ? *reinterpret_cast<const u32x4*>(grow + k) : zero;
-          xb[u] = xj < n && k < C ? *reinterpret_cast<const u32x4*>(xrow + k) : zero;
+        for (int I = 0; I < 4; ++I) {
+          const uint32_t row = (uint32_t)(16 * I) * rowb;
+          buf_load<0>(ga[I], rg, FULL ? lc : lc + row, FULL ? cb + row : cb);
+          buf_load<0>(xb[I], rx, FULL ? lc : lc + row, FULL ? cb + row : cb);
         }
+        // dy and yn of channels 32 k + 8 q .. + 7 of the slab (written by this wave above)
+        const float4* dyp = reinterpret_cast<const float4*>(s_y + (slab * 16 + 4 * k + q) * 8);
+        const float4* ynp = reinterpret_cast<const float4*>(s_d + (slab * 16 + 4 * k + q) * 8);
+        const float4 dy0 = dyp[0], dy1 = dyp[1], yn0 = ynp[0], yn1 = ynp[1];
+        const float dyc[8] = {dy0.x, dy0.y, dy0.z, dy0.w, dy1.x, dy1.y, dy1.z, dy1.w};
+        const float ync[8] = {yn0.x, yn0.y, yn0.z, yn0.w, yn1.x, yn1.y, yn1.z, yn1.w};
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (k0 + 32 * u < C) acc = mfma32k<XT>(ga[u], xb[u], acc);
-      }
-      dmb[b] = acc;
-    }
-    // dA_j (e < n) and dP_i (e >= n): wave sums over the channels, added into s_dap by their owner;
-    // the rows go four at a time, their loads issued before the sums
-    for (int e0 = wave; e0 < 2 * n; e0 += 4 * nwaves) {
-      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int c = 8 * lane; c < C; c += 512) {  // eight channels per lane: one 16-byte load per row
-        Vec<XT, 8> xv[4];
+        for (int I = 0; I < 4; ++I) {
+          const u32x4 a = {ga[I].w[0], ga[I].w[1], ga[I].w[2], ga[I].w[3]};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int e = e0 + u * nwaves;
-          if (e < 2 * n) {
-            const int j = e < n ? e : e - n;
-            xv[u].load((e < n ? xt : gt) + (int64_t)j * C + c);
-          } else {
-            xv[u].zero();
+          for (int J = 0; J < 4; ++J) {
+            const u32x4 b = {xb[J].w[0], xb[J].w[1], xb[J].w[2], xb[J].w[3]};
+            dmb[I][J] = mfma32k<XT>(a, b, dmb[I][J]);
           }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int e = e0 + u * nwaves;
-          const float* other = e < n ? s_y : s_d;
-          const float4 o0 = *reinterpret_cast<const float4*>(other + c);
-          const float4 o1 = *reinterpret_cast<const float4*>(other + c + 4);
-          const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+        for (int I = 0; I < 4; ++I) {
+          float sa = 0.0f, sp = 0.0f;
 #pragma unroll
-          for (int v = 0; v < 8; ++v) acc[u] = fmaf(ov[v], xv[u].get(v), acc[u]);
+          for (int e = 0; e < 8; ++e) {
+            sa = fmaf(dyc[e], xb[I].get(e), sa);
+            sp = fmaf(ync[e], ga[I].get(e), sp);
+          }
+          dAp[I] += sa;
+          dPp[I] += sp;
         }
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = e0 + u * nwaves;
-        const float a = wave_sum(acc[u]);
-        if (lane == 0 && e < 2 * n) s_dap[e] += a;
-      }
     }
-    __syncthreads();  // phase C done with dy / yn before the next token's phase A writes y / dyn
   }
 
-  // ---- partial row: [dw C | 0 .. Cp | dM n*n | dA n | dP n | 0 .. P]
+  // ---- partial row: [dw C | 0 .. Cp | dM n*n | dA n | dP n | 0 .. P].  The waves' sums are added in
+  // wave order in LDS (in the parameter operands' space, free once every wave is past its last token).
 #pragma unroll
-  for (int b = 0; b < kBlkW; ++b) {
-    if (b >= nblk_w) break;
-    const int blk = wave + b * nwaves;
-    const int I = blk >> 2, J = blk & 3;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = 16 * I + 4 * q + k, j = 16 * J + r;
-      if (i < n && j < n) prow[A.Cp + i * n + j] = dmb[b][k];
-    }
+  for (int I = 0; I < 4; ++I) {
+    dAp[I] += shfl_xor(dAp[I], 16);
+    dAp[I] += shfl_xor(dAp[I], 32);
+    dPp[I] += shfl_xor(dPp[I], 16);
+    dPp[I] += shfl_xor(dPp[I], 32);
   }
-  for (int e = tid; e < 2 * n; e += blockDim.x) prow[A.Cp + n * n + e] = s_dap[e];  // dA, then dP
+  __syncthreads();
+  float* const s_acc = reinterpret_cast<float*>(&s_amt[0][0][0][0]);  // dM [64][64], dA [64], dP [64]
+  static_assert(sizeof(s_amt) >= (64 * 64 + 128) * sizeof(float), "LDS for the wave-order sums");
+  for (int w = 0; w < nwaves; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int J = 0; J < 4; ++J)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            float* d = s_acc + (16 * I + 4 * q + k) * 64 + 16 * J + r;
+            *d = w == 0 ? dmb[I][J][k] : *d + dmb[I][J][k];
+          }
+      if (q == 0) {
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          float* da = s_acc + 4096 + 16 * I + r;
+          float* dp = s_acc + 4096 + 64 + 16 * I + r;
+          *da = w == 0 ? dAp[I] : *da + dAp[I];
+          *dp = w == 0 ? dPp[I] : *dp + dPp[I];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < n * n; e += blockDim.x) prow[A.Cp + e] = s_acc[(e / n) * 64 + e % n];
+  for (int e = tid; e < 2 * n; e += blockDim.x) prow[A.Cp + n * n + e] = s_acc[4096 + (e < n ? e : 64 + e - n)];
 }
 
 // ---------------------------------------------------------------------------

@@ -222,6 +222,12 @@ def test_generic_backward_mfma_parameter_sums(T, n, C, per_token, dt, knobs):
         assert rel_err(np_of(got), ref) < GRAD_TOL
 
 
+def _where_unequal(u, v, k=8):
+    """How many elements of two runs differ, and the first k positions with both values."""
+    d = (u != v).nonzero()
+    return int(d.shape[0]), [(tuple(i.tolist()), float(u[tuple(i)]), float(v[tuple(i)])) for i in d[:k]]
+
+
 @pytest.mark.parametrize("T,n,C", [(64, 64, 512), (300, 64, 1024), (20, 48, 512), (9, 33, 2048), (5, 64, 4096),
                                    (40, 40, 768)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
@@ -251,8 +257,8 @@ def test_mfma64_backward(T, n, C, dt, grid, knobs):
     knobs("MHC_BWD_MFMA", 0)
     gen = run()
     torch.cuda.synchronize()
-    for u, v in zip(a, b):
-        assert torch.equal(u, v)
+    for name, u, v in zip(("dx", "dH_pre", "dH_post", "dH_res", "d_w"), a, b):
+        assert torch.equal(u, v), (name, _where_unequal(u, v))
     refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
     assert rel_err(np_of(a[0]), refs[0]) < TOL[dt]
     _ulp_bound(np_of(a[0]), refs[0], dt)
