@@ -1107,7 +1107,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     }
     s_a[lane] = lane < n ? act_pre<RAW>(A.hpre[lane]) : 0.0f;
   }
-  for (int c = tid; c < A.P; c += blockDim.x) prow[c] = 0.0f;  // dw accumulates here across tokens
+  for (int c = tid; c < C; c += blockDim.x) s_dw[c] = 0.0f;
   __syncthreads();
 
   // phase C sums of the wave's slabs over every token: dM blocks [I][J] (rows 16 I + 4 q + k, column
@@ -1232,7 +1232,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
         yn[v] = yi * wv[v];
       }
       if (q == 0) {
-        float* pw = prow + slab * 128 + 8 * r;
+        float* pw = s_dw + slab * 128 + 8 * r;
 #pragma unroll
         for (int v = 0; v < 8; ++v) pw[v] = fmaf(dyn[v], y[v] * inv, pw[v]);
         reinterpret_cast<float4*>(yp)[0] = make_float4(dy[0], dy[1], dy[2], dy[3]);
@@ -1350,8 +1350,13 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     }
     __syncthreads();
   }
-  for (int e = tid; e < n * n; e += blockDim.x) prow[A.Cp + e] = s_acc[(e / n) * 64 + e % n];
-  for (int e = tid; e < 2 * n; e += blockDim.x) prow[A.Cp + n * n + e] = s_acc[4096 + (e < n ? e : 64 + e - n)];
+  for (int c = tid; c < A.Cp; c += blockDim.x) prow[c] = c < C ? s_dw[c] : 0.0f;
+  for (int e = tid; e < A.P - A.Cp; e += blockDim.x) {
+    float v = 0.0f;
+    if (e < n * n) v = s_acc[(e / n) * 64 + e % n];
+    else if (e < n * n + 2 * n) v = s_acc[4096 + (e < n * n + n ? e - n * n : 64 + e - n * n - n)];
+    prow[A.Cp + e] = v;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2012,7 +2017,7 @@ int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     if (S % w == 0 && (waves == 0 || std::abs(w - target) < std::abs(waves - target))) waves = w;
   if (waves == 0) return 1;  // fewer than four slabs, or no split into 4 to 8 waves
   const int spw = S / waves;
-  const size_t smem = (size_t)2 * S * 128 * sizeof(float);
+  const size_t smem = (size_t)3 * S * 128 * sizeof(float);  // y, dyn and dw
   const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
