@@ -160,10 +160,10 @@ struct OutRows {
   // row k through a buffer resource (lane offset voff, uniform offset soff)
   MHC_DEV void store_buf(int k, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) const {
     if constexpr (kHalf) {
-      __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}, rs, voff, soff, kBufNt);
+      buf_store_b128<kBufNt>(u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}, rs, voff, soff);
     } else {
-      __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}, rs, voff, soff, 0);
-      __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[k][4], w[k][5], w[k][6], w[k][7]}, rs, voff, soff + 16, 0);
+      buf_store_b128<0>(u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}, rs, voff, soff);
+      buf_store_b128<0>(u32x4{w[k][4], w[k][5], w[k][6], w[k][7]}, rs, voff, soff + 16);
     }
   }
 };
@@ -1028,16 +1028,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 //     parameters); the token sums sum y^2 and sum dyn y w; y and dyn of the
 //     slab's channels to LDS.
 //   RMS barrier.
-//   B (per slab): dy and yn per channel (overwriting y and dyn in LDS), the
-//     dw term added to the workgroup's partial row, g read again and
-//     dx = M^T G + a dy on MFMA in four 16-row blocks, stored as 16-byte rows.
-//   C (per slab, right after its B): the slab's part of dM = G X^T, all
-//     sixteen 16 x 16 blocks, per 32-channel chunk from eight 16-byte row
-//     pieces per lane (four 16-row blocks of G as A operands, four of X as
-//     B operands, each used by four MFMAs), read again from the caches (the
-//     slab was just read): the token's rows are read once here, not once per
-//     block row or column.  dA_j = sum dy x_j and dP_i = sum g_i yn come from
-//     the same operands (the slab's dy and yn from LDS), as lane partials.
+//   Then per slab: B1, dy and yn per channel (overwriting y and dyn in LDS)
+//     and the dw term (the workgroup's dw is in LDS); C, the slab's part of
+//     dM = G X^T, all sixteen 16 x 16 blocks, per 32-channel chunk from
+//     eight 16-byte row pieces per lane (four 16-row blocks of G as A
+//     operands, four of X as B operands, each used by four MFMAs): the
+//     token's rows are read once here, not once per block row or column;
+//     dA_j = sum dy x_j and dP_i = sum g_i yn come from the same operands
+//     (the slab's dy and yn from LDS), as lane partials; B2, g read again
+//     and dx = M^T G + a dy on MFMA in four 16-row blocks, stored as 16-byte
+//     rows (C's loads go out before B2's stores: a wait for a load issued
+//     after a store also waits for the store).
 //   The dM blocks (in registers) and the dA, dP partials are the wave's over
 //   its slabs and every token; they are added in wave order at the end.
 // Every LDS value a wave reads after the RMS barrier is one it wrote itself,
@@ -1241,38 +1242,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
         reinterpret_cast<float4*>(dp)[1] = make_float4(yn[4], yn[5], yn[6], yn[7]);
       }
       // ---- B2: dx = M^T G + a dy
-      u32x4 bg[2][8];
-      load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 0, bg[0]);
-      load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 1, bg[1]);
       const uint32_t sob = (uint32_t)slab * 128 * kEs;
-      asm volatile("" ::: "memory");
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        u32x4 amt[2][3];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int e = 0; e < 3; ++e) amt[h][e] = s_amt[J][h][e][lane];
-        float a4[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) a4[k] = s_a[16 * J + 4 * q + k];
-        OutRows<XT> rows;
-        f32x4 even;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          f32x4 acc = {a4[0] * dy[v], a4[1] * dy[v], a4[2] * dy[v], a4[3] * dy[v]};
-          acc = mfma_split3<XT>(amt[0], bg[0][v], acc);
-          acc = mfma_split3<XT>(amt[1], bg[1][v], acc);
-          if (v & 1) rows.put(v >> 1, even, acc);
-          else even = acc;
-        }
-        const uint32_t lo = FULL ? lane_out : opaque_u32(lane_out);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t row = (uint32_t)(16 * J + k) * rowb;
-          rows.store_buf(k, rdx, FULL ? lo : lo + row, FULL ? sob + row : sob);
-        }
-      }
       // ---- C: 32-channel chunks, each chunk's loads issued before its MFMAs
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -1310,6 +1280,37 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
           }
           dAp[I] += sa;
           dPp[I] += sp;
+        }
+      }
+      u32x4 bg[2][8];
+      load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 0, bg[0]);
+      load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 1, bg[1]);
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        u32x4 amt[2][3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 3; ++e) amt[h][e] = s_amt[J][h][e][lane];
+        float a4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a4[k] = s_a[16 * J + 4 * q + k];
+        OutRows<XT> rows;
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = {a4[0] * dy[v], a4[1] * dy[v], a4[2] * dy[v], a4[3] * dy[v]};
+          acc = mfma_split3<XT>(amt[0], bg[0][v], acc);
+          acc = mfma_split3<XT>(amt[1], bg[1][v], acc);
+          if (v & 1) rows.put(v >> 1, even, acc);
+          else even = acc;
+        }
+        const uint32_t lo = FULL ? lane_out : opaque_u32(lane_out);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t row = (uint32_t)(16 * J + k) * rowb;
+          rows.store_buf(k, rdx, FULL ? lo : lo + row, FULL ? sob + row : sob);
         }
       }
     }
@@ -1543,9 +1544,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx,
-                                                 FULL ? lane_dx : lane_dx + (uint32_t)(16 * J + k) * rowb,
-                                                 FULL ? sb + (uint32_t)(16 * J + k) * rowb : sb, kBufNt);
+          buf_store_b128<kBufNt>(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx,
+                                 FULL ? lane_dx : lane_dx + (uint32_t)(16 * J + k) * rowb,
+                                 FULL ? sb + (uint32_t)(16 * J + k) * rowb : sb);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e)
@@ -1792,9 +1793,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
           }
 #pragma unroll
           for (int k = 0; k < 4; ++k)
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx,
-                                                   FULL ? lane_dx : lane_dx + (uint32_t)(16 * J + k) * rowb,
-                                                   FULL ? sb + (uint32_t)(16 * J + k) * rowb : sb, kBufNt);
+            buf_store_b128<kBufNt>(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx,
+                                   FULL ? lane_dx : lane_dx + (uint32_t)(16 * J + k) * rowb,
+                                   FULL ? sb + (uint32_t)(16 * J + k) * rowb : sb);
         }
       }
       {

@@ -154,6 +154,22 @@ MHC_DEV void st_nt(uint32_t* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) 
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+// A 16-byte buffer store whose data registers are not written again until two
+// wait states after it.  The compiler pads a VALU write of the registers of a
+// store of more than 8 bytes (the store reads its data after it issues) only
+// when the store's soffset is not an SGPR; on gfx950 an SGPR soffset is no
+// exemption: with a second wave on the SIMD, lanes 12..15 of each 16-lane row
+// stored the value that the next instruction wrote into the data registers.
+// The s_nop reads the data registers, so they stay unwritten until it has
+// issued; the scheduling barriers keep it right behind the store.
+template <int AUX>
+MHC_DEV void buf_store_b128(u32x4 v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, voff, soff, AUX);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 1" ::"v"(v));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // A 16-byte word: non-temporal when the lane's whole span is this word,
 // cached when it is part of a wider span (see Vec::load).
 template <bool NT>

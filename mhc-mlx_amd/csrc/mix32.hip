@@ -489,10 +489,9 @@ MHC_DEV void mx_bload4(Vec<T, 4>& v, __amdgpu_buffer_rsrc_t rs, uint32_t voff, u
 template <typename T>
 MHC_DEV void mx_bstore4(const float (&o)[4], __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
   if constexpr (ElemTraits<T>::kBytes == 4) {
-    __builtin_amdgcn_raw_buffer_store_b128(
-        u32x4{__builtin_bit_cast(uint32_t, o[0]), __builtin_bit_cast(uint32_t, o[1]),
-              __builtin_bit_cast(uint32_t, o[2]), __builtin_bit_cast(uint32_t, o[3])},
-        rs, voff, soff, 0);
+    buf_store_b128<0>(u32x4{__builtin_bit_cast(uint32_t, o[0]), __builtin_bit_cast(uint32_t, o[1]),
+                            __builtin_bit_cast(uint32_t, o[2]), __builtin_bit_cast(uint32_t, o[3])},
+                      rs, voff, soff);
   } else {
     __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3])}, rs, voff, soff, 0);
   }
