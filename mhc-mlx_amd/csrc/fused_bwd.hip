@@ -1736,6 +1736,7 @@ extern "C" int mhc_fused_bwd_partials(const void* x, int x_dtype, const void* do
     F.x = x; F.g = dout; F.out = dx; F.M = M; F.hpre = h_pre; F.hpost = h_post; F.w = rms_weight;
     F.part = (float*)workspace; F.T = T; F.M_ts = M_token_stride; F.h_ts = h_token_stride; F.n = n; F.C = C;
     F.Cp = L.Cp; F.P = L.P; F.h_mode = h_mode; F.eps = eps;
+    F.dM_tok = dM_tok; F.dpre_tok = dh_pre_tok; F.dpost_tok = dh_post_tok;
     const int rc = mf32_fused_bwd(F, x_dtype, dout_dtype, L.gmax, (hipStream_t)stream, num_partials);
     if (rc != 1) return rc;
     GenArgs G{};

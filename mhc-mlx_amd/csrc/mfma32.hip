@@ -719,7 +719,8 @@ struct Mf32BwdPar {
 };
 
 template <typename XT, bool RAW>
-MHC_DEV void mf32_bwd_params(const Mf32Args& A, int n, Mf32BwdPar& P) {
+MHC_DEV void mf32_bwd_params(const float* __restrict__ M, const float* __restrict__ hpre,
+                             const float* __restrict__ hpost, int n, Mf32BwdPar& P) {
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4, r = lane & 15;
   if (r == 0) {
@@ -727,8 +728,8 @@ MHC_DEV void mf32_bwd_params(const Mf32Args& A, int n, Mf32BwdPar& P) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int i = 8 * q + e;
-      av[e] = i < n ? act_pre<RAW>(A.hpre[i]) : 0.0f;
-      pv[e] = i < n ? act_post<RAW>(A.hpost[i]) : 0.0f;
+      av[e] = i < n ? act_pre<RAW>(hpre[i]) : 0.0f;
+      pv[e] = i < n ? act_post<RAW>(hpost[i]) : 0.0f;
     }
     u32x4 aa[3], ap[3];
     split3x8<XT>(av, aa);
@@ -744,7 +745,7 @@ MHC_DEV void mf32_bwd_params(const Mf32Args& A, int n, Mf32BwdPar& P) {
     const int col = 16 * J + r;
     float mv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) mv[e] = (col < n && 8 * q + e < n) ? A.M[(8 * q + e) * n + col] : 0.0f;
+    for (int e = 0; e < 8; ++e) mv[e] = (col < n && 8 * q + e < n) ? M[(8 * q + e) * n + col] : 0.0f;
     u32x4 amt[3];
     split3x8<XT>(mv, amt);
 #pragma unroll
@@ -754,7 +755,7 @@ MHC_DEV void mf32_bwd_params(const Mf32Args& A, int n, Mf32BwdPar& P) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int j = 16 * J + 4 * q + k;
-        a4[k] = j < n ? act_pre<RAW>(A.hpre[j]) : 0.0f;
+        a4[k] = j < n ? act_pre<RAW>(hpre[j]) : 0.0f;
       }
       P.a4[J][q] = make_float4(a4[0], a4[1], a4[2], a4[3]);
     }
@@ -827,7 +828,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   // parameters, split once by wave 0 into LDS and read per token (registers
   // are kept for the next token's loads)
   __shared__ Mf32BwdPar s_par;
-  if (wave == 0) mf32_bwd_params<XT, RAW>(A, n, s_par);
+  if (wave == 0) mf32_bwd_params<XT, RAW>(A.M, A.hpre, A.hpost, n, s_par);
   __syncthreads();
   float wv[8];
   {
@@ -1017,6 +1018,278 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   if (tid == 0)
     for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
   mf32_bwd_param_sums(A, prow, mf32_lds, n, dm, dA, dP);
+}
+
+// ---------------------------------------------------------------------------
+// Backward for 16 < n <= 32 with per-token parameters, 16-bit x == dout, C a
+// multiple of 128 up to 1024: mf32_bwd_kernel's per-slab work (one slab per
+// wave, staged in the wave's LDS slab buffer) with the token's own M, a, p:
+//   - wave 0 splits the next token's parameters (as mf32_bwd_params does the
+//     layer's) into one of two LDS blocks by token parity, after its dx pass;
+//     the block's readers, two tokens back, are past this token's RMS
+//     barrier by then, and the barrier after the parts below publishes it;
+//   - after the dx pass each wave writes its dM, dA, dP over its slab into
+//     its own slab buffer (free by then), a barrier, one thread per output
+//     adds the waves' parts in wave order and writes the token's dM, dh_pre,
+//     dh_post (with the activation chain), and a barrier before the next
+//     token's slabs overwrite the parts.
+// dw stays in registers across the workgroup's tokens and ends in its
+// partial row.
+// ---------------------------------------------------------------------------
+template <typename XT, bool RAW, bool FULL>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void mf32_bwd_pt_kernel(Mf32Args A) {
+  extern __shared__ __align__(16) uint16_t mf32_lds[];
+  __shared__ float s_red[2][2][kMf32MaxWaves];
+  __shared__ Mf32BwdPar s_par[2];
+  __shared__ float s_act[2][64];  // activated a [32], p [32] of the token, by parity
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int n = FULL ? 32 : A.n;
+  const int C = A.C;
+  const int64_t nC = (int64_t)n * C;
+  uint16_t* xs = mf32_lds + (size_t)wave * kMf32Slab;
+  uint16_t* gs = xs + 32 * kMf32Row;
+  const int cb = wave * 128 + 8 * r;
+
+  auto params = [&](int64_t t, int par) {
+    mf32_bwd_params<XT, RAW>(A.M + t * A.M_ts, A.hpre + t * A.h_ts, A.hpost + t * A.h_ts, n, s_par[par]);
+    if (lane < 32) {
+      s_act[par][lane] = lane < n ? act_pre<RAW>(A.hpre[t * A.h_ts + lane]) : 0.0f;
+      s_act[par][32 + lane] = lane < n ? act_post<RAW>(A.hpost[t * A.h_ts + lane]) : 0.0f;
+    }
+  };
+  if (wave == 0 && (int64_t)blockIdx.x < A.T) params(blockIdx.x, 0);
+  __syncthreads();
+  float wv[8];
+  {
+    const float4 w0 = *reinterpret_cast<const float4*>(A.w + cb);
+    const float4 w1 = *reinterpret_cast<const float4*>(A.w + cb + 4);
+    wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+    wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+  }
+  float dwv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dwv[e] = 0.0f;
+
+  int it = 0;
+  for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
+    const Mf32BwdPar& P = s_par[it & 1];
+    const XT* xt = (const XT*)A.x + t * nC;
+    const XT* gt = (const XT*)A.g + t * nC;
+    // rows past n (n < 32) are loaded from row n - 1 and zeroed by a select: no per-row branch
+    Vec<XT, 8> xr[8], gr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int row = FULL ? 8 * q + e : min(8 * q + e, n - 1);
+      xr[e].load(xt + (int64_t)row * C + cb);
+      gr[e].load(gt + (int64_t)row * C + cb);
+    }
+    if constexpr (!FULL) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool in = 8 * q + e < n;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          xr[e].w[m] = in ? xr[e].w[m] : 0u;
+          gr[e].w[m] = in ? gr[e].w[m] : 0u;
+        }
+      }
+    }
+    f32x4 dm[2][2];
+#pragma unroll
+    for (int I = 0; I < 2; ++I)
+#pragma unroll
+      for (int J = 0; J < 2; ++J) dm[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float dA[8], dP[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dA[e] = dP[e] = 0.0f;
+    float y[8], dyn[8];
+    float ss = 0.0f, sr = 0.0f;
+    {
+      // stage the slab (one LDS row per stream; zero rows for streams >= n)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        *reinterpret_cast<u32x4*>(&xs[(8 * q + e) * kMf32Row + 8 * r]) =
+            u32x4{xr[e].w[0], xr[e].w[1], xr[e].w[2], xr[e].w[3]};
+        *reinterpret_cast<u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]) =
+            u32x4{gr[e].w[0], gr[e].w[1], gr[e].w[2], gr[e].w[3]};
+      }
+      const u32x4 aa[3] = {P.aa[0][q], P.aa[1][q], P.aa[2][q]};
+      const u32x4 ap[3] = {P.ap[0][q], P.ap[1][q], P.ap[2][q]};
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const f32x4 ay = mfma_split3<XT>(aa, column8<XT>(xr, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        const f32x4 ad = mfma_split3<XT>(ap, column8<XT>(gr, v), f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        y[v] = ay[0];
+        dyn[v] = ad[0];
+        ss = fmaf(ay[0], ay[0], ss);
+        sr = fmaf(ad[0] * ay[0], wv[v], sr);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // dM over the slab: A = g rows 16I + r, B = x rows 16J + r, 32 channels per step
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      u32x4 ga[2], xb[2];
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        ga[I] = *reinterpret_cast<const u32x4*>(&gs[(16 * I + r) * kMf32Row + 32 * kk + 8 * q]);
+        xb[I] = *reinterpret_cast<const u32x4*>(&xs[(16 * I + r) * kMf32Row + 32 * kk + 8 * q]);
+      }
+#pragma unroll
+      for (int I = 0; I < 2; ++I)
+#pragma unroll
+        for (int J = 0; J < 2; ++J) dm[I][J] = mfma32k<XT>(ga[I], xb[J], dm[I][J]);
+    }
+    // the four lane groups q hold the same y and dyn: count them once
+    ss = q == 0 ? ss : 0.0f;
+    sr = q == 0 ? sr : 0.0f;
+    ss = wave_sum(ss);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_red[it & 1][0][wave] = ss;
+      s_red[it & 1][1][wave] = sr;
+    }
+    lds_barrier();
+    float tss = 0.0f, tsr = 0.0f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += s_red[it & 1][0][w];
+      tsr += s_red[it & 1][1][w];
+    }
+    const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * tsr;
+
+    float dyv[8], ynv[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const float yi = y[v] * inv;
+      dyv[v] = dyn[v] * inv * wv[v] - kf * y[v];
+      ynv[v] = yi * wv[v];
+      dwv[v] = fmaf(dyn[v], yi, dwv[v]);
+    }
+    // dx rows through a buffer resource spanning the token's n rows: the range check drops the stores of
+    // rows past n (a per-row branch around the stores made the compiler spill)
+    const auto rdx = rows_rsrc((XT*)A.out + t * nC, (uint32_t)(nC * (int64_t)sizeof(XT)));
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      // g back from the slab: dx = M^T g + a dy, and dP
+      Vec<XT, 8> gr2[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(&gs[(8 * q + e) * kMf32Row + 8 * r]);
+        gr2[e].w[0] = u[0]; gr2[e].w[1] = u[1]; gr2[e].w[2] = u[2]; gr2[e].w[3] = u[3];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) dP[e] = fmaf(gr2[e].get(v), ynv[v], dP[e]);
+#pragma unroll
+      for (int J = 0; J < 2; ++J) {
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 amt[3] = {P.amt[J][0][lane], P.amt[J][1][lane], P.amt[J][2][lane]};
+        const float4 a4 = P.a4[J][q];
+        uint32_t ow[4][4];
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const u32x4 bg = column8<XT>(gr2, v);
+          f32x4 acc = {a4.x * dyv[v], a4.y * dyv[v], a4.z * dyv[v], a4.w * dyv[v]};
+          acc = mfma_split3<XT>(amt, bg, acc);
+          if (v & 1) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ow[k][v >> 1] = pack2<XT>(even[k], acc[k]);
+          } else {
+            even = acc;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t vo = (uint32_t)((16 * J + 4 * q + k) * C + cb) * (uint32_t)sizeof(XT);
+          buf_store_b128<kBufNt>(u32x4{ow[k][0], ow[k][1], ow[k][2], ow[k][3]}, rdx, vo, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      // x back from the slab: dA
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        Vec<XT, 8> xv;
+        const u32x4 u = *reinterpret_cast<const u32x4*>(&xs[(8 * q + e) * kMf32Row + 8 * r]);
+        xv.w[0] = u[0]; xv.w[1] = u[1]; xv.w[2] = u[2]; xv.w[3] = u[3];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) dA[e] = fmaf(dyv[v], xv.get(v), dA[e]);
+      }
+    }
+    // this wave's part of the token's dM, dA, dP into its own slab buffer (its reads of the slab above
+    // come first in the wave's program order)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      dA[e] = group_sum<16>(dA[e]);
+      dP[e] = group_sum<16>(dP[e]);
+    }
+    float* mine = reinterpret_cast<float*>(xs);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int I = 0; I < 2; ++I)
+#pragma unroll
+      for (int J = 0; J < 2; ++J)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) mine[(16 * I + 4 * q + k) * 32 + 16 * J + r] = dm[I][J][k];
+    if (r == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        mine[1024 + 8 * q + e] = dA[e];
+        mine[1024 + 32 + 8 * q + e] = dP[e];
+      }
+    }
+    // the next token's parameters (wave 0, into the other parity block), once the token's own sums are
+    // out of its registers
+    if (wave == 0 && t + gridDim.x < A.T) params(t + gridDim.x, (it + 1) & 1);
+    lds_barrier();
+    const int nn = n * n;
+    for (int k = tid; k < nn + 2 * n; k += blockDim.x) {
+      int src;
+      if (k < nn) src = (k / n) * 32 + (k % n);
+      else if (k < nn + n) src = 1024 + (k - nn);
+      else src = 1024 + 32 + (k - nn - n);
+      float sum = 0.0f;
+      for (int w = 0; w < nwaves; ++w) sum += reinterpret_cast<const float*>(mf32_lds + (size_t)w * kMf32Slab)[src];
+      if (k < nn) {
+        A.dM_tok[t * nn + k] = sum;
+      } else if (k < nn + n) {
+        const int j = k - nn;
+        if constexpr (RAW) {
+          const float av = s_act[it & 1][j];
+          sum *= av * (1.0f - av);
+        }
+        A.dpre_tok[t * n + j] = sum;
+      } else {
+        const int i = k - nn - n;
+        if constexpr (RAW) {
+          const float pv = s_act[it & 1][32 + i];
+          sum *= pv * (1.0f - 0.5f * pv);
+        }
+        A.dpost_tok[t * n + i] = sum;
+      }
+    }
+    lds_barrier();  // the parts are read before the next token's slabs are staged over them
+  }
+
+  // ---- the workgroup's partial row [dw C | 0 .. Cp]
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  if (q == 0) {
+    *reinterpret_cast<float4*>(prow + cb) = make_float4(dwv[0], dwv[1], dwv[2], dwv[3]);
+    *reinterpret_cast<float4*>(prow + cb + 4) = make_float4(dwv[4], dwv[5], dwv[6], dwv[7]);
+  }
+  if (tid == 0)
+    for (int c = C; c < A.Cp; ++c) prow[c] = 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -1401,7 +1674,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   const uint32_t lane_dx = (uint32_t)(4 * q * C + 8 * r) * kEs;  // stream 4q (+ 16 J + k rows)
   const uint32_t tokb = (uint32_t)(nC * kEs);
 
-  if (wave == 0) mf32_bwd_params<XT, RAW>(A, n, s_par);
+  if (wave == 0) mf32_bwd_params<XT, RAW>(A.M, A.hpre, A.hpost, n, s_par);
   __syncthreads();
   f32x4 dm[2][2];
 #pragma unroll
@@ -1598,7 +1871,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
   const uint32_t lane_dx = (uint32_t)(4 * q * C + 8 * r) * kEs;  // stream 4q (+ 16 J + k rows)
   const uint32_t tokb = (uint32_t)(nC * kEs);
 
-  if (wave == 0) mf32_bwd_params<XT, RAW>(A, n, s_par);
+  if (wave == 0) mf32_bwd_params<XT, RAW>(A.M, A.hpre, A.hpost, n, s_par);
   __syncthreads();
   f32x4 dm[2][2];
 #pragma unroll
@@ -2042,8 +2315,44 @@ int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   });
 }
 
+// 16 < n <= 32 with per-token parameters (mf32_bwd_pt_kernel): one slab per wave, so C up to 1024.
+int mf32_fused_bwd_pt(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
+  if (A.n <= 16 || A.n > 32 || A.C % 128 != 0 || A.C / 128 > kMf32MaxWaves) return 1;
+  if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
+  if (A.P != A.Cp || A.dM_tok == nullptr || A.dpre_tok == nullptr || A.dpost_tok == nullptr) return 1;
+  if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.out, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
+    return 1;
+  if (knob(kKnobBwdMfma, 1) == 0) return 1;
+  const int waves = A.C / 128;
+  const size_t smem = (size_t)waves * kMf32Slab * sizeof(uint16_t);
+  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 32;
+  return by_half(xd, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    const void* kfn = full ? (raw ? (const void*)mf32_bwd_pt_kernel<XT, true, true>
+                                  : (const void*)mf32_bwd_pt_kernel<XT, false, true>)
+                           : (raw ? (const void*)mf32_bwd_pt_kernel<XT, true, false>
+                                  : (const void*)mf32_bwd_pt_kernel<XT, false, false>);
+    const int occ = occupancy_blocks(kfn, waves * 64, smem);
+    if (occ <= 0) return 1;
+    int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
+    const int grid_pref = knob(kKnobBwdGrid, 0);
+    if (grid_pref > 0) blocks = std::min<int64_t>(gmax, grid_pref);
+    blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
+    const dim3 g((unsigned)blocks), b(waves * 64);
+    with_full(full, [&](auto fc) {
+      constexpr bool F = decltype(fc)::value;
+      if (raw) hipLaunchKernelGGL((mf32_bwd_pt_kernel<XT, true, F>), g, b, smem, s, A);
+      else hipLaunchKernelGGL((mf32_bwd_pt_kernel<XT, false, F>), g, b, smem, s, A);
+    });
+    MHC_CHECK_LAUNCH("mf32_bwd_pt_kernel");
+    *num_partials = blocks;
+    return MHC_OK;
+  });
+}
+
 int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
   if (A.n > 32) return mf64_fused_bwd(A, xd, gd, gmax, s, num_partials);
+  if (A.M_ts != 0) return mf32_fused_bwd_pt(A, xd, gd, gmax, s, num_partials);
   if (A.n <= 16 || A.n > 32 || A.M_ts != 0 || A.C % 128 != 0) return 1;
   if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
   if (A.P != A.Cp + round_up(A.n * A.n + 2 * A.n, 4)) return 1;

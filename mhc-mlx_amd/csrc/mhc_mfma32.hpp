@@ -30,6 +30,11 @@ struct Mf32Args {
   const float* hres;
   float* M_out;
   int iters;
+  // backward with per-token parameters: the token's dM [n, n] and dh_pre, dh_post [n] (with the
+  // activation chain in raw-logit mode)
+  float* dM_tok;
+  float* dpre_tok;
+  float* dpost_tok;
 };
 
 // Forward (out = M x + p * rms_norm(a^T x) w) for 16 < n <= 32, 16-bit x,
@@ -46,7 +51,10 @@ int mf32_layer_fwd_single_launch(const Mf32Args& A, int x_dtype, int out_dtype, 
 // Backward partial-sums pass for 16 < n <= 32 with layer-wide parameters,
 // 16-bit x and dout of one dtype, C a multiple of 128 up to 1024: dx, and one
 // partial row [dw C | pad | dM n*n | dA n | dP n | pad] per workgroup (at
-// most gmax workgroups).  Returns 1 when the shape is not covered.
+// most gmax workgroups).  With per-token parameters (16 < n <= 32, C a
+// multiple of 128 up to 1024): dx, the token's dM, dh_pre, dh_post (A.dM_tok,
+// A.dpre_tok, A.dpost_tok) and one partial row [dw C | pad] per workgroup.
+// Returns 1 when the shape is not covered.
 int mf32_fused_bwd(const Mf32Args& A, int x_dtype, int g_dtype, int64_t gmax, hipStream_t s,
                    int64_t* num_partials);
 

@@ -3,9 +3,10 @@
 The forward covers n = 17 to 32, C from one 128-channel slab to 4096 (one, two and four slabs per wave),
 16-bit x with 16-bit or fp32 output, layer-wide and per-token parameters; the backward covers
 layer-wide parameters with 16-bit x and dout up to C = 1024, and above it up to C = 8192 at n = 32
-(2 to 8 slabs per wave, x and g read again after the RMS barrier) and 5120 below n = 32.  With the grid knobs at a few
-workgroups every workgroup walks many tokens.  Shapes outside these ranges (odd C, fp32 x, fp32
-dout, per-token backward) take the generic kernels and are covered by tests/test_gpu_fused.py.
+(2 to 8 slabs per wave, x and g read again after the RMS barrier) and 5120 below n = 32, and per-token
+parameters up to C = 1024.  With the grid knobs at a few workgroups every workgroup walks many tokens.
+Shapes outside these ranges (odd C, fp32 x, fp32 dout, per-token backward above C = 1024) take the
+generic kernels and are covered by tests/test_gpu_fused.py.
 """
 
 import numpy as np
@@ -117,6 +118,46 @@ def _backward_layer_wide(T, n, C, dt, knobs):
         assert rel_err(np_of(got), r) < GRAD_TOL, (name, rel_err(np_of(got), r))
 
 
+@pytest.mark.parametrize("T,n,C", [(5, 32, 128), (300, 32, 512), (40, 24, 256), (33, 17, 640), (7, 32, 1024),
+                                   (64, 28, 384), (9, 20, 896)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("grid", [None, 3])
+def test_mfma32_backward_per_token(T, n, C, dt, grid, knobs):
+    """Per-token parameters on MFMA (mf32_bwd_pt_kernel: the token's parameters split by wave 0 one token
+    ahead into one of two LDS blocks, the token's dM, dh_pre, dh_post summed across the waves through their
+    slab buffers), C a multiple of 128 up to 1024: against the oracle (every gradient), against the
+    generic kernel (MHC_BWD_MFMA=0), and bitwise between two runs; with MHC_BWD_GRID=3 each workgroup
+    walks many tokens, so both parameter blocks are used."""
+    if grid is not None:
+        knobs("MHC_BWD_GRID", grid)
+    knobs("MHC_SK_BLK_RECORD", 0)
+    g = rng(3500 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T)
+
+    def run():
+        xt = dev_tensor(x, dt).requires_grad_(True)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        out = ops.mhc_layer_forward_dynamic(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+        out.backward(dev_tensor(dout, dt))
+        return [xt.grad] + [p.grad for p in ps]
+
+    a, b = run(), run()
+    knobs("MHC_BWD_MFMA", 0)
+    gen = run()
+    torch.cuda.synchronize()
+    for name, u, v in zip(("dx", "dH_pre", "dH_post", "dH_res", "d_w"), a, b):
+        assert torch.equal(u, v), (name, _where_unequal(u, v))
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    _ulp_bound(np_of(a[0]), refs[0], dt)
+    for name, got, ref in zip(("dH_pre", "dH_post", "dH_res", "d_w"), a[1:], refs[1:]):
+        assert rel_err(np_of(got), ref) < GRAD_TOL, (name, rel_err(np_of(got), ref))
+    assert rel_err(np_of(a[0]), np_of(gen[0])) < TOL[dt]
+    for got, ref in zip(a[1:], gen[1:]):
+        assert rel_err(np_of(got), np_of(ref)) < 1e-5
+
+
 def test_mfma32_matches_the_generic_kernels(knobs):
     """The MFMA kernels and the VALU kernels they replace agree to rounding on the same inputs."""
     T, n, C = 64, 32, 512
@@ -191,7 +232,7 @@ def test_mfma64_forward(T, n, C, xdt, odt, grid, knobs):
 
 @pytest.mark.parametrize("T,n,C,per_token", [(50, 64, 256, False), (20, 48, 512, False), (33, 33, 96, False),
                                              (300, 40, 128, False), (16, 24, 160, True), (9, 64, 64, True),
-                                             (12, 32, 256, True), (7, 20, 40, False)])
+                                             (12, 32, 224, True), (7, 20, 40, False)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_generic_backward_mfma_parameter_sums(T, n, C, per_token, dt, knobs):
     """The generic backward (n > 32, per-token n > 16, and C that the n <= 32 MFMA kernels do not take)
