@@ -1295,30 +1295,36 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 // ---------------------------------------------------------------------------
 // Backward for 32 < n <= 64, layer-wide parameters, 16-bit x == dout, C a
 // multiple of 128 up to 4096.  A persistent workgroup of W waves walks
-// tokens; each wave takes SPW slabs of 128 channels.  Per token:
-//   A (per slab): x and g as two 32-stream halves, transposed into B
-//     operands; y = a^T X and dyn = p^T G on MFMA (two chained halves, split3
-//     parameters); the token sums sum y^2 and sum dyn y w; y and dyn of the
-//     slab's channels to LDS.
+// tokens; each wave takes SPW slabs of 128 channels.  With
+// dy = dyn inv w - kf y and yn = y inv w (inv and kf the token's RMS
+// scalars), dA_i = sum dy x_i = inv sum x_i dyn w - kf sum x_i y and
+// dP_i = sum g_i yn = inv sum g_i y w: every parameter sum can be formed
+// before the token's RMS sums are known, so only dx needs the token after
+// the barrier.  Per token:
+//   Before the barrier, per slab and 32-channel chunk, x and g rows in the
+//     A-operand layout (rows 16 I + r, channels 32 k + 8 q .. + 7, one
+//     16-byte piece per lane and 16-row block): y = a^T X and dyn = p^T G
+//     per channel (the lane's four rows, then a sum over the 16 lanes r);
+//     the slab's part of dM = G X^T on MFMA (four 16-row blocks of G as A
+//     operands, four of X as B operands, each used by four MFMAs); the lane
+//     partials of sum x_i dyn w, sum x_i y and sum g_i y w; the token sums
+//     sum y^2 and sum dyn y w; y and dyn to LDS.  G of the wave's last slab
+//     is also read in the B-operand layout (two 32-stream halves,
+//     transposed) and kept in registers.
 //   RMS barrier.
-//   Then per slab: B1, dy and yn per channel (overwriting y and dyn in LDS)
-//     and the dw term (the workgroup's dw is in LDS); C, the slab's part of
-//     dM = G X^T, all sixteen 16 x 16 blocks, per 32-channel chunk from
-//     eight 16-byte row pieces per lane (four 16-row blocks of G as A
-//     operands, four of X as B operands, each used by four MFMAs): the
-//     token's rows are read once here, not once per block row or column;
-//     dA_j = sum dy x_j and dP_i = sum g_i yn come from the same operands
-//     (the slab's dy and yn from LDS), as lane partials; B2, g read again
-//     and dx = M^T G + a dy on MFMA in four 16-row blocks, stored as 16-byte
-//     rows (C's loads go out before B2's stores: a wait for a load issued
-//     after a store also waits for the store).
+//   After it: dA, dP partials += the token's partials times inv and kf;
+//     per slab (the last first), dy per channel and the dw term (the
+//     workgroup's dw is in LDS), then dx = M^T G + a dy on MFMA in four
+//     16-row blocks, stored as 16-byte rows; slabs other than the last read
+//     G again.
 //   The dM blocks (in registers) and the dA, dP partials are the wave's over
 //   its slabs and every token; they are added in wave order at the end.
 // Every LDS value a wave reads after the RMS barrier is one it wrote itself,
 // so the RMS barrier is the token's only one.  Every sum has one owner and a
-// fixed order.  Rows past n (n < 64) read as zero and their stores are
-// dropped (the row part of the offset is in the lane offset, which the
-// buffer range check covers).
+// fixed order.  Row offsets go in the lane offset (at n = 64 too: uniform
+// row offsets are loop-invariant, and held in SGPRs across the token loop
+// they spill), so rows past n (n < 64) read as zero and their stores are
+// dropped by the buffer range check.
 // ---------------------------------------------------------------------------
 constexpr int kMf64BwdMaxC = 4096;
 
@@ -1327,8 +1333,8 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   extern __shared__ float4 s_yd4[];  // [2][S][16 r][8]: y then dyn (after the RMS barrier: dy then yn); dw [C]
   float* const s_y = reinterpret_cast<float*>(s_yd4);
   __shared__ float s_red[2][2][16];
-  __shared__ u32x4 s_aa[2][3][64], s_ap[2][3][64], s_amt[4][2][3][64];
-  __shared__ float s_a[64];
+  __shared__ u32x4 s_amt[4][2][3][64];
+  __shared__ float s_a[64], s_p[64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1347,24 +1353,11 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   const uint32_t tokb = (uint32_t)(nC * kEs);
   float* prow = A.part + (int64_t)blockIdx.x * A.P;
 
-  // parameters, split once by wave 0
+  // parameters: M^T split once by wave 0 into A operands; a and p
   if (wave == 0) {
     u32x4 sp[3];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      float av[8], pv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = 32 * h + 8 * q + e;
-        av[e] = i < n ? act_pre<RAW>(A.hpre[i]) : 0.0f;
-        pv[e] = i < n ? act_post<RAW>(A.hpost[i]) : 0.0f;
-      }
-      split3x8<XT>(av, sp);
-#pragma unroll
-      for (int e = 0; e < 3; ++e) s_aa[h][e][lane] = sp[e];
-      split3x8<XT>(pv, sp);
-#pragma unroll
-      for (int e = 0; e < 3; ++e) s_ap[h][e][lane] = sp[e];
 #pragma unroll
       for (int J = 0; J < 4; ++J) {
         const int j = 16 * J + r;
@@ -1380,6 +1373,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
       }
     }
     s_a[lane] = lane < n ? act_pre<RAW>(A.hpre[lane]) : 0.0f;
+    s_p[lane] = lane < n ? act_post<RAW>(A.hpost[lane]) : 0.0f;
   }
   for (int c = tid; c < C; c += blockDim.x) s_dw[c] = 0.0f;
   __syncthreads();
@@ -1395,6 +1389,12 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     for (int J = 0; J < 4; ++J) dmb[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   const uint32_t lane_c = (uint32_t)(r * C + 8 * q) * kEs;  // stream r (+ 16 I rows), channel 8q of a chunk
+  float a_r[4], p_r[4];  // a and p of the lane's rows 16 I + r
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+    a_r[I] = s_a[16 * I + r];
+    p_r[I] = s_p[16 * I + r];
+  }
 
   int it = 0;
   for (int64_t t = blockIdx.x; t < A.T; t += gridDim.x, ++it) {
@@ -1406,72 +1406,108 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     auto load_half = [&](auto aux, const __amdgpu_buffer_rsrc_t& rs, int slab, int h, u32x4 (&b)[8]) {
       const uint32_t sb = (uint32_t)slab * 128 * kEs;
       const uint32_t hb = (uint32_t)(32 * h) * rowb;
-      const uint32_t li = FULL ? lane_in : opaque_u32(lane_in);
+      const uint32_t li = opaque_u32(lane_in);
       Vec<XT, 8> xr[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        buf_load<decltype(aux)::value>(xr[e], rs, FULL ? li : li + hb + (uint32_t)e * rowb,
-                                       FULL ? sb + hb + (uint32_t)e * rowb : sb);
+        buf_load<decltype(aux)::value>(xr[e], rs, li + hb + (uint32_t)e * rowb, sb);
       transpose8<XT>(xr, b);
     };
-    // ---- phase A
+    // ---- before the RMS barrier, per slab and 32-channel chunk: x and g rows 16 I + r at channels
+    // 32 k + 8 q .. + 7 (A-operand layout); y = a^T X and dyn = p^T G per channel (the lane's four rows,
+    // then a sum over the 16 lanes r); the slab's part of dM = G X^T on MFMA (four 16-row blocks of G as
+    // A operands, four of X as B operands, each used by four MFMAs); the lane partials of
+    // sum x_i dyn w, sum x_i y and sum g_i y w.  G of the wave's last slab is also read in the B-operand
+    // layout (two 32-stream halves, transposed) and kept for the dx pass.
     float ss = 0.0f, sr = 0.0f;
+    float ua[4], va[4], wa[4];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) ua[I] = va[I] = wa[I] = 0.0f;
+    u32x4 bg[2][8];
     for (int s = 0; s < spw; ++s) {
       const int slab = wave * spw + s;
-      float y[8], dyn[8];
-      {
-        u32x4 bx[2][8];
-        load_half(std::integral_constant<int, 0>{}, rx, slab, 0, bx[0]);
-        load_half(std::integral_constant<int, 0>{}, rx, slab, 1, bx[1]);
-        asm volatile("" ::: "memory");
-        u32x4 aa[2][3];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int e = 0; e < 3; ++e) aa[h][e] = s_aa[h][e][lane];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          f32x4 acc = mfma_split3<XT>(aa[0], bx[0][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-          acc = mfma_split3<XT>(aa[1], bx[1][v], acc);
-          y[v] = acc[0];
-        }
-      }
-      {
-        u32x4 bg[2][8];
+      const uint32_t sob = (uint32_t)slab * 128 * kEs;
+      if (s == spw - 1) {
         load_half(std::integral_constant<int, 0>{}, rg, slab, 0, bg[0]);
         load_half(std::integral_constant<int, 0>{}, rg, slab, 1, bg[1]);
-        asm volatile("" ::: "memory");
-        u32x4 ap[2][3];
+      }
+#pragma unroll 1  // unrolled, the chunks' rows and sums spill
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t cb = sob + (uint32_t)(32 * k) * kEs;
+        const uint32_t lc = opaque_u32(lane_c);
+        Vec<XT, 8> ga[4], xb[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int I = 0; I < 4; ++I) {
+          const uint32_t row = (uint32_t)(16 * I) * rowb;
+          buf_load<0>(xb[I], rx, lc + row, cb);
+          buf_load<0>(ga[I], rg, lc + row, cb);
+        }
+        float wc[8];
+        load_w8(A.w + slab * 128 + 32 * k + 8 * q, wc);
+        float yc[8], dc[8];
 #pragma unroll
-          for (int e = 0; e < 3; ++e) ap[h][e] = s_ap[h][e][lane];
+        for (int e = 0; e < 8; ++e) {
+          float ys = 0.0f, ds = 0.0f;
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          f32x4 acc = mfma_split3<XT>(ap[0], bg[0][v], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-          acc = mfma_split3<XT>(ap[1], bg[1][v], acc);
-          dyn[v] = acc[0];
+          for (int I = 0; I < 4; ++I) {
+            ys = fmaf(a_r[I], xb[I].get(e), ys);
+            ds = fmaf(p_r[I], ga[I].get(e), ds);
+          }
+          yc[e] = strided_sum<1, 16>(ys);
+          dc[e] = strided_sum<1, 16>(ds);
+        }
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          const u32x4 a = {ga[I].w[0], ga[I].w[1], ga[I].w[2], ga[I].w[3]};
+#pragma unroll
+          for (int J = 0; J < 4; ++J) {
+            const u32x4 b = {xb[J].w[0], xb[J].w[1], xb[J].w[2], xb[J].w[3]};
+            dmb[I][J] = mfma32k<XT>(a, b, dmb[I][J]);
+          }
+        }
+        // the rows are converted again below rather than kept as 64 floats
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            xb[I].w[e] = opaque_u32(xb[I].w[e]);
+            ga[I].w[e] = opaque_u32(ga[I].w[e]);
+          }
+        float dw8[8], yw8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dw8[e] = dc[e] * wc[e];
+          yw8[e] = yc[e] * wc[e];
+          // the 16 lanes r hold the same y and dyn: lane r = 0 counts them
+          ss = fmaf(yc[e], yc[e], ss);
+          sr = fmaf(dw8[e], yc[e], sr);
+        }
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          float su = 0.0f, sv = 0.0f, sw = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float xe = xb[I].get(e);
+            su = fmaf(dw8[e], xe, su);
+            sv = fmaf(yc[e], xe, sv);
+            sw = fmaf(yw8[e], ga[I].get(e), sw);
+          }
+          ua[I] += su;
+          va[I] += sv;
+          wa[I] += sw;
+        }
+        if (r == 0) {
+          float4* y4 = reinterpret_cast<float4*>(s_y + slab * 128 + 32 * k + 8 * q);
+          float4* d4 = reinterpret_cast<float4*>(s_d + slab * 128 + 32 * k + 8 * q);
+          y4[0] = make_float4(yc[0], yc[1], yc[2], yc[3]);
+          y4[1] = make_float4(yc[4], yc[5], yc[6], yc[7]);
+          d4[0] = make_float4(dc[0], dc[1], dc[2], dc[3]);
+          d4[1] = make_float4(dc[4], dc[5], dc[6], dc[7]);
         }
       }
-      float wv[8];
-      load_w8(A.w + slab * 128 + 8 * r, wv);
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        ss = fmaf(y[v], y[v], ss);
-        sr = fmaf(dyn[v] * y[v], wv[v], sr);
-      }
-      if (q == 0) {
-        float4* dy4 = reinterpret_cast<float4*>(s_y + (slab * 16 + r) * 8);
-        float4* dd4 = reinterpret_cast<float4*>(s_d + (slab * 16 + r) * 8);
-        dy4[0] = make_float4(y[0], y[1], y[2], y[3]);
-        dy4[1] = make_float4(y[4], y[5], y[6], y[7]);
-        dd4[0] = make_float4(dyn[0], dyn[1], dyn[2], dyn[3]);
-        dd4[1] = make_float4(dyn[4], dyn[5], dyn[6], dyn[7]);
-      }
     }
-    // the four lane groups q hold the same y and dyn: count them once
-    ss = q == 0 ? ss : 0.0f;
-    sr = q == 0 ? sr : 0.0f;
+    ss = r == 0 ? ss : 0.0f;
+    sr = r == 0 ? sr : 0.0f;
     ss = wave_sum(ss);
     sr = wave_sum(sr);
     if (lane == 0) {
@@ -1486,79 +1522,38 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     }
     const float inv = 1.0f / sqrtf(tss / (float)C + A.eps);
     const float kf = (inv * inv * inv / (float)C) * tsr;
-    // ---- per slab: dy, yn and dw (B1), the slab's dM, dA, dP (C), then dx (B2): C's loads go out before
-    // B2's stores (a wait for a load issued after a store also waits for the store)
-    for (int s = 0; s < spw; ++s) {
+    // dy = dyn inv w - kf y and yn = y inv w: dA_i = inv sum x_i dyn w - kf sum x_i y, dP_i = inv sum g_i y w
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      dAp[I] += inv * ua[I] - kf * va[I];
+      dPp[I] += inv * wa[I];
+    }
+    // ---- after it, per slab (the last first: its G is in registers): dy and dw, then
+    // dx = M^T G + a dy on MFMA in four 16-row blocks, stored as 16-byte rows
+    for (int s = spw - 1; s >= 0; --s) {
       const int slab = wave * spw + s;
-      float* yp = s_y + (slab * 16 + r) * 8;
-      float* dp = s_d + (slab * 16 + r) * 8;
+      const float* yp = s_y + (slab * 16 + r) * 8;
+      const float* dp = s_d + (slab * 16 + r) * 8;
       const float4 y0 = reinterpret_cast<const float4*>(yp)[0], y1 = reinterpret_cast<const float4*>(yp)[1];
       const float4 d0 = reinterpret_cast<const float4*>(dp)[0], d1 = reinterpret_cast<const float4*>(dp)[1];
       const float y[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
       const float dyn[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
       float wv[8];
       load_w8(A.w + slab * 128 + 8 * r, wv);
-      float dy[8], yn[8];
+      float dy[8];
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const float yi = y[v] * inv;
-        dy[v] = dyn[v] * inv * wv[v] - kf * y[v];
-        yn[v] = yi * wv[v];
-      }
+      for (int v = 0; v < 8; ++v) dy[v] = dyn[v] * inv * wv[v] - kf * y[v];
       if (q == 0) {
         float* pw = s_dw + slab * 128 + 8 * r;
 #pragma unroll
         for (int v = 0; v < 8; ++v) pw[v] = fmaf(dyn[v], y[v] * inv, pw[v]);
-        reinterpret_cast<float4*>(yp)[0] = make_float4(dy[0], dy[1], dy[2], dy[3]);
-        reinterpret_cast<float4*>(yp)[1] = make_float4(dy[4], dy[5], dy[6], dy[7]);
-        reinterpret_cast<float4*>(dp)[0] = make_float4(yn[0], yn[1], yn[2], yn[3]);
-        reinterpret_cast<float4*>(dp)[1] = make_float4(yn[4], yn[5], yn[6], yn[7]);
       }
-      // ---- B2: dx = M^T G + a dy
+      if (s != spw - 1) {
+        load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 0, bg[0]);
+        load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 1, bg[1]);
+        asm volatile("" ::: "memory");
+      }
       const uint32_t sob = (uint32_t)slab * 128 * kEs;
-      // ---- C: 32-channel chunks, each chunk's loads issued before its MFMAs
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t cb = sob + (uint32_t)(32 * k) * kEs;
-        const uint32_t lc = FULL ? lane_c : opaque_u32(lane_c);
-        Vec<XT, 8> ga[4], xb[4];
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          const uint32_t row = (uint32_t)(16 * I) * rowb;
-          buf_load<0>(ga[I], rg, FULL ? lc : lc + row, FULL ? cb + row : cb);
-          buf_load<0>(xb[I], rx, FULL ? lc : lc + row, FULL ? cb + row : cb);
-        }
-        // dy and yn of channels 32 k + 8 q .. + 7 of the slab (written by this wave above)
-        const float4* dyp = reinterpret_cast<const float4*>(s_y + (slab * 16 + 4 * k + q) * 8);
-        const float4* ynp = reinterpret_cast<const float4*>(s_d + (slab * 16 + 4 * k + q) * 8);
-        const float4 dy0 = dyp[0], dy1 = dyp[1], yn0 = ynp[0], yn1 = ynp[1];
-        const float dyc[8] = {dy0.x, dy0.y, dy0.z, dy0.w, dy1.x, dy1.y, dy1.z, dy1.w};
-        const float ync[8] = {yn0.x, yn0.y, yn0.z, yn0.w, yn1.x, yn1.y, yn1.z, yn1.w};
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          const u32x4 a = {ga[I].w[0], ga[I].w[1], ga[I].w[2], ga[I].w[3]};
-#pragma unroll
-          for (int J = 0; J < 4; ++J) {
-            const u32x4 b = {xb[J].w[0], xb[J].w[1], xb[J].w[2], xb[J].w[3]};
-            dmb[I][J] = mfma32k<XT>(a, b, dmb[I][J]);
-          }
-        }
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          float sa = 0.0f, sp = 0.0f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            sa = fmaf(dyc[e], xb[I].get(e), sa);
-            sp = fmaf(ync[e], ga[I].get(e), sp);
-          }
-          dAp[I] += sa;
-          dPp[I] += sp;
-        }
-      }
-      u32x4 bg[2][8];
-      load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 0, bg[0]);
-      load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 1, bg[1]);
-      asm volatile("" ::: "memory");
 #pragma unroll
       for (int J = 0; J < 4; ++J) {
         u32x4 amt[2][3];
@@ -1579,11 +1574,11 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
           if (v & 1) rows.put(v >> 1, even, acc);
           else even = acc;
         }
-        const uint32_t lo = FULL ? lane_out : opaque_u32(lane_out);
+        const uint32_t lo = opaque_u32(lane_out);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const uint32_t row = (uint32_t)(16 * J + k) * rowb;
-          rows.store_buf(k, rdx, FULL ? lo : lo + row, FULL ? sob + row : sob);
+          rows.store_buf(k, rdx, lo + row, sob);
         }
       }
     }
