@@ -1294,7 +1294,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 
 // ---------------------------------------------------------------------------
 // Backward for 32 < n <= 64, layer-wide parameters, 16-bit x == dout, C a
-// multiple of 128 up to 4096.  A persistent workgroup of W waves walks
+// multiple of 128 up to 8192.  A persistent workgroup of W waves walks
 // tokens; each wave takes SPW slabs of 128 channels.  With
 // dy = dyn inv w - kf y and yn = y inv w (inv and kf the token's RMS
 // scalars), dA_i = sum dy x_i = inv sum x_i dyn w - kf sum x_i y and
@@ -1326,7 +1326,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 // they spill), so rows past n (n < 64) read as zero and their stores are
 // dropped by the buffer range check.
 // ---------------------------------------------------------------------------
-constexpr int kMf64BwdMaxC = 4096;
+constexpr int kMf64BwdMaxC = 8192;  // y, dyn and dw of a token in LDS: 96 KB
 
 template <typename XT, bool RAW, bool FULL>
 __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
@@ -2271,7 +2271,7 @@ int mf32_layer_fwd_single_launch(const Mf32Args& A, int xd, int od, hipStream_t 
 }
 
 // 32 < n <= 64 (mf64_bwd_kernel): the wave count nearest MHC_MF32_WAVES (default 8) dividing the slab
-// count, two workgroups per CU when they fit.
+// count (below C = 512 one wave per slab), as many workgroups per CU as fit.
 int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
   if (A.n <= 32 || A.n > 64 || A.M_ts != 0 || A.C % 128 != 0 || A.C > kMf64BwdMaxC) return 1;
   if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
@@ -2281,10 +2281,9 @@ int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   if (knob(kKnobBwdMfma, 1) == 0) return 1;
   const int S = A.C / 128;
   const int target = std::min(kMf32MaxWaves, std::max(4, knob(kKnobMf32Waves, 8)));
-  int waves = 0;
-  for (int w = 4; w <= kMf32MaxWaves; ++w)
-    if (S % w == 0 && (waves == 0 || std::abs(w - target) < std::abs(waves - target))) waves = w;
-  if (waves == 0) return 1;  // fewer than four slabs, or no split into 4 to 8 waves
+  int waves = 1;
+  for (int w = 1; w <= kMf32MaxWaves; ++w)
+    if (S % w == 0 && std::abs(w - target) < std::abs(waves - target)) waves = w;
   const int spw = S / waves;
   const size_t smem = (size_t)3 * S * 128 * sizeof(float);  // y, dyn and dw
   const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;

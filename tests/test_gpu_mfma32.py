@@ -270,15 +270,16 @@ def _where_unequal(u, v, k=8):
 
 
 @pytest.mark.parametrize("T,n,C", [(64, 64, 512), (300, 64, 1024), (20, 48, 512), (9, 33, 2048), (5, 64, 4096),
-                                   (40, 40, 768)])
+                                   (40, 40, 768), (50, 64, 128), (33, 40, 256), (17, 64, 384), (4, 64, 8192),
+                                   (3, 37, 6272)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("grid", [None, 2])
 def test_mfma64_backward(T, n, C, dt, grid, knobs):
-    """32 < n <= 64 layer-wide backward on MFMA (mf64_bwd_kernel: y, dyn and dx = M^T G on MFMA in two
-    32-stream halves, dM = G X^T in wave-owned 16 x 16 blocks, dA and dP as wave dot products), C a
-    multiple of 128 from 512 to 4096 (4 to 8 waves), against the oracle for every gradient and against
-    the generic backward (MHC_BWD_MFMA=0); with MHC_BWD_GRID=2 each workgroup walks many tokens.  Two
-    runs are bitwise equal."""
+    """32 < n <= 64 layer-wide backward on MFMA (mf64_bwd_kernel: dM = G X^T in 16 x 16 blocks and the
+    parameter dot products before the RMS barrier, dx = M^T G on MFMA in two 32-stream halves after
+    it), C a multiple of 128 from 128 to 8192 (one to eight waves, one to seven slabs per wave),
+    against the oracle for every gradient and against the generic backward (MHC_BWD_MFMA=0); with
+    MHC_BWD_GRID=2 each workgroup walks many tokens.  Two runs are bitwise equal."""
     if grid is not None:
         knobs("MHC_BWD_GRID", grid)
     knobs("MHC_SK_BLK_RECORD", 0)
@@ -307,3 +308,5 @@ def test_mfma64_backward(T, n, C, dt, grid, knobs):
         assert rel_err(np_of(got), ref) < GRAD_TOL
     for got, other in zip(a[1:], gen[1:]):
         assert rel_err(np_of(got), np_of(other)) < 1e-5
+    # the MFMA kernel ran: its parameter sums associate differently from the generic kernel's
+    assert not all(torch.equal(u, v) for u, v in zip(a[1:], gen[1:]))
