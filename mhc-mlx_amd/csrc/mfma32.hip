@@ -532,24 +532,28 @@ __global__ __launch_bounds__(512) void mf32_fwd_loop_kernel(Mf32Args A, int spw)
 }
 
 // ---------------------------------------------------------------------------
-// Forward for 32 < n <= 64, layer-wide parameters: the loop kernel above
-// with the streams in two halves of 32.  Per slab the lane loads streams
+// Forward for 32 < n <= 64, layer-wide or per-token parameters: the loop
+// kernel above with the streams in two halves of 32.  Per slab the lane loads streams
 // 32h + 8q .. 32h + 8q + 7 (h = 0, 1) of channels 8r .. 8r + 7 and
 // transposes each half into B operands, so every contraction over streams
 // is two chained MFMAs (K = 32 each): y = a^T X as before, and the mix in
 // four 16-row blocks of M (rows 16I + r as the A operand, output rows
 // 16I + 4q + k in D).  The split operands of a, M (two halves, four row
 // blocks: 30 words of 16 bytes per lane) live in LDS and are read at each
-// use.  For n < 64 the row part of each stream's offset is in the lane
+// use.  Per-token parameters (PT): each lane splits the token's a into its
+// own operands before the slab pass, and the workgroup splits the token's M
+// (512 tasks of 8 values) and p into LDS buffers of the token's parity,
+// read after the RMS barrier; a buffer is written again two tokens later,
+// after every wave has passed the next token's barrier.  For n < 64 the row part of each stream's offset is in the lane
 // offset, so rows past n read as zero and their stores are dropped.
 // ---------------------------------------------------------------------------
-template <typename XT, typename OT, bool RAW, bool FULL>
+template <typename XT, typename OT, bool RAW, bool FULL, bool PT>
 __global__ __launch_bounds__(512) void mf64_fwd_loop_kernel(Mf32Args A, int spw) {
   extern __shared__ float4 s_y4[];  // [S][16 r][8 channels]
   float* const s_y = reinterpret_cast<float*>(s_y4);
   __shared__ float s_red[2][16];
-  __shared__ u32x4 s_aa[2][3][64], s_am[4][2][3][64];
-  __shared__ float s_pv[64];
+  __shared__ u32x4 s_aa[PT ? 1 : 2][3][64], s_am[PT ? 2 : 1][4][2][3][64];
+  __shared__ float s_pv[PT ? 2 : 1][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -565,7 +569,7 @@ __global__ __launch_bounds__(512) void mf64_fwd_loop_kernel(Mf32Args A, int spw)
   const uint32_t tokb = (uint32_t)(nC * kEs), otokb = (uint32_t)(nC * kOs);
 
   // split operands, written by wave 0 (one (h) or (I, h) block at a time)
-  if (wave == 0) {
+  if (!PT && wave == 0) {
     u32x4 sp[3];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -577,7 +581,7 @@ __global__ __launch_bounds__(512) void mf64_fwd_loop_kernel(Mf32Args A, int spw)
       }
       split3x8<XT>(av, sp);
 #pragma unroll
-      for (int e = 0; e < 3; ++e) s_aa[h][e][lane] = sp[e];
+      for (int e = 0; e < 3; ++e) s_aa[PT ? 0 : h][e][lane] = sp[e];
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
         const int row = 16 * I + r;
@@ -589,10 +593,10 @@ __global__ __launch_bounds__(512) void mf64_fwd_loop_kernel(Mf32Args A, int spw)
         }
         split3x8<XT>(mv, sp);
 #pragma unroll
-        for (int e = 0; e < 3; ++e) s_am[I][h][e][lane] = sp[e];
+        for (int e = 0; e < 3; ++e) s_am[0][I][h][e][lane] = sp[e];
       }
     }
-    s_pv[lane] = lane < n ? act_post<RAW>(A.hpost[lane]) : 0.0f;
+    s_pv[0][lane] = lane < n ? act_post<RAW>(A.hpost[lane]) : 0.0f;
   }
   __syncthreads();
 
@@ -611,6 +615,35 @@ __global__ __launch_bounds__(512) void mf64_fwd_loop_kernel(Mf32Args A, int spw)
                                        FULL ? sb + hb + (uint32_t)e * rowb : sb);
       transpose8<XT>(xr, b);
     };
+    const int pb = PT ? (it & 1) : 0;
+    u32x4 ta[2][3];  // PT: the token's a, split per lane
+    if constexpr (PT) {
+      const float* Mt = A.M + t * A.M_ts;
+      const float* hp = A.hpre + t * A.h_ts;
+      const float* hq = A.hpost + t * A.h_ts;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float av[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = 32 * h + 8 * q + e;
+          av[e] = j < n ? act_pre<RAW>(hp[j]) : 0.0f;
+        }
+        split3x8<XT>(av, ta[h]);
+      }
+      for (int task = tid; task < 4 * 2 * 64; task += blockDim.x) {
+        const int I = task >> 7, h = (task >> 6) & 1, l = task & 63;
+        const int row = 16 * I + (l & 15), j0 = 32 * h + 8 * (l >> 4);
+        float mv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mv[e] = (row < n && j0 + e < n) ? Mt[row * n + j0 + e] : 0.0f;
+        u32x4 sp[3];
+        split3x8<XT>(mv, sp);
+#pragma unroll
+        for (int e = 0; e < 3; ++e) s_am[pb][I][h][e][l] = sp[e];
+      }
+      if (tid < 64) s_pv[pb][tid] = tid < n ? act_post<RAW>(hq[tid]) : 0.0f;
+    }
     float ss = 0.0f;
     for (int s = 0; s < spw; ++s) {
       const int slab = wave * spw + s;
@@ -622,7 +655,7 @@ __global__ __launch_bounds__(512) void mf64_fwd_loop_kernel(Mf32Args A, int spw)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int e = 0; e < 3; ++e) aa[h][e] = s_aa[h][e][lane];
+        for (int e = 0; e < 3; ++e) aa[h][e] = PT ? ta[h][e] : s_aa[PT ? 0 : h][e][lane];
       float y[8];
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
@@ -666,10 +699,10 @@ __global__ __launch_bounds__(512) void mf64_fwd_loop_kernel(Mf32Args A, int spw)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int e = 0; e < 3; ++e) am[h][e] = s_am[I][h][e][lane];
+          for (int e = 0; e < 3; ++e) am[h][e] = s_am[pb][I][h][e][lane];
         float pv[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) pv[k] = s_pv[16 * I + 4 * q + k];
+        for (int k = 0; k < 4; ++k) pv[k] = s_pv[pb][16 * I + 4 * q + k];
         OutRows<OT> rows;
         f32x4 even;
 #pragma unroll
@@ -2226,10 +2259,10 @@ int mf32_fused_fwd_loop(const Mf32Args& A, int xd, int od, hipStream_t s, bool s
   });
 }
 
-// 32 < n <= 64, layer-wide parameters: mf64_fwd_loop_kernel (W waves near MHC_MF32_FWD_WAVES walking
-// the slabs, C a multiple of 128 up to 8192: the y buffer and the split operands fit in LDS).
+// 32 < n <= 64: mf64_fwd_loop_kernel (W waves near MHC_MF32_FWD_WAVES walking the slabs, C a multiple
+// of 128 up to 8192: the y buffer and the split operands fit in LDS), layer-wide or per-token parameters.
 int mf64_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
-  if (A.n <= 32 || A.n > 64 || A.C % 128 != 0 || A.C > 8192 || A.M_ts != 0) return 1;
+  if (A.n <= 32 || A.n > 64 || A.C % 128 != 0 || A.C > 8192) return 1;
   if (od != MHC_DTYPE_F32 && od != xd) return 1;
   if (!aligned(A.x, 16) || !aligned(A.out, 16) || !aligned(A.w, 16)) return 1;
   if (knob(kKnobFwdMfma, 1) == 0) return 1;
@@ -2240,7 +2273,7 @@ int mf64_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
     if (S % w == 0 && std::abs(w - target) < std::abs(waves - target)) waves = w;
   const int spw = S / waves;
   const size_t smem = (size_t)S * 16 * 8 * sizeof(float);
-  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;
+  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64, pt = A.M_ts != 0;
   const int per_cu = knob(kKnobFwdGrid, 8);
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(A.T, (int64_t)device_cu_count() * std::max(per_cu, 1)));
   const dim3 g((unsigned)blocks), b(waves * 64);
@@ -2250,8 +2283,13 @@ int mf64_fused_fwd(const Mf32Args& A, int xd, int od, hipStream_t s) {
       using OT = std::remove_pointer_t<decltype(op)>;
       with_full(full, [&](auto fc) {
         constexpr bool F = decltype(fc)::value;
-        if (raw) hipLaunchKernelGGL((mf64_fwd_loop_kernel<XT, OT, true, F>), g, b, smem, s, A, spw);
-        else hipLaunchKernelGGL((mf64_fwd_loop_kernel<XT, OT, false, F>), g, b, smem, s, A, spw);
+        if (pt) {
+          if (raw) hipLaunchKernelGGL((mf64_fwd_loop_kernel<XT, OT, true, F, true>), g, b, smem, s, A, spw);
+          else hipLaunchKernelGGL((mf64_fwd_loop_kernel<XT, OT, false, F, true>), g, b, smem, s, A, spw);
+        } else {
+          if (raw) hipLaunchKernelGGL((mf64_fwd_loop_kernel<XT, OT, true, F, false>), g, b, smem, s, A, spw);
+          else hipLaunchKernelGGL((mf64_fwd_loop_kernel<XT, OT, false, F, false>), g, b, smem, s, A, spw);
+        }
       });
       MHC_CHECK_LAUNCH("mf64_fwd_loop_kernel");
       return MHC_OK;

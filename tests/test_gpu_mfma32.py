@@ -230,6 +230,39 @@ def test_mfma64_forward(T, n, C, xdt, odt, grid, knobs):
         _ulp_bound(got, ref, odt)
 
 
+@pytest.mark.parametrize("T,n,C", [(5, 64, 128), (40, 64, 512), (7, 48, 384), (3, 64, 1024), (2, 40, 4096),
+                                   (1, 64, 8192), (300, 64, 256), (6, 56, 1280)])
+@pytest.mark.parametrize("xdt,odt", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
+@pytest.mark.parametrize("grid", [None, 1])
+def test_mfma64_forward_per_token(T, n, C, xdt, odt, grid, knobs):
+    """32 < n <= 64 with per-token parameters on MFMA (mf64_fwd_loop_kernel<PT>: the token's a split per
+    lane, its M and p split by the workgroup into LDS buffers of the token's parity), against the
+    oracle; with MHC_FWD_GRID=1 every workgroup walks several tokens, so both buffers are reused.  An
+    fp32 output differs in its last bits from the generic kernel's (MHC_FWD_MFMA=0), so the MFMA kernel
+    ran."""
+    if grid is not None:
+        knobs("MHC_FWD_GRID", grid)
+    g = rng(6500 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), xdt)
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T)
+    xt = dev_tensor(x, xdt)
+    ps = [dev_tensor(v) for v in (hpre, hpost, hres, w)]
+    run = lambda: ops.mhc_layer_forward_dynamic(xt, *ps, sinkhorn_iters=20, eps=EPS,
+                                                output_dtype=None if odt == "f32" else xt.dtype)
+    with torch.no_grad():
+        out = run()
+        knobs("MHC_FWD_MFMA", 0)
+        gen = run()
+    ref = O.mhc_forward_reference(x, hpre, hpost, hres, w, sinkhorn_iters=20, eps=EPS)
+    got = np_of(out)
+    assert rel_err(got, ref) < (1e-5 if odt == "f32" else TOL[odt]), rel_err(got, ref)
+    assert rel_err(got, np_of(gen)) < (1e-5 if odt == "f32" else TOL[odt])
+    if odt != "f32":
+        _ulp_bound(got, ref, odt)
+    else:
+        assert not torch.equal(out, gen)
+
+
 @pytest.mark.parametrize("T,n,C,per_token", [(50, 64, 256, False), (20, 48, 512, False), (33, 33, 96, False),
                                              (300, 40, 128, False), (16, 24, 160, True), (9, 64, 64, True),
                                              (12, 32, 224, True), (7, 20, 40, False)])
