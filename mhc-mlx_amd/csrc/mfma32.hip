@@ -1662,6 +1662,269 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
 }
 
 // ---------------------------------------------------------------------------
+// Backward for 32 < n <= 64 with per-token parameters, 16-bit x == dout, C a
+// multiple of 128 up to 4096.  Each wave takes whole tokens (the wave's
+// global index, then steps of the total wave count), so a token's RMS sums
+// and its dM, dh_pre and dh_post are the wave's own: no barrier and no sum
+// across waves per token.  Per token: a and p of the lane's rows 16 I + r;
+// per slab and 32-channel chunk the pass of the layer-wide kernel before its
+// barrier (x and g rows in the A-operand layout, y and dyn on the VALU with a
+// sum over the 16 lanes r, dM = G X^T on MFMA, the lane partials of
+// sum x_i dyn w, sum x_i y and sum g_i y w, y and dyn to the wave's LDS);
+// the RMS scalars from two wave sums; the token's dM (the wave's 64
+// accumulator registers), dh_pre and dh_post (lane partials summed over the
+// lane groups q, with the activation chain) written out; then per slab, dy
+// and the wave's dw term (its dw is in its LDS), g read in the B-operand
+// layout and dx = M^T G + a dy on MFMA, the token's M^T split per lane for
+// each 16-row block.  At the end the waves' dw are added in wave order into
+// the workgroup's partial row [dw C | 0 .. Cp].
+// ---------------------------------------------------------------------------
+constexpr int kMf64BwdPtMaxC = 4096;  // y, dyn, dw, a and p of a token per wave in LDS: 48.5 KB
+
+template <typename XT, bool RAW, bool FULL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mf64_bwd_pt_kernel(Mf32Args A) {
+  extern __shared__ float s_pt[];  // per wave [y C][dyn C][dw C][a 64][p 64]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int n = FULL ? 64 : A.n;
+  const int C = A.C;
+  const int S = C / 128;
+  float* const s_y = s_pt + (size_t)wave * (3 * C + 128);
+  float* const s_d = s_y + C;
+  float* const s_dw = s_d + C;
+  float* const s_ap = s_dw + C;  // the token's a and p
+  const int64_t nC = (int64_t)n * C;
+  constexpr uint32_t kEs = sizeof(XT);
+  const uint32_t rowb = (uint32_t)C * kEs;
+  const uint32_t lane_in = (uint32_t)(8 * q * C + 8 * r) * kEs;   // stream 8q (+ 32 h + e rows)
+  const uint32_t lane_out = (uint32_t)(4 * q * C + 8 * r) * kEs;  // stream 4q (+ 16 J + k rows)
+  const uint32_t lane_c = (uint32_t)(r * C + 8 * q) * kEs;      // stream r (+ 16 I rows), channel 8q of a chunk
+  const uint32_t tokb = (uint32_t)(nC * kEs);
+  for (int c = lane; c < C; c += 64) s_dw[c] = 0.0f;
+
+  const int64_t nw = (int64_t)gridDim.x * nwaves;
+  for (int64_t t = (int64_t)blockIdx.x * nwaves + wave; t < A.T; t += nw) {
+    const float* Mt = A.M + t * A.M_ts;
+    const float* hp = A.hpre + t * A.h_ts;
+    const float* hq = A.hpost + t * A.h_ts;
+    s_ap[lane] = lane < n ? act_pre<RAW>(hp[lane]) : 0.0f;
+    s_ap[64 + lane] = lane < n ? act_post<RAW>(hq[lane]) : 0.0f;
+    const auto rx = rows_rsrc((const XT*)A.x + t * nC, tokb);
+    const auto rg = rows_rsrc((const XT*)A.g + t * nC, tokb);
+    const auto rdx = rows_rsrc((XT*)A.out + t * nC, tokb);
+    f32x4 dmb[4][4];
+    float ua[4], va[4], wa[4];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      ua[I] = va[I] = wa[I] = 0.0f;
+#pragma unroll
+      for (int J = 0; J < 4; ++J) dmb[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    float ss = 0.0f, sr = 0.0f;
+    for (int slab = 0; slab < S; ++slab) {
+      const uint32_t sob = (uint32_t)slab * 128 * kEs;
+#pragma unroll 1  // unrolled, the chunks' rows and sums spill
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t cb = sob + (uint32_t)(32 * k) * kEs;
+        const uint32_t lc = opaque_u32(lane_c);
+        Vec<XT, 8> ga[4], xb[4];
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          const uint32_t row = (uint32_t)(16 * I) * rowb;
+          buf_load<0>(xb[I], rx, lc + row, cb);
+          buf_load<0>(ga[I], rg, lc + row, cb);
+        }
+        float wc[8];
+        load_w8(A.w + slab * 128 + 32 * k + 8 * q, wc);
+        float a_r[4], p_r[4];  // a and p of the lane's rows 16 I + r
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          a_r[I] = s_ap[16 * I + r];
+          p_r[I] = s_ap[64 + 16 * I + r];
+        }
+        float yc[8], dc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float ys = 0.0f, ds = 0.0f;
+#pragma unroll
+          for (int I = 0; I < 4; ++I) {
+            ys = fmaf(a_r[I], xb[I].get(e), ys);
+            ds = fmaf(p_r[I], ga[I].get(e), ds);
+          }
+          yc[e] = strided_sum<1, 16>(ys);
+          dc[e] = strided_sum<1, 16>(ds);
+        }
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          const u32x4 a = {ga[I].w[0], ga[I].w[1], ga[I].w[2], ga[I].w[3]};
+#pragma unroll
+          for (int J = 0; J < 4; ++J) {
+            const u32x4 b = {xb[J].w[0], xb[J].w[1], xb[J].w[2], xb[J].w[3]};
+            dmb[I][J] = mfma32k<XT>(a, b, dmb[I][J]);
+          }
+        }
+        // the rows are converted again below rather than kept as 64 floats
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            xb[I].w[e] = opaque_u32(xb[I].w[e]);
+            ga[I].w[e] = opaque_u32(ga[I].w[e]);
+          }
+        float dw8[8], yw8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dw8[e] = dc[e] * wc[e];
+          yw8[e] = yc[e] * wc[e];
+          // the 16 lanes r hold the same y and dyn: lane r = 0 counts them
+          ss = fmaf(yc[e], yc[e], ss);
+          sr = fmaf(dw8[e], yc[e], sr);
+        }
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          float su = 0.0f, sv = 0.0f, sw = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float xe = xb[I].get(e);
+            su = fmaf(dw8[e], xe, su);
+            sv = fmaf(yc[e], xe, sv);
+            sw = fmaf(yw8[e], ga[I].get(e), sw);
+          }
+          ua[I] += su;
+          va[I] += sv;
+          wa[I] += sw;
+        }
+        if (r == 0) {
+          float4* y4 = reinterpret_cast<float4*>(s_y + slab * 128 + 32 * k + 8 * q);
+          float4* d4 = reinterpret_cast<float4*>(s_d + slab * 128 + 32 * k + 8 * q);
+          y4[0] = make_float4(yc[0], yc[1], yc[2], yc[3]);
+          y4[1] = make_float4(yc[4], yc[5], yc[6], yc[7]);
+          d4[0] = make_float4(dc[0], dc[1], dc[2], dc[3]);
+          d4[1] = make_float4(dc[4], dc[5], dc[6], dc[7]);
+        }
+      }
+    }
+    ss = wave_sum(r == 0 ? ss : 0.0f);
+    sr = wave_sum(r == 0 ? sr : 0.0f);
+    const float inv = 1.0f / sqrtf(ss / (float)C + A.eps);
+    const float kf = (inv * inv * inv / (float)C) * sr;
+    // the token's dh_pre and dh_post (dA_i = inv sum x_i dyn w - kf sum x_i y, dP_i = inv sum g_i y w) and dM
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      float da = inv * ua[I] - kf * va[I], dp = inv * wa[I];
+      da += shfl_xor(da, 16);
+      da += shfl_xor(da, 32);
+      dp += shfl_xor(dp, 16);
+      dp += shfl_xor(dp, 32);
+      const int i = 16 * I + r;
+      if (q == 0 && i < n) {
+        if constexpr (RAW) {
+          const float av = s_ap[i], pv = s_ap[64 + i];
+          da *= av * (1.0f - av);
+          dp *= pv * (1.0f - 0.5f * pv);
+        }
+        A.dpre_tok[t * n + i] = da;
+        A.dpost_tok[t * n + i] = dp;
+      }
+    }
+    // dM through a buffer resource of the token's n * n values: entries past n get an offset beyond it
+    // (dropped by the range check) rather than a branch each
+    const auto rdm = rows_rsrc(A.dM_tok + t * (int64_t)n * n, (uint32_t)(n * n * sizeof(float)));
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int J = 0; J < 4; ++J)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int row = 16 * I + 4 * q + k, col = 16 * J + r;
+          const uint32_t off = (row < n && col < n) ? (uint32_t)(row * n + col) * 4u : 0x80000000u;
+          // the element as a scalar first: __builtin_bit_cast of a vector element compiled to a cast of
+          // the vector's first element
+          const float v = dmb[I][J][k];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rdm, off, 0, 0);
+        }
+    // dx = M^T G + a dy per slab, in four 16-row blocks
+    for (int slab = 0; slab < S; ++slab) {
+      const float* yp = s_y + (slab * 16 + r) * 8;
+      const float* dp = s_d + (slab * 16 + r) * 8;
+      const float4 y0 = reinterpret_cast<const float4*>(yp)[0], y1 = reinterpret_cast<const float4*>(yp)[1];
+      const float4 d0 = reinterpret_cast<const float4*>(dp)[0], d1 = reinterpret_cast<const float4*>(dp)[1];
+      const float y[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+      const float dyn[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      float wv[8];
+      load_w8(A.w + slab * 128 + 8 * r, wv);
+      float dy[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) dy[v] = dyn[v] * inv * wv[v] - kf * y[v];
+      if (q == 0) {
+        float* pw = s_dw + slab * 128 + 8 * r;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) pw[v] = fmaf(dyn[v], y[v] * inv, pw[v]);
+      }
+      // streams 32h + 8q .. + 7 of channels 8r .. 8r + 7, transposed into B operands
+      u32x4 bg[2][8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t li = opaque_u32(lane_in);
+        Vec<XT, 8> xr[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          buf_load<kBufNt>(xr[e], rg, li + (uint32_t)(32 * h + e) * rowb, (uint32_t)slab * 128 * kEs);
+        transpose8<XT>(xr, bg[h]);
+      }
+      const uint32_t sob = (uint32_t)slab * 128 * kEs;
+#pragma unroll 1
+      for (int J = 0; J < 4; ++J) {
+        u32x4 amt[2][3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int j = 16 * J + r;
+          float mv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int i = 32 * h + 8 * q + e;
+            mv[e] = (i < n && j < n) ? Mt[i * n + j] : 0.0f;
+          }
+          split3x8<XT>(mv, amt[h]);
+        }
+        float a4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a4[k] = s_ap[16 * J + 4 * q + k];
+        OutRows<XT> rows;
+        f32x4 even;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          f32x4 acc = {a4[0] * dy[v], a4[1] * dy[v], a4[2] * dy[v], a4[3] * dy[v]};
+          acc = mfma_split3<XT>(amt[0], bg[0][v], acc);
+          acc = mfma_split3<XT>(amt[1], bg[1][v], acc);
+          if (v & 1) rows.put(v >> 1, even, acc);
+          else even = acc;
+        }
+        const uint32_t lo = opaque_u32(lane_out);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t row = (uint32_t)(16 * J + k) * rowb;
+          rows.store_buf(k, rdx, lo + row, sob);
+        }
+      }
+    }
+  }
+
+  // ---- the workgroup's partial row [dw C | 0 .. Cp]: the waves' dw in wave order
+  __syncthreads();
+  float* prow = A.part + (int64_t)blockIdx.x * A.P;
+  for (int c = tid; c < A.Cp; c += blockDim.x) {
+    float v = 0.0f;
+    if (c < C)
+      for (int w = 0; w < nwaves; ++w) v += s_pt[(size_t)w * (3 * C + 128) + 2 * C + c];
+    prow[c] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Backward for 16 < n <= 32 above C = 1024 (layer-wide): SPW slabs per wave,
 // up to 8 waves.  A token's slabs do not fit in registers across the
 // RMS barrier, so the work splits around it:
@@ -2308,10 +2571,48 @@ int mf32_layer_fwd_single_launch(const Mf32Args& A, int xd, int od, hipStream_t 
   return mf32_fused_fwd_impl(A, xd, od, s, true);
 }
 
+// 32 < n <= 64 with per-token parameters (mf64_bwd_pt_kernel): whole tokens per wave, up to four waves per
+// workgroup as the waves' LDS (12 C + 512 bytes each) allows two workgroups per CU.
+int mf64_fused_bwd_pt(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
+  if (A.n <= 32 || A.n > 64 || A.C % 128 != 0 || A.C > kMf64BwdPtMaxC) return 1;
+  if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
+  if (A.P != A.Cp || A.dM_tok == nullptr || A.dpre_tok == nullptr || A.dpost_tok == nullptr) return 1;
+  if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.out, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
+    return 1;
+  if (knob(kKnobBwdMfma, 1) == 0) return 1;
+  const size_t per_wave = (size_t)(3 * A.C + 128) * sizeof(float);
+  const int waves = (int)std::max<size_t>(1, std::min<size_t>(4, (size_t)(80 * 1024) / per_wave));
+  const size_t smem = waves * per_wave;
+  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;
+  return by_half(xd, [&](auto* xp) {
+    using XT = std::remove_pointer_t<decltype(xp)>;
+    const void* kfn = full ? (raw ? (const void*)mf64_bwd_pt_kernel<XT, true, true>
+                                  : (const void*)mf64_bwd_pt_kernel<XT, false, true>)
+                           : (raw ? (const void*)mf64_bwd_pt_kernel<XT, true, false>
+                                  : (const void*)mf64_bwd_pt_kernel<XT, false, false>);
+    const int occ = occupancy_blocks(kfn, waves * 64, smem);
+    if (occ <= 0) return 1;
+    int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
+    const int grid_pref = knob(kKnobBwdGrid, 0);
+    if (grid_pref > 0) blocks = std::min<int64_t>(gmax, grid_pref);
+    blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, (A.T + waves - 1) / waves));
+    const dim3 g((unsigned)blocks), b(waves * 64);
+    with_full(full, [&](auto fc) {
+      constexpr bool F = decltype(fc)::value;
+      if (raw) hipLaunchKernelGGL((mf64_bwd_pt_kernel<XT, true, F>), g, b, smem, s, A);
+      else hipLaunchKernelGGL((mf64_bwd_pt_kernel<XT, false, F>), g, b, smem, s, A);
+    });
+    MHC_CHECK_LAUNCH("mf64_bwd_pt_kernel");
+    *num_partials = blocks;
+    return MHC_OK;
+  });
+}
+
 // 32 < n <= 64 (mf64_bwd_kernel): the wave count nearest MHC_MF32_WAVES (default 8) dividing the slab
 // count (below C = 512 one wave per slab), as many workgroups per CU as fit.
 int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
-  if (A.n <= 32 || A.n > 64 || A.M_ts != 0 || A.C % 128 != 0 || A.C > kMf64BwdMaxC) return 1;
+  if (A.M_ts != 0) return mf64_fused_bwd_pt(A, xd, gd, gmax, s, num_partials);
+  if (A.n <= 32 || A.n > 64 || A.C % 128 != 0 || A.C > kMf64BwdMaxC) return 1;
   if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
   if (A.P != A.Cp + round_up(A.n * A.n + 2 * A.n, 4)) return 1;
   if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.out, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))

@@ -158,6 +158,47 @@ def test_mfma32_backward_per_token(T, n, C, dt, grid, knobs):
         assert rel_err(np_of(got), np_of(ref)) < 1e-5
 
 
+@pytest.mark.parametrize("T,n,C", [(5, 64, 128), (300, 64, 512), (40, 48, 256), (33, 33, 640), (7, 64, 1024),
+                                   (9, 40, 2048), (3, 64, 4096)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("grid", [None, 3])
+def test_mfma64_backward_per_token(T, n, C, dt, grid, knobs):
+    """Per-token parameters at 32 < n <= 64 on MFMA (mf64_bwd_pt_kernel: whole tokens per wave, the
+    token's dM, dh_pre and dh_post written from the wave's own sums, dx with the token's M^T split per
+    lane), C a multiple of 128 up to 4096: against the oracle (every gradient), against the generic
+    kernel (MHC_BWD_MFMA=0; the two paths' parameter sums differ in their last bits, so the MFMA kernel
+    ran), and bitwise between two runs; with MHC_BWD_GRID=3 each wave walks many tokens."""
+    if grid is not None:
+        knobs("MHC_BWD_GRID", grid)
+    knobs("MHC_SK_BLK_RECORD", 0)
+    g = rng(3600 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C, per_token_B=T)
+
+    def run():
+        xt = dev_tensor(x, dt).requires_grad_(True)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        out = ops.mhc_layer_forward_dynamic(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+        out.backward(dev_tensor(dout, dt))
+        return [xt.grad] + [p.grad for p in ps]
+
+    a, b = run(), run()
+    knobs("MHC_BWD_MFMA", 0)
+    gen = run()
+    torch.cuda.synchronize()
+    for name, u, v in zip(("dx", "dH_pre", "dH_post", "dH_res", "d_w"), a, b):
+        assert torch.equal(u, v), (name, _where_unequal(u, v))
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    _ulp_bound(np_of(a[0]), refs[0], dt)
+    for name, got, ref in zip(("dH_pre", "dH_post", "dH_res", "d_w"), a[1:], refs[1:]):
+        assert rel_err(np_of(got), ref) < GRAD_TOL, (name, rel_err(np_of(got), ref))
+    assert rel_err(np_of(a[0]), np_of(gen[0])) < TOL[dt]
+    for got, ref in zip(a[1:], gen[1:]):
+        assert rel_err(np_of(got), np_of(ref)) < 1e-5
+    assert not all(torch.equal(u, v) for u, v in zip(a[1:], gen[1:]))
+
+
 def test_mfma32_matches_the_generic_kernels(knobs):
     """The MFMA kernels and the VALU kernels they replace agree to rounding on the same inputs."""
     T, n, C = 64, 32, 512
