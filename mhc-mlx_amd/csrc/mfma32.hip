@@ -2571,10 +2571,11 @@ int mf32_layer_fwd_single_launch(const Mf32Args& A, int xd, int od, hipStream_t 
   return mf32_fused_fwd_impl(A, xd, od, s, true);
 }
 
-// 32 < n <= 64 with per-token parameters (mf64_bwd_pt_kernel): whole tokens per wave, up to four waves per
+// 16 < n <= 64 with per-token parameters (mf64_bwd_pt_kernel; the n <= 32 kernel takes C up to 1024): whole
+// tokens per wave, up to four waves per
 // workgroup as the waves' LDS (12 C + 512 bytes each) allows two workgroups per CU.
 int mf64_fused_bwd_pt(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
-  if (A.n <= 32 || A.n > 64 || A.C % 128 != 0 || A.C > kMf64BwdPtMaxC) return 1;
+  if (A.n <= 16 || A.n > 64 || A.C % 128 != 0 || A.C > kMf64BwdPtMaxC) return 1;
   if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
   if (A.P != A.Cp || A.dM_tok == nullptr || A.dpre_tok == nullptr || A.dpost_tok == nullptr) return 1;
   if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.out, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
@@ -2608,11 +2609,12 @@ int mf64_fused_bwd_pt(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream
   });
 }
 
-// 32 < n <= 64 (mf64_bwd_kernel): the wave count nearest MHC_MF32_WAVES (default 8) dividing the slab
+// 16 < n <= 64 (mf64_bwd_kernel; below n = 32 where the n <= 32 kernels do not reach): the wave count
+// nearest MHC_MF32_WAVES (default 8) dividing the slab
 // count (below C = 512 one wave per slab), as many workgroups per CU as fit.
 int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
   if (A.M_ts != 0) return mf64_fused_bwd_pt(A, xd, gd, gmax, s, num_partials);
-  if (A.n <= 32 || A.n > 64 || A.C % 128 != 0 || A.C > kMf64BwdMaxC) return 1;
+  if (A.n <= 16 || A.n > 64 || A.C % 128 != 0 || A.C > kMf64BwdMaxC) return 1;
   if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
   if (A.P != A.Cp + round_up(A.n * A.n + 2 * A.n, 4)) return 1;
   if (!aligned(A.x, 16) || !aligned(A.g, 16) || !aligned(A.out, 16) || !aligned(A.w, 16) || !aligned(A.part, 16))
@@ -2683,9 +2685,20 @@ int mf32_fused_bwd_pt(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream
   });
 }
 
+static int mf32_fused_bwd_lw(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s,
+                             int64_t* num_partials);
+
+// 16 < n <= 32: the n = 32 kernels, and where they do not reach (per-token above C = 1024, layer-wide
+// above C = 5120 for n < 32) the 32 < n <= 64 kernels with the rows past n read as zero.
 int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
   if (A.n > 32) return mf64_fused_bwd(A, xd, gd, gmax, s, num_partials);
-  if (A.M_ts != 0) return mf32_fused_bwd_pt(A, xd, gd, gmax, s, num_partials);
+  const int rc = A.M_ts != 0 ? mf32_fused_bwd_pt(A, xd, gd, gmax, s, num_partials)
+                             : mf32_fused_bwd_lw(A, xd, gd, gmax, s, num_partials);
+  return rc == 1 ? mf64_fused_bwd(A, xd, gd, gmax, s, num_partials) : rc;
+}
+
+static int mf32_fused_bwd_lw(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s,
+                             int64_t* num_partials) {
   if (A.n <= 16 || A.n > 32 || A.M_ts != 0 || A.C % 128 != 0) return 1;
   if (gd != xd || (xd != MHC_DTYPE_BF16 && xd != MHC_DTYPE_F16)) return 1;
   if (A.P != A.Cp + round_up(A.n * A.n + 2 * A.n, 4)) return 1;

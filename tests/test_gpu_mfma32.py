@@ -159,7 +159,9 @@ def test_mfma32_backward_per_token(T, n, C, dt, grid, knobs):
 
 
 @pytest.mark.parametrize("T,n,C", [(5, 64, 128), (300, 64, 512), (40, 48, 256), (33, 33, 640), (7, 64, 1024),
-                                   (9, 40, 2048), (3, 64, 4096)])
+                                   (9, 40, 2048), (3, 64, 4096),
+                                   # 16 < n <= 32 above C = 1024, beyond the n <= 32 per-token kernel
+                                   (6, 32, 2048), (4, 24, 1536), (3, 17, 4096)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("grid", [None, 3])
 def test_mfma64_backward_per_token(T, n, C, dt, grid, knobs):
@@ -345,7 +347,9 @@ def _where_unequal(u, v, k=8):
 
 @pytest.mark.parametrize("T,n,C", [(64, 64, 512), (300, 64, 1024), (20, 48, 512), (9, 33, 2048), (5, 64, 4096),
                                    (40, 40, 768), (50, 64, 128), (33, 40, 256), (17, 64, 384), (4, 64, 8192),
-                                   (3, 37, 6272)])
+                                   (3, 37, 6272),
+                                   # 16 < n < 32 above C = 5120, beyond the n <= 32 layer-wide kernels
+                                   (3, 24, 6144), (2, 20, 8192)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("grid", [None, 2])
 def test_mfma64_backward(T, n, C, dt, grid, knobs):
