@@ -1343,13 +1343,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 //     partials of sum x_i dyn w, sum x_i y and sum g_i y w; the token sums
 //     sum y^2 and sum dyn y w; y and dyn to LDS.  G of the wave's last slab
 //     is also read in the B-operand layout (two 32-stream halves,
-//     transposed) and kept in registers.
+//     transposed) and kept in registers (GL: see below).
 //   RMS barrier.
 //   After it: dA, dP partials += the token's partials times inv and kf;
 //     per slab (the last first), dy per channel and the dw term (the
 //     workgroup's dw is in LDS), then dx = M^T G + a dy on MFMA in four
 //     16-row blocks, stored as 16-byte rows; slabs other than the last read
 //     G again.
+// With one slab per wave and at least two waves (GL), G does not go through
+// HBM twice: the row pieces are also written to the wave's LDS channel-major
+// (16 KB), where the B operands are 16-byte reads after the barrier; the
+// M^T operands are then split per lane at each use (their 24 KB of LDS
+// would leave one workgroup per CU).
 //   The dM blocks (in registers) and the dA, dP partials are the wave's over
 //   its slabs and every token; they are added in wave order at the end.
 // Every LDS value a wave reads after the RMS barrier is one it wrote itself,
@@ -1361,12 +1366,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 // ---------------------------------------------------------------------------
 constexpr int kMf64BwdMaxC = 8192;  // y, dyn and dw of a token in LDS: 96 KB
 
-template <typename XT, bool RAW, bool FULL>
+template <typename XT, bool RAW, bool FULL, bool GL>
 __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
-  extern __shared__ float4 s_yd4[];  // [2][S][16 r][8]: y then dyn (after the RMS barrier: dy then yn); dw [C]
+  // [S][16 r][8] y, then dyn; dw [C]; with GL (one slab per wave) then each wave's G, [128 channels][64 streams]
+  extern __shared__ float4 s_yd4[];
   float* const s_y = reinterpret_cast<float*>(s_yd4);
   __shared__ float s_red[2][2][16];
-  __shared__ u32x4 s_amt[4][2][3][64];
+  __shared__ u32x4 s_amt[GL ? 1 : 4][2][3][64];
   __shared__ float s_a[64], s_p[64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1378,6 +1384,8 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   const int S = C / 128;
   float* const s_d = s_y + S * 128;
   float* const s_dw = s_d + S * 128;  // the workgroup's dw, one owner lane per channel
+  uint16_t* const s_g0 = reinterpret_cast<uint16_t*>(s_dw + C);
+  uint16_t* const s_g = s_g0 + (size_t)wave * 128 * 64;  // GL: the wave's G, channel-major
   const int64_t nC = (int64_t)n * C;
   constexpr uint32_t kEs = sizeof(XT);
   const uint32_t rowb = (uint32_t)C * kEs;
@@ -1386,11 +1394,11 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   const uint32_t tokb = (uint32_t)(nC * kEs);
   float* prow = A.part + (int64_t)blockIdx.x * A.P;
 
-  // parameters: M^T split once by wave 0 into A operands; a and p
+  // parameters: M^T split once by wave 0 into A operands (GL: per lane at each use); a and p
   if (wave == 0) {
     u32x4 sp[3];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < (GL ? 0 : 2); ++h) {
 #pragma unroll
       for (int J = 0; J < 4; ++J) {
         const int j = 16 * J + r;
@@ -1402,7 +1410,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
         }
         split3x8<XT>(mv, sp);
 #pragma unroll
-        for (int e = 0; e < 3; ++e) s_amt[J][h][e][lane] = sp[e];
+        for (int e = 0; e < 3; ++e) s_amt[GL ? 0 : J][h][e][lane] = sp[e];
       }
     }
     s_a[lane] = lane < n ? act_pre<RAW>(A.hpre[lane]) : 0.0f;
@@ -1460,7 +1468,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     for (int s = 0; s < spw; ++s) {
       const int slab = wave * spw + s;
       const uint32_t sob = (uint32_t)slab * 128 * kEs;
-      if (s == spw - 1) {
+      if (!GL && s == spw - 1) {
         load_half(std::integral_constant<int, 0>{}, rg, slab, 0, bg[0]);
         load_half(std::integral_constant<int, 0>{}, rg, slab, 1, bg[1]);
       }
@@ -1497,6 +1505,15 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
             const u32x4 b = {xb[J].w[0], xb[J].w[1], xb[J].w[2], xb[J].w[3]};
             dmb[I][J] = mfma32k<XT>(a, b, dmb[I][J]);
           }
+        }
+        if constexpr (GL) {
+          // G to the wave's LDS, channel-major: element e of the piece is channel 32 k + 8 q + e of
+          // stream 16 I + r (the B-operand reads after the barrier take 8 streams of a channel at once)
+#pragma unroll
+          for (int I = 0; I < 4; ++I)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              s_g[(32 * k + 8 * q + e) * 64 + 16 * I + r] = (uint16_t)(ga[I].w[e >> 1] >> (16 * (e & 1)));
         }
         // the rows are converted again below rather than kept as 64 floats
 #pragma unroll
@@ -1581,19 +1598,40 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
 #pragma unroll
         for (int v = 0; v < 8; ++v) pw[v] = fmaf(dyn[v], y[v] * inv, pw[v]);
       }
-      if (s != spw - 1) {
+      if constexpr (GL) {
+        // streams 32 h + 8 q .. + 7 of channel 8 r + v: the B operands, from the wave's LDS
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            bg[h][v] = *reinterpret_cast<const u32x4*>(s_g + (8 * r + v) * 64 + 32 * h + 8 * q);
+      } else if (s != spw - 1) {
         load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 0, bg[0]);
         load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 1, bg[1]);
         asm volatile("" ::: "memory");
       }
       const uint32_t sob = (uint32_t)slab * 128 * kEs;
-#pragma unroll
+#pragma unroll 1
       for (int J = 0; J < 4; ++J) {
         u32x4 amt[2][3];
+        if constexpr (GL) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+          for (int h = 0; h < 2; ++h) {
+            const int j = 16 * J + r;
+            float mv[8];
 #pragma unroll
-          for (int e = 0; e < 3; ++e) amt[h][e] = s_amt[J][h][e][lane];
+            for (int e = 0; e < 8; ++e) {
+              const int i = 32 * h + 8 * q + e;
+              mv[e] = (i < n && j < n) ? A.M[i * n + j] : 0.0f;
+            }
+            split3x8<XT>(mv, amt[h]);
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 3; ++e) amt[h][e] = s_amt[J][h][e][lane];
+        }
         float a4[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) a4[k] = s_a[16 * J + 4 * q + k];
@@ -1627,8 +1665,9 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     dPp[I] += shfl_xor(dPp[I], 32);
   }
   __syncthreads();
-  float* const s_acc = reinterpret_cast<float*>(&s_amt[0][0][0][0]);  // dM [64][64], dA [64], dP [64]
-  static_assert(sizeof(s_amt) >= (64 * 64 + 128) * sizeof(float), "LDS for the wave-order sums");
+  // dM [64][64], dA [64], dP [64]: in the parameter operands' space, or (GL) the waves' G buffers
+  float* const s_acc = GL ? reinterpret_cast<float*>(s_g0) : reinterpret_cast<float*>(&s_amt[0][0][0][0]);
+  static_assert(GL || sizeof(s_amt) >= (64 * 64 + 128) * sizeof(float), "LDS for the wave-order sums");
   for (int w = 0; w < nwaves; ++w) {
     if (wave == w) {
 #pragma unroll
@@ -2626,12 +2665,17 @@ int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   for (int w = 1; w <= kMf32MaxWaves; ++w)
     if (S % w == 0 && std::abs(w - target) < std::abs(waves - target)) waves = w;
   const int spw = S / waves;
-  const size_t smem = (size_t)3 * S * 128 * sizeof(float);  // y, dyn and dw
+  // one slab per wave and at least two waves: G stays in LDS across the RMS barrier (16 KB per wave)
+  const bool gl = spw == 1 && waves >= 2 && knob(kKnobBwdPipe, 1) != 0;
+  const size_t smem = (size_t)3 * S * 128 * sizeof(float) + (gl ? (size_t)waves * 128 * 64 * sizeof(uint16_t) : 0);
   const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
-    const void* kfn = full ? (raw ? (const void*)mf64_bwd_kernel<XT, true, true> : (const void*)mf64_bwd_kernel<XT, false, true>)
-                           : (raw ? (const void*)mf64_bwd_kernel<XT, true, false> : (const void*)mf64_bwd_kernel<XT, false, false>);
+    const void* kfn;
+    if (gl) kfn = full ? (raw ? (const void*)mf64_bwd_kernel<XT, true, true, true> : (const void*)mf64_bwd_kernel<XT, false, true, true>)
+                       : (raw ? (const void*)mf64_bwd_kernel<XT, true, false, true> : (const void*)mf64_bwd_kernel<XT, false, false, true>);
+    else kfn = full ? (raw ? (const void*)mf64_bwd_kernel<XT, true, true, false> : (const void*)mf64_bwd_kernel<XT, false, true, false>)
+                    : (raw ? (const void*)mf64_bwd_kernel<XT, true, false, false> : (const void*)mf64_bwd_kernel<XT, false, false, false>);
     const int occ = occupancy_blocks(kfn, waves * 64, smem);
     if (occ <= 0) return 1;
     int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
@@ -2641,8 +2685,13 @@ int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     const dim3 g((unsigned)blocks), b(waves * 64);
     with_full(full, [&](auto fc) {
       constexpr bool F = decltype(fc)::value;
-      if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, F>), g, b, smem, s, A, spw);
-      else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, F>), g, b, smem, s, A, spw);
+      if (gl) {
+        if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, F, true>), g, b, smem, s, A, spw);
+        else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, F, true>), g, b, smem, s, A, spw);
+      } else {
+        if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, F, false>), g, b, smem, s, A, spw);
+        else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, F, false>), g, b, smem, s, A, spw);
+      }
     });
     MHC_CHECK_LAUNCH("mf64_bwd_kernel");
     *num_partials = blocks;
