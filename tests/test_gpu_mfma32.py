@@ -158,6 +158,35 @@ def test_mfma32_backward_per_token(T, n, C, dt, grid, knobs):
         assert rel_err(np_of(got), np_of(ref)) < 1e-5
 
 
+@pytest.mark.parametrize("T,n,C", [(64, 64, 512), (30, 40, 256), (9, 64, 1024), (20, 48, 768)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_mfma64_backward_g_through_lds_is_bitwise(T, n, C, dt, knobs):
+    """With one slab per wave the 32 < n <= 64 layer backward keeps G in LDS across the RMS barrier and
+    splits M^T per lane (GL); MHC_BWD_PIPE=0 reads G again from memory and takes M^T from the workgroup's
+    LDS copy.  The operands and every sum are the same, so all gradients are bitwise equal."""
+    knobs("MHC_SK_BLK_RECORD", 0)
+    g = rng(6700 + T + n + C)
+    x = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    dout = to_dtype_np(g.standard_normal((T, n, C)), dt)
+    hpre, hpost, hres, w = params(g, n, C)
+
+    def run():
+        xt = dev_tensor(x, dt).requires_grad_(True)
+        ps = [dev_tensor(v).requires_grad_(True) for v in (hpre, hpost, hres, w)]
+        out = ops.mhc_layer_forward(xt, *ps, sinkhorn_iters=20, eps=EPS, output_dtype=xt.dtype)
+        out.backward(dev_tensor(dout, dt))
+        return [xt.grad] + [p.grad for p in ps]
+
+    a = run()
+    knobs("MHC_BWD_PIPE", 0)
+    b = run()
+    torch.cuda.synchronize()
+    for name, u, v in zip(("dx", "dH_pre", "dH_post", "dH_res", "d_w"), a, b):
+        assert torch.equal(u, v), (name, _where_unequal(u, v))
+    refs = O.mhc_backward_reference(x, hpre, hpost, hres, w, dout, sinkhorn_iters=20, eps=EPS)
+    _ulp_bound(np_of(a[0]), refs[0], dt)
+
+
 @pytest.mark.parametrize("T,n,C", [(5, 64, 128), (300, 64, 512), (40, 48, 256), (33, 33, 640), (7, 64, 1024),
                                    (9, 40, 2048), (3, 64, 4096),
                                    # 16 < n <= 32 above C = 1024, beyond the n <= 32 per-token kernel
