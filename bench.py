@@ -16,7 +16,8 @@ of a 32-token batch (eager module against a graph of the C ABI's forward and
 allocation-free backward); config 3 (per-token H, n=16) fwd+bwd; config 4
 (MHCRewire around Linear(4096, 4096)) with mHC kernel time reported apart
 from the GEMM; residual_add_agg at config 2's shape; n=32 training steps
-(MHCLayer at 8192 x 32 x 512, MHCRewire(Linear(4096, 4096)) at n=32); the
+(MHCLayer at 8192 x 32 x 512, MHCRewire(Linear(4096, 4096)) at n=32); n=64
+training steps (MHCLayer at 4096 x 64 x 512, layer-wide and per-token H); the
 reference's own benchmark scenarios (scripts/record_benchmarks.py: n=32
 forward latency at B=1 and throughput at B=32, MHCLayer and MHCRewire) with
 its published Apple-silicon figures beside them.  cpu_baseline: the
@@ -324,23 +325,33 @@ def _reference_scenarios(dev):
                       "(Apple silicon, context only)", "rows": rows}
 
 
-def _n32_layer_row(dev, T, C, steps, warmup, seed):
-    """One MHCLayer fwd+bwd row at n=32, bf16 I/O, layer-wide parameters."""
+def _layer_row(dev, T, n, C, steps, warmup, seed, per_token=False):
+    """One MHCLayer fwd+bwd row, bf16 I/O; layer-wide parameters, or per-token H (the dynamic forward) with
+    every parameter gradient.  step_hbm_frac counts x, out, dout, dx and, per token, M (read twice), dM and
+    the a, p vectors."""
     import numpy as np
     import torch
 
-    from mhc_mlx_amd import kernel_timer
+    from mhc_mlx_amd import kernel_timer, ops
 
-    n = 32
-    layer = _layer(n, C, dev, np.random.default_rng(seed))
     gen = torch.Generator(dev).manual_seed(seed)
     x = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen).requires_grad_(True)
     dout = torch.randn(T, n, C, device=dev, dtype=torch.bfloat16, generator=gen)
-    params = [layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight]
+    if per_token:
+        ps = [torch.tensor(v, device=dev).requires_grad_(True)
+              for v in _params(np.random.default_rng(seed), n, C, per_token=T)]
 
-    def step():
-        out = layer(x, return_dtype=torch.bfloat16)
-        return torch.autograd.grad(out, [x] + params, dout)
+        def step():
+            out = ops.mhc_layer_forward_dynamic(x, *ps, sinkhorn_iters=20, eps=EPS,
+                                                output_dtype=torch.bfloat16)
+            return torch.autograd.grad(out, [x] + ps, dout)
+    else:
+        layer = _layer(n, C, dev, np.random.default_rng(seed))
+        params = [layer.H_pre_raw, layer.H_post_raw, layer.H_res_raw, layer.rms_weight]
+
+        def step():
+            out = layer(x, return_dtype=torch.bfloat16)
+            return torch.autograd.grad(out, [x] + params, dout)
 
     for _ in range(warmup):
         step()
@@ -348,13 +359,25 @@ def _n32_layer_row(dev, T, C, steps, warmup, seed):
     with kernel_timer() as kt:
         _time_loop(step, steps)
         st = kt.stats()
-    e = T * n * C * 2
-    row = {"workload": f"MHCLayer fwd+bwd, {T} tokens, n=32, C={C}, bf16 I/O", "ms_per_step": ms,
-           "tokens_per_s": T / (ms / 1e3), "step_hbm_frac": 5 * e / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+    nbytes = 5 * T * n * C * 2 + (T * (3 * n * n + 4 * n) * 4 if per_token else 0)
+    kind = "per-token H" if per_token else "layer-wide H"
+    row = {"workload": f"MHCLayer fwd+bwd, {T} tokens, n={n}, C={C}, {kind}, bf16 I/O", "ms_per_step": ms,
+           "tokens_per_s": T / (ms / 1e3), "step_hbm_frac": nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
            "kernels_us": {k: round(v["mean_ms"] * 1e3, 1) for k, v in st.items()}}
-    del x, dout, layer
+    del x, dout, step
     torch.cuda.empty_cache()
     return row
+
+
+def _n32_layer_row(dev, T, C, steps, warmup, seed):
+    """One MHCLayer fwd+bwd row at n=32, bf16 I/O, layer-wide parameters."""
+    return _layer_row(dev, T, 32, C, steps, warmup, seed)
+
+
+def _n64_training(dev, steps=20, warmup=20):
+    """n=64 training steps, 4096 x 64 x 512 bf16: MHCLayer with layer-wide H, and per-token H."""
+    return {"layer": _layer_row(dev, 4096, 64, 512, steps, warmup, 10),
+            "layer_per_token": _layer_row(dev, 4096, 64, 512, steps, warmup, 11, per_token=True)}
 
 
 def _n32_training(dev, steps=20, warmup=20):
@@ -665,6 +688,8 @@ def main() -> int:
         result["residual_add_agg"] = _residual(dev, 10, 3)
         torch.cuda.empty_cache()
         result["n32"] = _n32_training(dev)
+        torch.cuda.empty_cache()
+        result["n64"] = _n64_training(dev)
         torch.cuda.empty_cache()
         result["reference_scenarios"] = _reference_scenarios(dev)
         torch.cuda.empty_cache()
