@@ -91,6 +91,7 @@ const char* const kKnobNames[kNumKnobs] = {
     "MHC_RES_GRID", "MHC_MIX_FWD_GRID", "MHC_MIX_BWD_GRID", "MHC_SCALE_FWD_GRID", "MHC_SCALE_BWD_GRID",
     "MHC_BWD_PIPE", "MHC_MIX32", "MHC_MF32_WAVES", "MHC_SK_BLK_RECORD", "MHC_MF32_FWD_LOOP",
     "MHC_MF32_FWD_WAVES", "MHC_FWD_PIPE", "MHC_SCALE_FWD_FLAT", "MHC_SCALE_BWD_FLAT", "MHC_GEN_MFMA",
+    "MHC_SK_WG",
 };
 std::atomic<int> g_knobs[kNumKnobs];
 

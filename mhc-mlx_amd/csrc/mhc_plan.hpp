@@ -79,7 +79,7 @@ enum Knob : int {
   kKnobSk16, kKnobSk16Cpl, kKnobSk16Record,
   kKnobResGrid, kKnobMixFwdGrid, kKnobMixBwdGrid, kKnobScaleFwdGrid, kKnobScaleBwdGrid,
   kKnobBwdPipe, kKnobMix32, kKnobMf32Waves, kKnobSkBlkRecord, kKnobFwdLoop, kKnobMf32FwdWaves,
-  kKnobFwdPipe, kKnobScaleFwdFlat, kKnobScaleBwdFlat, kKnobGenMfma,
+  kKnobFwdPipe, kKnobScaleFwdFlat, kKnobScaleBwdFlat, kKnobGenMfma, kKnobSkWg,
   kNumKnobs
 };
 

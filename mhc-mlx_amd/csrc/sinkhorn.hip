@@ -86,6 +86,264 @@ __global__ __launch_bounds__(kSkThreads) void sinkhorn_blk_fwd_kernel(const floa
     sk_fwd_blk<NP, REC>(logits + m * nn, out + m * nn, n, iters, eps, lane, REC ? rec + m * per_matrix : nullptr);
 }
 
+// ---------------------------------------------------------------------------
+// One 32 < n <= 64 matrix per workgroup of four waves, for few matrices (a
+// layer-wide projection, MHCRewire's): one wave per matrix runs every
+// instruction of an iteration's dependent chain itself, four waves a quarter
+// of them.  Wave w holds rows 16 w .. 16 w + 15; lane (rq = lane / 8,
+// cq = lane % 8) rows 16 w + 2 rq and + 1, columns 8 cq .. 8 cq + 7.  Row
+// sums stay in the wave (the 8 lanes of a row, DPP); a column sum adds the
+// wave's lanes of the column (stride 8), then the four waves' partials from
+// LDS in wave order: one barrier per iteration, the partials double-buffered
+// by the iteration's parity.  The VJP state has the block layout's format
+// (sk_blk_state_floats(64, iters) floats per matrix: row vectors by the row's
+// lane cq = 0, column vectors by wave 0's lanes rq = 0), so a record from
+// this forward serves this VJP; the values differ from the one-wave kernel's
+// in summation order, so forward and VJP choose the same kernel family.
+// ---------------------------------------------------------------------------
+constexpr int kSkWgWaves = 4;
+constexpr int kSkWgMaxStateBytes = 48 * 1024;  // the recomputing VJP's state in LDS: up to 32 iterations
+
+struct SkWgLane {
+  int lane, w, rq, cq, r0, c0;
+};
+
+MHC_DEV SkWgLane sk_wg_lane() {
+  SkWgLane L;
+  L.lane = threadIdx.x & 63;
+  L.w = threadIdx.x >> 6;
+  L.rq = L.lane >> 3;
+  L.cq = L.lane & 7;
+  L.r0 = 16 * L.w + 2 * L.rq;
+  L.c0 = 8 * L.cq;
+  return L;
+}
+
+// cs: the lane's partial sums of its 8 columns over its two rows -> the column sums over every row.
+MHC_DEV void sk_wg_colsum(float (&cs)[8], float (*s_cs)[kSkWgWaves][64], int par, const SkWgLane& L) {
+#pragma unroll
+  for (int b = 0; b < 8; ++b) cs[b] = strided_sum<8, 64>(cs[b]);
+  if (L.rq == 0) {
+    float4* d = reinterpret_cast<float4*>(&s_cs[par][L.w][L.c0]);
+    d[0] = make_float4(cs[0], cs[1], cs[2], cs[3]);
+    d[1] = make_float4(cs[4], cs[5], cs[6], cs[7]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < 8; ++b) cs[b] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kSkWgWaves; ++w) {
+    const float4* src = reinterpret_cast<const float4*>(&s_cs[par][w][L.c0]);
+    const float4 u = src[0], v = src[1];
+    cs[0] += u.x; cs[1] += u.y; cs[2] += u.z; cs[3] += u.w;
+    cs[4] += v.x; cs[5] += v.y; cs[6] += v.z; cs[7] += v.w;
+  }
+}
+
+// exp(H - rowmax) of the lane's 2 x 8 block (0 outside the matrix) and the row-maximum ties (bit 8a + b).
+MHC_DEV uint32_t sk_wg_load_exp(const float* __restrict__ H, int n, const SkWgLane& L, float (&K)[2][8]) {
+  uint32_t tie = 0;
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    float hv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool v = L.r0 + a < n && L.c0 + b < n;
+      const float h = H[v ? (L.r0 + a) * n + L.c0 + b : 0];
+      hv[b] = v ? h : -INFINITY;
+      mx = fmaxf(mx, hv[b]);
+    }
+    mx = group_max<8>(mx);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool v = L.r0 + a < n && L.c0 + b < n;
+      K[a][b] = v ? expf(hv[b] - mx) : 0.0f;
+      if (v && hv[b] == mx) tie |= 1u << (8 * a + b);
+    }
+  }
+  return tie;
+}
+
+// `iters` iterations on the lane's block P (the block layout's arithmetic per element: row step, then
+// column step, masks and state as sk_blk_iterate); par counts the workgroup's column-sum rounds.
+template <bool REC>
+MHC_DEV void sk_wg_iterate(float (&P)[2][8], int n, int iters, float eps, const SkWgLane& L,
+                           float (*s_cs)[kSkWgWaves][64], int& par, float* st) {
+  float Rc[2] = {1.0f, 1.0f}, Cc[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) Cc[b] = 1.0f;
+  for (int it = 0; it < iters; ++it) {
+    float rsc[2], rf[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      float s = P[a][0];
+#pragma unroll
+      for (int b = 1; b < 8; ++b) s += P[a][b];
+      s = group_sum<8>(s);
+      const bool ok = L.r0 + a < n && s > eps;
+      rsc[a] = ok ? sk_rcp(s) : 1.0f;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) P[a][b] *= rsc[a];
+      if (REC) {
+        rf[a] = ok ? Rc[a] * rsc[a] * rsc[a] : 0.0f;
+        Rc[a] *= rsc[a];
+      }
+    }
+    float cs[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) cs[b] = P[0][b] + P[1][b];
+    sk_wg_colsum(cs, s_cs, par, L);
+    par ^= 1;
+    float csc[8], cf[8], Cp[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool ok = L.c0 + b < n && cs[b] > eps;
+      csc[b] = ok ? sk_rcp(cs[b]) : 0.0f;
+      P[0][b] *= csc[b];
+      P[1][b] *= csc[b];
+      if (REC) {
+        Cp[b] = Cc[b];
+        cf[b] = ok ? Cc[b] * csc[b] * csc[b] : 0.0f;
+        Cc[b] *= csc[b];
+      }
+    }
+    if (REC) {
+      float* sti = st + (int64_t)it * kSkBlkStateVecs * 64;
+      if (L.cq == 0) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          sti[L.r0 + a] = Rc[a];
+          sti[2 * 64 + L.r0 + a] = rsc[a];
+          sti[3 * 64 + L.r0 + a] = rf[a];
+        }
+      }
+      if (L.w == 0 && L.rq == 0) {
+        sk_blk_st_store<8>(sti + 64 + L.c0, Cp);
+        sk_blk_st_store<8>(sti + 4 * 64 + L.c0, csc);
+        sk_blk_st_store<8>(sti + 5 * 64 + L.c0, cf);
+      }
+    }
+  }
+}
+
+template <bool REC>
+__global__ __launch_bounds__(kSkWgWaves * 64) void sinkhorn_wg_fwd_kernel(const float* __restrict__ logits,
+                                                                          float* __restrict__ out, int64_t batch,
+                                                                          int n, int iters, float eps,
+                                                                          float* __restrict__ rec) {
+  __shared__ __align__(16) float s_cs[2][kSkWgWaves][64];
+  const SkWgLane L = sk_wg_lane();
+  const int64_t nn = (int64_t)n * n;
+  const int64_t per_matrix = sk_blk_state_floats(64, iters);
+  int par = 0;
+  for (int64_t m = blockIdx.x; m < batch; m += gridDim.x) {
+    float P[2][8];
+    sk_wg_load_exp(logits + m * nn, n, L, P);
+    sk_wg_iterate<REC>(P, n, iters, eps, L, s_cs, par, REC ? rec + m * per_matrix : nullptr);
+    float* o = out + m * nn;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        if (L.r0 + a < n && L.c0 + b < n) o[(L.r0 + a) * n + L.c0 + b] = P[a][b];
+  }
+}
+
+// VJP: RECORDED reads the forward's record where it lies; otherwise the iterations are recomputed into
+// LDS first (at most kSkWgMaxStateBytes).  Reverse step k (column step, then row step):
+//   Gd = csc Gd - cf * sum_rows(Gd K R_k),  Gd = rsc Gd - rf * sum_cols(Gd K C_k-1).
+template <bool RECORDED>
+__global__ __launch_bounds__(kSkWgWaves * 64) void sinkhorn_wg_bwd_kernel(const float* __restrict__ logits,
+                                                                          const float* __restrict__ dM,
+                                                                          float* __restrict__ dlogits,
+                                                                          int64_t batch, int n, int iters,
+                                                                          float eps, const float* __restrict__ rec) {
+  extern __shared__ float4 sk_wg_smem4[];
+  float* const s_st = reinterpret_cast<float*>(sk_wg_smem4);
+  __shared__ __align__(16) float s_cs[2][kSkWgWaves][64];
+  const SkWgLane L = sk_wg_lane();
+  const int64_t nn = (int64_t)n * n;
+  const int64_t per_matrix = sk_blk_state_floats(64, iters);
+  int par = 0;
+  for (int64_t m = blockIdx.x; m < batch; m += gridDim.x) {
+    float K[2][8], Gd[2][8];
+    const uint32_t tie = sk_wg_load_exp(logits + m * nn, n, L, K);
+    const float* st;
+    if constexpr (RECORDED) {
+      st = rec + m * per_matrix;
+    } else {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) Gd[a][b] = K[a][b];
+      sk_wg_iterate<true>(Gd, n, iters, eps, L, s_cs, par, s_st);
+      __syncthreads();  // every lane's state entries before any lane reads them
+      st = s_st;
+    }
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const bool v = L.r0 + a < n && L.c0 + b < n;
+        const float g = dM[m * nn + (v ? (L.r0 + a) * n + L.c0 + b : 0)];
+        Gd[a][b] = v ? g : 0.0f;
+      }
+    for (int it = iters - 1; it >= 0; --it) {
+      const float* sti = st + (int64_t)it * kSkBlkStateVecs * 64;
+      float Rk[2], rsc[2], rf[2], Cp[8], csc[8], cf[8];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        Rk[a] = sti[L.r0 + a];
+        rsc[a] = sti[2 * 64 + L.r0 + a];
+        rf[a] = sti[3 * 64 + L.r0 + a];
+      }
+      sk_blk_st_load<8>(sti + 64 + L.c0, Cp);
+      sk_blk_st_load<8>(sti + 4 * 64 + L.c0, csc);
+      sk_blk_st_load<8>(sti + 5 * 64 + L.c0, cf);
+      float cs[8];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) cs[b] = Gd[0][b] * K[0][b] * Rk[0] + Gd[1][b] * K[1][b] * Rk[1];
+      sk_wg_colsum(cs, s_cs, par, L);
+      par ^= 1;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const float sub = cs[b] * cf[b];
+        Gd[0][b] = csc[b] * Gd[0][b] - sub;
+        Gd[1][b] = csc[b] * Gd[1][b] - sub;
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        float dot = Gd[a][0] * (K[a][0] * Cp[0]);
+#pragma unroll
+        for (int b = 1; b < 8; ++b) dot += Gd[a][b] * (K[a][b] * Cp[b]);
+        const float sub = group_sum<8>(dot) * rf[a];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) Gd[a][b] = rsc[a] * Gd[a][b] - sub;
+      }
+    }
+    // through exp and the row-max shift (the gradient of the max split evenly among tied maxima)
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      float tot = 0.0f, cnt = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        Gd[a][b] *= K[a][b];
+        tot += Gd[a][b];
+        cnt += (tie >> (8 * a + b)) & 1 ? 1.0f : 0.0f;
+      }
+      tot = group_sum<8>(tot);
+      cnt = group_sum<8>(cnt);
+      const float corr = cnt > 0.0f ? tot / cnt : 0.0f;
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        if (L.r0 + a < n && L.c0 + b < n)
+          dlogits[m * nn + (L.r0 + a) * n + L.c0 + b] = Gd[a][b] - ((tie >> (8 * a + b)) & 1 ? corr : 0.0f);
+    }
+    if constexpr (!RECORDED) __syncthreads();  // the state is read before the next matrix writes over it
+  }
+}
+
 // Where the block-layout VJP finds its state.
 enum SkBlkState : int {
   kSkBlkLds = 0,        // recomputed into the wave's LDS
@@ -980,6 +1238,33 @@ SkPlan plan_blk(int64_t batch, int n, int iters, int cus) {
 
 bool use_blk(int n) { return n > 16; }
 
+// 32 < n <= 64 and at most one matrix per CU: one four-wave workgroup per matrix (sinkhorn_wg_*), when
+// the recomputing VJP's state fits its LDS.  Forward and VJP decide alike, so the VJP recomputes the
+// forward's own iterates.  MHC_SK_WG=0 keeps the one-wave block kernels.
+bool use_wg(int64_t batch, int n, int iters) {
+  return n > 32 && batch <= device_cu_count() && knob(kKnobSkWg, 1) != 0 &&
+         (size_t)sk_blk_state_floats(64, iters) * sizeof(float) <= (size_t)kSkWgMaxStateBytes;
+}
+
+void launch_wg_fwd(const float* logits, float* M, int64_t batch, int n, int iters, float eps, float* rec,
+                   hipStream_t s) {
+  const dim3 g((unsigned)batch), b(kSkWgWaves * 64);
+  if (rec != nullptr) hipLaunchKernelGGL((sinkhorn_wg_fwd_kernel<true>), g, b, 0, s, logits, M, batch, n, iters, eps, rec);
+  else hipLaunchKernelGGL((sinkhorn_wg_fwd_kernel<false>), g, b, 0, s, logits, M, batch, n, iters, eps, nullptr);
+}
+
+void launch_wg_bwd(const float* logits, const float* dM, float* dlogits, int64_t batch, int n, int iters,
+                   float eps, const float* rec, hipStream_t s) {
+  const dim3 g((unsigned)batch), b(kSkWgWaves * 64);
+  if (rec != nullptr) {
+    hipLaunchKernelGGL((sinkhorn_wg_bwd_kernel<true>), g, b, 0, s, logits, dM, dlogits, batch, n, iters, eps, rec);
+  } else {
+    const size_t smem = (size_t)sk_blk_state_floats(64, iters) * sizeof(float);
+    hipLaunchKernelGGL((sinkhorn_wg_bwd_kernel<false>), g, b, smem, s, logits, dM, dlogits, batch, n, iters, eps,
+                       nullptr);
+  }
+}
+
 // The first 256-byte boundary at or after p.
 template <typename T>
 T* align256(void* p) {
@@ -1072,6 +1357,11 @@ extern "C" int mhc_sinkhorn_fwd(const float* logits, float* M, int64_t batch, in
     MHC_CHECK_LAUNCH("sinkhorn16_fwd_kernel");
     return MHC_OK;
   }
+  if (use_wg(batch, n, iters)) {
+    launch_wg_fwd(logits, M, batch, n, iters, eps, nullptr, s);
+    MHC_CHECK_LAUNCH("sinkhorn_wg_fwd_kernel");
+    return MHC_OK;
+  }
   if (use_blk(n)) {
     const SkPlan p = plan_blk(batch, n, iters, cus);
     if (p.np == 32) launch_blk_fwd<32>(p, logits, M, batch, n, iters, eps, nullptr, s);
@@ -1145,6 +1435,11 @@ extern "C" int mhc_sinkhorn_bwd(const float* logits, const float* dM, float* dlo
       return MHC_OK;
     }
   }
+  if (use_wg(batch, n, iters)) {
+    launch_wg_bwd(logits, dM, dlogits, batch, n, iters, eps, nullptr, s);
+    MHC_CHECK_LAUNCH("sinkhorn_wg_bwd_kernel");
+    return MHC_OK;
+  }
   if (use_blk(n)) {
     const SkPlan p = plan_blk(batch, n, iters, device_cu_count());
     MHC_CHECK_ARG(workspace_bytes >= p.ws_bytes && (p.ws_bytes == 0 || workspace != nullptr),
@@ -1217,6 +1512,11 @@ extern "C" int mhc_sinkhorn_fwd_record(const float* logits, float* M, void* stat
   MHC_CHECK_ARG(st != nullptr, "state of %zu bytes is smaller than the %zu bytes required", state_bytes,
                 sk_record_bytes(batch, n, iters) + 256);
   hipStream_t s = (hipStream_t)stream;
+  if (use_wg(batch, n, iters)) {
+    launch_wg_fwd(logits, M, batch, n, iters, eps, st, s);
+    MHC_CHECK_LAUNCH("sinkhorn_wg_fwd_kernel");
+    return MHC_OK;
+  }
   if (n > 16) {
     const SkPlan p = plan_blk(batch, n, iters, device_cu_count());
     if (p.np == 32) launch_blk_fwd<32>(p, logits, M, batch, n, iters, eps, st, s);
@@ -1246,6 +1546,11 @@ extern "C" int mhc_sinkhorn_bwd_recorded(const float* logits, const float* dM, f
   MHC_CHECK_ARG(st != nullptr, "state of %zu bytes is smaller than the %zu bytes required", state_bytes,
                 sk_record_bytes(batch, n, iters) + 256);
   hipStream_t s = (hipStream_t)stream;
+  if (use_wg(batch, n, iters)) {
+    launch_wg_bwd(logits, dM, dlogits, batch, n, iters, eps, st, s);
+    MHC_CHECK_LAUNCH("sinkhorn_wg_bwd_kernel");
+    return MHC_OK;
+  }
   if (n > 16) {
     const SkPlan p = plan_blk(batch, n, iters, device_cu_count());
     if (p.np == 32) launch_blk_bwd<32>(p, logits, dM, dlogits, batch, n, iters, eps, nullptr, st, s);
