@@ -392,3 +392,37 @@ def test_sinkhorn16_identity_init_and_bomb():
     Hb = np.full((20, n, n), 100.0, np.float32)
     got = _fwd(Hb, 20, 1e-5)
     assert np.isfinite(got).all() and np.abs(got - 1.0 / n).max() < 1e-6
+
+
+@pytest.mark.parametrize("n,batch,iters", [(64, 1, 20), (48, 7, 1), (33, 2, 0), (64, 3, 32), (40, 1, 5),
+                                           (64, 1, 33)])
+def test_sinkhorn_workgroup_kernels_match_one_wave_kernels(n, batch, iters, knobs):
+    """32 < n <= 64 with at most one matrix per CU runs on one four-wave workgroup per matrix (column sums
+    through LDS; MHC_SK_WG=0 keeps one wave per matrix).  Forward and VJP agree with the one-wave
+    kernels to summation order and with the oracle, with masked rows and columns; above 32 iterations
+    (the recomputed state no longer fits the workgroup's LDS) both sides take the one-wave kernels and
+    agree bitwise."""
+    g = rng(4600 + n + batch + iters)
+    H = (2.0 * g.standard_normal((batch, n, n))).astype(np.float32)
+    H[::2, :, 3] = -40.0
+    H[:, 5, :] = -30.0
+    dM = g.standard_normal((batch, n, n)).astype(np.float32)
+
+    def run():
+        Ht = dev_tensor(H).requires_grad_(True)
+        M = ops.sinkhorn_knopp_hip_autograd(Ht, iters=iters, eps=1e-5)
+        M.backward(dev_tensor(dM))
+        return M.detach(), Ht.grad
+
+    M1, d1 = run()
+    knobs("MHC_SK_WG", 0)
+    M0, d0 = run()
+    torch.cuda.synchronize()
+    if iters > 32:
+        assert torch.equal(M1, M0) and torch.equal(d1, d0)
+    assert rel_err(np_of(M1), np_of(M0), 1.0) < 1e-6
+    assert rel_err(np_of(d1), np_of(d0), 1e-3) < 1e-5
+    rm = O.mixing_matrix_from_logits(H.astype(np.float64), iters=iters, eps=1e-5)
+    assert rel_err(np_of(M1), rm, 1.0) < 1e-5
+    rg = O.sinkhorn_knopp_vjp(H.astype(np.float64), dM, iters=iters, eps=1e-5)
+    assert rel_err(np_of(d1), rg, 1e-3) < 1e-5
