@@ -87,10 +87,9 @@ __global__ __launch_bounds__(kSkThreads) void sinkhorn_blk_fwd_kernel(const floa
 }
 
 // ---------------------------------------------------------------------------
-// One 32 < n <= 64 matrix per workgroup of four waves, for few matrices (a
-// layer-wide projection, MHCRewire's): one wave per matrix runs every
-// instruction of an iteration's dependent chain itself, four waves a quarter
-// of them.  Wave w holds rows 16 w .. 16 w + 15; lane (rq = lane / 8,
+// One 32 < n <= 64 matrix per workgroup of four waves: one wave per matrix
+// runs every instruction of an iteration's dependent chain itself, four
+// waves a quarter of them.  Wave w holds rows 16 w .. 16 w + 15; lane (rq = lane / 8,
 // cq = lane % 8) rows 16 w + 2 rq and + 1, columns 8 cq .. 8 cq + 7.  Row
 // sums stay in the wave (the 8 lanes of a row, DPP); a column sum adds the
 // wave's lanes of the column (stride 8), then the four waves' partials from
@@ -1238,24 +1237,29 @@ SkPlan plan_blk(int64_t batch, int n, int iters, int cus) {
 
 bool use_blk(int n) { return n > 16; }
 
-// 32 < n <= 64 and at most one matrix per CU: one four-wave workgroup per matrix (sinkhorn_wg_*), when
-// the recomputing VJP's state fits its LDS.  Forward and VJP decide alike, so the VJP recomputes the
-// forward's own iterates.  MHC_SK_WG=0 keeps the one-wave block kernels.
+// 32 < n <= 64: one four-wave workgroup per matrix (sinkhorn_wg_*), when the recomputing VJP's state
+// fits its LDS.  Forward and VJP decide alike, so the VJP recomputes the forward's own iterates.  A
+// single matrix is latency-bound on one wave; batched, the one-wave kernels hold one wave per SIMD
+// (their 64 elements per lane take every register) and the workgroups several.  MHC_SK_WG=0 keeps the
+// one-wave block kernels.
 bool use_wg(int64_t batch, int n, int iters) {
-  return n > 32 && batch <= device_cu_count() && knob(kKnobSkWg, 1) != 0 &&
+  (void)batch;
+  return n > 32 && knob(kKnobSkWg, 1) != 0 &&
          (size_t)sk_blk_state_floats(64, iters) * sizeof(float) <= (size_t)kSkWgMaxStateBytes;
 }
 
+dim3 wg_grid(int64_t batch) { return dim3((unsigned)std::min<int64_t>(batch, (int64_t)device_cu_count() * 16)); }
+
 void launch_wg_fwd(const float* logits, float* M, int64_t batch, int n, int iters, float eps, float* rec,
                    hipStream_t s) {
-  const dim3 g((unsigned)batch), b(kSkWgWaves * 64);
+  const dim3 g = wg_grid(batch), b(kSkWgWaves * 64);
   if (rec != nullptr) hipLaunchKernelGGL((sinkhorn_wg_fwd_kernel<true>), g, b, 0, s, logits, M, batch, n, iters, eps, rec);
   else hipLaunchKernelGGL((sinkhorn_wg_fwd_kernel<false>), g, b, 0, s, logits, M, batch, n, iters, eps, nullptr);
 }
 
 void launch_wg_bwd(const float* logits, const float* dM, float* dlogits, int64_t batch, int n, int iters,
                    float eps, const float* rec, hipStream_t s) {
-  const dim3 g((unsigned)batch), b(kSkWgWaves * 64);
+  const dim3 g = wg_grid(batch), b(kSkWgWaves * 64);
   if (rec != nullptr) {
     hipLaunchKernelGGL((sinkhorn_wg_bwd_kernel<true>), g, b, 0, s, logits, dM, dlogits, batch, n, iters, eps, rec);
   } else {

@@ -395,10 +395,10 @@ def test_sinkhorn16_identity_init_and_bomb():
 
 
 @pytest.mark.parametrize("n,batch,iters", [(64, 1, 20), (48, 7, 1), (33, 2, 0), (64, 3, 32), (40, 1, 5),
-                                           (64, 1, 33)])
+                                           (64, 1, 33), (64, 5000, 20)])
 def test_sinkhorn_workgroup_kernels_match_one_wave_kernels(n, batch, iters, knobs):
-    """32 < n <= 64 with at most one matrix per CU runs on one four-wave workgroup per matrix (column sums
-    through LDS; MHC_SK_WG=0 keeps one wave per matrix).  Forward and VJP agree with the one-wave
+    """32 < n <= 64 runs on one four-wave workgroup per matrix (column sums through LDS; MHC_SK_WG=0
+    keeps one wave per matrix).  Forward and VJP agree with the one-wave
     kernels to summation order and with the oracle, with masked rows and columns; above 32 iterations
     (the recomputed state no longer fits the workgroup's LDS) both sides take the one-wave kernels and
     agree bitwise."""
