@@ -1701,8 +1701,9 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward for 32 < n <= 64 with per-token parameters, 16-bit x == dout, C a
-// multiple of 128 up to 4096.  Each wave takes whole tokens (the wave's
+// Backward for 16 < n <= 64 with per-token parameters, 16-bit x == dout, C a
+// multiple of 128 up to 4096; NB 16-row blocks of streams (4, or 2 for
+// n <= 32).  Each wave takes whole tokens (the wave's
 // global index, then steps of the total wave count), so a token's RMS sums
 // and its dM, dh_pre and dh_post are the wave's own: no barrier and no sum
 // across waves per token.  Per token: a and p of the lane's rows 16 I + r;
@@ -1720,8 +1721,9 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
 // ---------------------------------------------------------------------------
 constexpr int kMf64BwdPtMaxC = 4096;  // y, dyn, dw, a and p of a token per wave in LDS: 48.5 KB
 
-template <typename XT, bool RAW, bool FULL>
+template <typename XT, bool RAW, bool FULL, int NB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mf64_bwd_pt_kernel(Mf32Args A) {
+  constexpr int NH = NB / 2;  // 32-stream halves
   extern __shared__ float s_pt[];  // per wave [y C][dyn C][dw C][a 64][p 64]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1754,13 +1756,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const auto rx = rows_rsrc((const XT*)A.x + t * nC, tokb);
     const auto rg = rows_rsrc((const XT*)A.g + t * nC, tokb);
     const auto rdx = rows_rsrc((XT*)A.out + t * nC, tokb);
-    f32x4 dmb[4][4];
-    float ua[4], va[4], wa[4];
+    f32x4 dmb[NB][NB];
+    float ua[NB], va[NB], wa[NB];
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
+    for (int I = 0; I < NB; ++I) {
       ua[I] = va[I] = wa[I] = 0.0f;
 #pragma unroll
-      for (int J = 0; J < 4; ++J) dmb[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int J = 0; J < NB; ++J) dmb[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     float ss = 0.0f, sr = 0.0f;
     for (int slab = 0; slab < S; ++slab) {
@@ -1769,18 +1771,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       for (int k = 0; k < 4; ++k) {
         const uint32_t cb = sob + (uint32_t)(32 * k) * kEs;
         const uint32_t lc = opaque_u32(lane_c);
-        Vec<XT, 8> ga[4], xb[4];
+        Vec<XT, 8> ga[NB], xb[NB];
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
+        for (int I = 0; I < NB; ++I) {
           const uint32_t row = (uint32_t)(16 * I) * rowb;
           buf_load<0>(xb[I], rx, lc + row, cb);
           buf_load<0>(ga[I], rg, lc + row, cb);
         }
         float wc[8];
         load_w8(A.w + slab * 128 + 32 * k + 8 * q, wc);
-        float a_r[4], p_r[4];  // a and p of the lane's rows 16 I + r
+        float a_r[NB], p_r[NB];  // a and p of the lane's rows 16 I + r
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
+        for (int I = 0; I < NB; ++I) {
           a_r[I] = s_ap[16 * I + r];
           p_r[I] = s_ap[64 + 16 * I + r];
         }
@@ -1789,7 +1791,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         for (int e = 0; e < 8; ++e) {
           float ys = 0.0f, ds = 0.0f;
 #pragma unroll
-          for (int I = 0; I < 4; ++I) {
+          for (int I = 0; I < NB; ++I) {
             ys = fmaf(a_r[I], xb[I].get(e), ys);
             ds = fmaf(p_r[I], ga[I].get(e), ds);
           }
@@ -1797,17 +1799,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
           dc[e] = strided_sum<1, 16>(ds);
         }
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
+        for (int I = 0; I < NB; ++I) {
           const u32x4 a = {ga[I].w[0], ga[I].w[1], ga[I].w[2], ga[I].w[3]};
 #pragma unroll
-          for (int J = 0; J < 4; ++J) {
+          for (int J = 0; J < NB; ++J) {
             const u32x4 b = {xb[J].w[0], xb[J].w[1], xb[J].w[2], xb[J].w[3]};
             dmb[I][J] = mfma32k<XT>(a, b, dmb[I][J]);
           }
         }
         // the rows are converted again below rather than kept as 64 floats
 #pragma unroll
-        for (int I = 0; I < 4; ++I)
+        for (int I = 0; I < NB; ++I)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             xb[I].w[e] = opaque_u32(xb[I].w[e]);
@@ -1823,7 +1825,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
           sr = fmaf(dw8[e], yc[e], sr);
         }
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
+        for (int I = 0; I < NB; ++I) {
           float su = 0.0f, sv = 0.0f, sw = 0.0f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -1852,7 +1854,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const float kf = (inv * inv * inv / (float)C) * sr;
     // the token's dh_pre and dh_post (dA_i = inv sum x_i dyn w - kf sum x_i y, dP_i = inv sum g_i y w) and dM
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
+    for (int I = 0; I < NB; ++I) {
       float da = inv * ua[I] - kf * va[I], dp = inv * wa[I];
       da += shfl_xor(da, 16);
       da += shfl_xor(da, 32);
@@ -1873,9 +1875,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     // (dropped by the range check) rather than a branch each
     const auto rdm = rows_rsrc(A.dM_tok + t * (int64_t)n * n, (uint32_t)(n * n * sizeof(float)));
 #pragma unroll
-    for (int I = 0; I < 4; ++I)
+    for (int I = 0; I < NB; ++I)
 #pragma unroll
-      for (int J = 0; J < 4; ++J)
+      for (int J = 0; J < NB; ++J)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int row = 16 * I + 4 * q + k, col = 16 * J + r;
@@ -1904,9 +1906,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         for (int v = 0; v < 8; ++v) pw[v] = fmaf(dyn[v], y[v] * inv, pw[v]);
       }
       // streams 32h + 8q .. + 7 of channels 8r .. 8r + 7, transposed into B operands
-      u32x4 bg[2][8];
+      u32x4 bg[NH][8];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NH; ++h) {
         const uint32_t li = opaque_u32(lane_in);
         Vec<XT, 8> xr[8];
 #pragma unroll
@@ -1916,10 +1918,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       }
       const uint32_t sob = (uint32_t)slab * 128 * kEs;
 #pragma unroll 1
-      for (int J = 0; J < 4; ++J) {
-        u32x4 amt[2][3];
+      for (int J = 0; J < NB; ++J) {
+        u32x4 amt[NH][3];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NH; ++h) {
           const int j = 16 * J + r;
           float mv[8];
 #pragma unroll
@@ -1937,8 +1939,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           f32x4 acc = {a4[0] * dy[v], a4[1] * dy[v], a4[2] * dy[v], a4[3] * dy[v]};
-          acc = mfma_split3<XT>(amt[0], bg[0][v], acc);
-          acc = mfma_split3<XT>(amt[1], bg[1][v], acc);
+#pragma unroll
+          for (int h = 0; h < NH; ++h) acc = mfma_split3<XT>(amt[h], bg[h][v], acc);
           if (v & 1) rows.put(v >> 1, even, acc);
           else even = acc;
         }
@@ -2623,13 +2625,15 @@ int mf64_fused_bwd_pt(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream
   const size_t per_wave = (size_t)(3 * A.C + 128) * sizeof(float);
   const int waves = (int)std::max<size_t>(1, std::min<size_t>(4, (size_t)(80 * 1024) / per_wave));
   const size_t smem = waves * per_wave;
-  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;
+  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64, nb2 = A.n <= 32;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
-    const void* kfn = full ? (raw ? (const void*)mf64_bwd_pt_kernel<XT, true, true>
-                                  : (const void*)mf64_bwd_pt_kernel<XT, false, true>)
-                           : (raw ? (const void*)mf64_bwd_pt_kernel<XT, true, false>
-                                  : (const void*)mf64_bwd_pt_kernel<XT, false, false>);
+    const void* kfn = nb2 ? (raw ? (const void*)mf64_bwd_pt_kernel<XT, true, false, 2>
+                                 : (const void*)mf64_bwd_pt_kernel<XT, false, false, 2>)
+                    : full ? (raw ? (const void*)mf64_bwd_pt_kernel<XT, true, true, 4>
+                                  : (const void*)mf64_bwd_pt_kernel<XT, false, true, 4>)
+                           : (raw ? (const void*)mf64_bwd_pt_kernel<XT, true, false, 4>
+                                  : (const void*)mf64_bwd_pt_kernel<XT, false, false, 4>);
     const int occ = occupancy_blocks(kfn, waves * 64, smem);
     if (occ <= 0) return 1;
     int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
@@ -2637,11 +2641,16 @@ int mf64_fused_bwd_pt(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream
     if (grid_pref > 0) blocks = std::min<int64_t>(gmax, grid_pref);
     blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, (A.T + waves - 1) / waves));
     const dim3 g((unsigned)blocks), b(waves * 64);
-    with_full(full, [&](auto fc) {
-      constexpr bool F = decltype(fc)::value;
-      if (raw) hipLaunchKernelGGL((mf64_bwd_pt_kernel<XT, true, F>), g, b, smem, s, A);
-      else hipLaunchKernelGGL((mf64_bwd_pt_kernel<XT, false, F>), g, b, smem, s, A);
-    });
+    if (nb2) {
+      if (raw) hipLaunchKernelGGL((mf64_bwd_pt_kernel<XT, true, false, 2>), g, b, smem, s, A);
+      else hipLaunchKernelGGL((mf64_bwd_pt_kernel<XT, false, false, 2>), g, b, smem, s, A);
+    } else {
+      with_full(full, [&](auto fc) {
+        constexpr bool F = decltype(fc)::value;
+        if (raw) hipLaunchKernelGGL((mf64_bwd_pt_kernel<XT, true, F, 4>), g, b, smem, s, A);
+        else hipLaunchKernelGGL((mf64_bwd_pt_kernel<XT, false, F, 4>), g, b, smem, s, A);
+      });
+    }
     MHC_CHECK_LAUNCH("mf64_bwd_pt_kernel");
     *num_partials = blocks;
     return MHC_OK;
@@ -2737,12 +2746,22 @@ int mf32_fused_bwd_pt(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream
 static int mf32_fused_bwd_lw(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s,
                              int64_t* num_partials);
 
-// 16 < n <= 32: the n = 32 kernels, and where they do not reach (per-token above C = 1024, layer-wide
-// above C = 5120 for n < 32) the 32 < n <= 64 kernels with the rows past n read as zero.
+// 16 < n <= 32, layer-wide parameters: the n = 32 kernels, and where they do not reach (above C = 5120
+// for n < 32) the 32 < n <= 64 kernel with the rows past n read as zero.  Per-token parameters: whole
+// tokens per wave (mf64_bwd_pt_kernel with two 16-row blocks); MHC_BWD_LEGACY=1 takes the workgroup-
+// per-token kernel (mf32_bwd_pt_kernel, C up to 1024) first.  Measured, bf16 backward kernel:
+// 8192 x 32 x 512 284 -> 222 us, 4096 x 24 x 512 170 -> 95 us, 2048 x 32 x 1024 111 us both.
 int mf32_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t s, int64_t* num_partials) {
   if (A.n > 32) return mf64_fused_bwd(A, xd, gd, gmax, s, num_partials);
-  const int rc = A.M_ts != 0 ? mf32_fused_bwd_pt(A, xd, gd, gmax, s, num_partials)
-                             : mf32_fused_bwd_lw(A, xd, gd, gmax, s, num_partials);
+  if (A.M_ts != 0) {
+    const bool legacy = knob(kKnobBwdLegacy, 0) == 1;
+    int rc = legacy ? mf32_fused_bwd_pt(A, xd, gd, gmax, s, num_partials)
+                    : mf64_fused_bwd_pt(A, xd, gd, gmax, s, num_partials);
+    if (rc == 1) rc = legacy ? mf64_fused_bwd_pt(A, xd, gd, gmax, s, num_partials)
+                             : mf32_fused_bwd_pt(A, xd, gd, gmax, s, num_partials);
+    return rc;
+  }
+  const int rc = mf32_fused_bwd_lw(A, xd, gd, gmax, s, num_partials);
   return rc == 1 ? mf64_fused_bwd(A, xd, gd, gmax, s, num_partials) : rc;
 }
 

@@ -122,14 +122,18 @@ def _backward_layer_wide(T, n, C, dt, knobs):
                                    (64, 28, 384), (9, 20, 896)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("grid", [None, 3])
-def test_mfma32_backward_per_token(T, n, C, dt, grid, knobs):
-    """Per-token parameters on MFMA (mf32_bwd_pt_kernel: the token's parameters split by wave 0 one token
-    ahead into one of two LDS blocks, the token's dM, dh_pre, dh_post summed across the waves through their
-    slab buffers), C a multiple of 128 up to 1024: against the oracle (every gradient), against the
-    generic kernel (MHC_BWD_MFMA=0), and bitwise between two runs; with MHC_BWD_GRID=3 each workgroup
-    walks many tokens, so both parameter blocks are used."""
+@pytest.mark.parametrize("legacy", [0, 1])
+def test_mfma32_backward_per_token(T, n, C, dt, grid, legacy, knobs):
+    """Per-token parameters at 16 < n <= 32 on MFMA, C a multiple of 128 up to 1024: whole tokens per
+    wave (mf64_bwd_pt_kernel with two 16-row blocks, the default) or, with MHC_BWD_LEGACY=1, one
+    workgroup per token (mf32_bwd_pt_kernel: the token's parameters split by wave 0 one token ahead into
+    one of two LDS blocks, the token's dM, dh_pre, dh_post summed across the waves through their slab
+    buffers): against the oracle (every gradient), against the generic kernel (MHC_BWD_MFMA=0), and
+    bitwise between two runs; with MHC_BWD_GRID=3 each workgroup walks many tokens, so both parameter
+    blocks are used."""
     if grid is not None:
         knobs("MHC_BWD_GRID", grid)
+    knobs("MHC_BWD_LEGACY", legacy)
     knobs("MHC_SK_BLK_RECORD", 0)
     g = rng(3500 + T + n + C)
     x = to_dtype_np(g.standard_normal((T, n, C)), dt)
