@@ -1366,8 +1366,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void m
 // ---------------------------------------------------------------------------
 constexpr int kMf64BwdMaxC = 8192;  // y, dyn and dw of a token in LDS: 96 KB
 
-template <typename XT, bool RAW, bool FULL, bool GL>
+template <typename XT, bool RAW, bool FULL, bool GL, int NB>
 __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
+  constexpr int NH = NB / 2;  // 32-stream halves
   // [S][16 r][8] y, then dyn; dw [C]; with GL (one slab per wave) then each wave's G, [128 channels][64 streams]
   extern __shared__ float4 s_yd4[];
   float* const s_y = reinterpret_cast<float*>(s_yd4);
@@ -1398,9 +1399,9 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   if (wave == 0) {
     u32x4 sp[3];
 #pragma unroll
-    for (int h = 0; h < (GL ? 0 : 2); ++h) {
+    for (int h = 0; h < (GL ? 0 : NH); ++h) {
 #pragma unroll
-      for (int J = 0; J < 4; ++J) {
+      for (int J = 0; J < NB; ++J) {
         const int j = 16 * J + r;
         float mv[8];
 #pragma unroll
@@ -1421,18 +1422,18 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
 
   // phase C sums of the wave's slabs over every token: dM blocks [I][J] (rows 16 I + 4 q + k, column
   // 16 J + r), dA of streams 16 J + r and dP of streams 16 I + r over the lane's channels
-  f32x4 dmb[4][4];
-  float dAp[4], dPp[4];
+  f32x4 dmb[NB][NB];
+  float dAp[NB], dPp[NB];
 #pragma unroll
-  for (int I = 0; I < 4; ++I) {
+  for (int I = 0; I < NB; ++I) {
     dAp[I] = dPp[I] = 0.0f;
 #pragma unroll
-    for (int J = 0; J < 4; ++J) dmb[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int J = 0; J < NB; ++J) dmb[I][J] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   const uint32_t lane_c = (uint32_t)(r * C + 8 * q) * kEs;  // stream r (+ 16 I rows), channel 8q of a chunk
-  float a_r[4], p_r[4];  // a and p of the lane's rows 16 I + r
+  float a_r[NB], p_r[NB];  // a and p of the lane's rows 16 I + r
 #pragma unroll
-  for (int I = 0; I < 4; ++I) {
+  for (int I = 0; I < NB; ++I) {
     a_r[I] = s_a[16 * I + r];
     p_r[I] = s_p[16 * I + r];
   }
@@ -1461,24 +1462,24 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     // sum x_i dyn w, sum x_i y and sum g_i y w.  G of the wave's last slab is also read in the B-operand
     // layout (two 32-stream halves, transposed) and kept for the dx pass.
     float ss = 0.0f, sr = 0.0f;
-    float ua[4], va[4], wa[4];
+    float ua[NB], va[NB], wa[NB];
 #pragma unroll
-    for (int I = 0; I < 4; ++I) ua[I] = va[I] = wa[I] = 0.0f;
-    u32x4 bg[2][8];
+    for (int I = 0; I < NB; ++I) ua[I] = va[I] = wa[I] = 0.0f;
+    u32x4 bg[NH][8];
     for (int s = 0; s < spw; ++s) {
       const int slab = wave * spw + s;
       const uint32_t sob = (uint32_t)slab * 128 * kEs;
       if (!GL && s == spw - 1) {
-        load_half(std::integral_constant<int, 0>{}, rg, slab, 0, bg[0]);
-        load_half(std::integral_constant<int, 0>{}, rg, slab, 1, bg[1]);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) load_half(std::integral_constant<int, 0>{}, rg, slab, h, bg[h]);
       }
 #pragma unroll 1  // unrolled, the chunks' rows and sums spill
       for (int k = 0; k < 4; ++k) {
         const uint32_t cb = sob + (uint32_t)(32 * k) * kEs;
         const uint32_t lc = opaque_u32(lane_c);
-        Vec<XT, 8> ga[4], xb[4];
+        Vec<XT, 8> ga[NB], xb[NB];
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
+        for (int I = 0; I < NB; ++I) {
           const uint32_t row = (uint32_t)(16 * I) * rowb;
           buf_load<0>(xb[I], rx, lc + row, cb);
           buf_load<0>(ga[I], rg, lc + row, cb);
@@ -1490,7 +1491,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
         for (int e = 0; e < 8; ++e) {
           float ys = 0.0f, ds = 0.0f;
 #pragma unroll
-          for (int I = 0; I < 4; ++I) {
+          for (int I = 0; I < NB; ++I) {
             ys = fmaf(a_r[I], xb[I].get(e), ys);
             ds = fmaf(p_r[I], ga[I].get(e), ds);
           }
@@ -1498,10 +1499,10 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
           dc[e] = strided_sum<1, 16>(ds);
         }
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
+        for (int I = 0; I < NB; ++I) {
           const u32x4 a = {ga[I].w[0], ga[I].w[1], ga[I].w[2], ga[I].w[3]};
 #pragma unroll
-          for (int J = 0; J < 4; ++J) {
+          for (int J = 0; J < NB; ++J) {
             const u32x4 b = {xb[J].w[0], xb[J].w[1], xb[J].w[2], xb[J].w[3]};
             dmb[I][J] = mfma32k<XT>(a, b, dmb[I][J]);
           }
@@ -1510,14 +1511,14 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
           // G to the wave's LDS, channel-major: element e of the piece is channel 32 k + 8 q + e of
           // stream 16 I + r (the B-operand reads after the barrier take 8 streams of a channel at once)
 #pragma unroll
-          for (int I = 0; I < 4; ++I)
+          for (int I = 0; I < NB; ++I)
 #pragma unroll
             for (int e = 0; e < 8; ++e)
               s_g[(32 * k + 8 * q + e) * 64 + 16 * I + r] = (uint16_t)(ga[I].w[e >> 1] >> (16 * (e & 1)));
         }
         // the rows are converted again below rather than kept as 64 floats
 #pragma unroll
-        for (int I = 0; I < 4; ++I)
+        for (int I = 0; I < NB; ++I)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             xb[I].w[e] = opaque_u32(xb[I].w[e]);
@@ -1533,7 +1534,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
           sr = fmaf(dw8[e], yc[e], sr);
         }
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
+        for (int I = 0; I < NB; ++I) {
           float su = 0.0f, sv = 0.0f, sw = 0.0f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -1574,7 +1575,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
     const float kf = (inv * inv * inv / (float)C) * tsr;
     // dy = dyn inv w - kf y and yn = y inv w: dA_i = inv sum x_i dyn w - kf sum x_i y, dP_i = inv sum g_i y w
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
+    for (int I = 0; I < NB; ++I) {
       dAp[I] += inv * ua[I] - kf * va[I];
       dPp[I] += inv * wa[I];
     }
@@ -1601,22 +1602,22 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
       if constexpr (GL) {
         // streams 32 h + 8 q .. + 7 of channel 8 r + v: the B operands, from the wave's LDS
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < NH; ++h)
 #pragma unroll
           for (int v = 0; v < 8; ++v)
             bg[h][v] = *reinterpret_cast<const u32x4*>(s_g + (8 * r + v) * 64 + 32 * h + 8 * q);
       } else if (s != spw - 1) {
-        load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 0, bg[0]);
-        load_half(std::integral_constant<int, kBufNt>{}, rg, slab, 1, bg[1]);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) load_half(std::integral_constant<int, kBufNt>{}, rg, slab, h, bg[h]);
         asm volatile("" ::: "memory");
       }
       const uint32_t sob = (uint32_t)slab * 128 * kEs;
 #pragma unroll 1
-      for (int J = 0; J < 4; ++J) {
-        u32x4 amt[2][3];
+      for (int J = 0; J < NB; ++J) {
+        u32x4 amt[NH][3];
         if constexpr (GL) {
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
+          for (int h = 0; h < NH; ++h) {
             const int j = 16 * J + r;
             float mv[8];
 #pragma unroll
@@ -1628,7 +1629,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
           }
         } else {
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
+          for (int h = 0; h < NH; ++h)
 #pragma unroll
             for (int e = 0; e < 3; ++e) amt[h][e] = s_amt[J][h][e][lane];
         }
@@ -1640,8 +1641,8 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           f32x4 acc = {a4[0] * dy[v], a4[1] * dy[v], a4[2] * dy[v], a4[3] * dy[v]};
-          acc = mfma_split3<XT>(amt[0], bg[0][v], acc);
-          acc = mfma_split3<XT>(amt[1], bg[1][v], acc);
+#pragma unroll
+          for (int h = 0; h < NH; ++h) acc = mfma_split3<XT>(amt[h], bg[h][v], acc);
           if (v & 1) rows.put(v >> 1, even, acc);
           else even = acc;
         }
@@ -1658,7 +1659,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   // ---- partial row: [dw C | 0 .. Cp | dM n*n | dA n | dP n | 0 .. P].  The waves' sums are added in
   // wave order in LDS (in the parameter operands' space, free once every wave is past its last token).
 #pragma unroll
-  for (int I = 0; I < 4; ++I) {
+  for (int I = 0; I < NB; ++I) {
     dAp[I] += shfl_xor(dAp[I], 16);
     dAp[I] += shfl_xor(dAp[I], 32);
     dPp[I] += shfl_xor(dPp[I], 16);
@@ -1671,9 +1672,9 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
   for (int w = 0; w < nwaves; ++w) {
     if (wave == w) {
 #pragma unroll
-      for (int I = 0; I < 4; ++I)
+      for (int I = 0; I < NB; ++I)
 #pragma unroll
-        for (int J = 0; J < 4; ++J)
+        for (int J = 0; J < NB; ++J)
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             float* d = s_acc + (16 * I + 4 * q + k) * 64 + 16 * J + r;
@@ -1681,7 +1682,7 @@ __global__ __launch_bounds__(512) void mf64_bwd_kernel(Mf32Args A, int spw) {
           }
       if (q == 0) {
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
+        for (int I = 0; I < NB; ++I) {
           float* da = s_acc + 4096 + 16 * I + r;
           float* dp = s_acc + 4096 + 64 + 16 * I + r;
           *da = w == 0 ? dAp[I] : *da + dAp[I];
@@ -2677,14 +2678,16 @@ int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
   // one slab per wave and at least two waves: G stays in LDS across the RMS barrier (16 KB per wave)
   const bool gl = spw == 1 && waves >= 2 && knob(kKnobBwdPipe, 1) != 0;
   const size_t smem = (size_t)3 * S * 128 * sizeof(float) + (gl ? (size_t)waves * 128 * 64 * sizeof(uint16_t) : 0);
-  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64;
+  const bool raw = A.h_mode == MHC_H_RAW, full = A.n == 64, nb2 = A.n <= 32;
   return by_half(xd, [&](auto* xp) {
     using XT = std::remove_pointer_t<decltype(xp)>;
     const void* kfn;
-    if (gl) kfn = full ? (raw ? (const void*)mf64_bwd_kernel<XT, true, true, true> : (const void*)mf64_bwd_kernel<XT, false, true, true>)
-                       : (raw ? (const void*)mf64_bwd_kernel<XT, true, false, true> : (const void*)mf64_bwd_kernel<XT, false, false, true>);
-    else kfn = full ? (raw ? (const void*)mf64_bwd_kernel<XT, true, true, false> : (const void*)mf64_bwd_kernel<XT, false, true, false>)
-                    : (raw ? (const void*)mf64_bwd_kernel<XT, true, false, false> : (const void*)mf64_bwd_kernel<XT, false, false, false>);
+    if (nb2) kfn = gl ? (raw ? (const void*)mf64_bwd_kernel<XT, true, false, true, 2> : (const void*)mf64_bwd_kernel<XT, false, false, true, 2>)
+                      : (raw ? (const void*)mf64_bwd_kernel<XT, true, false, false, 2> : (const void*)mf64_bwd_kernel<XT, false, false, false, 2>);
+    else if (gl) kfn = full ? (raw ? (const void*)mf64_bwd_kernel<XT, true, true, true, 4> : (const void*)mf64_bwd_kernel<XT, false, true, true, 4>)
+                            : (raw ? (const void*)mf64_bwd_kernel<XT, true, false, true, 4> : (const void*)mf64_bwd_kernel<XT, false, false, true, 4>);
+    else kfn = full ? (raw ? (const void*)mf64_bwd_kernel<XT, true, true, false, 4> : (const void*)mf64_bwd_kernel<XT, false, true, false, 4>)
+                    : (raw ? (const void*)mf64_bwd_kernel<XT, true, false, false, 4> : (const void*)mf64_bwd_kernel<XT, false, false, false, 4>);
     const int occ = occupancy_blocks(kfn, waves * 64, smem);
     if (occ <= 0) return 1;
     int64_t blocks = std::min<int64_t>(gmax, (int64_t)device_cu_count() * occ);
@@ -2692,16 +2695,26 @@ int mf64_fused_bwd(const Mf32Args& A, int xd, int gd, int64_t gmax, hipStream_t 
     if (grid_pref > 0) blocks = std::min<int64_t>(gmax, grid_pref);
     blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, A.T));
     const dim3 g((unsigned)blocks), b(waves * 64);
-    with_full(full, [&](auto fc) {
-      constexpr bool F = decltype(fc)::value;
+    if (nb2) {
       if (gl) {
-        if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, F, true>), g, b, smem, s, A, spw);
-        else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, F, true>), g, b, smem, s, A, spw);
+        if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, false, true, 2>), g, b, smem, s, A, spw);
+        else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, false, true, 2>), g, b, smem, s, A, spw);
       } else {
-        if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, F, false>), g, b, smem, s, A, spw);
-        else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, F, false>), g, b, smem, s, A, spw);
+        if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, false, false, 2>), g, b, smem, s, A, spw);
+        else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, false, false, 2>), g, b, smem, s, A, spw);
       }
-    });
+    } else {
+      with_full(full, [&](auto fc) {
+        constexpr bool F = decltype(fc)::value;
+        if (gl) {
+          if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, F, true, 4>), g, b, smem, s, A, spw);
+          else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, F, true, 4>), g, b, smem, s, A, spw);
+        } else {
+          if (raw) hipLaunchKernelGGL((mf64_bwd_kernel<XT, true, F, false, 4>), g, b, smem, s, A, spw);
+          else hipLaunchKernelGGL((mf64_bwd_kernel<XT, false, F, false, 4>), g, b, smem, s, A, spw);
+        }
+      });
+    }
     MHC_CHECK_LAUNCH("mf64_bwd_kernel");
     *num_partials = blocks;
     return MHC_OK;
