@@ -87,10 +87,12 @@ __global__ __launch_bounds__(kSkThreads) void sinkhorn_blk_fwd_kernel(const floa
 }
 
 // ---------------------------------------------------------------------------
-// One 32 < n <= 64 matrix per workgroup of four waves: one wave per matrix
-// runs every instruction of an iteration's dependent chain itself, four
-// waves a quarter of them.  Wave w holds rows 16 w .. 16 w + 15; lane (rq = lane / 8,
-// cq = lane % 8) rows 16 w + 2 rq and + 1, columns 8 cq .. 8 cq + 7.  Row
+// One 32 < n <= 64 matrix per workgroup of 8 / R waves (R = 2: four waves
+// for few matrices, whose projection is latency-bound; R = 4: two waves for
+// many, where the instruction count per matrix matters): one wave per matrix
+// runs every instruction of an iteration's dependent chain itself, W waves a
+// W-th of them.  Wave w holds rows 8 R w .. 8 R w + 8 R - 1; lane (rq = lane
+// / 8, cq = lane % 8) rows 8 R w + R rq .. + R - 1, columns 8 cq .. 8 cq + 7.  Row
 // sums stay in the wave (the 8 lanes of a row, DPP); a column sum adds the
 // wave's lanes of the column (stride 8), then the four waves' partials from
 // LDS in wave order: one barrier per iteration, the partials double-buffered
@@ -100,26 +102,28 @@ __global__ __launch_bounds__(kSkThreads) void sinkhorn_blk_fwd_kernel(const floa
 // this forward serves this VJP; the values differ from the one-wave kernel's
 // in summation order, so forward and VJP choose the same kernel family.
 // ---------------------------------------------------------------------------
-constexpr int kSkWgWaves = 4;
 constexpr int kSkWgMaxStateBytes = 48 * 1024;  // the recomputing VJP's state in LDS: up to 32 iterations
 
 struct SkWgLane {
   int lane, w, rq, cq, r0, c0;
 };
 
+// R rows per lane: 8 / R waves of 8 R rows each.
+template <int R>
 MHC_DEV SkWgLane sk_wg_lane() {
   SkWgLane L;
   L.lane = threadIdx.x & 63;
   L.w = threadIdx.x >> 6;
   L.rq = L.lane >> 3;
   L.cq = L.lane & 7;
-  L.r0 = 16 * L.w + 2 * L.rq;
+  L.r0 = 8 * R * L.w + R * L.rq;
   L.c0 = 8 * L.cq;
   return L;
 }
 
 // cs: the lane's partial sums of its 8 columns over its two rows -> the column sums over every row.
-MHC_DEV void sk_wg_colsum(float (&cs)[8], float (*s_cs)[kSkWgWaves][64], int par, const SkWgLane& L) {
+template <int W>
+MHC_DEV void sk_wg_colsum(float (&cs)[8], float (*s_cs)[W][64], int par, const SkWgLane& L) {
 #pragma unroll
   for (int b = 0; b < 8; ++b) cs[b] = strided_sum<8, 64>(cs[b]);
   if (L.rq == 0) {
@@ -131,7 +135,7 @@ MHC_DEV void sk_wg_colsum(float (&cs)[8], float (*s_cs)[kSkWgWaves][64], int par
 #pragma unroll
   for (int b = 0; b < 8; ++b) cs[b] = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kSkWgWaves; ++w) {
+  for (int w = 0; w < W; ++w) {
     const float4* src = reinterpret_cast<const float4*>(&s_cs[par][w][L.c0]);
     const float4 u = src[0], v = src[1];
     cs[0] += u.x; cs[1] += u.y; cs[2] += u.z; cs[3] += u.w;
@@ -140,10 +144,11 @@ MHC_DEV void sk_wg_colsum(float (&cs)[8], float (*s_cs)[kSkWgWaves][64], int par
 }
 
 // exp(H - rowmax) of the lane's 2 x 8 block (0 outside the matrix) and the row-maximum ties (bit 8a + b).
-MHC_DEV uint32_t sk_wg_load_exp(const float* __restrict__ H, int n, const SkWgLane& L, float (&K)[2][8]) {
+template <int R>
+MHC_DEV uint32_t sk_wg_load_exp(const float* __restrict__ H, int n, const SkWgLane& L, float (&K)[R][8]) {
   uint32_t tie = 0;
 #pragma unroll
-  for (int a = 0; a < 2; ++a) {
+  for (int a = 0; a < R; ++a) {
     float hv[8];
     float mx = -INFINITY;
 #pragma unroll
@@ -166,16 +171,18 @@ MHC_DEV uint32_t sk_wg_load_exp(const float* __restrict__ H, int n, const SkWgLa
 
 // `iters` iterations on the lane's block P (the block layout's arithmetic per element: row step, then
 // column step, masks and state as sk_blk_iterate); par counts the workgroup's column-sum rounds.
-template <bool REC>
-MHC_DEV void sk_wg_iterate(float (&P)[2][8], int n, int iters, float eps, const SkWgLane& L,
-                           float (*s_cs)[kSkWgWaves][64], int& par, float* st) {
-  float Rc[2] = {1.0f, 1.0f}, Cc[8];
+template <int R, bool REC>
+MHC_DEV void sk_wg_iterate(float (&P)[R][8], int n, int iters, float eps, const SkWgLane& L,
+                           float (*s_cs)[8 / R][64], int& par, float* st) {
+  float Rc[R], Cc[8];
+#pragma unroll
+  for (int a = 0; a < R; ++a) Rc[a] = 1.0f;
 #pragma unroll
   for (int b = 0; b < 8; ++b) Cc[b] = 1.0f;
   for (int it = 0; it < iters; ++it) {
-    float rsc[2], rf[2];
+    float rsc[R], rf[R];
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
+    for (int a = 0; a < R; ++a) {
       float s = P[a][0];
 #pragma unroll
       for (int b = 1; b < 8; ++b) s += P[a][b];
@@ -191,16 +198,20 @@ MHC_DEV void sk_wg_iterate(float (&P)[2][8], int n, int iters, float eps, const 
     }
     float cs[8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) cs[b] = P[0][b] + P[1][b];
-    sk_wg_colsum(cs, s_cs, par, L);
+    for (int b = 0; b < 8; ++b) {
+      cs[b] = P[0][b];
+#pragma unroll
+      for (int a = 1; a < R; ++a) cs[b] += P[a][b];
+    }
+    sk_wg_colsum<8 / R>(cs, s_cs, par, L);
     par ^= 1;
     float csc[8], cf[8], Cp[8];
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const bool ok = L.c0 + b < n && cs[b] > eps;
       csc[b] = ok ? sk_rcp(cs[b]) : 0.0f;
-      P[0][b] *= csc[b];
-      P[1][b] *= csc[b];
+#pragma unroll
+      for (int a = 0; a < R; ++a) P[a][b] *= csc[b];
       if (REC) {
         Cp[b] = Cc[b];
         cf[b] = ok ? Cc[b] * csc[b] * csc[b] : 0.0f;
@@ -211,7 +222,7 @@ MHC_DEV void sk_wg_iterate(float (&P)[2][8], int n, int iters, float eps, const 
       float* sti = st + (int64_t)it * kSkBlkStateVecs * 64;
       if (L.cq == 0) {
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
+        for (int a = 0; a < R; ++a) {
           sti[L.r0 + a] = Rc[a];
           sti[2 * 64 + L.r0 + a] = rsc[a];
           sti[3 * 64 + L.r0 + a] = rf[a];
@@ -226,23 +237,23 @@ MHC_DEV void sk_wg_iterate(float (&P)[2][8], int n, int iters, float eps, const 
   }
 }
 
-template <bool REC>
-__global__ __launch_bounds__(kSkWgWaves * 64) void sinkhorn_wg_fwd_kernel(const float* __restrict__ logits,
+template <int R, bool REC>
+__global__ __launch_bounds__(512 / R) void sinkhorn_wg_fwd_kernel(const float* __restrict__ logits,
                                                                           float* __restrict__ out, int64_t batch,
                                                                           int n, int iters, float eps,
                                                                           float* __restrict__ rec) {
-  __shared__ __align__(16) float s_cs[2][kSkWgWaves][64];
-  const SkWgLane L = sk_wg_lane();
+  __shared__ __align__(16) float s_cs[2][8 / R][64];
+  const SkWgLane L = sk_wg_lane<R>();
   const int64_t nn = (int64_t)n * n;
   const int64_t per_matrix = sk_blk_state_floats(64, iters);
   int par = 0;
   for (int64_t m = blockIdx.x; m < batch; m += gridDim.x) {
-    float P[2][8];
-    sk_wg_load_exp(logits + m * nn, n, L, P);
-    sk_wg_iterate<REC>(P, n, iters, eps, L, s_cs, par, REC ? rec + m * per_matrix : nullptr);
+    float P[R][8];
+    sk_wg_load_exp<R>(logits + m * nn, n, L, P);
+    sk_wg_iterate<R, REC>(P, n, iters, eps, L, s_cs, par, REC ? rec + m * per_matrix : nullptr);
     float* o = out + m * nn;
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < R; ++a)
 #pragma unroll
       for (int b = 0; b < 8; ++b)
         if (L.r0 + a < n && L.c0 + b < n) o[(L.r0 + a) * n + L.c0 + b] = P[a][b];
@@ -252,36 +263,36 @@ __global__ __launch_bounds__(kSkWgWaves * 64) void sinkhorn_wg_fwd_kernel(const 
 // VJP: RECORDED reads the forward's record where it lies; otherwise the iterations are recomputed into
 // LDS first (at most kSkWgMaxStateBytes).  Reverse step k (column step, then row step):
 //   Gd = csc Gd - cf * sum_rows(Gd K R_k),  Gd = rsc Gd - rf * sum_cols(Gd K C_k-1).
-template <bool RECORDED>
-__global__ __launch_bounds__(kSkWgWaves * 64) void sinkhorn_wg_bwd_kernel(const float* __restrict__ logits,
+template <int R, bool RECORDED>
+__global__ __launch_bounds__(512 / R) void sinkhorn_wg_bwd_kernel(const float* __restrict__ logits,
                                                                           const float* __restrict__ dM,
                                                                           float* __restrict__ dlogits,
                                                                           int64_t batch, int n, int iters,
                                                                           float eps, const float* __restrict__ rec) {
   extern __shared__ float4 sk_wg_smem4[];
   float* const s_st = reinterpret_cast<float*>(sk_wg_smem4);
-  __shared__ __align__(16) float s_cs[2][kSkWgWaves][64];
-  const SkWgLane L = sk_wg_lane();
+  __shared__ __align__(16) float s_cs[2][8 / R][64];
+  const SkWgLane L = sk_wg_lane<R>();
   const int64_t nn = (int64_t)n * n;
   const int64_t per_matrix = sk_blk_state_floats(64, iters);
   int par = 0;
   for (int64_t m = blockIdx.x; m < batch; m += gridDim.x) {
-    float K[2][8], Gd[2][8];
-    const uint32_t tie = sk_wg_load_exp(logits + m * nn, n, L, K);
+    float K[R][8], Gd[R][8];
+    const uint32_t tie = sk_wg_load_exp<R>(logits + m * nn, n, L, K);
     const float* st;
     if constexpr (RECORDED) {
       st = rec + m * per_matrix;
     } else {
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < R; ++a)
 #pragma unroll
         for (int b = 0; b < 8; ++b) Gd[a][b] = K[a][b];
-      sk_wg_iterate<true>(Gd, n, iters, eps, L, s_cs, par, s_st);
+      sk_wg_iterate<R, true>(Gd, n, iters, eps, L, s_cs, par, s_st);
       __syncthreads();  // every lane's state entries before any lane reads them
       st = s_st;
     }
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < R; ++a)
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
         const bool v = L.r0 + a < n && L.c0 + b < n;
@@ -290,9 +301,9 @@ __global__ __launch_bounds__(kSkWgWaves * 64) void sinkhorn_wg_bwd_kernel(const 
       }
     for (int it = iters - 1; it >= 0; --it) {
       const float* sti = st + (int64_t)it * kSkBlkStateVecs * 64;
-      float Rk[2], rsc[2], rf[2], Cp[8], csc[8], cf[8];
+      float Rk[R], rsc[R], rf[R], Cp[8], csc[8], cf[8];
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
+      for (int a = 0; a < R; ++a) {
         Rk[a] = sti[L.r0 + a];
         rsc[a] = sti[2 * 64 + L.r0 + a];
         rf[a] = sti[3 * 64 + L.r0 + a];
@@ -302,17 +313,21 @@ __global__ __launch_bounds__(kSkWgWaves * 64) void sinkhorn_wg_bwd_kernel(const 
       sk_blk_st_load<8>(sti + 5 * 64 + L.c0, cf);
       float cs[8];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) cs[b] = Gd[0][b] * K[0][b] * Rk[0] + Gd[1][b] * K[1][b] * Rk[1];
-      sk_wg_colsum(cs, s_cs, par, L);
+      for (int b = 0; b < 8; ++b) {
+        cs[b] = Gd[0][b] * K[0][b] * Rk[0];
+#pragma unroll
+        for (int a = 1; a < R; ++a) cs[b] += Gd[a][b] * K[a][b] * Rk[a];
+      }
+      sk_wg_colsum<8 / R>(cs, s_cs, par, L);
       par ^= 1;
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
         const float sub = cs[b] * cf[b];
-        Gd[0][b] = csc[b] * Gd[0][b] - sub;
-        Gd[1][b] = csc[b] * Gd[1][b] - sub;
+#pragma unroll
+        for (int a = 0; a < R; ++a) Gd[a][b] = csc[b] * Gd[a][b] - sub;
       }
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
+      for (int a = 0; a < R; ++a) {
         float dot = Gd[a][0] * (K[a][0] * Cp[0]);
 #pragma unroll
         for (int b = 1; b < 8; ++b) dot += Gd[a][b] * (K[a][b] * Cp[b]);
@@ -323,7 +338,7 @@ __global__ __launch_bounds__(kSkWgWaves * 64) void sinkhorn_wg_bwd_kernel(const 
     }
     // through exp and the row-max shift (the gradient of the max split evenly among tied maxima)
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
+    for (int a = 0; a < R; ++a) {
       float tot = 0.0f, cnt = 0.0f;
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
@@ -1250,23 +1265,39 @@ bool use_wg(int64_t batch, int n, int iters) {
 
 dim3 wg_grid(int64_t batch) { return dim3((unsigned)std::min<int64_t>(batch, (int64_t)device_cu_count() * 16)); }
 
+// Four waves per matrix up to one matrix per CU, two above (MHC_SK_WG=2: four at every batch).
+bool wg_two_waves(int64_t batch) { return batch > device_cu_count() && knob(kKnobSkWg, 1) != 2; }
+
 void launch_wg_fwd(const float* logits, float* M, int64_t batch, int n, int iters, float eps, float* rec,
                    hipStream_t s) {
-  const dim3 g = wg_grid(batch), b(kSkWgWaves * 64);
-  if (rec != nullptr) hipLaunchKernelGGL((sinkhorn_wg_fwd_kernel<true>), g, b, 0, s, logits, M, batch, n, iters, eps, rec);
-  else hipLaunchKernelGGL((sinkhorn_wg_fwd_kernel<false>), g, b, 0, s, logits, M, batch, n, iters, eps, nullptr);
+  const dim3 g = wg_grid(batch);
+  auto go = [&](auto rc) {
+    constexpr int R = decltype(rc)::value;
+    if (rec != nullptr)
+      hipLaunchKernelGGL((sinkhorn_wg_fwd_kernel<R, true>), g, dim3(512 / R), 0, s, logits, M, batch, n, iters, eps, rec);
+    else
+      hipLaunchKernelGGL((sinkhorn_wg_fwd_kernel<R, false>), g, dim3(512 / R), 0, s, logits, M, batch, n, iters, eps,
+                         nullptr);
+  };
+  if (wg_two_waves(batch)) go(std::integral_constant<int, 4>{});
+  else go(std::integral_constant<int, 2>{});
 }
 
 void launch_wg_bwd(const float* logits, const float* dM, float* dlogits, int64_t batch, int n, int iters,
                    float eps, const float* rec, hipStream_t s) {
-  const dim3 g = wg_grid(batch), b(kSkWgWaves * 64);
-  if (rec != nullptr) {
-    hipLaunchKernelGGL((sinkhorn_wg_bwd_kernel<true>), g, b, 0, s, logits, dM, dlogits, batch, n, iters, eps, rec);
-  } else {
-    const size_t smem = (size_t)sk_blk_state_floats(64, iters) * sizeof(float);
-    hipLaunchKernelGGL((sinkhorn_wg_bwd_kernel<false>), g, b, smem, s, logits, dM, dlogits, batch, n, iters, eps,
-                       nullptr);
-  }
+  const dim3 g = wg_grid(batch);
+  const size_t smem = (size_t)sk_blk_state_floats(64, iters) * sizeof(float);
+  auto go = [&](auto rc) {
+    constexpr int R = decltype(rc)::value;
+    if (rec != nullptr)
+      hipLaunchKernelGGL((sinkhorn_wg_bwd_kernel<R, true>), g, dim3(512 / R), 0, s, logits, dM, dlogits, batch, n, iters,
+                         eps, rec);
+    else
+      hipLaunchKernelGGL((sinkhorn_wg_bwd_kernel<R, false>), g, dim3(512 / R), smem, s, logits, dM, dlogits, batch, n,
+                         iters, eps, nullptr);
+  };
+  if (wg_two_waves(batch)) go(std::integral_constant<int, 4>{});
+  else go(std::integral_constant<int, 2>{});
 }
 
 // The first 256-byte boundary at or after p.
