@@ -341,7 +341,7 @@ def test_sinkhorn16_layouts_agree(cpl, knobs):
 
 
 @pytest.mark.parametrize("B,n,iters", [(1, 32, 20), (1, 24, 20), (5, 32, 3), (1, 64, 20), (3, 48, 1), (9, 17, 0),
-                                       (1, 32, 90), (700, 32, 20)])
+                                       (1, 32, 90), (700, 32, 20), (700, 64, 20), (300, 48, 5)])
 def test_sinkhorn_blk_recorded_state_matches_recompute(B, n, iters):
     """16 < n <= 64: mhc_sinkhorn_fwd_record / mhc_sinkhorn_bwd_recorded give bitwise the results of
     mhc_sinkhorn_fwd / mhc_sinkhorn_bwd (the forward records the same state the VJP otherwise
