@@ -675,9 +675,15 @@ def main() -> int:
     del x, dout
     torch.cuda.empty_cache()
     if not args.no_latency:
+        # the small step first: its eager figure depends on what ran before it in the process (48-50 µs in a
+        # fresh process; 83-86 µs when measured right after the forward-latency graphs, which are captured
+        # after no-grad eager calls of the same layer shape, with the same kernels and HIP calls); the
+        # figure after those graphs is reported beside it
+        small = _small_step_latency(dev)
         result["fwd_latency"] = {"config1_B32_C2048": _fwd_latency(4, 2048, 32, dev),
                                  "B1_C4096": _fwd_latency(4, 4096, 1, dev)}
-        result["small_step_latency"] = _small_step_latency(dev)
+        small["eager_us_after_fwd_graphs"] = _small_step_latency(dev)["eager_us"]
+        result["small_step_latency"] = small
     if not args.no_extra:
         # 20 warmup steps: the first ~20 steps after a change of workload run a few percent slow
         # (config 3: 0.56-0.61 ms against 0.545 ms from then on)
