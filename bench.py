@@ -610,8 +610,9 @@ def main() -> int:
         return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build runs on one GPU per box; the mHC path shards by token "
-                                   "(see DESIGN.md) and has no multi-GPU benchmark", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU per box; the mHC path would shard by token "
+                                   "(each GPU its own tokens, the parameter gradients summed across GPUs) and "
+                                   "has no multi-GPU benchmark", "n_gpus": args.gpus}))
         return 2
 
     import numpy as np
