@@ -676,10 +676,10 @@ def main() -> int:
     del x, dout
     torch.cuda.empty_cache()
     if not args.no_latency:
-        # the small step first: its eager figure depends on what ran before it in the process (48-50 µs in a
-        # fresh process; 83-86 µs when measured right after the forward-latency graphs, which are captured
-        # after no-grad eager calls of the same layer shape, with the same kernels and HIP calls); the
-        # figure after those graphs is reported beside it
+        # the small step's eager figure depends on what ran before it in the process, with the same kernels
+        # and HIP calls: 48-50 µs in a fresh process, 60-86 µs from run to run here after the config-2
+        # steps, and 83-86 µs in a fresh process after no-grad eager calls followed by a graph capture of
+        # the same layer shape; it is timed before the forward-latency graphs and after them
         small = _small_step_latency(dev)
         result["fwd_latency"] = {"config1_B32_C2048": _fwd_latency(4, 2048, 32, dev),
                                  "B1_C4096": _fwd_latency(4, 4096, 1, dev)}
